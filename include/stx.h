@@ -1,0 +1,122 @@
+/* stx.h — C ABI of the MI355X (gfx950) spectral + elementwise hot path of stems.cpp.
+ *
+ * Every entry point here replaces one host function or ggml op of the reference
+ * (betweentwomidnights/stems.cpp v0.1.7); the comment above each declaration cites the
+ * reference interface it replaces as file:line.
+ *
+ * Conventions (after the libstems V1 ABI, src/libstems_v1.h:53-63 and :18-20):
+ *   - Every call returns an stx_status. On failure stx_last_error() holds a message for the
+ *     calling thread. No C++ exception crosses this boundary.
+ *   - STX_STATUS_INVALID_ARGUMENT is what the reference reports with std::invalid_argument,
+ *     STX_STATUS_RUNTIME_ERROR what it reports with std::runtime_error.
+ *   - Buffers marked "device" are caller-owned device memory (hipMalloc or any allocator);
+ *     the hot calls never allocate. Work is enqueued on `stream` (a hipStream_t; NULL is the
+ *     null stream) and runs asynchronously; results are valid once the stream is synchronised.
+ *   - Complex arrays are interleaved float pairs (re, im), i.e. complex64.
+ *   - Spectra use layout STX_SPEC_F_MAJOR, the reference's own (spec[(c * F + f) * T + t],
+ *     src/stft.h:76-78), or STX_SPEC_T_MAJOR (spec[(c * T + t) * F + f]), which keeps every
+ *     frame contiguous and is what the device pipeline prefers.
+ *   - Handles (stx_fft, stx_bands) are immutable after creation and may be shared between
+ *     threads and streams, as st::FFT is (src/stft.h:19-55).
+ */
+#ifndef STX_H
+#define STX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__)
+#  define STX_API __attribute__((visibility("default")))
+#else
+#  define STX_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int32_t stx_status;
+enum {
+    STX_STATUS_OK               = 0,
+    STX_STATUS_INVALID_ARGUMENT = 1,   /* std::invalid_argument in the reference */
+    STX_STATUS_UNSUPPORTED      = 2,   /* valid for the reference, not implemented here */
+    STX_STATUS_CANCELLED        = 3,   /* st::Cancelled (src/separator.h:34-36) */
+    STX_STATUS_RUNTIME_ERROR    = 4,   /* std::runtime_error in the reference */
+    STX_STATUS_OUT_OF_MEMORY    = 6,
+    STX_STATUS_DEVICE_ERROR     = 7    /* a HIP call failed */
+};
+
+typedef int32_t stx_spec_layout;
+enum {
+    STX_SPEC_F_MAJOR = 0,              /* spec[(c * F + f) * T + t]: stft.h's layout */
+    STX_SPEC_T_MAJOR = 1               /* spec[(c * T + t) * F + f] */
+};
+
+typedef void* stx_stream;              /* a hipStream_t */
+
+/* Library version string, e.g. "0.1.0". */
+STX_API const char* stx_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+STX_API const char* stx_last_error(void);
+
+/* ------------------------------------------------------------------------------------------
+ * FFT plan. Replaces st::FFT (src/stft.h:19-55).
+ * ---------------------------------------------------------------------------------------- */
+typedef struct stx_fft stx_fft;
+
+/* st::FFT::FFT(int n) (src/stft.h:21-31): INVALID_ARGUMENT unless n is a power of two >= 2,
+ * exactly like the reference; UNSUPPORTED for powers of two outside [16, 8192], which this
+ * build has no kernels for. Allocates the plan's device tables (window, twiddles) on the
+ * current device. */
+STX_API stx_status stx_fft_create(int n, stx_fft** out);
+STX_API void       stx_fft_destroy(stx_fft* fft);
+/* st::FFT::size() (src/stft.h:32). */
+STX_API int        stx_fft_size(const stx_fft* fft);
+
+/* st::FFT::run(a, inverse) (src/stft.h:34-49), batched: data is device [batch][n] complex,
+ * transformed in place, unnormalised; inverse uses conjugate twiddles (no 1/n). */
+STX_API stx_status stx_fft_run(const stx_fft* fft, float* data, int batch, int inverse,
+                               stx_stream stream);
+
+/* ------------------------------------------------------------------------------------------
+ * STFT / iSTFT. Replace src/stft.h:79-197, batched over channels. Input signals are
+ * contiguous device [channels][len] float32.
+ * ---------------------------------------------------------------------------------------- */
+
+/* Frame count of torch_stft: len / hop + 1 (src/stft.h:153). */
+STX_API int stx_torch_stft_frames(int len, int hop);
+/* Frame count of htdemucs_spec: ceil(len / (n_fft / 4)) (src/stft.h:81,93). */
+STX_API int stx_htdemucs_frames(int n_fft, int len);
+
+/* torch_stft (src/stft.h:146-164): hann_window(n) periodic, center=True reflect pad,
+ * onesided, F = n/2 + 1 bins, T = len/hop + 1 frames, optional 1/sqrt(n) normalisation.
+ * spec: device [channels][F][T] (F_MAJOR) or [channels][T][F] (T_MAJOR) complex.
+ * RUNTIME_ERROR if len <= n/2 (the reference's reflect_pad check, src/stft.h:59). */
+STX_API stx_status stx_torch_stft(const stx_fft* fft, const float* x, int channels, int len,
+                                  int hop, int normalized, float* spec, stx_spec_layout layout,
+                                  stx_stream stream);
+
+/* torch_istft (src/stft.h:166-197): DC and Nyquist imaginary parts ignored, window-squared
+ * overlap-add normalisation, length = hop * (n_frames - 1). out: device [channels][length]. */
+STX_API stx_status stx_torch_istft(const stx_fft* fft, const float* spec, int channels,
+                                   int n_frames, int hop, int normalized, float* out,
+                                   stx_spec_layout layout, stx_stream stream);
+
+/* htdemucs_spec (src/stft.h:76-103): HTDemucs._spec; hop n/4, F = n/2 bins (Nyquist dropped),
+ * T = ceil(len / hop) frames, 1/sqrt(n) normalised. spec: device [channels][F][T] or
+ * [channels][T][F]. RUNTIME_ERROR where the reference's reflect pads would throw. */
+STX_API stx_status stx_htdemucs_spec(const stx_fft* fft, const float* x, int channels, int len,
+                                     float* spec, stx_spec_layout layout, stx_stream stream);
+
+/* htdemucs_ispec (src/stft.h:105-140): HTDemucs._ispec; spec has F = n/2 bins and n_frames
+ * frames; out: device [channels][length]. */
+STX_API stx_status stx_htdemucs_ispec(const stx_fft* fft, const float* spec, int channels,
+                                      int n_frames, int length, float* out,
+                                      stx_spec_layout layout, stx_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STX_H */

@@ -1,0 +1,91 @@
+// common.hpp — status/error plumbing and launch helpers shared by every translation unit.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <new>
+#include <stdexcept>
+#include <string>
+
+#include "stx.h"
+
+namespace stx {
+
+// An error that maps onto one stx_status; thrown inside the library, caught at the C ABI.
+struct Error : std::exception {
+    stx_status code;
+    std::string msg;
+    Error(stx_status c, std::string m) : code(c), msg(std::move(m)) {}
+    const char* what() const noexcept override { return msg.c_str(); }
+};
+
+[[noreturn]] inline void fail(stx_status code, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    throw Error(code, buf);
+}
+
+void set_last_error(const char* msg);
+
+// Runs f, converting every exception into a status and the thread's last-error message.
+template <class F>
+stx_status guard(F&& f) noexcept {
+    try {
+        f();
+        set_last_error("");
+        return STX_STATUS_OK;
+    } catch (const Error& e) {
+        set_last_error(e.msg.c_str());
+        return e.code;
+    } catch (const std::bad_alloc&) {
+        set_last_error("out of host memory");
+        return STX_STATUS_OUT_OF_MEMORY;
+    } catch (const std::exception& e) {
+        set_last_error(e.what());
+        return STX_STATUS_RUNTIME_ERROR;
+    } catch (...) {
+        set_last_error("unknown C++ exception");
+        return STX_STATUS_RUNTIME_ERROR;
+    }
+}
+
+inline void hip_check(hipError_t e, const char* what) {
+    if (e == hipSuccess) return;
+    if (e == hipErrorOutOfMemory)
+        fail(STX_STATUS_OUT_OF_MEMORY, "%s: %s", what, hipGetErrorString(e));
+    fail(STX_STATUS_DEVICE_ERROR, "%s: %s", what, hipGetErrorString(e));
+}
+
+// Call right after a kernel launch: reports launch-configuration errors.
+inline void launch_check(const char* kernel) { hip_check(hipGetLastError(), kernel); }
+
+#define STX_REQUIRE(cond, ...) \
+    do { if (!(cond)) ::stx::fail(STX_STATUS_INVALID_ARGUMENT, __VA_ARGS__); } while (0)
+
+inline hipStream_t as_stream(stx_stream s) { return reinterpret_cast<hipStream_t>(s); }
+
+constexpr int kXcds = 8;   // MI355X: 8 XCDs; workgroups are dealt to them round-robin
+
+// Grid size rounded up to a multiple of the XCD count, for xcd_block().
+inline unsigned xcd_grid(long long blocks) {
+    return (unsigned)((blocks + kXcds - 1) / kXcds * kXcds);
+}
+
+// Maps the hardware block id to a logical one so that each XCD receives a contiguous run of
+// logical blocks: neighbouring tiles (which share halo data and partial cache lines) then
+// meet in the same L2. gridDim.x must be a multiple of kXcds; callers skip ids >= the real
+// block count.
+__device__ __forceinline__ int xcd_block() {
+    const int per = (int)gridDim.x / kXcds;
+    return ((int)blockIdx.x % kXcds) * per + (int)blockIdx.x / kXcds;
+}
+
+inline bool is_pow2(long long n) { return n >= 1 && (n & (n - 1)) == 0; }
+
+}  // namespace stx

@@ -1,0 +1,191 @@
+"""ctypes binding of libstx.so, the C ABI declared in include/stx.h.
+
+This is the Python face of the library for tests, the benchmark and Python callers. Device
+buffers are torch tensors (torch is used only for device memory and streams); every call goes
+straight to the HIP kernels in libstx.so. There is no fallback: if the library is missing,
+loading it raises.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libstx.so")
+
+STATUS_OK = 0
+STATUS_INVALID_ARGUMENT = 1
+STATUS_UNSUPPORTED = 2
+STATUS_CANCELLED = 3
+STATUS_RUNTIME_ERROR = 4
+STATUS_OUT_OF_MEMORY = 6
+STATUS_DEVICE_ERROR = 7
+
+F_MAJOR = 0
+T_MAJOR = 1
+
+_c_int_p = ctypes.POINTER(ctypes.c_int)
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+
+# name -> (restype, argtypes); every STX_API function of include/stx.h.
+_SIGNATURES = {
+    "stx_version": (ctypes.c_char_p, []),
+    "stx_last_error": (ctypes.c_char_p, []),
+    "stx_fft_create": (_i, [_i, ctypes.POINTER(_vp)]),
+    "stx_fft_destroy": (None, [_vp]),
+    "stx_fft_size": (_i, [_vp]),
+    "stx_fft_run": (_i, [_vp, _vp, _i, _i, _vp]),
+    "stx_torch_stft_frames": (_i, [_i, _i]),
+    "stx_htdemucs_frames": (_i, [_i, _i]),
+    "stx_torch_stft": (_i, [_vp, _vp, _i, _i, _i, _i, _vp, _i, _vp]),
+    "stx_torch_istft": (_i, [_vp, _vp, _i, _i, _i, _i, _vp, _i, _vp]),
+    "stx_htdemucs_spec": (_i, [_vp, _vp, _i, _i, _vp, _i, _vp]),
+    "stx_htdemucs_ispec": (_i, [_vp, _vp, _i, _i, _i, _vp, _i, _vp]),
+}
+
+
+class StxError(RuntimeError):
+    def __init__(self, status, message):
+        super().__init__(f"stx status {status}: {message}")
+        self.status = status
+        self.message = message
+
+
+_lib = None
+
+
+def lib():
+    """The loaded libstx.so (loaded on first use; raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise OSError(f"{LIB_PATH} is missing: build it with __graft_entry__.build()")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(status):
+    if status != STATUS_OK:
+        raise StxError(status, lib().stx_last_error().decode())
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    """hipStream_t of a torch stream (default: torch's current stream)."""
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _require(t, dtype, what):
+    import torch
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise TypeError(f"{what} must be a CUDA (HIP) tensor")
+    if t.dtype != dtype:
+        raise TypeError(f"{what} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{what} must be contiguous")
+
+
+class FFT:
+    """st::FFT (src/stft.h:19-55) on the device: plan holding the window and twiddle tables."""
+
+    def __init__(self, n):
+        h = ctypes.c_void_p()
+        check(lib().stx_fft_create(int(n), ctypes.byref(h)))
+        self.handle = h
+        self.n = int(n)
+
+    def close(self):
+        if getattr(self, "handle", None):
+            lib().stx_fft_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def size(self):
+        return lib().stx_fft_size(self.handle)
+
+    def run(self, data, inverse=False, stream=None):
+        """In-place batched unnormalised FFT of complex64 data [..., n]."""
+        import torch
+        _require(data, torch.complex64, "data")
+        if data.shape[-1] != self.n:
+            raise ValueError("last dimension must be the FFT size")
+        batch = data.numel() // self.n
+        check(lib().stx_fft_run(self.handle, _ptr(data), batch, int(bool(inverse)), _stream(stream)))
+        return data
+
+
+def torch_stft_frames(length, hop):
+    return lib().stx_torch_stft_frames(int(length), int(hop))
+
+
+def htdemucs_frames(n_fft, length):
+    return lib().stx_htdemucs_frames(int(n_fft), int(length))
+
+
+def torch_stft(fft, x, hop, normalized=False, layout=F_MAJOR, out=None, stream=None):
+    """x: float32 [C, len] -> complex64 [C, F, T] (F_MAJOR) or [C, T, F] (T_MAJOR)."""
+    import torch
+    _require(x, torch.float32, "x")
+    C, L = x.shape
+    T = L // hop + 1
+    F = fft.n // 2 + 1
+    shape = (C, F, T) if layout == F_MAJOR else (C, T, F)
+    if out is None:
+        out = torch.empty(shape, dtype=torch.complex64, device=x.device)
+    check(lib().stx_torch_stft(fft.handle, _ptr(x), C, L, int(hop), int(bool(normalized)), _ptr(out),
+                               int(layout), _stream(stream)))
+    return out
+
+
+def torch_istft(fft, spec, hop, normalized=False, layout=F_MAJOR, out=None, stream=None):
+    """spec: complex64 [C, F, T] or [C, T, F] -> float32 [C, hop * (T - 1)]."""
+    import torch
+    _require(spec, torch.complex64, "spec")
+    C = spec.shape[0]
+    T = spec.shape[2] if layout == F_MAJOR else spec.shape[1]
+    if out is None:
+        out = torch.empty((C, hop * (T - 1)), dtype=torch.float32, device=spec.device)
+    check(lib().stx_torch_istft(fft.handle, _ptr(spec), C, T, int(hop), int(bool(normalized)), _ptr(out),
+                                int(layout), _stream(stream)))
+    return out
+
+
+def htdemucs_spec(fft, x, layout=F_MAJOR, out=None, stream=None):
+    """x: float32 [C, len] -> complex64 [C, n/2, T] (F_MAJOR) or [C, T, n/2]."""
+    import torch
+    _require(x, torch.float32, "x")
+    C, L = x.shape
+    T = htdemucs_frames(fft.n, L)
+    F = fft.n // 2
+    shape = (C, F, T) if layout == F_MAJOR else (C, T, F)
+    if out is None:
+        out = torch.empty(shape, dtype=torch.complex64, device=x.device)
+    check(lib().stx_htdemucs_spec(fft.handle, _ptr(x), C, L, _ptr(out), int(layout), _stream(stream)))
+    return out
+
+
+def htdemucs_ispec(fft, spec, length, layout=F_MAJOR, out=None, stream=None):
+    """spec: complex64 [C, n/2, T] or [C, T, n/2] -> float32 [C, length]."""
+    import torch
+    _require(spec, torch.complex64, "spec")
+    C = spec.shape[0]
+    T = spec.shape[2] if layout == F_MAJOR else spec.shape[1]
+    if out is None:
+        out = torch.empty((C, length), dtype=torch.float32, device=spec.device)
+    check(lib().stx_htdemucs_ispec(fft.handle, _ptr(spec), C, T, int(length), _ptr(out), int(layout),
+                                   _stream(stream)))
+    return out

@@ -1,0 +1,104 @@
+"""ctypes access to the CPU oracle (oracle/liboracle.so) and, where it was built, to the
+reference's own src/stft.h (oracle/_ref/libstft_ref.so). Test infrastructure only."""
+import ctypes
+import os
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_PATH = os.path.join(ROOT, "oracle", "liboracle.so")
+REF_PATH = os.path.join(ROOT, "oracle", "_ref", "libstft_ref.so")
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+
+
+def _np(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+class _Stft:
+    """The stft.h entry points with numpy in/out, over a library with prefix `pre`."""
+
+    def __init__(self, path, pre):
+        if not os.path.exists(path):
+            raise OSError(f"{path} not built (make -C oracle)")
+        self.L = ctypes.CDLL(path)
+        self.pre = pre
+        for name, args in {
+            "fft": [_vp, _i, _i],
+            "torch_stft": [_vp, _i, _i, _i, _i, _vp, _vp],
+            "torch_istft": [_vp, _i, _i, _i, _i, _vp],
+            "htdemucs_spec": [_vp, _i, _i, _vp, _vp],
+            "htdemucs_ispec": [_vp, _i, _i, _i, _vp],
+        }.items():
+            fn = getattr(self.L, pre + name)
+            fn.restype = _i
+            fn.argtypes = args
+
+    def _fn(self, name):
+        return getattr(self.L, self.pre + name)
+
+    def fft(self, a, inverse=False):
+        a = np.ascontiguousarray(a, dtype=np.complex128).copy()
+        rc = self._fn("fft")(_np(a), a.size, int(inverse))
+        if rc:
+            raise ValueError(f"fft rc={rc}")
+        return a
+
+    def torch_stft(self, x, n_fft, hop, normalized=False):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        T = x.size // hop + 1
+        spec = np.zeros((n_fft // 2 + 1, T), dtype=np.complex128)
+        nf = ctypes.c_int(0)
+        rc = self._fn("torch_stft")(_np(x), x.size, n_fft, hop, int(normalized), _np(spec), ctypes.byref(nf))
+        if rc:
+            raise RuntimeError(f"torch_stft rc={rc}")
+        return spec
+
+    def torch_istft(self, spec, n_fft, hop, normalized=False):
+        spec = np.ascontiguousarray(spec, dtype=np.complex128)
+        T = spec.shape[1]
+        out = np.zeros(hop * (T - 1), dtype=np.float32)
+        rc = self._fn("torch_istft")(_np(spec), T, n_fft, hop, int(normalized), _np(out))
+        if rc:
+            raise RuntimeError(f"torch_istft rc={rc}")
+        return out
+
+    def htdemucs_spec(self, x, n_fft):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        hl = n_fft // 4
+        T = (x.size + hl - 1) // hl
+        spec = np.zeros((n_fft // 2, T), dtype=np.complex128)
+        nf = ctypes.c_int(0)
+        rc = self._fn("htdemucs_spec")(_np(x), x.size, n_fft, _np(spec), ctypes.byref(nf))
+        if rc:
+            raise RuntimeError(f"htdemucs_spec rc={rc}")
+        return spec
+
+    def htdemucs_ispec(self, spec, n_fft, length):
+        spec = np.ascontiguousarray(spec, dtype=np.complex128)
+        out = np.zeros(length, dtype=np.float32)
+        rc = self._fn("htdemucs_ispec")(_np(spec), spec.shape[1], n_fft, length, _np(out))
+        if rc:
+            raise RuntimeError(f"htdemucs_ispec rc={rc}")
+        return out
+
+
+_oracle = None
+
+
+def oracle():
+    global _oracle
+    if _oracle is None:
+        _oracle = _Stft(ORACLE_PATH, "orc_")
+    return _oracle
+
+
+def reference():
+    """The reference's own stft.h (raises OSError where oracle/_ref was not built)."""
+    return _Stft(REF_PATH, "ref_")
+
+
+def ref_available():
+    return os.path.exists(REF_PATH)

@@ -1,0 +1,192 @@
+"""GPU parity of the STFT family (stft.hip) against the oracle and the reference's golden vectors.
+
+Bound (north star): SNR >= 110 dB for spectra (the oracle's double spectrum is the reference)
+and for STFT -> iSTFT reconstructions, SNR = 10 log10(sum ref^2 / sum err^2)
+(tools/stems-parity.cpp:36). Layout changes are exact (bit-identical values).
+"""
+import glob
+import os
+
+import numpy as np
+import pytest
+
+import oracle_lib
+import stx
+import synth
+from metrics import snr_db
+
+pytestmark = pytest.mark.gpu
+
+SNR_DB = 110.0
+GOLDEN = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "stft_*.npz")))
+SPEC_GOLDEN = [p for p in GOLDEN if "torch" in p or "htdemucs" in p]
+
+
+@pytest.fixture(scope="module")
+def orc():
+    return oracle_lib.oracle()
+
+
+_plans = {}
+
+
+def plan(n):
+    if n not in _plans:
+        _plans[n] = stx.FFT(n)
+    return _plans[n]
+
+
+def to_dev(a, device):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+@pytest.mark.parametrize("path", SPEC_GOLDEN, ids=[os.path.basename(p)[5:-4] for p in SPEC_GOLDEN])
+@pytest.mark.parametrize("layout", [stx.F_MAJOR, stx.T_MAJOR])
+def test_golden_spectrum_and_inverse(device, path, layout):
+    d = np.load(path)
+    n = int(d["n_fft"])
+    x = to_dev(d["x"][None, :], device)
+    spec_ref = d["spec"]
+    if "torch" in path:
+        hop, nm = int(d["hop"]), bool(int(d["normalized"]))
+        spec = stx.torch_stft(plan(n), x, hop, nm, layout=layout)
+    else:
+        spec = stx.htdemucs_spec(plan(n), x, layout=layout)
+    got = host(spec)[0]
+    if layout == stx.T_MAJOR:
+        got = got.T
+    assert got.shape == spec_ref.shape
+    assert snr_db(got, spec_ref) >= SNR_DB
+    # Inverse of the reference spectrum rounded to complex64.
+    s = spec_ref.astype(np.complex64)[None]
+    sdev = to_dev(s if layout == stx.F_MAJOR else np.ascontiguousarray(s.transpose(0, 2, 1)), device)
+    if "torch" in path:
+        y = stx.torch_istft(plan(n), sdev, hop, nm, layout=layout)
+    else:
+        y = stx.htdemucs_ispec(plan(n), sdev, d["x"].size, layout=layout)
+    y = host(y)[0]
+    assert y.shape == d["y"].shape
+    assert snr_db(y, d["y"]) >= SNR_DB
+
+
+def _stereo(seed, length, sigma=0.1):
+    return synth.normal(seed, (2, length), sigma)
+
+
+def test_htdemucs_spec_c1_full_size(device, orc):
+    # HTDemucs spec: stereo 343,980 samples, n_fft 4096, hop 1024 -> [2][2048][336].
+    length = 343980
+    x = _stereo(2024, length)
+    f = plan(4096)
+    spec = stx.htdemucs_spec(f, to_dev(x, device))
+    y = stx.htdemucs_ispec(f, spec, length)
+    spec_h, y_h = host(spec), host(y)
+    assert spec_h.shape == (2, 2048, 336)
+    for c in range(2):
+        ref = orc.htdemucs_spec(x[c], 4096)
+        assert snr_db(spec_h[c], ref) >= SNR_DB
+        yref = orc.htdemucs_ispec(ref, 4096, length)
+        assert snr_db(y_h[c], yref) >= SNR_DB
+
+
+def test_torch_stft_c1_plain_call(device, orc):
+    length = 343980
+    x = _stereo(2025, length)
+    f = plan(4096)
+    spec = stx.torch_stft(f, to_dev(x, device), 1024)
+    y = stx.torch_istft(f, spec, 1024)
+    spec_h, y_h = host(spec), host(y)
+    assert spec_h.shape == (2, 2049, 336)
+    for c in range(2):
+        ref = orc.torch_stft(x[c], 4096, 1024)
+        assert snr_db(spec_h[c], ref) >= SNR_DB
+        assert snr_db(y_h[c], orc.torch_istft(ref, 4096, 1024)) >= SNR_DB
+        assert snr_db(y_h[c], x[c][: y_h.shape[1]]) >= SNR_DB
+
+
+@pytest.mark.parametrize("normalized", [False, True])
+def test_roformer_stft_c3_full_size(device, orc, normalized):
+    # RoFormer chunk: stereo 352,800 samples, n_fft 2048, hop 441 -> [2][1025][801] (odd T).
+    length = 352800
+    x = _stereo(2026, length)
+    f = plan(2048)
+    spec = stx.torch_stft(f, to_dev(x, device), 441, normalized)
+    spec_t = stx.torch_stft(f, to_dev(x, device), 441, normalized, layout=stx.T_MAJOR)
+    y = stx.torch_istft(f, spec, 441, normalized)
+    y_t = stx.torch_istft(f, spec_t, 441, normalized, layout=stx.T_MAJOR)
+    spec_h, spec_th, y_h, y_th = host(spec), host(spec_t), host(y), host(y_t)
+    assert spec_h.shape == (2, 1025, 801)
+    assert np.array_equal(spec_h, spec_th.transpose(0, 2, 1))
+    assert np.array_equal(y_h, y_th)
+    for c in range(2):
+        ref = orc.torch_stft(x[c], 2048, 441, normalized)
+        assert snr_db(spec_h[c], ref) >= SNR_DB
+        assert snr_db(y_h[c], orc.torch_istft(ref, 2048, 441, normalized)) >= SNR_DB
+        assert snr_db(y_h[c], x[c]) >= SNR_DB
+
+
+@pytest.mark.parametrize("n", [16, 32, 64, 128, 256, 512, 1024, 2048, 4096, 8192])
+def test_every_fft_size_stft_round_trip(device, orc, n):
+    hop = max(1, n // 4 - 1)
+    length = 3 * n + 5
+    x = _stereo(300 + n, length, 0.5)
+    f = plan(n)
+    spec = stx.torch_stft(f, to_dev(x, device), hop)
+    y = stx.torch_istft(f, spec, hop)
+    spec_h, y_h = host(spec), host(y)
+    for c in range(2):
+        ref = orc.torch_stft(x[c], n, hop)
+        assert snr_db(spec_h[c], ref) >= SNR_DB
+        assert snr_db(y_h[c], orc.torch_istft(ref, n, hop)) >= SNR_DB
+    if length > 3 * n // 8 * 2:
+        s2 = stx.htdemucs_spec(f, to_dev(x, device))
+        y2 = stx.htdemucs_ispec(f, s2, length)
+        s2h, y2h = host(s2), host(y2)
+        for c in range(2):
+            ref = orc.htdemucs_spec(x[c], n)
+            assert snr_db(s2h[c], ref) >= SNR_DB
+            assert snr_db(y2h[c], orc.htdemucs_ispec(ref, n, length)) >= SNR_DB
+
+
+@pytest.mark.parametrize("n", [16, 256, 2048, 4096, 8192])
+def test_fft_run_against_oracle(device, orc, n):
+    import torch
+    v = synth.normal(n, (3, 2 * n), 1.0).astype(np.float64)
+    a = v[:, 0::2] + 1j * v[:, 1::2]
+    d = to_dev(a.astype(np.complex64), device)
+    plan(n).run(d)
+    fw = host(d)
+    plan(n).run(d, inverse=True)
+    back = host(d) / n
+    for b in range(3):
+        assert snr_db(fw[b], orc.fft(a[b].astype(np.complex64).astype(np.complex128))) >= SNR_DB
+        assert snr_db(back[b], a[b].astype(np.complex64)) >= SNR_DB
+    del torch
+
+
+def test_fft_impulse_known_answer(device):
+    n = 2048
+    a = np.zeros((1, n), np.complex64)
+    a[0, 7] = 1.0
+    d = to_dev(a, device)
+    plan(n).run(d)
+    k = np.arange(n)
+    assert np.max(np.abs(host(d)[0] - np.exp(-2j * np.pi * 7 * k / n))) < 1e-6
+
+
+def test_stft_errors(device):
+    import torch
+    x = torch.zeros((1, 1024), dtype=torch.float32, device=device)
+    with pytest.raises(stx.StxError) as e:
+        stx.torch_stft(plan(2048), x, 441)
+    assert e.value.status == stx.STATUS_RUNTIME_ERROR
+    with pytest.raises(stx.StxError) as e:
+        stx.htdemucs_spec(plan(4096), x)
+    assert e.value.status == stx.STATUS_RUNTIME_ERROR
