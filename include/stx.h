@@ -115,6 +115,24 @@ STX_API stx_status stx_htdemucs_ispec(const stx_fft* fft, const float* spec, int
                                       int n_frames, int length, float* out,
                                       stx_spec_layout layout, stx_stream stream);
 
+/* Bytes of device workspace for the *_ws iSTFT variants: channels * n_frames * n floats. */
+STX_API size_t stx_istft_workspace_size(const stx_fft* fft, int channels, int n_frames);
+
+/* stx_torch_istft / stx_htdemucs_ispec with a caller-owned device workspace of at least
+ * stx_istft_workspace_size() bytes (INVALID_ARGUMENT if smaller). They inverse-transform each
+ * frame once into the workspace and overlap-add in a second kernel, which keeps every CU busy
+ * when there are few frames (one segment); the plain entry points need no workspace and
+ * transform frames shared by two output tiles twice. Results are the same to rounding.
+ * A NULL workspace selects the plain path. */
+STX_API stx_status stx_torch_istft_ws(const stx_fft* fft, const float* spec, int channels,
+                                      int n_frames, int hop, int normalized, float* out,
+                                      stx_spec_layout layout, void* workspace,
+                                      size_t workspace_bytes, stx_stream stream);
+STX_API stx_status stx_htdemucs_ispec_ws(const stx_fft* fft, const float* spec, int channels,
+                                         int n_frames, int length, float* out,
+                                         stx_spec_layout layout, void* workspace,
+                                         size_t workspace_bytes, stx_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

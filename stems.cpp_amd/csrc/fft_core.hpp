@@ -1,16 +1,23 @@
 // fft_core.hpp — the complex FFT building blocks of every spectral kernel.
 //
-// One complex N-point transform (N a power of two, 16 <= N <= 8192) is computed by N/16
-// threads with a self-sorting Stockham formulation: the first radix-16 pass runs straight on
-// registers loaded from global memory, the remaining passes (radix 16, then one radix 2/4/8
-// pass when log2 N is not a multiple of 4) exchange through LDS. Input and output are in
-// natural order, so no bit reversal is needed (the reference's radix-2 DIT does one,
-// src/stft.h:36). Twiddles come from a table of W_N^m = exp(-2*pi*i*m/N) computed once in
-// double precision and rounded to float, never from recurrences.
+// One complex M-point transform (M a power of two, 8 <= M <= 4096) is computed by M/P
+// threads holding P = 8 or 16 points each, with a self-sorting Stockham formulation: the
+// first radix-P pass runs straight on registers loaded from global memory, the remaining
+// passes (radix P, then one smaller radix when log_P M is not an integer) exchange through
+// LDS. Input and output are in natural order, so no bit reversal is needed (the reference's
+// radix-2 DIT does one, src/stft.h:36). P = 8 gives short waves (latency-bound small
+// batches), P = 16 the fewest LDS passes (throughput-bound large batches).
 //
-// Pass with radix R after sub-transforms of length Ns: butterfly jj in [0, N/R) reads
-// a[jj + r*N/R] (r < R), multiplies element r by W_{Ns*R}^{(jj mod Ns)*r}, takes an R-point
+// Pass with radix R after sub-transforms of length Ns: butterfly jj in [0, M/R) reads
+// a[jj + r*M/R] (r < R), multiplies element r by W_{Ns*R}^{(jj mod Ns)*r}, takes an R-point
 // DFT and writes element r to b[(jj / Ns)*Ns*R + (jj mod Ns) + r*Ns].
+//
+// Twiddles come from one table for TN points (TN = M for a complex transform, 2M for the
+// half-length transform of a real one, i.e. the real transform's n_fft):
+// W_TN^m = lo[m mod L] * hi[m / L] (L = 2^ceil(log2(TN)/2); at most 1.5 KB, staged in LDS at
+// kernel start, every entry computed in double and rounded to float once). A butterfly looks
+// up w^1, w^2, w^4, w^8 of its base twiddle and forms the other powers as products of those
+// (at most three deep): about 140 dB against an exact DFT, 2 dB below exact tables.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -26,13 +33,10 @@ STX_HD float2 cmul(float2 a, float2 b) {
 }
 STX_HD float2 cmul_mi(float2 a) { return make_float2(a.y, -a.x); }          // a * (-i)
 STX_HD float2 cconj(float2 a) { return make_float2(a.x, -a.y); }
+STX_HD float2 cscale(float2 a, float s) { return make_float2(a.x * s, a.y * s); }
 
 // Forward DFTs (kernel exp(-2*pi*i*n*k/R)) in natural order, in place on v[0..R).
 template <int R> struct Dft;
-
-template <> struct Dft<1> {
-    static STX_HD void run(float2*) {}
-};
 
 template <> struct Dft<2> {
     static STX_HD void run(float2* v) {
@@ -104,56 +108,134 @@ template <> struct Dft<16> {
     }
 };
 
-// LDS index with one float2 of padding every 16: spreads the radix-16 scatter of the first
-// pass (stride 16 float2 = 128 B) over all banks.
-STX_HD int lds_idx(int i) { return i + (i >> 4); }
+constexpr int ilog2(int n) { return n <= 1 ? 0 : 1 + ilog2(n / 2); }
 
-template <int N> struct FftShape {
-    static_assert(N >= 16 && N <= 8192 && (N & (N - 1)) == 0, "N must be a power of two in [16, 8192]");
-    static constexpr int TPJ = N / 16;               // threads per transform
-    static constexpr int PADN = N + N / 16;          // LDS float2 per transform
+// Two-level twiddle table for TN points: [L low entries W^m, m < L][H high entries W^(L*h)].
+template <int TN> struct TwTable {
+    static constexpr int LBITS = (ilog2(TN) + 1) / 2;
+    static constexpr int L = 1 << LBITS;
+    static constexpr int H = TN / L;
+    static constexpr int SIZE = L + H;
 };
 
-// First pass (Ns = 1, radix 16): v holds a[j + r*N/16] for r < 16 on entry. Writes the
-// result to LDS buffer `buf` (of one transform). No twiddles: jj mod 1 == 0.
-template <int N>
-__device__ __forceinline__ void fft_first_pass(float2* v, float2* buf, int j) {
-    Dft<16>::run(v);
+inline int twiddle_table_size(int tn) {
+    const int lb = (ilog2(tn) + 1) / 2;
+    return (1 << lb) + tn / (1 << lb);
+}
+
+// W_TN^m (0 <= m < TN) from the LDS copy of the table.
+template <int TN>
+__device__ __forceinline__ float2 tw_lookup(const float2* __restrict__ twt, int m) {
+    using T = TwTable<TN>;
+    return cmul(twt[m & (T::L - 1)], twt[T::L + (m >> T::LBITS)]);
+}
+
+// Copies the table to LDS; the caller's next barrier publishes it.
+template <int TN>
+__device__ __forceinline__ void stage_twiddles(float2* twt, const float2* __restrict__ g, int tid, int nt) {
+    for (int i = tid; i < TwTable<TN>::SIZE; i += nt) twt[i] = g[i];
+}
+
+// Shape of an M-point transform with P points per thread.
+template <int M, int P, int TN_> struct FftCfg {
+    static_assert(P == 8 || P == 16, "P must be 8 or 16");
+    static_assert(M >= P && M <= 8192 && (M & (M - 1)) == 0, "M must be a power of two in [P, 8192]");
+    static_assert(TN_ % M == 0, "the twiddle table must cover the transform");
+    static constexpr int TPJ = M / P;                 // threads per transform
+    static constexpr int TN = TN_;                    // twiddle table size
+    // LDS float2 per transform: the padded transform (one pad per P), at least M + 2 for the
+    // staged half spectra, rounded to even.
+    static constexpr int PADN = ((M + M / P > M + 2 ? M + M / P : M + 2) + 1) / 2 * 2;
+    static STX_HD int idx(int i) { return i + i / P; }
+};
+
+// w[r] = W_{Ns*R}^{k*r} = W_TN^{k*r*scale} for r < R, scale = TN / (Ns*R).
+template <int TN, int R>
+__device__ __forceinline__ void twiddle_powers(const float2* __restrict__ twt, int m1, float2* w) {
+    w[1] = tw_lookup<TN>(twt, m1);
+    if constexpr (R > 2) {
+        w[2] = tw_lookup<TN>(twt, 2 * m1);
+        w[3] = cmul(w[2], w[1]);
+    }
+    if constexpr (R > 4) {
+        w[4] = tw_lookup<TN>(twt, 4 * m1);
+        w[5] = cmul(w[4], w[1]);
+        w[6] = cmul(w[4], w[2]);
+        w[7] = cmul(w[4], w[3]);
+    }
+    if constexpr (R > 8) {
+        w[8] = tw_lookup<TN>(twt, 8 * m1);
 #pragma unroll
-    for (int r = 0; r < 16; r++) buf[lds_idx(j * 16 + r)] = v[r];
+        for (int r = 9; r < 16; r++) w[r] = cmul(w[8], w[r - 8]);
+    }
+}
+
+// First pass (Ns = 1, radix P): v holds a[j + r*M/P] for r < P on entry. Writes to the LDS
+// buffer, or, when it is also the last pass (M == P), to `sink` through `post`.
+template <int M, int P, int TN, class Post, class Sink>
+__device__ __forceinline__ void fft_first_pass(float2* v, float2* buf, int j, const Post& post, const Sink& sink) {
+    using C = FftCfg<M, P, TN>;
+    Dft<P>::run(v);
+#pragma unroll
+    for (int r = 0; r < P; r++) {
+        const int n = j * P + r;
+        if constexpr (M == P) sink(n, post(n, v[r]));
+        else buf[C::idx(n)] = v[r];
+    }
 }
 
 // Remaining passes, in place in `buf`. Every thread of the workgroup must call this (it
-// contains barriers), also threads whose transform is idle.
-template <int N, int Ns>
-__device__ __forceinline__ void fft_rest_passes(float2* buf, int j, const float2* __restrict__ tw) {
-    if constexpr (Ns < N) {
-        constexpr int R = (N / Ns >= 16) ? 16 : N / Ns;
-        constexpr int TPJ = N / 16;
-        constexpr int BPT = 16 / R;                  // butterflies per thread
-        constexpr int TSTRIDE = N / (Ns * R);        // W_{Ns*R}^e = W_N^(e*TSTRIDE)
-        float2 v[16];
+// contains barriers), also threads whose transform is idle. The last pass hands every output
+// element n (natural order) to sink(n, post(n, v)).
+template <int M, int P, int TN, int Ns, class Post, class Sink>
+__device__ __forceinline__ void fft_rest_passes(float2* buf, int j, const float2* __restrict__ twt,
+                                                const Post& post, const Sink& sink) {
+    if constexpr (Ns < M) {
+        using C = FftCfg<M, P, TN>;
+        constexpr int R = (M / Ns >= P) ? P : M / Ns;
+        constexpr int TPJ = C::TPJ;
+        constexpr int BPT = P / R;                    // butterflies per thread
+        constexpr int SCALE = C::TN / (Ns * R);       // W_{Ns*R}^e = W_TN^(e*SCALE)
+        constexpr bool LAST = (Ns * R == M);
+        float2 v[P];
 #pragma unroll
         for (int q = 0; q < BPT; q++) {
             const int jj = j + q * TPJ;
 #pragma unroll
-            for (int r = 0; r < R; r++) v[q * R + r] = buf[lds_idx(jj + r * (N / R))];
+            for (int r = 0; r < R; r++) v[q * R + r] = buf[C::idx(jj + r * (M / R))];
         }
         __syncthreads();
 #pragma unroll
         for (int q = 0; q < BPT; q++) {
             const int jj = j + q * TPJ;
             const int k = jj % Ns;
+            float2 w[R];
+            twiddle_powers<C::TN, R>(twt, k * SCALE, w);
 #pragma unroll
-            for (int r = 1; r < R; r++) v[q * R + r] = cmul(v[q * R + r], tw[k * r * TSTRIDE]);
+            for (int r = 1; r < R; r++) v[q * R + r] = cmul(v[q * R + r], w[r]);
             Dft<R>::run(&v[q * R]);
             const int base = (jj / Ns) * Ns * R + k;
 #pragma unroll
-            for (int r = 0; r < R; r++) buf[lds_idx(base + r * Ns)] = v[q * R + r];
+            for (int r = 0; r < R; r++) {
+                const int n = base + r * Ns;
+                if constexpr (LAST) sink(n, post(n, v[q * R + r]));
+                else buf[C::idx(n)] = v[q * R + r];
+            }
         }
         __syncthreads();
-        fft_rest_passes<N, Ns * R>(buf, j, tw);
+        fft_rest_passes<M, P, TN, Ns * R>(buf, j, twt, post, sink);
     }
 }
+
+struct NoPost {
+    __device__ __forceinline__ float2 operator()(int, float2 v) const { return v; }
+};
+
+// Sink writing into the transform's own LDS buffer (natural order).
+template <int P>
+struct ToLds {
+    float2* buf;
+    __device__ __forceinline__ void operator()(int n, float2 v) const { buf[n + n / P] = v; }
+};
 
 }  // namespace stx

@@ -3,18 +3,24 @@
 // Reference: src/stft.h (torch_stft :146-164, torch_istft :167-197, htdemucs_spec :79-103,
 // htdemucs_ispec :106-140). The reference runs one double-precision radix-2 FFT per frame on
 // the host. Here:
-//   * two real frames of one channel (t, t+1) share one complex N-point FFT
-//     (z = a + i*b, A[k] = (Z[k] + conj Z[N-k]) / 2, B[k] = (Z[k] - conj Z[N-k]) / 2i),
-//     which halves the arithmetic of a real transform;
+//   * every real frame of N samples is one complex N/2-point FFT of z[n] = x[2n] + i x[2n+1]
+//     followed by the split X[k] = E[k] + W_N^k O[k] with E = (Z[k] + conj Z[N/2-k]) / 2,
+//     O = (Z[k] - conj Z[N/2-k]) / 2i, which halves the arithmetic of a real transform and
+//     makes one job per frame;
 //   * the reflect padding of both modes (torch's center pad, and HTDemucs' extra pad before
 //     it) is index arithmetic on the load, so the padded signal is never materialised;
-//   * the inverse transform is the forward one on conjugated data (ifft(X) = conj fft conj X);
-//   * the iSTFT is an overlap-add in gather form: each workgroup owns a tile of output
-//     samples, inverse-transforms every frame that overlaps it (frames shared by two tiles
-//     are transformed by both, their spectra re-read from L2), accumulates the windowed
-//     frames in registers in frame order, and divides by the window-squared envelope, which
-//     is data independent and evaluated in closed form per sample. No atomics, no scratch,
-//     one pass over the spectrum and one over the output.
+//     frames that touch no padding skip it;
+//   * the inverse transform is the forward one on conjugated data (ifft(X) = conj fft conj X),
+//     after the inverse split Z' = (X[k] + conj X[N/2-k]) + i W_N^-k (X[k] - conj X[N/2-k]);
+//   * the iSTFT overlap-add is in gather form, without atomics, in one of two ways:
+//       - fused (no workspace): each workgroup owns a tile of output samples, inverse-
+//         transforms every frame that overlaps it (frames shared by two tiles are transformed
+//         by both), sums the windowed frames in frame order in registers and divides by the
+//         window-squared envelope, evaluated in closed form per sample;
+//       - two kernels (with a workspace of C*T*N floats): one inverse-transforms each frame
+//         once and writes it windowed to the workspace, the next sums and divides. This
+//         keeps every CU busy when there are few frames.
+#include <algorithm>
 #include <cmath>
 #include <vector>
 
@@ -24,19 +30,23 @@
 struct stx_fft {
     int n = 0;
     int device = 0;
-    float2* tw = nullptr;    // device [n]: W_n^m = exp(-2*pi*i*m/n)
+    float2* twt = nullptr;   // device: two-level twiddle table for n points (fft_core.hpp)
     float* win = nullptr;    // device [n]: periodic Hann
 };
 
 namespace stx {
 namespace {
 
+// floor(x / h) and ceil(x / h) for h > 0 and x of either sign.
+__device__ __forceinline__ int floordiv(int x, int h) { return x >= 0 ? x / h : -((-x + h - 1) / h); }
+__device__ __forceinline__ int ceildiv(int x, int h) { return -floordiv(-x, h); }
+
 // --------------------------------------------------------------------------------- STFT
 struct StftArgs {
     const float* x;          // [C][len]
     float2* spec;            // [C][F][T] or [C][T][F]
     const float* win;        // [N]
-    const float2* tw;        // [N]
+    const float2* twt;       // twiddle table for N
     int len;                 // samples per channel
     int len1;                // length of the pre-padded signal (len when there is no pre-pad)
     int pre_left;            // left size of the pre-pad (HTDemucs' pad, 0 for torch)
@@ -44,12 +54,10 @@ struct StftArgs {
     int frame0;              // padded index of frame 0's first sample
     int T;                   // frames per channel
     int F;                   // bins written per frame
-    int pairs;               // ceil(T / 2)
-    int jobs;                // channels * pairs
+    int jobs;                // channels * T
     int nblocks;             // real (logical) block count
     int layout;              // STX_SPEC_*
-    int vec4;                // F-major pair stores may use one 16-byte store
-    float half_scale;        // 0.5 * normalisation
+    float scale;             // normalisation
 };
 
 // torch reflect (edge not repeated): j < 0 -> -j; j >= n -> 2(n - 1) - j (src/stft.h:58-68).
@@ -68,67 +76,81 @@ __device__ __forceinline__ float padded_sample(const float* __restrict__ xc, int
     return xc[j];
 }
 
-template <int N, int JOBS>
-__global__ __launch_bounds__(JOBS * (N / 16)) void stft_kernel(StftArgs a) {
-    using S = FftShape<N>;
-    constexpr int TPJ = S::TPJ;
-    __shared__ float2 lds[JOBS * S::PADN];
+// One workgroup transforms JOBS consecutive frames (one per N/2/P threads), then writes them so
+// that neighbouring lanes store neighbouring addresses: consecutive frames of one bin row
+// (F-major) or consecutive bins of one frame (T-major).
+template <int N, int P, int JOBS>
+__global__ __launch_bounds__(JOBS * (N / 2 / P)) void stft_kernel(StftArgs a) {
+    constexpr int M = N / 2;
+    using C = FftCfg<M, P, N>;
+    constexpr int TPJ = C::TPJ;
+    constexpr int NT = JOBS * TPJ;
+    __shared__ float2 lds[JOBS * C::PADN];
+    __shared__ float2 twt[TwTable<N>::SIZE];
 
     const int lb = xcd_block();
     if (lb >= a.nblocks) return;                       // whole block idle: no barrier reached
-    const int slot = (int)threadIdx.x / TPJ;
-    const int j = (int)threadIdx.x % TPJ;
-    const int job = lb * JOBS + slot;
-    const bool active = job < a.jobs;
-    float2* buf = lds + slot * S::PADN;
+    const int tid = (int)threadIdx.x;
+    const int slot = tid / TPJ;
+    const int j = tid % TPJ;
+    const int f = lb * JOBS + slot;
+    const bool active = f < a.jobs;
+    float2* buf = lds + slot * C::PADN;
 
-    const int c = active ? job / a.pairs : 0;
-    const int t = active ? 2 * (job % a.pairs) : 0;
-    const bool has_b = active && (t + 1 < a.T);
+    const int c = active ? f / a.T : 0;
+    const int t = active ? f - c * a.T : 0;
     const float* xc = a.x + (size_t)c * a.len;
-    const int m0 = a.frame0 + t * a.hop;
+    const int m0 = a.frame0 + t * a.hop;               // padded index of the first sample
+    const int base = m0 - N / 2 - a.pre_left;          // its signal index when nothing reflects
+    const bool interior = base >= 0 && base + N <= a.len;
+    const float2* win2 = reinterpret_cast<const float2*>(a.win);
 
-    float2 v[16];
+    float2 v[P];
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
+    for (int r = 0; r < P; r++) {
         const int n = j + r * TPJ;
-        const float w = a.win[n];
-        float re = 0.f, im = 0.f;
+        const float2 w = win2[n];
+        float s0 = 0.f, s1 = 0.f;
         if (active) {
-            re = padded_sample<N>(xc, m0 + n, a) * w;
-            if (has_b) im = padded_sample<N>(xc, m0 + a.hop + n, a) * w;
-        }
-        v[r] = make_float2(re, im);
-    }
-    fft_first_pass<N>(v, buf, j);
-    __syncthreads();
-    fft_rest_passes<N, 16>(buf, j, a.tw);
-
-    if (!active) return;
-    // Separate the two real spectra and store bins k = j + q*TPJ (+ Nyquist).
-    const float hs = a.half_scale;
-    auto store = [&](int k) {
-        const float2 zk = buf[lds_idx(k)];
-        const float2 zm = buf[lds_idx((N - k) & (N - 1))];
-        const float2 A = make_float2((zk.x + zm.x) * hs, (zk.y - zm.y) * hs);
-        const float2 B = make_float2((zk.y + zm.y) * hs, (zm.x - zk.x) * hs);
-        if (a.layout == STX_SPEC_F_MAJOR) {
-            float2* p = a.spec + ((size_t)c * a.F + k) * a.T + t;
-            if (has_b && a.vec4) {
-                *reinterpret_cast<float4*>(p) = make_float4(A.x, A.y, B.x, B.y);
+            if (interior) {
+                s0 = xc[base + 2 * n];
+                s1 = xc[base + 2 * n + 1];
             } else {
-                p[0] = A;
-                if (has_b) p[1] = B;
+                s0 = padded_sample<N>(xc, m0 + 2 * n, a);
+                s1 = padded_sample<N>(xc, m0 + 2 * n + 1, a);
             }
-        } else {
-            float2* p = a.spec + ((size_t)c * a.T + t) * a.F + k;
-            p[0] = A;
-            if (has_b) p[a.F] = B;
         }
+        v[r] = make_float2(s0 * w.x, s1 * w.y);
+    }
+    stage_twiddles<N>(twt, a.twt, tid, NT);
+    fft_first_pass<M, P, N>(v, buf, j, NoPost{}, ToLds<P>{buf});
+    __syncthreads();
+    fft_rest_passes<M, P, N, P>(buf, j, twt, NoPost{}, ToLds<P>{buf});
+
+    // X[k] = E[k] + W_N^k O[k] for frame g of the block, k <= N/2.
+    const float hs = 0.5f * a.scale;
+    const int f0 = lb * JOBS;
+    const int c0 = f0 / a.T, t0 = f0 - c0 * a.T;
+    auto emit = [&](int k, int g) {
+        if (f0 + g >= a.jobs) return;
+        int tt = t0 + g, cc = c0;
+        while (tt >= a.T) { tt -= a.T; cc++; }
+        const float2* bs = lds + g * C::PADN;
+        const float2 zk = bs[C::idx(k & (M - 1))];
+        const float2 zm = bs[C::idx((M - k) & (M - 1))];
+        const float er = zk.x + zm.x, ei = zk.y - zm.y;       // 2E
+        const float orr = zk.y + zm.y, oi = zm.x - zk.x;      // 2O
+        const float2 w = tw_lookup<N>(twt, k);
+        const float2 val = make_float2((er + w.x * orr - w.y * oi) * hs, (ei + w.x * oi + w.y * orr) * hs);
+        if (a.layout == STX_SPEC_F_MAJOR) a.spec[((size_t)cc * a.F + k) * a.T + tt] = val;
+        else a.spec[((size_t)cc * a.T + tt) * a.F + k] = val;
     };
-#pragma unroll
-    for (int q = 0; q < 8; q++) store(j + q * TPJ);    // 8 * TPJ = N/2 bins
-    if (a.F > N / 2 && j == 0) store(N / 2);
+    if (a.layout == STX_SPEC_F_MAJOR) {
+        for (int e = tid; e < a.F * JOBS; e += NT) emit(e / JOBS, e % JOBS);
+    } else {
+        for (int g = 0; g < JOBS; g++)
+            for (int k = tid; k < a.F; k += NT) emit(k, g);
+    }
 }
 
 // -------------------------------------------------------------------------------- iSTFT
@@ -136,7 +158,8 @@ struct IstftArgs {
     const float2* spec;
     float* out;              // [C][out_len]
     const float* win;
-    const float2* tw;
+    const float2* twt;
+    float* frames;           // two-kernel path: [C][T][N] windowed frames
     int T;                   // spectrum frames
     int F;                   // bins per frame in spec
     int layout;
@@ -147,53 +170,134 @@ struct IstftArgs {
     int out_len;             // samples per channel
     int valid_end;           // out[i] = 0 where out_off + i >= valid_end
     int keep_nyquist;        // 1: Nyquist real part used (torch); 0: Nyquist zeroed (HTDemucs)
-    int tiles;               // tiles per channel
-    int nblocks;             // channels * tiles
+    int tile_origin;         // fused: full-signal index where tile 0 starts
+    int tile_len;            // fused: full-signal samples per tile
+    int tiles;               // fused: tiles per channel
+    int jobs;                // two-kernel: channels * T
+    int nblocks;
     float norm;
 };
 
-template <int N>
-__device__ __forceinline__ float2 load_bin(const IstftArgs& a, const float2* __restrict__ sc, int st, int k) {
-    if (a.layout == STX_SPEC_F_MAJOR) return sc[(size_t)k * a.T + st];
-    return sc[(size_t)st * a.F + k];
+__device__ __forceinline__ float2 spec_bin(const IstftArgs& a, const float2* __restrict__ sc, int st, int k) {
+    return a.layout == STX_SPEC_F_MAJOR ? sc[(size_t)k * a.T + st] : sc[(size_t)st * a.F + k];
 }
 
-// conj(Z[k]) where Z = A + iB is the full (Hermitian-extended) spectrum of frames sa, sb.
+// conj Z'[k] for k < N/2 from X[k] and X[N/2 - k] of one frame: the inverse split, with the
+// DC and Nyquist imaginary parts ignored (src/stft.h:121,177,182) and the Nyquist bin zeroed
+// for HTDemucs (:126).
 template <int N>
-__device__ __forceinline__ float2 load_pair_bin(const IstftArgs& a, const float2* __restrict__ sc,
-                                                int sa, bool ha, int sb, bool hb, int k) {
-    float2 A = make_float2(0.f, 0.f), B = make_float2(0.f, 0.f);
-    float2 z;
+__device__ __forceinline__ float2 inverse_split(float2 xk, float2 xm, int k, int keep_nyquist,
+                                                const float2* __restrict__ twt) {
     if (k == 0) {
-        if (ha) A = load_bin<N>(a, sc, sa, 0);
-        if (hb) B = load_bin<N>(a, sc, sb, 0);
-        z = make_float2(A.x, B.x);                       // DC imaginary parts ignored
-    } else if (k < N / 2) {
-        if (ha) A = load_bin<N>(a, sc, sa, k);
-        if (hb) B = load_bin<N>(a, sc, sb, k);
-        z = make_float2(A.x - B.y, A.y + B.x);
-    } else if (k == N / 2) {
-        if (a.keep_nyquist) {
-            if (ha) A = load_bin<N>(a, sc, sa, k);
-            if (hb) B = load_bin<N>(a, sc, sb, k);
-        }
-        z = make_float2(A.x, B.x);                       // Nyquist imaginary parts ignored
-    } else {
-        const int m = N - k;
-        if (ha) A = load_bin<N>(a, sc, sa, m);
-        if (hb) B = load_bin<N>(a, sc, sb, m);
-        z = make_float2(A.x + B.y, B.x - A.y);
+        xk = make_float2(xk.x, 0.f);
+        xm = keep_nyquist ? make_float2(xm.x, 0.f) : make_float2(0.f, 0.f);
     }
-    return cconj(z);
+    const float er = xk.x + xm.x, ei = xk.y - xm.y;          // X[k] + conj X[M-k]
+    const float dr = xk.x - xm.x, di = xk.y + xm.y;          // X[k] - conj X[M-k]
+    const float2 w = tw_lookup<N>(twt, k);                   // times conj(W_N^k)
+    const float orr = dr * w.x + di * w.y, oi = di * w.x - dr * w.y;
+    return make_float2(er - oi, -(ei + orr));                // conj(E' + i O')
 }
 
-template <int N, int JOBS, int PER>
-__global__ __launch_bounds__(JOBS * (N / 16)) void istft_kernel(IstftArgs a) {
-    using S = FftShape<N>;
-    constexpr int TPJ = S::TPJ;
+// Windowed output of the inverse transform: z[n] = conj(fft(conj Z'))[n] holds samples
+// 2n (real) and 2n + 1 (imaginary); returns them times win * norm.
+struct WindowPost {
+    const float2* win2;
+    float norm;
+    __device__ __forceinline__ float2 operator()(int n, float2 r) const {
+        const float2 w = win2[n];
+        return make_float2(r.x * w.x * norm, -r.y * w.y * norm);
+    }
+};
+
+// Two-kernel path, step 1: one inverse transform per frame, written windowed to the workspace.
+template <int N, int P, int JOBS>
+__global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_frames_kernel(IstftArgs a) {
+    constexpr int M = N / 2;
+    using C = FftCfg<M, P, N>;
+    constexpr int TPJ = C::TPJ;
     constexpr int NT = JOBS * TPJ;
-    constexpr int OT = PER * NT;                         // output samples per tile
-    __shared__ float2 lds[JOBS * S::PADN];
+    __shared__ float2 lds[JOBS * C::PADN];
+    __shared__ float2 twt[TwTable<N>::SIZE];
+    __shared__ float wl[N];
+
+    const int lb = xcd_block();
+    if (lb >= a.nblocks) return;
+    const int tid = (int)threadIdx.x;
+    const int slot = tid / TPJ;
+    const int j = tid % TPJ;
+    const int f = lb * JOBS + slot;
+    const bool active = f < a.jobs;
+    float2* buf = lds + slot * C::PADN;
+    const int c = active ? f / a.T : 0;
+    const int st = active ? f - c * a.T : 0;
+    const float2* sc = a.spec + (size_t)c * a.T * a.F;
+
+    float2 xk[P], xm[P];
+#pragma unroll
+    for (int r = 0; r < P; r++) {
+        const int k = j + r * TPJ;
+        xk[r] = active ? spec_bin(a, sc, st, k) : make_float2(0.f, 0.f);
+        const int km = M - k;
+        xm[r] = (active && (km < M || a.keep_nyquist)) ? spec_bin(a, sc, st, km) : make_float2(0.f, 0.f);
+    }
+    stage_twiddles<N>(twt, a.twt, tid, NT);
+    for (int i = tid; i < N; i += NT) wl[i] = a.win[i];
+    __syncthreads();
+    float2 v[P];
+#pragma unroll
+    for (int r = 0; r < P; r++) v[r] = inverse_split<N>(xk[r], xm[r], j + r * TPJ, a.keep_nyquist, twt);
+
+    const WindowPost post{reinterpret_cast<const float2*>(wl), a.norm};
+    float2* dst = reinterpret_cast<float2*>(a.frames + (size_t)f * N);
+    auto sink = [&](int n, float2 val) {
+        if (active) dst[n] = val;
+    };
+    fft_first_pass<M, P, N>(v, buf, j, post, sink);
+    __syncthreads();
+    fft_rest_passes<M, P, N, P>(buf, j, twt, post, sink);
+}
+
+// Two-kernel path, step 2: out = sum of the windowed frames over the frames covering each
+// sample, in frame order, divided by the window-squared envelope.
+__global__ __launch_bounds__(256) void istft_ola_kernel(IstftArgs a, int N) {
+    const int i = (int)(blockIdx.x * 256 + threadIdx.x);
+    const int c = (int)blockIdx.y;
+    if (i >= a.out_len) return;
+    const int J = a.out_off + i;
+    float y = 0.f;
+    if (J < a.valid_end) {
+        const int hop = a.hop;
+        const int lo = max(0, ceildiv(J - N + 1, hop));
+        const int hi = min(a.env_frames - 1, J / hop);
+        const float* fc = a.frames + (size_t)c * a.T * N;
+        float env = 0.f, sum = 0.f;
+        for (int tf = lo; tf <= hi; tf++) {
+            const int s = J - tf * hop;
+            const float w = a.win[s];
+            env += w * w;
+            const int st = tf - a.frame_off;
+            if (st >= 0 && st < a.T) sum += fc[(size_t)st * N + s];
+        }
+        y = env > 1e-11f ? sum / env : 0.f;
+    }
+    a.out[(size_t)c * a.out_len + i] = y;
+}
+
+// Fused path: one workgroup owns a tile of output samples and inverse-transforms, JOBS frames
+// at a time (normally all at once), every frame that overlaps it; the last FFT pass applies
+// window * norm; each thread sums its samples over the overlapping frames in frame order and
+// divides by the window-squared envelope.
+template <int N, int P, int JOBS, int PER>
+__global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) {
+    constexpr int M = N / 2;
+    using C = FftCfg<M, P, N>;
+    constexpr int TPJ = C::TPJ;
+    constexpr int NT = JOBS * TPJ;
+    constexpr bool WIN_LDS = (size_t)JOBS * C::PADN * 8 + TwTable<N>::SIZE * 8 + N * 4 <= 160 * 1024;
+    __shared__ float2 lds[JOBS * C::PADN];
+    __shared__ float2 twt[TwTable<N>::SIZE];
+    __shared__ float wl[WIN_LDS ? N : 2];
 
     const int lb = xcd_block();
     if (lb >= a.nblocks) return;
@@ -202,44 +306,71 @@ __global__ __launch_bounds__(JOBS * (N / 16)) void istft_kernel(IstftArgs a) {
     const int tid = (int)threadIdx.x;
     const int slot = tid / TPJ;
     const int j = tid % TPJ;
-    float2* buf = lds + slot * S::PADN;
+    float2* buf = lds + slot * C::PADN;
+    const int hop = a.hop;
 
-    const int i0 = tile * OT;
-    const int i1 = min(i0 + OT, a.out_len);
-    const int J0 = a.out_off + i0, J1 = a.out_off + i1;
+    stage_twiddles<N>(twt, a.twt, tid, NT);
+    if constexpr (WIN_LDS)
+        for (int i = tid; i < N; i += NT) wl[i] = a.win[i];
+    const float* win = WIN_LDS ? wl : a.win;
+
+    const int J0 = max(a.out_off, a.tile_origin + tile * a.tile_len);
+    const int J1 = min(a.out_off + a.out_len, a.tile_origin + (tile + 1) * a.tile_len);
     // Spectrum frames overlapping [J0, J1): envelope frame tf covers [tf*hop, tf*hop + N).
-    const int tf_lo = max(0, (J0 - N + 1 + a.hop - 1) / a.hop);   // J0 - N + 1 may be < 0: clamped
-    const int tf_hi = (J1 - 1) / a.hop;
-    const int st_lo = max(0, max(tf_lo, 0) - a.frame_off);
-    const int st_hi = min(a.T - 1, tf_hi - a.frame_off);
+    const int st_lo = max(0, max(0, ceildiv(J0 - N + 1, hop)) - a.frame_off);
+    const int st_hi = min(a.T - 1, floordiv(J1 - 1, hop) - a.frame_off);
     const float2* sc = a.spec + (size_t)c * a.T * a.F;
+    const WindowPost post{reinterpret_cast<const float2*>(win), a.norm};
 
     float acc[PER];
 #pragma unroll
     for (int q = 0; q < PER; q++) acc[q] = 0.f;
 
-    for (int s0 = st_lo; s0 <= st_hi; s0 += 2 * JOBS) {
-        const int sa = s0 + 2 * slot, sb = sa + 1;
-        const bool ha = sa <= st_hi, hb = sb <= st_hi;
-        float2 v[16];
-#pragma unroll
-        for (int r = 0; r < 16; r++) v[r] = load_pair_bin<N>(a, sc, sa, ha, sb, hb, j + r * TPJ);
-        fft_first_pass<N>(v, buf, j);
+    for (int s0 = st_lo; s0 <= st_hi; s0 += JOBS) {
+        // An opaque copy of the lane index: keeps the compiler from hoisting the (round
+        // invariant) twiddle reads out of this loop, which would hold them in registers.
+        int jr = j;
+        asm volatile("" : "+v"(jr));
+        // Stage X[0..M] of frame s0 + g into slot g, neighbouring lanes on neighbouring
+        // addresses in either layout.
+        auto stage = [&](int k, int g) {
+            const int st = s0 + g;
+            float2 val = make_float2(0.f, 0.f);
+            if (st <= st_hi && k < a.F) val = spec_bin(a, sc, st, k);
+            lds[g * C::PADN + k] = val;
+        };
+        if (a.layout == STX_SPEC_F_MAJOR) {
+            for (int e = tid; e < (M + 1) * JOBS; e += NT) stage(e / JOBS, e % JOBS);
+        } else {
+            for (int g = 0; g < JOBS; g++)
+                for (int k = tid; k <= M; k += NT) stage(k, g);
+        }
         __syncthreads();
-        fft_rest_passes<N, 16>(buf, j, a.tw);
-        // buf[n] = fft(conj Z)[n]: frame sa is Re, frame sb is -Im (times N).
+        float2 v[P];
+#pragma unroll
+        for (int r = 0; r < P; r++) {
+            const int k = jr + r * TPJ;
+            v[r] = inverse_split<N>(buf[k], buf[M - k], k, a.keep_nyquist, twt);
+        }
+        __syncthreads();                            // staging read before the FFT overwrites it
+        fft_first_pass<M, P, N>(v, buf, jr, post, ToLds<P>{buf});
+        __syncthreads();
+        fft_rest_passes<M, P, N, P>(buf, jr, twt, post, ToLds<P>{buf});
+        // Slot g now holds samples (2n, 2n + 1) of frame s0 + g at LDS index n, windowed.
+        const int s_end = min(st_hi, s0 + JOBS - 1);
 #pragma unroll
         for (int q = 0; q < PER; q++) {
             const int J = J0 + q * NT + tid;
-#pragma unroll
-            for (int s = 0; s < JOBS; s++) {
-                const int fa = s0 + 2 * s;
-                const float2* bs = lds + s * S::PADN;
-                const int na = J - (fa + a.frame_off) * a.hop;
-                if (fa <= st_hi && na >= 0 && na < N) acc[q] += bs[lds_idx(na)].x * a.win[na];
-                const int nb = na - a.hop;
-                if (fa + 1 <= st_hi && nb >= 0 && nb < N) acc[q] -= bs[lds_idx(nb)].y * a.win[nb];
+            if (J >= J1) continue;
+            const int lo = max(s0, ceildiv(J - N + 1, hop) - a.frame_off);
+            const int hi = min(s_end, J / hop - a.frame_off);
+            float sum = acc[q];
+            for (int st = lo; st <= hi; st++) {
+                const int s = J - (st + a.frame_off) * hop;
+                const float2 z = lds[(st - s0) * C::PADN + C::idx(s >> 1)];
+                sum += (s & 1) ? z.y : z.x;
             }
+            acc[q] = sum;
         }
         __syncthreads();
     }
@@ -247,92 +378,117 @@ __global__ __launch_bounds__(JOBS * (N / 16)) void istft_kernel(IstftArgs a) {
     float* oc = a.out + (size_t)c * a.out_len;
 #pragma unroll
     for (int q = 0; q < PER; q++) {
-        const int i = i0 + q * NT + tid;
-        if (i >= i1) continue;
-        const int J = a.out_off + i;
+        const int J = J0 + q * NT + tid;
+        if (J >= J1) continue;
         float y = 0.f;
         if (J < a.valid_end) {
             // Envelope: sum of win^2 over every frame covering J (src/stft.h:130,187).
-            const int lo = max(0, (J - N + a.hop) / a.hop);
-            const int hi = min(a.env_frames - 1, J / a.hop);
+            const int lo = max(0, ceildiv(J - N + 1, hop));
+            const int hi = min(a.env_frames - 1, J / hop);
             float env = 0.f;
             for (int tf = lo; tf <= hi; tf++) {
-                const int n = J - tf * a.hop;
-                if (n >= 0 && n < N) {
-                    const float w = a.win[n];
-                    env += w * w;
-                }
+                const float w = win[J - tf * hop];
+                env += w * w;
             }
-            y = env > 1e-11f ? acc[q] * a.norm / env : 0.f;
+            y = env > 1e-11f ? acc[q] / env : 0.f;
         }
-        oc[i] = y;
+        oc[J - a.out_off] = y;
     }
 }
 
 // ------------------------------------------------------------------------ plain FFT
-template <int N, int JOBS>
-__global__ __launch_bounds__(JOBS * (N / 16)) void fft_kernel(float2* data, int batch, int inverse,
-                                                              const float2* __restrict__ tw, int nblocks) {
-    using S = FftShape<N>;
-    constexpr int TPJ = S::TPJ;
-    __shared__ float2 lds[JOBS * S::PADN];
+template <int N, int P, int JOBS>
+__global__ __launch_bounds__(JOBS * (N / P)) void fft_kernel(float2* data, int batch, int inverse,
+                                                             const float2* __restrict__ gtw, int nblocks) {
+    using C = FftCfg<N, P, N>;
+    constexpr int TPJ = C::TPJ;
+    __shared__ float2 lds[JOBS * C::PADN];
+    __shared__ float2 twt[TwTable<N>::SIZE];
     const int lb = xcd_block();
     if (lb >= nblocks) return;
-    const int slot = (int)threadIdx.x / TPJ;
-    const int j = (int)threadIdx.x % TPJ;
+    const int tid = (int)threadIdx.x;
+    const int slot = tid / TPJ;
+    const int j = tid % TPJ;
     const int job = lb * JOBS + slot;
     const bool active = job < batch;
-    float2* buf = lds + slot * S::PADN;
+    float2* buf = lds + slot * C::PADN;
     float2* d = data + (size_t)(active ? job : 0) * N;
-    float2 v[16];
+    float2 v[P];
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-        float2 x = active ? d[j + r * TPJ] : make_float2(0.f, 0.f);
+    for (int r = 0; r < P; r++) {
+        const float2 x = active ? d[j + r * TPJ] : make_float2(0.f, 0.f);
         v[r] = inverse ? cconj(x) : x;
     }
-    fft_first_pass<N>(v, buf, j);
+    stage_twiddles<N>(twt, gtw, tid, JOBS * TPJ);
+    auto sink = [&](int k, float2 y) {
+        if (active) d[k] = inverse ? cconj(y) : y;
+    };
+    fft_first_pass<N, P, N>(v, buf, j, NoPost{}, sink);
     __syncthreads();
-    fft_rest_passes<N, 16>(buf, j, tw);
-    if (!active) return;
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-        const int k = j + r * TPJ;
-        const float2 y = buf[lds_idx(k)];
-        d[k] = inverse ? cconj(y) : y;
-    }
+    fft_rest_passes<N, P, N, P>(buf, j, twt, NoPost{}, sink);
 }
 
 // ------------------------------------------------------------------------ dispatch
-constexpr int jobs_per_block(int n) { return n >= 4096 ? 1 : 4096 / n; }
+constexpr int block_jobs(int tpj, int threads) { return tpj >= threads ? 1 : threads / tpj; }
+constexpr int kIstftPer = 6;                           // fused: output samples per thread per tile
+
+// Points per thread: 8 keeps waves short for the small, latency-bound batches of one
+// segment; the fused iSTFT uses 16 so that one workgroup holds as many frames as possible.
+constexpr int kStftP = 8;
+constexpr int fused_p(int n) { return n / 2 >= 16 ? 16 : 8; }
 
 template <int N>
 void launch_stft(const StftArgs& a0, hipStream_t s) {
-    constexpr int JOBS = jobs_per_block(N);
+    constexpr int P = kStftP;
+    constexpr int TPJ = N / 2 / P;
+    constexpr int JOBS = block_jobs(TPJ, 256);
     StftArgs a = a0;
     a.nblocks = (a.jobs + JOBS - 1) / JOBS;
-    hipLaunchKernelGGL((stft_kernel<N, JOBS>), dim3(xcd_grid(a.nblocks)), dim3(JOBS * (N / 16)), 0, s, a);
+    hipLaunchKernelGGL((stft_kernel<N, P, JOBS>), dim3(xcd_grid(a.nblocks)), dim3(JOBS * TPJ), 0, s, a);
     launch_check("stft_kernel");
 }
 
-constexpr int kIstftPer = 16;
-
 template <int N>
-void launch_istft(IstftArgs a, int channels, hipStream_t s) {
-    constexpr int JOBS = jobs_per_block(N);
-    constexpr int OT = kIstftPer * JOBS * (N / 16);
-    a.tiles = (a.out_len + OT - 1) / OT;
+void launch_istft_fused(IstftArgs a, int channels, hipStream_t s) {
+    constexpr int P = fused_p(N);
+    constexpr int TPJ = N / 2 / P;
+    constexpr int JOBS = block_jobs(TPJ, 1024);
+    constexpr int NT = JOBS * TPJ;
+    // Tiles of m hops need m + ceil(N/hop) - 1 frames; pick m so that they fit one round of
+    // JOBS frames, within the PER*NT samples the threads accumulate.
+    const int span = (N + a.hop - 1) / a.hop;
+    const long long m = std::max(1, JOBS - span + 1);
+    const long long tile_len = std::min<long long>(m * a.hop, (long long)kIstftPer * NT);
+    a.tile_len = (int)tile_len;
+    a.tile_origin = (tile_len % a.hop == 0) ? a.out_off - a.out_off % a.hop : a.out_off;
+    const long long end = (long long)a.out_off + a.out_len;
+    a.tiles = (int)((end - a.tile_origin + tile_len - 1) / tile_len);
     a.nblocks = a.tiles * channels;
-    hipLaunchKernelGGL((istft_kernel<N, JOBS, kIstftPer>), dim3(xcd_grid(a.nblocks)),
-                       dim3(JOBS * (N / 16)), 0, s, a);
+    hipLaunchKernelGGL((istft_kernel<N, P, JOBS, kIstftPer>), dim3(xcd_grid(a.nblocks)), dim3(NT), 0, s, a);
     launch_check("istft_kernel");
 }
 
 template <int N>
-void launch_fft(float2* data, int batch, int inverse, const float2* tw, hipStream_t s) {
-    constexpr int JOBS = jobs_per_block(N);
+void launch_istft_two_step(IstftArgs a, int channels, hipStream_t s) {
+    constexpr int P = kStftP;
+    constexpr int TPJ = N / 2 / P;
+    constexpr int JOBS = block_jobs(TPJ, 256);
+    a.jobs = channels * a.T;
+    a.nblocks = (a.jobs + JOBS - 1) / JOBS;
+    hipLaunchKernelGGL((istft_frames_kernel<N, P, JOBS>), dim3(xcd_grid(a.nblocks)), dim3(JOBS * TPJ), 0, s, a);
+    launch_check("istft_frames_kernel");
+    hipLaunchKernelGGL(istft_ola_kernel, dim3((a.out_len + 255) / 256, channels), dim3(256), 0, s, a, N);
+    launch_check("istft_ola_kernel");
+}
+
+template <int N>
+void launch_fft(float2* data, int batch, int inverse, const float2* twt, hipStream_t s) {
+    constexpr int P = N >= 16 ? 16 : 8;
+    constexpr int TPJ = N / P;
+    constexpr int JOBS = block_jobs(TPJ, 256);
     const int nblocks = (batch + JOBS - 1) / JOBS;
-    hipLaunchKernelGGL((fft_kernel<N, JOBS>), dim3(xcd_grid(nblocks)), dim3(JOBS * (N / 16)), 0, s,
-                       data, batch, inverse, tw, nblocks);
+    hipLaunchKernelGGL((fft_kernel<N, P, JOBS>), dim3(xcd_grid(nblocks)), dim3(JOBS * TPJ), 0, s,
+                       data, batch, inverse, twt, nblocks);
     launch_check("fft_kernel");
 }
 
@@ -354,7 +510,10 @@ void by_size(int n, Args&&... args) {
 }
 template <int N> struct StftL { static void go(const StftArgs& a, hipStream_t s) { launch_stft<N>(a, s); } };
 template <int N> struct IstftL {
-    static void go(const IstftArgs& a, int ch, hipStream_t s) { launch_istft<N>(a, ch, s); }
+    static void go(const IstftArgs& a, int ch, bool two_step, hipStream_t s) {
+        if (two_step) launch_istft_two_step<N>(a, ch, s);
+        else launch_istft_fused<N>(a, ch, s);
+    }
 };
 template <int N> struct FftL {
     static void go(float2* d, int b, int inv, const float2* tw, hipStream_t s) { launch_fft<N>(d, b, inv, tw, s); }
@@ -373,6 +532,97 @@ void check_extent(long long elems, const char* what) {
     STX_REQUIRE(elems >= 0 && elems < (1LL << 31), "%s too large (%lld elements)", what, elems);
 }
 
+size_t istft_workspace_bytes(int n, int channels, int n_frames) {
+    return sizeof(float) * (size_t)n * (size_t)std::max(channels, 0) * (size_t)std::max(n_frames, 0);
+}
+
+// Shared body of the four iSTFT entry points.
+void run_istft(const stx_fft* f, IstftArgs a, int channels, void* workspace, size_t ws_bytes, hipStream_t s) {
+    const bool two_step = workspace != nullptr;
+    if (two_step) {
+        const size_t need = istft_workspace_bytes(f->n, channels, a.T);
+        STX_REQUIRE(ws_bytes >= need, "workspace too small: %zu bytes, need %zu", ws_bytes, need);
+        check_extent((long long)channels * a.T * f->n, "workspace");
+        a.frames = static_cast<float*>(workspace);
+    }
+    by_size<IstftL>(f->n, a, channels, two_step, s);
+}
+
+stx_status torch_istft_impl(const stx_fft* f, const float* spec, int channels, int n_frames, int hop,
+                            int normalized, float* out, stx_spec_layout layout, void* ws, size_t ws_bytes,
+                            stx_stream stream) {
+    return guard([&] {
+        check_fft(f);
+        check_layout(layout);
+        const int n = f->n;
+        STX_REQUIRE(channels >= 0 && hop > 0 && n_frames >= 1, "bad channels/hop/n_frames");
+        const long long length = (long long)hop * (n_frames - 1);
+        check_extent(length + n, "signal");
+        check_extent((long long)channels * n_frames * (n / 2 + 1), "spectrum");
+        check_extent((long long)channels * length, "output");
+        if (channels == 0 || length == 0) return;
+        STX_REQUIRE(spec && out, "NULL buffer");
+        IstftArgs a{};
+        a.spec = reinterpret_cast<const float2*>(spec);
+        a.out = out;
+        a.win = f->win;
+        a.twt = f->twt;
+        a.T = n_frames;
+        a.F = n / 2 + 1;
+        a.layout = layout;
+        a.hop = hop;
+        a.env_frames = n_frames;
+        a.frame_off = 0;
+        a.out_off = n / 2;
+        a.out_len = (int)length;
+        a.valid_end = (int)(n + (long long)hop * (n_frames - 1));
+        a.keep_nyquist = 1;
+        a.norm = (float)((normalized ? std::sqrt((double)n) : 1.0) / n);
+        run_istft(f, a, channels, ws, ws_bytes, as_stream(stream));
+    });
+}
+
+stx_status htdemucs_ispec_impl(const stx_fft* f, const float* spec, int channels, int n_frames, int length,
+                               float* out, stx_spec_layout layout, void* ws, size_t ws_bytes, stx_stream stream) {
+    return guard([&] {
+        check_fft(f);
+        check_layout(layout);
+        const int n = f->n, hl = n / 4, pad = hl / 2 * 3;
+        STX_REQUIRE(channels >= 0 && n_frames >= 0 && length >= 0, "bad channels/n_frames/length");
+        const long long frames = (long long)n_frames + 4;             // two zero frames each side
+        const long long full = n + (long long)hl * (frames - 1);
+        const long long le_out = (long long)hl * ((length + hl - 1) / hl) + 2 * pad;
+        check_extent(full + length, "signal");
+        check_extent((long long)channels * n_frames * (n / 2), "spectrum");
+        check_extent((long long)channels * length, "output");
+        if (channels == 0 || length == 0) return;
+        STX_REQUIRE(spec && out, "NULL buffer");
+        if (n_frames == 0) {
+            hip_check(hipMemsetAsync(out, 0, sizeof(float) * (size_t)channels * length, as_stream(stream)),
+                      "hipMemsetAsync");
+            return;
+        }
+        IstftArgs a{};
+        a.spec = reinterpret_cast<const float2*>(spec);
+        a.out = out;
+        a.win = f->win;
+        a.twt = f->twt;
+        a.T = n_frames;
+        a.F = n / 2;
+        a.layout = layout;
+        a.hop = hl;
+        a.env_frames = (int)frames;
+        a.frame_off = 2;
+        a.out_off = n / 2 + pad;
+        a.out_len = length;
+        // out[i] = 0 where j - n/2 >= le_out or j >= full (src/stft.h:135-136), j = n/2 + pad + i.
+        a.valid_end = (int)std::min(full, le_out + n / 2);
+        a.keep_nyquist = 0;
+        a.norm = (float)(std::sqrt((double)n) / n);
+        run_istft(f, a, channels, ws, ws_bytes, as_stream(stream));
+    });
+}
+
 }  // namespace
 }  // namespace stx
 
@@ -387,20 +637,22 @@ STX_API stx_status stx_fft_create(int n, stx_fft** out) {
         // st::FFT's own check (src/stft.h:22).
         if (n < 2 || (n & (n - 1))) fail(STX_STATUS_INVALID_ARGUMENT, "FFT size must be a power of two");
         if (n < 16 || n > 8192) fail(STX_STATUS_UNSUPPORTED, "FFT size %d has no kernel (supported: 16..8192)", n);
-        std::vector<float2> tw(n);
+        const int lbits = (ilog2(n) + 1) / 2, L = 1 << lbits, H = n / L;
+        std::vector<float2> twt(L + H);
+        auto w_n = [n](long long m) {
+            const double th = 2.0 * M_PI * (double)m / n;
+            return make_float2((float)std::cos(th), (float)-std::sin(th));
+        };
+        for (int m = 0; m < L; m++) twt[m] = w_n(m);
+        for (int h = 0; h < H; h++) twt[L + h] = w_n((long long)h * L);
         std::vector<float> win(n);
-        for (int m = 0; m < n; m++) {
-            const double th = 2.0 * M_PI * m / n;
-            tw[m] = make_float2((float)std::cos(th), (float)-std::sin(th));
-            // hann_periodic (src/stft.h:70-74), in double, rounded once.
-            win[m] = (float)(0.5 - 0.5 * std::cos(2.0 * M_PI * m / n));
-        }
+        for (int m = 0; m < n; m++) win[m] = (float)(0.5 - 0.5 * std::cos(2.0 * M_PI * m / n));   // hann_periodic (src/stft.h:70-74)
         stx_fft* f = new stx_fft;
         f->n = n;
         hipError_t e = hipGetDevice(&f->device);
-        if (e == hipSuccess) e = hipMalloc(&f->tw, sizeof(float2) * n);
+        if (e == hipSuccess) e = hipMalloc(&f->twt, sizeof(float2) * twt.size());
         if (e == hipSuccess) e = hipMalloc(&f->win, sizeof(float) * n);
-        if (e == hipSuccess) e = hipMemcpy(f->tw, tw.data(), sizeof(float2) * n, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(f->twt, twt.data(), sizeof(float2) * twt.size(), hipMemcpyHostToDevice);
         if (e == hipSuccess) e = hipMemcpy(f->win, win.data(), sizeof(float) * n, hipMemcpyHostToDevice);
         if (e != hipSuccess) {
             stx_fft_destroy(f);
@@ -412,7 +664,7 @@ STX_API stx_status stx_fft_create(int n, stx_fft** out) {
 
 STX_API void stx_fft_destroy(stx_fft* f) {
     if (!f) return;
-    if (f->tw) (void)hipFree(f->tw);
+    if (f->twt) (void)hipFree(f->twt);
     if (f->win) (void)hipFree(f->win);
     delete f;
 }
@@ -426,7 +678,7 @@ STX_API stx_status stx_fft_run(const stx_fft* f, float* data, int batch, int inv
         if (batch == 0) return;
         STX_REQUIRE(data != nullptr, "data is NULL");
         check_extent((long long)batch * f->n, "FFT batch");
-        by_size<FftL>(f->n, reinterpret_cast<float2*>(data), batch, inverse ? 1 : 0, f->tw, as_stream(stream));
+        by_size<FftL>(f->n, reinterpret_cast<float2*>(data), batch, inverse ? 1 : 0, f->twt, as_stream(stream));
     });
 }
 
@@ -452,7 +704,7 @@ STX_API stx_status stx_torch_stft(const stx_fft* f, const float* x, int channels
         a.x = x;
         a.spec = reinterpret_cast<float2*>(spec);
         a.win = f->win;
-        a.tw = f->tw;
+        a.twt = f->twt;
         a.len = len;
         a.len1 = len;
         a.pre_left = 0;
@@ -460,13 +712,11 @@ STX_API stx_status stx_torch_stft(const stx_fft* f, const float* x, int channels
         a.frame0 = 0;
         a.T = len / hop + 1;
         a.F = n / 2 + 1;
-        a.pairs = (a.T + 1) / 2;
-        a.jobs = channels * a.pairs;
+        a.jobs = channels * a.T;
         a.layout = layout;
-        a.vec4 = (a.T % 2 == 0) && ((uintptr_t)spec % 16 == 0);
-        a.half_scale = 0.5f * (normalized ? (float)(1.0 / std::sqrt((double)n)) : 1.0f);
+        a.scale = normalized ? (float)(1.0 / std::sqrt((double)n)) : 1.0f;
         check_extent((long long)channels * a.T * a.F, "spectrum");
-        check_extent((long long)channels * len, "signal");
+        check_extent((long long)channels * len + n, "signal");
         by_size<StftL>(n, a, as_stream(stream));
     });
 }
@@ -491,7 +741,7 @@ STX_API stx_status stx_htdemucs_spec(const stx_fft* f, const float* x, int chann
         a.x = x;
         a.spec = reinterpret_cast<float2*>(spec);
         a.win = f->win;
-        a.tw = f->tw;
+        a.twt = f->twt;
         a.len = len;
         a.len1 = len1;
         a.pre_left = pad;
@@ -499,89 +749,41 @@ STX_API stx_status stx_htdemucs_spec(const stx_fft* f, const float* x, int chann
         a.frame0 = 2 * hl;                                    // skip the first two frames (:97)
         a.T = le;
         a.F = n / 2;                                          // Nyquist dropped (:100)
-        a.pairs = (a.T + 1) / 2;
-        a.jobs = channels * a.pairs;
+        a.jobs = channels * a.T;
         a.layout = layout;
-        a.vec4 = (a.T % 2 == 0) && ((uintptr_t)spec % 16 == 0);
-        a.half_scale = (float)(0.5 / std::sqrt((double)n));
+        a.scale = (float)(1.0 / std::sqrt((double)n));
         check_extent((long long)channels * a.T * a.F, "spectrum");
         check_extent((long long)channels * len1 + n, "signal");
         by_size<StftL>(n, a, as_stream(stream));
     });
 }
 
+STX_API size_t stx_istft_workspace_size(const stx_fft* f, int channels, int n_frames) {
+    return f ? istft_workspace_bytes(f->n, channels, n_frames) : 0;
+}
+
 STX_API stx_status stx_torch_istft(const stx_fft* f, const float* spec, int channels, int n_frames, int hop,
                                    int normalized, float* out, stx_spec_layout layout, stx_stream stream) {
-    return guard([&] {
-        check_fft(f);
-        check_layout(layout);
-        const int n = f->n;
-        STX_REQUIRE(channels >= 0 && hop > 0 && n_frames >= 1, "bad channels/hop/n_frames");
-        const long long length = (long long)hop * (n_frames - 1);
-        check_extent(length + n, "signal");
-        check_extent((long long)channels * n_frames * (n / 2 + 1), "spectrum");
-        check_extent((long long)channels * length, "output");
-        if (channels == 0 || length == 0) return;
-        STX_REQUIRE(spec && out, "NULL buffer");
-        IstftArgs a{};
-        a.spec = reinterpret_cast<const float2*>(spec);
-        a.out = out;
-        a.win = f->win;
-        a.tw = f->tw;
-        a.T = n_frames;
-        a.F = n / 2 + 1;
-        a.layout = layout;
-        a.hop = hop;
-        a.env_frames = n_frames;
-        a.frame_off = 0;
-        a.out_off = n / 2;
-        a.out_len = (int)length;
-        a.valid_end = (int)(n + (long long)hop * (n_frames - 1));
-        a.keep_nyquist = 1;
-        a.norm = (float)((normalized ? std::sqrt((double)n) : 1.0) / n);
-        by_size<IstftL>(n, a, channels, as_stream(stream));
-    });
+    return torch_istft_impl(f, spec, channels, n_frames, hop, normalized, out, layout, nullptr, 0, stream);
+}
+
+STX_API stx_status stx_torch_istft_ws(const stx_fft* f, const float* spec, int channels, int n_frames, int hop,
+                                      int normalized, float* out, stx_spec_layout layout, void* workspace,
+                                      size_t workspace_bytes, stx_stream stream) {
+    return torch_istft_impl(f, spec, channels, n_frames, hop, normalized, out, layout, workspace,
+                            workspace_bytes, stream);
 }
 
 STX_API stx_status stx_htdemucs_ispec(const stx_fft* f, const float* spec, int channels, int n_frames,
                                       int length, float* out, stx_spec_layout layout, stx_stream stream) {
-    return guard([&] {
-        check_fft(f);
-        check_layout(layout);
-        const int n = f->n, hl = n / 4, pad = hl / 2 * 3;
-        STX_REQUIRE(channels >= 0 && n_frames >= 0 && length >= 0, "bad channels/n_frames/length");
-        const long long frames = (long long)n_frames + 4;             // two zero frames each side
-        const long long full = n + (long long)hl * (frames - 1);
-        const long long le_out = (long long)hl * ((length + hl - 1) / hl) + 2 * pad;
-        check_extent(full + length, "signal");
-        check_extent((long long)channels * n_frames * (n / 2), "spectrum");
-        check_extent((long long)channels * length, "output");
-        if (channels == 0 || length == 0) return;
-        STX_REQUIRE(spec && out, "NULL buffer");
-        IstftArgs a{};
-        a.spec = reinterpret_cast<const float2*>(spec);
-        a.out = out;
-        a.win = f->win;
-        a.tw = f->tw;
-        a.T = n_frames;
-        a.F = n / 2;
-        a.layout = layout;
-        a.hop = hl;
-        a.env_frames = (int)frames;
-        a.frame_off = 2;
-        a.out_off = n / 2 + pad;
-        a.out_len = length;
-        // out[i] = 0 where j - n/2 >= le_out or j >= full (src/stft.h:135-136), j = n/2 + pad + i.
-        a.valid_end = (int)std::min(full, le_out + n / 2);
-        a.keep_nyquist = 0;
-        a.norm = (float)(std::sqrt((double)n) / n);
-        if (n_frames == 0) {
-            hip_check(hipMemsetAsync(out, 0, sizeof(float) * (size_t)channels * length, as_stream(stream)),
-                      "hipMemsetAsync");
-            return;
-        }
-        by_size<IstftL>(n, a, channels, as_stream(stream));
-    });
+    return htdemucs_ispec_impl(f, spec, channels, n_frames, length, out, layout, nullptr, 0, stream);
+}
+
+STX_API stx_status stx_htdemucs_ispec_ws(const stx_fft* f, const float* spec, int channels, int n_frames,
+                                         int length, float* out, stx_spec_layout layout, void* workspace,
+                                         size_t workspace_bytes, stx_stream stream) {
+    return htdemucs_ispec_impl(f, spec, channels, n_frames, length, out, layout, workspace, workspace_bytes,
+                               stream);
 }
 
 }  // extern "C"

@@ -40,6 +40,9 @@ _SIGNATURES = {
     "stx_torch_istft": (_i, [_vp, _vp, _i, _i, _i, _i, _vp, _i, _vp]),
     "stx_htdemucs_spec": (_i, [_vp, _vp, _i, _i, _vp, _i, _vp]),
     "stx_htdemucs_ispec": (_i, [_vp, _vp, _i, _i, _i, _vp, _i, _vp]),
+    "stx_istft_workspace_size": (ctypes.c_size_t, [_vp, _i, _i]),
+    "stx_torch_istft_ws": (_i, [_vp, _vp, _i, _i, _i, _i, _vp, _i, _vp, ctypes.c_size_t, _vp]),
+    "stx_htdemucs_ispec_ws": (_i, [_vp, _vp, _i, _i, _i, _vp, _i, _vp, ctypes.c_size_t, _vp]),
 }
 
 
@@ -151,16 +154,32 @@ def torch_stft(fft, x, hop, normalized=False, layout=F_MAJOR, out=None, stream=N
     return out
 
 
-def torch_istft(fft, spec, hop, normalized=False, layout=F_MAJOR, out=None, stream=None):
-    """spec: complex64 [C, F, T] or [C, T, F] -> float32 [C, hop * (T - 1)]."""
+def istft_workspace_size(fft, channels, n_frames):
+    return lib().stx_istft_workspace_size(fft.handle, int(channels), int(n_frames))
+
+
+def _ws(workspace):
+    """(pointer, bytes) of an optional workspace tensor."""
+    if workspace is None:
+        return None, 0
+    import torch
+    if not isinstance(workspace, torch.Tensor) or not workspace.is_cuda:
+        raise TypeError("workspace must be a CUDA (HIP) tensor")
+    return ctypes.c_void_p(workspace.data_ptr()), workspace.numel() * workspace.element_size()
+
+
+def torch_istft(fft, spec, hop, normalized=False, layout=F_MAJOR, out=None, stream=None, workspace=None):
+    """spec: complex64 [C, F, T] or [C, T, F] -> float32 [C, hop * (T - 1)]. With a workspace
+    tensor of at least istft_workspace_size() bytes the two-kernel path runs."""
     import torch
     _require(spec, torch.complex64, "spec")
     C = spec.shape[0]
     T = spec.shape[2] if layout == F_MAJOR else spec.shape[1]
     if out is None:
         out = torch.empty((C, hop * (T - 1)), dtype=torch.float32, device=spec.device)
-    check(lib().stx_torch_istft(fft.handle, _ptr(spec), C, T, int(hop), int(bool(normalized)), _ptr(out),
-                                int(layout), _stream(stream)))
+    wp, wb = _ws(workspace)
+    check(lib().stx_torch_istft_ws(fft.handle, _ptr(spec), C, T, int(hop), int(bool(normalized)), _ptr(out),
+                                   int(layout), wp, wb, _stream(stream)))
     return out
 
 
@@ -178,7 +197,7 @@ def htdemucs_spec(fft, x, layout=F_MAJOR, out=None, stream=None):
     return out
 
 
-def htdemucs_ispec(fft, spec, length, layout=F_MAJOR, out=None, stream=None):
+def htdemucs_ispec(fft, spec, length, layout=F_MAJOR, out=None, stream=None, workspace=None):
     """spec: complex64 [C, n/2, T] or [C, T, n/2] -> float32 [C, length]."""
     import torch
     _require(spec, torch.complex64, "spec")
@@ -186,6 +205,13 @@ def htdemucs_ispec(fft, spec, length, layout=F_MAJOR, out=None, stream=None):
     T = spec.shape[2] if layout == F_MAJOR else spec.shape[1]
     if out is None:
         out = torch.empty((C, length), dtype=torch.float32, device=spec.device)
-    check(lib().stx_htdemucs_ispec(fft.handle, _ptr(spec), C, T, int(length), _ptr(out), int(layout),
-                                   _stream(stream)))
+    wp, wb = _ws(workspace)
+    check(lib().stx_htdemucs_ispec_ws(fft.handle, _ptr(spec), C, T, int(length), _ptr(out), int(layout),
+                                      wp, wb, _stream(stream)))
     return out
+
+
+def workspace(nbytes, device):
+    """A device workspace tensor of at least nbytes."""
+    import torch
+    return torch.empty(max(1, (int(nbytes) + 3) // 4), dtype=torch.float32, device=device)

@@ -47,9 +47,14 @@ def host(t):
     return t.cpu().numpy()
 
 
+def ws_for(fft, channels, frames, device, use):
+    return stx.workspace(stx.istft_workspace_size(fft, channels, frames), device) if use else None
+
+
 @pytest.mark.parametrize("path", SPEC_GOLDEN, ids=[os.path.basename(p)[5:-4] for p in SPEC_GOLDEN])
 @pytest.mark.parametrize("layout", [stx.F_MAJOR, stx.T_MAJOR])
-def test_golden_spectrum_and_inverse(device, path, layout):
+@pytest.mark.parametrize("use_ws", [False, True], ids=["fused", "two_step"])
+def test_golden_spectrum_and_inverse(device, path, layout, use_ws):
     d = np.load(path)
     n = int(d["n_fft"])
     x = to_dev(d["x"][None, :], device)
@@ -67,10 +72,11 @@ def test_golden_spectrum_and_inverse(device, path, layout):
     # Inverse of the reference spectrum rounded to complex64.
     s = spec_ref.astype(np.complex64)[None]
     sdev = to_dev(s if layout == stx.F_MAJOR else np.ascontiguousarray(s.transpose(0, 2, 1)), device)
+    ws = ws_for(plan(n), 1, spec_ref.shape[1], device, use_ws)
     if "torch" in path:
-        y = stx.torch_istft(plan(n), sdev, hop, nm, layout=layout)
+        y = stx.torch_istft(plan(n), sdev, hop, nm, layout=layout, workspace=ws)
     else:
-        y = stx.htdemucs_ispec(plan(n), sdev, d["x"].size, layout=layout)
+        y = stx.htdemucs_ispec(plan(n), sdev, d["x"].size, layout=layout, workspace=ws)
     y = host(y)[0]
     assert y.shape == d["y"].shape
     assert snr_db(y, d["y"]) >= SNR_DB
@@ -80,13 +86,14 @@ def _stereo(seed, length, sigma=0.1):
     return synth.normal(seed, (2, length), sigma)
 
 
-def test_htdemucs_spec_c1_full_size(device, orc):
+@pytest.mark.parametrize("use_ws", [False, True], ids=["fused", "two_step"])
+def test_htdemucs_spec_c1_full_size(device, orc, use_ws):
     # HTDemucs spec: stereo 343,980 samples, n_fft 4096, hop 1024 -> [2][2048][336].
     length = 343980
     x = _stereo(2024, length)
     f = plan(4096)
     spec = stx.htdemucs_spec(f, to_dev(x, device))
-    y = stx.htdemucs_ispec(f, spec, length)
+    y = stx.htdemucs_ispec(f, spec, length, workspace=ws_for(f, 2, 336, device, use_ws))
     spec_h, y_h = host(spec), host(y)
     assert spec_h.shape == (2, 2048, 336)
     for c in range(2):
@@ -112,15 +119,17 @@ def test_torch_stft_c1_plain_call(device, orc):
 
 
 @pytest.mark.parametrize("normalized", [False, True])
-def test_roformer_stft_c3_full_size(device, orc, normalized):
+@pytest.mark.parametrize("use_ws", [False, True], ids=["fused", "two_step"])
+def test_roformer_stft_c3_full_size(device, orc, normalized, use_ws):
     # RoFormer chunk: stereo 352,800 samples, n_fft 2048, hop 441 -> [2][1025][801] (odd T).
     length = 352800
     x = _stereo(2026, length)
     f = plan(2048)
     spec = stx.torch_stft(f, to_dev(x, device), 441, normalized)
     spec_t = stx.torch_stft(f, to_dev(x, device), 441, normalized, layout=stx.T_MAJOR)
-    y = stx.torch_istft(f, spec, 441, normalized)
-    y_t = stx.torch_istft(f, spec_t, 441, normalized, layout=stx.T_MAJOR)
+    ws = ws_for(f, 2, 801, device, use_ws)
+    y = stx.torch_istft(f, spec, 441, normalized, workspace=ws)
+    y_t = stx.torch_istft(f, spec_t, 441, normalized, layout=stx.T_MAJOR, workspace=ws)
     spec_h, spec_th, y_h, y_th = host(spec), host(spec_t), host(y), host(y_t)
     assert spec_h.shape == (2, 1025, 801)
     assert np.array_equal(spec_h, spec_th.transpose(0, 2, 1))
@@ -133,13 +142,14 @@ def test_roformer_stft_c3_full_size(device, orc, normalized):
 
 
 @pytest.mark.parametrize("n", [16, 32, 64, 128, 256, 512, 1024, 2048, 4096, 8192])
-def test_every_fft_size_stft_round_trip(device, orc, n):
+@pytest.mark.parametrize("use_ws", [False, True], ids=["fused", "two_step"])
+def test_every_fft_size_stft_round_trip(device, orc, n, use_ws):
     hop = max(1, n // 4 - 1)
     length = 3 * n + 5
     x = _stereo(300 + n, length, 0.5)
     f = plan(n)
     spec = stx.torch_stft(f, to_dev(x, device), hop)
-    y = stx.torch_istft(f, spec, hop)
+    y = stx.torch_istft(f, spec, hop, workspace=ws_for(f, 2, length // hop + 1, device, use_ws))
     spec_h, y_h = host(spec), host(y)
     for c in range(2):
         ref = orc.torch_stft(x[c], n, hop)
@@ -147,7 +157,7 @@ def test_every_fft_size_stft_round_trip(device, orc, n):
         assert snr_db(y_h[c], orc.torch_istft(ref, n, hop)) >= SNR_DB
     if length > 3 * n // 8 * 2:
         s2 = stx.htdemucs_spec(f, to_dev(x, device))
-        y2 = stx.htdemucs_ispec(f, s2, length)
+        y2 = stx.htdemucs_ispec(f, s2, length, workspace=ws_for(f, 2, s2.shape[2], device, use_ws))
         s2h, y2h = host(s2), host(y2)
         for c in range(2):
             ref = orc.htdemucs_spec(x[c], n)
@@ -190,3 +200,28 @@ def test_stft_errors(device):
     with pytest.raises(stx.StxError) as e:
         stx.htdemucs_spec(plan(4096), x)
     assert e.value.status == stx.STATUS_RUNTIME_ERROR
+
+
+def test_small_hop_needs_several_rounds(device, orc):
+    # hop n/32 makes every output tile overlap more frames than one workgroup transforms at
+    # once, so the fused path loops over rounds.
+    n, hop, length = 1024, 32, 4000
+    x = _stereo(55, length, 0.3)
+    f = plan(n)
+    spec = stx.torch_stft(f, to_dev(x, device), hop)
+    y = host(stx.torch_istft(f, spec, hop))
+    spec_h = host(spec)
+    for c in range(2):
+        ref = orc.torch_stft(x[c], n, hop)
+        assert snr_db(spec_h[c], ref) >= SNR_DB
+        assert snr_db(y[c], orc.torch_istft(ref, n, hop)) >= SNR_DB
+
+
+def test_workspace_too_small(device):
+    f = plan(2048)
+    x = to_dev(_stereo(56, 20000), device)
+    spec = stx.torch_stft(f, x, 441)
+    ws = stx.workspace(stx.istft_workspace_size(f, 2, spec.shape[2]) - 4096, device)
+    with pytest.raises(stx.StxError) as e:
+        stx.torch_istft(f, spec, 441, workspace=ws)
+    assert e.value.status == stx.STATUS_INVALID_ARGUMENT
