@@ -133,6 +133,61 @@ STX_API stx_status stx_htdemucs_ispec_ws(const stx_fft* fft, const float* spec, 
                                          stx_spec_layout layout, void* workspace,
                                          size_t workspace_bytes, stx_stream stream);
 
+/* ------------------------------------------------------------------------------------------
+ * RoFormer band maps, band tables, band gather and mask scatter-average + apply.
+ * Replace the host loops of RoFormer::Impl (src/roformer.cpp:217-283) and the band-map rules
+ * of tools/convert_roformer.py:107-124. Layout of band features, per batch item (one chunk):
+ * feat[band_feat_off[b] * T + t * dim_in(b) + (j * C + c) * 2 + {re, im}], dim_in(b) =
+ * band_sizes[b] * C * 2 (src/roformer.cpp:85,226-241); masks of S stems use the same layout,
+ * stem-major ([S][total_feat * T]).
+ * ---------------------------------------------------------------------------------------- */
+typedef struct stx_bands stx_bands;
+
+/* MelBandRoformer's band map, tools/convert_roformer.py:107-115: librosa.filters.mel(sr, n_fft,
+ * n_mels) (Slaney, fmin 0, fmax sr/2) with fb[0][0] = fb[-1][-1] = 1; band b holds the bins with
+ * a positive weight, ascending. Writes band_sizes[n_mels] and band_freqs[*n_freqs]; with both
+ * outputs NULL only *n_freqs is set (size query). RUNTIME_ERROR if a bin is left uncovered
+ * (the converter's assertion, :114). Host only. */
+STX_API stx_status stx_mel_band_map(int sample_rate, int n_fft, int n_mels, int32_t* band_sizes,
+                                    int32_t* band_freqs, int64_t capacity, int64_t* n_freqs);
+
+/* BSRoformer's contiguous bands, tools/convert_roformer.py:118-124: RUNTIME_ERROR unless the
+ * sizes sum to n_fft/2 + 1. Host only. */
+STX_API stx_status stx_bs_band_map(const int32_t* freqs_per_bands, int n_bands, int n_fft,
+                                   int32_t* band_freqs, int64_t capacity, int64_t* n_freqs);
+
+/* The RoFormer constructor's band tables and checks (src/roformer.cpp:394-411): RUNTIME_ERROR
+ * if the sizes do not sum to n_freqs or a bin is out of [0, n_bins). Writes
+ * band_freq_off[n_bands + 1], band_feat_off[n_bands + 1] (floats per frame) and
+ * bands_per_freq[n_bins]; any output may be NULL. Host only. */
+STX_API stx_status stx_bands_layout(const int32_t* band_sizes, int n_bands, const int32_t* band_freqs,
+                                    int64_t n_freqs, int n_bins, int channels, int64_t* band_freq_off,
+                                    int64_t* band_feat_off, int32_t* bands_per_freq);
+
+/* Device band table for `channels` channels and n_bins STFT bins, same checks as
+ * stx_bands_layout. */
+STX_API stx_status stx_bands_create(const int32_t* band_sizes, int n_bands, const int32_t* band_freqs,
+                                    int64_t n_freqs, int n_bins, int channels, stx_bands** out);
+STX_API void       stx_bands_destroy(stx_bands* bands);
+/* band_feat_off.back() = sum of dim_in(b): feature floats per frame (src/roformer.cpp:86). */
+STX_API int64_t    stx_bands_total_feat(const stx_bands* bands);
+
+/* Band gather (src/roformer.cpp:226-241) for `batch` chunks: spec is device
+ * [batch][C][F][T] (F_MAJOR) or [batch][C][T][F] complex64; feat is device
+ * [batch][total_feat * T] float, each value the spectrum's float re/im. */
+STX_API stx_status stx_band_gather(const stx_bands* bands, const float* spec, int batch, int n_frames,
+                                   stx_spec_layout layout, float* feat, stx_stream stream);
+
+/* Mask scatter-average and complex mask apply (src/roformer.cpp:251-278) for `batch` chunks and
+ * n_stems stems: out[b][s][c] = spec[b][c] * (sum of the stem's band masks covering each bin /
+ * max(bands_per_freq, 1)), accumulated and applied in double and rounded once; bin 0 is zeroed
+ * when zero_dc (:278). masks: device [batch][n_stems][total_feat * T]; spec: device
+ * [batch][C][...] and out: device [batch][n_stems][C][...] complex64 in `layout`. */
+STX_API stx_status stx_band_scatter_apply(const stx_bands* bands, const float* masks, int n_stems,
+                                          const float* spec, int batch, int n_frames,
+                                          stx_spec_layout layout, int zero_dc, float* out,
+                                          stx_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -15,6 +15,16 @@
  *     written by the reference's own src/stft.h (tests/golden/), plus closed forms (impulse
  *     known answer, brute-force DFT, Parseval) and the reference's round-trip tolerances
  *     (tests/dsp_test.cpp:63,76-77,95).
+ *   orc_mel_band_map: the counts the survey of the reference restated independently (60 bands,
+ *     1,979 entries, sizes 7, 6, 6, ..., 122, 130, 71 bins in one band and 954 in two), an
+ *     independent vectorised float32 restatement of librosa's filterbank in the test, and the
+ *     margin between every bin frequency and every mel vertex (>= 0.098 Hz), which shows that
+ *     ulp-level differences in log/exp cannot change the map. Exact librosa-version behaviour
+ *     is parity unpinned (librosa is not installed).
+ *   orc_bands_layout / orc_band_gather / orc_band_scatter_apply: brute force against
+ *     independent numpy formulations on small tables, and invariants (gather then scatter of
+ *     bin-constant masks returns the spectrum times that constant; band counts sum to the
+ *     table size).
  */
 #ifndef STX_ORACLE_H
 #define STX_ORACLE_H
@@ -45,6 +55,22 @@ int orc_htdemucs_spec(const float* x, int len, int n_fft, double* spec, int* n_f
 
 /* st::htdemucs_ispec (src/stft.h:105-140): out has `length` floats. */
 int orc_htdemucs_ispec(const double* spec, int n_frames, int n_fft, int length, float* out);
+
+/* Mel band map of tools/convert_roformer.py:107-115. Returns -2 if a bin is uncovered. */
+int orc_mel_band_map(int sr, int n_fft, int n_mels, int* band_sizes, int* band_freqs, long cap, long* n_total);
+
+/* RoFormer constructor tables (src/roformer.cpp:394-411); -2 where the constructor throws. */
+int orc_bands_layout(const int* band_sizes, int n_bands, const int* band_freqs, long n_freqs, int n_bins,
+                     int channels, long* freq_off, long* feat_off, int* bpf);
+
+/* Band gather, src/roformer.cpp:226-241: z complex [C][F][T] -> feat [total_feat * T]. */
+void orc_band_gather(const int* band_sizes, int n_bands, const int* band_freqs, int C, int F, int T,
+                     const double* z, float* feat);
+
+/* Scatter-average + complex mask apply, src/roformer.cpp:251-278: masks [S][total_feat * T],
+ * z complex [C][F][T] -> out complex [S][C][F][T] (before the iSTFT). */
+void orc_band_scatter_apply(const int* band_sizes, int n_bands, const int* band_freqs, int C, int F, int T,
+                            const float* masks, int S, const double* z, int zero_dc, double* out);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,323 @@
+// bands.hip — RoFormer band gather and mask scatter-average + complex mask apply on gfx950.
+//
+// Reference: RoFormer::Impl::run, src/roformer.cpp:226-241 (gather) and :251-278 (scatter,
+// average, apply, zero_dc). Both are rewritten in gather form so that no two threads write
+// one element:
+//   * band gather: one workgroup per (band, tile of frames, batch item) writes the band's
+//     feature rows feat[t][(j*C + c)*2 + {re,im}] contiguously; T-major spectra are read
+//     row-wise directly, F-major ones through an LDS transpose so that both sides stay
+//     coalesced.
+//   * scatter + apply: one thread per (bin, channel, frame, stem) walks the list of
+//     (band, position) pairs that cover its bin (a CSR table built once per band table, in
+//     the reference's band-then-position order), sums their mask values in double, divides
+//     by the band count and multiplies the spectrum, all in double like the reference, and
+//     rounds once. Neighbouring lanes take neighbouring (bin, channel) pairs, which are
+//     neighbouring floats of the mask rows, so mask reads are coalesced in T-major layout.
+#include <algorithm>
+#include <type_traits>
+#include <vector>
+
+#include "bands_host.hpp"
+#include "common.hpp"
+
+namespace stx {
+struct BandInfo {
+    long long feat_off;      // band_feat_off[b]: first float of the band's block, per frame
+    int freq_off;            // band_freq_off[b]
+    int size;                // band_sizes[b]
+};
+struct CsrEntry {
+    long long feat_off;      // band_feat_off[b] of the covering band
+    int din;                 // dim_in(b) = size * C * 2
+    int col;                 // j * C * 2: the bin's column inside the band's rows
+};
+}  // namespace stx
+
+struct stx_bands {
+    int n_bands = 0, n_bins = 0, channels = 0;
+    long long n_freqs = 0, total_feat = 0;
+    int max_pairs = 0;                               // max band size * channels
+    std::vector<int64_t> freq_off, feat_off;
+    std::vector<int32_t> bpf;
+    stx::BandInfo* d_bands = nullptr;
+    int* d_band_freqs = nullptr;
+    int* d_csr_off = nullptr;                        // [n_bins + 1]
+    stx::CsrEntry* d_csr = nullptr;                  // [n_freqs]
+    double* d_denom = nullptr;                       // [n_bins]: max(bands_per_freq, 1)
+};
+
+namespace stx {
+namespace {
+
+struct GatherArgs {
+    const float2* spec;      // [batch][C][F][T] or [batch][C][T][F]
+    float2* feat;            // [batch][total_feat * T / 2]
+    const BandInfo* bands;
+    const int* band_freqs;
+    int C, F, T;
+    long long total_feat;    // floats per frame of one batch item
+    int TT;                  // frames per tile
+};
+
+// T-major: lanes walk a band row (j, c) for one frame at a time; reads and writes coalesced.
+__global__ __launch_bounds__(256) void band_gather_t_kernel(GatherArgs a) {
+    const int b = (int)blockIdx.x;
+    const int t0 = (int)blockIdx.y * a.TT;
+    const int bt = (int)blockIdx.z;
+    const BandInfo bi = a.bands[b];
+    const int pairs = bi.size * a.C;
+    const float2* sb = a.spec + (size_t)bt * a.C * a.T * a.F;
+    float2* fb = a.feat + ((size_t)bt * a.total_feat * a.T + (size_t)bi.feat_off * a.T) / 2;
+    const int t1 = min(t0 + a.TT, a.T);
+    for (int t = t0; t < t1; t++) {
+        float2* row = fb + (size_t)t * pairs;
+        for (int q = (int)threadIdx.x; q < pairs; q += 256) {
+            const int j = q / a.C, c = q - j * a.C;
+            const int f = a.band_freqs[bi.freq_off + j];
+            row[q] = sb[((size_t)c * a.T + t) * a.F + f];
+        }
+    }
+}
+
+// F-major: a tile [pairs][TT] is read along t (coalesced) into LDS and written along the
+// band rows (coalesced).
+__global__ __launch_bounds__(256) void band_gather_f_kernel(GatherArgs a) {
+    extern __shared__ float2 tile[];                 // [pairs][TT + 1]
+    const int b = (int)blockIdx.x;
+    const int t0 = (int)blockIdx.y * a.TT;
+    const int bt = (int)blockIdx.z;
+    const BandInfo bi = a.bands[b];
+    const int pairs = bi.size * a.C;
+    const int TT = a.TT, ld = TT + 1;
+    const float2* sb = a.spec + (size_t)bt * a.C * a.F * a.T;
+    float2* fb = a.feat + ((size_t)bt * a.total_feat * a.T + (size_t)bi.feat_off * a.T) / 2;
+    for (int e = (int)threadIdx.x; e < pairs * TT; e += 256) {
+        const int q = e / TT, tt = e - q * TT;
+        const int t = t0 + tt;
+        if (t < a.T) {
+            const int j = q / a.C, c = q - j * a.C;
+            const int f = a.band_freqs[bi.freq_off + j];
+            tile[q * ld + tt] = sb[((size_t)c * a.F + f) * a.T + t];
+        }
+    }
+    __syncthreads();
+    for (int e = (int)threadIdx.x; e < pairs * TT; e += 256) {
+        const int tt = e / pairs, q = e - tt * pairs;
+        const int t = t0 + tt;
+        if (t < a.T) fb[(size_t)t * pairs + q] = tile[q * ld + tt];
+    }
+}
+
+struct ScatterArgs {
+    const float* masks;      // [batch][S][total_feat * T]
+    const float2* spec;      // [batch][C][F][T] or [batch][C][T][F]
+    float2* out;             // [batch][S][C][F][T] or [batch][S][C][T][F]
+    const int* csr_off;
+    const CsrEntry* csr;
+    const double* denom;
+    int C, F, T, S, zero_dc;
+    long long total_feat;
+};
+
+// out = spec * (sum of the covering masks / band count), one rounding, src/roformer.cpp:266-278.
+__device__ __forceinline__ float2 masked_bin(const ScatterArgs& a, const float* __restrict__ mb, float2 z,
+                                             int f, int c, int t) {
+#pragma clang fp contract(off)
+    if (a.zero_dc && f == 0) return make_float2(0.f, 0.f);
+    double ar = 0.0, ai = 0.0;
+    const int e1 = a.csr_off[f + 1];
+    for (int e = a.csr_off[f]; e < e1; e++) {
+        const CsrEntry E = a.csr[e];
+        const float2 m = *reinterpret_cast<const float2*>(mb + (size_t)E.feat_off * a.T + (size_t)t * E.din + E.col + 2 * c);
+        ar += (double)m.x;
+        ai += (double)m.y;
+    }
+    const double d = a.denom[f];
+    const double qr = ar / d, qi = ai / d;
+    const double zr = z.x, zi = z.y;
+    return make_float2((float)(zr * qr - zi * qi), (float)(zr * qi + zi * qr));
+}
+
+// T-major: thread = (bin, channel) of one frame; lanes cover consecutive mask floats.
+__global__ __launch_bounds__(256) void band_scatter_t_kernel(ScatterArgs a) {
+    const int i = (int)(blockIdx.x * 256 + threadIdx.x);
+    if (i >= a.F * a.C) return;
+    const int f = i / a.C, c = i - f * a.C;
+    const int t = (int)blockIdx.y;
+    const int bt = (int)blockIdx.z / a.S, s = (int)blockIdx.z % a.S;
+    const float* mb = a.masks + ((size_t)bt * a.S + s) * a.total_feat * a.T;
+    const size_t zi = (((size_t)bt * a.C + c) * a.T + t) * a.F + f;
+    const float2 z = a.spec[zi];
+    a.out[(((size_t)bt * a.S + s) * a.C + c) * a.T * a.F + (size_t)t * a.F + f] = masked_bin(a, mb, z, f, c, t);
+}
+
+// F-major: thread = frame of one (bin, channel); spectrum and output coalesced along t.
+__global__ __launch_bounds__(256) void band_scatter_f_kernel(ScatterArgs a) {
+    const int t = (int)(blockIdx.x * 256 + threadIdx.x);
+    if (t >= a.T) return;
+    const int f = (int)blockIdx.y;
+    const int z3 = (int)blockIdx.z;                   // (bt * S + s) * C + c
+    const int c = z3 % a.C, s = (z3 / a.C) % a.S, bt = z3 / (a.C * a.S);
+    const float* mb = a.masks + ((size_t)bt * a.S + s) * a.total_feat * a.T;
+    const float2 z = a.spec[(((size_t)bt * a.C + c) * a.F + f) * a.T + t];
+    a.out[(((size_t)bt * a.S + s) * a.C + c) * a.F * a.T + (size_t)f * a.T + t] = masked_bin(a, mb, z, f, c, t);
+}
+
+void check_bands(const stx_bands* b) { STX_REQUIRE(b != nullptr && b->d_bands != nullptr, "null band table"); }
+
+}  // namespace
+}  // namespace stx
+
+using namespace stx;
+
+extern "C" {
+
+STX_API stx_status stx_bands_create(const int32_t* band_sizes, int n_bands, const int32_t* band_freqs,
+                                    int64_t n_freqs, int n_bins, int channels, stx_bands** out) {
+    return guard([&] {
+        STX_REQUIRE(out != nullptr, "out is NULL");
+        *out = nullptr;
+        std::vector<int64_t> fo, fe;
+        std::vector<int32_t> bpf;
+        check_band_tables(band_sizes, n_bands, band_freqs, n_freqs, n_bins, channels, fo, fe, bpf);
+        STX_REQUIRE(fe.back() < (1LL << 40) && n_freqs < (1LL << 31), "band table too large");
+        std::vector<BandInfo> bi(n_bands);
+        int max_pairs = 0;
+        for (int b = 0; b < n_bands; b++) {
+            bi[b] = BandInfo{(long long)fe[b], (int)fo[b], band_sizes[b]};
+            max_pairs = std::max(max_pairs, band_sizes[b] * channels);
+        }
+        // CSR of (band, position) pairs per bin, in band then position order.
+        std::vector<int> csr_off(n_bins + 1, 0);
+        for (int64_t i = 0; i < n_freqs; i++) csr_off[band_freqs[i] + 1]++;
+        for (int f = 0; f < n_bins; f++) csr_off[f + 1] += csr_off[f];
+        std::vector<CsrEntry> csr(std::max<int64_t>(n_freqs, 1));
+        std::vector<int> fill(csr_off.begin(), csr_off.end() - 1);
+        for (int b = 0; b < n_bands; b++)
+            for (int j = 0; j < band_sizes[b]; j++) {
+                const int f = band_freqs[fo[b] + j];
+                csr[fill[f]++] = CsrEntry{(long long)fe[b], band_sizes[b] * channels * 2, j * channels * 2};
+            }
+        std::vector<double> denom(n_bins);
+        for (int f = 0; f < n_bins; f++) denom[f] = (double)std::max(bpf[f], 1);   // src/roformer.cpp:272
+
+        stx_bands* h = new stx_bands;
+        h->n_bands = n_bands;
+        h->n_bins = n_bins;
+        h->channels = channels;
+        h->n_freqs = n_freqs;
+        h->total_feat = fe.back();
+        h->max_pairs = max_pairs;
+        h->freq_off = fo;
+        h->feat_off = fe;
+        h->bpf = bpf;
+        hipError_t e = hipSuccess;
+        auto up = [&](auto** dst, const auto& v) {
+            using T = std::remove_reference_t<decltype(v[0])>;
+            if (e == hipSuccess) e = hipMalloc(dst, sizeof(T) * std::max<size_t>(v.size(), 1));
+            if (e == hipSuccess && !v.empty())
+                e = hipMemcpy(*dst, v.data(), sizeof(T) * v.size(), hipMemcpyHostToDevice);
+        };
+        std::vector<int> bf(band_freqs, band_freqs + n_freqs);
+        up(&h->d_bands, bi);
+        up(&h->d_band_freqs, bf);
+        up(&h->d_csr_off, csr_off);
+        up(&h->d_csr, csr);
+        up(&h->d_denom, denom);
+        if (e != hipSuccess) {
+            stx_bands_destroy(h);
+            hip_check(e, "stx_bands_create");
+        }
+        *out = h;
+    });
+}
+
+STX_API void stx_bands_destroy(stx_bands* h) {
+    if (!h) return;
+    (void)hipFree(h->d_bands);
+    (void)hipFree(h->d_band_freqs);
+    (void)hipFree(h->d_csr_off);
+    (void)hipFree(h->d_csr);
+    (void)hipFree(h->d_denom);
+    delete h;
+}
+
+STX_API int64_t stx_bands_total_feat(const stx_bands* h) { return h ? h->total_feat : 0; }
+
+STX_API stx_status stx_band_gather(const stx_bands* h, const float* spec, int batch, int n_frames,
+                                   stx_spec_layout layout, float* feat, stx_stream stream) {
+    return guard([&] {
+        check_bands(h);
+        STX_REQUIRE(layout == STX_SPEC_F_MAJOR || layout == STX_SPEC_T_MAJOR, "unknown spectrum layout");
+        STX_REQUIRE(batch >= 0 && n_frames >= 0, "bad batch/n_frames");
+        if (batch == 0 || n_frames == 0 || h->total_feat == 0) return;
+        STX_REQUIRE(spec && feat, "NULL buffer");
+        STX_REQUIRE(n_frames < 65536 && batch < 65536, "too many frames or batch items");
+        GatherArgs a{};
+        a.spec = reinterpret_cast<const float2*>(spec);
+        a.feat = reinterpret_cast<float2*>(feat);
+        a.bands = h->d_bands;
+        a.band_freqs = h->d_band_freqs;
+        a.C = h->channels;
+        a.F = h->n_bins;
+        a.T = n_frames;
+        a.total_feat = h->total_feat;
+        const hipStream_t s = as_stream(stream);
+        if (layout == STX_SPEC_T_MAJOR) {
+            a.TT = 8;
+            dim3 grid(h->n_bands, (n_frames + a.TT - 1) / a.TT, batch);
+            hipLaunchKernelGGL(band_gather_t_kernel, grid, dim3(256), 0, s, a);
+            launch_check("band_gather_t_kernel");
+            return;
+        }
+        // LDS tile [max_pairs][TT + 1] float2 within 64 KB.
+        int TT = 32;
+        while (TT > 1 && (size_t)h->max_pairs * (TT + 1) * sizeof(float2) > 65536) TT /= 2;
+        if ((size_t)h->max_pairs * (TT + 1) * sizeof(float2) > 65536)
+            fail(STX_STATUS_UNSUPPORTED, "band of %d (bin, channel) pairs is too wide for the F-major gather",
+                 h->max_pairs);
+        a.TT = TT;
+        dim3 grid(h->n_bands, (n_frames + TT - 1) / TT, batch);
+        hipLaunchKernelGGL(band_gather_f_kernel, grid, dim3(256), (size_t)h->max_pairs * (TT + 1) * sizeof(float2),
+                           s, a);
+        launch_check("band_gather_f_kernel");
+    });
+}
+
+STX_API stx_status stx_band_scatter_apply(const stx_bands* h, const float* masks, int n_stems, const float* spec,
+                                          int batch, int n_frames, stx_spec_layout layout, int zero_dc, float* out,
+                                          stx_stream stream) {
+    return guard([&] {
+        check_bands(h);
+        STX_REQUIRE(layout == STX_SPEC_F_MAJOR || layout == STX_SPEC_T_MAJOR, "unknown spectrum layout");
+        STX_REQUIRE(batch >= 0 && n_frames >= 0 && n_stems >= 0, "bad batch/n_frames/n_stems");
+        if (batch == 0 || n_frames == 0 || n_stems == 0) return;
+        STX_REQUIRE(masks && spec && out, "NULL buffer");
+        STX_REQUIRE(n_frames < 65536 && (long long)batch * n_stems * h->channels < 65536, "grid too large");
+        ScatterArgs a{};
+        a.masks = masks;
+        a.spec = reinterpret_cast<const float2*>(spec);
+        a.out = reinterpret_cast<float2*>(out);
+        a.csr_off = h->d_csr_off;
+        a.csr = h->d_csr;
+        a.denom = h->d_denom;
+        a.C = h->channels;
+        a.F = h->n_bins;
+        a.T = n_frames;
+        a.S = n_stems;
+        a.zero_dc = zero_dc ? 1 : 0;
+        a.total_feat = h->total_feat;
+        const hipStream_t s = as_stream(stream);
+        if (layout == STX_SPEC_T_MAJOR) {
+            dim3 grid((a.F * a.C + 255) / 256, n_frames, batch * n_stems);
+            hipLaunchKernelGGL(band_scatter_t_kernel, grid, dim3(256), 0, s, a);
+            launch_check("band_scatter_t_kernel");
+        } else {
+            dim3 grid((n_frames + 255) / 256, a.F, batch * n_stems * a.C);
+            hipLaunchKernelGGL(band_scatter_f_kernel, grid, dim3(256), 0, s, a);
+            launch_check("band_scatter_f_kernel");
+        }
+    });
+}
+
+}  // extern "C"

@@ -43,6 +43,14 @@ _SIGNATURES = {
     "stx_istft_workspace_size": (ctypes.c_size_t, [_vp, _i, _i]),
     "stx_torch_istft_ws": (_i, [_vp, _vp, _i, _i, _i, _i, _vp, _i, _vp, ctypes.c_size_t, _vp]),
     "stx_htdemucs_ispec_ws": (_i, [_vp, _vp, _i, _i, _i, _vp, _i, _vp, ctypes.c_size_t, _vp]),
+    "stx_mel_band_map": (_i, [_i, _i, _i, _vp, _vp, ctypes.c_int64, _vp]),
+    "stx_bs_band_map": (_i, [_vp, _i, _i, _vp, ctypes.c_int64, _vp]),
+    "stx_bands_layout": (_i, [_vp, _i, _vp, ctypes.c_int64, _i, _i, _vp, _vp, _vp]),
+    "stx_bands_create": (_i, [_vp, _i, _vp, ctypes.c_int64, _i, _i, ctypes.POINTER(_vp)]),
+    "stx_bands_destroy": (None, [_vp]),
+    "stx_bands_total_feat": (ctypes.c_int64, [_vp]),
+    "stx_band_gather": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp]),
+    "stx_band_scatter_apply": (_i, [_vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _vp]),
 }
 
 
@@ -215,3 +223,93 @@ def workspace(nbytes, device):
     """A device workspace tensor of at least nbytes."""
     import torch
     return torch.empty(max(1, (int(nbytes) + 3) // 4), dtype=torch.float32, device=device)
+
+
+# ------------------------------------------------------------------------------- bands
+def _np_ptr(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def mel_band_map(sample_rate, n_fft, n_mels):
+    """(band_sizes int32[n_mels], band_freqs int32[...]) of MelBandRoformer (host only)."""
+    import numpy as np
+    n = ctypes.c_int64(0)
+    check(lib().stx_mel_band_map(int(sample_rate), int(n_fft), int(n_mels), None, None, 0, ctypes.byref(n)))
+    sizes = np.zeros(n_mels, dtype=np.int32)
+    freqs = np.zeros(max(1, n.value), dtype=np.int32)
+    check(lib().stx_mel_band_map(int(sample_rate), int(n_fft), int(n_mels), _np_ptr(sizes), _np_ptr(freqs),
+                                 freqs.size, ctypes.byref(n)))
+    return sizes, freqs[: n.value].copy()
+
+
+def bs_band_map(freqs_per_bands, n_fft):
+    import numpy as np
+    fpb = np.ascontiguousarray(freqs_per_bands, dtype=np.int32)
+    n = ctypes.c_int64(0)
+    out = np.zeros(n_fft // 2 + 1, dtype=np.int32)
+    check(lib().stx_bs_band_map(_np_ptr(fpb), fpb.size, int(n_fft), _np_ptr(out), out.size, ctypes.byref(n)))
+    return out[: n.value].copy()
+
+
+def bands_layout(band_sizes, band_freqs, n_bins, channels):
+    """(band_freq_off int64[B+1], band_feat_off int64[B+1], bands_per_freq int32[n_bins]) (host only)."""
+    import numpy as np
+    sizes = np.ascontiguousarray(band_sizes, dtype=np.int32)
+    freqs = np.ascontiguousarray(band_freqs, dtype=np.int32)
+    fo = np.zeros(sizes.size + 1, dtype=np.int64)
+    fe = np.zeros(sizes.size + 1, dtype=np.int64)
+    bpf = np.zeros(n_bins, dtype=np.int32)
+    check(lib().stx_bands_layout(_np_ptr(sizes), sizes.size, _np_ptr(freqs), freqs.size, int(n_bins), int(channels),
+                                 _np_ptr(fo), _np_ptr(fe), _np_ptr(bpf)))
+    return fo, fe, bpf
+
+
+class Bands:
+    """Device band table of a RoFormer (src/roformer.cpp:394-411)."""
+
+    def __init__(self, band_sizes, band_freqs, n_bins, channels):
+        import numpy as np
+        self.sizes = np.ascontiguousarray(band_sizes, dtype=np.int32)
+        self.freqs = np.ascontiguousarray(band_freqs, dtype=np.int32)
+        h = ctypes.c_void_p()
+        check(lib().stx_bands_create(_np_ptr(self.sizes), self.sizes.size, _np_ptr(self.freqs), self.freqs.size,
+                                     int(n_bins), int(channels), ctypes.byref(h)))
+        self.handle = h
+        self.n_bins = int(n_bins)
+        self.channels = int(channels)
+        self.total_feat = lib().stx_bands_total_feat(h)
+
+    def close(self):
+        if getattr(self, "handle", None):
+            lib().stx_bands_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def gather(self, spec, n_frames, layout=T_MAJOR, out=None, stream=None):
+        """spec: complex64 [batch, C, F, T] or [batch, C, T, F] -> float32 [batch, total_feat * T]."""
+        import torch
+        _require(spec, torch.complex64, "spec")
+        batch = spec.shape[0]
+        if out is None:
+            out = torch.empty((batch, self.total_feat * n_frames), dtype=torch.float32, device=spec.device)
+        check(lib().stx_band_gather(self.handle, _ptr(spec), batch, int(n_frames), int(layout), _ptr(out),
+                                    _stream(stream)))
+        return out
+
+    def scatter_apply(self, masks, spec, n_frames, layout=T_MAJOR, zero_dc=False, out=None, stream=None):
+        """masks: float32 [batch, S, total_feat * T]; spec: complex64 [batch, C, ...] ->
+        complex64 [batch, S, C, ...]."""
+        import torch
+        _require(masks, torch.float32, "masks")
+        _require(spec, torch.complex64, "spec")
+        batch, S = masks.shape[0], masks.shape[1]
+        if out is None:
+            out = torch.empty((batch, S) + tuple(spec.shape[1:]), dtype=torch.complex64, device=spec.device)
+        check(lib().stx_band_scatter_apply(self.handle, _ptr(masks), S, _ptr(spec), batch, int(n_frames), int(layout),
+                                           int(bool(zero_dc)), _ptr(out), _stream(stream)))
+        return out

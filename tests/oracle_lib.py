@@ -102,3 +102,74 @@ def reference():
 
 def ref_available():
     return os.path.exists(REF_PATH)
+
+
+class _Bands:
+    """The band-path oracle functions (oracle/band_oracle.c) with numpy in/out."""
+
+    def __init__(self):
+        self.L = ctypes.CDLL(ORACLE_PATH)
+        L = self.L
+        L.orc_mel_band_map.restype = _i
+        L.orc_mel_band_map.argtypes = [_i, _i, _i, _vp, _vp, ctypes.c_long, _vp]
+        L.orc_bands_layout.restype = _i
+        L.orc_bands_layout.argtypes = [_vp, _i, _vp, ctypes.c_long, _i, _i, _vp, _vp, _vp]
+        L.orc_band_gather.restype = None
+        L.orc_band_gather.argtypes = [_vp, _i, _vp, _i, _i, _i, _vp, _vp]
+        L.orc_band_scatter_apply.restype = None
+        L.orc_band_scatter_apply.argtypes = [_vp, _i, _vp, _i, _i, _i, _vp, _i, _vp, _i, _vp]
+
+    def mel_band_map(self, sr, n_fft, n_mels):
+        sizes = np.zeros(n_mels, dtype=np.int32)
+        cap = n_mels * (n_fft // 2 + 1)
+        freqs = np.zeros(cap, dtype=np.int32)
+        n = ctypes.c_long(0)
+        rc = self.L.orc_mel_band_map(sr, n_fft, n_mels, _np(sizes), _np(freqs), cap, ctypes.byref(n))
+        if rc:
+            raise RuntimeError(f"mel_band_map rc={rc}")
+        return sizes, freqs[: n.value].copy()
+
+    def layout(self, sizes, freqs, n_bins, channels):
+        sizes = np.ascontiguousarray(sizes, dtype=np.int32)
+        freqs = np.ascontiguousarray(freqs, dtype=np.int32)
+        fo = np.zeros(sizes.size + 1, dtype=np.int64)
+        fe = np.zeros(sizes.size + 1, dtype=np.int64)
+        bpf = np.zeros(n_bins, dtype=np.int32)
+        rc = self.L.orc_bands_layout(_np(sizes), sizes.size, _np(freqs), freqs.size, n_bins, channels,
+                                     _np(fo), _np(fe), _np(bpf))
+        if rc:
+            raise RuntimeError(f"bands_layout rc={rc}")
+        return fo, fe, bpf
+
+    def gather(self, sizes, freqs, z):
+        """z: complex128 [C][F][T] -> feat float32 [total_feat * T]."""
+        sizes = np.ascontiguousarray(sizes, dtype=np.int32)
+        freqs = np.ascontiguousarray(freqs, dtype=np.int32)
+        z = np.ascontiguousarray(z, dtype=np.complex128)
+        C, F, T = z.shape
+        feat = np.zeros(int(sizes.sum()) * C * 2 * T, dtype=np.float32)
+        self.L.orc_band_gather(_np(sizes), sizes.size, _np(freqs), C, F, T, _np(z), _np(feat))
+        return feat
+
+    def scatter_apply(self, sizes, freqs, masks, z, zero_dc=False):
+        """masks: float32 [S][total_feat * T], z: complex128 [C][F][T] -> complex128 [S][C][F][T]."""
+        sizes = np.ascontiguousarray(sizes, dtype=np.int32)
+        freqs = np.ascontiguousarray(freqs, dtype=np.int32)
+        masks = np.ascontiguousarray(masks, dtype=np.float32)
+        z = np.ascontiguousarray(z, dtype=np.complex128)
+        C, F, T = z.shape
+        S = masks.shape[0]
+        out = np.zeros((S, C, F, T), dtype=np.complex128)
+        self.L.orc_band_scatter_apply(_np(sizes), sizes.size, _np(freqs), C, F, T, _np(masks), S, _np(z),
+                                      int(bool(zero_dc)), _np(out))
+        return out
+
+
+_bands = None
+
+
+def bands():
+    global _bands
+    if _bands is None:
+        _bands = _Bands()
+    return _bands

@@ -1,0 +1,152 @@
+"""GPU parity of the band path (bands.hip) against the oracle.
+
+Band gather and scatter-average + apply are compared bit for bit with the oracle fed the same
+complex64 spectrum (both accumulate the masks in double in the reference's order and round
+once). The whole RoFormer spectral path on one 8 s stereo chunk (STFT 2048/441 -> band gather
+-> seeded masks -> scatter-average + apply -> iSTFT) is compared with the oracle's double
+path at SNR >= 110 dB per stem and channel (tools/stems-parity.cpp:36).
+"""
+import numpy as np
+import pytest
+
+import oracle_lib
+import stx
+import synth
+from metrics import snr_db
+
+pytestmark = pytest.mark.gpu
+
+SR, NFFT, HOP, NMELS = 44100, 2048, 441, 60
+BS_FPB = [2] * 24 + [4] * 12 + [12] * 8 + [24] * 8 + [48] * 8 + [128, 129]
+
+
+@pytest.fixture(scope="module")
+def ob():
+    return oracle_lib.bands()
+
+
+@pytest.fixture(scope="module")
+def mel():
+    return stx.mel_band_map(SR, NFFT, NMELS)
+
+
+def dev(a, device):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def rand_spec(seed, batch, C, F, T):
+    v = synth.normal(seed, (2, batch, C, F, T), 1.0)
+    return (v[0] + 1j * v[1]).astype(np.complex64)            # [batch][C][F][T]
+
+
+@pytest.mark.parametrize("kind", ["mel", "bs"])
+@pytest.mark.parametrize("layout", [stx.F_MAJOR, stx.T_MAJOR])
+def test_gather_bit_exact(device, ob, mel, kind, layout):
+    sizes, freqs = mel if kind == "mel" else (np.array(BS_FPB, np.int32), np.arange(1025, dtype=np.int32))
+    C, F, T, batch = 2, 1025, 801, 2
+    z = rand_spec(11, batch, C, F, T)
+    bands = stx.Bands(sizes, freqs, F, C)
+    zd = z if layout == stx.F_MAJOR else np.ascontiguousarray(z.transpose(0, 1, 3, 2))
+    feat = host(bands.gather(dev(zd, device), T, layout=layout))
+    assert feat.shape == (batch, int(sizes.sum()) * C * 2 * T)
+    for b in range(batch):
+        assert np.array_equal(feat[b], ob.gather(sizes, freqs, z[b].astype(np.complex128)))
+
+
+@pytest.mark.parametrize("kind", ["mel", "bs"])
+@pytest.mark.parametrize("layout", [stx.F_MAJOR, stx.T_MAJOR])
+@pytest.mark.parametrize("S,zero_dc", [(1, False), (4, True)])
+def test_scatter_apply_bit_exact(device, ob, mel, kind, layout, S, zero_dc):
+    sizes, freqs = mel if kind == "mel" else (np.array(BS_FPB, np.int32), np.arange(1025, dtype=np.int32))
+    C, F, T, batch = 2, 1025, 801 if S == 1 else 97, 2
+    z = rand_spec(12, batch, C, F, T)
+    tf = int(sizes.sum()) * C * 2
+    masks = synth.uniform(13, (batch, S, tf * T))
+    bands = stx.Bands(sizes, freqs, F, C)
+    zd = z if layout == stx.F_MAJOR else np.ascontiguousarray(z.transpose(0, 1, 3, 2))
+    out = host(bands.scatter_apply(dev(masks, device), dev(zd, device), T, layout=layout, zero_dc=zero_dc))
+    if layout == stx.T_MAJOR:
+        out = out.transpose(0, 1, 2, 4, 3)
+    for b in range(batch):
+        ref = ob.scatter_apply(sizes, freqs, masks[b], z[b].astype(np.complex128), zero_dc)
+        assert np.array_equal(out[b], ref.astype(np.complex64))
+
+
+def test_small_random_table_bit_exact(device, ob):
+    from test_oracle_bands import random_table
+    sizes, freqs = random_table(5, 33, 9)
+    C, F, T, S, batch = 3, 33, 19, 2, 3
+    z = rand_spec(14, batch, C, F, T)
+    bands = stx.Bands(sizes, freqs, F, C)
+    for layout in (stx.F_MAJOR, stx.T_MAJOR):
+        zd = z if layout == stx.F_MAJOR else np.ascontiguousarray(z.transpose(0, 1, 3, 2))
+        feat = host(bands.gather(dev(zd, device), T, layout=layout))
+        masks = synth.uniform(15, (batch, S, bands.total_feat * T))
+        out = host(bands.scatter_apply(dev(masks, device), dev(zd, device), T, layout=layout))
+        if layout == stx.T_MAJOR:
+            out = out.transpose(0, 1, 2, 4, 3)
+        for b in range(batch):
+            zb = z[b].astype(np.complex128)
+            assert np.array_equal(feat[b], ob.gather(sizes, freqs, zb))
+            assert np.array_equal(out[b], ob.scatter_apply(sizes, freqs, masks[b], zb).astype(np.complex64))
+
+
+@pytest.mark.parametrize("S", [1, 4])
+def test_roformer_spectral_path_c3(device, mel, S):
+    # One RoFormer chunk: stereo 352,800 samples, n_fft 2048, hop 441, 60 mel bands; per-band
+    # complex masks uniform in [-1, 1]; GPU path in the T-major layout.
+    import torch
+    sizes, freqs = mel
+    orc = oracle_lib.oracle()
+    C, L = 2, 352800
+    x = synth.normal(2027, (C, L), 0.1)
+    fft = stx.FFT(NFFT)
+    bands = stx.Bands(sizes, freqs, NFFT // 2 + 1, C)
+    spec = stx.torch_stft(fft, dev(x, device), HOP, layout=stx.T_MAJOR)          # [C][T][F]
+    T = spec.shape[1]
+    feat = bands.gather(spec[None], T)
+    masks = dev(synth.uniform(2028, (1, S, bands.total_feat * T)), device)
+    y_spec = bands.scatter_apply(masks, spec[None], T)[0]                         # [S][C][T][F]
+    y = stx.torch_istft(fft, y_spec.reshape(S * C, T, NFFT // 2 + 1), HOP, layout=stx.T_MAJOR)
+    y = host(y).reshape(S, C, -1)
+    # Oracle: double STFT, band masks, double iSTFT.
+    z = np.stack([orc.torch_stft(x[c], NFFT, HOP) for c in range(C)])             # [C][F][T]
+    feat_ref = oracle_lib.bands().gather(sizes, freqs, z)
+    assert snr_db(host(feat)[0], feat_ref) >= 110.0
+    ys = oracle_lib.bands().scatter_apply(sizes, freqs, host(masks)[0], z)        # [S][C][F][T]
+    for s in range(S):
+        for c in range(C):
+            yref = orc.torch_istft(ys[s, c], NFFT, HOP)
+            assert snr_db(y[s, c], yref) >= 110.0
+    del torch
+
+
+def test_all_ones_masks_reconstruct_input(device, mel):
+    # An all-ones mask in every band averages to 1 on every bin, so the path is STFT -> iSTFT.
+    sizes, freqs = mel
+    C, L = 2, 44100 * 2
+    x = synth.normal(31, (C, L), 0.1)
+    fft = stx.FFT(NFFT)
+    bands = stx.Bands(sizes, freqs, NFFT // 2 + 1, C)
+    spec = stx.torch_stft(fft, dev(x, device), HOP, layout=stx.T_MAJOR)
+    T = spec.shape[1]
+    import torch
+    ones = torch.ones((1, 1, bands.total_feat * T), dtype=torch.float32, device=device)
+    ones[..., 1::2] = 0.0                                                          # 1 + 0i
+    out = bands.scatter_apply(ones, spec[None], T)[0, 0]
+    y = host(stx.torch_istft(fft, out, HOP, layout=stx.T_MAJOR))
+    n = (T - 1) * HOP
+    assert snr_db(y, x[:, :n]) >= 110.0
+
+
+def test_band_table_errors(device):
+    with pytest.raises(stx.StxError) as e:
+        stx.Bands(np.array([2, 2], np.int32), np.array([0, 1, 2], np.int32), 8, 2)
+    assert e.value.status == stx.STATUS_RUNTIME_ERROR
