@@ -188,6 +188,102 @@ STX_API stx_status stx_band_scatter_apply(const stx_bands* bands, const float* m
                                           stx_spec_layout layout, int zero_dc, float* out,
                                           stx_stream stream);
 
+/* ------------------------------------------------------------------------------------------
+ * Chunked overlap-add demix. Replaces RoFormer::Impl::demix (src/roformer.cpp:286-351),
+ * n_chunks (:353-357) and RoFormer::separate (:436-486): chunks of `chunk` samples every `step`
+ * over the input reflect-padded by border = chunk - step on both sides (when
+ * len > 2 * border > 0), linear fades of chunk / 10 samples at both ends of every chunk's
+ * weight (none at the start of the first chunk, none at the end of a chunk reaching the end),
+ * sum of weight * output over chunks in double, divided by the summed weights; non-finite
+ * results become 0 (np.nan_to_num).
+ * ---------------------------------------------------------------------------------------- */
+enum {
+    STX_CHUNK_FULL    = 0,     /* length == chunk */
+    STX_CHUNK_REFLECT = 1,     /* short chunk reflect-padded to `chunk` (length > chunk/2 + 1) */
+    STX_CHUNK_ZERO    = 2      /* short chunk zero-padded (src/roformer.cpp:323-330) */
+};
+
+typedef struct {
+    int64_t start;             /* first sample in the padded signal (k * step) */
+    int32_t length;            /* samples taken from the padded signal, <= chunk */
+    int32_t pad_mode;          /* STX_CHUNK_* */
+    int32_t fade_in;           /* 1: the weight keeps its fade-in (0 for the first chunk) */
+    int32_t fade_out;          /* 1: the weight keeps its fade-out (0 for chunks reaching the end) */
+} stx_chunk;
+
+typedef struct {
+    int64_t len;               /* samples per channel */
+    int64_t padded_len;        /* Lp */
+    int64_t n_chunks;
+    int32_t chunk, step, border, fade, reflect_border;
+} stx_demix_geometry;
+
+/* Step of RoFormer::separate (src/roformer.cpp:442-443): chunk / num_overlap for overlap < 0,
+ * else max(1, lround(chunk * (1 - overlap))); 0 for overlap >= 1 (the reference rejects it). */
+STX_API int stx_demix_step(int chunk, int num_overlap, float overlap);
+
+/* The integer chunk table (host only): geometry, and chunks[n_chunks] unless chunks is NULL.
+ * INVALID_ARGUMENT for len <= 0 ("empty input") or chunk/step <= 0. */
+STX_API stx_status stx_demix_plan(int64_t len, int chunk, int step, stx_demix_geometry* geom,
+                                  stx_chunk* chunks, int64_t capacity);
+
+/* The fade window of src/roformer.cpp:303-313 (host only): window[chunk] floats, before the
+ * first/last chunk edits. */
+STX_API stx_status stx_demix_window(int chunk, float* window);
+
+typedef struct stx_demix stx_demix;
+
+/* Device plan for one input length: geometry and window on the device. */
+STX_API stx_status stx_demix_create(int64_t len, int channels, int chunk, int step, stx_demix** out);
+STX_API void       stx_demix_destroy(stx_demix* demix);
+STX_API int64_t    stx_demix_n_chunks(const stx_demix* demix);
+
+/* Chunk inputs first .. first+count-1 (src/roformer.cpp:289-331): mix is device [C][len],
+ * parts is device [count][C][chunk]; the border and short-chunk padding are done on the fly. */
+STX_API stx_status stx_demix_chunks(const stx_demix* demix, const float* mix, int64_t first, int64_t count,
+                                    float* parts, stx_stream stream);
+
+/* Overlap-add of every chunk's separated output (src/roformer.cpp:334-350): y is device
+ * [n_chunks][n_stems][C][chunk], out is device [n_stems][C][len]. Bit-identical to the
+ * reference for identical chunk outputs. */
+STX_API stx_status stx_demix_overlap_add(const stx_demix* demix, const float* y, int n_stems, float* out,
+                                         stx_stream stream);
+
+/* Separator callback of stx_demix_track: separates chunks first .. first+count-1. parts is
+ * device [count][C][chunk] (read only), y is device [count][n_stems][C][chunk] (to fill).
+ * Work may be enqueued on `stream`; return 0 on success. */
+typedef int32_t (*stx_separate_fn)(void* user, const float* parts, int64_t first, int64_t count, float* y,
+                                   stx_stream stream);
+typedef void (*stx_progress_fn)(void* user, int32_t done, int32_t total);
+typedef int32_t (*stx_cancel_fn)(void* user);
+
+/* st::SeparateOptions (src/separator.h:19-32). */
+typedef struct {
+    int32_t shifts;                /* random time shifts averaged; 0 = one deterministic pass */
+    float overlap;                 /* [0, 1); negative = the model's num_overlap */
+    uint32_t seed;                 /* for the shift offsets (std::mt19937) */
+    stx_progress_fn progress;      /* (done, total) chunk passes; may be NULL */
+    stx_cancel_fn should_cancel;   /* polled before every chunk; non-zero cancels; may be NULL */
+    void* user;
+} stx_separate_options;
+
+/* Bytes of device workspace stx_demix_track needs (batch = chunks per separator call). */
+STX_API size_t stx_demix_track_workspace_size(int channels, int64_t len, int chunk, int step, int n_stems,
+                                              int batch, int shifts, int sample_rate);
+
+/* RoFormer::separate (src/roformer.cpp:436-486) around any separator: step from
+ * num_overlap/overlap (:442-443), demix (:286-351) through `separate` in batches of `batch`
+ * chunks, demucs' shift averaging (:456-478, offsets from std::mt19937(seed)), and, when
+ * `complement`, one more output plane mix - stem 0 (:481-485). mix is device [C][len]; out is
+ * device [n_stems + complement][C][len]. CANCELLED when should_cancel returns non-zero;
+ * INVALID_ARGUMENT for len <= 0 ("empty input") or overlap >= 1. Progress and cancel callbacks
+ * run on the calling thread, before each chunk. */
+STX_API stx_status stx_demix_track(const float* mix, int channels, int64_t len, int chunk, int num_overlap,
+                                   int n_stems, int complement, int sample_rate, int batch,
+                                   stx_separate_fn separate, void* separate_user,
+                                   const stx_separate_options* options, float* out, void* workspace,
+                                   size_t workspace_bytes, stx_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -25,6 +25,11 @@
  *     independent numpy formulations on small tables, and invariants (gather then scatter of
  *     bin-constant masks returns the spectrum times that constant; band counts sum to the
  *     table size).
+ *   orc_demix_*: the chunk table the survey of the reference derived for 180 s at chunk 352,800
+ *     and step 88,200 (96 chunks, four without fade-out, short chunks of 264,600 (reflect),
+ *     176,400 and 88,200 (zero) samples), torch.linspace(0, 1, fade) in float32 for the fade
+ *     (the reference computes "the way torch does"), and the identity separator, which must
+ *     return the input (sum of w * x over sum of w).
  */
 #ifndef STX_ORACLE_H
 #define STX_ORACLE_H
@@ -71,6 +76,18 @@ void orc_band_gather(const int* band_sizes, int n_bands, const int* band_freqs, 
  * z complex [C][F][T] -> out complex [S][C][F][T] (before the iSTFT). */
 void orc_band_scatter_apply(const int* band_sizes, int n_bands, const int* band_freqs, int C, int F, int T,
                             const float* masks, int S, const double* z, int zero_dc, double* out);
+
+/* Chunk count of src/roformer.cpp:353-357. */
+long orc_demix_n_chunks(long len, int chunk, int step);
+
+/* Fade window of src/roformer.cpp:303-313 (window[chunk]). */
+void orc_demix_window(int chunk, float* window);
+
+/* Chunk inputs of src/roformer.cpp:289-331: mix [C][len] -> parts [n_chunks][C][chunk]. */
+int orc_demix_chunks(const float* mix, int C, long len, int chunk, int step, float* parts);
+
+/* Overlap-add of src/roformer.cpp:334-350: y [n_chunks][S][C][chunk] -> out [S][C][len]. */
+int orc_demix_ola(const float* y, int S, int C, long len, int chunk, int step, float* out);
 
 #ifdef __cplusplus
 }

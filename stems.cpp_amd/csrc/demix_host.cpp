@@ -1,0 +1,103 @@
+// demix_host.cpp — host-side bookkeeping of the chunked overlap-add demix.
+//
+// Reference: RoFormer::Impl::demix (src/roformer.cpp:286-351), n_chunks (:353-357) and the step
+// rule of RoFormer::separate (:442-443). Everything here is integer or single float operations
+// in the reference's order, so the chunk table and the fade window are bit-identical to the
+// reference's.
+#include <cmath>
+#include <vector>
+
+#include "common.hpp"
+#include "demix_host.hpp"
+
+namespace stx {
+
+DemixGeometry demix_geometry(int64_t len, int chunk, int step) {
+    STX_REQUIRE(len > 0, "empty input");
+    STX_REQUIRE(chunk > 0 && step > 0, "bad chunk/step");
+    DemixGeometry g;
+    g.len = len;
+    g.chunk = chunk;
+    g.step = step;
+    g.fade = chunk / 10;
+    g.border = chunk - step;
+    g.reflect_border = (len > 2LL * g.border && g.border > 0) ? 1 : 0;      // :290
+    g.padded_len = g.reflect_border ? len + 2LL * g.border : len;           // :291
+    g.n_chunks = (g.padded_len + step - 1) / step;                          // :353-357
+    return g;
+}
+
+stx_chunk demix_chunk(const DemixGeometry& g, int64_t k) {
+    stx_chunk c{};
+    const int64_t i = k * g.step;
+    c.start = i;
+    c.length = (int32_t)std::min<int64_t>(g.chunk, g.padded_len - i);      // :318
+    if (c.length == g.chunk) c.pad_mode = STX_CHUNK_FULL;
+    else if (c.length > g.chunk / 2 + 1) c.pad_mode = STX_CHUNK_REFLECT;    // :324
+    else c.pad_mode = STX_CHUNK_ZERO;
+    // :335-336: the first chunk drops its fade-in, otherwise a chunk reaching the end drops its
+    // fade-out.
+    c.fade_in = i == 0 ? 0 : 1;
+    c.fade_out = (i != 0 && i + g.chunk >= g.padded_len) ? 0 : 1;
+    return c;
+}
+
+void demix_window(int chunk, float* window) {
+    const int fade = chunk / 10;
+    // torch.linspace(0, 1, fade) in float32, from both ends (:303-309); fade_in stays zero when
+    // fade == 1 (only fade > 1 fills it).
+    std::vector<float> fade_in(std::max(fade, 0), 0.0f);
+    if (fade > 1) {
+        const float stp = 1.0f / (float)(fade - 1);
+        for (int i = 0; i < fade; i++)
+            fade_in[i] = i < fade / 2 ? (float)i * stp : 1.0f - (float)(fade - 1 - i) * stp;
+    }
+    for (int t = 0; t < chunk; t++) window[t] = 1.0f;
+    for (int i = 0; i < fade; i++) {                                        // :310-313
+        window[i] *= fade_in[i];
+        window[chunk - 1 - i] *= fade_in[i];
+    }
+}
+
+}  // namespace stx
+
+using namespace stx;
+
+extern "C" {
+
+STX_API int stx_demix_step(int chunk, int num_overlap, float overlap) {
+    if (chunk <= 0) return 0;
+    if (overlap < 0.0f) return num_overlap > 0 ? chunk / num_overlap : 0;                  // :442
+    if (overlap >= 1.0f) return 0;                                                          // :440
+    return std::max(1, (int)std::lround(chunk * (1.0 - overlap)));                          // :443
+}
+
+STX_API stx_status stx_demix_plan(int64_t len, int chunk, int step, stx_demix_geometry* geom, stx_chunk* chunks,
+                                  int64_t capacity) {
+    return guard([&] {
+        const DemixGeometry g = demix_geometry(len, chunk, step);
+        if (geom) {
+            geom->len = g.len;
+            geom->padded_len = g.padded_len;
+            geom->chunk = g.chunk;
+            geom->step = g.step;
+            geom->border = g.border;
+            geom->fade = g.fade;
+            geom->reflect_border = g.reflect_border;
+            geom->n_chunks = g.n_chunks;
+        }
+        if (!chunks) return;
+        STX_REQUIRE(capacity >= g.n_chunks, "chunk table capacity %lld < %lld", (long long)capacity,
+                    (long long)g.n_chunks);
+        for (int64_t k = 0; k < g.n_chunks; k++) chunks[k] = demix_chunk(g, k);
+    });
+}
+
+STX_API stx_status stx_demix_window(int chunk, float* window) {
+    return guard([&] {
+        STX_REQUIRE(chunk > 0 && window, "bad chunk/window");
+        demix_window(chunk, window);
+    });
+}
+
+}  // extern "C"

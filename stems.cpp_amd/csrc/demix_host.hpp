@@ -1,0 +1,24 @@
+// demix_host.hpp — chunk geometry of the overlap-add demix, shared by demix_host.cpp and demix.hip.
+#pragma once
+
+#include <cstdint>
+
+#include "stx.h"
+
+namespace stx {
+
+struct DemixGeometry {
+    int64_t len = 0;             // samples per channel of the input
+    int64_t padded_len = 0;      // Lp: len + 2 * border when the borders are reflect-padded
+    int64_t n_chunks = 0;
+    int chunk = 0, step = 0;
+    int border = 0;              // chunk - step
+    int fade = 0;                // chunk / 10
+    int reflect_border = 0;      // len > 2 * border && border > 0
+};
+
+DemixGeometry demix_geometry(int64_t len, int chunk, int step);   // throws stx::Error
+stx_chunk demix_chunk(const DemixGeometry& g, int64_t k);
+void demix_window(int chunk, float* window);
+
+}  // namespace stx

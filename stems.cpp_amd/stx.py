@@ -51,6 +51,17 @@ _SIGNATURES = {
     "stx_bands_total_feat": (ctypes.c_int64, [_vp]),
     "stx_band_gather": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp]),
     "stx_band_scatter_apply": (_i, [_vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _vp]),
+    "stx_demix_step": (_i, [_i, _i, ctypes.c_float]),
+    "stx_demix_plan": (_i, [ctypes.c_int64, _i, _i, _vp, _vp, ctypes.c_int64]),
+    "stx_demix_window": (_i, [_i, _vp]),
+    "stx_demix_create": (_i, [ctypes.c_int64, _i, _i, _i, ctypes.POINTER(_vp)]),
+    "stx_demix_destroy": (None, [_vp]),
+    "stx_demix_n_chunks": (ctypes.c_int64, [_vp]),
+    "stx_demix_chunks": (_i, [_vp, _vp, ctypes.c_int64, ctypes.c_int64, _vp, _vp]),
+    "stx_demix_overlap_add": (_i, [_vp, _vp, _i, _vp, _vp]),
+    "stx_demix_track_workspace_size": (ctypes.c_size_t, [_i, ctypes.c_int64, _i, _i, _i, _i, _i, _i]),
+    "stx_demix_track": (_i, [_vp, _i, ctypes.c_int64, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp,
+                             ctypes.c_size_t, _vp]),
 }
 
 
@@ -313,3 +324,134 @@ class Bands:
         check(lib().stx_band_scatter_apply(self.handle, _ptr(masks), S, _ptr(spec), batch, int(n_frames), int(layout),
                                            int(bool(zero_dc)), _ptr(out), _stream(stream)))
         return out
+
+
+# ------------------------------------------------------------------------------- demix
+CHUNK_FULL, CHUNK_REFLECT, CHUNK_ZERO = 0, 1, 2
+
+
+class DemixGeometry(ctypes.Structure):
+    _fields_ = [("len", ctypes.c_int64), ("padded_len", ctypes.c_int64), ("n_chunks", ctypes.c_int64),
+                ("chunk", ctypes.c_int32), ("step", ctypes.c_int32), ("border", ctypes.c_int32),
+                ("fade", ctypes.c_int32), ("reflect_border", ctypes.c_int32)]
+
+
+class Chunk(ctypes.Structure):
+    _fields_ = [("start", ctypes.c_int64), ("length", ctypes.c_int32), ("pad_mode", ctypes.c_int32),
+                ("fade_in", ctypes.c_int32), ("fade_out", ctypes.c_int32)]
+
+
+SEPARATE_FN = ctypes.CFUNCTYPE(ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                               ctypes.c_void_p, ctypes.c_void_p)
+PROGRESS_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32)
+CANCEL_FN = ctypes.CFUNCTYPE(ctypes.c_int32, ctypes.c_void_p)
+
+
+class SeparateOptions(ctypes.Structure):
+    _fields_ = [("shifts", ctypes.c_int32), ("overlap", ctypes.c_float), ("seed", ctypes.c_uint32),
+                ("progress", PROGRESS_FN), ("should_cancel", CANCEL_FN), ("user", ctypes.c_void_p)]
+
+
+def demix_step(chunk, num_overlap, overlap=-1.0):
+    return lib().stx_demix_step(int(chunk), int(num_overlap), float(overlap))
+
+
+def demix_plan(length, chunk, step):
+    """(geometry dict, numpy structured chunk table) of the overlap-add demix (host only)."""
+    import numpy as np
+    g = DemixGeometry()
+    check(lib().stx_demix_plan(int(length), int(chunk), int(step), ctypes.byref(g), None, 0))
+    table = (Chunk * max(1, g.n_chunks))()
+    check(lib().stx_demix_plan(int(length), int(chunk), int(step), ctypes.byref(g), table, g.n_chunks))
+    geom = {f: getattr(g, f) for f, _ in DemixGeometry._fields_}
+    arr = np.array([(c.start, c.length, c.pad_mode, c.fade_in, c.fade_out) for c in table[: g.n_chunks]],
+                   dtype=[("start", np.int64), ("length", np.int32), ("pad_mode", np.int32),
+                          ("fade_in", np.int32), ("fade_out", np.int32)])
+    return geom, arr
+
+
+def demix_window(chunk):
+    import numpy as np
+    w = np.zeros(chunk, dtype=np.float32)
+    check(lib().stx_demix_window(int(chunk), _np_ptr(w)))
+    return w
+
+
+class Demix:
+    """Device plan of the overlap-add demix for one input length."""
+
+    def __init__(self, length, channels, chunk, step):
+        h = ctypes.c_void_p()
+        check(lib().stx_demix_create(int(length), int(channels), int(chunk), int(step), ctypes.byref(h)))
+        self.handle = h
+        self.length, self.channels, self.chunk, self.step = int(length), int(channels), int(chunk), int(step)
+        self.n_chunks = lib().stx_demix_n_chunks(h)
+
+    def close(self):
+        if getattr(self, "handle", None):
+            lib().stx_demix_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def chunks(self, mix, first=0, count=None, out=None, stream=None):
+        """mix float32 [C, len] -> parts float32 [count, C, chunk]."""
+        import torch
+        _require(mix, torch.float32, "mix")
+        count = self.n_chunks - first if count is None else count
+        if out is None:
+            out = torch.empty((count, self.channels, self.chunk), dtype=torch.float32, device=mix.device)
+        check(lib().stx_demix_chunks(self.handle, _ptr(mix), int(first), int(count), _ptr(out), _stream(stream)))
+        return out
+
+    def overlap_add(self, y, out=None, stream=None):
+        """y float32 [n_chunks, S, C, chunk] -> float32 [S, C, len]."""
+        import torch
+        _require(y, torch.float32, "y")
+        S = y.shape[1]
+        if out is None:
+            out = torch.empty((S, self.channels, self.length), dtype=torch.float32, device=y.device)
+        check(lib().stx_demix_overlap_add(self.handle, _ptr(y), int(S), _ptr(out), _stream(stream)))
+        return out
+
+
+def demix_track(mix, chunk, num_overlap, n_stems, separate, complement=False, sample_rate=44100, batch=8,
+                shifts=0, overlap=-1.0, seed=0, progress=None, should_cancel=None, stream=None):
+    """RoFormer::separate around a Python separator.
+
+    separate(parts_ptr, first, count, y_ptr, stream_ptr) -> int gets raw device pointers:
+    parts [count][C][chunk] and y [count][n_stems][C][chunk] float32."""
+    import torch
+    _require(mix, torch.float32, "mix")
+    C, L = mix.shape
+    step = demix_step(chunk, num_overlap, overlap)
+    ws_bytes = lib().stx_demix_track_workspace_size(C, L, chunk, max(step, 1), n_stems, batch, shifts, sample_rate)
+    ws = workspace(max(ws_bytes, 4), mix.device)
+    out = torch.empty((n_stems + (1 if complement else 0), C, L), dtype=torch.float32, device=mix.device)
+
+    def sep(user, parts, first, count, y, st):
+        try:
+            return int(separate(parts, first, count, y, st))
+        except Exception:
+            import traceback
+            traceback.print_exc()
+            return -1
+
+    def prog(user, done, total):
+        progress(done, total)
+
+    def canc(user):
+        return 1 if should_cancel() else 0
+
+    cb = SEPARATE_FN(sep)
+    opt = SeparateOptions(int(shifts), float(overlap), int(seed),
+                          PROGRESS_FN(prog) if progress else PROGRESS_FN(),
+                          CANCEL_FN(canc) if should_cancel else CANCEL_FN(), None)
+    check(lib().stx_demix_track(_ptr(mix), C, L, int(chunk), int(num_overlap), int(n_stems), int(bool(complement)),
+                                int(sample_rate), int(batch), ctypes.cast(cb, ctypes.c_void_p), None,
+                                ctypes.byref(opt), _ptr(out), _ptr(ws), ws.numel() * 4, _stream(stream)))
+    return out

@@ -173,3 +173,54 @@ def bands():
     if _bands is None:
         _bands = _Bands()
     return _bands
+
+
+class _Demix:
+    """The demix oracle functions (oracle/demix_oracle.c) with numpy in/out."""
+
+    def __init__(self):
+        L = ctypes.CDLL(ORACLE_PATH)
+        L.orc_demix_n_chunks.restype = ctypes.c_long
+        L.orc_demix_n_chunks.argtypes = [ctypes.c_long, _i, _i]
+        L.orc_demix_window.restype = None
+        L.orc_demix_window.argtypes = [_i, _vp]
+        L.orc_demix_chunks.restype = _i
+        L.orc_demix_chunks.argtypes = [_vp, _i, ctypes.c_long, _i, _i, _vp]
+        L.orc_demix_ola.restype = _i
+        L.orc_demix_ola.argtypes = [_vp, _i, _i, ctypes.c_long, _i, _i, _vp]
+        self.L = L
+
+    def n_chunks(self, length, chunk, step):
+        return self.L.orc_demix_n_chunks(length, chunk, step)
+
+    def window(self, chunk):
+        w = np.zeros(chunk, dtype=np.float32)
+        self.L.orc_demix_window(chunk, _np(w))
+        return w
+
+    def chunks(self, mix, chunk, step):
+        mix = np.ascontiguousarray(mix, dtype=np.float32)
+        C, length = mix.shape
+        n = self.n_chunks(length, chunk, step)
+        parts = np.zeros((n, C, chunk), dtype=np.float32)
+        rc = self.L.orc_demix_chunks(_np(mix), C, length, chunk, step, _np(parts))
+        if rc:
+            raise RuntimeError(f"demix_chunks rc={rc}")
+        return parts
+
+    def ola(self, y, length, chunk, step):
+        y = np.ascontiguousarray(y, dtype=np.float32)
+        n, S, C, _ = y.shape
+        out = np.zeros((S, C, length), dtype=np.float32)
+        self.L.orc_demix_ola(_np(y), S, C, length, chunk, step, _np(out))
+        return out
+
+
+_demix = None
+
+
+def demix():
+    global _demix
+    if _demix is None:
+        _demix = _Demix()
+    return _demix
