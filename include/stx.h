@@ -284,6 +284,82 @@ STX_API stx_status stx_demix_track(const float* mix, int channels, int64_t len, 
                                    const stx_separate_options* options, float* out, void* workspace,
                                    size_t workspace_bytes, stx_stream stream);
 
+/* ------------------------------------------------------------------------------------------
+ * ggml ops of the HTDemucs and RoFormer graphs. ggml's sources are not in the reference tree
+ * (an un-vendored submodule), so each entry point cites the call sites whose semantics it
+ * implements. Tensors are fp32 with ggml's shape convention: ne[0] is the fastest dimension,
+ * nb[] are byte strides, and rows must be contiguous (nb[0] == 4). Unused trailing dimensions
+ * have ne = 1. A broadcast operand "repeats into" dst when every dst->ne[i] is a multiple of
+ * its ne[i] (ggml_can_repeat). Normalisations and softmax compute their statistics in double
+ * and round once; ADD, MUL and MUL_ADD round after every operation like the separate ggml ops.
+ * ---------------------------------------------------------------------------------------- */
+typedef struct {
+    void* data;                    /* device */
+    int64_t ne[4];                 /* elements per dimension, ne[0] fastest */
+    int64_t nb[4];                 /* byte strides; nb[0] must be 4 */
+} stx_tensor;
+
+/* ggml_group_norm(a, n_groups, eps) (src/htdemucs.cpp:118,124,224), fused with the affine
+ * mul/add that follows it (:127,:226) and optionally with the GELU after that (:136). Channels
+ * (ne2) are split into groups of ceil(ne2 / n_groups); each group of each ne3 slice is
+ * normalised over ne0 x ne1 x its channels with the biased variance. weight and bias (either
+ * may be NULL) repeat into a; gelu != 0 applies GELU-erf last. a and dst must be contiguous
+ * (dst may be a). workspace: device, stx_group_norm_workspace_size() bytes. */
+STX_API size_t     stx_group_norm_workspace_size(const stx_tensor* a, int n_groups);
+STX_API stx_status stx_group_norm(const stx_tensor* a, const stx_tensor* dst, int n_groups, float eps,
+                                  const stx_tensor* weight, const stx_tensor* bias, int gelu, void* workspace,
+                                  size_t workspace_bytes, stx_stream stream);
+
+/* ggml_norm(a, eps) over ne0 (src/htdemucs.cpp:215): (x - mean) / sqrt(var + eps). */
+STX_API stx_status stx_norm(const stx_tensor* a, const stx_tensor* dst, float eps, stx_stream stream);
+/* layer_norm of src/htdemucs.cpp:213-215: ggml_norm then * weight[ne0] + bias[ne0], fused.
+ * weight or bias may be NULL. */
+STX_API stx_status stx_norm_affine(const stx_tensor* a, const float* weight, const float* bias, const stx_tensor* dst,
+                                   float eps, stx_stream stream);
+
+/* ggml_rms_norm(a, eps) over ne0 (src/roformer.cpp:34): x / sqrt(mean(x^2) + eps). */
+STX_API stx_status stx_rms_norm(const stx_tensor* a, const stx_tensor* dst, float eps, stx_stream stream);
+/* Graph::rms (src/roformer.cpp:96-98): ggml_rms_norm then * gamma[ne0], fused. */
+STX_API stx_status stx_rms_norm_mul(const stx_tensor* a, const float* gamma, const stx_tensor* dst, float eps,
+                                    stx_stream stream);
+
+/* ggml_soft_max_ext(a, mask, scale, max_bias) along ne0 (src/roformer.cpp:127,
+ * src/htdemucs.cpp:238): softmax(scale * x). The reference passes mask = NULL and
+ * max_bias = 0; anything else is UNSUPPORTED, as are rows longer than 2048. */
+STX_API stx_status stx_soft_max_ext(const stx_tensor* a, const stx_tensor* mask, const stx_tensor* dst, float scale,
+                                    float max_bias, stx_stream stream);
+
+/* ggml_gelu_erf(a) (src/roformer.cpp:147, src/htdemucs.cpp:136,154,210,246):
+ * x/2 * (1 + erf(x / sqrt2)). */
+STX_API stx_status stx_gelu_erf(const stx_tensor* a, const stx_tensor* dst, stx_stream stream);
+/* ggml_gelu_erf(ggml_add(a, b)) with b repeating into a: the bias add + GELU of the
+ * feed-forward layers (src/roformer.cpp:147, src/htdemucs.cpp:246), fused. */
+STX_API stx_status stx_add_gelu_erf(const stx_tensor* a, const stx_tensor* b, const stx_tensor* dst,
+                                    stx_stream stream);
+
+/* GLU, ggml_mul(first half, ggml_sigmoid(second half)) along dimension dim of a
+ * (src/htdemucs.cpp:105-110 splits ne2, src/roformer.cpp:199-202 splits ne0). dst has
+ * ne[dim] = a->ne[dim] / 2. */
+STX_API stx_status stx_glu(const stx_tensor* a, const stx_tensor* dst, int dim, stx_stream stream);
+
+/* ggml_add / ggml_mul with b repeating into a (src/htdemucs.cpp:100,139,220,
+ * src/roformer.cpp:97,136,145,148). */
+STX_API stx_status stx_add(const stx_tensor* a, const stx_tensor* b, const stx_tensor* dst, stx_stream stream);
+STX_API stx_status stx_mul(const stx_tensor* a, const stx_tensor* b, const stx_tensor* dst, stx_stream stream);
+/* ggml_add(x, ggml_mul(h, s)): LayerScale + residual (src/htdemucs.cpp:139,250-251), fused,
+ * with the same two roundings. h and s repeat into x. */
+STX_API stx_status stx_mul_add(const stx_tensor* x, const stx_tensor* h, const stx_tensor* s, const stx_tensor* dst,
+                               stx_stream stream);
+
+/* ggml_rope_ext(a, pos, NULL, n_dims, mode, n_ctx_orig, freq_base, freq_scale, ext_factor,
+ * attn_factor, beta_fast, beta_slow) (src/roformer.cpp:109-113): rotates each ne0 row of
+ * position pos[i2] (pos: device int32[ne2]) by theta_i = freq_scale * pos * freq_base^(-2i/n_dims).
+ * Mode 0 (the reference's) rotates adjacent pairs, mode 2 (NEOX) pairs (i, i + n_dims/2).
+ * ext_factor != 0 (YaRN) and other modes are UNSUPPORTED. */
+STX_API stx_status stx_rope_ext(const stx_tensor* a, const int32_t* pos, const stx_tensor* dst, int n_dims, int mode,
+                                int n_ctx_orig, float freq_base, float freq_scale, float ext_factor, float attn_factor,
+                                float beta_fast, float beta_slow, stx_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -25,6 +25,14 @@
  *     independent numpy formulations on small tables, and invariants (gather then scatter of
  *     bin-constant masks returns the spectrum times that constant; band counts sum to the
  *     table size).
+ *   orc_group_norm, orc_norm, orc_soft_max, orc_gelu_erf, orc_glu, orc_rope: torch's own
+ *     float64 implementations (F.group_norm, F.layer_norm, F.rms_norm, softmax, F.gelu, F.glu)
+ *     as an independent library, a complex-multiplication restatement of RoPE, and invariants
+ *     (normalised groups have mean 0 and variance var/(var+eps); softmax rows sum to 1;
+ *     gelu(x) - gelu(-x) = x; RoPE preserves pair norms and q.k depends only on the position
+ *     difference). ggml-specific rounding (the float theta recurrence of ggml's RoPE, its float
+ *     softmax and norm arithmetic) is parity unpinned: ggml's sources are not in the reference.
+ *   orc_binary: numpy's float32 arithmetic on explicitly tiled operands, bit for bit.
  *   orc_demix_*: the chunk table the survey of the reference derived for 180 s at chunk 352,800
  *     and step 88,200 (96 chunks, four without fade-out, short chunks of 264,600 (reflect),
  *     176,400 and 88,200 (zero) samples), torch.linspace(0, 1, fade) in float32 for the fade
@@ -88,6 +96,19 @@ int orc_demix_chunks(const float* mix, int C, long len, int chunk, int step, flo
 
 /* Overlap-add of src/roformer.cpp:334-350: y [n_chunks][S][C][chunk] -> out [S][C][len]. */
 int orc_demix_ola(const float* y, int S, int C, long len, int chunk, int step, float* out);
+
+/* ggml ops (ops_oracle.c). Contiguous tensors, ggml extents ne[4] (ne[0] fastest); broadcast
+ * operands repeat into ne. */
+int orc_group_norm(const float* x, const int64_t ne[4], int n_groups, float eps, const float* w, const int64_t wne[4],
+                   const float* b, const int64_t bne[4], int gelu, float* y);
+int orc_norm(const float* x, int64_t ne0, int64_t rows, float eps, int rms, const float* w, const float* b, float* y);
+int orc_soft_max(const float* x, int64_t ne0, int64_t rows, float scale, float* y);
+void orc_gelu_erf(const float* x, int64_t n, float* y);
+int orc_glu(const float* x, const int64_t ne[4], int dim, float* y);
+int orc_binary(int op, const float* a, const int64_t ne[4], const float* b, const int64_t bne[4], const float* c,
+               const int64_t cne[4], float* y);
+int orc_rope(const float* x, const int64_t ne[4], const int32_t* pos, int n_dims, int mode, float freq_base,
+             float freq_scale, float attn_factor, float* y);
 
 #ifdef __cplusplus
 }

@@ -62,6 +62,21 @@ _SIGNATURES = {
     "stx_demix_track_workspace_size": (ctypes.c_size_t, [_i, ctypes.c_int64, _i, _i, _i, _i, _i, _i]),
     "stx_demix_track": (_i, [_vp, _i, ctypes.c_int64, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp,
                              ctypes.c_size_t, _vp]),
+    "stx_group_norm_workspace_size": (ctypes.c_size_t, [_vp, _i]),
+    "stx_group_norm": (_i, [_vp, _vp, _i, ctypes.c_float, _vp, _vp, _i, _vp, ctypes.c_size_t, _vp]),
+    "stx_norm": (_i, [_vp, _vp, ctypes.c_float, _vp]),
+    "stx_norm_affine": (_i, [_vp, _vp, _vp, _vp, ctypes.c_float, _vp]),
+    "stx_rms_norm": (_i, [_vp, _vp, ctypes.c_float, _vp]),
+    "stx_rms_norm_mul": (_i, [_vp, _vp, _vp, ctypes.c_float, _vp]),
+    "stx_soft_max_ext": (_i, [_vp, _vp, _vp, ctypes.c_float, ctypes.c_float, _vp]),
+    "stx_gelu_erf": (_i, [_vp, _vp, _vp]),
+    "stx_add_gelu_erf": (_i, [_vp, _vp, _vp, _vp]),
+    "stx_glu": (_i, [_vp, _vp, _i, _vp]),
+    "stx_add": (_i, [_vp, _vp, _vp, _vp]),
+    "stx_mul": (_i, [_vp, _vp, _vp, _vp]),
+    "stx_mul_add": (_i, [_vp, _vp, _vp, _vp, _vp]),
+    "stx_rope_ext": (_i, [_vp, _vp, _vp, _i, _i, _i, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+                          ctypes.c_float, ctypes.c_float, ctypes.c_float, _vp]),
 }
 
 
@@ -454,4 +469,136 @@ def demix_track(mix, chunk, num_overlap, n_stems, separate, complement=False, sa
     check(lib().stx_demix_track(_ptr(mix), C, L, int(chunk), int(num_overlap), int(n_stems), int(bool(complement)),
                                 int(sample_rate), int(batch), ctypes.cast(cb, ctypes.c_void_p), None,
                                 ctypes.byref(opt), _ptr(out), _ptr(ws), ws.numel() * 4, _stream(stream)))
+    return out
+
+
+# --------------------------------------------------------------------------------- ops
+class Tensor(ctypes.Structure):
+    """stx_tensor: ggml's view of a tensor (ne[0] fastest, byte strides nb)."""
+    _fields_ = [("data", ctypes.c_void_p), ("ne", ctypes.c_int64 * 4), ("nb", ctypes.c_int64 * 4)]
+
+
+def as_tensor(t):
+    """stx_tensor of a float32 device tensor of up to 4 dims: torch's last dim is ne[0]."""
+    import torch
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise TypeError("operands must be CUDA (HIP) tensors")
+    if t.dtype != torch.float32:
+        raise TypeError(f"operands must be float32, got {t.dtype}")
+    if t.dim() > 4:
+        raise ValueError("at most 4 dimensions")
+    shape, strides = list(t.shape)[::-1], list(t.stride())[::-1]
+    d = Tensor()
+    d.data = t.data_ptr()
+    for i in range(4):
+        if i < len(shape):
+            d.ne[i] = shape[i]
+            d.nb[i] = 4 * strides[i]
+        else:                                   # missing leading torch dims: extent 1
+            d.ne[i] = 1
+            d.nb[i] = d.nb[i - 1] * d.ne[i - 1] if i else 4
+    if t.dim() == 0 or shape[0] == 1:
+        d.nb[0] = 4
+    return d
+
+
+def _t(t):
+    return None if t is None else ctypes.byref(as_tensor(t))
+
+
+def _out(out, like):
+    import torch
+    return torch.empty_like(like, memory_format=torch.contiguous_format) if out is None else out
+
+
+def group_norm_workspace_size(x, n_groups):
+    return lib().stx_group_norm_workspace_size(ctypes.byref(as_tensor(x)), int(n_groups))
+
+
+def group_norm(x, n_groups, eps=1e-5, weight=None, bias=None, gelu=False, out=None, workspace=None, stream=None):
+    """ggml_group_norm(x, n_groups, eps) [* weight + bias] [-> gelu]; weight/bias repeat into x."""
+    out = _out(out, x)
+    need = group_norm_workspace_size(x, n_groups)
+    if workspace is None:
+        workspace = globals()["workspace"](need, x.device)
+    check(lib().stx_group_norm(_t(x), _t(out), int(n_groups), float(eps), _t(weight), _t(bias), int(bool(gelu)),
+                               _ptr(workspace), workspace.numel() * workspace.element_size(), _stream(stream)))
+    return out
+
+
+def norm(x, eps=1e-5, weight=None, bias=None, out=None, stream=None):
+    """ggml_norm over the last torch dim (ne0) [* weight + bias]."""
+    out = _out(out, x)
+    if weight is None and bias is None:
+        check(lib().stx_norm(_t(x), _t(out), float(eps), _stream(stream)))
+    else:
+        check(lib().stx_norm_affine(_t(x), _ptr(weight), _ptr(bias), _t(out), float(eps), _stream(stream)))
+    return out
+
+
+def rms_norm(x, eps=1e-24, gamma=None, out=None, stream=None):
+    """ggml_rms_norm over the last torch dim (ne0) [* gamma]."""
+    out = _out(out, x)
+    if gamma is None:
+        check(lib().stx_rms_norm(_t(x), _t(out), float(eps), _stream(stream)))
+    else:
+        check(lib().stx_rms_norm_mul(_t(x), _ptr(gamma), _t(out), float(eps), _stream(stream)))
+    return out
+
+
+def soft_max_ext(x, scale=1.0, mask=None, max_bias=0.0, out=None, stream=None):
+    out = _out(out, x)
+    check(lib().stx_soft_max_ext(_t(x), _t(mask), _t(out), float(scale), float(max_bias), _stream(stream)))
+    return out
+
+
+def gelu_erf(x, bias=None, out=None, stream=None):
+    """ggml_gelu_erf(x), or ggml_gelu_erf(ggml_add(x, bias)) fused."""
+    out = _out(out, x)
+    if bias is None:
+        check(lib().stx_gelu_erf(_t(x), _t(out), _stream(stream)))
+    else:
+        check(lib().stx_add_gelu_erf(_t(x), _t(bias), _t(out), _stream(stream)))
+    return out
+
+
+def glu(x, dim, out=None, stream=None):
+    """GLU along ggml dimension dim (0 = torch's last dim)."""
+    import torch
+    if out is None:
+        shape = list(x.shape)
+        shape[x.dim() - 1 - dim] //= 2
+        out = torch.empty(shape, dtype=x.dtype, device=x.device)
+    check(lib().stx_glu(_t(x), _t(out), int(dim), _stream(stream)))
+    return out
+
+
+def add(a, b, out=None, stream=None):
+    out = _out(out, a)
+    check(lib().stx_add(_t(a), _t(b), _t(out), _stream(stream)))
+    return out
+
+
+def mul(a, b, out=None, stream=None):
+    out = _out(out, a)
+    check(lib().stx_mul(_t(a), _t(b), _t(out), _stream(stream)))
+    return out
+
+
+def mul_add(x, h, s, out=None, stream=None):
+    """x + h * s (LayerScale + residual), rounded like ggml_add(x, ggml_mul(h, s))."""
+    out = _out(out, x)
+    check(lib().stx_mul_add(_t(x), _t(h), _t(s), _t(out), _stream(stream)))
+    return out
+
+
+def rope_ext(x, pos, n_dims, mode=0, freq_base=10000.0, freq_scale=1.0, ext_factor=0.0, attn_factor=1.0,
+             n_ctx_orig=0, beta_fast=0.0, beta_slow=0.0, out=None, stream=None):
+    """ggml_rope_ext; pos is an int32 device tensor with one entry per ne2 index."""
+    import torch
+    _require(pos, torch.int32, "pos")
+    out = _out(out, x)
+    check(lib().stx_rope_ext(_t(x), _ptr(pos), _t(out), int(n_dims), int(mode), int(n_ctx_orig), float(freq_base),
+                             float(freq_scale), float(ext_factor), float(attn_factor), float(beta_fast),
+                             float(beta_slow), _stream(stream)))
     return out

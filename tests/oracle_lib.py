@@ -224,3 +224,116 @@ def demix():
     if _demix is None:
         _demix = _Demix()
     return _demix
+
+
+def _ne(shape):
+    """ggml extents of a numpy shape (torch/numpy's last dim is ne[0])."""
+    s = list(shape)[::-1] + [1] * (4 - len(shape))
+    return (ctypes.c_int64 * 4)(*s)
+
+
+class _Ops:
+    """The ggml op oracle functions (oracle/ops_oracle.c) with numpy in/out. Shapes are numpy
+    shapes (last axis = ne0); broadcast operands have numpy shapes of the same rank."""
+
+    def __init__(self):
+        L = ctypes.CDLL(ORACLE_PATH)
+        i64p = ctypes.POINTER(ctypes.c_int64)
+        L.orc_group_norm.restype = _i
+        L.orc_group_norm.argtypes = [_vp, i64p, _i, ctypes.c_float, _vp, i64p, _vp, i64p, _i, _vp]
+        L.orc_norm.restype = _i
+        L.orc_norm.argtypes = [_vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_float, _i, _vp, _vp, _vp]
+        L.orc_soft_max.restype = _i
+        L.orc_soft_max.argtypes = [_vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_float, _vp]
+        L.orc_gelu_erf.restype = None
+        L.orc_gelu_erf.argtypes = [_vp, ctypes.c_int64, _vp]
+        L.orc_glu.restype = _i
+        L.orc_glu.argtypes = [_vp, i64p, _i, _vp]
+        L.orc_binary.restype = _i
+        L.orc_binary.argtypes = [_i, _vp, i64p, _vp, i64p, _vp, i64p, _vp]
+        L.orc_rope.restype = _i
+        L.orc_rope.argtypes = [_vp, i64p, _vp, _i, _i, ctypes.c_float, ctypes.c_float, ctypes.c_float, _vp]
+        self.L = L
+
+    @staticmethod
+    def _f(a):
+        return np.ascontiguousarray(a, dtype=np.float32)
+
+    def group_norm(self, x, n_groups, eps=1e-5, w=None, b=None, gelu=False):
+        x = self._f(x)
+        y = np.empty_like(x)
+        wa = None if w is None else self._f(w)
+        ba = None if b is None else self._f(b)
+        rc = self.L.orc_group_norm(_np(x), _ne(x.shape), n_groups, eps, None if wa is None else _np(wa),
+                                   _ne(wa.shape if wa is not None else x.shape), None if ba is None else _np(ba),
+                                   _ne(ba.shape if ba is not None else x.shape), int(gelu), _np(y))
+        if rc:
+            raise ValueError(f"group_norm rc={rc}")
+        return y
+
+    def norm(self, x, eps, rms=False, w=None, b=None):
+        x = self._f(x)
+        y = np.empty_like(x)
+        wa = None if w is None else self._f(w)
+        ba = None if b is None else self._f(b)
+        n0 = x.shape[-1]
+        rc = self.L.orc_norm(_np(x), n0, x.size // max(n0, 1), eps, int(rms), None if wa is None else _np(wa),
+                             None if ba is None else _np(ba), _np(y))
+        if rc:
+            raise ValueError(f"norm rc={rc}")
+        return y
+
+    def soft_max(self, x, scale):
+        x = self._f(x)
+        y = np.empty_like(x)
+        n0 = x.shape[-1]
+        if self.L.orc_soft_max(_np(x), n0, x.size // n0, scale, _np(y)):
+            raise ValueError("soft_max")
+        return y
+
+    def gelu(self, x):
+        x = self._f(x)
+        y = np.empty_like(x)
+        self.L.orc_gelu_erf(_np(x), x.size, _np(y))
+        return y
+
+    def glu(self, x, dim):
+        """dim is the ggml dimension (0 = last numpy axis)."""
+        x = self._f(x)
+        shape = list(x.shape) + []
+        ax = x.ndim - 1 - dim
+        shape[ax] //= 2
+        y = np.empty(shape, np.float32)
+        if self.L.orc_glu(_np(x), _ne(x.shape), dim, _np(y)):
+            raise ValueError("glu")
+        return y
+
+    def binary(self, op, a, b, c=None):
+        """op: 'add', 'mul', 'mul_add' (a + b * c) or 'add_gelu' (gelu(a + b))."""
+        code = {"add": 0, "mul": 1, "mul_add": 2, "add_gelu": 3}[op]
+        a, b = self._f(a), self._f(b)
+        c = self._f(c) if c is not None else b
+        y = np.empty_like(a)
+        pad = lambda s: (1,) * (a.ndim - len(s)) + tuple(s)
+        if self.L.orc_binary(code, _np(a), _ne(a.shape), _np(b), _ne(pad(b.shape)), _np(c), _ne(pad(c.shape)),
+                             _np(y)):
+            raise ValueError("binary")
+        return y
+
+    def rope(self, x, pos, n_dims, mode=0, freq_base=10000.0, freq_scale=1.0, attn_factor=1.0):
+        x = self._f(x)
+        pos = np.ascontiguousarray(pos, dtype=np.int32)
+        y = np.empty_like(x)
+        if self.L.orc_rope(_np(x), _ne(x.shape), _np(pos), n_dims, mode, freq_base, freq_scale, attn_factor, _np(y)):
+            raise ValueError("rope")
+        return y
+
+
+_ops = None
+
+
+def ops():
+    global _ops
+    if _ops is None:
+        _ops = _Ops()
+    return _ops
