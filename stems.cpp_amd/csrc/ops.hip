@@ -49,8 +49,14 @@ T4 view(const stx_tensor* t) {
 long long nrows(const T4& t) { return t.ne[1] * t.ne[2] * t.ne[3]; }
 long long nelem(const T4& t) { return t.ne[0] * nrows(t); }
 
+// Dense row-major layout; the stride of a dimension of extent 1 is never used and may be anything.
 bool contiguous(const T4& t) {
-    return t.nb[0] == 4 && t.nb[1] == 4 * t.ne[0] && t.nb[2] == t.nb[1] * t.ne[1] && t.nb[3] == t.nb[2] * t.ne[2];
+    long long expect = 4;
+    for (int i = 0; i < 4; i++) {
+        if (t.ne[i] > 1 && t.nb[i] != expect) return false;
+        expect *= t.ne[i];
+    }
+    return true;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -114,24 +120,19 @@ __device__ __forceinline__ double block_sum(double v, double* red) {
     return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-// gelu(x) = x/2 * erfc(-x/sqrt2), evaluated to a few ulp everywhere.
-//
-// gelu_erf_hl takes its argument as a float head x plus a small tail dx (x + dx is the value),
-// so that a fused producer can hand over a double result without rounding it first: in the
-// negative tail d ln gelu / d ln x ~ 1 + x^2, so one ulp of input rounding would become ~x^2
-// ulps of output error.
-//
-// x >= -1: erfcf of u = -x/sqrt2, with the rounding error du of u (from the product and from
-//   1/sqrt2 itself) corrected to first order, erfc(u + du) = erfc(u) - 2/sqrt(pi) exp(-u^2) du.
-// x < -1: erfc(u) = exp(-u^2) erfcx(u) with u^2 = x^2/2 split exactly into head and tail by an
-//   fma, so exp(-u^2) costs one ulp instead of the 2u^2 ulps an unsplit exponent costs, and
-//   erfcx from Shepherd & Laframboise's substitution (Chebyshev approximation of
-//   (1 + 2u) exp(u^2) erfc(u), J. Comput. Phys. 1981): (1 + 2u) erfcx(u) = P(t),
-//   t = (u - 2.5) / (u + 2.5), with P of degree 10 fitted here by weighted least squares in
-//   double to relative error 1.3e-9 on u >= 0.7.
+// 1/d from the hardware reciprocal refined by one Newton-Raphson step (d normal, finite).
+__device__ __forceinline__ float rcp_nr(float d) {
+    const float r = __builtin_amdgcn_rcpf(d);
+    return fmaf(r, fmaf(-d, r, 1.0f), r);
+}
+
+// erfcx(u) = exp(u^2) erfc(u) for u >= 0.7, by Shepherd & Laframboise's substitution
+// (Chebyshev approximation of (1 + 2u) exp(u^2) erfc(u), J. Comput. Phys. 1981):
+// (1 + 2u) erfcx(u) = P(t), t = (u - 2.5) / (u + 2.5). P has degree 10, fitted for this
+// library by weighted least squares in double to relative error 1.3e-9 on u >= 0.7.
 __device__ __forceinline__ float erfcx_scaled(float u) {
     constexpr float K = 2.5f;
-    const float t = (u - K) / (u + K);
+    const float t = (u - K) * rcp_nr(u + K);
     float p = -1.919762726e-04f;
     p = fmaf(p, t, 5.875547067e-04f);
     p = fmaf(p, t, 5.759609630e-04f);
@@ -143,26 +144,43 @@ __device__ __forceinline__ float erfcx_scaled(float u) {
     p = fmaf(p, t, -9.902466089e-02f);
     p = fmaf(p, t, -1.223567501e-01f);
     p = fmaf(p, t, 1.264838219e+00f);
-    return p / fmaf(2.f, u, 1.f);
+    return p * rcp_nr(fmaf(2.f, u, 1.f));
 }
 
+// gelu(x) = x Phi(x), Phi(x) = (1 + erf(x/sqrt2)) / 2, to a few ulp everywhere (no library
+// erf/erfc: the ROCm erfcf loses ~2u^2 ulps in its tail because it does not split u^2).
+//   |x| < 1:  erf(x/sqrt2) = x Q(x^2), Q of degree 5 fitted for this library (relative error
+//             of Phi 1.6e-9 on |x| <= 1).
+//   |x| >= 1: Phi(-|x|) = exp(-x^2/2) erfcx(|x|/sqrt2) / 2 with x^2 split exactly into head and
+//             tail by an fma, so the exponential costs one ulp instead of ~x^2 ulps; Phi(x) is
+//             that or 1 minus it.
+//   x > 10:   Phi(x) = 1 to float precision; x < -15: gelu underflows (0 * x keeps -0, NaN).
+// gelu_erf_hl takes its argument as a float head x plus a small tail dx (x + dx is the value)
+// so that a fused producer can hand over a double result without rounding it first: in the
+// negative tail d ln gelu / d ln x ~ 1 + x^2, so one ulp of input rounding would become ~x^2
+// ulps of output error.
 __device__ __forceinline__ float gelu_erf_hl(float x, float dx) {
-    constexpr float R = 0.70710678118654752440f;         // fl(1/sqrt2)
-    constexpr float R_LO = 1.2101617e-08f;               // 1/sqrt2 - fl(1/sqrt2)
-    const float u = -x * R;
-    if (x < -1.f) {
-        const float h = x * x;
-        const float l = h < 1e37f ? fmaf(x, x, -h) : 0.f;                   // x^2 = h + l exactly
-        float e = expf(-0.5f * h);
-        e = fmaf(e, -fmaf(x, dx, 0.5f * l), e);          // * exp(-l/2 - x dx), first order
-        const float q = 0.5f * e * erfcx_scaled(u);
-        return fmaf(q, dx, q * x);
+    const float a = fabsf(x);
+    if (a < 1.f) {
+        const float s = x * x;
+        float q = -1.532521674e-05f;
+        q = fmaf(q, s, 2.270149562e-04f);
+        q = fmaf(q, s, -2.372696996e-03f);
+        q = fmaf(q, s, 1.994666085e-02f);
+        q = fmaf(q, s, -1.329807192e-01f);
+        q = fmaf(q, s, 7.978845835e-01f);
+        const float ph = 0.5f * fmaf(x, q, 1.f);
+        return fmaf(ph, dx, x * ph);
     }
-    // (Past |x| = 1e30 the correction is meaningless and would turn infinities into NaN.)
-    const float du = fabsf(x) < 1e30f ? fmaf(-x, R, -u) - x * R_LO - dx * R : 0.f;
-    float e = erfcf(u);
-    e = fmaf(-1.1283791670955126f * expf(-u * u), du, e);
-    return fmaf(0.5f * dx, e, 0.5f * x * e);
+    if (x > 10.f) return x + dx;
+    if (!(x > -15.f)) return x * 0.f;
+    const float h = x * x;
+    const float l = fmaf(x, x, -h);                      // x^2 = h + l exactly
+    float e = expf(-0.5f * h);
+    e = fmaf(e, -fmaf(x, dx, 0.5f * l), e);              // * exp(-l/2 - x dx), first order
+    const float g = 0.5f * e * erfcx_scaled(a * 0.70710678118654752440f);   // Phi(-|x|)
+    const float ph = x < 0.f ? g : 1.f - g;
+    return fmaf(ph, dx, x * ph);
 }
 
 __device__ __forceinline__ float gelu_erf(float x) { return gelu_erf_hl(x, 0.f); }
@@ -308,26 +326,28 @@ enum EwOp { EW_GELU = 0, EW_GLU = 1, EW_ADD = 2, EW_MUL = 3, EW_MUL_ADD = 4, EW_
 // GLU: x * sigmoid(y) with x and y two halves of one source. MUL_ADD: x + fl(y * z), rounded
 // after each operation like ggml_add(x, ggml_mul(h, s)). ADD_GELU: gelu(fl(x + y)), a bias
 // add followed by GELU.
-__device__ __forceinline__ float ew_apply(int op, float x, float y, float z) {
+template <int OP>
+__device__ __forceinline__ float ew_apply(float x, float y, float z) {
 #pragma clang fp contract(off)
-    switch (op) {
-        case EW_GELU: return gelu_erf(x);
-        case EW_GLU: return x / (1.0f + expf(-y));
-        case EW_ADD: return x + y;
-        case EW_MUL: return x * y;
-        case EW_MUL_ADD: {
-            const float p = y * z;
-            return x + p;
-        }
-        default: return gelu_erf(x + y);
+    if constexpr (OP == EW_GELU) return gelu_erf(x);
+    if constexpr (OP == EW_GLU) return x / (1.0f + expf(-y));
+    if constexpr (OP == EW_ADD) return x + y;
+    if constexpr (OP == EW_MUL) return x * y;
+    if constexpr (OP == EW_MUL_ADD) {
+        const float p = y * z;
+        return x + p;
     }
+    if constexpr (OP == EW_ADD_GELU) return gelu_erf(x + y);
+    return 0.f;
 }
+
+template <int OP> constexpr bool has_b() { return OP != EW_GELU; }
+template <int OP> constexpr bool has_c() { return OP == EW_MUL_ADD; }
 
 // General path. a: same shape as dst (any row strides). b, c repeat into dst. Work unit =
 // (row, 1024-element chunk of the row).
 struct EwArgs {
     T4 a, b, c, dst;
-    int op;
 };
 
 __device__ __forceinline__ const float* bcast_row(const T4& t, long long i1, long long i2, long long i3) {
@@ -339,66 +359,109 @@ __device__ __forceinline__ float bcast_at(const float* row, long long ne0, long 
     return ne0 == n0 ? row[i] : ne0 == 1 ? row[0] : row[i % ne0];
 }
 
+template <int OP>
 __global__ __launch_bounds__(256) void ew_rows_kernel(EwArgs a) {
     const long long rows = a.dst.ne[1] * a.dst.ne[2] * a.dst.ne[3];
     const long long n0 = a.dst.ne[0];
     const long long cpr = (n0 + 1023) / 1024;
-    const bool has_b = a.op != EW_GELU, has_c = a.op == EW_MUL_ADD;
     for (long long u = blockIdx.x; u < rows * cpr; u += gridDim.x) {
         const long long r = u / cpr;
         const long long base = (u - r * cpr) * 1024;
         const long long i1 = r % a.dst.ne[1], q = r / a.dst.ne[1];
         const long long i2 = q % a.dst.ne[2], i3 = q / a.dst.ne[2];
         const float* xa = reinterpret_cast<const float*>(a.a.data + i1 * a.a.nb[1] + i2 * a.a.nb[2] + i3 * a.a.nb[3]);
-        const float* xb = has_b ? bcast_row(a.b, i1, i2, i3) : nullptr;
-        const float* xc = has_c ? bcast_row(a.c, i1, i2, i3) : nullptr;
+        const float* xb = has_b<OP>() ? bcast_row(a.b, i1, i2, i3) : nullptr;
+        const float* xc = has_c<OP>() ? bcast_row(a.c, i1, i2, i3) : nullptr;
         float* y = reinterpret_cast<float*>(a.dst.data + i1 * a.dst.nb[1] + i2 * a.dst.nb[2] + i3 * a.dst.nb[3]);
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             const long long i = base + k * 256 + threadIdx.x;
             if (i < n0) {
-                const float vb = has_b ? bcast_at(xb, a.b.ne[0], n0, i) : 0.f;
-                const float vc = has_c ? bcast_at(xc, a.c.ne[0], n0, i) : 0.f;
-                y[i] = ew_apply(a.op, xa[i], vb, vc);
+                const float vb = has_b<OP>() ? bcast_at(xb, a.b.ne[0], n0, i) : 0.f;
+                const float vc = has_c<OP>() ? bcast_at(xc, a.c.ne[0], n0, i) : 0.f;
+                y[i] = ew_apply<OP>(xa[i], vb, vc);
             }
         }
     }
 }
 
-// Contiguous, same-shape, 16-byte aligned operands: flat float4 path.
-__global__ __launch_bounds__(256) void ew_flat_kernel(int op, const float* __restrict__ xa, const float* __restrict__ xb,
-                                                      const float* __restrict__ xc, float* __restrict__ y, long long n) {
-    const long long n4 = n / 4;
-    const float4* a4 = reinterpret_cast<const float4*>(xa);
-    const float4* b4 = reinterpret_cast<const float4*>(xb);
-    const float4* c4 = reinterpret_cast<const float4*>(xc);
-    float4* y4 = reinterpret_cast<float4*>(y);
-    const long long stride = (long long)gridDim.x * 256;
-    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) {
-        const float4 p = a4[i];
-        const float4 q = xb ? b4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-        const float4 s = xc ? c4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-        y4[i] = make_float4(ew_apply(op, p.x, q.x, s.x), ew_apply(op, p.y, q.y, s.y), ew_apply(op, p.z, q.z, s.z),
-                            ew_apply(op, p.w, q.w, s.w));
+// Flat path: a and dst contiguous and 16-byte aligned, fewer than 2^32 elements. An operand
+// either has dst's shape (read as float4) or is a contiguous block that repeats: flat element
+// i of dst reads p[(i / div) % mod], which covers row vectors (bias, gamma: div 1), channel
+// vectors (LayerScale: div = the plane size) and any full-extent block of middle dimensions.
+enum FlatMode { FLAT_NONE = 0, FLAT_SAME = 1, FLAT_ROW4 = 2, FLAT_SPLAT = 3, FLAT_GENERAL = 4 };
+
+struct Flat {
+    const float* p;
+    unsigned div, mod;
+    int mode;        // SAME: float4 at i; ROW4: float4 at i % mod (div 1, mod % 4 == 0);
+                     // SPLAT: one value for all four (div % 4 == 0); GENERAL: per element
+};
+
+__device__ __forceinline__ void flat_load(const Flat& f, unsigned i, float (&v)[4]) {
+    if (f.mode == FLAT_SAME || f.mode == FLAT_ROW4) {
+        const float4 q = *reinterpret_cast<const float4*>(f.p + (f.mode == FLAT_SAME ? i : i % f.mod));
+        v[0] = q.x;
+        v[1] = q.y;
+        v[2] = q.z;
+        v[3] = q.w;
+    } else if (f.mode == FLAT_SPLAT) {
+        v[0] = v[1] = v[2] = v[3] = f.p[(i / f.div) % f.mod];
+    } else if (f.mode == FLAT_GENERAL) {
+        unsigned q = i / f.div;
+        unsigned r = i - q * f.div;
+        q %= f.mod;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            v[j] = f.p[q];
+            if (++r == f.div) {
+                r = 0;
+                if (++q == f.mod) q = 0;
+            }
+        }
+    } else {
+        v[0] = v[1] = v[2] = v[3] = 0.f;
     }
-    for (long long i = n4 * 4 + (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += stride)
-        y[i] = ew_apply(op, xa[i], xb ? xb[i] : 0.f, xc ? xc[i] : 0.f);
+}
+
+__device__ __forceinline__ float flat_at(const Flat& f, unsigned i) {
+    if (f.mode == FLAT_NONE) return 0.f;
+    return f.mode == FLAT_SAME ? f.p[i] : f.p[(i / f.div) % f.mod];
+}
+
+template <int OP>
+__global__ __launch_bounds__(256) void ew_flat_kernel(const float* __restrict__ xa, Flat b, Flat c,
+                                                      float* __restrict__ y, unsigned n) {
+    const unsigned n4 = n / 4;
+    const unsigned stride = gridDim.x * 256;
+    for (unsigned k = blockIdx.x * 256 + threadIdx.x; k < n4; k += stride) {
+        const unsigned i = 4 * k;
+        const float4 p = *reinterpret_cast<const float4*>(xa + i);
+        float vb[4], vc[4];
+        flat_load(b, i, vb);
+        flat_load(c, i, vc);
+        *reinterpret_cast<float4*>(y + i) = make_float4(ew_apply<OP>(p.x, vb[0], vc[0]), ew_apply<OP>(p.y, vb[1], vc[1]),
+                                                        ew_apply<OP>(p.z, vb[2], vc[2]), ew_apply<OP>(p.w, vb[3], vc[3]));
+    }
+    for (unsigned i = 4 * n4 + blockIdx.x * 256 + threadIdx.x; i < n; i += stride)
+        y[i] = ew_apply<OP>(xa[i], flat_at(b, i), flat_at(c, i));
 }
 
 // ----------------------------------------------------------------------- GROUP_NORM
 // Groups: for each i3, channels (ne2) [g*cpg, min((g+1)*cpg, ne2)) with cpg = ceil(ne2 / G),
 // normalised together over ne0 x ne1 x channels (ggml_group_norm). Contiguous tensors only,
-// so a group is one contiguous span of floats.
-//   pass 1 (gn_partial_kernel): one block per 4096-float chunk of a group writes the chunk's
-//     sum and its sum of squared deviations from its own mean (Chan et al.'s pairwise form,
-//     no cancellation);
-//   pass 2 (gn_apply_kernel): every block first combines its group's partials in a fixed
-//     order (so all blocks agree bit for bit and the result is deterministic),
-//     M2 = sum_k [M2_k + n_k (mean_k - mean)^2], then writes
-//     ((x - mean) / sqrt(M2/N + eps)) [* w + b] [-> gelu] for 16384 floats, in double up to
-//     the GELU, which takes the double as a float head and tail.
-constexpr int kGnChunk = 4096;          // floats per partial (16 per thread)
-constexpr int kGnApply = 4;             // chunks per apply block
+// so a group is one contiguous span of floats (fewer than 2^32 of them).
+//   pass 1 (gn_partial_kernel): one block per chunk of kGnChunk floats of a group writes the
+//     chunk's sums of d and d^2 in double, d = x - K with K the group's first element: the
+//     shift removes a common offset, so S2 - S1^2/N below loses only ~1e-16 ((mean - K)/sigma)^2
+//     relative;
+//   pass 2 (gn_apply_kernel): every block issues its chunk's loads (and its affine
+//     parameters) first, then adds up all of its group's partials in a fixed order (every
+//     block gets the same statistics bit for bit, deterministically) and writes
+//     ((x - mean) / sqrt(M2/N + eps)) [* w + b] [-> gelu], in double up to the GELU, which
+//     takes the double as a float head and tail.
+constexpr int kGnVec = 4;                         // float4 loads per thread per chunk
+constexpr int kGnChunk = 256 * 4 * kGnVec;        // floats per partial and per apply block
 
 enum AffineKind { AFF_NONE = 0, AFF_CHANNEL = 1, AFF_NE0 = 2, AFF_GENERAL = 3 };
 
@@ -406,7 +469,7 @@ struct Affine {
     const float* p;
     long long ne[4];                     // broadcast extents (elements)
     long long nb[4];                     // strides in floats
-    int kind;
+    int kind;                            // CHANNEL: p[c]; NE0: p[i0]; GENERAL: broadcast
 };
 
 struct GroupNormArgs {
@@ -414,8 +477,9 @@ struct GroupNormArgs {
     float* y;
     Affine w, b;
     double* part;            // [groups_total][chunks][2]
-    long long ne0, ne1, ne2; // dims of x (ne3 folded into the group index)
-    long long plane;         // ne0 * ne1
+    unsigned ne0, ne1;       // dims of x (ne3 is folded into the group index)
+    long long ne2;
+    unsigned plane;          // ne0 * ne1
     long long cpg;           // channels per group
     int groups;              // groups per ne3 slice
     int chunks;              // partials per group (max over groups)
@@ -424,23 +488,23 @@ struct GroupNormArgs {
     int vec;                 // all group spans 16-byte aligned
 };
 
-__device__ __forceinline__ void group_span(const GroupNormArgs& a, int gt, long long& begin, long long& count,
+__device__ __forceinline__ void group_span(const GroupNormArgs& a, int gt, long long& begin, unsigned& count,
                                            long long& c0, long long& i3) {
     i3 = gt / a.groups;
     const long long g = gt % a.groups;
     c0 = g * a.cpg;
     const long long c1 = min(c0 + a.cpg, a.ne2);
-    begin = i3 * a.ne2 * a.plane + c0 * a.plane;
-    count = (c1 - c0) * a.plane;
+    begin = (i3 * a.ne2 + c0) * (long long)a.plane;
+    count = (unsigned)((c1 - c0) * a.plane);
 }
 
-// Loads the 16 values of this thread in chunk [lo, hi) of base: float4 k covers positions
+// Loads this thread's values of chunk [lo, hi) of base: float4 k covers positions
 // lo + (k * 256 + tid) * 4 .. +3.
-__device__ __forceinline__ void gn_load(const GroupNormArgs& a, const float* base, long long lo, long long hi,
-                                        float (&v)[16], bool (&ok)[16]) {
+__device__ __forceinline__ void gn_load(const GroupNormArgs& a, const float* base, unsigned lo, unsigned hi,
+                                        float (&v)[4 * kGnVec], bool (&ok)[4 * kGnVec]) {
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const long long p = lo + ((long long)k * 256 + threadIdx.x) * 4;
+    for (int k = 0; k < kGnVec; k++) {
+        const unsigned p = lo + (k * 256 + threadIdx.x) * 4;
         if (a.vec && p + 3 < hi) {
             const float4 q = *reinterpret_cast<const float4*>(base + p);
             v[4 * k] = q.x;
@@ -459,111 +523,134 @@ __device__ __forceinline__ void gn_load(const GroupNormArgs& a, const float* bas
     }
 }
 
-__global__ __launch_bounds__(256) void gn_partial_kernel(GroupNormArgs a) {
-    __shared__ double red[4];
-    const int gt = (int)blockIdx.y;
-    long long begin, count, c0, i3;
-    group_span(a, gt, begin, count, c0, i3);
-    const long long lo = (long long)blockIdx.x * kGnChunk;
-    if (lo >= count) return;                                   // uniform over the block
-    const long long hi = min(lo + kGnChunk, count);
-    float v[16];
-    bool ok[16];
-    gn_load(a, a.x + begin, lo, hi, v, ok);
-    double s = 0.0;
-#pragma unroll
-    for (int k = 0; k < 16; k++) s += (double)v[k];
-    s = block_sum(s, red);
-    const double mu = s / (double)(hi - lo);
-    double m2 = 0.0;
-#pragma unroll
-    for (int k = 0; k < 16; k++) {
-        const double d = (double)v[k] - mu;
-        m2 += ok[k] ? d * d : 0.0;
+// Sums of two doubles over a 256-thread block in a fixed order. red holds 8 doubles.
+__device__ __forceinline__ void block_sum2(double& a, double& b, double* red) {
+    a = group_sum<kWave>(a);
+    b = group_sum<kWave>(b);
+    __syncthreads();
+    if (threadIdx.x % kWave == 0) {
+        red[threadIdx.x / kWave] = a;
+        red[4 + threadIdx.x / kWave] = b;
     }
-    m2 = block_sum(m2, red);
+    __syncthreads();
+    a = (red[0] + red[1]) + (red[2] + red[3]);
+    b = (red[4] + red[5]) + (red[6] + red[7]);
+}
+
+__global__ __launch_bounds__(256) void gn_partial_kernel(GroupNormArgs a) {
+    __shared__ double red[8];
+    const int gt = (int)blockIdx.y;
+    long long begin, c0, i3;
+    unsigned count;
+    group_span(a, gt, begin, count, c0, i3);
+    const unsigned lo = blockIdx.x * (unsigned)kGnChunk;
+    if (lo >= count) return;                                   // uniform over the block
+    const unsigned hi = min(lo + (unsigned)kGnChunk, count);
+    const float* xg = a.x + begin;
+    float v[4 * kGnVec];
+    bool ok[4 * kGnVec];
+    gn_load(a, xg, lo, hi, v, ok);
+    const double shift = (double)xg[0];
+    double s1 = 0.0, s2 = 0.0;
+#pragma unroll
+    for (int k = 0; k < 4 * kGnVec; k++) {
+        const double d = ok[k] ? (double)v[k] - shift : 0.0;
+        s1 += d;
+        s2 += d * d;
+    }
+    block_sum2(s1, s2, red);
     if (threadIdx.x == 0) {
         double* p = a.part + ((size_t)gt * a.chunks + blockIdx.x) * 2;
-        p[0] = s;
-        p[1] = m2;
+        p[0] = s1;
+        p[1] = s2;
     }
 }
 
-__device__ __forceinline__ float affine_at(const Affine& f, long long c, long long i0, long long i1, long long i3) {
-    switch (f.kind) {
-        case AFF_CHANNEL: return f.p[c];
-        case AFF_NE0: return f.p[i0];
-        default:
-            return f.p[(i0 % f.ne[0]) * f.nb[0] + (i1 % f.ne[1]) * f.nb[1] + (c % f.ne[2]) * f.nb[2] +
-                       (i3 % f.ne[3]) * f.nb[3]];
-    }
+// One affine operand at element (channel c, i0, i1, i3) under the kernel's affine mode AK:
+// CHANNEL reads p[c], NE0 reads p[i0], GENERAL broadcasts over all four dimensions.
+template <int AK>
+__device__ __forceinline__ float affine_at(const Affine& f, long long c, unsigned i0, unsigned i1, long long i3) {
+    if constexpr (AK == AFF_CHANNEL) return f.p[c];
+    if constexpr (AK == AFF_NE0) return f.p[i0];
+    return f.p[(i0 % f.ne[0]) * f.nb[0] + (i1 % f.ne[1]) * f.nb[1] + (c % f.ne[2]) * f.nb[2] + (i3 % f.ne[3]) * f.nb[3]];
 }
 
+template <int AK, bool GELU>
 __global__ __launch_bounds__(256) void gn_apply_kernel(GroupNormArgs a) {
-    __shared__ double red[4];
+    __shared__ double red[8];
     const int gt = (int)blockIdx.y;
-    long long begin, count, c0, i3;
+    long long begin, c0, i3;
+    unsigned count;
     group_span(a, gt, begin, count, c0, i3);
-    const long long lo0 = (long long)blockIdx.x * kGnChunk * kGnApply;
-    if (lo0 >= count) return;                                  // uniform over the block
-    const int nch = (int)((count + kGnChunk - 1) / kGnChunk);
-    const double* part = a.part + (size_t)gt * a.chunks * 2;
-    double s = 0.0;
-    for (int k = threadIdx.x; k < nch; k += 256) s += part[2 * k];
-    const double N = (double)count;
-    const double mean = block_sum(s, red) / N;
-    double m2 = 0.0;
-    for (int k = threadIdx.x; k < nch; k += 256) {
-        const double nk = (double)(min((long long)(k + 1) * kGnChunk, count) - (long long)k * kGnChunk);
-        const double d = part[2 * k] / nk - mean;
-        m2 += part[2 * k + 1] + nk * d * d;
-    }
-    m2 = block_sum(m2, red);
-    const double rstd = 1.0 / sqrt(m2 / N + (double)a.eps);
+    const unsigned lo = blockIdx.x * (unsigned)kGnChunk;
+    if (lo >= count) return;                                   // uniform over the block
+    const unsigned hi = min(lo + (unsigned)kGnChunk, count);
     const float* xg = a.x + begin;
     float* yg = a.y + begin;
-    for (int cc = 0; cc < kGnApply; cc++) {
-        const long long lo = lo0 + (long long)cc * kGnChunk;
-        if (lo >= count) break;
-        const long long hi = min(lo + kGnChunk, count);
-        float v[16];
-        bool ok[16];
-        gn_load(a, xg, lo, hi, v, ok);
+    float v[4 * kGnVec];
+    bool ok[4 * kGnVec];
+    gn_load(a, xg, lo, hi, v, ok);                             // in flight while the stats merge
+    // Affine parameters of every element, also loaded before the merge: channel c and (i0, i1)
+    // inside its plane of element p, advanced element by element.
+    float wv[4 * kGnVec], bv[4 * kGnVec];
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const long long p = lo + ((long long)k * 256 + threadIdx.x) * 4;
-            if (p >= hi) continue;
-            // Channel c and (i0, i1) inside its plane of element p, advanced element by element.
-            long long c = 0, i0 = 0, i1 = 0;
-            if (a.w.kind || a.b.kind) {
-                c = c0 + p / a.plane;
-                const long long q = p % a.plane;
-                i1 = q / a.ne0;
-                i0 = q % a.ne0;
-            }
-            float o[4];
+    for (int k = 0; k < kGnVec; k++) {
+        const unsigned p = lo + (k * 256 + threadIdx.x) * 4;
+        long long c = 0;
+        unsigned i0 = 0, i1 = 0;
+        if constexpr (AK == AFF_NE0) {
+            i0 = p % a.ne0;
+        } else {
+            const unsigned cp = p / a.plane, q = p - cp * a.plane;
+            c = c0 + cp;
+            i1 = q / a.ne0;
+            i0 = q - i1 * a.ne0;
+        }
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                double t = ((double)v[4 * k + j] - mean) * rstd;
-                if (a.w.kind) t *= (double)affine_at(a.w, c, i0, i1, i3);
-                if (a.b.kind) t += (double)affine_at(a.b, c, i0, i1, i3);
-                const float f = (float)t;
-                o[j] = a.gelu ? gelu_erf_hl(f, (float)(t - (double)f)) : f;
-                if (++i0 == a.ne0) {
-                    i0 = 0;
+        for (int j = 0; j < 4; j++) {
+            const bool in = ok[4 * k + j];
+            wv[4 * k + j] = a.w.p && in ? affine_at<AK>(a.w, c, i0, i1, i3) : 1.f;
+            bv[4 * k + j] = a.b.p && in ? affine_at<AK>(a.b, c, i0, i1, i3) : 0.f;
+            if (++i0 == a.ne0) {
+                i0 = 0;
+                if constexpr (AK != AFF_NE0) {
                     if (++i1 == a.ne1) {
                         i1 = 0;
                         ++c;
                     }
                 }
             }
-            if (a.vec && p + 3 < hi) {
-                *reinterpret_cast<float4*>(yg + p) = make_float4(o[0], o[1], o[2], o[3]);
-            } else {
+        }
+    }
+    const int nch = (int)((count + kGnChunk - 1) / kGnChunk);
+    const double* part = a.part + (size_t)gt * a.chunks * 2;
+    double s1 = 0.0, s2 = 0.0;
+    for (int k = threadIdx.x; k < nch; k += 256) {
+        s1 += part[2 * k];
+        s2 += part[2 * k + 1];
+    }
+    block_sum2(s1, s2, red);
+    const double N = (double)count, dm = s1 / N;
+    const double mean = (double)xg[0] + dm;
+    const double rstd = 1.0 / sqrt(fmax(s2 / N - dm * dm, 0.0) + (double)a.eps);
+#pragma unroll 1
+    for (int k = 0; k < kGnVec; k++) {
+        const unsigned p = lo + (k * 256 + threadIdx.x) * 4;
+        if (p >= hi) continue;
+        float o[4];
 #pragma unroll
-                for (int j = 0; j < 4; j++)
-                    if (ok[4 * k + j]) yg[p + j] = o[j];
-            }
+        for (int j = 0; j < 4; j++) {
+            const double t = fma(((double)v[4 * k + j] - mean) * rstd, (double)wv[4 * k + j], (double)bv[4 * k + j]);
+            const float f = (float)t;
+            if constexpr (GELU) o[j] = gelu_erf_hl(f, (float)(t - (double)f));
+            else o[j] = f;
+        }
+        if (a.vec && p + 3 < hi) {
+            *reinterpret_cast<float4*>(yg + p) = make_float4(o[0], o[1], o[2], o[3]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (ok[4 * k + j]) yg[p + j] = o[j];
         }
     }
 }
@@ -679,37 +766,78 @@ void row_norm(const stx_tensor* a, const stx_tensor* dst, const float* gamma, co
     }
 }
 
-void elementwise(int op, const stx_tensor* a, const stx_tensor* b, const stx_tensor* c, const stx_tensor* dst,
-                 stx_stream stream) {
-    EwArgs args{};
-    args.op = op;
-    args.a = view(a);
-    args.dst = view(dst);
-    if (b) args.b = view(b);
-    if (c) args.c = view(c);
-    const long long n = nelem(args.dst);
-    if (n == 0) return;
-    const hipStream_t s = as_stream(stream);
-    bool flat = contiguous(args.a) && contiguous(args.dst) && aligned16(args.a.data) && aligned16(args.dst.data);
-    for (const stx_tensor* t : {b, c}) {
-        if (!t) continue;
-        const T4 v = view(t);
-        flat = flat && contiguous(v) && aligned16(v.data);
-        for (int i = 0; i < 4; i++) flat = flat && t->ne[i] == dst->ne[i];
+// How operand t (NULL: none) is read on the flat path over dst; false if it cannot be.
+bool flat_operand(const stx_tensor* t, const stx_tensor* dst, Flat& f) {
+    f = Flat{};
+    if (!t) return true;
+    const T4 v = view(t);
+    if (!contiguous(v)) return false;
+    f.p = reinterpret_cast<const float*>(v.data);
+    bool same = true;
+    for (int i = 0; i < 4; i++) same = same && t->ne[i] == dst->ne[i];
+    if (same) {
+        f.mode = FLAT_SAME;
+        return aligned16(v.data);
     }
+    // Non-unit dimensions of t must be one full-extent run [d0, d1] of dst's dimensions.
+    int d0 = -1, d1 = -1;
+    for (int i = 0; i < 4; i++)
+        if (t->ne[i] > 1) {
+            if (d0 < 0) d0 = i;
+            d1 = i;
+        }
+    unsigned long long div = 1, mod = 1;
+    if (d0 >= 0) {
+        for (int i = d0; i <= d1; i++)
+            if (t->ne[i] != dst->ne[i]) return false;
+        for (int i = 0; i < d0; i++) div *= (unsigned long long)dst->ne[i];
+        for (int i = d0; i <= d1; i++) mod *= (unsigned long long)dst->ne[i];
+    }
+    f.div = (unsigned)div;
+    f.mod = (unsigned)mod;
+    if (div == 1 && mod % 4 == 0 && aligned16(v.data)) f.mode = FLAT_ROW4;
+    else if (div % 4 == 0) f.mode = FLAT_SPLAT;
+    else f.mode = FLAT_GENERAL;
+    return true;
+}
+
+template <int OP>
+void launch_elementwise(const EwArgs& args, const stx_tensor* b, const stx_tensor* c, const stx_tensor* dst,
+                        hipStream_t s) {
+    const long long n = nelem(args.dst);
+    Flat fb, fc;
+    const bool flat = n < (1LL << 32) - 1024 && contiguous(args.a) && contiguous(args.dst) && aligned16(args.a.data) &&
+                      aligned16(args.dst.data) && flat_operand(b, dst, fb) && flat_operand(c, dst, fc);
     if (flat) {
         const unsigned blocks = (unsigned)std::min<long long>((n / 4 + 255) / 256 + 1, 1 << 16);
-        hipLaunchKernelGGL(ew_flat_kernel, dim3(blocks), dim3(256), 0, s, op,
-                           reinterpret_cast<const float*>(args.a.data),
-                           b ? reinterpret_cast<const float*>(args.b.data) : nullptr,
-                           c ? reinterpret_cast<const float*>(args.c.data) : nullptr,
-                           reinterpret_cast<float*>(args.dst.data), n);
+        hipLaunchKernelGGL((ew_flat_kernel<OP>), dim3(blocks), dim3(256), 0, s,
+                           reinterpret_cast<const float*>(args.a.data), fb, fc,
+                           reinterpret_cast<float*>(args.dst.data), (unsigned)n);
         launch_check("ew_flat_kernel");
         return;
     }
     const long long units = nrows(args.dst) * ((args.dst.ne[0] + 1023) / 1024);
-    hipLaunchKernelGGL(ew_rows_kernel, dim3((unsigned)std::min<long long>(units, 1 << 20)), dim3(256), 0, s, args);
+    hipLaunchKernelGGL((ew_rows_kernel<OP>), dim3((unsigned)std::min<long long>(units, 1 << 20)), dim3(256), 0, s, args);
     launch_check("ew_rows_kernel");
+}
+
+void elementwise(int op, const stx_tensor* a, const stx_tensor* b, const stx_tensor* c, const stx_tensor* dst,
+                 stx_stream stream) {
+    EwArgs args{};
+    args.a = view(a);
+    args.dst = view(dst);
+    if (b) args.b = view(b);
+    if (c) args.c = view(c);
+    if (nelem(args.dst) == 0) return;
+    const hipStream_t s = as_stream(stream);
+    switch (op) {
+        case EW_GELU: launch_elementwise<EW_GELU>(args, b, c, dst, s); break;
+        case EW_GLU: launch_elementwise<EW_GLU>(args, b, c, dst, s); break;
+        case EW_ADD: launch_elementwise<EW_ADD>(args, b, c, dst, s); break;
+        case EW_MUL: launch_elementwise<EW_MUL>(args, b, c, dst, s); break;
+        case EW_MUL_ADD: launch_elementwise<EW_MUL_ADD>(args, b, c, dst, s); break;
+        default: launch_elementwise<EW_ADD_GELU>(args, b, c, dst, s); break;
+    }
 }
 
 // Classifies an affine operand (weight or bias) that repeats into x.
@@ -891,7 +1019,8 @@ STX_API stx_status stx_group_norm(const stx_tensor* a, const stx_tensor* dst, in
         if (nelem(ta) == 0) return;
         const GnPlan p = gn_plan(a, n_groups);
         STX_REQUIRE(p.groups_total < 65536, "group_norm: more than 65535 groups");
-        STX_REQUIRE(p.chunks < (1LL << 31), "group_norm: group too large");
+        STX_REQUIRE(p.cpg * a->ne[0] * a->ne[1] < (1LL << 32) - kGnChunk,
+                    "group_norm: groups of 2^32 floats or more are not supported");
         const size_t need = sizeof(double) * 2 * (size_t)(p.chunks * p.groups_total);
         STX_REQUIRE(workspace != nullptr && workspace_bytes >= need, "group_norm: workspace too small (%zu, need %zu)",
                     workspace_bytes, need);
@@ -901,25 +1030,38 @@ STX_API stx_status stx_group_norm(const stx_tensor* a, const stx_tensor* dst, in
         g.w = w;
         g.b = b;
         g.part = static_cast<double*>(workspace);
-        g.ne0 = ta.ne[0];
-        g.ne1 = ta.ne[1];
+        g.ne0 = (unsigned)ta.ne[0];
+        g.ne1 = (unsigned)ta.ne[1];
         g.ne2 = ta.ne[2];
-        g.plane = ta.ne[0] * ta.ne[1];
+        g.plane = (unsigned)(ta.ne[0] * ta.ne[1]);
         g.cpg = p.cpg;
         g.groups = (int)p.groups;
         g.chunks = (int)p.chunks;
         g.eps = eps;
         g.gelu = gelu ? 1 : 0;
         // Every group span starts at (i3 * ne2 + g * cpg) * plane floats.
-        g.vec = aligned16(ta.data) && aligned16(td.data) && (g.cpg * g.plane) % 4 == 0 &&
-                        (ta.ne[3] == 1 || (g.ne2 * g.plane) % 4 == 0)
+        g.vec = aligned16(ta.data) && aligned16(td.data) && (g.cpg * (long long)g.plane) % 4 == 0 &&
+                        (ta.ne[3] == 1 || (g.ne2 * (long long)g.plane) % 4 == 0)
                     ? 1
                     : 0;
         const hipStream_t s = as_stream(stream);
         hipLaunchKernelGGL(gn_partial_kernel, dim3((unsigned)p.chunks, (unsigned)p.groups_total), dim3(256), 0, s, g);
         launch_check("gn_partial_kernel");
-        const unsigned apply_blocks = (unsigned)((p.chunks + kGnApply - 1) / kGnApply);
-        hipLaunchKernelGGL(gn_apply_kernel, dim3(apply_blocks, (unsigned)p.groups_total), dim3(256), 0, s, g);
+        const dim3 agrid((unsigned)p.chunks, (unsigned)p.groups_total);
+        auto fits = [&](int kind) {
+            return (g.w.kind == AFF_NONE || g.w.kind == kind) && (g.b.kind == AFF_NONE || g.b.kind == kind);
+        };
+        const int ak = fits(AFF_CHANNEL) ? AFF_CHANNEL : fits(AFF_NE0) ? AFF_NE0 : AFF_GENERAL;
+        if (ak == AFF_CHANNEL) {
+            if (g.gelu) hipLaunchKernelGGL((gn_apply_kernel<AFF_CHANNEL, true>), agrid, dim3(256), 0, s, g);
+            else hipLaunchKernelGGL((gn_apply_kernel<AFF_CHANNEL, false>), agrid, dim3(256), 0, s, g);
+        } else if (ak == AFF_NE0) {
+            if (g.gelu) hipLaunchKernelGGL((gn_apply_kernel<AFF_NE0, true>), agrid, dim3(256), 0, s, g);
+            else hipLaunchKernelGGL((gn_apply_kernel<AFF_NE0, false>), agrid, dim3(256), 0, s, g);
+        } else {
+            if (g.gelu) hipLaunchKernelGGL((gn_apply_kernel<AFF_GENERAL, true>), agrid, dim3(256), 0, s, g);
+            else hipLaunchKernelGGL((gn_apply_kernel<AFF_GENERAL, false>), agrid, dim3(256), 0, s, g);
+        }
         launch_check("gn_apply_kernel");
     });
 }
