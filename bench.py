@@ -1,21 +1,36 @@
-"""Benchmark of the spectral hot path on one MI355X.
+"""Benchmark of the spectral + elementwise hot path on one MI355X. Prints ONE JSON line.
 
-Headline workload (one "step"): the HTDemucs-spec STFT -> iSTFT round trip on stereo fp32,
-343,980 samples per channel (7.8 s at 44.1 kHz), n_fft 4096, hop 1024, periodic Hann, reflect
-pad, center=True: stx_htdemucs_spec then stx_htdemucs_ispec, the drop-in replacements of
-src/stft.h:79-140, spectrum in the reference's f-major layout. Inputs are resident in HBM
-before timing and rotate over enough copies (> 512 MB) that the 256 MB Infinity Cache cannot
-hold them, so the numbers are cold-cache numbers.
+Headline workload (one "step"): the HTDemucs elementwise/reduction op set on fp32 inputs drawn
+N(0, 1) from a seed, for each (C, T) in (48, 85995), (96, 21499), (192, 5375), (384, 1344):
+  1. GroupNorm(num_groups=1) over [1, C, T], * w[C] + b[C], then GELU (erf), fused:
+     stx_group_norm (src/htdemucs.cpp:114-128,136);
+  2. GLU over 2C channels of a [1, 2C, T] input -> [1, C, T]: stx_glu (src/htdemucs.cpp:105-110);
+  3. LayerScale broadcast MUL plus residual ADD, x + h * scale[C]: stx_mul_add
+     (src/htdemucs.cpp:139).
+The 12 calls of a step are captured once into a HIP graph per buffer set and replayed on one
+stream; buffer sets rotate so that more than 512 MB is touched between reuses, larger than the
+256 MB Infinity Cache: cold-cache numbers.
 
-value = Msamples/s = 2 * 343,980 samples per step / step time.
-roofline: the slower of the two kernels, algorithmic bytes per launch (fp32 signal read or
-written once + complex64 spectrum written or read once = 13,761,888 B) / its average
-duration, timed with HIP events on the stream the kernels run on.
-cpu_baseline: the reference's own stft.h (oracle/_ref, built from the reference sources) or,
-where that is absent, the C oracle restating it, single-threaded as the reference runs it,
-on a bounded number of round trips of the same input.
+value = algorithmic HBM bytes per step / step time, in GB/s (32 bytes per element of [C, T]:
+GroupNorm reads x and writes y, GLU reads 2C rows and writes C, LayerScale reads x and h and
+writes the sum; parameters add 12 C bytes).
+roofline: the op with the largest share of the step (GroupNorm+GELU): its algorithmic bytes
+(8 per element) / its duration (gn_partial_kernel + gn_apply_kernel), from a graph of instances
+of that op on more than 512 MB of distinct buffers (cold, like the step) replayed between two
+HIP events on the stream the kernels run on. traffic: HBM bytes of that op
+per step measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter
+on a plain copy of known size), read from profiles/pmc_traffic.json when present.
+cpu_baseline: the C oracle (a double-precision restatement; ggml's CPU backend is not in the
+reference tree), single-threaded, on whole steps of the same workload for a bounded time.
 
-Prints ONE JSON line.
+The same line carries the spectral half of the metric, STFT+iSTFT Msamples/s:
+  spectral.htdemucs_round_trip: stx_htdemucs_spec + stx_htdemucs_ispec (src/stft.h:76-140) on
+    stereo 343,980 samples, n_fft 4096 (hop 1024), reference f-major layout; its CPU baseline is
+    the reference's own src/stft.h compiled from the reference sources (oracle/_ref) or, where
+    that is absent, the C oracle;
+  spectral.roformer_chunk: stx_torch_stft (n_fft 2048, hop 441) -> stx_band_scatter_apply with
+    60 mel bands and uniform [-1, 1] masks (one stem) -> stx_torch_istft on one stereo chunk of
+    352,800 samples (src/roformer.cpp:217-283).
 """
 import argparse
 import json
@@ -28,166 +43,401 @@ sys.path.insert(0, os.path.join(ROOT, "stems.cpp_amd"))
 
 METRIC = "STFT+iSTFT Msamples/s; norm/softmax/elementwise HBM GB/s (% of 8 TB/s)"
 HBM_PEAK_GBS = 8000.0
-C1_LEN, C1_NFFT = 343980, 4096
+SHAPES = [(48, 85995), (96, 21499), (192, 5375), (384, 1344)]
+EPS = 1e-5
 
 
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
-    p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on each CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-spectral", action="store_true")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="end with one 256 MiB device copy (the reference kernel for PMC byte counters)")
     return p.parse_args()
 
 
-def traffic_for(kernel):
-    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by
-    a copy kernel of known size), if that measurement was committed under profiles/."""
+def traffic_for(name):
+    """HBM bytes per step of op `name` from the committed PMC measurement, or None."""
     path = os.path.join(ROOT, "profiles", "pmc_traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        return json.load(f).get(kernel)
+        entry = json.load(f).get("ops", {}).get(name)
+    return None if entry is None else entry.get("bytes_per_step")
 
 
-def cpu_baseline(x, budget_s):
+def spin(torch, us=3000):
+    """Occupies the stream for about `us` microseconds so that the host can enqueue ahead."""
+    torch.cuda._sleep(int(us * 2400))
+
+
+class OpSet:
+    """Buffers and calls of the headline workload."""
+
+    def __init__(self, torch, stx, dev, copies):
+        g = torch.Generator(device=dev)
+        g.manual_seed(2025)
+        rn = lambda *s: torch.randn(s, generator=g, device=dev, dtype=torch.float32)
+        self.torch = torch
+        self.stx = stx
+        self.params = []
+        for C, T in SHAPES:
+            w, b, s = rn(C, 1, 1), rn(C, 1, 1), rn(C, 1, 1) * 0.1
+            ws = stx.workspace(stx.group_norm_workspace_size(torch.empty((C, 1, T), device=dev), 1), dev)
+            self.params.append((w, b, s, ws))
+        self.sets = []
+        for _ in range(copies):
+            bufs = []
+            for C, T in SHAPES:
+                bufs.append({"x": rn(C, 1, T), "y": torch.empty((C, 1, T), device=dev), "h": rn(2 * C, 1, T),
+                             "g": torch.empty((C, 1, T), device=dev), "r": rn(C, 1, T),
+                             "o": torch.empty((C, 1, T), device=dev)})
+            self.sets.append(bufs)
+
+    def gn(self, k, i, stream=None):
+        w, b, _, ws = self.params[i]
+        B = self.sets[k][i]
+        self.stx.group_norm(B["x"], 1, EPS, w, b, gelu=True, out=B["y"], workspace=ws, stream=stream)
+
+    def glu(self, k, i, stream=None):
+        B = self.sets[k][i]
+        self.stx.glu(B["h"], 2, out=B["g"], stream=stream)
+
+    def scale_residual(self, k, i, stream=None):
+        B = self.sets[k][i]
+        self.stx.mul_add(B["r"], B["g"], self.params[i][2], out=B["o"], stream=stream)
+
+    def instance(self, name, i):
+        """A call of op `name` at shape i on freshly allocated buffers of its own."""
+        torch, stx = self.torch, self.stx
+        C, T = SHAPES[i]
+        w, b, s, ws = self.params[i]
+        dev = w.device
+        if name == "gn":
+            x, y = torch.randn((C, 1, T), device=dev), torch.empty((C, 1, T), device=dev)
+            return lambda st: stx.group_norm(x, 1, EPS, w, b, gelu=True, out=y, workspace=ws, stream=st)
+        if name == "glu":
+            h, g = torch.randn((2 * C, 1, T), device=dev), torch.empty((C, 1, T), device=dev)
+            return lambda st: stx.glu(h, 2, out=g, stream=st)
+        r, g, o = torch.randn((C, 1, T), device=dev), torch.randn((C, 1, T), device=dev), torch.empty((C, 1, T), device=dev)
+        return lambda st: stx.mul_add(r, g, s, out=o, stream=st)
+
+    def step(self, k, stream=None):
+        for i in range(len(SHAPES)):
+            self.gn(k, i, stream)
+            self.glu(k, i, stream)
+            self.scale_residual(k, i, stream)
+
+
+def op_bytes():
+    per = {"gn": [], "glu": [], "scale_residual": []}
+    for C, T in SHAPES:
+        per["gn"].append(8 * C * T + 8 * C)
+        per["glu"].append(12 * C * T)
+        per["scale_residual"].append(12 * C * T + 4 * C)
+    return per
+
+
+def run_ops(args, torch, stx, dev):
+    elems = sum(C * T for C, T in SHAPES)
+    per_set = 28 * elems
+    copies = max(2, int(512e6 // per_set) + 1)
+    ops = OpSet(torch, stx, dev, copies)
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+
+    # One graph per buffer set: the 12 calls (16 kernels) of a step.
+    graphs = []
+    with torch.cuda.stream(stream):
+        for k in range(copies):
+            ops.step(k, stream)                        # eager run before capture
+        torch.cuda.synchronize()
+        for k in range(copies):
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=stream):
+                ops.step(k, stream)
+            graphs.append(gr)
+    torch.cuda.synchronize()
+
+    for i in range(args.warmup):
+        graphs[i % copies].replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    cur = torch.cuda.current_stream()
+    t0.record(cur)
+    for i in range(args.steps):
+        graphs[i % copies].replay()
+    t1.record(cur)
+    torch.cuda.synchronize()
+    ms_per_step = t0.elapsed_time(t1) / args.steps
+
+    # Per-op durations, cold like the step: per (op, shape), one graph of instances on their
+    # own buffers, more than 512 MB of them, replayed between two HIP events on the stream the
+    # kernels run on (no launch gaps between kernels, graph launch cost amortised).
+    REPLAYS = 3
+    names = ["gn", "glu", "scale_residual"]
+    nbytes = op_bytes()
+    us = {}
+    with torch.cuda.stream(stream):
+        for name in names:
+            for i in range(len(SHAPES)):
+                n_inst = int(512e6 // nbytes[name][i]) + 2
+                calls = [ops.instance(name, i) for _ in range(n_inst)]
+                for c in calls:
+                    c(stream)
+                gr = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(gr, stream=stream):
+                    for c in calls:
+                        c(stream)
+                gr.replay()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(REPLAYS):
+                    gr.replay()
+                e1.record(stream)
+                e1.synchronize()
+                us[(name, i)] = e0.elapsed_time(e1) * 1e3 / (REPLAYS * n_inst)
+                del gr, calls
+    torch.cuda.synchronize()
+    ops_us = {f"{n}[C={SHAPES[i][0]},T={SHAPES[i][1]}]": round(us[(n, i)], 3) for n in names for i in range(len(SHAPES))}
+    share = {n: sum(us[(n, i)] for i in range(len(SHAPES))) for n in names}
+    dom = max(share, key=share.get)
+    dom_bytes = sum(nbytes[dom])
+    achieved = dom_bytes / (share[dom] * 1e-6) / 1e9
+    step_bytes = sum(sum(v) for v in nbytes.values())
+    kernel_names = {"gn": "group_norm+gelu (gn_partial_kernel + gn_apply_kernel<channel,gelu>)",
+                    "glu": "glu (ew_flat_kernel<GLU>)", "scale_residual": "layer scale + residual (ew_flat_kernel<MUL_ADD>)"}
+    res = {
+        "value": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
+        "ms_per_step": round(ms_per_step, 6),
+        "config": {
+            "workload": "htdemucs_op_set: GroupNorm(1)+affine+GELU on [1,C,T], GLU 2C->C, LayerScale MUL + residual ADD",
+            "shapes_CT": [list(s) for s in SHAPES],
+            "bytes_per_step": step_bytes,
+            "execution": "one HIP graph per step (16 kernels), one stream",
+            "buffer_sets_rotated": copies,
+            "input": "N(0,1) fp32 from seed 2025",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": kernel_names[dom],
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic_for(dom),
+            "algorithmic_bytes_per_step": dom_bytes,
+            "us_per_step": round(share[dom], 3),
+        },
+        "ops_us": ops_us,
+        "ops_share_us": {k: round(v, 3) for k, v in share.items()},
+    }
+    return res, ops
+
+
+def cpu_ops_baseline(budget_s):
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import numpy as np
+    import oracle_lib
+    import synth
+    o = oracle_lib.ops()
+    data = []
+    for C, T in SHAPES:
+        data.append((synth.normal(C, (C, 1, T), 1.0), synth.normal(C + 1, (C, 1, 1), 1.0),
+                     synth.normal(C + 2, (C, 1, 1), 1.0), synth.normal(C + 3, (2 * C, 1, T), 1.0),
+                     synth.normal(C + 4, (C, 1, T), 1.0), synth.normal(C + 5, (C, 1, 1), 0.1)))
+    steps = 0
+    t0 = time.perf_counter()
+    while True:
+        for x, w, b, h, r, s in data:
+            o.group_norm(x, 1, EPS, w, b, gelu=True)
+            g = o.glu(h, 2)
+            o.binary("mul_add", r, g, s)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    step_bytes = sum(sum(v) for v in op_bytes().values())
+    return {
+        "value": round(steps * step_bytes / el / 1e9, 3),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{steps} whole steps of the same op set ({el:.1f} s, single thread): the C oracle, a "
+                  "double-precision restatement of the ops (ggml's CPU backend is absent from the reference)",
+    }
+
+
+def run_spectral(args, torch, stx, dev):
+    import numpy as np
+    import synth
+    out = {}
+    steps = max(20, args.steps)
+    # HTDemucs spec round trip, reference layout.
+    n_fft, L, C = 4096, 343980, 2
+    fft = stx.FFT(n_fft)
+    T = stx.htdemucs_frames(n_fft, L)
+    F = n_fft // 2
+    x_host = synth.normal(2024, (C, L), 0.1)
+    per = C * L * 4 * 2 + C * F * T * 8
+    copies = max(2, int(512e6 // per) + 1)
+    xs = [torch.from_numpy(x_host).to(dev) for _ in range(copies)]
+    specs = [torch.empty((C, F, T), dtype=torch.complex64, device=dev) for _ in range(copies)]
+    ys = [torch.empty((C, L), device=dev) for _ in range(copies)]
+    stream = torch.cuda.Stream()
+
+    def rt(k):
+        stx.htdemucs_spec(fft, xs[k], out=specs[k], stream=stream)
+        stx.htdemucs_ispec(fft, specs[k], L, out=ys[k], stream=stream)
+    out["htdemucs_round_trip"] = time_graphs(torch, stream, rt, copies, steps, C * L, args.warmup)
+    out["htdemucs_round_trip"]["config"] = {"channels": C, "samples": L, "n_fft": n_fft, "hop": n_fft // 4,
+                                            "frames": T, "layout": "f_major", "buffer_sets_rotated": copies}
+    # Per-kernel durations behind a spin kernel.
+    evs = []
+    with torch.cuda.stream(stream):
+        for r in range(20):
+            spin(torch, 500)
+            k = r % copies
+            e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+            e[0].record(stream)
+            stx.htdemucs_spec(fft, xs[k], out=specs[k], stream=stream)
+            e[1].record(stream)
+            stx.htdemucs_ispec(fft, specs[k], L, out=ys[k], stream=stream)
+            e[2].record(stream)
+            evs.append(e)
+    torch.cuda.synchronize()
+    alg = C * L * 4 + C * F * T * 8
+    for name, a, b in (("stft", 0, 1), ("istft", 1, 2)):
+        t = float(np.median([e[a].elapsed_time(e[b]) * 1e3 for e in evs]))
+        out["htdemucs_round_trip"][f"{name}_us"] = round(t, 3)
+        out["htdemucs_round_trip"][f"{name}_GBps"] = round(alg / (t * 1e-6) / 1e9, 1)
+    del xs, specs, ys
+
+    # RoFormer chunk: STFT -> mask scatter-average + apply -> iSTFT.
+    n_fft, hop, L, C, S = 2048, 441, 352800, 2, 1
+    fft2 = stx.FFT(n_fft)
+    sizes, freqs = stx.mel_band_map(44100, n_fft, 60)
+    bands = stx.Bands(sizes, freqs, n_fft // 2 + 1, C)
+    T = stx.torch_stft_frames(L, hop)
+    F = n_fft // 2 + 1
+    per = C * L * 8 + C * F * T * 16 + S * bands.total_feat * T * 4
+    copies = max(2, int(512e6 // per) + 1)
+    x_host = synth.normal(2026, (C, L), 0.1)
+    xs = [torch.from_numpy(x_host).to(dev) for _ in range(copies)]
+    ms = [torch.from_numpy(synth.uniform(7 + k, (1, S, bands.total_feat * T))).to(dev) for k in range(copies)]
+    specs = [torch.empty((C, T, F), dtype=torch.complex64, device=dev) for _ in range(copies)]
+    masked = [torch.empty((1, S, C, T, F), dtype=torch.complex64, device=dev) for _ in range(copies)]
+    ys = [torch.empty((S * C, hop * (T - 1)), device=dev) for _ in range(copies)]
+
+    def chunk(k):
+        stx.torch_stft(fft2, xs[k], hop, layout=stx.T_MAJOR, out=specs[k], stream=stream)
+        bands.scatter_apply(ms[k], specs[k].view(1, C, T, F), T, layout=stx.T_MAJOR, out=masked[k], stream=stream)
+        stx.torch_istft(fft2, masked[k].view(S * C, T, F), hop, layout=stx.T_MAJOR, out=ys[k], stream=stream)
+    out["roformer_chunk"] = time_graphs(torch, stream, chunk, copies, steps, C * L, args.warmup)
+    out["roformer_chunk"]["config"] = {"channels": C, "samples": L, "n_fft": n_fft, "hop": hop, "frames": T,
+                                       "bins": F, "bands": 60, "stems": S, "layout": "t_major",
+                                       "buffer_sets_rotated": copies}
+    return out
+
+
+def time_graphs(torch, stream, fn, copies, steps, samples, warmup):
+    graphs = []
+    with torch.cuda.stream(stream):
+        for k in range(copies):
+            fn(k)
+        torch.cuda.synchronize()
+        for k in range(copies):
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=stream):
+                fn(k)
+            graphs.append(gr)
+    for i in range(warmup):
+        graphs[i % copies].replay()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    cur = torch.cuda.current_stream()
+    t0.record(cur)
+    for i in range(steps):
+        graphs[i % copies].replay()
+    t1.record(cur)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    return {"metric": "Msamples/s", "value": round(samples / (ms * 1e-3) / 1e6, 3), "ms_per_step": round(ms, 6),
+            "steps": steps}
+
+
+def cpu_spectral_baseline(budget_s):
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib
+    import synth
     kind = "reference" if oracle_lib.ref_available() else "port"
     lib = oracle_lib.reference() if kind == "reference" else oracle_lib.oracle()
-    C, L = x.shape
+    C, L, n_fft = 2, 343980, 4096
+    x = synth.normal(2024, (C, L), 0.1)
     reps = 0
     t0 = time.perf_counter()
     while True:
         for c in range(C):
-            s = lib.htdemucs_spec(x[c], C1_NFFT)
-            lib.htdemucs_ispec(s, C1_NFFT, L)
+            s = lib.htdemucs_spec(x[c], n_fft)
+            lib.htdemucs_ispec(s, n_fft, L)
         reps += 1
         el = time.perf_counter() - t0
         if el >= budget_s:
             break
-    return {
-        "value": round(reps * C * L / el / 1e6, 3),
-        "unit": "Msamples/s",
-        "cores": 1,
-        "kind": kind,
-        "sample": f"{reps} HTDemucs-spec STFT->iSTFT round trips of the same stereo {L}-sample input "
-                  f"({el:.1f} s, single thread, double precision, "
-                  + ("src/stft.h built from the reference sources" if kind == "reference"
-                     else "C restatement of src/stft.h") + ")",
-    }
+    return {"value": round(reps * C * L / el / 1e6, 3), "unit": "Msamples/s", "cores": 1, "kind": kind,
+            "sample": f"{reps} HTDemucs-spec STFT->iSTFT round trips of stereo {L} samples ({el:.1f} s, single "
+                      "thread, double precision, " + ("src/stft.h compiled from the reference sources" if kind ==
+                                                      "reference" else "C restatement of src/stft.h") + ")"}
 
 
 def main():
     args = parse()
     if args.gpus != 1:
-        print("bench.py: this build measures one GPU; --gpus N > 1 is not supported "
-              "(no multi-GPU path is built)", file=sys.stderr)
+        print(f"bench.py: --gpus {args.gpus}: this build runs on one GPU; there is no multi-GPU path "
+              "(the workload shards by independent channels/chunks, see the design notes)", file=sys.stderr)
         sys.exit(2)
-    import numpy as np
     import torch
 
     import stx
-    import synth
 
     dev = torch.device("cuda:0")
-    stream = torch.cuda.current_stream()
-    fft = stx.FFT(C1_NFFT)
-    C, L = 2, C1_LEN
-    T = stx.htdemucs_frames(C1_NFFT, L)
-    F = C1_NFFT // 2
-    x_host = synth.normal(2024, (C, L), 0.1)
-    x0 = torch.from_numpy(x_host).to(dev)
-    per_copy = (C * L * 4) * 2 + C * F * T * 8
-    copies = max(2, int(np.ceil(512e6 / per_copy)) + 1)
-    xs = [x0.clone() for _ in range(copies)]
-    specs = [torch.empty((C, F, T), dtype=torch.complex64, device=dev) for _ in range(copies)]
-    ys = [torch.empty((C, L), dtype=torch.float32, device=dev) for _ in range(copies)]
-
-    def step(i, ev=None):
-        k = i % copies
-        if ev is not None:
-            ev[0].record(stream)
-        stx.htdemucs_spec(fft, xs[k], out=specs[k], stream=stream)
-        if ev is not None:
-            ev[1].record(stream)
-        stx.htdemucs_ispec(fft, specs[k], L, out=ys[k], stream=stream)
-        if ev is not None:
-            ev[2].record(stream)
-
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-
-    # Timed region 1: the steps alone.
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0.record(stream)
-    for i in range(args.steps):
-        step(i)
-    t1.record(stream)
-    torch.cuda.synchronize()
-    ms_per_step = t0.elapsed_time(t1) / args.steps
-
-    # Timed region 2: the same steps with HIP events around each kernel.
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    for i in range(args.steps):
-        step(i, evs[i])
-    torch.cuda.synchronize()
-    stft_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
-    istft_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
-
-    samples = C * L
-    alg_bytes = samples * 4 + C * F * T * 8           # 13,761,888 B, same for both kernels
-    kernels = {"stft_kernel<4096,1>": stft_ms, "istft_kernel<4096,1,16>": istft_ms}
-    dom = max(kernels, key=kernels.get)
-    achieved = alg_bytes / (kernels[dom] * 1e-3) / 1e9
-    traffic = traffic_for(dom)
-
-    # Parity of the measured output against the oracle (one channel), reported alongside.
+    res, _ = run_ops(args, torch, stx, dev)
     out = {
         "metric": METRIC,
-        "value": round(samples / (ms_per_step * 1e-3) / 1e6, 3),
-        "unit": "Msamples/s",
+        "value": res["value"],
+        "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 6),
+        "ms_per_step": res["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {
-            "workload": "htdemucs_spec_ispec_round_trip",
-            "channels": C,
-            "samples_per_channel": L,
-            "n_fft": C1_NFFT,
-            "hop": C1_NFFT // 4,
-            "frames": T,
-            "bins": F,
-            "layout": "f_major",
-            "input": "N(0, 0.1^2) fp32 from seed 2024",
-            "input_copies_rotated": copies,
-        },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": dom,
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-            "algorithmic_bytes": alg_bytes,
-            "avg_us": round(kernels[dom] * 1e3, 3),
-        },
-        "kernels_us": {k: round(v * 1e3, 3) for k, v in kernels.items()},
+        "config": res["config"],
+        "roofline": res["roofline"],
+        "hbm_frac_of_peak": round(res["value"] / HBM_PEAK_GBS, 4),
+        "ops_us": res["ops_us"],
+        "ops_share_us": res["ops_share_us"],
     }
+    torch.cuda.empty_cache()
+    if not args.no_spectral:
+        out["spectral"] = run_spectral(args, torch, stx, dev)
+    if args.copy_calibration:
+        a = torch.empty(64 << 20, device=dev)
+        b = torch.empty_like(a)
+        b.copy_(a)
+        torch.cuda.synchronize()
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(x_host, args.cpu_seconds)
+        out["cpu_baseline"] = cpu_ops_baseline(args.cpu_seconds)
+        if "spectral" in out:
+            out["spectral"]["htdemucs_round_trip"]["cpu_baseline"] = cpu_spectral_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)
 
 
