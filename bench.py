@@ -31,6 +31,9 @@ The same line carries the spectral half of the metric, STFT+iSTFT Msamples/s:
   spectral.roformer_chunk: stx_torch_stft (n_fft 2048, hop 441) -> stx_band_scatter_apply with
     60 mel bands and uniform [-1, 1] masks (one stem) -> stx_torch_istft on one stereo chunk of
     352,800 samples (src/roformer.cpp:217-283).
+rows: every other hot-path kernel at its config shape (c3 band gather / scatter-apply / STFT /
+iSTFT, c4 RMSNorm, RoPE, softmax, bias+GELU, c5 demix chunk build and overlap-add), each timed
+cold (a graph of calls on more than 512 MB of distinct buffers) against its algorithmic bytes.
 """
 import argparse
 import json
@@ -55,6 +58,7 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on each CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-spectral", action="store_true")
+    p.add_argument("--no-rows", action="store_true", help="skip the per-kernel timings of the other configs")
     p.add_argument("--copy-calibration", action="store_true",
                    help="end with one 256 MiB device copy (the reference kernel for PMC byte counters)")
     return p.parse_args()
@@ -371,6 +375,115 @@ def time_graphs(torch, stream, fn, copies, steps, samples, warmup):
             "steps": steps}
 
 
+def time_call(torch, stream, make, nbytes, replays=3):
+    """Cold timing of one op: a graph of calls on distinct buffers (more than 512 MB of them in
+    total) replayed `replays` times between two HIP events; microseconds per call."""
+    n_inst = max(1, int(512e6 // max(nbytes, 1)) + 1) if nbytes < 512e6 else 1
+    calls = [make() for _ in range(n_inst)]
+    with torch.cuda.stream(stream):
+        for c in calls:
+            c()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr, stream=stream):
+            for c in calls:
+                c()
+        gr.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(replays):
+            gr.replay()
+        e1.record(stream)
+    e1.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (replays * n_inst)
+    del gr, calls
+    torch.cuda.empty_cache()
+    return {"us": round(us, 3), "algorithmic_bytes": int(nbytes), "GBps": round(nbytes / us / 1e3, 1),
+            "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+
+def run_rows(torch, stx, dev):
+    """Every other hot-path kernel at its config shape, cold, against its algorithmic bytes."""
+    import synth
+    stream = torch.cuda.Stream()
+    rn = lambda *shape: torch.randn(shape, device=dev)
+    out = {}
+    # c3: RoFormer chunk spectral path (stereo 352,800, n_fft 2048, hop 441; 60 mel bands).
+    n_fft, hop, L, C = 2048, 441, 352800, 2
+    fft = stx.FFT(n_fft)
+    sizes, freqs = stx.mel_band_map(44100, n_fft, 60)
+    bands = stx.Bands(sizes, freqs, n_fft // 2 + 1, C)
+    T, F = stx.torch_stft_frames(L, hop), n_fft // 2 + 1
+    feat = bands.total_feat * T
+
+    def mk_stft():
+        x, y = rn(C, L), torch.empty((C, T, F), dtype=torch.complex64, device=dev)
+        return lambda: stx.torch_stft(fft, x, hop, layout=stx.T_MAJOR, out=y, stream=stream)
+    out["c3_stft_t_major"] = time_call(torch, stream, mk_stft, C * L * 4 + C * T * F * 8)
+
+    def mk_gather():
+        z, f = torch.randn((1, C, T, F), dtype=torch.complex64, device=dev), torch.empty((1, feat), device=dev)
+        return lambda: bands.gather(z, T, layout=stx.T_MAJOR, out=f, stream=stream)
+    out["c3_band_gather"] = time_call(torch, stream, mk_gather, C * T * F * 8 + feat * 4)
+
+    def mk_scatter():
+        m = torch.from_numpy(synth.uniform(3, (1, 1, feat))).to(dev)
+        z = torch.randn((1, C, T, F), dtype=torch.complex64, device=dev)
+        o = torch.empty((1, 1, C, T, F), dtype=torch.complex64, device=dev)
+        return lambda: bands.scatter_apply(m, z, T, layout=stx.T_MAJOR, out=o, stream=stream)
+    out["c3_scatter_apply"] = time_call(torch, stream, mk_scatter, feat * 4 + 2 * C * T * F * 8)
+
+    def mk_istft():
+        z, y = torch.randn((C, T, F), dtype=torch.complex64, device=dev), torch.empty((C, hop * (T - 1)), device=dev)
+        return lambda: stx.torch_istft(fft, z, hop, layout=stx.T_MAJOR, out=y, stream=stream)
+    out["c3_istft_t_major"] = time_call(torch, stream, mk_istft, C * L * 4 + C * T * F * 8)
+    del bands, fft
+
+    # c4: RoFormer transformer ops (dim 384, 8 heads x 64, 60 bands x 801 frames).
+    def mk_rms():
+        x, g, y = rn(48060, 384), rn(384), torch.empty((48060, 384), device=dev)
+        return lambda: stx.rms_norm(x, 1e-24, gamma=g, out=y, stream=stream)
+    out["c4_rms_norm_mul"] = time_call(torch, stream, mk_rms, 2 * 48060 * 384 * 4 + 384 * 4)
+    for name, shape, n in (("c4_rope_time", (60, 801, 8, 64), 801), ("c4_rope_band", (801, 60, 8, 64), 60)):
+        def mk_rope(shape=shape, n=n):
+            x, y = rn(*shape), torch.empty(shape, device=dev)
+            pos = torch.arange(n, dtype=torch.int32, device=dev)
+            return lambda: stx.rope_ext(x, pos, 64, mode=0, freq_base=10000.0, out=y, stream=stream)
+        out[name] = time_call(torch, stream, mk_rope, 2 * 64 * 8 * 801 * 60 * 4 + n * 4)
+    for name, shape in (("c4_softmax_time", (60, 8, 801, 801)), ("c4_softmax_band", (801, 8, 60, 60))):
+        def mk_sm(shape=shape):
+            x, y = rn(*shape), torch.empty(shape, device=dev)
+            return lambda: stx.soft_max_ext(x, 0.125, out=y, stream=stream)
+        n = 1
+        for d in shape:
+            n *= d
+        out[name] = time_call(torch, stream, mk_sm, 8 * n)
+
+    def mk_ff():
+        h, bb, y = rn(60, 801, 1536), rn(1536), torch.empty((60, 801, 1536), device=dev)
+        return lambda: stx.gelu_erf(h, bias=bb, out=y, stream=stream)
+    out["c4_gelu_ff_bias"] = time_call(torch, stream, mk_ff, 2 * 60 * 801 * 1536 * 4 + 1536 * 4)
+
+    # c5: full-song demix (180 s stereo, chunk 352,800, step 88,200, 4 stems).
+    Lsong, chunk, step, S = 7938000, 352800, 88200, 4
+    plan = stx.Demix(Lsong, C, chunk, step)
+    _, table = stx.demix_plan(Lsong, chunk, step)
+    lens = int(table["length"].astype("int64").sum())
+    mix = torch.from_numpy(synth.sines_plus_pink(5, C, Lsong)).to(dev)
+
+    def mk_chunks():
+        m, parts = mix.clone(), torch.empty((plan.n_chunks, C, chunk), device=dev)
+        return lambda: plan.chunks(m, out=parts, stream=stream)
+    out["c5_demix_chunks"] = time_call(torch, stream, mk_chunks, C * Lsong * 4 + plan.n_chunks * C * chunk * 4)
+
+    def mk_ola():
+        y, o = rn(plan.n_chunks, S, C, chunk), torch.empty((S, C, Lsong), device=dev)
+        return lambda: plan.overlap_add(y, out=o, stream=stream)
+    out["c5_demix_overlap_add"] = time_call(torch, stream, mk_ola, lens * S * C * 4 + S * C * Lsong * 4)
+    del plan
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_spectral_baseline(budget_s):
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib
@@ -429,6 +542,8 @@ def main():
     torch.cuda.empty_cache()
     if not args.no_spectral:
         out["spectral"] = run_spectral(args, torch, stx, dev)
+    if not args.no_rows:
+        out["rows"] = run_rows(torch, stx, dev)
     if args.copy_calibration:
         a = torch.empty(64 << 20, device=dev)
         b = torch.empty_like(a)

@@ -147,8 +147,8 @@ __device__ __forceinline__ float erfcx_scaled(float u) {
     return p * rcp_nr(fmaf(2.f, u, 1.f));
 }
 
-// gelu(x) = x Phi(x), Phi(x) = (1 + erf(x/sqrt2)) / 2, to a few ulp everywhere (no library
-// erf/erfc: the ROCm erfcf loses ~2u^2 ulps in its tail because it does not split u^2).
+// gelu(x) = x Phi(x), Phi(x) = (1 + erf(x/sqrt2)) / 2, to a few ulp everywhere, without a
+// library erf/erfc call (one short path per sign, ~50 VALU instructions per element).
 //   |x| < 1:  erf(x/sqrt2) = x Q(x^2), Q of degree 5 fitted for this library (relative error
 //             of Phi 1.6e-9 on |x| <= 1).
 //   |x| >= 1: Phi(-|x|) = exp(-x^2/2) erfcx(|x|/sqrt2) / 2 with x^2 split exactly into head and
