@@ -304,7 +304,8 @@ typedef struct {
  * (ne2) are split into groups of ceil(ne2 / n_groups); each group of each ne3 slice is
  * normalised over ne0 x ne1 x its channels with the biased variance. weight and bias (either
  * may be NULL) repeat into a; gelu != 0 applies GELU-erf last. a and dst must be contiguous
- * (dst may be a). workspace: device, stx_group_norm_workspace_size() bytes. */
+ * (dst may be a). workspace: device, 256-byte aligned, stx_group_norm_workspace_size() bytes,
+ * no initialisation needed; calls that share a workspace must not run concurrently. */
 STX_API size_t     stx_group_norm_workspace_size(const stx_tensor* a, int n_groups);
 STX_API stx_status stx_group_norm(const stx_tensor* a, const stx_tensor* dst, int n_groups, float eps,
                                   const stx_tensor* weight, const stx_tensor* bias, int gelu, void* workspace,
@@ -350,6 +351,11 @@ STX_API stx_status stx_mul(const stx_tensor* a, const stx_tensor* b, const stx_t
  * with the same two roundings. h and s repeat into x. */
 STX_API stx_status stx_mul_add(const stx_tensor* x, const stx_tensor* h, const stx_tensor* s, const stx_tensor* dst,
                                stx_stream stream);
+/* ggml_add(x, ggml_mul(glu(a), s)): the GLU + LayerScale + residual of a DConv branch
+ * (src/htdemucs.cpp:137-139), fused; bit-identical to stx_glu then stx_mul_add. a is split
+ * along `dim` as in stx_glu; x, dst have the GLU output's shape; s repeats into dst. */
+STX_API stx_status stx_glu_mul_add(const stx_tensor* x, const stx_tensor* a, int dim, const stx_tensor* s,
+                                   const stx_tensor* dst, stx_stream stream);
 
 /* ggml_rope_ext(a, pos, NULL, n_dims, mode, n_ctx_orig, freq_base, freq_scale, ext_factor,
  * attn_factor, beta_fast, beta_slow) (src/roformer.cpp:109-113): rotates each ne0 row of

@@ -321,16 +321,19 @@ __global__ __launch_bounds__(256) void softmax_kernel(SoftmaxArgs a) {
 }
 
 // --------------------------------------------------------------------- elementwise
-enum EwOp { EW_GELU = 0, EW_GLU = 1, EW_ADD = 2, EW_MUL = 3, EW_MUL_ADD = 4, EW_ADD_GELU = 5 };
+enum EwOp { EW_GELU = 0, EW_GLU = 1, EW_ADD = 2, EW_MUL = 3, EW_MUL_ADD = 4, EW_ADD_GELU = 5, EW_GLU_MUL_ADD = 6 };
+
+__device__ __forceinline__ float glu_value(float a, float g) { return a / (1.0f + expf(-g)); }
 
 // GLU: x * sigmoid(y) with x and y two halves of one source. MUL_ADD: x + fl(y * z), rounded
 // after each operation like ggml_add(x, ggml_mul(h, s)). ADD_GELU: gelu(fl(x + y)), a bias
-// add followed by GELU.
+// add followed by GELU. GLU_MUL_ADD: x + fl(glu(y, z) * w), the GLU + LayerScale + residual
+// of a DConv branch, bit-identical to GLU followed by MUL_ADD.
 template <int OP>
-__device__ __forceinline__ float ew_apply(float x, float y, float z) {
+__device__ __forceinline__ float ew_apply(float x, float y, float z, float w) {
 #pragma clang fp contract(off)
     if constexpr (OP == EW_GELU) return gelu_erf(x);
-    if constexpr (OP == EW_GLU) return x / (1.0f + expf(-y));
+    if constexpr (OP == EW_GLU) return glu_value(x, y);
     if constexpr (OP == EW_ADD) return x + y;
     if constexpr (OP == EW_MUL) return x * y;
     if constexpr (OP == EW_MUL_ADD) {
@@ -338,16 +341,21 @@ __device__ __forceinline__ float ew_apply(float x, float y, float z) {
         return x + p;
     }
     if constexpr (OP == EW_ADD_GELU) return gelu_erf(x + y);
+    if constexpr (OP == EW_GLU_MUL_ADD) {
+        const float p = glu_value(y, z) * w;
+        return x + p;
+    }
     return 0.f;
 }
 
 template <int OP> constexpr bool has_b() { return OP != EW_GELU; }
-template <int OP> constexpr bool has_c() { return OP == EW_MUL_ADD; }
+template <int OP> constexpr bool has_c() { return OP == EW_MUL_ADD || OP == EW_GLU_MUL_ADD; }
+template <int OP> constexpr bool has_d() { return OP == EW_GLU_MUL_ADD; }
 
-// General path. a: same shape as dst (any row strides). b, c repeat into dst. Work unit =
+// General path. a: same shape as dst (any row strides). b, c, d repeat into dst. Work unit =
 // (row, 1024-element chunk of the row).
 struct EwArgs {
-    T4 a, b, c, dst;
+    T4 a, b, c, d, dst;
 };
 
 __device__ __forceinline__ const float* bcast_row(const T4& t, long long i1, long long i2, long long i3) {
@@ -372,6 +380,7 @@ __global__ __launch_bounds__(256) void ew_rows_kernel(EwArgs a) {
         const float* xa = reinterpret_cast<const float*>(a.a.data + i1 * a.a.nb[1] + i2 * a.a.nb[2] + i3 * a.a.nb[3]);
         const float* xb = has_b<OP>() ? bcast_row(a.b, i1, i2, i3) : nullptr;
         const float* xc = has_c<OP>() ? bcast_row(a.c, i1, i2, i3) : nullptr;
+        const float* xd = has_d<OP>() ? bcast_row(a.d, i1, i2, i3) : nullptr;
         float* y = reinterpret_cast<float*>(a.dst.data + i1 * a.dst.nb[1] + i2 * a.dst.nb[2] + i3 * a.dst.nb[3]);
 #pragma unroll
         for (int k = 0; k < 4; k++) {
@@ -379,7 +388,8 @@ __global__ __launch_bounds__(256) void ew_rows_kernel(EwArgs a) {
             if (i < n0) {
                 const float vb = has_b<OP>() ? bcast_at(xb, a.b.ne[0], n0, i) : 0.f;
                 const float vc = has_c<OP>() ? bcast_at(xc, a.c.ne[0], n0, i) : 0.f;
-                y[i] = ew_apply<OP>(xa[i], vb, vc);
+                const float vd = has_d<OP>() ? bcast_at(xd, a.d.ne[0], n0, i) : 0.f;
+                y[i] = ew_apply<OP>(xa[i], vb, vc, vd);
             }
         }
     }
@@ -430,38 +440,47 @@ __device__ __forceinline__ float flat_at(const Flat& f, unsigned i) {
 }
 
 template <int OP>
-__global__ __launch_bounds__(256) void ew_flat_kernel(const float* __restrict__ xa, Flat b, Flat c,
+__global__ __launch_bounds__(256) void ew_flat_kernel(const float* __restrict__ xa, Flat b, Flat c, Flat d,
                                                       float* __restrict__ y, unsigned n) {
     const unsigned n4 = n / 4;
     const unsigned stride = gridDim.x * 256;
     for (unsigned k = blockIdx.x * 256 + threadIdx.x; k < n4; k += stride) {
         const unsigned i = 4 * k;
         const float4 p = *reinterpret_cast<const float4*>(xa + i);
-        float vb[4], vc[4];
+        float vb[4], vc[4], vd[4];
         flat_load(b, i, vb);
         flat_load(c, i, vc);
-        *reinterpret_cast<float4*>(y + i) = make_float4(ew_apply<OP>(p.x, vb[0], vc[0]), ew_apply<OP>(p.y, vb[1], vc[1]),
-                                                        ew_apply<OP>(p.z, vb[2], vc[2]), ew_apply<OP>(p.w, vb[3], vc[3]));
+        flat_load(d, i, vd);
+        *reinterpret_cast<float4*>(y + i) =
+            make_float4(ew_apply<OP>(p.x, vb[0], vc[0], vd[0]), ew_apply<OP>(p.y, vb[1], vc[1], vd[1]),
+                        ew_apply<OP>(p.z, vb[2], vc[2], vd[2]), ew_apply<OP>(p.w, vb[3], vc[3], vd[3]));
     }
     for (unsigned i = 4 * n4 + blockIdx.x * 256 + threadIdx.x; i < n; i += stride)
-        y[i] = ew_apply<OP>(xa[i], flat_at(b, i), flat_at(c, i));
+        y[i] = ew_apply<OP>(xa[i], flat_at(b, i), flat_at(c, i), flat_at(d, i));
 }
 
 // ----------------------------------------------------------------------- GROUP_NORM
 // Groups: for each i3, channels (ne2) [g*cpg, min((g+1)*cpg, ne2)) with cpg = ceil(ne2 / G),
 // normalised together over ne0 x ne1 x channels (ggml_group_norm). Contiguous tensors only,
 // so a group is one contiguous span of floats (fewer than 2^32 of them).
-//   pass 1 (gn_partial_kernel): one block per chunk of kGnChunk floats of a group writes the
-//     chunk's sums of d and d^2 in double, d = x - K with K the group's first element: the
-//     shift removes a common offset, so S2 - S1^2/N below loses only ~1e-16 ((mean - K)/sigma)^2
-//     relative;
-//   pass 2 (gn_apply_kernel): every block issues its chunk's loads (and its affine
-//     parameters) first, then adds up all of its group's partials in a fixed order (every
-//     block gets the same statistics bit for bit, deterministically) and writes
+//   pass 1 (gn_partial_kernel): one block per chunk of a group writes the chunk's sums of d
+//     and d^2 in double, d = x - K with K the group's first element (the shift removes a
+//     common offset, so S2 - S1^2/N loses only ~1e-16 ((mean - K)/sigma)^2 relative); the
+//     first block also stores K, so that pass 2 does not re-read x[0] (x may be y);
+//   pass 2 (gn_apply_kernel): every block issues its chunk's loads and its affine parameters
+//     first, then adds up all of its group's partial sums in a fixed order (so every block gets
+//     the same statistics bit for bit, deterministically, without atomics) and writes
 //     ((x - mean) / sqrt(M2/N + eps)) [* w + b] [-> gelu], in double up to the GELU, which
 //     takes the double as a float head and tail.
-constexpr int kGnVec = 4;                         // float4 loads per thread per chunk
-constexpr int kGnChunk = 256 * 4 * kGnVec;        // floats per partial and per apply block
+// A single pass would need a grid-wide barrier; same-address atomics serialise across the
+// eight XCDs (about 0.1 us per arriving block, measured), which costs more than the second
+// read of x at these sizes.
+//
+// Workspace: [groups] shift | [groups][partial chunks][2] partial sums.
+// VEC float4 per thread: chunks of 1024 * VEC floats, chosen separately for the two passes.
+constexpr int kGnVecPartial = 4, kGnVecApply = 1;
+template <int VEC> constexpr int gn_chunk() { return 256 * 4 * VEC; }
+constexpr unsigned kSpinLimit = 1u << 22;         // barrier polls (~0.25 s) before giving up
 
 enum AffineKind { AFF_NONE = 0, AFF_CHANNEL = 1, AFF_NE0 = 2, AFF_GENERAL = 3 };
 
@@ -476,15 +495,15 @@ struct GroupNormArgs {
     const float* x;
     float* y;
     Affine w, b;
-    double* part;            // [groups_total][chunks][2]
+    double* shift;           // [groups_total]
+    double* part;            // [groups_total][partial chunks][2]
     unsigned ne0, ne1;       // dims of x (ne3 is folded into the group index)
     long long ne2;
     unsigned plane;          // ne0 * ne1
     long long cpg;           // channels per group
     int groups;              // groups per ne3 slice
-    int chunks;              // partials per group (max over groups)
+    int chunks;              // partial chunks per group (max over groups)
     float eps;
-    int gelu;
     int vec;                 // all group spans 16-byte aligned
 };
 
@@ -500,10 +519,11 @@ __device__ __forceinline__ void group_span(const GroupNormArgs& a, int gt, long 
 
 // Loads this thread's values of chunk [lo, hi) of base: float4 k covers positions
 // lo + (k * 256 + tid) * 4 .. +3.
+template <int VEC>
 __device__ __forceinline__ void gn_load(const GroupNormArgs& a, const float* base, unsigned lo, unsigned hi,
-                                        float (&v)[4 * kGnVec], bool (&ok)[4 * kGnVec]) {
+                                        float (&v)[4 * VEC], bool (&ok)[4 * VEC]) {
 #pragma unroll
-    for (int k = 0; k < kGnVec; k++) {
+    for (int k = 0; k < VEC; k++) {
         const unsigned p = lo + (k * 256 + threadIdx.x) * 4;
         if (a.vec && p + 3 < hi) {
             const float4 q = *reinterpret_cast<const float4*>(base + p);
@@ -537,23 +557,13 @@ __device__ __forceinline__ void block_sum2(double& a, double& b, double* red) {
     b = (red[4] + red[5]) + (red[6] + red[7]);
 }
 
-__global__ __launch_bounds__(256) void gn_partial_kernel(GroupNormArgs a) {
-    __shared__ double red[8];
-    const int gt = (int)blockIdx.y;
-    long long begin, c0, i3;
-    unsigned count;
-    group_span(a, gt, begin, count, c0, i3);
-    const unsigned lo = blockIdx.x * (unsigned)kGnChunk;
-    if (lo >= count) return;                                   // uniform over the block
-    const unsigned hi = min(lo + (unsigned)kGnChunk, count);
-    const float* xg = a.x + begin;
-    float v[4 * kGnVec];
-    bool ok[4 * kGnVec];
-    gn_load(a, xg, lo, hi, v, ok);
-    const double shift = (double)xg[0];
+// Block partial sums of d = v - shift over this thread's valid values, written to part.
+template <int VEC>
+__device__ __forceinline__ void gn_write_partial(const GroupNormArgs& a, int gt, const float (&v)[4 * VEC],
+                                                 const bool (&ok)[4 * VEC], double shift, double* red) {
     double s1 = 0.0, s2 = 0.0;
 #pragma unroll
-    for (int k = 0; k < 4 * kGnVec; k++) {
+    for (int k = 0; k < 4 * VEC; k++) {
         const double d = ok[k] ? (double)v[k] - shift : 0.0;
         s1 += d;
         s2 += d * d;
@@ -563,7 +573,25 @@ __global__ __launch_bounds__(256) void gn_partial_kernel(GroupNormArgs a) {
         double* p = a.part + ((size_t)gt * a.chunks + blockIdx.x) * 2;
         p[0] = s1;
         p[1] = s2;
+        if (blockIdx.x == 0) a.shift[gt] = shift;
     }
+}
+
+// mean and 1/sqrt(var + eps) of group gt from its partial sums (fixed order).
+template <int VEC>
+__device__ __forceinline__ void gn_stats(const GroupNormArgs& a, int gt, unsigned count, double shift, double* red,
+                                         double& mean, double& rstd) {
+    const int nch = (int)((count + gn_chunk<VEC>() - 1) / gn_chunk<VEC>());
+    const double* part = a.part + (size_t)gt * a.chunks * 2;
+    double s1 = 0.0, s2 = 0.0;
+    for (int k = threadIdx.x; k < nch; k += 256) {
+        s1 += part[2 * k];
+        s2 += part[2 * k + 1];
+    }
+    block_sum2(s1, s2, red);
+    const double N = (double)count, dm = s1 / N;
+    mean = shift + dm;
+    rstd = 1.0 / sqrt(fmax(s2 / N - dm * dm, 0.0) + (double)a.eps);
 }
 
 // One affine operand at element (channel c, i0, i1, i3) under the kernel's affine mode AK:
@@ -575,26 +603,13 @@ __device__ __forceinline__ float affine_at(const Affine& f, long long c, unsigne
     return f.p[(i0 % f.ne[0]) * f.nb[0] + (i1 % f.ne[1]) * f.nb[1] + (c % f.ne[2]) * f.nb[2] + (i3 % f.ne[3]) * f.nb[3]];
 }
 
-template <int AK, bool GELU>
-__global__ __launch_bounds__(256) void gn_apply_kernel(GroupNormArgs a) {
-    __shared__ double red[8];
-    const int gt = (int)blockIdx.y;
-    long long begin, c0, i3;
-    unsigned count;
-    group_span(a, gt, begin, count, c0, i3);
-    const unsigned lo = blockIdx.x * (unsigned)kGnChunk;
-    if (lo >= count) return;                                   // uniform over the block
-    const unsigned hi = min(lo + (unsigned)kGnChunk, count);
-    const float* xg = a.x + begin;
-    float* yg = a.y + begin;
-    float v[4 * kGnVec];
-    bool ok[4 * kGnVec];
-    gn_load(a, xg, lo, hi, v, ok);                             // in flight while the stats merge
-    // Affine parameters of every element, also loaded before the merge: channel c and (i0, i1)
-    // inside its plane of element p, advanced element by element.
-    float wv[4 * kGnVec], bv[4 * kGnVec];
+// Affine parameters of this thread's elements: channel c and (i0, i1) inside its plane of
+// element p, advanced element by element.
+template <int AK, int VEC>
+__device__ __forceinline__ void gn_affine(const GroupNormArgs& a, unsigned lo, long long c0, long long i3,
+                                          const bool (&ok)[4 * VEC], float (&wv)[4 * VEC], float (&bv)[4 * VEC]) {
 #pragma unroll
-    for (int k = 0; k < kGnVec; k++) {
+    for (int k = 0; k < VEC; k++) {
         const unsigned p = lo + (k * 256 + threadIdx.x) * 4;
         long long c = 0;
         unsigned i0 = 0, i1 = 0;
@@ -622,19 +637,14 @@ __global__ __launch_bounds__(256) void gn_apply_kernel(GroupNormArgs a) {
             }
         }
     }
-    const int nch = (int)((count + kGnChunk - 1) / kGnChunk);
-    const double* part = a.part + (size_t)gt * a.chunks * 2;
-    double s1 = 0.0, s2 = 0.0;
-    for (int k = threadIdx.x; k < nch; k += 256) {
-        s1 += part[2 * k];
-        s2 += part[2 * k + 1];
-    }
-    block_sum2(s1, s2, red);
-    const double N = (double)count, dm = s1 / N;
-    const double mean = (double)xg[0] + dm;
-    const double rstd = 1.0 / sqrt(fmax(s2 / N - dm * dm, 0.0) + (double)a.eps);
+}
+
+template <bool GELU, int VEC>
+__device__ __forceinline__ void gn_store(const GroupNormArgs& a, float* yg, unsigned lo, unsigned hi, double mean,
+                                         double rstd, const float (&v)[4 * VEC], const bool (&ok)[4 * VEC],
+                                         const float (&wv)[4 * VEC], const float (&bv)[4 * VEC]) {
 #pragma unroll 1
-    for (int k = 0; k < kGnVec; k++) {
+    for (int k = 0; k < VEC; k++) {
         const unsigned p = lo + (k * 256 + threadIdx.x) * 4;
         if (p >= hi) continue;
         float o[4];
@@ -653,6 +663,43 @@ __global__ __launch_bounds__(256) void gn_apply_kernel(GroupNormArgs a) {
                 if (ok[4 * k + j]) yg[p + j] = o[j];
         }
     }
+}
+
+__global__ __launch_bounds__(256) void gn_partial_kernel(GroupNormArgs a) {
+    constexpr int VEC = kGnVecPartial, CH = gn_chunk<VEC>();
+    __shared__ double red[8];
+    const int gt = (int)blockIdx.y;
+    long long begin, c0, i3;
+    unsigned count;
+    group_span(a, gt, begin, count, c0, i3);
+    const unsigned lo = blockIdx.x * (unsigned)CH;
+    if (lo >= count) return;                                   // uniform over the block
+    const unsigned hi = min(lo + (unsigned)CH, count);
+    const float* xg = a.x + begin;
+    float v[4 * VEC];
+    bool ok[4 * VEC];
+    gn_load<VEC>(a, xg, lo, hi, v, ok);
+    gn_write_partial<VEC>(a, gt, v, ok, (double)xg[0], red);
+}
+
+template <int AK, bool GELU>
+__global__ __launch_bounds__(256) void gn_apply_kernel(GroupNormArgs a) {
+    constexpr int VEC = kGnVecApply, CH = gn_chunk<VEC>();
+    __shared__ double red[8];
+    const int gt = (int)blockIdx.y;
+    long long begin, c0, i3;
+    unsigned count;
+    group_span(a, gt, begin, count, c0, i3);
+    const unsigned lo = blockIdx.x * (unsigned)CH;
+    if (lo >= count) return;                                   // uniform over the block
+    const unsigned hi = min(lo + (unsigned)CH, count);
+    float v[4 * VEC], wv[4 * VEC], bv[4 * VEC];
+    bool ok[4 * VEC];
+    gn_load<VEC>(a, a.x + begin, lo, hi, v, ok);               // in flight while the stats add up
+    gn_affine<AK, VEC>(a, lo, c0, i3, ok, wv, bv);
+    double mean, rstd;
+    gn_stats<kGnVecPartial>(a, gt, count, a.shift[gt], red, mean, rstd);   // shift from pass 1
+    gn_store<GELU, VEC>(a, a.y + begin, lo, hi, mean, rstd, v, ok, wv, bv);
 }
 
 // ----------------------------------------------------------------------------- ROPE
@@ -802,16 +849,17 @@ bool flat_operand(const stx_tensor* t, const stx_tensor* dst, Flat& f) {
 }
 
 template <int OP>
-void launch_elementwise(const EwArgs& args, const stx_tensor* b, const stx_tensor* c, const stx_tensor* dst,
-                        hipStream_t s) {
+void launch_elementwise(const EwArgs& args, const stx_tensor* b, const stx_tensor* c, const stx_tensor* d,
+                        const stx_tensor* dst, hipStream_t s) {
     const long long n = nelem(args.dst);
-    Flat fb, fc;
+    Flat fb, fc, fd;
     const bool flat = n < (1LL << 32) - 1024 && contiguous(args.a) && contiguous(args.dst) && aligned16(args.a.data) &&
-                      aligned16(args.dst.data) && flat_operand(b, dst, fb) && flat_operand(c, dst, fc);
+                      aligned16(args.dst.data) && flat_operand(b, dst, fb) && flat_operand(c, dst, fc) &&
+                      flat_operand(d, dst, fd);
     if (flat) {
         const unsigned blocks = (unsigned)std::min<long long>((n / 4 + 255) / 256 + 1, 1 << 16);
         hipLaunchKernelGGL((ew_flat_kernel<OP>), dim3(blocks), dim3(256), 0, s,
-                           reinterpret_cast<const float*>(args.a.data), fb, fc,
+                           reinterpret_cast<const float*>(args.a.data), fb, fc, fd,
                            reinterpret_cast<float*>(args.dst.data), (unsigned)n);
         launch_check("ew_flat_kernel");
         return;
@@ -821,22 +869,24 @@ void launch_elementwise(const EwArgs& args, const stx_tensor* b, const stx_tenso
     launch_check("ew_rows_kernel");
 }
 
-void elementwise(int op, const stx_tensor* a, const stx_tensor* b, const stx_tensor* c, const stx_tensor* dst,
-                 stx_stream stream) {
+void elementwise(int op, const stx_tensor* a, const stx_tensor* b, const stx_tensor* c, const stx_tensor* d,
+                 const stx_tensor* dst, stx_stream stream) {
     EwArgs args{};
     args.a = view(a);
     args.dst = view(dst);
     if (b) args.b = view(b);
     if (c) args.c = view(c);
+    if (d) args.d = view(d);
     if (nelem(args.dst) == 0) return;
     const hipStream_t s = as_stream(stream);
     switch (op) {
-        case EW_GELU: launch_elementwise<EW_GELU>(args, b, c, dst, s); break;
-        case EW_GLU: launch_elementwise<EW_GLU>(args, b, c, dst, s); break;
-        case EW_ADD: launch_elementwise<EW_ADD>(args, b, c, dst, s); break;
-        case EW_MUL: launch_elementwise<EW_MUL>(args, b, c, dst, s); break;
-        case EW_MUL_ADD: launch_elementwise<EW_MUL_ADD>(args, b, c, dst, s); break;
-        default: launch_elementwise<EW_ADD_GELU>(args, b, c, dst, s); break;
+        case EW_GELU: launch_elementwise<EW_GELU>(args, b, c, d, dst, s); break;
+        case EW_GLU: launch_elementwise<EW_GLU>(args, b, c, d, dst, s); break;
+        case EW_ADD: launch_elementwise<EW_ADD>(args, b, c, d, dst, s); break;
+        case EW_MUL: launch_elementwise<EW_MUL>(args, b, c, d, dst, s); break;
+        case EW_MUL_ADD: launch_elementwise<EW_MUL_ADD>(args, b, c, d, dst, s); break;
+        case EW_ADD_GELU: launch_elementwise<EW_ADD_GELU>(args, b, c, d, dst, s); break;
+        default: launch_elementwise<EW_GLU_MUL_ADD>(args, b, c, d, dst, s); break;
     }
 }
 
@@ -862,7 +912,8 @@ Affine make_affine(const stx_tensor* t, const stx_tensor* x, const char* what) {
 }
 
 struct GnPlan {
-    long long cpg, groups, groups_total, chunks;
+    long long cpg, groups, groups_total, chunks_partial, chunks_apply;
+    size_t shift_off, part_off, bytes;                   // workspace layout
 };
 
 GnPlan gn_plan(const stx_tensor* a, int n_groups) {
@@ -870,8 +921,26 @@ GnPlan gn_plan(const stx_tensor* a, int n_groups) {
     p.cpg = std::max<long long>(1, (a->ne[2] + n_groups - 1) / n_groups);
     p.groups = (a->ne[2] + p.cpg - 1) / p.cpg;
     p.groups_total = p.groups * a->ne[3];
-    p.chunks = (p.cpg * a->ne[0] * a->ne[1] + kGnChunk - 1) / kGnChunk;
+    const long long span = p.cpg * a->ne[0] * a->ne[1];
+    p.chunks_partial = (span + gn_chunk<kGnVecPartial>() - 1) / gn_chunk<kGnVecPartial>();
+    p.chunks_apply = (span + gn_chunk<kGnVecApply>() - 1) / gn_chunk<kGnVecApply>();
+    const size_t g = (size_t)std::max<long long>(1, p.groups_total);
+    auto up = [](size_t v) { return (v + 255) / 256 * 256; };
+    p.shift_off = 0;
+    p.part_off = up(sizeof(double) * g);
+    p.bytes = p.part_off + up(sizeof(double) * 2 * g * (size_t)std::max<long long>(1, p.chunks_partial));
     return p;
+}
+
+template <int AK, bool GELU>
+void launch_group_norm(GroupNormArgs g, const GnPlan& p, hipStream_t s) {
+    g.chunks = (int)p.chunks_partial;
+    hipLaunchKernelGGL(gn_partial_kernel, dim3((unsigned)p.chunks_partial, (unsigned)p.groups_total), dim3(256), 0, s,
+                       g);
+    launch_check("gn_partial_kernel");
+    hipLaunchKernelGGL((gn_apply_kernel<AK, GELU>), dim3((unsigned)p.chunks_apply, (unsigned)p.groups_total),
+                       dim3(256), 0, s, g);
+    launch_check("gn_apply_kernel");
 }
 
 }  // namespace
@@ -928,7 +997,7 @@ STX_API stx_status stx_gelu_erf(const stx_tensor* a, const stx_tensor* dst, stx_
         check_tensor(a, "a");
         check_tensor(dst, "dst");
         check_same_shape(a, dst, "gelu_erf");
-        elementwise(EW_GELU, a, nullptr, nullptr, dst, stream);
+        elementwise(EW_GELU, a, nullptr, nullptr, nullptr, dst, stream);
     });
 }
 
@@ -940,7 +1009,7 @@ STX_API stx_status stx_add_gelu_erf(const stx_tensor* a, const stx_tensor* b, co
         check_tensor(dst, "dst");
         check_same_shape(a, dst, "add_gelu_erf");
         check_repeat(b, dst, "add_gelu_erf");
-        elementwise(EW_ADD_GELU, a, b, nullptr, dst, stream);
+        elementwise(EW_ADD_GELU, a, b, nullptr, nullptr, dst, stream);
     });
 }
 
@@ -956,7 +1025,7 @@ STX_API stx_status stx_glu(const stx_tensor* a, const stx_tensor* dst, int dim, 
         stx_tensor va = *a, vg = *a;
         va.ne[dim] = vg.ne[dim] = a->ne[dim] / 2;
         vg.data = static_cast<char*>(a->data) + a->nb[dim] * (a->ne[dim] / 2);
-        elementwise(EW_GLU, &va, &vg, nullptr, dst, stream);
+        elementwise(EW_GLU, &va, &vg, nullptr, nullptr, dst, stream);
     });
 }
 
@@ -967,7 +1036,7 @@ STX_API stx_status stx_add(const stx_tensor* a, const stx_tensor* b, const stx_t
         check_tensor(dst, "dst");
         check_same_shape(a, dst, "add");
         check_repeat(b, dst, "add");
-        elementwise(EW_ADD, a, b, nullptr, dst, stream);
+        elementwise(EW_ADD, a, b, nullptr, nullptr, dst, stream);
     });
 }
 
@@ -978,7 +1047,7 @@ STX_API stx_status stx_mul(const stx_tensor* a, const stx_tensor* b, const stx_t
         check_tensor(dst, "dst");
         check_same_shape(a, dst, "mul");
         check_repeat(b, dst, "mul");
-        elementwise(EW_MUL, a, b, nullptr, dst, stream);
+        elementwise(EW_MUL, a, b, nullptr, nullptr, dst, stream);
     });
 }
 
@@ -992,7 +1061,28 @@ STX_API stx_status stx_mul_add(const stx_tensor* x, const stx_tensor* h, const s
         check_same_shape(x, dst, "mul_add");
         check_repeat(h, dst, "mul_add");
         check_repeat(s, dst, "mul_add");
-        elementwise(EW_MUL_ADD, x, h, s, dst, stream);
+        elementwise(EW_MUL_ADD, x, h, s, nullptr, dst, stream);
+    });
+}
+
+STX_API stx_status stx_glu_mul_add(const stx_tensor* x, const stx_tensor* a, int dim, const stx_tensor* s,
+                                   const stx_tensor* dst, stx_stream stream) {
+    return guard([&] {
+        check_tensor(x, "x");
+        check_tensor(a, "a");
+        check_tensor(s, "s");
+        check_tensor(dst, "dst");
+        check_same_shape(x, dst, "glu_mul_add");
+        STX_REQUIRE(dim >= 0 && dim < 4, "glu_mul_add: dim must be 0..3");
+        STX_REQUIRE(a->ne[dim] % 2 == 0 && a->ne[dim] / 2 == dst->ne[dim],
+                    "glu_mul_add: a->ne[dim] must be 2 * dst->ne[dim]");
+        for (int i = 0; i < 4; i++)
+            if (i != dim) STX_REQUIRE(a->ne[i] == dst->ne[i], "glu_mul_add: shape mismatch in ne[%d]", i);
+        check_repeat(s, dst, "glu_mul_add");
+        stx_tensor va = *a, vg = *a;
+        va.ne[dim] = vg.ne[dim] = a->ne[dim] / 2;
+        vg.data = static_cast<char*>(a->data) + a->nb[dim] * (a->ne[dim] / 2);
+        elementwise(EW_GLU_MUL_ADD, x, &va, &vg, s, dst, stream);
     });
 }
 
@@ -1000,8 +1090,7 @@ STX_API size_t stx_group_norm_workspace_size(const stx_tensor* a, int n_groups) 
     if (!a || n_groups < 1) return 0;
     for (int i = 0; i < 4; i++)
         if (a->ne[i] < 0) return 0;
-    const GnPlan p = gn_plan(a, n_groups);
-    return sizeof(double) * 2 * (size_t)std::max<long long>(1, p.chunks * p.groups_total);
+    return gn_plan(a, n_groups).bytes;
 }
 
 STX_API stx_status stx_group_norm(const stx_tensor* a, const stx_tensor* dst, int n_groups, float eps,
@@ -1019,50 +1108,46 @@ STX_API stx_status stx_group_norm(const stx_tensor* a, const stx_tensor* dst, in
         if (nelem(ta) == 0) return;
         const GnPlan p = gn_plan(a, n_groups);
         STX_REQUIRE(p.groups_total < 65536, "group_norm: more than 65535 groups");
-        STX_REQUIRE(p.cpg * a->ne[0] * a->ne[1] < (1LL << 32) - kGnChunk,
+        STX_REQUIRE(p.cpg * a->ne[0] * a->ne[1] < (1LL << 32) - gn_chunk<16>(),
                     "group_norm: groups of 2^32 floats or more are not supported");
-        const size_t need = sizeof(double) * 2 * (size_t)(p.chunks * p.groups_total);
-        STX_REQUIRE(workspace != nullptr && workspace_bytes >= need, "group_norm: workspace too small (%zu, need %zu)",
-                    workspace_bytes, need);
+        STX_REQUIRE(workspace != nullptr && workspace_bytes >= p.bytes, "group_norm: workspace too small (%zu, need %zu)",
+                    workspace_bytes, p.bytes);
+        STX_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0, "group_norm: workspace must be 256-byte aligned");
         GroupNormArgs g{};
         g.x = reinterpret_cast<const float*>(ta.data);
         g.y = reinterpret_cast<float*>(td.data);
         g.w = w;
         g.b = b;
-        g.part = static_cast<double*>(workspace);
+        char* ws = static_cast<char*>(workspace);
+        g.shift = reinterpret_cast<double*>(ws + p.shift_off);
+        g.part = reinterpret_cast<double*>(ws + p.part_off);
         g.ne0 = (unsigned)ta.ne[0];
         g.ne1 = (unsigned)ta.ne[1];
         g.ne2 = ta.ne[2];
         g.plane = (unsigned)(ta.ne[0] * ta.ne[1]);
         g.cpg = p.cpg;
         g.groups = (int)p.groups;
-        g.chunks = (int)p.chunks;
         g.eps = eps;
-        g.gelu = gelu ? 1 : 0;
         // Every group span starts at (i3 * ne2 + g * cpg) * plane floats.
         g.vec = aligned16(ta.data) && aligned16(td.data) && (g.cpg * (long long)g.plane) % 4 == 0 &&
                         (ta.ne[3] == 1 || (g.ne2 * (long long)g.plane) % 4 == 0)
                     ? 1
                     : 0;
         const hipStream_t s = as_stream(stream);
-        hipLaunchKernelGGL(gn_partial_kernel, dim3((unsigned)p.chunks, (unsigned)p.groups_total), dim3(256), 0, s, g);
-        launch_check("gn_partial_kernel");
-        const dim3 agrid((unsigned)p.chunks, (unsigned)p.groups_total);
         auto fits = [&](int kind) {
             return (g.w.kind == AFF_NONE || g.w.kind == kind) && (g.b.kind == AFF_NONE || g.b.kind == kind);
         };
         const int ak = fits(AFF_CHANNEL) ? AFF_CHANNEL : fits(AFF_NE0) ? AFF_NE0 : AFF_GENERAL;
         if (ak == AFF_CHANNEL) {
-            if (g.gelu) hipLaunchKernelGGL((gn_apply_kernel<AFF_CHANNEL, true>), agrid, dim3(256), 0, s, g);
-            else hipLaunchKernelGGL((gn_apply_kernel<AFF_CHANNEL, false>), agrid, dim3(256), 0, s, g);
+            if (gelu) launch_group_norm<AFF_CHANNEL, true>(g, p, s);
+            else launch_group_norm<AFF_CHANNEL, false>(g, p, s);
         } else if (ak == AFF_NE0) {
-            if (g.gelu) hipLaunchKernelGGL((gn_apply_kernel<AFF_NE0, true>), agrid, dim3(256), 0, s, g);
-            else hipLaunchKernelGGL((gn_apply_kernel<AFF_NE0, false>), agrid, dim3(256), 0, s, g);
+            if (gelu) launch_group_norm<AFF_NE0, true>(g, p, s);
+            else launch_group_norm<AFF_NE0, false>(g, p, s);
         } else {
-            if (g.gelu) hipLaunchKernelGGL((gn_apply_kernel<AFF_GENERAL, true>), agrid, dim3(256), 0, s, g);
-            else hipLaunchKernelGGL((gn_apply_kernel<AFF_GENERAL, false>), agrid, dim3(256), 0, s, g);
+            if (gelu) launch_group_norm<AFF_GENERAL, true>(g, p, s);
+            else launch_group_norm<AFF_GENERAL, false>(g, p, s);
         }
-        launch_check("gn_apply_kernel");
     });
 }
 

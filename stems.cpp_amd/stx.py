@@ -75,6 +75,7 @@ _SIGNATURES = {
     "stx_add": (_i, [_vp, _vp, _vp, _vp]),
     "stx_mul": (_i, [_vp, _vp, _vp, _vp]),
     "stx_mul_add": (_i, [_vp, _vp, _vp, _vp, _vp]),
+    "stx_glu_mul_add": (_i, [_vp, _vp, _i, _vp, _vp, _vp]),
     "stx_rope_ext": (_i, [_vp, _vp, _vp, _i, _i, _i, ctypes.c_float, ctypes.c_float, ctypes.c_float,
                           ctypes.c_float, ctypes.c_float, ctypes.c_float, _vp]),
 }
@@ -246,9 +247,9 @@ def htdemucs_ispec(fft, spec, length, layout=F_MAJOR, out=None, stream=None, wor
 
 
 def workspace(nbytes, device):
-    """A device workspace tensor of at least nbytes."""
+    """A zero-filled device workspace tensor of at least nbytes."""
     import torch
-    return torch.empty(max(1, (int(nbytes) + 3) // 4), dtype=torch.float32, device=device)
+    return torch.zeros(max(1, (int(nbytes) + 3) // 4), dtype=torch.float32, device=device)
 
 
 # ------------------------------------------------------------------------------- bands
@@ -589,6 +590,13 @@ def mul_add(x, h, s, out=None, stream=None):
     """x + h * s (LayerScale + residual), rounded like ggml_add(x, ggml_mul(h, s))."""
     out = _out(out, x)
     check(lib().stx_mul_add(_t(x), _t(h), _t(s), _t(out), _stream(stream)))
+    return out
+
+
+def glu_mul_add(x, a, dim, s, out=None, stream=None):
+    """x + glu(a along ggml dimension dim) * s: GLU + LayerScale + residual in one kernel."""
+    out = _out(out, x)
+    check(lib().stx_glu_mul_add(_t(x), _t(a), int(dim), _t(s), _t(out), _stream(stream)))
     return out
 
 

@@ -95,6 +95,23 @@ def test_group_norm_in_place_and_deterministic(device, ops):
     assert rel_err(a, ops.group_norm(xh, 1)) <= TOL
 
 
+@pytest.mark.parametrize("gelu", [False, True])
+def test_group_norm_shapes_share_a_workspace(device, ops, gelu):
+    """Large groups, many groups and batched groups: one workspace, filled with garbage first,
+    serves all of them in turn, twice (no initialisation, no state kept between calls)."""
+    import torch
+    ws = torch.full((1 << 16,), -7.25, device=device)
+    shapes = [((96, 1, 85995), 1), ((1000, 1, 8192), 1000), ((48, 1, 85995), 1), ((8, 3, 1, 999), 4)]
+    for rep in range(2):
+        for shape, G in shapes:
+            x = randn(device, shape, shape[0] + rep, 1.5, 0.5)
+            C = shape[-3]
+            w, b = randn(device, (C, 1, 1), 1), randn(device, (C, 1, 1), 2)
+            assert stx.group_norm_workspace_size(x, G) <= ws.numel() * 4
+            y = host(stx.group_norm(x, G, 1e-5, w, b, gelu=gelu, workspace=ws))
+            assert rel_err(y, ops.group_norm(host(x), G, 1e-5, host(w), host(b), gelu=gelu)) <= TOL
+
+
 def test_group_norm_errors(device):
     import torch
     x = randn(device, (4, 1, 100), 10)
@@ -227,6 +244,26 @@ def test_layer_scale_residual_bit_exact(device, ops, C, T):
     s = randn(device, (C, 1, 1), 22, 1e-2)
     y = host(stx.mul_add(x, h, s))
     assert np.array_equal(y, ops.binary("mul_add", host(x), host(h), host(s)))
+
+
+@pytest.mark.parametrize("C,T", HTDEMUCS_CT)
+def test_glu_layer_scale_residual_fused_bit_exact(device, C, T):
+    """x + glu(h) * scale (src/htdemucs.cpp:137-139) in one kernel is bit-identical to the
+    GLU and the LayerScale + residual run separately (each checked against the oracle above)."""
+    h = randn(device, (2 * C, 1, T), C, 2.0)
+    x, s = randn(device, (C, 1, T), C + 1), randn(device, (C, 1, 1), C + 2, 0.1)
+    fused = host(stx.glu_mul_add(x, h, 2, s))
+    sep = host(stx.mul_add(x, stx.glu(h, 2), s))
+    assert np.array_equal(fused, sep)
+
+
+def test_glu_layer_scale_residual_dim0_and_errors(device):
+    h = randn(device, (801, 2 * 132), 5, 2.0)
+    x, s = randn(device, (801, 132), 6), randn(device, (132,), 7)
+    assert np.array_equal(host(stx.glu_mul_add(x, h, 0, s)), host(stx.mul_add(x, stx.glu(h, 0), s)))
+    with pytest.raises(stx.StxError) as e:
+        stx.glu_mul_add(x, randn(device, (801, 263), 1), 0, s)
+    assert e.value.status == stx.STATUS_INVALID_ARGUMENT
 
 
 @pytest.mark.parametrize("shape,bshape", [((60, 801, 1536), (1536,)), ((48, 1, 85995), (48, 1, 1)),
