@@ -45,26 +45,35 @@ __device__ __forceinline__ float padded_mix(const float* __restrict__ xc, int64_
     return xc[j];
 }
 
-// parts[k - first][c][t] for chunks first .. first + count - 1.
+// parts[k - first][c][t] for chunks first .. first + count - 1. Block (x, y, z) = (tile of
+// 1024 samples, channel, chunk - first); 4 consecutive samples per thread, no divisions.
 __global__ __launch_bounds__(256) void demix_chunks_kernel(DemixArgs a, const float* __restrict__ mix,
-                                                           int64_t first, int64_t count, float* __restrict__ parts) {
-    const int64_t total = count * a.channels * a.chunk;
-    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
-        const int t = (int)(e % a.chunk);
-        const int64_t kc = e / a.chunk;
-        const int c = (int)(kc % a.channels);
-        const int64_t k = first + kc / a.channels;
-        const int64_t i = k * a.step;
-        const int64_t length = min((int64_t)a.chunk, a.padded_len - i);
-        const float* xc = mix + (size_t)c * a.len;
-        float v = 0.f;
-        if (t < length) {
-            v = padded_mix(xc, i + t, a);
-        } else if (length > a.chunk / 2 + 1) {
-            // reflect_pad(src, length, 0, chunk - length) (src/roformer.cpp:325)
-            v = padded_mix(xc, i + 2 * (length - 1) - t, a);
-        }
-        parts[e] = v;
+                                                           int64_t first, int vec, float* __restrict__ parts) {
+    const int t0 = ((int)blockIdx.x * 256 + (int)threadIdx.x) * 4;
+    if (t0 >= a.chunk) return;
+    const int c = (int)blockIdx.y;
+    const int64_t k = first + (int64_t)blockIdx.z;
+    const int64_t i = k * a.step;
+    const int64_t length = min((int64_t)a.chunk, a.padded_len - i);
+    const bool reflect_tail = length > a.chunk / 2 + 1;
+    const float* xc = mix + (size_t)c * a.len;
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int t = t0 + j;
+        float x = 0.f;
+        if (t < length) x = padded_mix(xc, i + t, a);
+        else if (t < a.chunk && reflect_tail)                       // reflect_pad(src, length, 0, chunk - length)
+            x = padded_mix(xc, i + 2 * (length - 1) - t, a);        // (src/roformer.cpp:325)
+        v[j] = x;
+    }
+    float* dst = parts + ((size_t)blockIdx.z * a.channels + c) * a.chunk + t0;
+    if (vec && t0 + 3 < a.chunk) {
+        *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (t0 + j < a.chunk) dst[j] = v[j];
     }
 }
 
@@ -76,9 +85,80 @@ __device__ __forceinline__ float chunk_weight(const float* __restrict__ window, 
 }
 
 // out[s][c][t] = sum_k y[k][s][c][p - k*step] * w_k / sum_k w_k, p = off + t, chunks in order.
+// Each thread takes 4 consecutive samples: their chunk weights and weight sums are formed once
+// and reused for every (stem, channel) plane, then each plane sums its chunk outputs in chunk
+// order in double (float x float is exact in double), divides once and rounds once.
+constexpr int kOlaMaxChunks = 8;      // chunks covering 4 consecutive samples
+
 __global__ __launch_bounds__(256) void demix_ola_kernel(DemixArgs a, const float* __restrict__ y,
-                                                        const float* __restrict__ window, int n_stems,
+                                                        const float* __restrict__ window, int planes, int vec,
                                                         float* __restrict__ out) {
+#pragma clang fp contract(off)
+    const int64_t t0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (t0 >= a.len) return;
+    const int64_t p0 = (a.reflect_border ? a.border : 0) + t0;
+    const int64_t k_lo = p0 >= a.chunk ? (p0 - a.chunk) / a.step + 1 : 0;   // first chunk with p0 < k*step + chunk
+    const int64_t k_hi = (p0 + 3) / a.step;                                 // last chunk starting at or before p0 + 3
+    const int nk = (int)min((int64_t)kOlaMaxChunks, k_hi - k_lo + 1);
+    float w[kOlaMaxChunks][4];
+    double cnt[4] = {0.0, 0.0, 0.0, 0.0};
+    bool all4 = true;                                       // every (chunk, sample) of the span valid
+#pragma unroll
+    for (int kk = 0; kk < kOlaMaxChunks; kk++) {
+        const int64_t k = k_lo + kk;
+        const int64_t i = k * a.step;
+        const int64_t length = min((int64_t)a.chunk, a.padded_len - i);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int64_t tt = p0 + j - i;
+            const bool ok = kk < nk && t0 + j < a.len && tt >= 0 && tt < length;
+            w[kk][j] = ok ? chunk_weight(window, k, (int)tt, a) : 0.f;
+            if (ok) cnt[j] += (double)w[kk][j];
+            if (kk < nk && !ok) all4 = false;
+        }
+    }
+    const size_t stride = (size_t)planes * a.chunk;          // one chunk's output
+    for (int sc = 0; sc < planes; sc++) {
+        double res[4] = {0.0, 0.0, 0.0, 0.0};
+        for (int kk = 0; kk < nk; kk++) {
+            const int64_t k = k_lo + kk;
+            const float* src = y + (size_t)k * stride + (size_t)sc * a.chunk + (p0 - k * a.step);
+            if (vec && all4) {
+                const float4 q = *reinterpret_cast<const float4*>(src);
+                res[0] += (double)q.x * (double)w[kk][0];
+                res[1] += (double)q.y * (double)w[kk][1];
+                res[2] += (double)q.z * (double)w[kk][2];
+                res[3] += (double)q.w * (double)w[kk][3];
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int64_t tt = p0 + j - k * a.step;
+                    const int64_t length = min((int64_t)a.chunk, a.padded_len - k * a.step);
+                    if (t0 + j < a.len && tt >= 0 && tt < length) res[j] += (double)src[j] * (double)w[kk][j];
+                }
+            }
+        }
+        float o[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const double v = res[j] / cnt[j];
+            o[j] = isfinite(v) ? (float)v : 0.0f;                             // np.nan_to_num
+        }
+        float* dst = out + (size_t)sc * a.len + t0;
+        if (vec && t0 + 3 < a.len) {
+            *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (t0 + j < a.len) dst[j] = o[j];
+        }
+    }
+}
+
+// The same sum for any overlap: one thread per (sample, plane).
+__global__ __launch_bounds__(256) void demix_ola_generic_kernel(DemixArgs a, const float* __restrict__ y,
+                                                                const float* __restrict__ window, int n_stems,
+                                                                float* __restrict__ out) {
 #pragma clang fp contract(off)
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (t >= a.len) return;
@@ -208,10 +288,10 @@ STX_API stx_status stx_demix_chunks(const stx_demix* d, const float* mix, int64_
         STX_REQUIRE(first >= 0 && count >= 0 && first + count <= d->g.n_chunks, "chunk range out of the plan");
         if (count == 0) return;
         STX_REQUIRE(mix && parts, "NULL buffer");
-        const int64_t total = count * d->channels * d->g.chunk;
-        const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 1 << 20);
-        hipLaunchKernelGGL(demix_chunks_kernel, dim3(blocks), dim3(256), 0, as_stream(stream), args_of(d), mix, first,
-                           count, parts);
+        STX_REQUIRE(count < 65536 && d->channels < 65536, "too many chunks or channels in one call");
+        const int vec = d->g.chunk % 4 == 0 && (reinterpret_cast<uintptr_t>(parts) & 15) == 0;
+        const dim3 grid((unsigned)((d->g.chunk + 1023) / 1024), (unsigned)d->channels, (unsigned)count);
+        hipLaunchKernelGGL(demix_chunks_kernel, grid, dim3(256), 0, as_stream(stream), args_of(d), mix, first, vec, parts);
         launch_check("demix_chunks_kernel");
     });
 }
@@ -223,10 +303,22 @@ STX_API stx_status stx_demix_overlap_add(const stx_demix* d, const float* y, int
         STX_REQUIRE(n_stems >= 1, "bad stem count");
         STX_REQUIRE(y && out, "NULL buffer");
         STX_REQUIRE((int64_t)n_stems * d->channels < 65536, "too many stems * channels");
-        dim3 grid((unsigned)((d->g.len + 255) / 256), n_stems * d->channels);
-        hipLaunchKernelGGL(demix_ola_kernel, grid, dim3(256), 0, as_stream(stream), args_of(d), y, d->d_window,
-                           n_stems, out);
-        launch_check("demix_ola_kernel");
+        const int planes = n_stems * d->channels;
+        // Chunks covering 4 consecutive samples: at most ceil((chunk + 3) / step).
+        if ((d->g.chunk + 3 + (int64_t)d->g.step - 1) / d->g.step <= kOlaMaxChunks) {
+            const int64_t off = d->g.reflect_border ? d->g.border : 0;
+            const int vec = d->g.chunk % 4 == 0 && d->g.step % 4 == 0 && off % 4 == 0 && d->g.len % 4 == 0 &&
+                            (reinterpret_cast<uintptr_t>(y) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+            const unsigned blocks = (unsigned)((d->g.len + 1023) / 1024);
+            hipLaunchKernelGGL(demix_ola_kernel, dim3(blocks), dim3(256), 0, as_stream(stream), args_of(d), y,
+                               d->d_window, planes, vec, out);
+            launch_check("demix_ola_kernel");
+        } else {
+            dim3 grid((unsigned)((d->g.len + 255) / 256), planes);
+            hipLaunchKernelGGL(demix_ola_generic_kernel, grid, dim3(256), 0, as_stream(stream), args_of(d), y,
+                               d->d_window, n_stems, out);
+            launch_check("demix_ola_generic_kernel");
+        }
     });
 }
 

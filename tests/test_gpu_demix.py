@@ -49,8 +49,10 @@ def host(t):
     return t.cpu().numpy()
 
 
+# The last two cover 8 chunks over 4 samples (the limit of the 4-sample kernel) and 11 (the
+# kernel for any overlap).
 CASES = [(7938000, 352800, 88200), (1000, 100, 25), (1000, 100, 100), (150, 100, 25), (60, 100, 50),
-         (1001, 97, 31), (100000, 8000, 2000)]
+         (1001, 97, 31), (100000, 8000, 2000), (5003, 64, 9), (2000, 100, 10)]
 
 
 @pytest.mark.parametrize("length,chunk,step", CASES)
