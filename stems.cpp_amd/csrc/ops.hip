@@ -88,6 +88,7 @@ void check_repeat(const stx_tensor* b, const stx_tensor* dst, const char* what) 
                     (long long)dst->ne[i]);
 }
 
+
 // Row r (flattened over ne1, ne2, ne3) of t.
 __device__ __forceinline__ char* row_ptr(const T4& t, long long r) {
     const long long i1 = r % t.ne[1];
@@ -95,6 +96,27 @@ __device__ __forceinline__ char* row_ptr(const T4& t, long long r) {
     const long long i2 = q % t.ne[2];
     const long long i3 = q / t.ne[2];
     return t.data + i1 * t.nb[1] + i2 * t.nb[2] + i3 * t.nb[3];
+}
+
+// Row r of t when the rows are equally spaced `rs` bytes apart (rs > 0), else row_ptr.
+__device__ __forceinline__ char* row_ptr_flat(const T4& t, long long r, long long rs) {
+    return rs > 0 ? t.data + r * rs : row_ptr(t, r);
+}
+
+// Byte distance between consecutive rows if all rows of t are equally spaced, else 0: the
+// row dimensions of extent > 1 must form one chain (each stride = previous stride * extent).
+long long row_spacing(const T4& t) {
+    long long rs = 0, expect = 0;
+    for (int i = 1; i < 4; i++) {
+        if (t.ne[i] <= 1) continue;
+        if (rs == 0) {
+            rs = t.nb[i];
+        } else if (t.nb[i] != expect) {
+            return 0;
+        }
+        expect = t.nb[i] * t.ne[i];
+    }
+    return rs > 0 ? rs : 4 * t.ne[0];          // a single row: any positive spacing works
 }
 
 template <int LANES>
@@ -193,6 +215,8 @@ struct RowNormArgs {
     const float* beta;       // + beta[ne0] (may be NULL)
     float eps;
     int rms;                 // 1: x / sqrt(mean x^2 + eps); 0: (x - mean) / sqrt(var + eps)
+    long long rs_src, rs_dst; // row spacing in bytes when equally spaced, else 0
+    int vec_params;          // gamma and beta (where given) 16-byte aligned
 };
 
 __device__ __forceinline__ float norm_out(const RowNormArgs& a, float x, double mean, double scale, int i) {
@@ -274,6 +298,7 @@ __global__ __launch_bounds__(256) void row_norm_big_kernel(RowNormArgs a) {
 struct SoftmaxArgs {
     T4 src, dst;
     float scale;
+    long long rs_src, rs_dst; // row spacing in bytes when equally spaced, else 0
 };
 
 __device__ __forceinline__ float exp_split(double d) {
@@ -317,6 +342,162 @@ __global__ __launch_bounds__(256) void softmax_kernel(SoftmaxArgs a) {
             const int i = lane + k * LANES;
             if (i < n) y[i] = (float)((double)e[k] * inv);
         }
+    }
+}
+
+// ------------------------------------------------------- row ops with vector loads
+// The same row ops with 16-byte loads and stores: a row of n floats is split into a head up
+// to the first 16-byte boundary (0..3 floats), an aligned body of float4 and a tail (0..3
+// floats). LANES lanes share a row: lane l holds body float4 l, l + LANES, ... (coalesced),
+// lanes 0..2 also hold the head floats and lanes 4..6 the tail floats. Used when source and
+// destination rows have the same alignment (the host checks it), so stores split the same way.
+struct RowSplit {
+    int h, nb4, tl;
+};
+
+__device__ __forceinline__ RowSplit row_split(const float* x, int n) {
+    int h = (int)((4u - ((unsigned)(reinterpret_cast<uintptr_t>(x) >> 2) & 3u)) & 3u);
+    h = min(h, n);
+    const int nb4 = (n - h) >> 2;
+    return {h, nb4, n - h - 4 * nb4};
+}
+
+// Index of the head or tail float owned by `lane`, or -1.
+__device__ __forceinline__ int row_extra(const RowSplit& sp, int lane) {
+    if (lane < sp.h) return lane;
+    if (lane >= 4 && lane < 4 + sp.tl) return sp.h + 4 * sp.nb4 + (lane - 4);
+    return -1;
+}
+
+template <int LANES, int V4>
+__device__ __forceinline__ void row_load(const float* x, const RowSplit& sp, int lane, float (&v)[4 * V4], float& e,
+                                         int& ei) {
+    const float4* b = reinterpret_cast<const float4*>(x + sp.h);
+#pragma unroll
+    for (int k = 0; k < V4; k++) {
+        const int q = lane + LANES * k;
+        const float4 f = q < sp.nb4 ? b[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        v[4 * k] = f.x;
+        v[4 * k + 1] = f.y;
+        v[4 * k + 2] = f.z;
+        v[4 * k + 3] = f.w;
+    }
+    ei = row_extra(sp, lane);
+    e = ei >= 0 ? x[ei] : 0.f;
+}
+
+template <int LANES, int V4>
+__global__ __launch_bounds__(256) void row_norm_v4_kernel(RowNormArgs a) {
+    const int lane = (int)threadIdx.x % LANES;
+    const long long gid = ((long long)blockIdx.x * 256 + threadIdx.x) / LANES;
+    const long long stride = (long long)gridDim.x * (256 / LANES);
+    const long long rows = a.src.ne[1] * a.src.ne[2] * a.src.ne[3];
+    const int n = (int)a.src.ne[0];
+    for (long long r = gid; r < rows; r += stride) {
+        const float* x = reinterpret_cast<const float*>(row_ptr_flat(a.src, r, a.rs_src));
+        float* y = reinterpret_cast<float*>(row_ptr_flat(a.dst, r, a.rs_dst));
+        const RowSplit sp = row_split(x, n);
+        float v[4 * V4], e;
+        int ei;
+        row_load<LANES, V4>(x, sp, lane, v, e, ei);
+        double mean = 0.0;
+        if (!a.rms) {
+            double s = ei >= 0 ? (double)e : 0.0;
+#pragma unroll
+            for (int k = 0; k < 4 * V4; k++) s += (double)v[k];       // invalid slots hold 0
+            mean = group_sum<LANES>(s) / n;
+        }
+        double ss = 0.0;
+        if (ei >= 0) ss = ((double)e - mean) * ((double)e - mean);
+#pragma unroll
+        for (int k = 0; k < V4; k++) {
+            if (lane + LANES * k < sp.nb4) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const double d = (double)v[4 * k + j] - mean;
+                    ss += d * d;
+                }
+            }
+        }
+        ss = group_sum<LANES>(ss);
+        const double scale = 1.0 / sqrt(ss / n + (double)a.eps);
+        float4* yb = reinterpret_cast<float4*>(y + sp.h);
+        const bool pvec = a.vec_params && sp.h == 0;       // parameter float4 at i0 aligned
+#pragma unroll
+        for (int k = 0; k < V4; k++) {
+            const int q = lane + LANES * k;
+            if (q < sp.nb4) {
+                const int i0 = sp.h + 4 * q;
+                float o[4];
+                if (pvec) {
+                    const float4 g = a.gamma ? *reinterpret_cast<const float4*>(a.gamma + i0) : make_float4(1.f, 1.f, 1.f, 1.f);
+                    const float4 bb = a.beta ? *reinterpret_cast<const float4*>(a.beta + i0) : make_float4(0.f, 0.f, 0.f, 0.f);
+                    const float gg[4] = {g.x, g.y, g.z, g.w}, bq[4] = {bb.x, bb.y, bb.z, bb.w};
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        double t = ((double)v[4 * k + j] - mean) * scale;
+                        if (a.gamma) t *= (double)gg[j];
+                        if (a.beta) t += (double)bq[j];
+                        o[j] = (float)t;
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; j++) o[j] = norm_out(a, v[4 * k + j], mean, scale, i0 + j);
+                }
+                yb[q] = make_float4(o[0], o[1], o[2], o[3]);
+            }
+        }
+        if (ei >= 0) y[ei] = norm_out(a, e, mean, scale, ei);
+    }
+}
+
+template <int LANES, int V4>
+__global__ __launch_bounds__(256) void softmax_v4_kernel(SoftmaxArgs a) {
+    const int lane = (int)threadIdx.x % LANES;
+    const long long gid = ((long long)blockIdx.x * 256 + threadIdx.x) / LANES;
+    const long long stride = (long long)gridDim.x * (256 / LANES);
+    const long long rows = a.src.ne[1] * a.src.ne[2] * a.src.ne[3];
+    const int n = (int)a.src.ne[0];
+    const double sc = (double)a.scale;
+    const float sgn = a.scale < 0.f ? -1.f : 1.f;      // max of s*x is s*max(x) for s >= 0
+    for (long long r = gid; r < rows; r += stride) {
+        const float* x = reinterpret_cast<const float*>(row_ptr_flat(a.src, r, a.rs_src));
+        float* y = reinterpret_cast<float*>(row_ptr_flat(a.dst, r, a.rs_dst));
+        const RowSplit sp = row_split(x, n);
+        float v[4 * V4], e;
+        int ei;
+        row_load<LANES, V4>(x, sp, lane, v, e, ei);
+        float m = ei >= 0 ? sgn * e : -INFINITY;
+#pragma unroll
+        for (int k = 0; k < V4; k++)
+            if (lane + LANES * k < sp.nb4)
+#pragma unroll
+                for (int j = 0; j < 4; j++) m = fmaxf(m, sgn * v[4 * k + j]);
+        const double ms = (double)(sgn * group_max<LANES>(m)) * sc;
+        double sum = 0.0;
+#pragma unroll
+        for (int k = 0; k < V4; k++) {
+            const bool ok = lane + LANES * k < sp.nb4;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                v[4 * k + j] = ok ? exp_split((double)v[4 * k + j] * sc - ms) : 0.f;
+                sum += (double)v[4 * k + j];
+            }
+        }
+        if (ei >= 0) {
+            e = exp_split((double)e * sc - ms);
+            sum += (double)e;
+        }
+        const double inv = 1.0 / group_sum<LANES>(sum);
+        float4* yb = reinterpret_cast<float4*>(y + sp.h);
+#pragma unroll
+        for (int k = 0; k < V4; k++) {
+            const int q = lane + LANES * k;
+            if (q < sp.nb4)
+                yb[q] = make_float4((float)((double)v[4 * k] * inv), (float)((double)v[4 * k + 1] * inv),
+                                    (float)((double)v[4 * k + 2] * inv), (float)((double)v[4 * k + 3] * inv));
+        }
+        if (ei >= 0) y[ei] = (float)((double)e * inv);
     }
 }
 
@@ -770,6 +951,44 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
     }
 }
 
+// Mode 0 with rows of a multiple of 4 floats, 16-byte aligned: each thread moves one float4,
+// i.e. two adjacent pairs (or 4 copied floats past n_dims), with 32-bit index arithmetic.
+__global__ __launch_bounds__(256) void rope_v4_kernel(RopeArgs a) {
+    extern __shared__ double cs[];                       // [n_dims/2][2]
+    const int half = a.n_dims / 2;
+    const long long i2 = blockIdx.x;
+    const double p = (double)a.pos[i2];
+    for (int i = (int)threadIdx.x; i < half; i += 256) {
+        const double theta = a.freq_scale * p * pow(a.freq_base, -2.0 * i / a.n_dims);
+        double sn, cn;
+        sincos(theta, &sn, &cn);
+        cs[2 * i] = cn * a.attn_factor;
+        cs[2 * i + 1] = sn * a.attn_factor;
+    }
+    __syncthreads();
+    const int ne1 = (int)a.src.ne[1];
+    const int u4 = (int)(a.src.ne[0] >> 2), d4 = a.n_dims >> 2;
+    const int rows = ne1 * (int)a.src.ne[3];
+    const int r0 = (int)blockIdx.y * kRopeRows;
+    const int total = min(kRopeRows, rows - r0) * u4;
+    const char* xs = a.src.data + i2 * a.src.nb[2];
+    char* ys = a.dst.data + i2 * a.dst.nb[2];
+    for (int e = (int)threadIdx.x; e < total; e += 256) {
+        const int rr = e / u4, q = e - rr * u4;
+        const int r = r0 + rr, i1 = r % ne1, i3 = r / ne1;
+        const float4 v = reinterpret_cast<const float4*>(xs + i1 * a.src.nb[1] + i3 * a.src.nb[3])[q];
+        float4 o = v;
+        if (q < d4) {
+            const double c0 = cs[4 * q], s0 = cs[4 * q + 1], c1 = cs[4 * q + 2], s1 = cs[4 * q + 3];
+            o.x = (float)((double)v.x * c0 - (double)v.y * s0);
+            o.y = (float)((double)v.x * s0 + (double)v.y * c0);
+            o.z = (float)((double)v.z * c1 - (double)v.w * s1);
+            o.w = (float)((double)v.z * s1 + (double)v.w * c1);
+        }
+        reinterpret_cast<float4*>(ys + i1 * a.dst.nb[1] + i3 * a.dst.nb[3])[q] = o;
+    }
+}
+
 // ------------------------------------------------------------------------ dispatch
 // Calls f(LANES, VPL) with the smallest lanes-per-row that keeps at most 16 values per lane
 // (32 for rows of 1025..2048).
@@ -781,6 +1000,25 @@ void pick_row_shape(long long n, F&& f) {
     else if (n <= 512) f(integral_constant<int, 32>{}, integral_constant<int, 16>{});
     else if (n <= 1024) f(integral_constant<int, 64>{}, integral_constant<int, 16>{});
     else f(integral_constant<int, 64>{}, integral_constant<int, 32>{});
+}
+
+// Calls f(LANES, V4) for the vector-load row kernels: LANES * V4 float4 cover the row body.
+template <class F>
+void pick_v4_shape(long long n, F&& f) {
+    using std::integral_constant;
+    if (n <= 128) f(integral_constant<int, 8>{}, integral_constant<int, 4>{});
+    else if (n <= 256) f(integral_constant<int, 16>{}, integral_constant<int, 4>{});
+    else if (n <= 512) f(integral_constant<int, 32>{}, integral_constant<int, 4>{});
+    else if (n <= 1024) f(integral_constant<int, 64>{}, integral_constant<int, 4>{});
+    else f(integral_constant<int, 64>{}, integral_constant<int, 8>{});
+}
+
+// Source and destination rows start at the same offset modulo 16 bytes.
+bool same_row_alignment(const T4& s, const T4& d) {
+    if ((reinterpret_cast<uintptr_t>(s.data) & 15) != (reinterpret_cast<uintptr_t>(d.data) & 15)) return false;
+    for (int i = 1; i < 4; i++)
+        if (s.ne[i] > 1 && (s.nb[i] - d.nb[i]) % 16 != 0) return false;
+    return true;
 }
 
 constexpr long long kMaxRowShapeN = 2048;
@@ -795,12 +1033,21 @@ void row_norm(const stx_tensor* a, const stx_tensor* dst, const float* gamma, co
     check_tensor(a, "a");
     check_tensor(dst, "dst");
     check_same_shape(a, dst, rms ? "rms_norm" : "norm");
-    RowNormArgs args{view(a), view(dst), gamma, beta, eps, rms};
+    RowNormArgs args{view(a), view(dst), gamma, beta, eps, rms, 0, 0, 0};
+    args.rs_src = row_spacing(args.src);
+    args.rs_dst = row_spacing(args.dst);
+    args.vec_params = (!gamma || aligned16(gamma)) && (!beta || aligned16(beta)) ? 1 : 0;
     const long long rows = nrows(args.src), n = args.src.ne[0];
     if (rows == 0 || n == 0) return;
     STX_REQUIRE(n < (1LL << 31), "row too long");
     const hipStream_t s = as_stream(stream);
-    if (n <= kMaxRowShapeN) {
+    if (n <= kMaxRowShapeN && same_row_alignment(args.src, args.dst)) {
+        pick_v4_shape(n, [&](auto lanes, auto v4) {
+            constexpr int L = decltype(lanes)::value, V = decltype(v4)::value;
+            hipLaunchKernelGGL((row_norm_v4_kernel<L, V>), dim3(row_blocks(rows, L)), dim3(256), 0, s, args);
+        });
+        launch_check("row_norm_v4_kernel");
+    } else if (n <= kMaxRowShapeN) {
         pick_row_shape(n, [&](auto lanes, auto vpl) {
             constexpr int L = decltype(lanes)::value, V = decltype(vpl)::value;
             hipLaunchKernelGGL((row_norm_kernel<L, V>), dim3(row_blocks(rows, L)), dim3(256), 0, s, args);
@@ -979,16 +1226,26 @@ STX_API stx_status stx_soft_max_ext(const stx_tensor* a, const stx_tensor* mask,
         check_tensor(a, "a");
         check_tensor(dst, "dst");
         check_same_shape(a, dst, "soft_max_ext");
-        SoftmaxArgs args{view(a), view(dst), scale};
+        SoftmaxArgs args{view(a), view(dst), scale, 0, 0};
+        args.rs_src = row_spacing(args.src);
+        args.rs_dst = row_spacing(args.dst);
         const long long rows = nrows(args.src), n = args.src.ne[0];
         if (rows == 0 || n == 0) return;
         if (n > kMaxRowShapeN) fail(STX_STATUS_UNSUPPORTED, "soft_max_ext: rows longer than 2048 are not supported");
         const hipStream_t s = as_stream(stream);
-        pick_row_shape(n, [&](auto lanes, auto vpl) {
-            constexpr int L = decltype(lanes)::value, V = decltype(vpl)::value;
-            hipLaunchKernelGGL((softmax_kernel<L, V>), dim3(row_blocks(rows, L)), dim3(256), 0, s, args);
-        });
-        launch_check("softmax_kernel");
+        if (same_row_alignment(args.src, args.dst)) {
+            pick_v4_shape(n, [&](auto lanes, auto v4) {
+                constexpr int L = decltype(lanes)::value, V = decltype(v4)::value;
+                hipLaunchKernelGGL((softmax_v4_kernel<L, V>), dim3(row_blocks(rows, L)), dim3(256), 0, s, args);
+            });
+            launch_check("softmax_v4_kernel");
+        } else {
+            pick_row_shape(n, [&](auto lanes, auto vpl) {
+                constexpr int L = decltype(lanes)::value, V = decltype(vpl)::value;
+                hipLaunchKernelGGL((softmax_kernel<L, V>), dim3(row_blocks(rows, L)), dim3(256), 0, s, args);
+            });
+            launch_check("softmax_kernel");
+        }
     });
 }
 
@@ -1175,9 +1432,18 @@ STX_API stx_status stx_rope_ext(const stx_tensor* a, const int32_t* pos, const s
                    (double)attn_factor};
         const long long row_tiles = (ta.ne[1] * ta.ne[3] + kRopeRows - 1) / kRopeRows;
         STX_REQUIRE(row_tiles < 65536, "rope_ext: too many rows per position");
-        hipLaunchKernelGGL(rope_kernel, dim3((unsigned)ta.ne[2], (unsigned)row_tiles), dim3(256),
-                           sizeof(double) * n_dims, as_stream(stream), r);
-        launch_check("rope_kernel");
+        bool v4 = mode == 0 && ta.ne[0] % 4 == 0 && n_dims % 4 == 0 && aligned16(ta.data) && aligned16(td.data) &&
+                  ta.ne[1] * ta.ne[3] < (1LL << 31);
+        for (int i = 1; i < 4; i++) v4 = v4 && ta.nb[i] % 16 == 0 && td.nb[i] % 16 == 0;
+        if (v4) {
+            hipLaunchKernelGGL(rope_v4_kernel, dim3((unsigned)ta.ne[2], (unsigned)row_tiles), dim3(256),
+                               sizeof(double) * n_dims, as_stream(stream), r);
+            launch_check("rope_v4_kernel");
+        } else {
+            hipLaunchKernelGGL(rope_kernel, dim3((unsigned)ta.ne[2], (unsigned)row_tiles), dim3(256),
+                               sizeof(double) * n_dims, as_stream(stream), r);
+            launch_check("rope_kernel");
+        }
     });
 }
 

@@ -168,6 +168,20 @@ def test_norm_strided_rows_in_place(device, ops):
     assert rel_err(host(v), want) <= TOL
 
 
+def test_row_ops_output_misaligned_with_input(device, ops):
+    """Rows whose output starts at a different offset modulo 16 bytes than the input take the
+    scalar-load kernels; rows with any head/tail split take the vector-load ones (801 floats)."""
+    import torch
+    rows, n = 300, 801
+    x = randn(device, (rows, n), 31, 2.0)
+    buf = torch.empty(rows * n + 1, device=device)
+    out = buf[1:].view(rows, n)                      # 4 bytes off the input's alignment
+    xh = host(x)
+    assert rel_err(host(stx.rms_norm(x, 1e-24, out=out)), ops.norm(xh, 1e-24, rms=True)) <= TOL
+    assert rel_err(host(stx.soft_max_ext(x, 0.125, out=out)), ops.soft_max(xh, 0.125)) <= TOL
+    assert rel_err(host(stx.norm(x, 1e-5, out=out)), ops.norm(xh, 1e-5)) <= TOL
+
+
 # ------------------------------------------------------------------------ SOFT_MAX
 @pytest.mark.parametrize("shape,sigma", [((13, 8, 801, 801), 8.0), ((801, 8, 60, 60), 8.0), ((4, 8, 801, 801), 60.0),
                                          ((3, 1000), 1.0), ((2, 2048), 4.0), ((17, 1), 1.0)])
@@ -311,6 +325,17 @@ def test_rope_neox_partial_dims_in_place(device, ops):
     want0 = ops.rope(xh, posh, 32)
     stx.rope_ext(x, pos, 32, out=x)
     assert rel_err(host(x), want0) <= TOL
+
+
+def test_rope_mode0_rows_not_multiple_of_4(device, ops):
+    """ne0 = 50 (not a multiple of 4 floats) takes the pair-per-thread kernel, 64 the float4 one;
+    both against the oracle."""
+    import torch
+    for ne0, nd in [(50, 46), (64, 64), (52, 40)]:
+        x = randn(device, (2, 33, 4, ne0), ne0)
+        posh = np.arange(33, dtype=np.int32) * 5
+        y = host(stx.rope_ext(x, torch.from_numpy(posh).to(device), nd))
+        assert rel_err(y, ops.rope(host(x), posh, nd)) <= TOL
 
 
 def test_rope_errors(device):
