@@ -585,23 +585,37 @@ enum FlatMode { FLAT_NONE = 0, FLAT_SAME = 1, FLAT_ROW4 = 2, FLAT_SPLAT = 3, FLA
 struct Flat {
     const float* p;
     unsigned div, mod;
+    double rdiv, rmod;   // 1/div, 1/mod
     int mode;        // SAME: float4 at i; ROW4: float4 at i % mod (div 1, mod % 4 == 0);
                      // SPLAT: one value for all four (div % 4 == 0); GENERAL: per element
 };
 
+// i / d for i < 2^32 from the double reciprocal (error < 1) and one correction step: a few
+// instructions instead of an integer division.
+__device__ __forceinline__ unsigned fast_div(unsigned i, unsigned d, double rd) {
+    unsigned q = (unsigned)((double)i * rd);
+    const long long r = (long long)i - (long long)q * d;
+    if (r < 0) q--;
+    else if (r >= (long long)d) q++;
+    return q;
+}
+
+__device__ __forceinline__ unsigned fast_mod(unsigned i, unsigned d, double rd) { return i - fast_div(i, d, rd) * d; }
+
 __device__ __forceinline__ void flat_load(const Flat& f, unsigned i, float (&v)[4]) {
     if (f.mode == FLAT_SAME || f.mode == FLAT_ROW4) {
-        const float4 q = *reinterpret_cast<const float4*>(f.p + (f.mode == FLAT_SAME ? i : i % f.mod));
+        const float4 q =
+            *reinterpret_cast<const float4*>(f.p + (f.mode == FLAT_SAME ? i : fast_mod(i, f.mod, f.rmod)));
         v[0] = q.x;
         v[1] = q.y;
         v[2] = q.z;
         v[3] = q.w;
     } else if (f.mode == FLAT_SPLAT) {
-        v[0] = v[1] = v[2] = v[3] = f.p[(i / f.div) % f.mod];
+        v[0] = v[1] = v[2] = v[3] = f.p[fast_mod(fast_div(i, f.div, f.rdiv), f.mod, f.rmod)];
     } else if (f.mode == FLAT_GENERAL) {
-        unsigned q = i / f.div;
+        unsigned q = fast_div(i, f.div, f.rdiv);
         unsigned r = i - q * f.div;
-        q %= f.mod;
+        q = fast_mod(q, f.mod, f.rmod);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             v[j] = f.p[q];
@@ -617,7 +631,7 @@ __device__ __forceinline__ void flat_load(const Flat& f, unsigned i, float (&v)[
 
 __device__ __forceinline__ float flat_at(const Flat& f, unsigned i) {
     if (f.mode == FLAT_NONE) return 0.f;
-    return f.mode == FLAT_SAME ? f.p[i] : f.p[(i / f.div) % f.mod];
+    return f.mode == FLAT_SAME ? f.p[i] : f.p[fast_mod(fast_div(i, f.div, f.rdiv), f.mod, f.rmod)];
 }
 
 template <int OP>
@@ -628,16 +642,17 @@ __global__ __launch_bounds__(256) void ew_flat_kernel(const float* __restrict__ 
     for (unsigned k = blockIdx.x * 256 + threadIdx.x; k < n4; k += stride) {
         const unsigned i = 4 * k;
         const float4 p = *reinterpret_cast<const float4*>(xa + i);
-        float vb[4], vc[4], vd[4];
-        flat_load(b, i, vb);
-        flat_load(c, i, vc);
-        flat_load(d, i, vd);
+        float vb[4] = {0.f, 0.f, 0.f, 0.f}, vc[4] = {0.f, 0.f, 0.f, 0.f}, vd[4] = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (has_b<OP>()) flat_load(b, i, vb);
+        if constexpr (has_c<OP>()) flat_load(c, i, vc);
+        if constexpr (has_d<OP>()) flat_load(d, i, vd);
         *reinterpret_cast<float4*>(y + i) =
             make_float4(ew_apply<OP>(p.x, vb[0], vc[0], vd[0]), ew_apply<OP>(p.y, vb[1], vc[1], vd[1]),
                         ew_apply<OP>(p.z, vb[2], vc[2], vd[2]), ew_apply<OP>(p.w, vb[3], vc[3], vd[3]));
     }
     for (unsigned i = 4 * n4 + blockIdx.x * 256 + threadIdx.x; i < n; i += stride)
-        y[i] = ew_apply<OP>(xa[i], flat_at(b, i), flat_at(c, i), flat_at(d, i));
+        y[i] = ew_apply<OP>(xa[i], has_b<OP>() ? flat_at(b, i) : 0.f, has_c<OP>() ? flat_at(c, i) : 0.f,
+                            has_d<OP>() ? flat_at(d, i) : 0.f);
 }
 
 // ----------------------------------------------------------------------- GROUP_NORM
@@ -681,6 +696,7 @@ struct GroupNormArgs {
     unsigned ne0, ne1;       // dims of x (ne3 is folded into the group index)
     long long ne2;
     unsigned plane;          // ne0 * ne1
+    double rplane, rne0;     // 1/plane, 1/ne0
     long long cpg;           // channels per group
     int groups;              // groups per ne3 slice
     int chunks;              // partial chunks per group (max over groups)
@@ -795,11 +811,11 @@ __device__ __forceinline__ void gn_affine(const GroupNormArgs& a, unsigned lo, l
         long long c = 0;
         unsigned i0 = 0, i1 = 0;
         if constexpr (AK == AFF_NE0) {
-            i0 = p % a.ne0;
+            i0 = fast_mod(p, a.ne0, a.rne0);
         } else {
-            const unsigned cp = p / a.plane, q = p - cp * a.plane;
+            const unsigned cp = fast_div(p, a.plane, a.rplane), q = p - cp * a.plane;
             c = c0 + cp;
-            i1 = q / a.ne0;
+            i1 = fast_div(q, a.ne0, a.rne0);
             i0 = q - i1 * a.ne0;
         }
 #pragma unroll
@@ -1089,6 +1105,8 @@ bool flat_operand(const stx_tensor* t, const stx_tensor* dst, Flat& f) {
     }
     f.div = (unsigned)div;
     f.mod = (unsigned)mod;
+    f.rdiv = 1.0 / (double)div;
+    f.rmod = 1.0 / (double)mod;
     if (div == 1 && mod % 4 == 0 && aligned16(v.data)) f.mode = FLAT_ROW4;
     else if (div % 4 == 0) f.mode = FLAT_SPLAT;
     else f.mode = FLAT_GENERAL;
@@ -1382,6 +1400,8 @@ STX_API stx_status stx_group_norm(const stx_tensor* a, const stx_tensor* dst, in
         g.ne1 = (unsigned)ta.ne[1];
         g.ne2 = ta.ne[2];
         g.plane = (unsigned)(ta.ne[0] * ta.ne[1]);
+        g.rplane = 1.0 / (double)g.plane;
+        g.rne0 = 1.0 / (double)g.ne0;
         g.cpg = p.cpg;
         g.groups = (int)p.groups;
         g.eps = eps;
