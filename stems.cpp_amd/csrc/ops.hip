@@ -906,7 +906,7 @@ __global__ __launch_bounds__(256) void gn_apply_kernel(GroupNormArgs a) {
 // (ne2 index) and kRopeRows of its (ne1, ne3) rows; it evaluates cos/sin in double once per
 // pair into LDS and rotates in double, rounding once. A thread owns a whole pair (or one
 // copied element), so dst may alias src.
-constexpr int kRopeRows = 32;
+constexpr int kRopeRows = 128;
 
 struct RopeArgs {
     T4 src, dst;
@@ -1018,15 +1018,26 @@ void pick_row_shape(long long n, F&& f) {
     else f(integral_constant<int, 64>{}, integral_constant<int, 32>{});
 }
 
-// Calls f(LANES, V4) for the vector-load row kernels: LANES * V4 float4 cover the row body.
+// Calls f(LANES, V4) for the vector-load row kernels: the smallest LANES (8..64) whose V4 =
+// ceil(ceil(n/4) / LANES) float4 per lane is at most 4 (8 for rows of 1025..2048), so that the
+// LANES * V4 slots cover the row body with as few idle slots as possible.
 template <class F>
 void pick_v4_shape(long long n, F&& f) {
     using std::integral_constant;
-    if (n <= 128) f(integral_constant<int, 8>{}, integral_constant<int, 4>{});
-    else if (n <= 256) f(integral_constant<int, 16>{}, integral_constant<int, 4>{});
-    else if (n <= 512) f(integral_constant<int, 32>{}, integral_constant<int, 4>{});
-    else if (n <= 1024) f(integral_constant<int, 64>{}, integral_constant<int, 4>{});
-    else f(integral_constant<int, 64>{}, integral_constant<int, 8>{});
+    const long long q = (n + 3) / 4;
+    auto with_lanes = [&](auto lanes) {
+        constexpr int L = decltype(lanes)::value;
+        const long long v = (q + L - 1) / L;
+        if (v <= 1) f(lanes, integral_constant<int, 1>{});
+        else if (v == 2) f(lanes, integral_constant<int, 2>{});
+        else if (v == 3) f(lanes, integral_constant<int, 3>{});
+        else if (v == 4) f(lanes, integral_constant<int, 4>{});
+        else f(lanes, integral_constant<int, 8>{});
+    };
+    if (q <= 32) with_lanes(integral_constant<int, 8>{});
+    else if (q <= 64) with_lanes(integral_constant<int, 16>{});
+    else if (q <= 128) with_lanes(integral_constant<int, 32>{});
+    else with_lanes(integral_constant<int, 64>{});
 }
 
 // Source and destination rows start at the same offset modulo 16 bytes.
