@@ -438,7 +438,34 @@ def run_rows(torch, stx, dev):
         z, y = torch.randn((C, T, F), dtype=torch.complex64, device=dev), torch.empty((C, hop * (T - 1)), device=dev)
         return lambda: stx.torch_istft(fft, z, hop, layout=stx.T_MAJOR, out=y, stream=stream)
     out["c3_istft_t_major"] = time_call(torch, stream, mk_istft, C * L * 4 + C * T * F * 8)
+
+    def mk_istft_ws():
+        z, y = torch.randn((C, T, F), dtype=torch.complex64, device=dev), torch.empty((C, hop * (T - 1)), device=dev)
+        ws = stx.workspace(stx.istft_workspace_size(fft, C, T), dev)
+        return lambda: stx.torch_istft(fft, z, hop, layout=stx.T_MAJOR, out=y, stream=stream, workspace=ws)
+    out["c3_istft_t_major_ws"] = time_call(torch, stream, mk_istft_ws, C * L * 4 + C * T * F * 8)
     del bands, fft
+
+    # c1: HTDemucs spectrogram of one stereo segment (343,980 samples, n_fft 4096, hop 1024).
+    n1, L1 = 4096, 343980
+    fft1 = stx.FFT(n1)
+    T1, F1 = stx.htdemucs_frames(n1, L1), n1 // 2
+    c1_bytes = C * L1 * 4 + C * T1 * F1 * 8
+
+    def mk_spec1():
+        x, y = rn(C, L1), torch.empty((C, F1, T1), dtype=torch.complex64, device=dev)
+        return lambda: stx.htdemucs_spec(fft1, x, out=y, stream=stream)
+    out["c1_htdemucs_spec"] = time_call(torch, stream, mk_spec1, c1_bytes)
+
+    def mk_ispec1(with_ws):
+        def mk():
+            z, y = torch.randn((C, F1, T1), dtype=torch.complex64, device=dev), torch.empty((C, L1), device=dev)
+            ws = stx.workspace(stx.istft_workspace_size(fft1, C, T1), dev) if with_ws else None
+            return lambda: stx.htdemucs_ispec(fft1, z, L1, out=y, stream=stream, workspace=ws)
+        return mk
+    out["c1_htdemucs_ispec"] = time_call(torch, stream, mk_ispec1(False), c1_bytes)
+    out["c1_htdemucs_ispec_ws"] = time_call(torch, stream, mk_ispec1(True), c1_bytes)
+    del fft1
 
     # c4: RoFormer transformer ops (dim 384, 8 heads x 64, 60 bands x 801 frames).
     def mk_rms():

@@ -130,10 +130,24 @@ __device__ __forceinline__ float2 tw_lookup(const float2* __restrict__ twt, int 
     return cmul(twt[m & (T::L - 1)], twt[T::L + (m >> T::LBITS)]);
 }
 
-// Copies the table to LDS; the caller's next barrier publishes it.
-template <int TN>
-__device__ __forceinline__ void stage_twiddles(float2* twt, const float2* __restrict__ g, int tid, int nt) {
-    for (int i = tid; i < TwTable<TN>::SIZE; i += nt) twt[i] = g[i];
+// Copies COUNT elements to LDS with NT threads, every load issued before the first LDS write
+// (a loop with a thread-dependent trip count would wait for each load in turn). The caller's
+// next barrier publishes the copy.
+template <int COUNT, int NT, class T>
+__device__ __forceinline__ void stage_lds(T* dst, const T* __restrict__ src, int tid) {
+    constexpr int R = (COUNT + NT - 1) / NT;
+    T v[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) v[r] = src[min(tid + r * NT, COUNT - 1)];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+        if (tid + r * NT < COUNT) dst[tid + r * NT] = v[r];
+}
+
+// Copies the twiddle table to LDS; the caller's next barrier publishes it.
+template <int TN, int NT>
+__device__ __forceinline__ void stage_twiddles(float2* twt, const float2* __restrict__ g, int tid) {
+    stage_lds<TwTable<TN>::SIZE, NT>(twt, g, tid);
 }
 
 // Shape of an M-point transform with P points per thread.

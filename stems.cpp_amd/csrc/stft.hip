@@ -67,13 +67,13 @@ __device__ __forceinline__ int reflect(int j, int n) {
     return j;
 }
 
-// Sample m of the fully padded signal (center pad N/2 around the pre-padded one).
+// Signal index of sample m of the fully padded signal (center pad N/2 around the pre-padded
+// one).
 template <int N>
-__device__ __forceinline__ float padded_sample(const float* __restrict__ xc, int m, const StftArgs& a) {
+__device__ __forceinline__ int padded_index(int m, const StftArgs& a) {
     int j = reflect(m - N / 2, a.len1) - a.pre_left;
     j = reflect(j, a.len);
-    j = min(max(j, 0), a.len - 1);   // host validation keeps j in range; this only guards memory
-    return xc[j];
+    return min(max(j, 0), a.len - 1);   // host validation keeps j in range; this only guards memory
 }
 
 // One workgroup transforms JOBS consecutive frames (one per N/2/P threads), then writes them so
@@ -105,24 +105,24 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void stft_kernel(StftArgs a) {
     const bool interior = base >= 0 && base + N <= a.len;
     const float2* win2 = reinterpret_cast<const float2*>(a.win);
 
-    float2 v[P];
+    // Signal indexes first, then every load without a branch between them (an inactive job
+    // reads frame 0 of channel 0, always in range; its slot is transformed but never written).
+    int ix[2 * P];
 #pragma unroll
     for (int r = 0; r < P; r++) {
         const int n = j + r * TPJ;
-        const float2 w = win2[n];
-        float s0 = 0.f, s1 = 0.f;
-        if (active) {
-            if (interior) {
-                s0 = xc[base + 2 * n];
-                s1 = xc[base + 2 * n + 1];
-            } else {
-                s0 = padded_sample<N>(xc, m0 + 2 * n, a);
-                s1 = padded_sample<N>(xc, m0 + 2 * n + 1, a);
-            }
-        }
-        v[r] = make_float2(s0 * w.x, s1 * w.y);
+        ix[2 * r] = interior ? base + 2 * n : padded_index<N>(m0 + 2 * n, a);
+        ix[2 * r + 1] = interior ? base + 2 * n + 1 : padded_index<N>(m0 + 2 * n + 1, a);
     }
-    stage_twiddles<N>(twt, a.twt, tid, NT);
+    float2 v[P];
+#pragma unroll
+    for (int r = 0; r < P; r++) v[r] = make_float2(xc[ix[2 * r]], xc[ix[2 * r + 1]]);
+    float2 w[P];
+#pragma unroll
+    for (int r = 0; r < P; r++) w[r] = win2[j + r * TPJ];
+#pragma unroll
+    for (int r = 0; r < P; r++) v[r] = make_float2(v[r].x * w[r].x, v[r].y * w[r].y);
+    stage_twiddles<N, NT>(twt, a.twt, tid);
     fft_first_pass<M, P, N>(v, buf, j, NoPost{}, ToLds<P>{buf});
     __syncthreads();
     fft_rest_passes<M, P, N, P>(buf, j, twt, NoPost{}, ToLds<P>{buf});
@@ -233,16 +233,23 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_frames_kernel(IstftA
     const int st = active ? f - c * a.T : 0;
     const float2* sc = a.spec + (size_t)c * a.T * a.F;
 
+    // Unconditional loads (an inactive job reads frame 0, a missing Nyquist bin bin F - 1),
+    // zeroed afterwards, so that no branch separates them.
     float2 xk[P], xm[P];
 #pragma unroll
     for (int r = 0; r < P; r++) {
         const int k = j + r * TPJ;
-        xk[r] = active ? spec_bin(a, sc, st, k) : make_float2(0.f, 0.f);
-        const int km = M - k;
-        xm[r] = (active && (km < M || a.keep_nyquist)) ? spec_bin(a, sc, st, km) : make_float2(0.f, 0.f);
+        xk[r] = spec_bin(a, sc, st, k);
+        xm[r] = spec_bin(a, sc, st, min(M - k, a.F - 1));
     }
-    stage_twiddles<N>(twt, a.twt, tid, NT);
-    for (int i = tid; i < N; i += NT) wl[i] = a.win[i];
+#pragma unroll
+    for (int r = 0; r < P; r++) {
+        const int km = M - (j + r * TPJ);
+        if (!active) xk[r] = make_float2(0.f, 0.f);
+        if (!active || (km == M && !a.keep_nyquist)) xm[r] = make_float2(0.f, 0.f);
+    }
+    stage_twiddles<N, NT>(twt, a.twt, tid);
+    stage_lds<N, NT>(wl, a.win, tid);
     __syncthreads();
     float2 v[P];
 #pragma unroll
@@ -309,9 +316,9 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
     float2* buf = lds + slot * C::PADN;
     const int hop = a.hop;
 
-    stage_twiddles<N>(twt, a.twt, tid, NT);
+    stage_twiddles<N, NT>(twt, a.twt, tid);
     if constexpr (WIN_LDS)
-        for (int i = tid; i < N; i += NT) wl[i] = a.win[i];
+        stage_lds<N, NT>(wl, a.win, tid);
     const float* win = WIN_LDS ? wl : a.win;
 
     const int J0 = max(a.out_off, a.tile_origin + tile * a.tile_len);
@@ -322,28 +329,66 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
     const float2* sc = a.spec + (size_t)c * a.T * a.F;
     const WindowPost post{reinterpret_cast<const float2*>(win), a.norm};
 
+    // Samples J = J0 + q*NT + tid (q < PER). With J = A*hop + R (0 <= R < hop), the frames
+    // covering J are tf = A - K .. A at positions s = R + K*hop .. R, where K = K0 when
+    // R <= rK and K0 - 1 otherwise (K0 = (N-1)/hop, rK = N-1 - K0*hop). One division per
+    // walk; A and R then advance by NT = dA*hop + dR per q. The walk is redone after each
+    // round's transform rather than held in registers across it.
+    const int K0 = (N - 1) / hop, rK = N - 1 - K0 * hop;
+    const int dA = NT / hop, dR = NT - dA * hop;
+    auto walk = [&](int lane, auto&& body) {
+        int A = (J0 + lane) / hop, R = J0 + lane - A * hop;
+#pragma unroll
+        for (int q = 0; q < PER; q++) {
+            const int K = R <= rK ? K0 : K0 - 1;
+            body(q, A - K, R + K * hop, K);    // first covering envelope frame, its position, K
+            R += dR;
+            A += dA;
+            if (R >= hop) { R -= hop; A++; }
+        }
+    };
     float acc[PER];
 #pragma unroll
     for (int q = 0; q < PER; q++) acc[q] = 0.f;
+    const float* ldsf = reinterpret_cast<const float*>(lds);
 
     for (int s0 = st_lo; s0 <= st_hi; s0 += JOBS) {
         // An opaque copy of the lane index: keeps the compiler from hoisting the (round
-        // invariant) twiddle reads out of this loop, which would hold them in registers.
-        int jr = j;
-        asm volatile("" : "+v"(jr));
-        // Stage X[0..M] of frame s0 + g into slot g, neighbouring lanes on neighbouring
-        // addresses in either layout.
-        auto stage = [&](int k, int g) {
-            const int st = s0 + g;
-            float2 val = make_float2(0.f, 0.f);
-            if (st <= st_hi && k < a.F) val = spec_bin(a, sc, st, k);
-            lds[g * C::PADN + k] = val;
-        };
+        // invariant) twiddle reads, staging addresses and sample walk out of this loop, which
+        // would hold them in registers across the transform.
+        int jr = j, tr = tid;
+        asm volatile("" : "+v"(jr), "+v"(tr));
+        __builtin_assume(jr >= 0 && jr < TPJ && tr >= 0 && tr < NT);
+        // Stage X[0..M] of frames s0 .. s0 + JOBS - 1 into the slots, neighbouring lanes on
+        // neighbouring addresses in either layout: bins k < M are P per thread
+        // (M * JOBS = P * NT), the Nyquist bins one each for the first JOBS threads. Every
+        // load of the round is issued before the first LDS write; frames past st_hi read
+        // frame st_hi and are zeroed afterwards.
+        float2 sv[P];
         if (a.layout == STX_SPEC_F_MAJOR) {
-            for (int e = tid; e < (M + 1) * JOBS; e += NT) stage(e / JOBS, e % JOBS);
+            // Element e = tr + i*NT: slot e % JOBS = tr % JOBS, bin e / JOBS = tr / JOBS + i*TPJ.
+            const int g = tr % JOBS, k0 = tr / JOBS;
+            const float2* col = sc + min(s0 + g, st_hi);
+#pragma unroll
+            for (int i = 0; i < P; i++) sv[i] = col[(size_t)(k0 + i * TPJ) * a.T];
+            const float2 nyq = sc[(size_t)min(M, a.F - 1) * a.T + min(s0 + min(tr, JOBS - 1), st_hi)];
+            const bool live = s0 + g <= st_hi;
+#pragma unroll
+            for (int i = 0; i < P; i++) lds[g * C::PADN + k0 + i * TPJ] = live ? sv[i] : make_float2(0.f, 0.f);
+            if (tr < JOBS)
+                lds[tr * C::PADN + M] = (s0 + tr <= st_hi && M < a.F) ? nyq : make_float2(0.f, 0.f);
         } else {
-            for (int g = 0; g < JOBS; g++)
-                for (int k = tid; k <= M; k += NT) stage(k, g);
+            // Element e = tr + i*NT: slot e / M, bin e % M.
+            auto slot_of = [&](int i) { return NT >= M ? tr / M + i * (NT / M) : i / (M / NT); };
+            auto bin_of = [&](int i) { return NT >= M ? tr % M : tr + (i % (M / NT)) * NT; };
+#pragma unroll
+            for (int i = 0; i < P; i++) sv[i] = sc[(size_t)min(s0 + slot_of(i), st_hi) * a.F + bin_of(i)];
+            const float2 nyq = sc[(size_t)min(s0 + min(tr, JOBS - 1), st_hi) * a.F + min(M, a.F - 1)];
+#pragma unroll
+            for (int i = 0; i < P; i++)
+                lds[slot_of(i) * C::PADN + bin_of(i)] = s0 + slot_of(i) <= st_hi ? sv[i] : make_float2(0.f, 0.f);
+            if (tr < JOBS)
+                lds[tr * C::PADN + M] = (s0 + tr <= st_hi && M < a.F) ? nyq : make_float2(0.f, 0.f);
         }
         __syncthreads();
         float2 v[P];
@@ -356,44 +401,49 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
         fft_first_pass<M, P, N>(v, buf, jr, post, ToLds<P>{buf});
         __syncthreads();
         fft_rest_passes<M, P, N, P>(buf, jr, twt, post, ToLds<P>{buf});
-        // Slot g now holds samples (2n, 2n + 1) of frame s0 + g at LDS index n, windowed.
+        // Slot g now holds samples (2n, 2n + 1) of frame s0 + g at LDS index n, windowed: add
+        // the frames of this round that cover each sample, in frame order.
         const int s_end = min(st_hi, s0 + JOBS - 1);
-#pragma unroll
-        for (int q = 0; q < PER; q++) {
-            const int J = J0 + q * NT + tid;
-            if (J >= J1) continue;
-            const int lo = max(s0, ceildiv(J - N + 1, hop) - a.frame_off);
-            const int hi = min(s_end, J / hop - a.frame_off);
+        walk(tr, [&](int q, int tf0, int s_first, int K) {
+            if (q * NT + tr >= J1 - J0) return;
+            const int first = tf0 - a.frame_off;              // spectrum frame of tf0
+            const int i0 = max(0, s0 - first), i1 = min(K, s_end - first);
+            // Sample pos (0 <= pos < N) of slot g is float 2*idx(pos/2) + pos%2 of the slot,
+            // i.e. pos + 2*(pos / 2P).
+            unsigned pos = (unsigned)(s_first - i0 * hop);
+            const float* sl = ldsf + 2 * C::PADN * (first + i0 - s0);
             float sum = acc[q];
-            for (int st = lo; st <= hi; st++) {
-                const int s = J - (st + a.frame_off) * hop;
-                const float2 z = lds[(st - s0) * C::PADN + C::idx(s >> 1)];
-                sum += (s & 1) ? z.y : z.x;
-            }
+            for (int i = i0; i <= i1; i++, pos -= (unsigned)hop, sl += 2 * C::PADN)
+                sum += sl[pos + 2 * (pos / (2 * P))];
             acc[q] = sum;
-        }
+        });
         __syncthreads();
     }
 
+    // Envelope: win^2 summed over the envelope frames 0 <= tf < env_frames covering J, in frame
+    // order (src/stft.h:130,187); out = acc / env where env > 1e-11, else 0.
     float* oc = a.out + (size_t)c * a.out_len;
-#pragma unroll
-    for (int q = 0; q < PER; q++) {
+    walk(tid, [&](int q, int tf0, int s_first, int K) {
         const int J = J0 + q * NT + tid;
-        if (J >= J1) continue;
+        if (J >= J1) return;
         float y = 0.f;
         if (J < a.valid_end) {
-            // Envelope: sum of win^2 over every frame covering J (src/stft.h:130,187).
-            const int lo = max(0, ceildiv(J - N + 1, hop));
-            const int hi = min(a.env_frames - 1, J / hop);
+            const int i0 = max(0, -tf0), i1 = min(K, a.env_frames - 1 - tf0);
+            unsigned pos = (unsigned)(s_first - i0 * hop);
             float env = 0.f;
-            for (int tf = lo; tf <= hi; tf++) {
-                const float w = win[J - tf * hop];
+            for (int i = i0; i <= i1; i++, pos -= (unsigned)hop) {
+                const float w = win[pos];
                 env += w * w;
             }
             y = env > 1e-11f ? acc[q] / env : 0.f;
         }
         oc[J - a.out_off] = y;
-    }
+    });
+}
+
+__global__ __launch_bounds__(256) void zero_kernel(float* out, size_t count) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < count) out[i] = 0.f;
 }
 
 // ------------------------------------------------------------------------ plain FFT
@@ -419,7 +469,7 @@ __global__ __launch_bounds__(JOBS * (N / P)) void fft_kernel(float2* data, int b
         const float2 x = active ? d[j + r * TPJ] : make_float2(0.f, 0.f);
         v[r] = inverse ? cconj(x) : x;
     }
-    stage_twiddles<N>(twt, gtw, tid, JOBS * TPJ);
+    stage_twiddles<N, JOBS * TPJ>(twt, gtw, tid);
     auto sink = [&](int k, float2 y) {
         if (active) d[k] = inverse ? cconj(y) : y;
     };
@@ -597,9 +647,11 @@ stx_status htdemucs_ispec_impl(const stx_fft* f, const float* spec, int channels
         check_extent((long long)channels * length, "output");
         if (channels == 0 || length == 0) return;
         STX_REQUIRE(spec && out, "NULL buffer");
-        if (n_frames == 0) {
-            hip_check(hipMemsetAsync(out, 0, sizeof(float) * (size_t)channels * length, as_stream(stream)),
-                      "hipMemsetAsync");
+        if (n_frames == 0) {   // no frames: silence (a fill kernel, which graph capture records safely)
+            const size_t count = (size_t)channels * length;
+            hipLaunchKernelGGL(zero_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, as_stream(stream),
+                               out, count);
+            launch_check("zero_kernel");
             return;
         }
         IstftArgs a{};
