@@ -673,10 +673,12 @@ __global__ __launch_bounds__(256) void ew_flat_kernel(const float* __restrict__ 
 // read of x at these sizes.
 //
 // Workspace: [groups] shift | [groups][partial chunks][2] partial sums.
-// VEC float4 per thread: chunks of 1024 * VEC floats, chosen separately for the two passes.
-constexpr int kGnVecPartial = 4, kGnVecApply = 1;
+// VEC float4 per thread: chunks of 1024 * VEC floats. Pass 1 uses 4; pass 2 uses 1 (more
+// blocks, shorter latency chains) unless a launch has at least kGnWideBlocks chunks of 4096
+// floats, where 4 amortises each block's statistics over four times as many elements.
+constexpr int kGnVecPartial = 4, kGnVecApplyNarrow = 1, kGnVecApplyWide = 4;
+constexpr long long kGnWideBlocks = 768;
 template <int VEC> constexpr int gn_chunk() { return 256 * 4 * VEC; }
-constexpr unsigned kSpinLimit = 1u << 22;         // barrier polls (~0.25 s) before giving up
 
 enum AffineKind { AFF_NONE = 0, AFF_CHANNEL = 1, AFF_NE0 = 2, AFF_GENERAL = 3 };
 
@@ -879,9 +881,9 @@ __global__ __launch_bounds__(256) void gn_partial_kernel(GroupNormArgs a) {
     gn_write_partial<VEC>(a, gt, v, ok, (double)xg[0], red);
 }
 
-template <int AK, bool GELU>
+template <int AK, bool GELU, int VEC>
 __global__ __launch_bounds__(256) void gn_apply_kernel(GroupNormArgs a) {
-    constexpr int VEC = kGnVecApply, CH = gn_chunk<VEC>();
+    constexpr int CH = gn_chunk<VEC>();
     __shared__ double red[8];
     const int gt = (int)blockIdx.y;
     long long begin, c0, i3;
@@ -1189,6 +1191,7 @@ Affine make_affine(const stx_tensor* t, const stx_tensor* x, const char* what) {
 
 struct GnPlan {
     long long cpg, groups, groups_total, chunks_partial, chunks_apply;
+    bool wide;                                           // pass 2 with kGnVecApplyWide
     size_t shift_off, part_off, bytes;                   // workspace layout
 };
 
@@ -1199,7 +1202,9 @@ GnPlan gn_plan(const stx_tensor* a, int n_groups) {
     p.groups_total = p.groups * a->ne[3];
     const long long span = p.cpg * a->ne[0] * a->ne[1];
     p.chunks_partial = (span + gn_chunk<kGnVecPartial>() - 1) / gn_chunk<kGnVecPartial>();
-    p.chunks_apply = (span + gn_chunk<kGnVecApply>() - 1) / gn_chunk<kGnVecApply>();
+    p.wide = p.chunks_partial * p.groups_total >= kGnWideBlocks;
+    const long long cha = p.wide ? gn_chunk<kGnVecApplyWide>() : gn_chunk<kGnVecApplyNarrow>();
+    p.chunks_apply = (span + cha - 1) / cha;
     const size_t g = (size_t)std::max<long long>(1, p.groups_total);
     auto up = [](size_t v) { return (v + 255) / 256 * 256; };
     p.shift_off = 0;
@@ -1214,8 +1219,12 @@ void launch_group_norm(GroupNormArgs g, const GnPlan& p, hipStream_t s) {
     hipLaunchKernelGGL(gn_partial_kernel, dim3((unsigned)p.chunks_partial, (unsigned)p.groups_total), dim3(256), 0, s,
                        g);
     launch_check("gn_partial_kernel");
-    hipLaunchKernelGGL((gn_apply_kernel<AK, GELU>), dim3((unsigned)p.chunks_apply, (unsigned)p.groups_total),
-                       dim3(256), 0, s, g);
+    if (p.wide)
+        hipLaunchKernelGGL((gn_apply_kernel<AK, GELU, kGnVecApplyWide>),
+                           dim3((unsigned)p.chunks_apply, (unsigned)p.groups_total), dim3(256), 0, s, g);
+    else
+        hipLaunchKernelGGL((gn_apply_kernel<AK, GELU, kGnVecApplyNarrow>),
+                           dim3((unsigned)p.chunks_apply, (unsigned)p.groups_total), dim3(256), 0, s, g);
     launch_check("gn_apply_kernel");
 }
 
