@@ -3,16 +3,20 @@
 // Reference: RoFormer::Impl::run, src/roformer.cpp:226-241 (gather) and :251-278 (scatter,
 // average, apply, zero_dc). Both are rewritten in gather form so that no two threads write
 // one element:
-//   * band gather: one workgroup per (band, tile of frames, batch item) writes the band's
-//     feature rows feat[t][(j*C + c)*2 + {re,im}] contiguously; T-major spectra are read
-//     row-wise directly, F-major ones through an LDS transpose so that both sides stay
-//     coalesced.
-//   * scatter + apply: one thread per (bin, channel, frame, stem) walks the list of
-//     (band, position) pairs that cover its bin (a CSR table built once per band table, in
-//     the reference's band-then-position order), sums their mask values in double, divides
-//     by the band count and multiplies the spectrum, all in double like the reference, and
-//     rounds once. Neighbouring lanes take neighbouring (bin, channel) pairs, which are
-//     neighbouring floats of the mask rows, so mask reads are coalesced in T-major layout.
+//   * band gather: band b's features are one contiguous block [T][size_b * C] of complex
+//     values (feat[t][(j*C + c)*2 + {re,im}]). T-major spectra: the output is walked flat,
+//     8 values per thread, each thread finding its band by a binary search over the band
+//     starts staged in LDS and its (channel, bin) in a per-pair table built once per band
+//     table; all loads are issued before the first store. F-major spectra: one workgroup per
+//     (band, tile of frames) through an LDS transpose, so that both sides stay coalesced.
+//   * scatter + apply: a thread per (bin, channel) and tile of frames (T-major) or per frame
+//     (F-major) walks the list of (band, position) pairs that cover its bin (a CSR table
+//     built once per band table, in the reference's band-then-position order), sums their
+//     mask values in double, divides by the band count and multiplies the spectrum, all in
+//     double like the reference, and rounds once. Neighbouring lanes take neighbouring
+//     (bin, channel) pairs, which are neighbouring floats of the mask rows, so mask reads are
+//     coalesced in T-major layout; the T-major thread reads its CSR entries once for all of
+//     its frames and issues the frames' loads together.
 #include <algorithm>
 #include <type_traits>
 #include <vector>
@@ -44,6 +48,10 @@ struct stx_bands {
     int* d_csr_off = nullptr;                        // [n_bins + 1]
     stx::CsrEntry* d_csr = nullptr;                  // [n_freqs]
     double* d_denom = nullptr;                       // [n_bins]: max(bands_per_freq, 1)
+    int* d_pair_off = nullptr;                       // [n_bands + 1]: first (bin, channel) pair of band b
+    int* d_pair_code = nullptr;                      // [total_feat / 2]: (channel << 16) | bin of each pair
+    int* d_freq_lo = nullptr;                        // [n_bands]: first bin of each band
+    bool ranges = false;                             // every band is a range of consecutive bins
 };
 
 namespace stx {
@@ -54,29 +62,71 @@ struct GatherArgs {
     float2* feat;            // [batch][total_feat * T / 2]
     const BandInfo* bands;
     const int* band_freqs;
+    const int* pair_off;     // [n_bands + 1]
+    const int* pair_code;    // [total_feat / 2]
+    const int* freq_lo;      // [n_bands]: first bin of each band when every band is a bin range
     int C, F, T;
+    int n_bands;
     long long total_feat;    // floats per frame of one batch item
-    int TT;                  // frames per tile
+    int TT;                  // F-major: frames per tile
 };
 
-// T-major: lanes walk a band row (j, c) for one frame at a time; reads and writes coalesced.
+constexpr int kGatherPer = 8;                        // T-major: outputs per thread
+
+// T-major: the batch item's features, n = (total_feat / 2) * T complex values, walked flat in
+// blocks of 256 * kGatherPer. Band b covers [pair_off[b] * T, pair_off[b + 1] * T); inside it,
+// value r is frame r / pairs_b, pair r % pairs_b. Reads of one band row are neighbouring bins
+// of two channel rows; writes are contiguous.
+// RANGES: every band is a range of consecutive bins, so pair q of band b is channel q % C of
+// bin freq_lo[b] + q / C and the pair table is not read.
+template <bool RANGES>
 __global__ __launch_bounds__(256) void band_gather_t_kernel(GatherArgs a) {
-    const int b = (int)blockIdx.x;
-    const int t0 = (int)blockIdx.y * a.TT;
-    const int bt = (int)blockIdx.z;
-    const BandInfo bi = a.bands[b];
-    const int pairs = bi.size * a.C;
-    const float2* sb = a.spec + (size_t)bt * a.C * a.T * a.F;
-    float2* fb = a.feat + ((size_t)bt * a.total_feat * a.T + (size_t)bi.feat_off * a.T) / 2;
-    const int t1 = min(t0 + a.TT, a.T);
-    for (int t = t0; t < t1; t++) {
-        float2* row = fb + (size_t)t * pairs;
-        for (int q = (int)threadIdx.x; q < pairs; q += 256) {
-            const int j = q / a.C, c = q - j * a.C;
-            const int f = a.band_freqs[bi.freq_off + j];
-            row[q] = sb[((size_t)c * a.T + t) * a.F + f];
+    extern __shared__ int po[];                      // [n_bands + 1] pair offsets, [n_bands] first bins
+    int* flo = po + a.n_bands + 1;
+    const int tid = (int)threadIdx.x;
+    for (int b = tid; b <= a.n_bands; b += 256) po[b] = a.pair_off[b];
+    if constexpr (RANGES)
+        for (int b = tid; b < a.n_bands; b += 256) flo[b] = a.freq_lo[b];
+    __syncthreads();
+    const int bt = (int)blockIdx.y;
+    const int n = po[a.n_bands] * a.T;
+    const int e0 = (int)blockIdx.x * (256 * kGatherPer) + tid;
+    if (e0 >= n) return;
+    int lo = 0, hi = a.n_bands;                      // po[lo] * T <= e0 < po[hi] * T
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (po[mid] * a.T <= e0) lo = mid;
+        else hi = mid;
+    }
+    int b = lo;
+    int pair[kGatherPer], t[kGatherPer], code[kGatherPer];
+#pragma unroll
+    for (int k = 0; k < kGatherPer; k++) {
+        const int e = min(e0 + k * 256, n - 1);
+        while (po[b + 1] * a.T <= e) b++;
+        const int pairs = po[b + 1] - po[b];
+        const int r = e - po[b] * a.T;
+        t[k] = r / pairs;
+        const int q = r - t[k] * pairs;
+        pair[k] = po[b] + q;
+        if constexpr (RANGES) {
+            const int j = q / a.C;
+            code[k] = ((q - j * a.C) << 16) | (flo[b] + j);
         }
     }
+    if constexpr (!RANGES) {
+#pragma unroll
+        for (int k = 0; k < kGatherPer; k++) code[k] = a.pair_code[pair[k]];
+    }
+    const float2* sb = a.spec + (size_t)bt * a.C * a.T * a.F;
+    float2 v[kGatherPer];
+#pragma unroll
+    for (int k = 0; k < kGatherPer; k++)
+        v[k] = sb[((size_t)(code[k] >> 16) * a.T + t[k]) * a.F + (code[k] & 0xffff)];
+    float2* fb = a.feat + (size_t)bt * n;
+#pragma unroll
+    for (int k = 0; k < kGatherPer; k++)
+        if (e0 + k * 256 < n) fb[e0 + k * 256] = v[k];
 }
 
 // F-major: a tile [pairs][TT] is read along t (coalesced) into LDS and written along the
@@ -138,17 +188,70 @@ __device__ __forceinline__ float2 masked_bin(const ScatterArgs& a, const float* 
     return make_float2((float)(zr * qr - zi * qi), (float)(zr * qi + zi * qr));
 }
 
-// T-major: thread = (bin, channel) of one frame; lanes cover consecutive mask floats.
+// T-major: thread = (bin, channel) for kScatterFrames frames; lanes cover consecutive mask
+// floats. The CSR entries are read once; the frames' spectrum and mask loads are issued
+// together, one covering band at a time, and each frame's sum runs in CSR order.
+constexpr int kScatterFrames = 8;
+
 __global__ __launch_bounds__(256) void band_scatter_t_kernel(ScatterArgs a) {
+#pragma clang fp contract(off)
     const int i = (int)(blockIdx.x * 256 + threadIdx.x);
     if (i >= a.F * a.C) return;
     const int f = i / a.C, c = i - f * a.C;
-    const int t = (int)blockIdx.y;
+    const int t0 = (int)blockIdx.y * kScatterFrames;
     const int bt = (int)blockIdx.z / a.S, s = (int)blockIdx.z % a.S;
     const float* mb = a.masks + ((size_t)bt * a.S + s) * a.total_feat * a.T;
-    const size_t zi = (((size_t)bt * a.C + c) * a.T + t) * a.F + f;
-    const float2 z = a.spec[zi];
-    a.out[(((size_t)bt * a.S + s) * a.C + c) * a.T * a.F + (size_t)t * a.F + f] = masked_bin(a, mb, z, f, c, t);
+    const float2* zc = a.spec + (((size_t)bt * a.C + c) * a.T) * a.F + f;
+    int tt[kScatterFrames];
+    float2 z[kScatterFrames];
+#pragma unroll
+    for (int k = 0; k < kScatterFrames; k++) {
+        tt[k] = min(t0 + k, a.T - 1);
+        z[k] = zc[(size_t)tt[k] * a.F];
+    }
+    double ar[kScatterFrames], ai[kScatterFrames];
+#pragma unroll
+    for (int k = 0; k < kScatterFrames; k++) ar[k] = ai[k] = 0.0;
+    // Covering bands two at a time (a bin is in one or two bands of a mel map): both CSR
+    // entries, then both bands' mask loads, then the sums in CSR order.
+    const int e1 = a.csr_off[f + 1];
+    for (int e = a.csr_off[f]; e < e1; e += 2) {
+        const bool two = e + 1 < e1;
+        const CsrEntry E0 = a.csr[e], E1 = a.csr[two ? e + 1 : e];
+        const float* r0 = mb + (size_t)E0.feat_off * a.T + E0.col + 2 * c;
+        const float* r1 = mb + (size_t)E1.feat_off * a.T + E1.col + 2 * c;
+        float2 m0[kScatterFrames], m1[kScatterFrames];
+#pragma unroll
+        for (int k = 0; k < kScatterFrames; k++) {
+            m0[k] = *reinterpret_cast<const float2*>(r0 + (size_t)tt[k] * E0.din);
+            m1[k] = *reinterpret_cast<const float2*>(r1 + (size_t)tt[k] * E1.din);
+        }
+#pragma unroll
+        for (int k = 0; k < kScatterFrames; k++) {
+            ar[k] += (double)m0[k].x;
+            ai[k] += (double)m0[k].y;
+        }
+        if (two) {
+#pragma unroll
+            for (int k = 0; k < kScatterFrames; k++) {
+                ar[k] += (double)m1[k].x;
+                ai[k] += (double)m1[k].y;
+            }
+        }
+    }
+    const double d = a.denom[f];
+    float2* oc = a.out + (((size_t)bt * a.S + s) * a.C + c) * a.T * a.F + f;
+#pragma unroll
+    for (int k = 0; k < kScatterFrames; k++) {
+        if (t0 + k >= a.T) break;
+        float2 o = make_float2(0.f, 0.f);
+        if (!(a.zero_dc && f == 0)) {
+            const double qr = ar[k] / d, qi = ai[k] / d;
+            const double zr = z[k].x, zi = z[k].y;
+            o = make_float2((float)(zr * qr - zi * qi), (float)(zr * qi + zi * qr));
+        }
+        oc[(size_t)(t0 + k) * a.F] = o;
+    }
 }
 
 // F-major: thread = frame of one (bin, channel); spectrum and output coalesced along t.
@@ -198,6 +301,22 @@ STX_API stx_status stx_bands_create(const int32_t* band_sizes, int n_bands, cons
                 const int f = band_freqs[fo[b] + j];
                 csr[fill[f]++] = CsrEntry{(long long)fe[b], band_sizes[b] * channels * 2, j * channels * 2};
             }
+        // Per (bin, channel) pair of every band, in feature order: (channel << 16) | bin.
+        STX_REQUIRE(n_bins < 65536 && channels < 32768, "band table: n_bins or channels too large");
+        std::vector<int> pair_off(n_bands + 1, 0), pair_code;
+        pair_code.reserve((size_t)(fe.back() / 2));
+        for (int b = 0; b < n_bands; b++) {
+            pair_off[b] = (int)(fe[b] / 2);
+            for (int j = 0; j < band_sizes[b]; j++)
+                for (int c = 0; c < channels; c++) pair_code.push_back((c << 16) | band_freqs[fo[b] + j]);
+        }
+        pair_off[n_bands] = (int)(fe.back() / 2);
+        std::vector<int> freq_lo(n_bands, 0);
+        bool ranges = true;
+        for (int b = 0; b < n_bands; b++) {
+            freq_lo[b] = band_sizes[b] > 0 ? band_freqs[fo[b]] : 0;
+            for (int j = 1; j < band_sizes[b]; j++) ranges = ranges && band_freqs[fo[b] + j] == freq_lo[b] + j;
+        }
         std::vector<double> denom(n_bins);
         for (int f = 0; f < n_bins; f++) denom[f] = (double)std::max(bpf[f], 1);   // src/roformer.cpp:272
 
@@ -224,6 +343,10 @@ STX_API stx_status stx_bands_create(const int32_t* band_sizes, int n_bands, cons
         up(&h->d_csr_off, csr_off);
         up(&h->d_csr, csr);
         up(&h->d_denom, denom);
+        up(&h->d_pair_off, pair_off);
+        up(&h->d_pair_code, pair_code);
+        up(&h->d_freq_lo, freq_lo);
+        h->ranges = ranges;
         if (e != hipSuccess) {
             stx_bands_destroy(h);
             hip_check(e, "stx_bands_create");
@@ -239,6 +362,9 @@ STX_API void stx_bands_destroy(stx_bands* h) {
     (void)hipFree(h->d_csr_off);
     (void)hipFree(h->d_csr);
     (void)hipFree(h->d_denom);
+    (void)hipFree(h->d_pair_off);
+    (void)hipFree(h->d_pair_code);
+    (void)hipFree(h->d_freq_lo);
     delete h;
 }
 
@@ -262,11 +388,19 @@ STX_API stx_status stx_band_gather(const stx_bands* h, const float* spec, int ba
         a.F = h->n_bins;
         a.T = n_frames;
         a.total_feat = h->total_feat;
+        a.pair_off = h->d_pair_off;
+        a.pair_code = h->d_pair_code;
+        a.freq_lo = h->d_freq_lo;
+        a.n_bands = h->n_bands;
         const hipStream_t s = as_stream(stream);
         if (layout == STX_SPEC_T_MAJOR) {
-            a.TT = 8;
-            dim3 grid(h->n_bands, (n_frames + a.TT - 1) / a.TT, batch);
-            hipLaunchKernelGGL(band_gather_t_kernel, grid, dim3(256), 0, s, a);
+            const long long n = h->total_feat / 2 * (long long)n_frames;
+            STX_REQUIRE(n < (1LL << 31) - 256 * kGatherPer, "band gather: too many features per chunk");
+            if (h->n_bands > 8191) fail(STX_STATUS_UNSUPPORTED, "T-major band gather: more than 8191 bands");
+            dim3 grid((unsigned)((n + 256 * kGatherPer - 1) / (256 * kGatherPer)), batch);
+            const size_t lds = sizeof(int) * (2 * (size_t)h->n_bands + 1);
+            if (h->ranges) hipLaunchKernelGGL(band_gather_t_kernel<true>, grid, dim3(256), lds, s, a);
+            else hipLaunchKernelGGL(band_gather_t_kernel<false>, grid, dim3(256), lds, s, a);
             launch_check("band_gather_t_kernel");
             return;
         }
@@ -309,7 +443,7 @@ STX_API stx_status stx_band_scatter_apply(const stx_bands* h, const float* masks
         a.total_feat = h->total_feat;
         const hipStream_t s = as_stream(stream);
         if (layout == STX_SPEC_T_MAJOR) {
-            dim3 grid((a.F * a.C + 255) / 256, n_frames, batch * n_stems);
+            dim3 grid((a.F * a.C + 255) / 256, (n_frames + kScatterFrames - 1) / kScatterFrames, batch * n_stems);
             hipLaunchKernelGGL(band_scatter_t_kernel, grid, dim3(256), 0, s, a);
             launch_check("band_scatter_t_kernel");
         } else {

@@ -105,18 +105,27 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void stft_kernel(StftArgs a) {
     const bool interior = base >= 0 && base + N <= a.len;
     const float2* win2 = reinterpret_cast<const float2*>(a.win);
 
-    // Signal indexes first, then every load without a branch between them (an inactive job
-    // reads frame 0 of channel 0, always in range; its slot is transformed but never written).
-    int ix[2 * P];
-#pragma unroll
-    for (int r = 0; r < P; r++) {
-        const int n = j + r * TPJ;
-        ix[2 * r] = interior ? base + 2 * n : padded_index<N>(m0 + 2 * n, a);
-        ix[2 * r + 1] = interior ? base + 2 * n + 1 : padded_index<N>(m0 + 2 * n + 1, a);
-    }
+    // Every load issued before the first wait (an inactive job reads frame 0 of channel 0,
+    // always in range; its slot is transformed but never written). `interior` is uniform over
+    // the job's threads, so only one of the two index paths runs.
     float2 v[P];
+    if (interior) {
 #pragma unroll
-    for (int r = 0; r < P; r++) v[r] = make_float2(xc[ix[2 * r]], xc[ix[2 * r + 1]]);
+        for (int r = 0; r < P; r++) {
+            const int n = j + r * TPJ;
+            v[r] = make_float2(xc[base + 2 * n], xc[base + 2 * n + 1]);
+        }
+    } else {
+        int ix[2 * P];
+#pragma unroll
+        for (int r = 0; r < P; r++) {
+            const int n = j + r * TPJ;
+            ix[2 * r] = padded_index<N>(m0 + 2 * n, a);
+            ix[2 * r + 1] = padded_index<N>(m0 + 2 * n + 1, a);
+        }
+#pragma unroll
+        for (int r = 0; r < P; r++) v[r] = make_float2(xc[ix[2 * r]], xc[ix[2 * r + 1]]);
+    }
     float2 w[P];
 #pragma unroll
     for (int r = 0; r < P; r++) w[r] = win2[j + r * TPJ];
@@ -131,25 +140,37 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void stft_kernel(StftArgs a) {
     const float hs = 0.5f * a.scale;
     const int f0 = lb * JOBS;
     const int c0 = f0 / a.T, t0 = f0 - c0 * a.T;
-    auto emit = [&](int k, int g) {
-        if (f0 + g >= a.jobs) return;
-        int tt = t0 + g, cc = c0;
-        while (tt >= a.T) { tt -= a.T; cc++; }
+    auto bin = [&](int k, int g, float2 w) {
         const float2* bs = lds + g * C::PADN;
         const float2 zk = bs[C::idx(k & (M - 1))];
         const float2 zm = bs[C::idx((M - k) & (M - 1))];
         const float er = zk.x + zm.x, ei = zk.y - zm.y;       // 2E
         const float orr = zk.y + zm.y, oi = zm.x - zk.x;      // 2O
-        const float2 w = tw_lookup<N>(twt, k);
-        const float2 val = make_float2((er + w.x * orr - w.y * oi) * hs, (ei + w.x * oi + w.y * orr) * hs);
-        if (a.layout == STX_SPEC_F_MAJOR) a.spec[((size_t)cc * a.F + k) * a.T + tt] = val;
-        else a.spec[((size_t)cc * a.T + tt) * a.F + k] = val;
+        return make_float2((er + w.x * orr - w.y * oi) * hs, (ei + w.x * oi + w.y * orr) * hs);
     };
     if (a.layout == STX_SPEC_F_MAJOR) {
-        for (int e = tid; e < a.F * JOBS; e += NT) emit(e / JOBS, e % JOBS);
+        for (int e = tid; e < a.F * JOBS; e += NT) {
+            const int k = e / JOBS, g = e % JOBS;
+            if (f0 + g >= a.jobs) continue;
+            int tt = t0 + g, cc = c0;
+            while (tt >= a.T) { tt -= a.T; cc++; }
+            a.spec[((size_t)cc * a.F + k) * a.T + tt] = bin(k, g, tw_lookup<N>(twt, k));
+        }
     } else {
-        for (int g = 0; g < JOBS; g++)
-            for (int k = tid; k < a.F; k += NT) emit(k, g);
+        // Row of frame g, then each bin's twiddle once for all JOBS frames.
+        float2* rows[JOBS];
+#pragma unroll
+        for (int g = 0; g < JOBS; g++) {
+            int tt = t0 + g, cc = c0;
+            while (tt >= a.T) { tt -= a.T; cc++; }
+            rows[g] = f0 + g < a.jobs ? a.spec + ((size_t)cc * a.T + tt) * a.F : nullptr;
+        }
+        for (int k = tid; k < a.F; k += NT) {
+            const float2 w = tw_lookup<N>(twt, k);
+#pragma unroll
+            for (int g = 0; g < JOBS; g++)
+                if (rows[g]) rows[g][k] = bin(k, g, w);
+        }
     }
 }
 
@@ -483,13 +504,14 @@ constexpr int block_jobs(int tpj, int threads) { return tpj >= threads ? 1 : thr
 constexpr int kIstftPer = 6;                           // fused: output samples per thread per tile
 
 // Points per thread: 8 keeps waves short for the small, latency-bound batches of one
-// segment; the fused iSTFT uses 16 so that one workgroup holds as many frames as possible.
+// segment (16 measured slower for the STFT at n_fft 2048, faster from 4096); the fused iSTFT
+// uses 16 so that one workgroup holds as many frames as possible.
 constexpr int kStftP = 8;
 constexpr int fused_p(int n) { return n / 2 >= 16 ? 16 : 8; }
 
 template <int N>
 void launch_stft(const StftArgs& a0, hipStream_t s) {
-    constexpr int P = kStftP;
+    constexpr int P = N >= 4096 ? 16 : kStftP;
     constexpr int TPJ = N / 2 / P;
     constexpr int JOBS = block_jobs(TPJ, 256);
     StftArgs a = a0;
