@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
@@ -87,5 +88,19 @@ __device__ __forceinline__ int xcd_block() {
 }
 
 inline bool is_pow2(long long n) { return n >= 1 && (n & (n - 1)) == 0; }
+
+// Compute units of the current device (cached per device id).
+inline int device_cus() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= 64) dev = 0;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n <= 0) {
+        hip_check(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
+        cache[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
 
 }  // namespace stx

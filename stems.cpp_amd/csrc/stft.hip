@@ -400,8 +400,16 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
                 lds[tr * C::PADN + M] = (s0 + tr <= st_hi && M < a.F) ? nyq : make_float2(0.f, 0.f);
         } else {
             // Element e = tr + i*NT: slot e / M, bin e % M.
-            auto slot_of = [&](int i) { return NT >= M ? tr / M + i * (NT / M) : i / (M / NT); };
-            auto bin_of = [&](int i) { return NT >= M ? tr % M : tr + (i % (M / NT)) * NT; };
+            auto slot_of = [&](int i) {
+                if constexpr (NT % M == 0) return tr / M + i * (NT / M);
+                else if constexpr (M % NT == 0) return i / (M / NT);
+                else return (tr + i * NT) / M;
+            };
+            auto bin_of = [&](int i) {
+                if constexpr (NT % M == 0) return tr % M;
+                else if constexpr (M % NT == 0) return tr + (i % (M / NT)) * NT;
+                else return (tr + i * NT) % M;
+            };
 #pragma unroll
             for (int i = 0; i < P; i++) sv[i] = sc[(size_t)min(s0 + slot_of(i), st_hi) * a.F + bin_of(i)];
             const float2 nyq = sc[(size_t)min(s0 + min(tr, JOBS - 1), st_hi) * a.F + min(M, a.F - 1)];
@@ -520,14 +528,11 @@ void launch_stft(const StftArgs& a0, hipStream_t s) {
     launch_check("stft_kernel");
 }
 
-template <int N>
-void launch_istft_fused(IstftArgs a, int channels, hipStream_t s) {
-    constexpr int P = fused_p(N);
-    constexpr int TPJ = N / 2 / P;
-    constexpr int JOBS = block_jobs(TPJ, 1024);
-    constexpr int NT = JOBS * TPJ;
-    // Tiles of m hops need m + ceil(N/hop) - 1 frames; pick m so that they fit one round of
-    // JOBS frames, within the PER*NT samples the threads accumulate.
+// Tiles of m hops need m + ceil(N/hop) - 1 frames; m is chosen so that they fit one round of
+// JOBS frames, within the PER*NT samples the threads accumulate. Returns the block count.
+template <int N, int JOBS>
+long long plan_istft_tiles(IstftArgs& a, int channels) {
+    constexpr int NT = JOBS * (N / 2 / fused_p(N));
     const int span = (N + a.hop - 1) / a.hop;
     const long long m = std::max(1, JOBS - span + 1);
     const long long tile_len = std::min<long long>(m * a.hop, (long long)kIstftPer * NT);
@@ -535,9 +540,36 @@ void launch_istft_fused(IstftArgs a, int channels, hipStream_t s) {
     a.tile_origin = (tile_len % a.hop == 0) ? a.out_off - a.out_off % a.hop : a.out_off;
     const long long end = (long long)a.out_off + a.out_len;
     a.tiles = (int)((end - a.tile_origin + tile_len - 1) / tile_len);
-    a.nblocks = a.tiles * channels;
-    hipLaunchKernelGGL((istft_kernel<N, P, JOBS, kIstftPer>), dim3(xcd_grid(a.nblocks)), dim3(NT), 0, s, a);
+    return (long long)a.tiles * channels;
+}
+
+template <int N, int JOBS>
+void launch_istft_fused_jobs(IstftArgs a, int channels, hipStream_t s) {
+    constexpr int P = fused_p(N);
+    a.nblocks = (int)plan_istft_tiles<N, JOBS>(a, channels);
+    hipLaunchKernelGGL((istft_kernel<N, P, JOBS, kIstftPer>), dim3(xcd_grid(a.nblocks)), dim3(JOBS * (N / 2 / P)),
+                       0, s, a);
     launch_check("istft_kernel");
+}
+
+// One workgroup per CU at most (the frames fill the LDS), so when the full-size tiles leave
+// CUs idle, tiles of 3/4 the frames (more of them, each frame transformed by more tiles) are
+// taken if they still fit in one round.
+template <int N>
+void launch_istft_fused(IstftArgs a, int channels, hipStream_t s) {
+    constexpr int JOBS = block_jobs(N / 2 / fused_p(N), 1024);
+    constexpr int ALT = JOBS * 3 / 4;
+    if constexpr (N >= 2048 && ALT >= 2) {
+        const int span = (N + a.hop - 1) / a.hop;
+        IstftArgs t = a;
+        const long long cus = device_cus();
+        if (ALT - span >= 1 && plan_istft_tiles<N, JOBS>(t, channels) < cus &&
+            plan_istft_tiles<N, ALT>(t, channels) <= cus) {
+            launch_istft_fused_jobs<N, ALT>(a, channels, s);
+            return;
+        }
+    }
+    launch_istft_fused_jobs<N, JOBS>(a, channels, s);
 }
 
 template <int N>
