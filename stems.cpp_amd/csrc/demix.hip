@@ -46,34 +46,56 @@ __device__ __forceinline__ float padded_mix(const float* __restrict__ xc, int64_
 }
 
 // parts[k - first][c][t] for chunks first .. first + count - 1. Block (x, y, z) = (tile of
-// 1024 samples, channel, chunk - first); 4 consecutive samples per thread, no divisions.
+// 256 * 4 * kChunkGroups samples, channel, chunk - first); each thread takes kChunkGroups
+// groups of 4 consecutive samples, 1024 samples apart, and issues all their loads before the
+// first store. A group inside the signal (no reflection, no tail) moves as one float4 when the
+// source is 16-byte aligned (vec bit 1); the rest goes sample by sample, with no divisions.
+constexpr int kChunkGroups = 4;
+
 __global__ __launch_bounds__(256) void demix_chunks_kernel(DemixArgs a, const float* __restrict__ mix,
                                                            int64_t first, int vec, float* __restrict__ parts) {
-    const int t0 = ((int)blockIdx.x * 256 + (int)threadIdx.x) * 4;
-    if (t0 >= a.chunk) return;
     const int c = (int)blockIdx.y;
     const int64_t k = first + (int64_t)blockIdx.z;
     const int64_t i = k * a.step;
     const int64_t length = min((int64_t)a.chunk, a.padded_len - i);
     const bool reflect_tail = length > a.chunk / 2 + 1;
     const float* xc = mix + (size_t)c * a.len;
-    float v[4];
+    const int64_t lead = a.reflect_border ? a.border : 0;    // padded index p is signal index p - lead
+    float v[kChunkGroups][4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int t = t0 + j;
-        float x = 0.f;
-        if (t < length) x = padded_mix(xc, i + t, a);
-        else if (t < a.chunk && reflect_tail)                       // reflect_pad(src, length, 0, chunk - length)
-            x = padded_mix(xc, i + 2 * (length - 1) - t, a);        // (src/roformer.cpp:325)
-        v[j] = x;
+    for (int g = 0; g < kChunkGroups; g++) {
+        const int t0 = ((int)blockIdx.x * kChunkGroups + g) * 1024 + (int)threadIdx.x * 4;
+        const int64_t s0 = i + t0 - lead;                    // signal index of sample t0
+        if ((vec & 2) && t0 + 3 < length && s0 >= 0 && s0 + 3 < a.len && (s0 & 3) == 0) {
+            const float4 q = *reinterpret_cast<const float4*>(xc + s0);
+            v[g][0] = q.x;
+            v[g][1] = q.y;
+            v[g][2] = q.z;
+            v[g][3] = q.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int t = t0 + j;
+                float x = 0.f;
+                if (t < length) x = padded_mix(xc, i + t, a);
+                else if (t < a.chunk && reflect_tail)                       // reflect_pad(src, length, 0, chunk - length)
+                    x = padded_mix(xc, i + 2 * (length - 1) - t, a);        // (src/roformer.cpp:325)
+                v[g][j] = x;
+            }
+        }
     }
-    float* dst = parts + ((size_t)blockIdx.z * a.channels + c) * a.chunk + t0;
-    if (vec && t0 + 3 < a.chunk) {
-        *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
-    } else {
+    float* dst = parts + ((size_t)blockIdx.z * a.channels + c) * a.chunk;
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            if (t0 + j < a.chunk) dst[j] = v[j];
+    for (int g = 0; g < kChunkGroups; g++) {
+        const int t0 = ((int)blockIdx.x * kChunkGroups + g) * 1024 + (int)threadIdx.x * 4;
+        if (t0 >= a.chunk) break;
+        if ((vec & 1) && t0 + 3 < a.chunk) {
+            *reinterpret_cast<float4*>(dst + t0) = make_float4(v[g][0], v[g][1], v[g][2], v[g][3]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (t0 + j < a.chunk) dst[t0 + j] = v[g][j];
+        }
     }
 }
 
@@ -88,8 +110,10 @@ __device__ __forceinline__ float chunk_weight(const float* __restrict__ window, 
 // Each thread takes 4 consecutive samples: their chunk weights and weight sums are formed once
 // and reused for every (stem, channel) plane, then each plane sums its chunk outputs in chunk
 // order in double (float x float is exact in double), divides once and rounds once.
-constexpr int kOlaMaxChunks = 8;      // chunks covering 4 consecutive samples
+// NK: the most chunks that cover 4 consecutive samples for the plan, ceil((chunk + 3) / step).
+constexpr int kOlaMaxChunks = 8;
 
+template <int NK>
 __global__ __launch_bounds__(256) void demix_ola_kernel(DemixArgs a, const float* __restrict__ y,
                                                         const float* __restrict__ window, int planes, int vec,
                                                         float* __restrict__ out) {
@@ -99,43 +123,80 @@ __global__ __launch_bounds__(256) void demix_ola_kernel(DemixArgs a, const float
     const int64_t p0 = (a.reflect_border ? a.border : 0) + t0;
     const int64_t k_lo = p0 >= a.chunk ? (p0 - a.chunk) / a.step + 1 : 0;   // first chunk with p0 < k*step + chunk
     const int64_t k_hi = (p0 + 3) / a.step;                                 // last chunk starting at or before p0 + 3
-    const int nk = (int)min((int64_t)kOlaMaxChunks, k_hi - k_lo + 1);
-    float w[kOlaMaxChunks][4];
+    const int nk = (int)min((int64_t)NK, k_hi - k_lo + 1);
+    // Window values first (clamped positions, every load before the first wait), then the
+    // chunk weights of src/roformer.cpp:334-336 by selection.
+    float w[NK][4];
+#pragma unroll
+    for (int kk = 0; kk < NK; kk++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int64_t tt = p0 + j - (k_lo + kk) * a.step;
+            w[kk][j] = window[min(max(tt, (int64_t)0), (int64_t)a.chunk - 1)];
+        }
     double cnt[4] = {0.0, 0.0, 0.0, 0.0};
     bool all4 = true;                                       // every (chunk, sample) of the span valid
 #pragma unroll
-    for (int kk = 0; kk < kOlaMaxChunks; kk++) {
+    for (int kk = 0; kk < NK; kk++) {
         const int64_t k = k_lo + kk;
         const int64_t i = k * a.step;
         const int64_t length = min((int64_t)a.chunk, a.padded_len - i);
+        const bool last = i + a.chunk >= a.padded_len;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int64_t tt = p0 + j - i;
             const bool ok = kk < nk && t0 + j < a.len && tt >= 0 && tt < length;
-            w[kk][j] = ok ? chunk_weight(window, k, (int)tt, a) : 0.f;
+            float wt = w[kk][j];
+            if (k == 0) wt = tt < a.fade ? 1.0f : wt;
+            else if (last && tt >= a.chunk - a.fade) wt = 1.0f;
+            w[kk][j] = ok ? wt : 0.f;
             if (ok) cnt[j] += (double)w[kk][j];
             if (kk < nk && !ok) all4 = false;
         }
     }
     const size_t stride = (size_t)planes * a.chunk;          // one chunk's output
+    if (vec && all4) {
+        // Chunks past nk re-read chunk nk - 1 and add +0.0 (an exact no-op: res never holds
+        // -0.0), so that every load is used and none is sunk behind a branch.
+        const float* src[NK];
+#pragma unroll
+        for (int kk = 0; kk < NK; kk++) {
+            const int64_t k = k_lo + min(kk, nk - 1);
+            src[kk] = y + (size_t)k * stride + (p0 - k * a.step);
+        }
+        for (int sc = 0; sc < planes; sc++) {
+            float4 q[NK];
+#pragma unroll
+            for (int kk = 0; kk < NK; kk++) q[kk] = *reinterpret_cast<const float4*>(src[kk] + (size_t)sc * a.chunk);
+            double res[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+            for (int kk = 0; kk < NK; kk++) {
+                const bool in = kk < nk;
+                res[0] += in ? (double)q[kk].x * (double)w[kk][0] : 0.0;
+                res[1] += in ? (double)q[kk].y * (double)w[kk][1] : 0.0;
+                res[2] += in ? (double)q[kk].z * (double)w[kk][2] : 0.0;
+                res[3] += in ? (double)q[kk].w * (double)w[kk][3] : 0.0;
+            }
+            float o[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const double v = res[j] / cnt[j];
+                o[j] = isfinite(v) ? (float)v : 0.0f;                         // np.nan_to_num
+            }
+            *reinterpret_cast<float4*>(out + (size_t)sc * a.len + t0) = make_float4(o[0], o[1], o[2], o[3]);
+        }
+        return;
+    }
     for (int sc = 0; sc < planes; sc++) {
         double res[4] = {0.0, 0.0, 0.0, 0.0};
         for (int kk = 0; kk < nk; kk++) {
             const int64_t k = k_lo + kk;
             const float* src = y + (size_t)k * stride + (size_t)sc * a.chunk + (p0 - k * a.step);
-            if (vec && all4) {
-                const float4 q = *reinterpret_cast<const float4*>(src);
-                res[0] += (double)q.x * (double)w[kk][0];
-                res[1] += (double)q.y * (double)w[kk][1];
-                res[2] += (double)q.z * (double)w[kk][2];
-                res[3] += (double)q.w * (double)w[kk][3];
-            } else {
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int64_t tt = p0 + j - k * a.step;
-                    const int64_t length = min((int64_t)a.chunk, a.padded_len - k * a.step);
-                    if (t0 + j < a.len && tt >= 0 && tt < length) res[j] += (double)src[j] * (double)w[kk][j];
-                }
+            for (int j = 0; j < 4; j++) {
+                const int64_t tt = p0 + j - k * a.step;
+                const int64_t length = min((int64_t)a.chunk, a.padded_len - k * a.step);
+                if (t0 + j < a.len && tt >= 0 && tt < length) res[j] += (double)src[j] * (double)w[kk][j];
             }
         }
         float o[4];
@@ -289,8 +350,11 @@ STX_API stx_status stx_demix_chunks(const stx_demix* d, const float* mix, int64_
         if (count == 0) return;
         STX_REQUIRE(mix && parts, "NULL buffer");
         STX_REQUIRE(count < 65536 && d->channels < 65536, "too many chunks or channels in one call");
-        const int vec = d->g.chunk % 4 == 0 && (reinterpret_cast<uintptr_t>(parts) & 15) == 0;
-        const dim3 grid((unsigned)((d->g.chunk + 1023) / 1024), (unsigned)d->channels, (unsigned)count);
+        // bit 0: float4 stores into parts; bit 1: float4 loads from the channel rows of mix.
+        const int vec = (d->g.chunk % 4 == 0 && (reinterpret_cast<uintptr_t>(parts) & 15) == 0 ? 1 : 0) |
+                        (d->g.len % 4 == 0 && (reinterpret_cast<uintptr_t>(mix) & 15) == 0 ? 2 : 0);
+        const dim3 grid((unsigned)((d->g.chunk + 1024 * kChunkGroups - 1) / (1024 * kChunkGroups)),
+                        (unsigned)d->channels, (unsigned)count);
         hipLaunchKernelGGL(demix_chunks_kernel, grid, dim3(256), 0, as_stream(stream), args_of(d), mix, first, vec, parts);
         launch_check("demix_chunks_kernel");
     });
@@ -310,8 +374,21 @@ STX_API stx_status stx_demix_overlap_add(const stx_demix* d, const float* y, int
             const int vec = d->g.chunk % 4 == 0 && d->g.step % 4 == 0 && off % 4 == 0 && d->g.len % 4 == 0 &&
                             (reinterpret_cast<uintptr_t>(y) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
             const unsigned blocks = (unsigned)((d->g.len + 1023) / 1024);
-            hipLaunchKernelGGL(demix_ola_kernel, dim3(blocks), dim3(256), 0, as_stream(stream), args_of(d), y,
-                               d->d_window, planes, vec, out);
+            const int nk = (int)((d->g.chunk + 3 + (int64_t)d->g.step - 1) / d->g.step);
+            auto go = [&](auto kernel) {
+                hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), 0, as_stream(stream), args_of(d), y, d->d_window,
+                                   planes, vec, out);
+            };
+            switch (nk) {
+                case 1: go(demix_ola_kernel<1>); break;
+                case 2: go(demix_ola_kernel<2>); break;
+                case 3: go(demix_ola_kernel<3>); break;
+                case 4: go(demix_ola_kernel<4>); break;
+                case 5: go(demix_ola_kernel<5>); break;
+                case 6: go(demix_ola_kernel<6>); break;
+                case 7: go(demix_ola_kernel<7>); break;
+                default: go(demix_ola_kernel<8>); break;
+            }
             launch_check("demix_ola_kernel");
         } else {
             dim3 grid((unsigned)((d->g.len + 255) / 256), planes);
