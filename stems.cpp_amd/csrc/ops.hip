@@ -369,21 +369,46 @@ __device__ __forceinline__ int row_extra(const RowSplit& sp, int lane) {
     return -1;
 }
 
+// The row's float4 body (slots past nb4 read as 0) and this lane's head/tail float. Every
+// load is issued before the first wait: slots past nb4 re-read float4 nb4 - 1 and are zeroed
+// afterwards (a row with no aligned float4 reads none), and a lane with no extra float reads
+// x[0].
 template <int LANES, int V4>
 __device__ __forceinline__ void row_load(const float* x, const RowSplit& sp, int lane, float (&v)[4 * V4], float& e,
                                          int& ei) {
     const float4* b = reinterpret_cast<const float4*>(x + sp.h);
+    ei = row_extra(sp, lane);
+    e = x[max(ei, 0)];
+    if (sp.nb4 > 0) {
+        float4 f[V4];
+#pragma unroll
+        for (int k = 0; k < V4; k++) f[k] = b[min(lane + LANES * k, sp.nb4 - 1)];
+#pragma unroll
+        for (int k = 0; k < V4; k++) {
+            const bool in = lane + LANES * k < sp.nb4;
+            v[4 * k] = in ? f[k].x : 0.f;
+            v[4 * k + 1] = in ? f[k].y : 0.f;
+            v[4 * k + 2] = in ? f[k].z : 0.f;
+            v[4 * k + 3] = in ? f[k].w : 0.f;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4 * V4; k++) v[k] = 0.f;
+    }
+    if (ei < 0) e = 0.f;
+}
+
+// gamma/beta float4 of the body slots (1 and 0 where absent), loaded before the row's
+// reductions so that their latency overlaps them.
+template <int LANES, int V4>
+__device__ __forceinline__ void row_params(const float* gamma, const float* beta, const RowSplit& sp, int lane,
+                                           float4 (&g)[V4], float4 (&bb)[V4]) {
 #pragma unroll
     for (int k = 0; k < V4; k++) {
-        const int q = lane + LANES * k;
-        const float4 f = q < sp.nb4 ? b[q] : make_float4(0.f, 0.f, 0.f, 0.f);
-        v[4 * k] = f.x;
-        v[4 * k + 1] = f.y;
-        v[4 * k + 2] = f.z;
-        v[4 * k + 3] = f.w;
+        const int i0 = sp.h + 4 * min(lane + LANES * k, max(sp.nb4 - 1, 0));
+        g[k] = gamma ? *reinterpret_cast<const float4*>(gamma + i0) : make_float4(1.f, 1.f, 1.f, 1.f);
+        bb[k] = beta ? *reinterpret_cast<const float4*>(beta + i0) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    ei = row_extra(sp, lane);
-    e = ei >= 0 ? x[ei] : 0.f;
 }
 
 template <int LANES, int V4>
@@ -400,6 +425,9 @@ __global__ __launch_bounds__(256) void row_norm_v4_kernel(RowNormArgs a) {
         float v[4 * V4], e;
         int ei;
         row_load<LANES, V4>(x, sp, lane, v, e, ei);
+        const bool pvec = a.vec_params && sp.h == 0 && sp.nb4 > 0;   // parameter float4 at i0 aligned
+        float4 gq[V4], bq[V4];
+        if (pvec) row_params<LANES, V4>(a.gamma, a.beta, sp, lane, gq, bq);
         double mean = 0.0;
         if (!a.rms) {
             double s = ei >= 0 ? (double)e : 0.0;
@@ -421,23 +449,31 @@ __global__ __launch_bounds__(256) void row_norm_v4_kernel(RowNormArgs a) {
         }
         ss = group_sum<LANES>(ss);
         const double scale = 1.0 / sqrt(ss / n + (double)a.eps);
+        const float scale_f = (float)scale;
         float4* yb = reinterpret_cast<float4*>(y + sp.h);
-        const bool pvec = a.vec_params && sp.h == 0;       // parameter float4 at i0 aligned
 #pragma unroll
         for (int k = 0; k < V4; k++) {
             const int q = lane + LANES * k;
             if (q < sp.nb4) {
                 const int i0 = sp.h + 4 * q;
                 float o[4];
-                if (pvec) {
-                    const float4 g = a.gamma ? *reinterpret_cast<const float4*>(a.gamma + i0) : make_float4(1.f, 1.f, 1.f, 1.f);
-                    const float4 bb = a.beta ? *reinterpret_cast<const float4*>(a.beta + i0) : make_float4(0.f, 0.f, 0.f, 0.f);
-                    const float gg[4] = {g.x, g.y, g.z, g.w}, bq[4] = {bb.x, bb.y, bb.z, bb.w};
+                if (pvec && !a.beta) {
+                    // No offset to cancel against: (x - mean) in double, then the scale and gamma
+                    // products in float (at most ~2 ulp from the double result).
+                    const float gg[4] = {gq[k].x, gq[k].y, gq[k].z, gq[k].w};
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const float d = a.rms ? v[4 * k + j] : (float)((double)v[4 * k + j] - mean);
+                        o[j] = a.gamma ? (d * scale_f) * gg[j] : d * scale_f;
+                    }
+                } else if (pvec) {
+                    const float gg[4] = {gq[k].x, gq[k].y, gq[k].z, gq[k].w};
+                    const float bv[4] = {bq[k].x, bq[k].y, bq[k].z, bq[k].w};
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
                         double t = ((double)v[4 * k + j] - mean) * scale;
                         if (a.gamma) t *= (double)gg[j];
-                        if (a.beta) t += (double)bq[j];
+                        t += (double)bv[j];
                         o[j] = (float)t;
                     }
                 } else {
