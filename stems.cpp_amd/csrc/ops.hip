@@ -1056,9 +1056,10 @@ void pick_row_shape(long long n, F&& f) {
     else f(integral_constant<int, 64>{}, integral_constant<int, 32>{});
 }
 
-// Calls f(LANES, V4) for the vector-load row kernels: the smallest LANES (8..64) whose V4 =
-// ceil(ceil(n/4) / LANES) float4 per lane is at most 4 (8 for rows of 1025..2048), so that the
-// LANES * V4 slots cover the row body with as few idle slots as possible.
+// Calls f(LANES, V4) for the vector-load row kernels, V4 = ceil(ceil(n/4) / LANES) float4 per
+// lane from {1, 2, 3, 4, 6, 8}: 8 lanes up to 32 float4, 16 lanes up to 128 (rows of up to 512
+// floats: more rows per wave share each row's fixed cost of reductions and square root), 64
+// lanes beyond (V4 up to 8, rows of up to 2048 floats).
 template <class F>
 void pick_v4_shape(long long n, F&& f) {
     using std::integral_constant;
@@ -1070,11 +1071,11 @@ void pick_v4_shape(long long n, F&& f) {
         else if (v == 2) f(lanes, integral_constant<int, 2>{});
         else if (v == 3) f(lanes, integral_constant<int, 3>{});
         else if (v == 4) f(lanes, integral_constant<int, 4>{});
+        else if (v <= 6) f(lanes, integral_constant<int, 6>{});
         else f(lanes, integral_constant<int, 8>{});
     };
     if (q <= 32) with_lanes(integral_constant<int, 8>{});
-    else if (q <= 64) with_lanes(integral_constant<int, 16>{});
-    else if (q <= 128) with_lanes(integral_constant<int, 32>{});
+    else if (q <= 128) with_lanes(integral_constant<int, 16>{});
     else with_lanes(integral_constant<int, 64>{});
 }
 
