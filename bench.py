@@ -32,9 +32,11 @@ The same line carries the spectral half of the metric, STFT+iSTFT Msamples/s:
   spectral.roformer_chunk: stx_torch_stft (n_fft 2048, hop 441) -> stx_band_scatter_apply with
     60 mel bands and uniform [-1, 1] masks (one stem) -> stx_torch_istft on one stereo chunk of
     352,800 samples (src/roformer.cpp:217-283).
-rows: every other hot-path kernel at its config shape (c3 band gather / scatter-apply / STFT /
-iSTFT, c4 RMSNorm, RoPE, softmax, bias+GELU, c5 demix chunk build and overlap-add), each timed
-cold (a graph of calls on more than 512 MB of distinct buffers) against its algorithmic bytes.
+rows: every other hot-path kernel at its config shape (c1 HTDemucs spec/ispec, c3 band gather /
+scatter-apply / STFT / iSTFT, c4 RMSNorm, RoPE, softmax, bias+GELU, c5 demix chunk build and
+overlap-add), each timed cold (a graph of calls on more than 512 MB of distinct buffers) against
+its algorithmic bytes and against a plain device copy of the same bytes at the same size
+(copy_us; frac_of_copy = copy_us / us), the practical ceiling for small, launch-bound sizes.
 """
 import argparse
 import json
@@ -404,7 +406,8 @@ def time_call(torch, stream, make, nbytes, replays=3):
 
 
 def run_rows(torch, stx, dev):
-    """Every other hot-path kernel at its config shape, cold, against its algorithmic bytes."""
+    """Every other hot-path kernel at its config shape, cold, against its algorithmic bytes and
+    against a plain device copy of the same bytes (copy_us, frac_of_copy = copy_us / us)."""
     import synth
     stream = torch.cuda.Stream()
     rn = lambda *shape: torch.randn(shape, device=dev)
@@ -510,6 +513,17 @@ def run_rows(torch, stx, dev):
     out["c5_demix_overlap_add"] = time_call(torch, stream, mk_ola, lens * S * C * 4 + S * C * Lsong * 4)
     del plan
     torch.cuda.empty_cache()
+    # The practical ceiling at each row's size: a plain device copy (torch's copy_) moving the
+    # same bytes (half read, half written), timed the same cold way.
+    for name, r in out.items():
+        n = max(1, r["algorithmic_bytes"] // 8)
+
+        def mk_copy(n=n):
+            x, y = torch.empty(n, device=dev), torch.empty(n, device=dev)
+            return lambda: y.copy_(x)
+        cp = time_call(torch, stream, mk_copy, 8 * n)
+        r["copy_us"] = cp["us"]
+        r["frac_of_copy"] = round(cp["us"] / r["us"], 3)
     return out
 
 
