@@ -709,11 +709,14 @@ __global__ __launch_bounds__(256) void ew_flat_kernel(const float* __restrict__ 
 // read of x at these sizes.
 //
 // Workspace: [groups] shift | [groups][partial chunks][2] partial sums.
-// VEC float4 per thread: chunks of 1024 * VEC floats. Pass 1 uses 4; pass 2 uses 1 (more
-// blocks, shorter latency chains) unless a launch has at least kGnWideBlocks chunks of 4096
-// floats, where 4 amortises each block's statistics over four times as many elements.
-constexpr int kGnVecPartial = 4, kGnVecApplyNarrow = 1, kGnVecApplyWide = 4;
+// VEC float4 per thread: chunks of 1024 * VEC floats, chosen per launch by the group span
+// (measured at the HTDemucs shapes): pass 1 uses 4 from 2M floats, 2 from 768K, else 1 (more,
+// shorter blocks for small groups); pass 2 uses 1 (more blocks, shorter latency chains) unless
+// a launch has at least kGnWideBlocks chunks of 4096 floats, where 4 amortises each block's
+// statistics over four times as many elements.
+constexpr int kGnVecApplyNarrow = 1, kGnVecApplyWide = 4;
 constexpr long long kGnWideBlocks = 768;
+inline int gn_partial_vec(long long span) { return span >= (2LL << 20) ? 4 : span >= (768LL << 10) ? 2 : 1; }
 template <int VEC> constexpr int gn_chunk() { return 256 * 4 * VEC; }
 
 enum AffineKind { AFF_NONE = 0, AFF_CHANNEL = 1, AFF_NE0 = 2, AFF_GENERAL = 3 };
@@ -738,6 +741,7 @@ struct GroupNormArgs {
     long long cpg;           // channels per group
     int groups;              // groups per ne3 slice
     int chunks;              // partial chunks per group (max over groups)
+    int pchunk;              // floats per partial chunk
     float eps;
     int vec;                 // all group spans 16-byte aligned
 };
@@ -813,10 +817,9 @@ __device__ __forceinline__ void gn_write_partial(const GroupNormArgs& a, int gt,
 }
 
 // mean and 1/sqrt(var + eps) of group gt from its partial sums (fixed order).
-template <int VEC>
 __device__ __forceinline__ void gn_stats(const GroupNormArgs& a, int gt, unsigned count, double shift, double* red,
                                          double& mean, double& rstd) {
-    const int nch = (int)((count + gn_chunk<VEC>() - 1) / gn_chunk<VEC>());
+    const int nch = (int)((count + (unsigned)a.pchunk - 1) / (unsigned)a.pchunk);
     const double* part = a.part + (size_t)gt * a.chunks * 2;
     double s1 = 0.0, s2 = 0.0;
     for (int k = threadIdx.x; k < nch; k += 256) {
@@ -900,8 +903,9 @@ __device__ __forceinline__ void gn_store(const GroupNormArgs& a, float* yg, unsi
     }
 }
 
+template <int VEC>
 __global__ __launch_bounds__(256) void gn_partial_kernel(GroupNormArgs a) {
-    constexpr int VEC = kGnVecPartial, CH = gn_chunk<VEC>();
+    constexpr int CH = gn_chunk<VEC>();
     __shared__ double red[8];
     const int gt = (int)blockIdx.y;
     long long begin, c0, i3;
@@ -933,7 +937,7 @@ __global__ __launch_bounds__(256) void gn_apply_kernel(GroupNormArgs a) {
     gn_load<VEC>(a, a.x + begin, lo, hi, v, ok);               // in flight while the stats add up
     gn_affine<AK, VEC>(a, lo, c0, i3, ok, wv, bv);
     double mean, rstd;
-    gn_stats<kGnVecPartial>(a, gt, count, a.shift[gt], red, mean, rstd);   // shift from pass 1
+    gn_stats(a, gt, count, a.shift[gt], red, mean, rstd);     // shift from pass 1
     gn_store<GELU, VEC>(a, a.y + begin, lo, hi, mean, rstd, v, ok, wv, bv);
 }
 
@@ -1228,6 +1232,7 @@ Affine make_affine(const stx_tensor* t, const stx_tensor* x, const char* what) {
 
 struct GnPlan {
     long long cpg, groups, groups_total, chunks_partial, chunks_apply;
+    int pvec;                                            // pass 1 width
     bool wide;                                           // pass 2 with kGnVecApplyWide
     size_t shift_off, part_off, bytes;                   // workspace layout
 };
@@ -1238,8 +1243,9 @@ GnPlan gn_plan(const stx_tensor* a, int n_groups) {
     p.groups = (a->ne[2] + p.cpg - 1) / p.cpg;
     p.groups_total = p.groups * a->ne[3];
     const long long span = p.cpg * a->ne[0] * a->ne[1];
-    p.chunks_partial = (span + gn_chunk<kGnVecPartial>() - 1) / gn_chunk<kGnVecPartial>();
-    p.wide = p.chunks_partial * p.groups_total >= kGnWideBlocks;
+    p.pvec = gn_partial_vec(span);
+    p.chunks_partial = (span + 1024LL * p.pvec - 1) / (1024LL * p.pvec);
+    p.wide = (span + gn_chunk<kGnVecApplyWide>() - 1) / gn_chunk<kGnVecApplyWide>() * p.groups_total >= kGnWideBlocks;
     const long long cha = p.wide ? gn_chunk<kGnVecApplyWide>() : gn_chunk<kGnVecApplyNarrow>();
     p.chunks_apply = (span + cha - 1) / cha;
     const size_t g = (size_t)std::max<long long>(1, p.groups_total);
@@ -1253,8 +1259,11 @@ GnPlan gn_plan(const stx_tensor* a, int n_groups) {
 template <int AK, bool GELU>
 void launch_group_norm(GroupNormArgs g, const GnPlan& p, hipStream_t s) {
     g.chunks = (int)p.chunks_partial;
-    hipLaunchKernelGGL(gn_partial_kernel, dim3((unsigned)p.chunks_partial, (unsigned)p.groups_total), dim3(256), 0, s,
-                       g);
+    g.pchunk = 1024 * p.pvec;
+    const dim3 grid1((unsigned)p.chunks_partial, (unsigned)p.groups_total);
+    if (p.pvec == 4) hipLaunchKernelGGL(gn_partial_kernel<4>, grid1, dim3(256), 0, s, g);
+    else if (p.pvec == 2) hipLaunchKernelGGL(gn_partial_kernel<2>, grid1, dim3(256), 0, s, g);
+    else hipLaunchKernelGGL(gn_partial_kernel<1>, grid1, dim3(256), 0, s, g);
     launch_check("gn_partial_kernel");
     if (p.wide)
         hipLaunchKernelGGL((gn_apply_kernel<AK, GELU, kGnVecApplyWide>),
