@@ -846,6 +846,28 @@ __device__ __forceinline__ float affine_at(const Affine& f, long long c, unsigne
 template <int AK, int VEC>
 __device__ __forceinline__ void gn_affine(const GroupNormArgs& a, unsigned lo, long long c0, long long i3,
                                           const bool (&ok)[4 * VEC], float (&wv)[4 * VEC], float (&bv)[4 * VEC]) {
+    if constexpr (AK == AFF_CHANNEL) {
+        if (a.plane >= 4) {
+            // Four consecutive elements lie in channel c or c + 1: two loads of each operand per
+            // group (clamped to a valid channel, unconditional), then a selection per element.
+#pragma unroll
+            for (int k = 0; k < VEC; k++) {
+                const unsigned p = lo + (k * 256 + threadIdx.x) * 4;
+                const unsigned cp = fast_div(p, a.plane, a.rplane), q = p - cp * a.plane;
+                const long long cl = a.ne2 - 1;
+                const long long c = min(c0 + cp, cl), c1 = min(c0 + cp + 1, cl);
+                const float w0 = a.w.p ? a.w.p[c] : 1.f, w1 = a.w.p ? a.w.p[c1] : 1.f;
+                const float b0 = a.b.p ? a.b.p[c] : 0.f, b1 = a.b.p ? a.b.p[c1] : 0.f;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const bool in = ok[4 * k + j], next = q + j >= a.plane;
+                    wv[4 * k + j] = in ? (next ? w1 : w0) : 1.f;
+                    bv[4 * k + j] = in ? (next ? b1 : b0) : 0.f;
+                }
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int k = 0; k < VEC; k++) {
         const unsigned p = lo + (k * 256 + threadIdx.x) * 4;
