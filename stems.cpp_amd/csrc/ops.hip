@@ -148,34 +148,57 @@ __device__ __forceinline__ float rcp_nr(float d) {
     return fmaf(r, fmaf(-d, r, 1.0f), r);
 }
 
-// erfcx(u) = exp(u^2) erfc(u) for u >= 0.7, by Shepherd & Laframboise's substitution
-// (Chebyshev approximation of (1 + 2u) exp(u^2) erfc(u), J. Comput. Phys. 1981):
-// (1 + 2u) erfcx(u) = P(t), t = (u - 2.5) / (u + 2.5). P has degree 10, fitted for this
-// library by weighted least squares in double to relative error 1.3e-9 on u >= 0.7.
-__device__ __forceinline__ float erfcx_scaled(float u) {
-    constexpr float K = 2.5f;
-    const float t = (u - K) * rcp_nr(u + K);
-    float p = -1.919762726e-04f;
-    p = fmaf(p, t, 5.875547067e-04f);
-    p = fmaf(p, t, 5.759609630e-04f);
-    p = fmaf(p, t, -4.387959838e-03f);
-    p = fmaf(p, t, 9.082683246e-04f);
-    p = fmaf(p, t, 3.276548162e-02f);
-    p = fmaf(p, t, -1.029642969e-01f);
-    p = fmaf(p, t, 1.576293558e-01f);
-    p = fmaf(p, t, -9.902466089e-02f);
-    p = fmaf(p, t, -1.223567501e-01f);
-    p = fmaf(p, t, 1.264838219e+00f);
-    return p * rcp_nr(fmaf(2.f, u, 1.f));
+// erfcx(u) = exp(u^2) erfc(u) for u >= 0.7 in the form of Hastings' approximation
+// (Abramowitz & Stegun 7.1.26): erfcx(u) = t P(t), t = 1 / (1 + 0.47 u), one reciprocal. P has
+// degree 11, fitted for this library by weighted least squares in double, its coefficients
+// rounded to float one at a time from the top with the rest refitted (relative error 6.4e-10
+// on u >= 0.7).
+__device__ __forceinline__ float erfcx_tail(float u) {
+    const float t = rcp_nr(fmaf(0.47f, u, 1.f));
+    float p = 4.219519719e-02f;
+    p = fmaf(p, t, -1.974450797e-01f);
+    p = fmaf(p, t, 3.449501991e-01f);
+    p = fmaf(p, t, -2.401850075e-01f);
+    p = fmaf(p, t, 3.913874179e-02f);
+    p = fmaf(p, t, -5.485558510e-02f);
+    p = fmaf(p, t, 2.373995818e-02f);
+    p = fmaf(p, t, 9.893336892e-02f);
+    p = fmaf(p, t, 1.773130894e-01f);
+    p = fmaf(p, t, 2.358806431e-01f);
+    p = fmaf(p, t, 2.651691437e-01f);
+    p = fmaf(p, t, 2.651691139e-01f);
+    return t * p;
+}
+
+// gelu(x + dx) for |x| >= 1 (see gelu_erf_hl).
+__device__ __forceinline__ float gelu_tail(float x, float dx) {
+    // No contraction here: yh must be the rounded product that the fma residual refers to
+    // (hipcc fuses a separate multiply and add by default, which would count the residual twice).
+#pragma clang fp contract(off)
+    constexpr float C1 = -0x1.715476p-1f;                 // -1/(2 ln 2) = C1 + C2 to 3e-16
+    constexpr float C2 = -0x1.4ae0cp-27f;
+    const float h = x * x;
+    const float l = fmaf(x, x, -h);                       // x^2 = h + l exactly
+    const float yh = h * C1;
+    const float yl = fmaf(h, C1, -yh) + fmaf(h, C2, fmaf(2.f * x, dx, l) * C1);
+    const float n = rintf(yh);
+    const float e = ldexpf(__builtin_amdgcn_exp2f((yh - n) + yl), (int)n);
+    const float g = 0.5f * e * erfcx_tail(fabsf(x) * 0.70710678118654752440f);   // Phi(-|x|)
+    const float ph = x < 0.f ? g : 1.f - g;
+    // x < -15 (including -inf, where x^2 overflows): 0 * x, keeping -0 and NaN.
+    return x > 10.f ? x + dx : x < -15.f ? x * 0.f : fmaf(ph, dx, x * ph);
 }
 
 // gelu(x) = x Phi(x), Phi(x) = (1 + erf(x/sqrt2)) / 2, to a few ulp everywhere, without a
-// library erf/erfc call (one short path per sign, ~50 VALU instructions per element).
+// library erf/erfc/exp call (one short path per sign, ~12 VALU instructions for |x| < 1 and
+// ~42 beyond).
 //   |x| < 1:  erf(x/sqrt2) = x Q(x^2), Q of degree 5 fitted for this library (relative error
 //             of Phi 1.6e-9 on |x| <= 1).
-//   |x| >= 1: Phi(-|x|) = exp(-x^2/2) erfcx(|x|/sqrt2) / 2 with x^2 split exactly into head and
-//             tail by an fma, so the exponential costs one ulp instead of ~x^2 ulps; Phi(x) is
-//             that or 1 minus it.
+//   |x| >= 1: Phi(-|x|) = exp(-x^2/2) erfcx(|x|/sqrt2) / 2; Phi(x) is that or 1 minus it. The
+//             exponential is 2^y with y = -(x + dx)^2 / (2 ln 2) formed as a head and tail
+//             (x^2 split exactly by an fma, the constant split in two floats), so it costs one
+//             ulp instead of ~x^2 ulps; 2^y = 2^n * 2^f, n = rint(y head), f in [-1/2, 1/2] on
+//             the hardware exp2.
 //   x > 10:   Phi(x) = 1 to float precision; x < -15: gelu underflows (0 * x keeps -0, NaN).
 // gelu_erf_hl takes its argument as a float head x plus a small tail dx (x + dx is the value)
 // so that a fused producer can hand over a double result without rounding it first: in the
@@ -194,15 +217,7 @@ __device__ __forceinline__ float gelu_erf_hl(float x, float dx) {
         const float ph = 0.5f * fmaf(x, q, 1.f);
         return fmaf(ph, dx, x * ph);
     }
-    if (x > 10.f) return x + dx;
-    if (!(x > -15.f)) return x * 0.f;
-    const float h = x * x;
-    const float l = fmaf(x, x, -h);                      // x^2 = h + l exactly
-    float e = expf(-0.5f * h);
-    e = fmaf(e, -fmaf(x, dx, 0.5f * l), e);              // * exp(-l/2 - x dx), first order
-    const float g = 0.5f * e * erfcx_scaled(a * 0.70710678118654752440f);   // Phi(-|x|)
-    const float ph = x < 0.f ? g : 1.f - g;
-    return fmaf(ph, dx, x * ph);
+    return gelu_tail(x, dx);
 }
 
 __device__ __forceinline__ float gelu_erf(float x) { return gelu_erf_hl(x, 0.f); }
