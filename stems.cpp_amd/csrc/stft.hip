@@ -323,9 +323,13 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
     constexpr int TPJ = C::TPJ;
     constexpr int NT = JOBS * TPJ;
     constexpr bool WIN_LDS = (size_t)JOBS * C::PADN * 8 + TwTable<N>::SIZE * 8 + N * 4 <= 160 * 1024;
+    // Reciprocal window-squared envelope per position R = J mod hop where every covering
+    // frame exists (R < N suffices: positions past N have no frame).
+    constexpr bool ENV_LDS = WIN_LDS && (size_t)JOBS * C::PADN * 8 + TwTable<N>::SIZE * 8 + N * 8 <= 160 * 1024;
     __shared__ float2 lds[JOBS * C::PADN];
     __shared__ float2 twt[TwTable<N>::SIZE];
     __shared__ float wl[WIN_LDS ? N : 2];
+    __shared__ float inv_env[ENV_LDS ? N : 2];
 
     const int lb = xcd_block();
     if (lb >= a.nblocks) return;
@@ -450,13 +454,32 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
     }
 
     // Envelope: win^2 summed over the envelope frames 0 <= tf < env_frames covering J, in frame
-    // order (src/stft.h:130,187); out = acc / env where env > 1e-11, else 0.
+    // order (src/stft.h:130,187); out = acc / env where env > 1e-11, else 0. Where all K + 1
+    // frames of J exist, env depends on R = J mod hop only: its reciprocal (0 for env <= 1e-11)
+    // comes from a table built once per workgroup (the product differs from the quotient by at
+    // most an ulp); elsewhere (the signal's ends) the sum runs here.
+    if constexpr (ENV_LDS) {
+        const int nr = min(hop, N);
+        for (int R = tid; R < nr; R += NT) {
+            const int K = R <= rK ? K0 : K0 - 1;
+            float env = 0.f;
+            for (int i = K; i >= 0; i--) {               // frame order: position R + K*hop first
+                const float w = win[R + i * hop];
+                env += w * w;
+            }
+            inv_env[R] = env > 1e-11f ? 1.f / env : 0.f;
+        }
+        __syncthreads();
+    }
     float* oc = a.out + (size_t)c * a.out_len;
     walk(tid, [&](int q, int tf0, int s_first, int K) {
         const int J = J0 + q * NT + tid;
         if (J >= J1) return;
         float y = 0.f;
-        if (J < a.valid_end) {
+        if (ENV_LDS && J < a.valid_end && tf0 >= 0 && tf0 + K < a.env_frames) {
+            const float r = inv_env[s_first - K * hop];
+            y = r > 0.f ? acc[q] * r : 0.f;
+        } else if (J < a.valid_end) {
             const int i0 = max(0, -tf0), i1 = min(K, a.env_frames - 1 - tf0);
             unsigned pos = (unsigned)(s_first - i0 * hop);
             float env = 0.f;
