@@ -155,7 +155,7 @@ __global__ __launch_bounds__(256) void demix_ola_kernel(DemixArgs a, const float
         }
     }
     const size_t stride = (size_t)planes * a.chunk;          // one chunk's output
-    if (vec && all4) {
+    if (vec && all4 && nk > 0) {                             // nk = 0: a gap between chunks (step > chunk)
         // Chunks past nk re-read chunk nk - 1 and add +0.0 (an exact no-op: res never holds
         // -0.0), so that every load is used and none is sunk behind a branch.
         const float* src[NK];

@@ -52,10 +52,11 @@ def host(t):
 # The last two cover 8 chunks over 4 samples (the limit of the 4-sample kernel) and 11 (the
 # kernel for any overlap).
 # Chunks covering 4 consecutive samples, ceil((chunk + 3) / step): 5, 5, 2, 5, 3, 4, 5, 8, 11
-# (the generic kernel), 6, 7, 2.
+# (the generic kernel), 6, 7, 2, and 1 with gaps between the chunks (step > chunk: uncovered
+# samples are 0/0 -> 0).
 CASES = [(7938000, 352800, 88200), (1000, 100, 25), (1000, 100, 100), (150, 100, 25), (60, 100, 50),
          (1001, 97, 31), (100000, 8000, 2000), (5003, 64, 9), (2000, 100, 10), (1000, 100, 20), (1000, 100, 17),
-         (4000, 400, 400)]
+         (4000, 400, 400), (1000, 100, 152)]
 
 
 @pytest.mark.parametrize("length,chunk,step", CASES)
