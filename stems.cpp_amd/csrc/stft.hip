@@ -149,12 +149,16 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void stft_kernel(StftArgs a) {
         return make_float2((er + w.x * orr - w.y * oi) * hs, (ei + w.x * oi + w.y * orr) * hs);
     };
     if (a.layout == STX_SPEC_F_MAJOR) {
-        for (int e = tid; e < a.F * JOBS; e += NT) {
-            const int k = e / JOBS, g = e % JOBS;
-            if (f0 + g >= a.jobs) continue;
-            int tt = t0 + g, cc = c0;
-            while (tt >= a.T) { tt -= a.T; cc++; }
-            a.spec[((size_t)cc * a.F + k) * a.T + tt] = bin(k, g, tw_lookup<N>(twt, k));
+        // Element e = k*JOBS + g: with NT a multiple of JOBS every thread keeps one frame
+        // g = tid % JOBS and takes bins tid / JOBS + i * NT / JOBS, so that the JOBS lanes of a
+        // bin write consecutive frames of its row.
+        const int g = tid % JOBS;
+        int tt = t0 + g, cc = c0;
+        while (tt >= a.T) { tt -= a.T; cc++; }
+        if (f0 + g < a.jobs) {
+            float2* col = a.spec + (size_t)cc * a.F * a.T + tt;
+#pragma unroll 4
+            for (int k = tid / JOBS; k < a.F; k += NT / JOBS) col[(size_t)k * a.T] = bin(k, g, tw_lookup<N>(twt, k));
         }
     } else {
         // Row of frame g, then each bin's twiddle once for all JOBS frames.
@@ -165,6 +169,7 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void stft_kernel(StftArgs a) {
             while (tt >= a.T) { tt -= a.T; cc++; }
             rows[g] = f0 + g < a.jobs ? a.spec + ((size_t)cc * a.T + tt) * a.F : nullptr;
         }
+#pragma unroll 4
         for (int k = tid; k < a.F; k += NT) {
             const float2 w = tw_lookup<N>(twt, k);
 #pragma unroll
