@@ -22,13 +22,16 @@ HIP events on the stream the kernels run on. traffic: HBM bytes of that op
 per step measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter
 on a plain copy of known size), read from profiles/pmc_traffic.json when present.
 cpu_baseline: the C oracle (a double-precision restatement; ggml's CPU backend is not in the
-reference tree), single-threaded, on whole steps of the same workload for a bounded time.
+reference tree) on whole steps of the same workload for a bounded time, on as many threads as
+physical cores (ggml's default; capped by OMP_NUM_THREADS where the job sets it), with the
+single-thread figure beside it.
 
 The same line carries the spectral half of the metric, STFT+iSTFT Msamples/s:
   spectral.htdemucs_round_trip: stx_htdemucs_spec + stx_htdemucs_ispec (src/stft.h:76-140) on
     stereo 343,980 samples, n_fft 4096 (hop 1024), reference f-major layout; its CPU baseline is
     the reference's own src/stft.h compiled from the reference sources (oracle/_ref) or, where
-    that is absent, the C oracle;
+    that is absent, the C oracle, single-threaded as the reference runs it, with a second figure
+    spreading channel round trips over the physical cores;
   spectral.roformer_chunk: stx_torch_stft (n_fft 2048, hop 441) -> stx_band_scatter_apply with
     60 mel bands and uniform [-1, 1] masks (one stem) -> stx_torch_istft on one stereo chunk of
     352,800 samples (src/roformer.cpp:217-283).
@@ -248,9 +251,46 @@ def run_ops(args, torch, stx, dev):
     return res, ops
 
 
+def cpu_threads():
+    """Physical cores, capped by the job's OMP_NUM_THREADS share when it is set."""
+    try:
+        import psutil
+        n = psutil.cpu_count(logical=False) or os.cpu_count() or 1
+    except ImportError:
+        n = os.cpu_count() or 1
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
+def timed_threads(n, unit, budget_s):
+    """Runs unit() repeatedly on n threads for about budget_s seconds; (units done, seconds). The
+    oracle is called through ctypes, which releases the GIL, so the threads run in parallel."""
+    import threading
+    counts = [0] * n
+    deadline = time.perf_counter() + budget_s
+
+    def work(i):
+        while True:
+            unit()
+            counts[i] += 1
+            if time.perf_counter() >= deadline:
+                break
+    t0 = time.perf_counter()
+    th = [threading.Thread(target=work, args=(i,)) for i in range(n)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    return sum(counts), time.perf_counter() - t0
+
+
 def cpu_ops_baseline(budget_s):
+    """The C oracle (a double-precision restatement; ggml's CPU backend is absent) on whole steps
+    of the op set: one step per thread at a time, on as many threads as physical cores (ggml's
+    default thread count), and on one thread."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
-    import numpy as np
     import oracle_lib
     import synth
     o = oracle_lib.ops()
@@ -259,25 +299,26 @@ def cpu_ops_baseline(budget_s):
         data.append((synth.normal(C, (C, 1, T), 1.0), synth.normal(C + 1, (C, 1, 1), 1.0),
                      synth.normal(C + 2, (C, 1, 1), 1.0), synth.normal(C + 3, (2 * C, 1, T), 1.0),
                      synth.normal(C + 4, (C, 1, T), 1.0), synth.normal(C + 5, (C, 1, 1), 0.1)))
-    steps = 0
-    t0 = time.perf_counter()
-    while True:
+
+    def step():
         for x, w, b, h, r, s in data:
             o.group_norm(x, 1, EPS, w, b, gelu=True)
             g = o.glu(h, 2)
             o.binary("mul_add", r, g, s)
-        steps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
     step_bytes = sum(sum(v) for v in op_bytes().values())
+    n = cpu_threads()
+    steps, el = timed_threads(n, step, budget_s / 2)
+    steps1, el1 = timed_threads(1, step, budget_s / 2)
     return {
         "value": round(steps * step_bytes / el / 1e9, 3),
         "unit": "GB/s",
-        "cores": 1,
+        "cores": n,
         "kind": "port",
-        "sample": f"{steps} whole steps of the same op set ({el:.1f} s, single thread): the C oracle, a "
-                  "double-precision restatement of the ops (ggml's CPU backend is absent from the reference)",
+        "sample": f"{steps} whole steps of the same op set in {el:.1f} s on {n} threads (one step per thread at a "
+                  "time): the C oracle, a double-precision restatement of the ops (ggml's CPU backend is absent "
+                  "from the reference)",
+        "single_thread": {"value": round(steps1 * step_bytes / el1 / 1e9, 3), "unit": "GB/s", "cores": 1,
+                          "sample": f"{steps1} steps in {el1:.1f} s"},
     }
 
 
@@ -528,6 +569,9 @@ def run_rows(torch, stx, dev):
 
 
 def cpu_spectral_baseline(budget_s):
+    """The reference's own src/stft.h (oracle/_ref; the C restatement where that is absent) on the
+    c1 round trip: single-threaded as the reference runs it, and with the channels' round trips
+    spread over as many threads as physical cores."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib
     import synth
@@ -535,20 +579,19 @@ def cpu_spectral_baseline(budget_s):
     lib = oracle_lib.reference() if kind == "reference" else oracle_lib.oracle()
     C, L, n_fft = 2, 343980, 4096
     x = synth.normal(2024, (C, L), 0.1)
-    reps = 0
-    t0 = time.perf_counter()
-    while True:
-        for c in range(C):
-            s = lib.htdemucs_spec(x[c], n_fft)
-            lib.htdemucs_ispec(s, n_fft, L)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
-    return {"value": round(reps * C * L / el / 1e6, 3), "unit": "Msamples/s", "cores": 1, "kind": kind,
-            "sample": f"{reps} HTDemucs-spec STFT->iSTFT round trips of stereo {L} samples ({el:.1f} s, single "
-                      "thread, double precision, " + ("src/stft.h compiled from the reference sources" if kind ==
-                                                      "reference" else "C restatement of src/stft.h") + ")"}
+
+    def channel_round_trip(c=0):
+        s = lib.htdemucs_spec(x[c], n_fft)
+        lib.htdemucs_ispec(s, n_fft, L)
+    what = "src/stft.h compiled from the reference sources" if kind == "reference" else "C restatement of src/stft.h"
+    reps1, el1 = timed_threads(1, channel_round_trip, budget_s / 2)
+    n = cpu_threads()
+    repsn, eln = timed_threads(n, channel_round_trip, budget_s / 2)
+    return {"value": round(reps1 * L / el1 / 1e6, 3), "unit": "Msamples/s", "cores": 1, "kind": kind,
+            "sample": f"{reps1} single-channel HTDemucs-spec STFT->iSTFT round trips of {L} samples ({el1:.1f} s, "
+                      f"single thread, double precision, {what})",
+            "multi_core": {"value": round(repsn * L / eln / 1e6, 3), "unit": "Msamples/s", "cores": n,
+                           "sample": f"{repsn} channel round trips in {eln:.1f} s on {n} threads"}}
 
 
 def main():
