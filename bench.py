@@ -536,6 +536,33 @@ def run_rows(torch, stx, dev):
         return lambda: stx.gelu_erf(h, bias=bb, out=y, stream=stream)
     out["c4_gelu_ff_bias"] = time_call(torch, stream, mk_ff, 2 * 60 * 801 * 1536 * 4 + 1536 * 4)
 
+    # c4 layout glue: the q/k/v split + RoPE + permutes of one attention layer (time axis: 60
+    # sequences of 801 frames; band axis: 801 sequences of 60 bands), the head merge, the
+    # [D, B, T] -> [D, T, B] transpose between the two transformers and the band-split concat.
+    for name, (b, n) in (("c4_qkv_rope_split_time", (60, 801)), ("c4_qkv_rope_split_band", (801, 60))):
+        def mk_split(b=b, n=n):
+            qkv = rn(b, n, 1536)
+            q, k = torch.empty((b, 8, n, 64), device=dev), torch.empty((b, 8, n, 64), device=dev)
+            vt = torch.empty((b, 8, 64, n), device=dev)
+            pos = torch.arange(n, dtype=torch.int32, device=dev)
+            return lambda: stx.qkv_rope_split(qkv, pos, 8, 10000.0, out=(q, k, vt), stream=stream)
+        out[name] = time_call(torch, stream, mk_split, 2 * b * n * 1536 * 4 + n * 4)
+
+    def mk_merge():
+        o, y = rn(60, 8, 801, 64), torch.empty((60, 801, 8, 64), device=dev)
+        return lambda: stx.merge_heads(o, out=y, stream=stream)
+    out["c4_merge_heads_time"] = time_call(torch, stream, mk_merge, 2 * 60 * 8 * 801 * 64 * 4)
+
+    def mk_transpose():
+        x, y = rn(801, 60, 384), torch.empty((60, 801, 384), device=dev)
+        return lambda: stx.cont_permute(x, (0, 2, 1, 3), out=y, stream=stream)
+    out["c4_permute_dbt"] = time_call(torch, stream, mk_transpose, 2 * 60 * 801 * 384 * 4)
+
+    def mk_concat():
+        xs, y = [rn(801, 1, 384) for _ in range(60)], torch.empty((801, 60, 384), device=dev)
+        return lambda: stx.concat(xs, 1, out=y, stream=stream)
+    out["c4_band_concat"] = time_call(torch, stream, mk_concat, 2 * 60 * 801 * 384 * 4)
+
     # c5: full-song demix (180 s stereo, chunk 352,800, step 88,200, 4 stems).
     Lsong, chunk, step, S = 7938000, 352800, 88200, 4
     plan = stx.Demix(Lsong, C, chunk, step)

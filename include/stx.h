@@ -366,6 +366,40 @@ STX_API stx_status stx_rope_ext(const stx_tensor* a, const int32_t* pos, const s
                                 int n_ctx_orig, float freq_base, float freq_scale, float ext_factor, float attn_factor,
                                 float beta_fast, float beta_slow, stx_stream stream);
 
+/* ------------------------------------------------------------------------------------------
+ * Layout glue around attention and the band split: each replaces a chain of ggml view / cont /
+ * permute / concat nodes by one pass over HBM, with results identical to that chain.
+ * ---------------------------------------------------------------------------------------- */
+
+/* The q/k/v split of RoFormer attention (src/roformer.cpp:101-112): qkv is the projection
+ * output [3 * n_head * dh, N, batch] ('b n (qkv h d)'); pos is device int32[N]. Writes
+ *   q  = cont(permute(rope_ext(part(0), pos, dh, mode 0, ...), 0, 2, 1, 3))   [dh, N, n_head, batch]
+ *   k  = the same for part(1)
+ *   vt = cont(permute(part(2), 1, 2, 0, 3))                                  [N, dh, n_head, batch]
+ * where part(i) is the dh x n_head slice at i * n_head * dh of each row. dh is q->ne[0]; 32, 64
+ * and 128 are built (others are UNSUPPORTED). The rotation is stx_rope_ext's, bit for bit. q, k
+ * and vt are dense and must not overlap qkv; qkv rows and q, k are 16-byte aligned. */
+STX_API stx_status stx_qkv_rope_split(const stx_tensor* qkv, const int32_t* pos, int n_head, float freq_base,
+                                      float freq_scale, float attn_factor, const stx_tensor* q,
+                                      const stx_tensor* k, const stx_tensor* vt, stx_stream stream);
+
+/* The head merge after attention (src/roformer.cpp:133-137): dst = cont(permute(o, 0, 2, 1, 3)),
+ * o [dh, N, H, batch] -> dst [dh, H, N, batch], times reshape_4d(gates, 1, H, N, batch) when
+ * gates (the sigmoid output, [1, H, N, batch]) is not NULL, rounded once like ggml_mul. */
+STX_API stx_status stx_merge_heads(const stx_tensor* o, const stx_tensor* gates, const stx_tensor* dst,
+                                   stx_stream stream);
+
+/* ggml_cont(ggml_permute(a, ax0, ax1, ax2, ax3)) (src/roformer.cpp:112,133,182,184,190):
+ * dimension i of a becomes dimension ax_i of dst. dst must not overlap a. */
+STX_API stx_status stx_cont_permute(const stx_tensor* a, int ax0, int ax1, int ax2, int ax3, const stx_tensor* dst,
+                                    stx_stream stream);
+
+/* ggml_concat of n_srcs tensors along dim, in order (src/roformer.cpp:52-60 concat_all, :132,
+ * :178; n_srcs = 2 is ggml_concat itself): every other dimension of the sources equals dst's,
+ * and their extents along dim add up to dst's. srcs is a host array of n_srcs descriptors. */
+STX_API stx_status stx_concat(const stx_tensor* const* srcs, int n_srcs, int dim, const stx_tensor* dst,
+                              stx_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -33,6 +33,11 @@
  *     difference). ggml-specific rounding (the float theta recurrence of ggml's RoPE, its float
  *     softmax and norm arithmetic) is parity unpinned: ggml's sources are not in the reference.
  *   orc_binary: numpy's float32 arithmetic on explicitly tiled operands, bit for bit.
+ *   orc_cont_permute / orc_concat / orc_merge_heads: numpy's transpose, concatenate and
+ *     multiply, bit for bit, and the shapes the reference's own comments give for its permutes
+ *     (src/roformer.cpp:112-114,133: [dh, N, H, batch] and [N, dh, H, batch] from
+ *     [dh, H, N, batch]). orc_qkv_rope_split: its q and k against the complex-multiplication
+ *     RoPE on numpy's slices of qkv, and its vt bit for bit against numpy's transpose.
  *   orc_demix_*: the chunk table the survey of the reference derived for 180 s at chunk 352,800
  *     and step 88,200 (96 chunks, four without fade-out, short chunks of 264,600 (reflect),
  *     176,400 and 88,200 (zero) samples), torch.linspace(0, 1, fade) in float32 for the fade
@@ -109,6 +114,13 @@ int orc_binary(int op, const float* a, const int64_t ne[4], const float* b, cons
                const int64_t cne[4], float* y);
 int orc_rope(const float* x, const int64_t ne[4], const int32_t* pos, int n_dims, int mode, float freq_base,
              float freq_scale, float attn_factor, float* y);
+
+/* Layout glue (layout_oracle.c). x and y contiguous; nes holds 4 extents per source. */
+int orc_cont_permute(const float* x, const int64_t ne[4], const int ax[4], float* y);
+int orc_concat(const float* const* xs, const int64_t* nes, int n, int dim, float* y);
+int orc_qkv_rope_split(const float* qkv, int64_t dh, int64_t H, int64_t N, int64_t batch, const int32_t* pos,
+                       float freq_base, float freq_scale, float attn_factor, float* q, float* k, float* vt);
+int orc_merge_heads(const float* o, const int64_t ne[4], const float* gates, float* y);
 
 #ifdef __cplusplus
 }

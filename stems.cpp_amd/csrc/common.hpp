@@ -89,6 +89,29 @@ __device__ __forceinline__ int xcd_block() {
 
 inline bool is_pow2(long long n) { return n >= 1 && (n & (n - 1)) == 0; }
 
+// Division of any n < 2^32 by a fixed d >= 1 with one high multiply, one add and one shift:
+// the round-up method of Granlund and Montgomery, "Division by invariant integers using
+// multiplication" (PLDI 1994), Fig. 4.1 with N = 32: l = ceil(log2 d),
+// m = floor(2^32 (2^l - d) / d) + 1 (fits 32 bits), q = (mulhi(m, n) + n) >> l, with the
+// add done in 64 bits so it cannot overflow.
+struct FastDiv {
+    unsigned d = 1, m = 1, l = 0;
+    FastDiv() = default;
+    explicit FastDiv(unsigned divisor) : d(divisor) {
+        while ((1ull << l) < d) l++;
+        m = (unsigned)((((1ull << l) - d) << 32) / d + 1);
+    }
+    __host__ __device__ __forceinline__ unsigned div(unsigned n) const {
+#ifdef __HIP_DEVICE_COMPILE__
+        const unsigned hi = __umulhi(m, n);
+#else
+        const unsigned hi = (unsigned)(((unsigned long long)m * n) >> 32);
+#endif
+        return (unsigned)(((unsigned long long)hi + n) >> l);
+    }
+    __host__ __device__ __forceinline__ unsigned mod(unsigned n) const { return n - div(n) * d; }
+};
+
 // Compute units of the current device (cached per device id).
 inline int device_cus() {
     static std::atomic<int> cache[64];

@@ -78,6 +78,10 @@ _SIGNATURES = {
     "stx_glu_mul_add": (_i, [_vp, _vp, _i, _vp, _vp, _vp]),
     "stx_rope_ext": (_i, [_vp, _vp, _vp, _i, _i, _i, ctypes.c_float, ctypes.c_float, ctypes.c_float,
                           ctypes.c_float, ctypes.c_float, ctypes.c_float, _vp]),
+    "stx_qkv_rope_split": (_i, [_vp, _vp, _i, ctypes.c_float, ctypes.c_float, ctypes.c_float, _vp, _vp, _vp, _vp]),
+    "stx_merge_heads": (_i, [_vp, _vp, _vp, _vp]),
+    "stx_cont_permute": (_i, [_vp, _i, _i, _i, _i, _vp, _vp]),
+    "stx_concat": (_i, [_vp, _i, _i, _vp, _vp]),
 }
 
 
@@ -609,4 +613,74 @@ def rope_ext(x, pos, n_dims, mode=0, freq_base=10000.0, freq_scale=1.0, ext_fact
     check(lib().stx_rope_ext(_t(x), _ptr(pos), _t(out), int(n_dims), int(mode), int(n_ctx_orig), float(freq_base),
                              float(freq_scale), float(ext_factor), float(attn_factor), float(beta_fast),
                              float(beta_slow), _stream(stream)))
+    return out
+
+
+# ------------------------------------------------------------------------ layout glue
+def qkv_rope_split(qkv, pos, n_head, freq_base=10000.0, freq_scale=1.0, attn_factor=1.0, out=None, stream=None):
+    """The q/k/v split of RoFormer attention, fused with RoPE and the permutes.
+
+    qkv: torch (batch, N, 3 * n_head * dh) = ggml [3*H*dh, N, batch]; pos: int32 device (N,).
+    Returns (q, k, vt) with torch shapes (batch, H, N, dh), (batch, H, N, dh), (batch, H, dh, N).
+    """
+    import torch
+    _require(pos, torch.int32, "pos")
+    batch, N, width = qkv.shape
+    dh = width // (3 * n_head)
+    if out is None:
+        q = torch.empty((batch, n_head, N, dh), dtype=qkv.dtype, device=qkv.device)
+        k = torch.empty_like(q)
+        vt = torch.empty((batch, n_head, dh, N), dtype=qkv.dtype, device=qkv.device)
+    else:
+        q, k, vt = out
+    check(lib().stx_qkv_rope_split(_t(qkv), _ptr(pos), int(n_head), float(freq_base), float(freq_scale),
+                                   float(attn_factor), _t(q), _t(k), _t(vt), _stream(stream)))
+    return q, k, vt
+
+
+def merge_heads(o, gates=None, out=None, stream=None):
+    """cont(permute(o, 0, 2, 1, 3)) [* gates]: torch (batch, H, N, dh) -> (batch, N, H, dh).
+
+    gates: torch (batch, N, H, 1) (ggml [1, H, N, batch]) or None.
+    """
+    import torch
+    if out is None:
+        b, H, N, dh = o.shape
+        out = torch.empty((b, N, H, dh), dtype=o.dtype, device=o.device)
+    check(lib().stx_merge_heads(_t(o), _t(gates), _t(out), _stream(stream)))
+    return out
+
+
+def ggml_permuted_shape(ne, axes):
+    """ne of ggml_permute(a, *axes) given a's ne (ggml order): a's dim i becomes dim axes[i]."""
+    out = [1, 1, 1, 1]
+    for i, ax in enumerate(axes):
+        out[ax] = ne[i]
+    return out
+
+
+def cont_permute(x, axes, out=None, stream=None):
+    """ggml_cont(ggml_permute(x, *axes)) on a torch tensor of up to 4 dims (ggml order = reversed)."""
+    import torch
+    if out is None:
+        ne = list(x.shape)[::-1] + [1] * (4 - x.dim())
+        pne = ggml_permuted_shape(ne, axes)
+        out = torch.empty(pne[::-1], dtype=x.dtype, device=x.device)
+    check(lib().stx_cont_permute(_t(x), int(axes[0]), int(axes[1]), int(axes[2]), int(axes[3]), _t(out),
+                                 _stream(stream)))
+    return out
+
+
+def concat(tensors, dim, out=None, stream=None):
+    """ggml_concat of a list of tensors along ggml dimension dim (0 = torch's last dim)."""
+    import torch
+    if out is None:
+        ref = tensors[0]
+        shape = list(ref.shape)
+        tdim = ref.dim() - 1 - dim
+        shape[tdim] = sum(t.shape[tdim] for t in tensors)
+        out = torch.empty(shape, dtype=ref.dtype, device=ref.device)
+    descs = [as_tensor(t) for t in tensors]
+    arr = (ctypes.c_void_p * len(descs))(*[ctypes.addressof(d) for d in descs])
+    check(lib().stx_concat(arr, len(descs), int(dim), _t(out), _stream(stream)))
     return out

@@ -253,6 +253,15 @@ class _Ops:
         L.orc_binary.argtypes = [_i, _vp, i64p, _vp, i64p, _vp, i64p, _vp]
         L.orc_rope.restype = _i
         L.orc_rope.argtypes = [_vp, i64p, _vp, _i, _i, ctypes.c_float, ctypes.c_float, ctypes.c_float, _vp]
+        L.orc_cont_permute.restype = _i
+        L.orc_cont_permute.argtypes = [_vp, i64p, ctypes.POINTER(ctypes.c_int), _vp]
+        L.orc_concat.restype = _i
+        L.orc_concat.argtypes = [_vp, i64p, _i, _i, _vp]
+        L.orc_qkv_rope_split.restype = _i
+        L.orc_qkv_rope_split.argtypes = [_vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _vp,
+                                         ctypes.c_float, ctypes.c_float, ctypes.c_float, _vp, _vp, _vp]
+        L.orc_merge_heads.restype = _i
+        L.orc_merge_heads.argtypes = [_vp, i64p, _vp, _vp]
         self.L = L
 
     @staticmethod
@@ -326,6 +335,57 @@ class _Ops:
         y = np.empty_like(x)
         if self.L.orc_rope(_np(x), _ne(x.shape), _np(pos), n_dims, mode, freq_base, freq_scale, attn_factor, _np(y)):
             raise ValueError("rope")
+        return y
+
+    def cont_permute(self, x, axes):
+        """ggml_cont(ggml_permute(x, *axes)); x is a numpy array of up to 4 dims (last = ne0)."""
+        x = self._f(x)
+        ne = list(x.shape)[::-1] + [1] * (4 - x.ndim)
+        yne = [1, 1, 1, 1]
+        for i, a in enumerate(axes):
+            yne[a] = ne[i]
+        y = np.empty(yne[::-1], np.float32)
+        if self.L.orc_cont_permute(_np(x), _ne(x.shape), (ctypes.c_int * 4)(*axes), _np(y)):
+            raise ValueError("cont_permute")
+        return y
+
+    def concat(self, xs, dim):
+        """ggml_concat of numpy arrays of equal rank along ggml dimension dim."""
+        xs = [self._f(x) for x in xs]
+        nes = []
+        for x in xs:
+            nes += list(_ne(x.shape))
+        shape = list(xs[0].shape)
+        ax = xs[0].ndim - 1 - dim
+        shape[ax] = sum(x.shape[ax] for x in xs)
+        y = np.empty(shape, np.float32)
+        ptrs = (ctypes.c_void_p * len(xs))(*[x.ctypes.data for x in xs])
+        if self.L.orc_concat(ptrs, (ctypes.c_int64 * len(nes))(*nes), len(xs), dim, _np(y)):
+            raise ValueError("concat")
+        return y
+
+    def qkv_rope_split(self, qkv, pos, n_head, freq_base=10000.0, freq_scale=1.0, attn_factor=1.0):
+        """qkv numpy (batch, N, 3*H*dh) -> q, k (batch, H, N, dh), vt (batch, H, dh, N)."""
+        qkv = self._f(qkv)
+        pos = np.ascontiguousarray(pos, dtype=np.int32)
+        batch, N, width = qkv.shape
+        dh = width // (3 * n_head)
+        q = np.empty((batch, n_head, N, dh), np.float32)
+        k = np.empty_like(q)
+        vt = np.empty((batch, n_head, dh, N), np.float32)
+        if self.L.orc_qkv_rope_split(_np(qkv), dh, n_head, N, batch, _np(pos), freq_base, freq_scale, attn_factor,
+                                     _np(q), _np(k), _np(vt)):
+            raise ValueError("qkv_rope_split")
+        return q, k, vt
+
+    def merge_heads(self, o, gates=None):
+        """o numpy (batch, H, N, dh) -> (batch, N, H, dh) [* gates (batch, N, H)]."""
+        o = self._f(o)
+        b, H, N, dh = o.shape
+        y = np.empty((b, N, H, dh), np.float32)
+        g = None if gates is None else self._f(gates)
+        if self.L.orc_merge_heads(_np(o), _ne(o.shape), None if g is None else _np(g), _np(y)):
+            raise ValueError("merge_heads")
         return y
 
 

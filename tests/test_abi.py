@@ -58,3 +58,54 @@ def test_frame_counts():
 def test_null_plan_is_invalid_argument():
     rc = stx.lib().stx_torch_stft(None, None, 1, 4096, 1024, 0, None, 0, None)
     assert rc == stx.STATUS_INVALID_ARGUMENT
+
+
+def _desc(ne, addr=0x10000):
+    """A dense stx_tensor descriptor at a fake address (never dereferenced: every call below is
+    rejected by its argument checks before any device work)."""
+    d = stx.Tensor()
+    d.data = addr
+    nb = 4
+    for i in range(4):
+        d.ne[i] = ne[i]
+        d.nb[i] = nb
+        nb *= ne[i]
+    return d
+
+
+def test_layout_argument_checks():
+    L = stx.lib()
+    a = _desc([4, 5, 6, 1])
+    d = _desc([5, 4, 6, 1], 0x900000)
+    bad_axes = L.stx_cont_permute(ctypes.byref(a), 0, 0, 1, 2, ctypes.byref(d), None)
+    assert bad_axes == stx.STATUS_INVALID_ARGUMENT
+    wrong_shape = L.stx_cont_permute(ctypes.byref(a), 0, 2, 1, 3, ctypes.byref(d), None)
+    assert wrong_shape == stx.STATUS_INVALID_ARGUMENT
+    same = _desc([4, 5, 6, 1])
+    overlap = L.stx_cont_permute(ctypes.byref(a), 0, 1, 2, 3, ctypes.byref(same), None)
+    assert overlap == stx.STATUS_INVALID_ARGUMENT and b"overlap" in L.stx_last_error()
+    assert L.stx_cont_permute(None, 0, 1, 2, 3, ctypes.byref(d), None) == stx.STATUS_INVALID_ARGUMENT
+    # dim_head 48 is not built; q/k/vt shapes are checked first.
+    qkv = _desc([3 * 2 * 48, 5, 2, 1])
+    q = _desc([48, 5, 2, 2], 0x1000000)
+    k = _desc([48, 5, 2, 2], 0x2000000)
+    vt = _desc([5, 48, 2, 2], 0x3000000)
+    rc = L.stx_qkv_rope_split(ctypes.byref(qkv), ctypes.c_void_p(0x4000000), 2, 1e4, 1.0, 1.0, ctypes.byref(q),
+                              ctypes.byref(k), ctypes.byref(vt), None)
+    assert rc == stx.STATUS_UNSUPPORTED
+    vt_bad = _desc([48, 5, 2, 2], 0x3000000)
+    rc = L.stx_qkv_rope_split(ctypes.byref(qkv), ctypes.c_void_p(0x4000000), 2, 1e4, 1.0, 1.0, ctypes.byref(q),
+                              ctypes.byref(k), ctypes.byref(vt_bad), None)
+    assert rc == stx.STATUS_INVALID_ARGUMENT
+    # concat: extents along dim must add up; other dims must match.
+    s0, s1 = _desc([4, 2, 3, 1]), _desc([4, 5, 3, 1], 0x20000)
+    arr = (ctypes.c_void_p * 2)(ctypes.addressof(s0), ctypes.addressof(s1))
+    dst = _desc([4, 6, 3, 1], 0x800000)
+    assert L.stx_concat(arr, 2, 1, ctypes.byref(dst), None) == stx.STATUS_INVALID_ARGUMENT
+    assert L.stx_concat(arr, 2, 4, ctypes.byref(dst), None) == stx.STATUS_INVALID_ARGUMENT
+    assert L.stx_concat(arr, 0, 1, ctypes.byref(dst), None) == stx.STATUS_INVALID_ARGUMENT
+    gates = _desc([2, 6, 5, 1], 0x30000)
+    o = _desc([4, 5, 6, 1])
+    md = _desc([4, 6, 5, 1], 0x900000)
+    assert L.stx_merge_heads(ctypes.byref(o), ctypes.byref(gates), ctypes.byref(md), None) == \
+        stx.STATUS_INVALID_ARGUMENT
