@@ -478,6 +478,20 @@ def run_rows(torch, stx, dev):
         return lambda: bands.scatter_apply(m, z, T, layout=stx.T_MAJOR, out=o, stream=stream)
     out["c3_scatter_apply"] = time_call(torch, stream, mk_scatter, feat * 4 + 2 * C * T * F * 8)
 
+    # The band split's RMSNorm of all 60 bands, and the mask heads' GLU for 4 stems, one launch each.
+    gammas = [rn(int(s) * C * 2) for s in sizes]
+
+    def mk_band_norm():
+        f, o = rn(1, feat), torch.empty((1, feat), device=dev)
+        return lambda: bands.rms_norm(f, T, gammas, 1e-24, out=o, stream=stream)
+    out["c3_band_rms_norm"] = time_call(torch, stream, mk_band_norm, 2 * feat * 4 + bands.total_feat * 4)
+
+    def mk_mask_glu():
+        heads = [rn(T, 2 * int(s) * C * 2) for _ in range(4) for s in sizes]
+        m = torch.empty((4, feat), device=dev)
+        return lambda: bands.mask_glu(heads, 4, T, out=m, stream=stream)
+    out["c3_band_mask_glu"] = time_call(torch, stream, mk_mask_glu, 4 * 3 * feat * 4)
+
     def mk_istft():
         z, y = torch.randn((C, T, F), dtype=torch.complex64, device=dev), torch.empty((C, hop * (T - 1)), device=dev)
         return lambda: stx.torch_istft(fft, z, hop, layout=stx.T_MAJOR, out=y, stream=stream)

@@ -188,6 +188,25 @@ STX_API stx_status stx_band_scatter_apply(const stx_bands* bands, const float* m
                                           stx_spec_layout layout, int zero_dc, float* out,
                                           stx_stream stream);
 
+/* The band split's RMSNorm (src/roformer.cpp:169-175, rms at :96-98) for every band in one
+ * launch: row t of band b, feat[batch][feat_off[b] * T + t * dim_in(b) + i] for
+ * i < dim_in(b), becomes x / sqrt(mean(x^2) + eps) * gammas[b][i] (ggml_mul(ggml_rms_norm(view,
+ * eps), gamma_b); the reference's eps is 1e-24, src/roformer.cpp:34). feat and out are device
+ * [batch][total_feat * T] in the layout stx_band_gather writes; out may be feat. gammas is a host
+ * array of n_bands device pointers, gammas[b] holding dim_in(b) floats. Bands of more than 1,024
+ * floats per frame are UNSUPPORTED. */
+STX_API stx_status stx_band_rms_norm(const stx_bands* bands, const float* feat, int batch, int n_frames,
+                                     const float* const* gammas, float eps, float* out, stx_stream stream);
+
+/* The GLU at the end of every mask estimator (src/roformer.cpp:193-204): heads[s * n_bands + b]
+ * is device [T][2 * dim_in(b)], the last layer's output for stem s and band b; masks gets
+ * a * sigmoid(gate) of its two halves, device [n_stems][total_feat * T] in the layout
+ * stx_band_scatter_apply reads (pass batch * n_stems as n_stems for several chunks, heads in
+ * the same order). heads is a host array of n_stems * n_bands device pointers. Each band's
+ * result equals stx_glu(dim 0) on that band. */
+STX_API stx_status stx_band_mask_glu(const stx_bands* bands, const float* const* heads, int n_stems, int n_frames,
+                                     float* masks, stx_stream stream);
+
 /* ------------------------------------------------------------------------------------------
  * Chunked overlap-add demix. Replaces RoFormer::Impl::demix (src/roformer.cpp:286-351),
  * n_chunks (:353-357) and RoFormer::separate (:436-486): chunks of `chunk` samples every `step`

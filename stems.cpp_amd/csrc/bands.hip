@@ -51,6 +51,7 @@ struct stx_bands {
     int* d_pair_off = nullptr;                       // [n_bands + 1]: first (bin, channel) pair of band b
     int* d_pair_code = nullptr;                      // [total_feat / 2]: (channel << 16) | bin of each pair
     int* d_freq_lo = nullptr;                        // [n_bands]: first bin of each band
+    stx::FastDiv* d_pair_div = nullptr;              // [n_bands]: division by the band's pairs per frame
     bool ranges = false;                             // every band is a range of consecutive bins
 };
 
@@ -266,6 +267,160 @@ __global__ __launch_bounds__(256) void band_scatter_f_kernel(ScatterArgs a) {
     a.out[(((size_t)bt * a.S + s) * a.C + c) * a.F * a.T + (size_t)f * a.T + t] = masked_bin(a, mb, z, f, c, t);
 }
 
+// ----------------------------------------------------------------- band-split RMSNorm
+// RMSNorm * gamma of every band's block at once (src/roformer.cpp:169-175 with rms at :96-98,
+// eps kRmsEps = 1e-24 at :34): row t of band b is feat[feat_off[b] * T + t * dim_in(b) + i],
+// i < dim_in(b) = size_b * C * 2. Band widths differ a lot (28 to 520 floats for the 60 mel
+// bands), so each band gets its own shape: L_b lanes per frame (a power of two, enough for at
+// most kBandNormPer float2 per lane, at most a wave) and 256 / L_b frames per block, which
+// gives every block a similar payload. Blocks are numbered band after band; a block finds its
+// band by binary search over the bands' first block. Each lane keeps its float2 in registers;
+// the sum of squares is accumulated in double and reduced across the row's lanes, and
+// y = (x * scale) * gamma in float with scale = 1 / sqrt(mean + eps) rounded once, the
+// arithmetic of stx_rms_norm_mul.
+constexpr int kBandNormPer = 4;
+constexpr int kBandTable = 160;                      // bands per launch
+
+struct BandNormArgs {
+    const float* gamma[kBandTable];
+    int first_block[kBandTable + 1];                 // of each band; [nb] = blocks of the launch
+    unsigned char lanes_log2[kBandTable];
+    const float* feat;
+    float* out;
+    const BandInfo* bands;
+    long long total_feat;
+    int T, C, b0, nb;                                // bands b0 .. b0 + nb - 1 in this launch
+    float eps;
+};
+static_assert(sizeof(BandNormArgs) <= 4096, "band table exceeds the kernel argument space");
+
+template <int V>
+__global__ __launch_bounds__(256) void band_rms_norm_kernel(BandNormArgs a) {
+    const int blk = (int)blockIdx.x;
+    int lo = 0, hi = a.nb - 1;                       // last band whose first block <= blk
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (a.first_block[mid] <= blk) lo = mid;
+        else hi = mid - 1;
+    }
+    const int bi = lo;
+    const BandInfo info = a.bands[a.b0 + bi];
+    const int d = info.size * a.C;                   // float2 per row
+    const int lg = a.lanes_log2[bi], L = 1 << lg;
+    const int lane = (int)threadIdx.x & (L - 1), rr = (int)threadIdx.x >> lg;
+    const int t = (blk - a.first_block[bi]) * (256 >> lg) + rr;
+    const long long base = (long long)blockIdx.y * a.total_feat * a.T + info.feat_off * a.T +
+                           (long long)min(t, a.T - 1) * 2 * d;
+    const float2* x = reinterpret_cast<const float2*>(a.feat + base);
+    const float2* g = reinterpret_cast<const float2*>(a.gamma[bi]);
+    const int nk = (d + L - 1) >> lg;                // float2 per lane, uniform over the block
+    float2 v[V], gv[V];
+#pragma unroll
+    for (int k = 0; k < V; k++) {                    // clamped loads, all issued up front;
+        if (k < nk) {                                // slots past nk are skipped uniformly
+            const int q = min(lane + (k << lg), d - 1);
+            v[k] = x[q];
+            gv[k] = g[q];
+        } else {
+            v[k] = gv[k] = make_float2(0.f, 0.f);
+        }
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int k = 0; k < V; k++) {
+        if (lane + (k << lg) < d) ss += (double)v[k].x * v[k].x + (double)v[k].y * v[k].y;
+    }
+    for (int m = L >> 1; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);   // stays inside the row's lanes
+    const float scale = (float)(1.0 / sqrt(ss / (2.0 * d) + (double)a.eps));
+    if (t >= a.T) return;
+    float2* y = reinterpret_cast<float2*>(a.out + base);
+#pragma unroll
+    for (int k = 0; k < V; k++) {
+        const int q = lane + (k << lg);
+        if (k < nk && q < d) y[q] = make_float2((v[k].x * scale) * gv[k].x, (v[k].y * scale) * gv[k].y);
+    }
+}
+
+// ------------------------------------------------------------------- mask-head GLU
+// The GLU that ends every mask estimator (src/roformer.cpp:199-204): for stem s and band b the
+// last layer's output h [T][2 * dim_in(b)] becomes m[t][i] = h[t][i] * sigmoid(h[t][dim_in + i]),
+// written straight into the band's block of the stem's mask buffer, the layout the
+// scatter-average reads. The stem's buffer is walked flat, kGluPer float2 per thread, each
+// finding its band by binary search over the band starts staged in LDS; the sigmoid is the
+// one of stx_glu, a / (1 + expf(-g)), so each band's result equals stx_glu on that band.
+constexpr int kGluPer = 4;
+constexpr int kGluTable = 448;                       // head pointers per launch
+
+struct BandGluArgs {
+    const float2* heads[kGluTable];                  // [stem - s0][band]
+    float2* masks;                                   // [n_stems][total_feat * T / 2]
+    const int* pair_off;                             // [n_bands + 1]
+    const FastDiv* pair_div;                         // [n_bands]
+    int total_pairs, T, n_bands, s0;
+};
+static_assert(sizeof(BandGluArgs) <= 4096, "head table exceeds the kernel argument space");
+
+__device__ __forceinline__ float glu_gate(float a, float g) { return a / (1.0f + expf(-g)); }
+
+// LDS: band starts [n_bands + 1] ints, then the stem's head pointers and the bands' divisors.
+size_t glu_lds_bytes(int n_bands) {
+    return (sizeof(int) * (n_bands + 1) + 7) / 8 * 8 + (sizeof(void*) + sizeof(FastDiv)) * n_bands;
+}
+
+__global__ __launch_bounds__(256) void band_mask_glu_kernel(BandGluArgs a) {
+    extern __shared__ __align__(8) unsigned char lds[];
+    const int B = a.n_bands;
+    int* start = reinterpret_cast<int*>(lds);                                   // first float2 of each band
+    const float2** ptr = reinterpret_cast<const float2**>(lds + (sizeof(int) * (B + 1) + 7) / 8 * 8);
+    FastDiv* div = reinterpret_cast<FastDiv*>(ptr + B);
+    const int si = (int)blockIdx.y;
+    for (int b = (int)threadIdx.x; b <= B; b += 256) {
+        start[b] = a.pair_off[b] * a.T;
+        if (b < B) {
+            ptr[b] = a.heads[si * B + b];
+            div[b] = a.pair_div[b];
+        }
+    }
+    __syncthreads();
+    const int n = a.total_pairs * a.T;
+    float2* out = a.masks + (long long)(a.s0 + si) * n;
+    const int e0 = (int)blockIdx.x * (256 * kGluPer) + (int)threadIdx.x;
+    if (e0 >= n) return;
+    // Pointers read back from LDS are generic to the compiler; flat loads would also count on the
+    // LDS counter and serialise against the next search, so they are cast back to global.
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    using gf2 = __attribute__((address_space(1))) const f2;
+    gf2* src0[kGluPer];
+    gf2* src1[kGluPer];
+#pragma unroll
+    for (int k = 0; k < kGluPer; k++) {                // LDS only: band, frame and column
+        const int e = min(e0 + 256 * k, n - 1);
+        int lo = 0, hi = B - 1;                      // last band with start <= e
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (start[mid] <= e) lo = mid;
+            else hi = mid - 1;
+        }
+        const FastDiv dv = div[lo];
+        const unsigned local = (unsigned)(e - start[lo]);
+        const unsigned t = dv.div(local), j = local - t * dv.d;
+        gf2* row = (gf2*)(ptr[lo] + (size_t)t * 2 * dv.d);
+        src0[k] = row + j;
+        src1[k] = row + dv.d + j;
+    }
+    f2 h0[kGluPer], h1[kGluPer];
+#pragma unroll
+    for (int k = 0; k < kGluPer; k++) {                // then every load at once
+        h0[k] = *src0[k];
+        h1[k] = *src1[k];
+    }
+#pragma unroll
+    for (int k = 0; k < kGluPer; k++) {
+        const int e = e0 + 256 * k;
+        if (e < n) out[e] = make_float2(glu_gate(h0[k].x, h1[k].x), glu_gate(h0[k].y, h1[k].y));
+    }
+}
+
 void check_bands(const stx_bands* b) { STX_REQUIRE(b != nullptr && b->d_bands != nullptr, "null band table"); }
 
 }  // namespace
@@ -346,6 +501,9 @@ STX_API stx_status stx_bands_create(const int32_t* band_sizes, int n_bands, cons
         up(&h->d_pair_off, pair_off);
         up(&h->d_pair_code, pair_code);
         up(&h->d_freq_lo, freq_lo);
+        std::vector<FastDiv> pair_div(n_bands);
+        for (int b = 0; b < n_bands; b++) pair_div[b] = FastDiv((unsigned)std::max(band_sizes[b] * channels, 1));
+        up(&h->d_pair_div, pair_div);
         h->ranges = ranges;
         if (e != hipSuccess) {
             stx_bands_destroy(h);
@@ -365,6 +523,7 @@ STX_API void stx_bands_destroy(stx_bands* h) {
     (void)hipFree(h->d_pair_off);
     (void)hipFree(h->d_pair_code);
     (void)hipFree(h->d_freq_lo);
+    (void)hipFree(h->d_pair_div);
     delete h;
 }
 
@@ -450,6 +609,94 @@ STX_API stx_status stx_band_scatter_apply(const stx_bands* h, const float* masks
             dim3 grid((n_frames + 255) / 256, a.F, batch * n_stems * a.C);
             hipLaunchKernelGGL(band_scatter_f_kernel, grid, dim3(256), 0, s, a);
             launch_check("band_scatter_f_kernel");
+        }
+    });
+}
+
+STX_API stx_status stx_band_rms_norm(const stx_bands* h, const float* feat, int batch, int n_frames,
+                                     const float* const* gammas, float eps, float* out, stx_stream stream) {
+    return guard([&] {
+        check_bands(h);
+        STX_REQUIRE(batch >= 0 && n_frames >= 0, "bad batch/n_frames");
+        if (batch == 0 || n_frames == 0 || h->total_feat == 0) return;
+        STX_REQUIRE(feat && out && gammas, "NULL buffer");
+        STX_REQUIRE(batch < 65536, "too many batch items");
+        for (int b = 0; b < h->n_bands; b++) {
+            const long long d = (h->feat_off[b + 1] - h->feat_off[b]) / 2;
+            STX_REQUIRE(d == 0 || gammas[b] != nullptr, "band_rms_norm: gamma of band %d is NULL", b);
+            if (d > 64LL * 16)
+                fail(STX_STATUS_UNSUPPORTED, "band_rms_norm: band %d has %lld floats per frame (at most 2048)", b,
+                     2 * d);
+        }
+        const hipStream_t s = as_stream(stream);
+        for (int b0 = 0; b0 < h->n_bands; b0 += kBandTable) {
+            BandNormArgs a{};
+            a.feat = feat;
+            a.out = out;
+            a.bands = h->d_bands;
+            a.total_feat = h->total_feat;
+            a.T = n_frames;
+            a.C = h->channels;
+            a.b0 = b0;
+            a.eps = eps;
+            long long blocks = 0;
+            int max_nk = 1;
+            const int nb = std::min(kBandTable, h->n_bands - b0);
+            for (int i = 0; i < nb; i++) {
+                const int d = (int)((h->feat_off[b0 + i + 1] - h->feat_off[b0 + i]) / 2);
+                int lg = 0;
+                while ((1 << lg) < 64 && (1 << lg) * kBandNormPer < d) lg++;
+                a.gamma[i] = gammas[b0 + i];
+                a.lanes_log2[i] = (unsigned char)lg;
+                a.first_block[i] = (int)blocks;      // an empty band gets no blocks: the search skips it
+                if (d > 0) blocks += (n_frames + (256 >> lg) - 1) / (256 >> lg);
+                max_nk = std::max(max_nk, (d + (1 << lg) - 1) >> lg);
+            }
+            if (blocks == 0) continue;
+            STX_REQUIRE(blocks < (1LL << 31), "band_rms_norm: too many frames");
+            a.first_block[nb] = (int)blocks;
+            a.nb = nb;
+            const dim3 grid((unsigned)blocks, (unsigned)batch);
+            if (max_nk <= 4) hipLaunchKernelGGL(band_rms_norm_kernel<4>, grid, dim3(256), 0, s, a);
+            else if (max_nk <= 8) hipLaunchKernelGGL(band_rms_norm_kernel<8>, grid, dim3(256), 0, s, a);
+            else hipLaunchKernelGGL(band_rms_norm_kernel<16>, grid, dim3(256), 0, s, a);
+            launch_check("band_rms_norm_kernel");
+        }
+    });
+}
+
+STX_API stx_status stx_band_mask_glu(const stx_bands* h, const float* const* heads, int n_stems, int n_frames,
+                                     float* masks, stx_stream stream) {
+    return guard([&] {
+        check_bands(h);
+        STX_REQUIRE(n_stems >= 0 && n_frames >= 0, "bad n_stems/n_frames");
+        if (n_stems == 0 || n_frames == 0 || h->total_feat == 0) return;
+        STX_REQUIRE(heads && masks, "NULL buffer");
+        const int B = h->n_bands;
+        for (long long i = 0; i < (long long)n_stems * B; i++) {
+            const bool empty = h->feat_off[i % B + 1] == h->feat_off[i % B];
+            STX_REQUIRE(empty || heads[i] != nullptr, "band_mask_glu: head %lld is NULL", i);
+        }
+        const long long n = h->total_feat / 2 * (long long)n_frames;
+        STX_REQUIRE(n < (1LL << 31) - 256 * kGluPer, "band_mask_glu: too many features per stem");
+        if (B > kGluTable) fail(STX_STATUS_UNSUPPORTED, "band_mask_glu: more than %d bands", kGluTable);
+        const int per_launch = kGluTable / B;
+        const hipStream_t s = as_stream(stream);
+        for (int s0 = 0; s0 < n_stems; s0 += per_launch) {
+            const int ns = std::min(per_launch, n_stems - s0);
+            STX_REQUIRE(ns < 65536, "too many stems");
+            BandGluArgs a{};
+            for (int i = 0; i < ns * B; i++) a.heads[i] = reinterpret_cast<const float2*>(heads[(long long)s0 * B + i]);
+            a.masks = reinterpret_cast<float2*>(masks);
+            a.pair_off = h->d_pair_off;
+            a.pair_div = h->d_pair_div;
+            a.total_pairs = (int)(h->total_feat / 2);
+            a.T = n_frames;
+            a.n_bands = B;
+            a.s0 = s0;
+            const dim3 grid((unsigned)((n + 256 * kGluPer - 1) / (256 * kGluPer)), (unsigned)ns);
+            hipLaunchKernelGGL(band_mask_glu_kernel, grid, dim3(256), glu_lds_bytes(B), s, a);
+            launch_check("band_mask_glu_kernel");
         }
     });
 }

@@ -51,6 +51,8 @@ _SIGNATURES = {
     "stx_bands_total_feat": (ctypes.c_int64, [_vp]),
     "stx_band_gather": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp]),
     "stx_band_scatter_apply": (_i, [_vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _vp]),
+    "stx_band_rms_norm": (_i, [_vp, _vp, _i, _i, _vp, ctypes.c_float, _vp, _vp]),
+    "stx_band_mask_glu": (_i, [_vp, _vp, _i, _i, _vp, _vp]),
     "stx_demix_step": (_i, [_i, _i, ctypes.c_float]),
     "stx_demix_plan": (_i, [ctypes.c_int64, _i, _i, _vp, _vp, ctypes.c_int64]),
     "stx_demix_window": (_i, [_i, _vp]),
@@ -343,6 +345,28 @@ class Bands:
             out = torch.empty((batch, S) + tuple(spec.shape[1:]), dtype=torch.complex64, device=spec.device)
         check(lib().stx_band_scatter_apply(self.handle, _ptr(masks), S, _ptr(spec), batch, int(n_frames), int(layout),
                                            int(bool(zero_dc)), _ptr(out), _stream(stream)))
+        return out
+
+    def rms_norm(self, feat, n_frames, gammas, eps=1e-24, out=None, stream=None):
+        """The band split's RMSNorm of every band: feat float32 [batch, total_feat * T]; gammas: one
+        float32 device tensor of dim_in(b) per band."""
+        import torch
+        _require(feat, torch.float32, "feat")
+        if out is None:
+            out = torch.empty_like(feat)
+        table = (ctypes.c_void_p * max(len(gammas), 1))(*[g.data_ptr() for g in gammas])
+        check(lib().stx_band_rms_norm(self.handle, _ptr(feat), feat.shape[0], int(n_frames), table, float(eps),
+                                      _ptr(out), _stream(stream)))
+        return out
+
+    def mask_glu(self, heads, n_stems, n_frames, out=None, stream=None):
+        """heads: n_stems * n_bands float32 device tensors [T, 2 * dim_in(b)] (stem-major) ->
+        masks float32 [n_stems, total_feat * T]."""
+        import torch
+        if out is None:
+            out = torch.empty((n_stems, self.total_feat * n_frames), dtype=torch.float32, device=heads[0].device)
+        table = (ctypes.c_void_p * max(len(heads), 1))(*[h.data_ptr() for h in heads])
+        check(lib().stx_band_mask_glu(self.handle, table, int(n_stems), int(n_frames), _ptr(out), _stream(stream)))
         return out
 
 

@@ -150,3 +150,81 @@ def test_band_table_errors(device):
     with pytest.raises(stx.StxError) as e:
         stx.Bands(np.array([2, 2], np.int32), np.array([0, 1, 2], np.int32), 8, 2)
     assert e.value.status == stx.STATUS_RUNTIME_ERROR
+
+
+# ------------------------------------------------- band-split RMSNorm and mask-head GLU
+def band_blocks(sizes, C, T):
+    """(offset, dim_in) of each band's [T][dim_in] block in a [total_feat * T] buffer."""
+    out, off = [], 0
+    for s in sizes:
+        din = int(s) * C * 2
+        out.append((off, din))
+        off += din * T
+    return out
+
+
+@pytest.mark.parametrize("kind,T,batch", [("mel", 801, 2), ("bs", 801, 1), ("mel", 17, 3)])
+def test_band_rms_norm(device, mel, kind, T, batch):
+    """src/roformer.cpp:169-175: rms(view_b, band.b.norm) for every band, against the oracle's
+    RMSNorm (double, rounded once) on each band's rows."""
+    import torch
+    ops = oracle_lib.ops()
+    sizes, freqs = mel if kind == "mel" else (np.array(BS_FPB, np.int32), np.arange(1025, dtype=np.int32))
+    C = 2
+    bands = stx.Bands(sizes, freqs, 1025, C)
+    feat = synth.normal(21, (batch, bands.total_feat * T), 0.7)
+    gam = [synth.normal(100 + b, (int(s) * C * 2,), 1.0) for b, s in enumerate(sizes)]
+    gd = [dev(g, device) for g in gam]
+    y = host(bands.rms_norm(dev(feat, device), T, gd, eps=1e-24))
+    for bi in range(batch):
+        for (off, din), g in zip(band_blocks(sizes, C, T), gam):
+            x = feat[bi, off:off + din * T].reshape(T, din)
+            want = ops.norm(x, 1e-24, rms=True, w=g)
+            got = y[bi, off:off + din * T].reshape(T, din)
+            assert np.max(np.abs(got - want)) <= 1e-6 * np.max(np.abs(want))
+    # In place, and equal to stx_rms_norm_mul on one band's view.
+    fd = dev(feat, device)
+    bands.rms_norm(fd, T, gd, out=fd)
+    assert np.array_equal(host(fd), y)
+    off, din = band_blocks(sizes, C, T)[5]
+    view = dev(feat[0, off:off + din * T].reshape(T, din), device)
+    one = host(stx.rms_norm(view, 1e-24, gamma=gd[5]))
+    assert np.max(np.abs(one - y[0, off:off + din * T].reshape(T, din))) <= 1e-6 * np.max(np.abs(one))
+
+
+@pytest.mark.parametrize("kind,S,T", [("mel", 4, 801), ("bs", 2, 801), ("mel", 9, 33)])
+def test_band_mask_glu(device, mel, kind, S, T):
+    """src/roformer.cpp:199-204: GLU on dim 0 of every (stem, band) head into the mask layout
+    the scatter reads; bit-identical to stx_glu per band, within 1e-6 of the oracle's GLU."""
+    ops = oracle_lib.ops()
+    sizes, freqs = mel if kind == "mel" else (np.array(BS_FPB, np.int32), np.arange(1025, dtype=np.int32))
+    C = 2
+    bands = stx.Bands(sizes, freqs, 1025, C)
+    heads_h = [synth.normal(1000 * s + b, (T, 2 * int(z) * C * 2), 2.0) for s in range(S) for b, z in enumerate(sizes)]
+    heads = [dev(h, device) for h in heads_h]
+    m = host(bands.mask_glu(heads, S, T))
+    blocks = band_blocks(sizes, C, T)
+    for s in range(S):
+        for b, (off, din) in enumerate(blocks):
+            h = heads_h[s * len(sizes) + b]
+            got = m[s, off:off + din * T].reshape(T, din)
+            want = ops.glu(h, 0)
+            assert np.max(np.abs(got - want)) <= 1e-6 * max(np.max(np.abs(want)), 1e-30)
+            if b % 17 == 0:
+                assert np.array_equal(got, host(stx.glu(heads[s * len(sizes) + b], 0)))
+
+
+def test_band_mask_glu_many_stems(device):
+    """More (stem, band) heads than one launch carries: 40 stems of 60 bands."""
+    sizes = np.array([1, 2, 3] * 20, np.int32)
+    freqs = np.arange(int(sizes.sum()), dtype=np.int32) % 100
+    C, T, S = 2, 5, 40
+    bands = stx.Bands(sizes, freqs, 100, C)
+    heads_h = [synth.normal(7 + i, (T, 2 * int(z) * C * 2), 1.0) for i, z in enumerate(np.tile(sizes, S))]
+    m = host(bands.mask_glu([dev(h, device) for h in heads_h], S, T))
+    ops = oracle_lib.ops()
+    blocks = band_blocks(sizes, C, T)
+    for s in range(S):
+        for b, (off, din) in enumerate(blocks):
+            want = ops.glu(heads_h[s * 60 + b], 0)
+            assert np.max(np.abs(m[s, off:off + din * T].reshape(T, din) - want)) <= 1e-6 * np.max(np.abs(want))
