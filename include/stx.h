@@ -304,6 +304,71 @@ STX_API stx_status stx_demix_track(const float* mix, int channels, int64_t len, 
                                    size_t workspace_bytes, stx_stream stream);
 
 /* ------------------------------------------------------------------------------------------
+ * HTDemucs pre/post-processing around the model graph, and apply_model's split. Replace the
+ * host loops of HTDemucs::Impl::run (src/htdemucs.cpp:419-474) and HTDemucs::separate
+ * (:534-644). Statistics are device double[2] {mean, sd}, written by the normalise calls and
+ * read by the denormalise calls, so nothing returns to the host between them.
+ * ---------------------------------------------------------------------------------------- */
+
+/* Bytes of device workspace for a normalise call over n values (16 per 8192 values). */
+STX_API size_t stx_htdemucs_norm_workspace_size(int64_t n);
+
+/* Complex-as-channels pack and normalisation of one segment's spectrum
+ * (src/htdemucs.cpp:424-436): spec is device complex64 [C][F][T] (f-major, as
+ * stx_htdemucs_spec writes it); mag is device [2C][F][T] with mag[2c] = re and mag[2c+1] = im,
+ * each (v - mean) / (1e-5 + sd) over all 2 C F T values (mean_of and the unbiased std_of,
+ * :293-302, in double). stats gets {mean, sd}. workspace: device, 16-byte aligned,
+ * stx_htdemucs_norm_workspace_size(2 C F T) bytes; calls that share one must not overlap. */
+STX_API stx_status stx_htdemucs_cac_normalize(const float* spec, int channels, int n_bins, int n_frames, float* mag,
+                                              double* stats, void* workspace, size_t workspace_bytes,
+                                              stx_stream stream);
+
+/* The waveform branch's normalisation (src/htdemucs.cpp:438-441): out = (x - mean) / (1e-5 + sd)
+ * over n values. stats gets {mean, sd}. */
+STX_API stx_status stx_htdemucs_wave_normalize(const float* x, int64_t n, float* out, double* stats, void* workspace,
+                                               size_t workspace_bytes, stx_stream stream);
+
+/* separate()'s normalisation by the mono mix (src/htdemucs.cpp:539-549): mono = sum_c x / C
+ * (rounded to float), ref_mean and ref_std = max(std, 1e-8) of mono, out = (x - ref_mean) /
+ * ref_std for every channel of mix [C][len]. stats gets {ref_mean, ref_std}. INVALID_ARGUMENT
+ * "empty input" when len <= 0, as the reference throws. workspace: norm_workspace_size(len). */
+STX_API stx_status stx_htdemucs_mix_normalize(const float* mix, int channels, int64_t len, float* out, double* stats,
+                                              void* workspace, size_t workspace_bytes, stx_stream stream);
+
+/* The spectral branch's denormalisation (src/htdemucs.cpp:465-468): ox is the model's
+ * [S][2C][F][T] output; spec gets complex64 [S][C][F][T] with re * sd + mean and
+ * im * sd + mean (double, rounded once), stats being the cac_normalize ones. Feed spec to
+ * stx_htdemucs_ispec with S * C channels. */
+STX_API stx_status stx_htdemucs_cac_denormalize(const float* ox, int n_sources, int channels, int n_bins, int n_frames,
+                                                const double* stats, float* spec, stx_stream stream);
+
+/* The time branch's denormalisation plus the spectral branch (src/htdemucs.cpp:469-470):
+ * out = (float)(xt * sd + mean) + y over n values, with the wave_normalize stats. */
+STX_API stx_status stx_htdemucs_time_add(const float* xt, const float* y, int64_t n, const double* stats, float* out,
+                                         stx_stream stream);
+
+/* split()'s chunking (src/htdemucs.cpp:564-566,589): stride = (int)((1 - overlap) * segment)
+ * (overlap < 0 means 0.25) and the number of chunks of a view of `length` samples.
+ * INVALID_ARGUMENT "overlap must be < 1" when stride <= 0. */
+STX_API stx_status stx_htdemucs_split_plan(int length, int segment, float overlap, int* stride, int* n_chunks);
+
+/* The padded model inputs of chunks first .. first + count - 1 of the view [offset, offset +
+ * length) of buf (device [C][total]) (TensorChunk.padded, src/htdemucs.cpp:552-561,589-593):
+ * chunk k starts at k * stride, keeps min(segment, length - k * stride) samples and is
+ * centre-padded to `segment` with buf's own samples around it where they exist, zeros beyond.
+ * parts: device [count][C][segment]. */
+STX_API stx_status stx_htdemucs_segments(const float* buf, int channels, int64_t total, int64_t offset, int length,
+                                         int segment, int stride, int first, int count, float* parts,
+                                         stx_stream stream);
+
+/* split()'s weighted overlap-add (src/htdemucs.cpp:566-573,594-606): y is device
+ * [n_chunks][tracks][segment], the model outputs of every chunk (tracks = S * C); each is
+ * center-trimmed, weighted by the triangular window and summed in chunk order in float, then
+ * divided by the summed weights: out device [tracks][length], bit-identical to the reference. */
+STX_API stx_status stx_htdemucs_split_overlap_add(const float* y, int tracks, int length, int segment, int stride,
+                                                  float* out, stx_stream stream);
+
+/* ------------------------------------------------------------------------------------------
  * ggml ops of the HTDemucs and RoFormer graphs. ggml's sources are not in the reference tree
  * (an un-vendored submodule), so each entry point cites the call sites whose semantics it
  * implements. Tensors are fp32 with ggml's shape convention: ne[0] is the fastest dimension,

@@ -33,6 +33,11 @@
  *     difference). ggml-specific rounding (the float theta recurrence of ggml's RoPE, its float
  *     softmax and norm arithmetic) is parity unpinned: ggml's sources are not in the reference.
  *   orc_binary: numpy's float32 arithmetic on explicitly tiled operands, bit for bit.
+ *   orc_mean_std / orc_*normalize / orc_time_add / orc_split_*: torch.std's unbiased estimator
+ *     and numpy float32 arithmetic on the same formulas, the weights' closed form (symmetric
+ *     up to the centre sample, maximum 1), the identity model (a split of a model that returns
+ *     its input gives the input back), and the TensorChunk rule that the last segment is
+ *     centre-padded with the audio before it, not with zeros (src/htdemucs.cpp:530-533).
  *   orc_cont_permute / orc_concat / orc_merge_heads: numpy's transpose, concatenate and
  *     multiply, bit for bit, and the shapes the reference's own comments give for its permutes
  *     (src/roformer.cpp:112-114,133: [dh, N, H, batch] and [N, dh, H, batch] from
@@ -121,6 +126,19 @@ int orc_concat(const float* const* xs, const int64_t* nes, int n, int dim, float
 int orc_qkv_rope_split(const float* qkv, int64_t dh, int64_t H, int64_t N, int64_t batch, const int32_t* pos,
                        float freq_base, float freq_scale, float attn_factor, float* q, float* k, float* vt);
 int orc_merge_heads(const float* o, const int64_t ne[4], const float* gates, float* y);
+
+/* HTDemucs pre/post-processing and apply_model's split (htdemucs_oracle.c). */
+void orc_mean_std(const float* x, int64_t n, double* mean, double* sd);
+void orc_cac_normalize(const float* spec, int C, int64_t FT, double mean, double sd, float* mag);
+void orc_normalize(const float* x, int64_t n, double mean, double sd, float* y);
+void orc_cac_denormalize(const float* ox, int S, int C, int64_t FT, double mean, double sd, float* spec);
+void orc_time_add(const float* t, const float* y, int64_t n, double mean, double sd, float* out);
+void orc_mix_normalize(const float* mix, int C, int64_t len, float* out, double* stats);
+void orc_split_weights(int seg, float* w);
+int orc_split_count(int length, int seg, float overlap, int* stride);
+void orc_segments(const float* buf, int C, int64_t total, int64_t offset, int length, int seg, int stride,
+                  float* parts);
+void orc_split_ola(const float* y, int tracks, int length, int seg, int stride, float* out, float* sum_w);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,384 @@
+// htdemucs.hip — the HTDemucs host pre/post-processing around the model graph, and the
+// split of apply_model, as gfx950 kernels over device buffers.
+//
+// Reference: HTDemucs::Impl::run (src/htdemucs.cpp:419-474) and HTDemucs::separate (:534-644):
+//   * complex-as-channels pack of the spectrum + global mean/std normalisation (:424-436), the
+//     waveform's normalisation (:438-441), and the inverse: denormalise the spectral branch
+//     for the iSTFT (:465-468) and denormalise + add the time branch (:469-470);
+//   * the mono-mix normalisation of separate() (:539-549);
+//   * split(): TensorChunk padding (:552-561), triangular weights (:566-573), center_trim and
+//     the weighted overlap-add (:589-607).
+//
+// The moments (mean_of / std_of, :293-302: double sums, unbiased std) take two kernels:
+// pass 1 writes one (sum d, sum d^2) pair in double per 8192 floats, with d = x - x[0] so
+// no cancellation occurs; pass 2 has every block add all pairs in one fixed order (so every
+// block gets bit-identical statistics) and then normalise its own chunk. The split's
+// overlap-add is in gather form: each output sample sums, in chunk order and in float like the
+// reference's `out += weight * seg_out`, the <= ceil(seg / stride) chunks covering it, and
+// divides by the summed weights, so it is bit-exact.
+#include <algorithm>
+#include <cmath>
+
+#include "common.hpp"
+
+namespace stx {
+namespace {
+
+constexpr int kMomChunk = 8192;                  // floats per pass-1 block (256 threads x 32)
+
+enum MomKind { MOM_FLAT = 0, MOM_MONO = 1 };
+
+struct MomArgs {
+    const float* x;              // FLAT: n floats; MONO: [C][n]
+    long long n;                 // FLAT: floats; MONO: samples per channel
+    int C;
+    double* partial;             // [blocks][2]
+};
+
+__device__ __forceinline__ float mono_at(const float* x, long long n, int C, long long i) {
+    double m = 0.0;
+    for (int c = 0; c < C; c++) m += x[c * n + i];
+    return (float)(m / C);
+}
+
+__device__ __forceinline__ double block_sum(double v, double* red) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    const int w = (int)threadIdx.x / 64, lane = (int)threadIdx.x % 64;
+    __syncthreads();                             // red may still be read by a previous call
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    return red[0] + red[1] + red[2] + red[3];    // 256 threads: 4 waves, summed in one order
+}
+
+template <int KIND>
+__global__ __launch_bounds__(256) void moments_kernel(MomArgs a) {
+    __shared__ double red[4];
+    const long long lo = (long long)blockIdx.x * kMomChunk;
+    const float shift = KIND == MOM_MONO ? mono_at(a.x, a.n, a.C, 0) : a.x[0];
+    float v[kMomChunk / 256];
+#pragma unroll
+    for (int j = 0; j < kMomChunk / 256; j++) {  // clamped loads, all issued first
+        const long long i = min(lo + threadIdx.x + 256LL * j, a.n - 1);
+        v[j] = KIND == MOM_MONO ? mono_at(a.x, a.n, a.C, i) : a.x[i];
+    }
+    double s = 0.0, q = 0.0;
+#pragma unroll
+    for (int j = 0; j < kMomChunk / 256; j++) {
+        if (lo + threadIdx.x + 256LL * j < a.n) {
+            const double d = (double)v[j] - shift;
+            s += d;
+            q += d * d;
+        }
+    }
+    s = block_sum(s, red);
+    q = block_sum(q, red);
+    if (threadIdx.x == 0) {
+        a.partial[2 * blockIdx.x] = s;
+        a.partial[2 * blockIdx.x + 1] = q;
+    }
+}
+
+enum NormKind { NORM_CAC = 0, NORM_FLAT = 1, NORM_MIX = 2 };
+
+struct NormArgs {
+    const float* x;              // CAC: complex [C][FT]; FLAT: [n]; MIX: [C][n]
+    float* y;                    // CAC: [2C][FT]; FLAT: [n]; MIX: [C][n]
+    long long n;                 // the moments' count (CAC: 2 C FT floats; FLAT: n; MIX: samples)
+    long long count;             // outputs this kernel walks (CAC: C FT complex; FLAT: n; MIX: C n)
+    long long ft;                // CAC: F * T
+    int C;
+    const double* partial;
+    int n_partial;
+    double* stats;               // {mean, sd} as used
+};
+
+// mean and unbiased std from the pass-1 pairs (identical in every block).
+__device__ __forceinline__ void block_moments(const NormArgs& a, double shift, double* red, double& mean, double& sd) {
+    double s = 0.0, q = 0.0;
+    for (int b = (int)threadIdx.x; b < a.n_partial; b += 256) {
+        s += a.partial[2 * b];
+        q += a.partial[2 * b + 1];
+    }
+    s = block_sum(s, red);
+    q = block_sum(q, red);
+    const double n = (double)a.n;
+    mean = shift + s / n;
+    sd = sqrt(fmax(q - s * (s / n), 0.0) / (n - 1.0));
+}
+
+template <int KIND>
+__global__ __launch_bounds__(256) void normalize_kernel(NormArgs a) {
+#pragma clang fp contract(off)
+    __shared__ double red[4];
+    constexpr int PER = 4;
+    const long long e0 = (long long)blockIdx.x * (256 * PER) + threadIdx.x;
+    // Loads first: they are in flight while the statistics add up.
+    float2 vc[PER];
+    float vf[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const long long e = min(e0 + 256LL * k, a.count - 1);
+        if (KIND == NORM_CAC) vc[k] = reinterpret_cast<const float2*>(a.x)[e];
+        else vf[k] = a.x[e];
+    }
+    const double shift = KIND == NORM_MIX ? (double)mono_at(a.x, a.n, a.C, 0) : (double)a.x[0];
+    double mean, sd;
+    block_moments(a, shift, red, mean, sd);
+    double den;
+    if (KIND == NORM_MIX) {
+        sd = sd < 1e-8 ? 1e-8 : sd;              // std::max(std, 1e-8), NaN kept
+        den = sd;
+    } else {
+        den = 1e-5 + sd;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        a.stats[0] = mean;
+        a.stats[1] = sd;
+    }
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const long long e = e0 + 256LL * k;
+        if (e >= a.count) break;
+        if (KIND == NORM_CAC) {
+            const long long c = e / a.ft, i = e - c * a.ft;
+            a.y[(2 * c) * a.ft + i] = (float)(((double)vc[k].x - mean) / den);
+            a.y[(2 * c + 1) * a.ft + i] = (float)(((double)vc[k].y - mean) / den);
+        } else {
+            a.y[e] = (float)(((double)vf[k] - mean) / den);
+        }
+    }
+}
+
+// Spectral branch denormalise: ox [S][2C][FT] -> complex64 spec [S][C][FT].
+__global__ __launch_bounds__(256) void cac_denorm_kernel(const float* ox, float2* spec, long long ft, int C,
+                                                         long long count, const double* stats) {
+#pragma clang fp contract(off)
+    const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (e >= count) return;
+    const double mean = stats[0], sd = stats[1];
+    const long long sc = e / ft, i = e - sc * ft;          // sc = s * C + c
+    const long long s = sc / C, c = sc - s * C;
+    const float re = ox[(s * 2 * C + 2 * c) * ft + i], im = ox[(s * 2 * C + 2 * c + 1) * ft + i];
+    spec[e] = make_float2((float)((double)re * sd + mean), (float)((double)im * sd + mean));
+}
+
+// Time branch: out = (float)(t * sd + mean) + y, the add in float.
+__global__ __launch_bounds__(256) void time_add_kernel(const float* t, const float* y, float* out, long long n,
+                                                       const double* stats) {
+#pragma clang fp contract(off)
+    const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (e >= n) return;
+    const double mean = stats[0], sd = stats[1];
+    const float a = (float)((double)t[e] * sd + mean);
+    out[e] = a + y[e];
+}
+
+// ------------------------------------------------------------------------------- split
+struct SegArgs {
+    const float* buf;            // [C][total]
+    float* parts;                // [count][C][seg]
+    long long total, offset;
+    int length, seg, stride, first, C;
+};
+
+// parts[k][c][i] = buf[c][start_k + i] where buf has it, else 0 (TensorChunk.padded).
+__global__ __launch_bounds__(256) void segments_kernel(SegArgs a) {
+    const int k = (int)blockIdx.z, c = (int)blockIdx.y;
+    const int i = (int)blockIdx.x * 256 + (int)threadIdx.x;
+    if (i >= a.seg) return;
+    const int off = (a.first + k) * a.stride;
+    const int clen = min(a.seg, a.length - off);
+    const long long j = a.offset + off - (a.seg - clen) / 2 + i;
+    const bool in = j >= 0 && j < a.total;
+    const float v = a.buf[(long long)c * a.total + (in ? j : 0)];
+    a.parts[((long long)k * a.C + c) * a.seg + i] = in ? v : 0.0f;
+}
+
+struct OlaArgs {
+    const float* y;              // [n_chunks][tracks][seg]
+    float* out;                  // [tracks][length]
+    int tracks, length, seg, stride, n_chunks;
+    float mx;                    // the weights' maximum
+};
+
+constexpr int kOlaPer = 4;
+
+// Gather form of split()'s overlap-add for kOlaPer samples of one track per thread.
+__global__ __launch_bounds__(256) void split_ola_kernel(OlaArgs a) {
+#pragma clang fp contract(off)
+    const int sc = (int)blockIdx.y;
+    const int half = a.seg / 2;
+#pragma unroll
+    for (int p = 0; p < kOlaPer; p++) {
+        const int i = ((int)blockIdx.x * kOlaPer + p) * 256 + (int)threadIdx.x;
+        if (i >= a.length) return;
+        const int k_hi = min(i / a.stride, a.n_chunks - 1);
+        const int k_lo = i >= a.seg ? (i - a.seg) / a.stride + 1 : 0;   // first chunk with i - off < seg
+        float acc = 0.0f, sw = 0.0f;
+        for (int k = k_lo; k <= k_hi; k++) {
+            const int off = k * a.stride, r = i - off;
+            const int clen = min(a.seg, a.length - off);
+            const int trim = (a.seg - clen) / 2;
+            const float w = (float)(r < half ? r + 1 : a.seg - r) / a.mx;
+            const float prod = w * a.y[((long long)k * a.tracks + sc) * a.seg + trim + r];
+            acc = acc + prod;
+            sw = sw + w;
+        }
+        a.out[(long long)sc * a.length + i] = acc / sw;
+    }
+}
+
+long long mom_blocks(long long n) { return (n + kMomChunk - 1) / kMomChunk; }
+
+void check_ws(void* ws, size_t bytes, long long n) {
+    STX_REQUIRE(ws != nullptr, "normalise: workspace is NULL");
+    STX_REQUIRE((reinterpret_cast<uintptr_t>(ws) & 15) == 0, "normalise: workspace must be 16-byte aligned");
+    STX_REQUIRE(bytes >= (size_t)mom_blocks(n) * 16, "normalise: workspace too small (%zu < %zu bytes)", bytes,
+                (size_t)mom_blocks(n) * 16);
+}
+
+template <int MK, int NK>
+void normalize(const float* x, long long n_mom, long long count, long long ft, int C, float* y, double* stats,
+               void* ws, hipStream_t s) {
+    double* partial = static_cast<double*>(ws);
+    const long long nb = mom_blocks(n_mom);
+    STX_REQUIRE(nb < (1LL << 31) && count < (1LL << 40), "normalise: too many elements");
+    MomArgs m{x, n_mom, C, partial};
+    hipLaunchKernelGGL((moments_kernel<MK>), dim3((unsigned)nb), dim3(256), 0, s, m);
+    launch_check("moments_kernel");
+    NormArgs a{x, y, n_mom, count, ft, C, partial, (int)nb, stats};
+    const long long blocks = (count + 1023) / 1024;
+    STX_REQUIRE(blocks < (1LL << 31), "normalise: too many elements");
+    hipLaunchKernelGGL((normalize_kernel<NK>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+    launch_check("normalize_kernel");
+}
+
+}  // namespace
+}  // namespace stx
+
+using namespace stx;
+
+extern "C" {
+
+STX_API size_t stx_htdemucs_norm_workspace_size(int64_t n) { return n > 0 ? (size_t)mom_blocks(n) * 16 : 16; }
+
+STX_API stx_status stx_htdemucs_cac_normalize(const float* spec, int channels, int n_bins, int n_frames, float* mag,
+                                              double* stats, void* workspace, size_t workspace_bytes,
+                                              stx_stream stream) {
+    return guard([&] {
+        STX_REQUIRE(channels > 0 && n_bins > 0 && n_frames > 0, "cac_normalize: empty spectrum");
+        STX_REQUIRE(spec && mag && stats, "NULL buffer");
+        const long long ft = (long long)n_bins * n_frames, n = 2LL * channels * ft;
+        STX_REQUIRE(n > 1, "cac_normalize: need at least two values for the unbiased std");
+        check_ws(workspace, workspace_bytes, n);
+        normalize<MOM_FLAT, NORM_CAC>(spec, n, (long long)channels * ft, ft, channels, mag, stats, workspace,
+                                      as_stream(stream));
+    });
+}
+
+STX_API stx_status stx_htdemucs_wave_normalize(const float* x, int64_t n, float* out, double* stats, void* workspace,
+                                               size_t workspace_bytes, stx_stream stream) {
+    return guard([&] {
+        STX_REQUIRE(n > 1, "wave_normalize: need at least two samples for the unbiased std");
+        STX_REQUIRE(x && out && stats, "NULL buffer");
+        check_ws(workspace, workspace_bytes, n);
+        normalize<MOM_FLAT, NORM_FLAT>(x, n, n, 0, 1, out, stats, workspace, as_stream(stream));
+    });
+}
+
+STX_API stx_status stx_htdemucs_mix_normalize(const float* mix, int channels, int64_t len, float* out, double* stats,
+                                              void* workspace, size_t workspace_bytes, stx_stream stream) {
+    return guard([&] {
+        if (len <= 0) fail(STX_STATUS_INVALID_ARGUMENT, "empty input");     // src/htdemucs.cpp:537
+        STX_REQUIRE(channels > 0, "mix_normalize: channels must be positive");
+        STX_REQUIRE(mix && out && stats, "NULL buffer");
+        check_ws(workspace, workspace_bytes, len);
+        normalize<MOM_MONO, NORM_MIX>(mix, len, (long long)channels * len, 0, channels, out, stats, workspace,
+                                      as_stream(stream));
+    });
+}
+
+STX_API stx_status stx_htdemucs_cac_denormalize(const float* ox, int n_sources, int channels, int n_bins, int n_frames,
+                                                const double* stats, float* spec, stx_stream stream) {
+    return guard([&] {
+        STX_REQUIRE(n_sources >= 0 && channels > 0 && n_bins > 0 && n_frames >= 0, "cac_denormalize: bad shape");
+        const long long ft = (long long)n_bins * n_frames, count = (long long)n_sources * channels * ft;
+        if (count == 0) return;
+        STX_REQUIRE(ox && spec && stats, "NULL buffer");
+        const long long blocks = (count + 255) / 256;
+        STX_REQUIRE(blocks < (1LL << 31), "cac_denormalize: too many elements");
+        hipLaunchKernelGGL(cac_denorm_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), ox,
+                           reinterpret_cast<float2*>(spec), ft, channels, count, stats);
+        launch_check("cac_denorm_kernel");
+    });
+}
+
+STX_API stx_status stx_htdemucs_time_add(const float* xt, const float* y, int64_t n, const double* stats, float* out,
+                                         stx_stream stream) {
+    return guard([&] {
+        STX_REQUIRE(n >= 0, "time_add: negative count");
+        if (n == 0) return;
+        STX_REQUIRE(xt && y && out && stats, "NULL buffer");
+        const long long blocks = (n + 255) / 256;
+        STX_REQUIRE(blocks < (1LL << 31), "time_add: too many elements");
+        hipLaunchKernelGGL(time_add_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), xt, y, out,
+                           (long long)n, stats);
+        launch_check("time_add_kernel");
+    });
+}
+
+STX_API stx_status stx_htdemucs_split_plan(int length, int segment, float overlap, int* stride, int* n_chunks) {
+    return guard([&] {
+        STX_REQUIRE(stride && n_chunks, "NULL output");
+        STX_REQUIRE(length > 0 && segment > 0, "split_plan: length and segment must be positive");
+        const double ov = overlap < 0.0f ? 0.25 : (double)overlap;          // src/htdemucs.cpp:564-566
+        const int st = (int)((1.0 - ov) * segment);
+        if (st <= 0) fail(STX_STATUS_INVALID_ARGUMENT, "overlap must be < 1");
+        *stride = st;
+        *n_chunks = (int)(((long long)length + st - 1) / st);
+    });
+}
+
+STX_API stx_status stx_htdemucs_segments(const float* buf, int channels, int64_t total, int64_t offset, int length,
+                                         int segment, int stride, int first, int count, float* parts,
+                                         stx_stream stream) {
+    return guard([&] {
+        STX_REQUIRE(channels > 0 && total >= 0 && length > 0 && segment > 0 && stride > 0, "segments: bad geometry");
+        const int n = (int)(((long long)length + stride - 1) / stride);
+        STX_REQUIRE(first >= 0 && count >= 0 && (long long)first + count <= n, "segments: chunks out of range");
+        if (count == 0) return;
+        STX_REQUIRE(buf && parts, "NULL buffer");
+        STX_REQUIRE(total > 0, "segments: empty buffer");
+        STX_REQUIRE(count < 65536 && channels < 65536, "segments: too many chunks or channels");
+        SegArgs a{buf, parts, total, offset, length, segment, stride, first, channels};
+        const dim3 grid((unsigned)((segment + 255) / 256), (unsigned)channels, (unsigned)count);
+        hipLaunchKernelGGL(segments_kernel, grid, dim3(256), 0, as_stream(stream), a);
+        launch_check("segments_kernel");
+    });
+}
+
+STX_API stx_status stx_htdemucs_split_overlap_add(const float* y, int tracks, int length, int segment, int stride,
+                                                  float* out, stx_stream stream) {
+    return guard([&] {
+        STX_REQUIRE(tracks > 0 && length > 0 && segment > 0 && stride > 0, "split_overlap_add: bad geometry");
+        STX_REQUIRE(stride <= segment, "split_overlap_add: stride > segment leaves samples with no weight");
+        STX_REQUIRE(y && out, "NULL buffer");
+        STX_REQUIRE(tracks < 65536, "split_overlap_add: too many tracks");
+        OlaArgs a{};
+        a.y = y;
+        a.out = out;
+        a.tracks = tracks;
+        a.length = length;
+        a.seg = segment;
+        a.stride = stride;
+        a.n_chunks = (int)(((long long)length + stride - 1) / stride);
+        const int half = segment / 2;
+        a.mx = (float)std::max(half, segment - half);
+        const dim3 grid((unsigned)((length + 256 * kOlaPer - 1) / (256 * kOlaPer)), (unsigned)tracks);
+        hipLaunchKernelGGL(split_ola_kernel, grid, dim3(256), 0, as_stream(stream), a);
+        launch_check("split_ola_kernel");
+    });
+}
+
+}  // extern "C"

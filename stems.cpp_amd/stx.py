@@ -64,6 +64,15 @@ _SIGNATURES = {
     "stx_demix_track_workspace_size": (ctypes.c_size_t, [_i, ctypes.c_int64, _i, _i, _i, _i, _i, _i]),
     "stx_demix_track": (_i, [_vp, _i, ctypes.c_int64, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp,
                              ctypes.c_size_t, _vp]),
+    "stx_htdemucs_norm_workspace_size": (ctypes.c_size_t, [ctypes.c_int64]),
+    "stx_htdemucs_cac_normalize": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
+    "stx_htdemucs_wave_normalize": (_i, [_vp, ctypes.c_int64, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
+    "stx_htdemucs_mix_normalize": (_i, [_vp, _i, ctypes.c_int64, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
+    "stx_htdemucs_cac_denormalize": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp]),
+    "stx_htdemucs_time_add": (_i, [_vp, _vp, ctypes.c_int64, _vp, _vp, _vp]),
+    "stx_htdemucs_split_plan": (_i, [_i, _i, ctypes.c_float, _c_int_p, _c_int_p]),
+    "stx_htdemucs_segments": (_i, [_vp, _i, ctypes.c_int64, ctypes.c_int64, _i, _i, _i, _i, _i, _vp, _vp]),
+    "stx_htdemucs_split_overlap_add": (_i, [_vp, _i, _i, _i, _i, _vp, _vp]),
     "stx_group_norm_workspace_size": (ctypes.c_size_t, [_vp, _i]),
     "stx_group_norm": (_i, [_vp, _vp, _i, ctypes.c_float, _vp, _vp, _i, _vp, ctypes.c_size_t, _vp]),
     "stx_norm": (_i, [_vp, _vp, ctypes.c_float, _vp]),
@@ -498,6 +507,96 @@ def demix_track(mix, chunk, num_overlap, n_stems, separate, complement=False, sa
     check(lib().stx_demix_track(_ptr(mix), C, L, int(chunk), int(num_overlap), int(n_stems), int(bool(complement)),
                                 int(sample_rate), int(batch), ctypes.cast(cb, ctypes.c_void_p), None,
                                 ctypes.byref(opt), _ptr(out), _ptr(ws), ws.numel() * 4, _stream(stream)))
+    return out
+
+
+# ------------------------------------------------------------ HTDemucs pre/post + split
+def _norm_ws(n, device, workspace):
+    import torch
+    need = lib().stx_htdemucs_norm_workspace_size(int(n))
+    if workspace is None:
+        workspace = torch.empty((need + 7) // 8, dtype=torch.float64, device=device)
+    return workspace, workspace.numel() * workspace.element_size()
+
+
+def htdemucs_cac_normalize(spec, out=None, stats=None, workspace=None, stream=None):
+    """spec: complex64 [C, F, T] (f-major) -> (mag float32 [2C, F, T], stats float64 [2])."""
+    import torch
+    _require(spec, torch.complex64, "spec")
+    C, F, T = spec.shape
+    out = torch.empty((2 * C, F, T), dtype=torch.float32, device=spec.device) if out is None else out
+    stats = torch.empty(2, dtype=torch.float64, device=spec.device) if stats is None else stats
+    ws, nb = _norm_ws(2 * C * F * T, spec.device, workspace)
+    check(lib().stx_htdemucs_cac_normalize(_ptr(spec), C, F, T, _ptr(out), _ptr(stats), _ptr(ws), nb, _stream(stream)))
+    return out, stats
+
+
+def htdemucs_wave_normalize(x, out=None, stats=None, workspace=None, stream=None):
+    import torch
+    _require(x, torch.float32, "x")
+    out = torch.empty_like(x) if out is None else out
+    stats = torch.empty(2, dtype=torch.float64, device=x.device) if stats is None else stats
+    ws, nb = _norm_ws(x.numel(), x.device, workspace)
+    check(lib().stx_htdemucs_wave_normalize(_ptr(x), x.numel(), _ptr(out), _ptr(stats), _ptr(ws), nb, _stream(stream)))
+    return out, stats
+
+
+def htdemucs_mix_normalize(mix, out=None, stats=None, workspace=None, stream=None):
+    """mix float32 [C, len] -> (normalised mix, stats {ref_mean, ref_std})."""
+    import torch
+    _require(mix, torch.float32, "mix")
+    C, L = mix.shape
+    out = torch.empty_like(mix) if out is None else out
+    stats = torch.empty(2, dtype=torch.float64, device=mix.device) if stats is None else stats
+    ws, nb = _norm_ws(L, mix.device, workspace)
+    check(lib().stx_htdemucs_mix_normalize(_ptr(mix), C, L, _ptr(out), _ptr(stats), _ptr(ws), nb, _stream(stream)))
+    return out, stats
+
+
+def htdemucs_cac_denormalize(ox, stats, out=None, stream=None):
+    """ox float32 [S, 2C, F, T] -> complex64 [S, C, F, T]."""
+    import torch
+    _require(ox, torch.float32, "ox")
+    S, C2, F, T = ox.shape
+    out = torch.empty((S, C2 // 2, F, T), dtype=torch.complex64, device=ox.device) if out is None else out
+    check(lib().stx_htdemucs_cac_denormalize(_ptr(ox), S, C2 // 2, F, T, _ptr(stats), _ptr(out), _stream(stream)))
+    return out
+
+
+def htdemucs_time_add(xt, y, stats, out=None, stream=None):
+    import torch
+    out = torch.empty_like(xt) if out is None else out
+    check(lib().stx_htdemucs_time_add(_ptr(xt), _ptr(y), xt.numel(), _ptr(stats), _ptr(out), _stream(stream)))
+    return out
+
+
+def htdemucs_split_plan(length, segment, overlap=0.25):
+    st, n = ctypes.c_int(), ctypes.c_int()
+    check(lib().stx_htdemucs_split_plan(int(length), int(segment), float(overlap), ctypes.byref(st), ctypes.byref(n)))
+    return st.value, n.value
+
+
+def htdemucs_segments(buf, offset, length, segment, stride, first=0, count=None, out=None, stream=None):
+    """Padded chunk inputs of the view [offset, offset + length) of buf float32 [C, total]."""
+    import torch
+    _require(buf, torch.float32, "buf")
+    C, total = buf.shape
+    n = (length + stride - 1) // stride
+    count = n - first if count is None else count
+    out = torch.empty((count, C, segment), dtype=torch.float32, device=buf.device) if out is None else out
+    check(lib().stx_htdemucs_segments(_ptr(buf), C, total, int(offset), int(length), int(segment), int(stride),
+                                      int(first), int(count), _ptr(out), _stream(stream)))
+    return out
+
+
+def htdemucs_split_overlap_add(y, length, stride, out=None, stream=None):
+    """y float32 [n_chunks, tracks, segment] -> [tracks, length]."""
+    import torch
+    _require(y, torch.float32, "y")
+    n, tracks, segment = y.shape
+    out = torch.empty((tracks, length), dtype=torch.float32, device=y.device) if out is None else out
+    check(lib().stx_htdemucs_split_overlap_add(_ptr(y), tracks, int(length), segment, int(stride), _ptr(out),
+                                               _stream(stream)))
     return out
 
 

@@ -397,3 +397,123 @@ def ops():
     if _ops is None:
         _ops = _Ops()
     return _ops
+
+
+class _HTDemucs:
+    """HTDemucs pre/post-processing and split oracle (oracle/htdemucs_oracle.c), numpy in/out."""
+
+    def __init__(self):
+        L = ctypes.CDLL(ORACLE_PATH)
+        d = ctypes.c_double
+        dp = ctypes.POINTER(d)
+        i64 = ctypes.c_int64
+        L.orc_mean_std.restype = None
+        L.orc_mean_std.argtypes = [_vp, i64, dp, dp]
+        L.orc_cac_normalize.restype = None
+        L.orc_cac_normalize.argtypes = [_vp, _i, i64, d, d, _vp]
+        L.orc_normalize.restype = None
+        L.orc_normalize.argtypes = [_vp, i64, d, d, _vp]
+        L.orc_cac_denormalize.restype = None
+        L.orc_cac_denormalize.argtypes = [_vp, _i, _i, i64, d, d, _vp]
+        L.orc_time_add.restype = None
+        L.orc_time_add.argtypes = [_vp, _vp, i64, d, d, _vp]
+        L.orc_mix_normalize.restype = None
+        L.orc_mix_normalize.argtypes = [_vp, _i, i64, _vp, _vp]
+        L.orc_split_weights.restype = None
+        L.orc_split_weights.argtypes = [_i, _vp]
+        L.orc_split_count.restype = _i
+        L.orc_split_count.argtypes = [_i, _i, ctypes.c_float, ctypes.POINTER(_i)]
+        L.orc_segments.restype = None
+        L.orc_segments.argtypes = [_vp, _i, i64, i64, _i, _i, _i, _vp]
+        L.orc_split_ola.restype = None
+        L.orc_split_ola.argtypes = [_vp, _i, _i, _i, _i, _vp, _vp]
+        self.L = L
+
+    @staticmethod
+    def _f(a):
+        return np.ascontiguousarray(a, dtype=np.float32)
+
+    def mean_std(self, x):
+        x = self._f(x)
+        m, s = ctypes.c_double(), ctypes.c_double()
+        self.L.orc_mean_std(_np(x), x.size, ctypes.byref(m), ctypes.byref(s))
+        return m.value, s.value
+
+    def cac_pack(self, spec):
+        """complex64 [C, F, T] -> float32 [2C, F, T] (re, im planes), no normalisation."""
+        C = spec.shape[0]
+        out = np.empty((2 * C,) + spec.shape[1:], np.float32)
+        out[0::2] = spec.real
+        out[1::2] = spec.imag
+        return out
+
+    def cac_normalize(self, spec, mean, sd):
+        spec = np.ascontiguousarray(spec, dtype=np.complex64)
+        C = spec.shape[0]
+        ft = spec[0].size
+        mag = np.empty((2 * C,) + spec.shape[1:], np.float32)
+        self.L.orc_cac_normalize(_np(spec), C, ft, mean, sd, _np(mag))
+        return mag
+
+    def normalize(self, x, mean, sd):
+        x = self._f(x)
+        y = np.empty_like(x)
+        self.L.orc_normalize(_np(x), x.size, mean, sd, _np(y))
+        return y
+
+    def cac_denormalize(self, ox, mean, sd):
+        ox = self._f(ox)
+        S, C2 = ox.shape[:2]
+        ft = ox[0, 0].size
+        spec = np.empty((S, C2 // 2) + ox.shape[2:], np.complex64)
+        self.L.orc_cac_denormalize(_np(ox), S, C2 // 2, ft, mean, sd, _np(spec))
+        return spec
+
+    def time_add(self, t, y, mean, sd):
+        t, y = self._f(t), self._f(y)
+        out = np.empty_like(t)
+        self.L.orc_time_add(_np(t), _np(y), t.size, mean, sd, _np(out))
+        return out
+
+    def mix_normalize(self, mix):
+        mix = self._f(mix)
+        out = np.empty_like(mix)
+        stats = np.zeros(2, np.float64)
+        self.L.orc_mix_normalize(_np(mix), mix.shape[0], mix.shape[1], _np(out), _np(stats))
+        return out, stats
+
+    def split_weights(self, seg):
+        w = np.empty(seg, np.float32)
+        self.L.orc_split_weights(seg, _np(w))
+        return w
+
+    def split_count(self, length, seg, overlap):
+        st = ctypes.c_int()
+        n = self.L.orc_split_count(length, seg, overlap, ctypes.byref(st))
+        return st.value, n
+
+    def segments(self, buf, offset, length, seg, stride):
+        buf = self._f(buf)
+        C, total = buf.shape
+        n = (length + stride - 1) // stride
+        parts = np.empty((n, C, seg), np.float32)
+        self.L.orc_segments(_np(buf), C, total, offset, length, seg, stride, _np(parts))
+        return parts
+
+    def split_ola(self, y, length, stride):
+        y = self._f(y)
+        n, tracks, seg = y.shape
+        out = np.empty((tracks, length), np.float32)
+        sw = np.empty(length, np.float32)
+        self.L.orc_split_ola(_np(y), tracks, length, seg, stride, _np(out), _np(sw))
+        return out
+
+
+_htd = None
+
+
+def htdemucs():
+    global _htd
+    if _htd is None:
+        _htd = _HTDemucs()
+    return _htd

@@ -1,0 +1,163 @@
+"""GPU parity of the HTDemucs pre/post-processing and split (htdemucs.hip) against the oracle.
+
+Bars: the device statistics (mean, unbiased std) within 1e-12 relative of the oracle's
+sequential double sums (only the summation order differs); every normalised, denormalised or
+added value bit-exact against the oracle given the same statistics, and within rel_err 1e-6
+with the oracle's own; segments and the split overlap-add bit-exact.
+
+Shapes: one c1 segment (stereo, 343,980 samples, n_fft 4096: spectrum [2][2048][336], four
+sources) and the 180 s stereo song split into 31 segments of 343,980 samples at overlap 0.25
+(stride 257,985), with and without a shift view.
+"""
+import numpy as np
+import pytest
+
+import oracle_lib
+import stx
+import synth
+from metrics import rel_err
+
+pytestmark = pytest.mark.gpu
+
+SEG, NFFT = 343980, 4096
+SONG = 7938000
+
+
+@pytest.fixture(scope="module")
+def htd():
+    return oracle_lib.htdemucs()
+
+
+def dev(a, device):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def close_stats(got, want):
+    return abs(got[0] - want[0]) <= 1e-12 * max(abs(want[0]), want[1]) and abs(got[1] - want[1]) <= 1e-12 * want[1]
+
+
+def test_cac_normalize_c1(device, htd):
+    """src/htdemucs.cpp:424-436 on the device spectrum of one c1 segment."""
+    x = dev(synth.normal(1, (2, SEG), 0.1), device)
+    fft = stx.FFT(NFFT)
+    spec = stx.htdemucs_spec(fft, x)                                   # complex64 [2, 2048, 336]
+    mag, stats = stx.htdemucs_cac_normalize(spec)
+    sh = host(spec)
+    st = host(stats)
+    want_stats = htd.mean_std(htd.cac_pack(sh))
+    assert close_stats(st, want_stats)
+    assert np.array_equal(host(mag), htd.cac_normalize(sh, st[0], st[1]))
+    assert rel_err(host(mag), htd.cac_normalize(sh, *want_stats)) <= 1e-6
+
+
+def test_wave_normalize_c1(device, htd):
+    xh = synth.normal(2, (2, SEG), 0.1) + 0.003
+    y, stats = stx.htdemucs_wave_normalize(dev(xh, device))
+    st = host(stats)
+    assert close_stats(st, htd.mean_std(xh))
+    assert np.array_equal(host(y), htd.normalize(xh, st[0], st[1]))
+
+
+@pytest.mark.parametrize("n", [2, 3, 8191, 8192, 8193, 100003])
+def test_wave_normalize_ragged(device, htd, n):
+    xh = synth.normal(3, (n,), 1.0) * 5 + 2
+    y, stats = stx.htdemucs_wave_normalize(dev(xh, device))
+    st = host(stats)
+    assert close_stats(st, htd.mean_std(xh))
+    assert np.array_equal(host(y), htd.normalize(xh, st[0], st[1]))
+
+
+def test_mix_normalize_song(device, htd):
+    """src/htdemucs.cpp:539-549 on the 180 s stereo song."""
+    mix = synth.sines_plus_pink(5, 2, SONG)
+    out, stats = stx.htdemucs_mix_normalize(dev(mix, device))
+    want, wstats = htd.mix_normalize(mix)
+    st = host(stats)
+    assert close_stats(st, wstats)
+    assert rel_err(host(out), want) <= 1e-6
+
+
+def test_mix_normalize_silence_and_errors(device):
+    import torch
+    out, stats = stx.htdemucs_mix_normalize(torch.zeros((2, 1000), device=device))
+    st = host(stats)
+    assert st[0] == 0.0 and st[1] == 1e-8
+    assert np.all(host(out) == 0.0)
+    with pytest.raises(stx.StxError) as e:
+        stx.htdemucs_mix_normalize(torch.zeros((2, 0), device=device))
+    assert e.value.status == stx.STATUS_INVALID_ARGUMENT and "empty input" in e.value.message
+
+
+def test_denormalize_and_time_add_c1(device, htd):
+    """src/htdemucs.cpp:465-470 for four sources: denormalise, iSTFT, time branch + add."""
+    import torch
+    S, C, F, T = 4, 2, 2048, 336
+    ox = dev(synth.normal(4, (S, 2 * C, F, T), 1.0), device)
+    stats = torch.tensor([0.0123, 0.456], dtype=torch.float64, device=device)
+    spec = stx.htdemucs_cac_denormalize(ox, stats)
+    want = htd.cac_denormalize(host(ox), 0.0123, 0.456)
+    assert np.array_equal(host(spec), want)
+    fft = stx.FFT(NFFT)
+    y = stx.htdemucs_ispec(fft, spec.reshape(S * C, F, T), SEG)
+    xt = dev(synth.normal(5, (S * C, SEG), 1.0), device)
+    tstats = torch.tensor([-0.002, 0.09], dtype=torch.float64, device=device)
+    out = stx.htdemucs_time_add(xt, y, tstats)
+    assert np.array_equal(host(out), htd.time_add(host(xt), host(y), -0.002, 0.09))
+
+
+@pytest.mark.parametrize("shifted", [False, True])
+def test_segments_song(device, htd, shifted):
+    """TensorChunk views of the 180 s song: the plain split and one shift view (the mix padded
+    by sr/2 on both sides, src/htdemucs.cpp:613-621)."""
+    mix = synth.sines_plus_pink(6, 2, SONG)
+    if shifted:
+        max_shift, off = 22050, 12345
+        buf = np.zeros((2, SONG + 2 * max_shift), np.float32)
+        buf[:, max_shift:max_shift + SONG] = mix
+        offset, length = off, SONG + max_shift - off
+    else:
+        buf, offset, length = mix, 0, SONG
+    stride, n = stx.htdemucs_split_plan(length, SEG, 0.25)
+    assert (stride, n) == htd.split_count(length, SEG, 0.25)
+    bd = dev(buf, device)
+    want = htd.segments(buf, offset, length, SEG, stride)
+    got = host(stx.htdemucs_segments(bd, offset, length, SEG, stride))
+    assert np.array_equal(got, want)
+    part = host(stx.htdemucs_segments(bd, offset, length, SEG, stride, first=n - 2, count=2))
+    assert np.array_equal(part, want[n - 2:])
+
+
+@pytest.mark.parametrize("length,tracks", [(SONG, 8), (SEG, 8), (1000, 3), (SEG + 1, 2)])
+def test_split_overlap_add(device, htd, length, tracks):
+    """src/htdemucs.cpp:594-606, bit-exact: float products and sums in chunk order."""
+    seg = SEG if length >= SEG else 300
+    stride, n = stx.htdemucs_split_plan(length, seg, 0.25)
+    y = synth.normal(7, (n, tracks, seg), 1.0)
+    got = host(stx.htdemucs_split_overlap_add(dev(y, device), length, stride))
+    assert np.array_equal(got, htd.split_ola(y, length, stride))
+
+
+def test_split_identity_model(device):
+    """A model that returns its input: split() gives the normalised mix back."""
+    import torch
+    mix = dev(synth.sines_plus_pink(8, 2, 1_000_000), device)
+    norm, stats = stx.htdemucs_mix_normalize(mix)
+    stride, n = stx.htdemucs_split_plan(1_000_000, SEG, 0.25)
+    parts = stx.htdemucs_segments(norm, 0, 1_000_000, SEG, stride)
+    y = torch.cat([parts, parts], dim=1).contiguous()                   # two sources
+    out = host(stx.htdemucs_split_overlap_add(y, 1_000_000, stride))
+    nh = host(norm)
+    assert np.max(np.abs(out[:2] - nh)) <= 4e-7 * np.max(np.abs(nh))
+
+
+def test_split_errors(device):
+    with pytest.raises(stx.StxError) as e:
+        stx.htdemucs_split_plan(1000, 300, 1.0)
+    assert "overlap must be < 1" in e.value.message
