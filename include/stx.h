@@ -368,6 +368,35 @@ STX_API stx_status stx_htdemucs_segments(const float* buf, int channels, int64_t
 STX_API stx_status stx_htdemucs_split_overlap_add(const float* y, int tracks, int length, int segment, int stride,
                                                   float* out, stx_stream stream);
 
+/* Model callback of stx_htdemucs_separate: runs model `model` of the bag on `count` segments.
+ * parts is device [count][C][segment] (normalised by the mono mix, read only); y is device
+ * [count][n_sources][C][segment] (to fill): HTDemucs::forward / Impl::run per segment
+ * (src/htdemucs.cpp:419-474, whose pre/post-processing the calls above provide). Work may be
+ * enqueued on `stream`; return 0 on success. */
+typedef int32_t (*stx_model_fn)(void* user, int32_t model, const float* parts, int64_t count, float* y,
+                                stx_stream stream);
+
+/* Bytes of device workspace stx_htdemucs_separate needs (batch = segments per model call). */
+STX_API size_t stx_htdemucs_separate_workspace_size(int channels, int64_t len, int segment, int n_sources, int batch,
+                                                   int shifts, int sample_rate, float overlap);
+
+/* HTDemucs::separate (src/htdemucs.cpp:534-644) around any model: normalise by the mono mix,
+ * for each model of the bag split() the mix (or, with shifts > 0, `shifts` views at offsets
+ * drawn from one std::mt19937(seed) with uniform_int_distribution(0, sample_rate / 2) per
+ * model, into the mix zero-padded by sample_rate / 2) through `forward` in batches of `batch`
+ * segments, average the shifts, weight the models by bag_weights (host [n_models][n_sources];
+ * a zero weight skips the source), divide by the weight totals and denormalise. mix is device
+ * [C][len]; out is device [n_sources][C][len]. Float arithmetic and orders as the reference's.
+ * options->overlap < 0 means 0.25. CANCELLED when should_cancel returns non-zero (polled before
+ * each segment); progress reports (done, n_models * max(1, shifts) * ceil(len / stride)) after
+ * each segment, as the reference does. INVALID_ARGUMENT for len <= 0 ("empty input") or
+ * overlap >= 1. n_sources is at most 64. */
+STX_API stx_status stx_htdemucs_separate(const float* mix, int channels, int64_t len, int segment, int n_sources,
+                                         int n_models, const float* bag_weights, int sample_rate, int batch,
+                                         stx_model_fn forward, void* forward_user,
+                                         const stx_separate_options* options, float* out, void* workspace,
+                                         size_t workspace_bytes, stx_stream stream);
+
 /* ------------------------------------------------------------------------------------------
  * ggml ops of the HTDemucs and RoFormer graphs. ggml's sources are not in the reference tree
  * (an un-vendored submodule), so each entry point cites the call sites whose semantics it

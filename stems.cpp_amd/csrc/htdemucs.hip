@@ -18,6 +18,8 @@
 // divides by the summed weights, so it is bit-exact.
 #include <algorithm>
 #include <cmath>
+#include <random>
+#include <vector>
 
 #include "common.hpp"
 
@@ -229,7 +231,102 @@ __global__ __launch_bounds__(256) void split_ola_kernel(OlaArgs a) {
     }
 }
 
+// ---------------------------------------------------------------- separate() accumulation
+// res[t][i] = (first ? 0 : res[t][i]) + o[t][src_off + i]: one shift's output, added in shift order
+// (src/htdemucs.cpp:622-624). The first shift also adds to 0.0f, as the reference's zeroed res does.
+__global__ __launch_bounds__(256) void shift_add_kernel(float* res, const float* o, long long len, long long o_len,
+                                                        long long src_off, long long count, int first) {
+    const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (e >= count) return;
+    const long long t = e / len, i = e - t * len;
+    const float prev = first ? 0.0f : res[e];
+    res[e] = prev + o[t * o_len + src_off + i];
+}
+
+// estimates[s] += w_s * (res[s] / shifts) for every source with w_s != 0 (:625-631, the
+// division by shifts of :626 when shifts > 0); the first model adds to 0.0f.
+struct BagArgs {
+    float* est;
+    const float* res;
+    long long plane;             // C * len
+    long long count;             // S * plane
+    float w[64];
+    float shifts;                // 0: no division
+    int first;
+};
+
+__global__ __launch_bounds__(256) void bag_add_kernel(BagArgs a) {
+#pragma clang fp contract(off)
+    const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (e >= a.count) return;
+    const int s = (int)(e / a.plane);
+    const float w = a.w[s];
+    const float prev = a.first ? 0.0f : a.est[e];
+    if (w == 0.0f) {
+        if (a.first) a.est[e] = prev;
+        return;
+    }
+    float v = a.res[e];
+    if (a.shifts != 0.0f) v = v / a.shifts;
+    const float p = w * v;
+    a.est[e] = prev + p;
+}
+
+// out = (float)(est / totals[s] * ref_std + ref_mean) (:633-638).
+struct FinalArgs {
+    float* est;
+    long long plane, count;
+    float totals[64];
+    const double* stats;
+};
+
+__global__ __launch_bounds__(256) void bag_final_kernel(FinalArgs a) {
+#pragma clang fp contract(off)
+    const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (e >= a.count) return;
+    const int s = (int)(e / a.plane);
+    const float q = a.est[e] / a.totals[s];
+    a.est[e] = (float)((double)q * a.stats[1] + a.stats[0]);
+}
+
 long long mom_blocks(long long n) { return (n + kMomChunk - 1) / kMomChunk; }
+
+unsigned grid256(long long n) { return (unsigned)((n + 255) / 256); }
+
+struct Cancelled {};
+
+struct SepLayout {
+    size_t mix, stats, mom, parts, y, o, res, total;
+    int stride, max_chunks;
+    long long max_view;
+};
+
+SepLayout sep_layout(int C, long long len, int seg, int S, int batch, int shifts, int sr, float overlap) {
+    SepLayout L{};
+    const double ov = overlap < 0.0f ? 0.25 : (double)overlap;
+    L.stride = (int)((1.0 - ov) * seg);
+    const long long max_shift = shifts > 0 ? sr / 2 : 0;
+    L.max_view = len + max_shift;                // a shift view's length is len + max_shift - offset
+    L.max_chunks = L.stride > 0 ? (int)((L.max_view + L.stride - 1) / L.stride) : 0;
+    auto align = [](size_t b) { return (b + 255) / 256 * 256; };
+    size_t o = 0;
+    L.mix = o;
+    o += align(sizeof(float) * (size_t)C * len);
+    L.stats = o;
+    o += align(2 * sizeof(double));
+    L.mom = o;
+    o += align((size_t)mom_blocks(len) * 16);
+    L.parts = o;
+    o += align(sizeof(float) * (size_t)batch * C * seg);
+    L.y = o;
+    o += align(sizeof(float) * (size_t)L.max_chunks * S * C * seg);
+    L.o = o;
+    o += align(sizeof(float) * (size_t)S * C * L.max_view);
+    L.res = o;
+    if (shifts > 0) o += align(sizeof(float) * (size_t)S * C * len);
+    L.total = o;
+    return L;
+}
 
 void check_ws(void* ws, size_t bytes, long long n) {
     STX_REQUIRE(ws != nullptr, "normalise: workspace is NULL");
@@ -378,6 +475,117 @@ STX_API stx_status stx_htdemucs_split_overlap_add(const float* y, int tracks, in
         const dim3 grid((unsigned)((length + 256 * kOlaPer - 1) / (256 * kOlaPer)), (unsigned)tracks);
         hipLaunchKernelGGL(split_ola_kernel, grid, dim3(256), 0, as_stream(stream), a);
         launch_check("split_ola_kernel");
+    });
+}
+
+STX_API size_t stx_htdemucs_separate_workspace_size(int channels, int64_t len, int segment, int n_sources, int batch,
+                                                   int shifts, int sample_rate, float overlap) {
+    if (channels <= 0 || len <= 0 || segment <= 0 || n_sources <= 0 || batch <= 0) return 0;
+    return sep_layout(channels, len, segment, n_sources, batch, std::max(0, shifts), sample_rate, overlap).total;
+}
+
+STX_API stx_status stx_htdemucs_separate(const float* mix, int channels, int64_t len, int segment, int n_sources,
+                                         int n_models, const float* bag_weights, int sample_rate, int batch,
+                                         stx_model_fn forward, void* forward_user,
+                                         const stx_separate_options* options, float* out, void* workspace,
+                                         size_t workspace_bytes, stx_stream stream) {
+    return guard([&] {
+        stx_separate_options opt{};
+        opt.overlap = -1.0f;
+        if (options) opt = *options;
+        if (len <= 0) fail(STX_STATUS_INVALID_ARGUMENT, "empty input");                        // :537
+        STX_REQUIRE(len < (1LL << 31) - sample_rate, "separate: input too long");
+        STX_REQUIRE(channels >= 1 && n_sources >= 1 && n_sources <= 64 && n_models >= 1 && segment >= 2 && batch >= 1,
+                    "separate: bad channels/sources/models/segment/batch");
+        STX_REQUIRE(mix && out && forward && workspace && bag_weights, "NULL argument");
+        const int shifts = std::max(0, opt.shifts);
+        STX_REQUIRE(shifts == 0 || sample_rate >= 2, "separate: bad sample rate for shifts");
+        const SepLayout L = sep_layout(channels, len, segment, n_sources, batch, shifts, sample_rate, opt.overlap);
+        if (L.stride <= 0) fail(STX_STATUS_INVALID_ARGUMENT, "overlap must be < 1");            // :566
+        STX_REQUIRE(workspace_bytes >= L.total, "workspace too small: %zu bytes, need %zu", workspace_bytes, L.total);
+        char* ws = static_cast<char*>(workspace);
+        float* d_mix = reinterpret_cast<float*>(ws + L.mix);
+        double* d_stats = reinterpret_cast<double*>(ws + L.stats);
+        float* d_parts = reinterpret_cast<float*>(ws + L.parts);
+        float* d_y = reinterpret_cast<float*>(ws + L.y);
+        float* d_o = reinterpret_cast<float*>(ws + L.o);
+        float* d_res = reinterpret_cast<float*>(ws + L.res);
+        const hipStream_t s = as_stream(stream);
+        const int S = n_sources, C = channels, tracks = S * C;
+        // Normalise by the mono mix (:539-549).
+        normalize<MOM_MONO, NORM_MIX>(mix, len, (long long)C * len, 0, C, d_mix, d_stats, ws + L.mom, s);
+
+        const int passes_per_split = (int)((len + L.stride - 1) / L.stride);                    // :577
+        const int total_passes = n_models * std::max(1, shifts) * passes_per_split;
+        int done = 0;
+        std::mt19937 rng(opt.seed);                                                              // :580
+        std::vector<float> totals(S, 0.0f);
+        // split() of one view of d_mix into d_o [tracks][length] (:589-607).
+        auto split = [&](int model, long long offset, int length) {
+            const int n = (int)(((long long)length + L.stride - 1) / L.stride);
+            for (int first = 0; first < n; first += batch) {
+                const int count = std::min(batch, n - first);
+                for (int k = 0; k < count; k++)
+                    if (opt.should_cancel && opt.should_cancel(opt.user)) throw Cancelled{};       // :591
+                const stx_status cs = stx_htdemucs_segments(d_mix, C, len, offset, length, segment, L.stride, first,
+                                                            count, d_parts, stream);
+                if (cs != STX_STATUS_OK) fail(cs, "%s", stx_last_error());
+                float* yk = d_y + (size_t)first * tracks * segment;
+                const int32_t rc = forward(forward_user, model, d_parts, count, yk, stream);
+                if (rc != 0) fail(STX_STATUS_RUNTIME_ERROR, "model forward failed with %d", rc);
+                for (int k = 0; k < count; k++)
+                    if (opt.progress) opt.progress(opt.user, ++done, total_passes);               // :603
+            }
+            const stx_status os = stx_htdemucs_split_overlap_add(d_y, tracks, length, segment, L.stride, d_o, stream);
+            if (os != STX_STATUS_OK) fail(os, "%s", stx_last_error());
+        };
+        try {
+            for (int mi = 0; mi < n_models; mi++) {
+                const float* res = d_o;
+                if (shifts == 0) {
+                    split(mi, 0, (int)len);
+                } else {
+                    // Shift views of the mix zero-padded by max_shift on both sides (:612-624): a view
+                    // at `offset` into the padded copy is the view at offset - max_shift of the mix
+                    // itself with zeros outside it, which is what the segment kernel reads.
+                    const int max_shift = sample_rate / 2;
+                    std::uniform_int_distribution<int> dist(0, max_shift);
+                    for (int k = 0; k < shifts; k++) {
+                        const int offset = dist(rng);
+                        const int length = (int)len + max_shift - offset;
+                        split(mi, (long long)offset - max_shift, length);
+                        hipLaunchKernelGGL(shift_add_kernel, dim3(grid256((long long)tracks * len)), dim3(256), 0, s,
+                                           d_res, d_o, (long long)len, (long long)length,
+                                           (long long)(max_shift - offset), (long long)tracks * len, k == 0 ? 1 : 0);
+                        launch_check("shift_add_kernel");
+                    }
+                    res = d_res;
+                }
+                BagArgs b{};
+                b.est = out;
+                b.res = res;
+                b.plane = (long long)C * len;
+                b.count = (long long)S * b.plane;
+                for (int si = 0; si < S; si++) {
+                    b.w[si] = bag_weights[(size_t)mi * S + si];
+                    totals[si] += b.w[si];                                                       // :627
+                }
+                b.shifts = shifts > 0 ? (float)shifts : 0.0f;
+                b.first = mi == 0 ? 1 : 0;
+                hipLaunchKernelGGL(bag_add_kernel, dim3(grid256(b.count)), dim3(256), 0, s, b);
+                launch_check("bag_add_kernel");
+            }
+        } catch (const Cancelled&) {
+            fail(STX_STATUS_CANCELLED, "cancelled");
+        }
+        FinalArgs f{};
+        f.est = out;
+        f.plane = (long long)C * len;
+        f.count = (long long)S * f.plane;
+        for (int si = 0; si < S; si++) f.totals[si] = totals[si];
+        f.stats = d_stats;
+        hipLaunchKernelGGL(bag_final_kernel, dim3(grid256(f.count)), dim3(256), 0, s, f);
+        launch_check("bag_final_kernel");
     });
 }
 

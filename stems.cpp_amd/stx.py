@@ -73,6 +73,10 @@ _SIGNATURES = {
     "stx_htdemucs_split_plan": (_i, [_i, _i, ctypes.c_float, _c_int_p, _c_int_p]),
     "stx_htdemucs_segments": (_i, [_vp, _i, ctypes.c_int64, ctypes.c_int64, _i, _i, _i, _i, _i, _vp, _vp]),
     "stx_htdemucs_split_overlap_add": (_i, [_vp, _i, _i, _i, _i, _vp, _vp]),
+    "stx_htdemucs_separate_workspace_size": (ctypes.c_size_t, [_i, ctypes.c_int64, _i, _i, _i, _i, _i,
+                                                               ctypes.c_float]),
+    "stx_htdemucs_separate": (_i, [_vp, _i, ctypes.c_int64, _i, _i, _i, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp,
+                                   ctypes.c_size_t, _vp]),
     "stx_group_norm_workspace_size": (ctypes.c_size_t, [_vp, _i]),
     "stx_group_norm": (_i, [_vp, _vp, _i, ctypes.c_float, _vp, _vp, _i, _vp, ctypes.c_size_t, _vp]),
     "stx_norm": (_i, [_vp, _vp, ctypes.c_float, _vp]),
@@ -597,6 +601,52 @@ def htdemucs_split_overlap_add(y, length, stride, out=None, stream=None):
     out = torch.empty((tracks, length), dtype=torch.float32, device=y.device) if out is None else out
     check(lib().stx_htdemucs_split_overlap_add(_ptr(y), tracks, int(length), segment, int(stride), _ptr(out),
                                                _stream(stream)))
+    return out
+
+
+MODEL_FN = ctypes.CFUNCTYPE(ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p, ctypes.c_int64,
+                            ctypes.c_void_p, ctypes.c_void_p)
+
+
+def htdemucs_separate(mix, segment, n_sources, bag_weights, forward, sample_rate=44100, batch=4, shifts=0,
+                      overlap=-1.0, seed=0, progress=None, should_cancel=None, stream=None):
+    """HTDemucs::separate around a Python model.
+
+    forward(model, parts_ptr, count, y_ptr, stream_ptr) -> int gets raw device pointers: parts
+    [count][C][segment] and y [count][n_sources][C][segment] float32. bag_weights: host
+    [n_models][n_sources]."""
+    import numpy as np
+    import torch
+    _require(mix, torch.float32, "mix")
+    C, L = mix.shape
+    bag = np.ascontiguousarray(bag_weights, dtype=np.float32)
+    n_models = bag.shape[0]
+    ws_bytes = lib().stx_htdemucs_separate_workspace_size(C, L, int(segment), int(n_sources), int(batch),
+                                                          int(shifts), int(sample_rate), float(overlap))
+    ws = workspace(max(ws_bytes, 4), mix.device)
+    out = torch.empty((n_sources, C, L), dtype=torch.float32, device=mix.device)
+
+    def fwd(user, model, parts, count, y, st):
+        try:
+            return int(forward(model, parts, count, y, st))
+        except Exception:
+            import traceback
+            traceback.print_exc()
+            return -1
+
+    def prog(user, done, total):
+        progress(done, total)
+
+    def canc(user):
+        return 1 if should_cancel() else 0
+
+    cb = MODEL_FN(fwd)
+    opt = SeparateOptions(int(shifts), float(overlap), int(seed),
+                          PROGRESS_FN(prog) if progress else PROGRESS_FN(),
+                          CANCEL_FN(canc) if should_cancel else CANCEL_FN(), None)
+    check(lib().stx_htdemucs_separate(_ptr(mix), C, L, int(segment), int(n_sources), n_models, _np_ptr(bag),
+                                      int(sample_rate), int(batch), ctypes.cast(cb, ctypes.c_void_p), None,
+                                      ctypes.byref(opt), _ptr(out), _ptr(ws), ws.numel() * 4, _stream(stream)))
     return out
 
 

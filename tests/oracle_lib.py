@@ -427,6 +427,8 @@ class _HTDemucs:
         L.orc_segments.argtypes = [_vp, _i, i64, i64, _i, _i, _i, _vp]
         L.orc_split_ola.restype = None
         L.orc_split_ola.argtypes = [_vp, _i, _i, _i, _i, _vp, _vp]
+        L.orc_htdemucs_shift_offsets.restype = None
+        L.orc_htdemucs_shift_offsets.argtypes = [ctypes.c_uint32, _i, _i, _i, _vp]
         self.L = L
 
     @staticmethod
@@ -499,6 +501,49 @@ class _HTDemucs:
         parts = np.empty((n, C, seg), np.float32)
         self.L.orc_segments(_np(buf), C, total, offset, length, seg, stride, _np(parts))
         return parts
+
+    def shift_offsets(self, seed, max_shift, n_models, shifts):
+        out = np.zeros((n_models, shifts), np.int32)
+        self.L.orc_htdemucs_shift_offsets(seed, max_shift, n_models, shifts, _np(out))
+        return out
+
+    def separate(self, mix, segment, bag, model, sample_rate=44100, shifts=0, overlap=-1.0, seed=0):
+        """HTDemucs::separate (src/htdemucs.cpp:534-644) composed from the oracle's pieces and numpy
+        float32 arithmetic; model(m, parts [n][C][seg]) -> [n][S*C][seg]."""
+        C, L = mix.shape
+        S = bag.shape[1]
+        norm, stats = self.mix_normalize(mix)
+        stride, _ = self.split_count(L, segment, overlap)
+
+        def split(m, offset, length):
+            parts = self.segments(norm, offset, length, segment, stride)
+            return self.split_ola(model(m, parts), length, stride)
+
+        est = np.zeros((S * C, L), np.float32)
+        totals = np.zeros(S, np.float32)
+        ms = sample_rate // 2
+        offs = self.shift_offsets(seed, ms, bag.shape[0], shifts) if shifts > 0 else None
+        for m in range(bag.shape[0]):
+            if shifts == 0:
+                res = split(m, 0, L)
+            else:
+                res = np.zeros((S * C, L), np.float32)
+                for k in range(shifts):
+                    off = int(offs[m, k])
+                    o = split(m, off - ms, L + ms - off)
+                    res += o[:, ms - off:ms - off + L]
+                res /= np.float32(shifts)
+            for s in range(S):
+                w = np.float32(bag[m, s])
+                totals[s] += w
+                if w == 0.0:
+                    continue
+                est[s * C:(s + 1) * C] += w * res[s * C:(s + 1) * C]
+        out = np.empty_like(est)
+        for s in range(S):
+            q = est[s * C:(s + 1) * C] / totals[s]
+            out[s * C:(s + 1) * C] = (q.astype(np.float64) * stats[1] + stats[0]).astype(np.float32)
+        return out.reshape(S, C, L)
 
     def split_ola(self, y, length, stride):
         y = self._f(y)

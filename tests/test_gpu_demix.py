@@ -5,32 +5,15 @@ Chunk inputs and the overlap-add are bit-exact with the oracle for identical chu
 (stx_demix_track, RoFormer::separate) is checked with a per-stem-gain separator (bit-exact),
 the identity separator under shifts, the complement stem, progress/cancel and error codes.
 """
-import ctypes
-
 import numpy as np
 import pytest
 
 import oracle_lib
 import stx
 import synth
+from hip_util import d2d
 
 pytestmark = pytest.mark.gpu
-
-_hip = None
-
-
-def hip():
-    global _hip
-    if _hip is None:
-        _hip = ctypes.CDLL("libamdhip64.so")
-        _hip.hipMemcpyAsync.restype = ctypes.c_int
-        _hip.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
-                                        ctypes.c_void_p]
-    return _hip
-
-
-def d2d(dst, src, nbytes, stream):
-    assert hip().hipMemcpyAsync(ctypes.c_void_p(dst), ctypes.c_void_p(src), nbytes, 3, ctypes.c_void_p(stream)) == 0
 
 
 @pytest.fixture(scope="module")

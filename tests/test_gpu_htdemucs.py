@@ -161,3 +161,64 @@ def test_split_errors(device):
     with pytest.raises(stx.StxError) as e:
         stx.htdemucs_split_plan(1000, 300, 1.0)
     assert "overlap must be < 1" in e.value.message
+
+
+# --------------------------------------------------------------------- separate() driver
+def gain_model(gains, C, seg, batch, device):
+    """Model m returns gains[m][s] * segment for source s: linear, so the oracle composes it."""
+    import torch
+    from hip_util import d2d
+    g = torch.tensor(gains, dtype=torch.float32, device=device)        # [n_models][S]
+    buf = torch.empty((batch, C, seg), dtype=torch.float32, device=device)
+
+    def forward(model, parts, count, y, stream):
+        d2d(buf.data_ptr(), parts, count * C * seg * 4, stream)
+        yt = (g[model][None, :, None, None] * buf[:count, None]).contiguous()   # [count][S][C][seg]
+        d2d(y, yt.data_ptr(), yt.numel() * 4, stream)
+        return 0
+
+    def np_model(m, parts):
+        gm = np.array(gains, np.float32)[m]
+        y = gm[None, :, None, None] * parts[:, None]
+        return y.reshape(parts.shape[0], -1, parts.shape[2])
+    return forward, np_model
+
+
+@pytest.mark.parametrize("shifts,n_models", [(0, 1), (2, 2)])
+def test_separate_gain_models_vs_oracle(device, htd, shifts, n_models):
+    """HTDemucs::separate with a bag of linear models against the oracle's composition
+    (same mono-mix statistics fed to both: the driver's are read back from its own normalise)."""
+    C, L, seg, sr = 2, 1_000_003, SEG, 44100
+    gains = [[0.5, -1.25, 2.0, 1.0], [1.5, 0.0, -0.5, 0.75]][:n_models]
+    bag = np.array([[1.0, 1.0, 1.0, 1.0], [0.5, 2.0, 0.0, 1.0]], np.float32)[:n_models]
+    mix = synth.sines_plus_pink(31, C, L)
+    forward, np_model = gain_model(gains, C, seg, 3, device)
+    out = host(stx.htdemucs_separate(dev(mix, device), seg, 4, bag, forward, sample_rate=sr, batch=3,
+                                      shifts=shifts, seed=11))
+    want = htd.separate(mix, seg, bag, np_model, sample_rate=sr, shifts=shifts, seed=11)
+    # The device mono-mix statistics differ from the oracle's sequential sums in the last bits of
+    # a double, which can move a normalised sample by one float ulp; everything after is exact.
+    assert rel_err(out, want) <= 1e-6
+
+
+def test_separate_progress_cancel_and_errors(device):
+    import torch
+    C, L, seg = 1, 50_000, 8_000
+    mix = dev(synth.normal(32, (C, L), 0.2), device)
+    forward, _ = gain_model([[1.0]], C, seg, 2, device)
+    seen = []
+    stx.htdemucs_separate(mix, seg, 1, np.ones((1, 1), np.float32), forward, batch=2,
+                          progress=lambda d, t: seen.append((d, t)))
+    stride, n = stx.htdemucs_split_plan(L, seg, 0.25)
+    assert seen == [(d, n) for d in range(1, n + 1)]
+    calls = []
+
+    def cancel():
+        calls.append(1)
+        return len(calls) >= 3
+    with pytest.raises(stx.StxError) as e:
+        stx.htdemucs_separate(mix, seg, 1, np.ones((1, 1), np.float32), forward, batch=1, should_cancel=cancel)
+    assert e.value.status == stx.STATUS_CANCELLED and len(calls) == 3
+    with pytest.raises(stx.StxError) as e:
+        stx.htdemucs_separate(mix, seg, 1, np.ones((1, 1), np.float32), forward, overlap=1.0)
+    assert e.value.status == stx.STATUS_INVALID_ARGUMENT and "overlap must be < 1" in e.value.message

@@ -153,3 +153,23 @@ def test_identity_model_returns_view(htd):
     out = htd.split_ola(y, length, stride)
     assert np.max(np.abs(out[:2] - buf)) <= 4e-7 * np.max(np.abs(buf))
     assert np.array_equal(out[:2], out[2:])
+
+
+def test_shift_offsets_range_and_determinism(htd):
+    a = htd.shift_offsets(7, 22050, 2, 5)
+    b = htd.shift_offsets(7, 22050, 2, 5)
+    assert np.array_equal(a, b) and a.min() >= 0 and a.max() <= 22050
+    # One generator across models: model 1 continues the sequence of model 0.
+    c = htd.shift_offsets(7, 22050, 1, 10)
+    assert np.array_equal(a.reshape(-1), c.reshape(-1))
+
+
+def test_separate_identity_bag(htd):
+    """Two models that both return the input for every source, any weights: separate() gives the
+    mix back (normalise, split, shifts, bag and denormalise undo each other to float rounding)."""
+    mix = synth.normal(16, (2, 3000), 0.3) + 0.01
+    bag = np.array([[1.0, 0.5], [0.25, 2.0]], np.float32)
+    ident = lambda m, parts: np.concatenate([parts, parts], axis=1)
+    out = htd.separate(mix, 512, bag, ident, sample_rate=400, shifts=2, seed=3)
+    for s in range(2):
+        assert np.max(np.abs(out[s] - mix)) <= 2e-6 * np.max(np.abs(mix))
