@@ -525,6 +525,35 @@ def run_rows(torch, stx, dev):
     out["c1_htdemucs_ispec_ws"] = time_call(torch, stream, mk_ispec1(True), c1_bytes)
     del fft1
 
+    # c1 pre/post-processing around the HTDemucs graph (4 sources): CaC pack + normalise of the
+    # spectrum, the waveform's normalise, the spectral denormalise and the time branch + add.
+    spec_bytes = C * F1 * T1 * 8
+
+    def mk_cac():
+        z, m = torch.randn((C, F1, T1), dtype=torch.complex64, device=dev), torch.empty((2 * C, F1, T1), device=dev)
+        st = torch.empty(2, dtype=torch.float64, device=dev)
+        return lambda: stx.htdemucs_cac_normalize(z, out=m, stats=st, stream=stream)
+    out["c1_cac_normalize"] = time_call(torch, stream, mk_cac, 2 * spec_bytes)
+
+    def mk_wave():
+        x, y = rn(C, L1), torch.empty((C, L1), device=dev)
+        st = torch.empty(2, dtype=torch.float64, device=dev)
+        return lambda: stx.htdemucs_wave_normalize(x, out=y, stats=st, stream=stream)
+    out["c1_wave_normalize"] = time_call(torch, stream, mk_wave, 2 * C * L1 * 4)
+
+    def mk_denorm():
+        ox, z = rn(4, 2 * C, F1, T1), torch.empty((4, C, F1, T1), dtype=torch.complex64, device=dev)
+        st = torch.tensor([0.01, 0.5], dtype=torch.float64, device=dev)
+        return lambda: stx.htdemucs_cac_denormalize(ox, st, out=z, stream=stream)
+    out["c1_cac_denormalize"] = time_call(torch, stream, mk_denorm, 2 * 4 * spec_bytes)
+
+    def mk_tadd():
+        xt, y, o = rn(4 * C, L1), rn(4 * C, L1), torch.empty((4 * C, L1), device=dev)
+        st = torch.tensor([0.01, 0.5], dtype=torch.float64, device=dev)
+        return lambda: stx.htdemucs_time_add(xt, y, st, out=o, stream=stream)
+    out["c1_time_add"] = time_call(torch, stream, mk_tadd, 3 * 4 * C * L1 * 4)
+
+
     # c4: RoFormer transformer ops (dim 384, 8 heads x 64, 60 bands x 801 frames).
     def mk_rms():
         x, g, y = rn(48060, 384), rn(384), torch.empty((48060, 384), device=dev)
@@ -594,6 +623,29 @@ def run_rows(torch, stx, dev):
         return lambda: plan.overlap_add(y, out=o, stream=stream)
     out["c5_demix_overlap_add"] = time_call(torch, stream, mk_ola, lens * S * C * 4 + S * C * Lsong * 4)
     del plan
+
+    # The same song through HTDemucs' apply_model split: mono-mix normalise, the 31 padded
+    # segments of 343,980 samples (stride 257,985) and the triangular-weight overlap-add.
+    seg = 343980
+    stride, n_seg = stx.htdemucs_split_plan(Lsong, seg, 0.25)
+
+    def mk_mixnorm():
+        m, o = mix.clone(), torch.empty((C, Lsong), device=dev)
+        st = torch.empty(2, dtype=torch.float64, device=dev)
+        return lambda: stx.htdemucs_mix_normalize(m, out=o, stats=st, stream=stream)
+    out["c5_htdemucs_mix_normalize"] = time_call(torch, stream, mk_mixnorm, 2 * C * Lsong * 4)
+
+    def mk_segments():
+        m, p = mix.clone(), torch.empty((n_seg, C, seg), device=dev)
+        return lambda: stx.htdemucs_segments(m, 0, Lsong, seg, stride, out=p, stream=stream)
+    out["c5_htdemucs_segments"] = time_call(torch, stream, mk_segments, C * Lsong * 4 + n_seg * C * seg * 4)
+
+    def mk_split_ola():
+        y, o = rn(n_seg, S * C, seg), torch.empty((S * C, Lsong), device=dev)
+        return lambda: stx.htdemucs_split_overlap_add(y, Lsong, stride, out=o, stream=stream)
+    last = Lsong - (n_seg - 1) * stride
+    valid = (n_seg - 1) * seg + last
+    out["c5_htdemucs_split_ola"] = time_call(torch, stream, mk_split_ola, (valid + Lsong) * S * C * 4)
     torch.cuda.empty_cache()
     # The practical ceiling at each row's size: a plain device copy (torch's copy_) moving the
     # same bytes (half read, half written), timed the same cold way.

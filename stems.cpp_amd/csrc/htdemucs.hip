@@ -43,6 +43,30 @@ __device__ __forceinline__ float mono_at(const float* x, long long n, int C, lon
     return (float)(m / C);
 }
 
+// mono_at for NC channels known at compile time (NC = 0: C at run time), written so that the
+// channel loads of all J samples are issued before the first sum.
+template <int NC, int J>
+__device__ __forceinline__ void mono_batch(const float* x, long long n, int C, const long long (&idx)[J],
+                                           float (&out)[J]) {
+    if constexpr (NC > 0) {
+        float v[J][NC];
+#pragma unroll
+        for (int j = 0; j < J; j++)
+#pragma unroll
+            for (int c = 0; c < NC; c++) v[j][c] = x[c * n + idx[j]];
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+            double m = 0.0;
+#pragma unroll
+            for (int c = 0; c < NC; c++) m += v[j][c];
+            out[j] = (float)(m / NC);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < J; j++) out[j] = mono_at(x, n, C, idx[j]);
+    }
+}
+
 __device__ __forceinline__ double block_sum(double v, double* red) {
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
@@ -53,16 +77,22 @@ __device__ __forceinline__ double block_sum(double v, double* red) {
     return red[0] + red[1] + red[2] + red[3];    // 256 threads: 4 waves, summed in one order
 }
 
-template <int KIND>
+// KIND: MOM_FLAT or MOM_MONO; NC: channels of the mono mix (compile time; 0 = run time).
+template <int KIND, int NC>
 __global__ __launch_bounds__(256) void moments_kernel(MomArgs a) {
     __shared__ double red[4];
     const long long lo = (long long)blockIdx.x * kMomChunk;
     const float shift = KIND == MOM_MONO ? mono_at(a.x, a.n, a.C, 0) : a.x[0];
-    float v[kMomChunk / 256];
+    constexpr int J = kMomChunk / 256;
+    float v[J];
+    long long idx[J];
 #pragma unroll
-    for (int j = 0; j < kMomChunk / 256; j++) {  // clamped loads, all issued first
-        const long long i = min(lo + threadIdx.x + 256LL * j, a.n - 1);
-        v[j] = KIND == MOM_MONO ? mono_at(a.x, a.n, a.C, i) : a.x[i];
+    for (int j = 0; j < J; j++) idx[j] = min(lo + threadIdx.x + 256LL * j, a.n - 1);   // clamped
+    if (KIND == MOM_MONO) {
+        mono_batch<NC, J>(a.x, a.n, a.C, idx, v);
+    } else {
+#pragma unroll
+        for (int j = 0; j < J; j++) v[j] = a.x[idx[j]];
     }
     double s = 0.0, q = 0.0;
 #pragma unroll
@@ -83,86 +113,88 @@ __global__ __launch_bounds__(256) void moments_kernel(MomArgs a) {
 
 enum NormKind { NORM_CAC = 0, NORM_FLAT = 1, NORM_MIX = 2 };
 
-struct NormArgs {
-    const float* x;              // CAC: complex [C][FT]; FLAT: [n]; MIX: [C][n]
-    float* y;                    // CAC: [2C][FT]; FLAT: [n]; MIX: [C][n]
-    long long n;                 // the moments' count (CAC: 2 C FT floats; FLAT: n; MIX: samples)
-    long long count;             // outputs this kernel walks (CAC: C FT complex; FLAT: n; MIX: C n)
-    long long ft;                // CAC: F * T
-    int C;
-    const double* partial;
-    int n_partial;
-    double* stats;               // {mean, sd} as used
-};
-
-// mean and unbiased std from the pass-1 pairs (identical in every block).
-__device__ __forceinline__ void block_moments(const NormArgs& a, double shift, double* red, double& mean, double& sd) {
+// One block adds the pass-1 pairs in a fixed order and writes {mean, sd}: the unbiased std,
+// floored at 1e-8 for the mix (std::max(std, 1e-8) keeps a NaN, as here).
+template <int KIND>
+__global__ __launch_bounds__(256) void moments_final_kernel(MomArgs a, int n_partial, double* stats) {
+    __shared__ double red[4];
     double s = 0.0, q = 0.0;
-    for (int b = (int)threadIdx.x; b < a.n_partial; b += 256) {
+    for (int b = (int)threadIdx.x; b < n_partial; b += 256) {
         s += a.partial[2 * b];
         q += a.partial[2 * b + 1];
     }
     s = block_sum(s, red);
     q = block_sum(q, red);
-    const double n = (double)a.n;
-    mean = shift + s / n;
-    sd = sqrt(fmax(q - s * (s / n), 0.0) / (n - 1.0));
+    if (threadIdx.x == 0) {
+        const double shift = KIND == NORM_MIX ? (double)mono_at(a.x, a.n, a.C, 0) : (double)a.x[0];
+        const double n = (double)a.n;
+        double sd = sqrt(fmax(q - s * (s / n), 0.0) / (n - 1.0));
+        if (KIND == NORM_MIX) sd = sd < 1e-8 ? 1e-8 : sd;
+        stats[0] = shift + s / n;
+        stats[1] = sd;
+    }
 }
 
+constexpr int kNormPer = 8;
+
+// (v - mean) / den with den = 1e-5 + sd (spectrum, waveform) or the floored sd (mix), in
+// double and rounded once. CAC: blockIdx.y is the channel, its re and im go to planes 2c and
+// 2c + 1. FLAT / MIX: a flat walk.
 template <int KIND>
-__global__ __launch_bounds__(256) void normalize_kernel(NormArgs a) {
-#pragma clang fp contract(off)
-    __shared__ double red[4];
-    constexpr int PER = 4;
-    const long long e0 = (long long)blockIdx.x * (256 * PER) + threadIdx.x;
-    // Loads first: they are in flight while the statistics add up.
-    float2 vc[PER];
-    float vf[PER];
+__global__ __launch_bounds__(256) void normalize_kernel(const float* x, float* y, long long count, const double* stats) {
+    const double mean = stats[0];
+    const double den = KIND == NORM_MIX ? stats[1] : 1e-5 + stats[1];
+    const long long e0 = (long long)blockIdx.x * (256 * kNormPer) + threadIdx.x;
+    if (KIND == NORM_CAC) {
+        const long long c = blockIdx.y;
+        const float2* src = reinterpret_cast<const float2*>(x) + c * count;
+        float* re = y + 2 * c * count;
+        float* im = re + count;
+        float2 v[kNormPer];
 #pragma unroll
-    for (int k = 0; k < PER; k++) {
-        const long long e = min(e0 + 256LL * k, a.count - 1);
-        if (KIND == NORM_CAC) vc[k] = reinterpret_cast<const float2*>(a.x)[e];
-        else vf[k] = a.x[e];
-    }
-    const double shift = KIND == NORM_MIX ? (double)mono_at(a.x, a.n, a.C, 0) : (double)a.x[0];
-    double mean, sd;
-    block_moments(a, shift, red, mean, sd);
-    double den;
-    if (KIND == NORM_MIX) {
-        sd = sd < 1e-8 ? 1e-8 : sd;              // std::max(std, 1e-8), NaN kept
-        den = sd;
+        for (int k = 0; k < kNormPer; k++) v[k] = src[min(e0 + 256LL * k, count - 1)];
+#pragma unroll
+        for (int k = 0; k < kNormPer; k++) {
+            const long long e = e0 + 256LL * k;
+            if (e < count) {
+                re[e] = (float)(((double)v[k].x - mean) / den);
+                im[e] = (float)(((double)v[k].y - mean) / den);
+            }
+        }
     } else {
-        den = 1e-5 + sd;
-    }
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        a.stats[0] = mean;
-        a.stats[1] = sd;
-    }
+        float v[kNormPer];
 #pragma unroll
-    for (int k = 0; k < PER; k++) {
-        const long long e = e0 + 256LL * k;
-        if (e >= a.count) break;
-        if (KIND == NORM_CAC) {
-            const long long c = e / a.ft, i = e - c * a.ft;
-            a.y[(2 * c) * a.ft + i] = (float)(((double)vc[k].x - mean) / den);
-            a.y[(2 * c + 1) * a.ft + i] = (float)(((double)vc[k].y - mean) / den);
-        } else {
-            a.y[e] = (float)(((double)vf[k] - mean) / den);
+        for (int k = 0; k < kNormPer; k++) v[k] = x[min(e0 + 256LL * k, count - 1)];
+#pragma unroll
+        for (int k = 0; k < kNormPer; k++) {
+            const long long e = e0 + 256LL * k;
+            if (e < count) y[e] = (float)(((double)v[k] - mean) / den);
         }
     }
 }
 
-// Spectral branch denormalise: ox [S][2C][FT] -> complex64 spec [S][C][FT].
-__global__ __launch_bounds__(256) void cac_denorm_kernel(const float* ox, float2* spec, long long ft, int C,
-                                                         long long count, const double* stats) {
+// Spectral branch denormalise: ox [S][2C][FT] -> complex64 spec [S][C][FT]; blockIdx.y = s * C + c.
+__global__ __launch_bounds__(256) void cac_denorm_kernel(const float* ox, float2* spec, long long ft,
+                                                         const double* stats) {
 #pragma clang fp contract(off)
-    const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
-    if (e >= count) return;
     const double mean = stats[0], sd = stats[1];
-    const long long sc = e / ft, i = e - sc * ft;          // sc = s * C + c
-    const long long s = sc / C, c = sc - s * C;
-    const float re = ox[(s * 2 * C + 2 * c) * ft + i], im = ox[(s * 2 * C + 2 * c + 1) * ft + i];
-    spec[e] = make_float2((float)((double)re * sd + mean), (float)((double)im * sd + mean));
+    const long long sc = blockIdx.y;
+    const float* re = ox + 2 * sc * ft;                    // planes 2c and 2c + 1 of source s
+    const float* im = re + ft;
+    float2* out = spec + sc * ft;
+    const long long e0 = (long long)blockIdx.x * (256 * kNormPer) + threadIdx.x;
+    float vr[kNormPer], vi[kNormPer];
+#pragma unroll
+    for (int k = 0; k < kNormPer; k++) {
+        const long long e = min(e0 + 256LL * k, ft - 1);
+        vr[k] = re[e];
+        vi[k] = im[e];
+    }
+#pragma unroll
+    for (int k = 0; k < kNormPer; k++) {
+        const long long e = e0 + 256LL * k;
+        if (e < ft) out[e] = make_float2((float)((double)vr[k] * sd + mean), (float)((double)vi[k] * sd + mean));
+    }
 }
 
 // Time branch: out = (float)(t * sd + mean) + y, the add in float.
@@ -184,17 +216,33 @@ struct SegArgs {
     int length, seg, stride, first, C;
 };
 
-// parts[k][c][i] = buf[c][start_k + i] where buf has it, else 0 (TensorChunk.padded).
+// parts[k][c][i] = buf[c][start_k + i] where buf has it, else 0 (TensorChunk.padded). Each
+// thread writes 4 consecutive samples (one float4 when segment rows are 16-byte aligned).
+template <bool V4>
 __global__ __launch_bounds__(256) void segments_kernel(SegArgs a) {
     const int k = (int)blockIdx.z, c = (int)blockIdx.y;
-    const int i = (int)blockIdx.x * 256 + (int)threadIdx.x;
-    if (i >= a.seg) return;
+    const int i0 = ((int)blockIdx.x * 256 + (int)threadIdx.x) * 4;
+    if (i0 >= a.seg) return;
     const int off = (a.first + k) * a.stride;
     const int clen = min(a.seg, a.length - off);
-    const long long j = a.offset + off - (a.seg - clen) / 2 + i;
-    const bool in = j >= 0 && j < a.total;
-    const float v = a.buf[(long long)c * a.total + (in ? j : 0)];
-    a.parts[((long long)k * a.C + c) * a.seg + i] = in ? v : 0.0f;
+    const long long j0 = a.offset + off - (a.seg - clen) / 2 + i0;
+    const float* row = a.buf + (long long)c * a.total;
+    float v[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const long long j = j0 + q;
+        const bool in = j >= 0 && j < a.total;
+        const float t = row[in ? j : 0];
+        v[q] = in ? t : 0.0f;
+    }
+    float* dst = a.parts + ((long long)k * a.C + c) * a.seg + i0;
+    if (V4) {
+        *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            if (i0 + q < a.seg) dst[q] = v[q];
+    }
 }
 
 struct OlaArgs {
@@ -202,54 +250,90 @@ struct OlaArgs {
     float* out;                  // [tracks][length]
     int tracks, length, seg, stride, n_chunks;
     float mx;                    // the weights' maximum
+    FastDiv sdiv;                // division by stride
 };
 
-constexpr int kOlaPer = 4;
+constexpr int kOlaPer = 2;
+constexpr int kOlaMaxCover = 8;                  // chunks covering one sample: ceil(seg / stride)
 
-// Gather form of split()'s overlap-add for kOlaPer samples of one track per thread.
+constexpr int kOlaTracks = 4;                    // tracks per thread (they share the weights)
+
+// Gather form of split()'s overlap-add. A thread takes kOlaPer samples i and kOlaTracks tracks;
+// the weights of the <= NK chunks covering i and their float sum are formed once and shared by
+// the tracks (the divisions dominate the cost otherwise). The chunk values are loaded from
+// clamped, always-valid addresses, all before the first use, and summed in chunk order over the
+// chunks that cover i, exactly as the reference's `out += weight * seg_out`, then divided by the
+// summed weights.
+template <int NK>
 __global__ __launch_bounds__(256) void split_ola_kernel(OlaArgs a) {
 #pragma clang fp contract(off)
-    const int sc = (int)blockIdx.y;
+    const int sc0 = (int)blockIdx.y * kOlaTracks;
     const int half = a.seg / 2;
 #pragma unroll
     for (int p = 0; p < kOlaPer; p++) {
         const int i = ((int)blockIdx.x * kOlaPer + p) * 256 + (int)threadIdx.x;
         if (i >= a.length) return;
-        const int k_hi = min(i / a.stride, a.n_chunks - 1);
-        const int k_lo = i >= a.seg ? (i - a.seg) / a.stride + 1 : 0;   // first chunk with i - off < seg
-        float acc = 0.0f, sw = 0.0f;
-        for (int k = k_lo; k <= k_hi; k++) {
+        const int k_hi = (int)min(a.sdiv.div((unsigned)i), (unsigned)(a.n_chunks - 1));
+        long long base[NK];                          // offset of (chunk, track 0, sample) in y
+        bool in[NK];
+        float w[NK];
+#pragma unroll
+        for (int q = 0; q < NK; q++) {               // chunk k_hi - q
+            const int k = max(k_hi - q, 0);
             const int off = k * a.stride, r = i - off;
             const int clen = min(a.seg, a.length - off);
             const int trim = (a.seg - clen) / 2;
-            const float w = (float)(r < half ? r + 1 : a.seg - r) / a.mx;
-            const float prod = w * a.y[((long long)k * a.tracks + sc) * a.seg + trim + r];
-            acc = acc + prod;
-            sw = sw + w;
+            in[q] = k_hi - q >= 0 && r < a.seg;
+            base[q] = (long long)k * a.tracks * a.seg + trim + min(min(r, a.seg - 1), clen - 1);
+            w[q] = (float)(r < half ? r + 1 : a.seg - r) / a.mx;
         }
-        a.out[(long long)sc * a.length + i] = acc / sw;
+        float v[kOlaTracks][NK];
+#pragma unroll
+        for (int t = 0; t < kOlaTracks; t++) {
+            const long long sc = min(sc0 + t, a.tracks - 1);
+#pragma unroll
+            for (int q = 0; q < NK; q++) v[t][q] = a.y[base[q] + sc * a.seg];
+        }
+        float sw = 0.0f;
+#pragma unroll
+        for (int q = NK - 1; q >= 0; q--)            // chunk order: ascending k
+            if (in[q]) sw = sw + w[q];
+#pragma unroll
+        for (int t = 0; t < kOlaTracks; t++) {
+            if (sc0 + t >= a.tracks) break;
+            float acc = 0.0f;
+#pragma unroll
+            for (int q = NK - 1; q >= 0; q--) {
+                if (in[q]) {
+                    const float prod = w[q] * v[t][q];
+                    acc = acc + prod;
+                }
+            }
+            a.out[(long long)(sc0 + t) * a.length + i] = acc / sw;
+        }
     }
 }
 
 // ---------------------------------------------------------------- separate() accumulation
 // res[t][i] = (first ? 0 : res[t][i]) + o[t][src_off + i]: one shift's output, added in shift order
-// (src/htdemucs.cpp:622-624). The first shift also adds to 0.0f, as the reference's zeroed res does.
+// (src/htdemucs.cpp:622-624); blockIdx.y = t. The first shift also adds to 0.0f, as the
+// reference's zeroed res does.
 __global__ __launch_bounds__(256) void shift_add_kernel(float* res, const float* o, long long len, long long o_len,
-                                                        long long src_off, long long count, int first) {
-    const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
-    if (e >= count) return;
-    const long long t = e / len, i = e - t * len;
-    const float prev = first ? 0.0f : res[e];
-    res[e] = prev + o[t * o_len + src_off + i];
+                                                        long long src_off, int first) {
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= len) return;
+    const long long t = blockIdx.y;
+    const float v = o[t * o_len + src_off + i];
+    const float prev = first ? 0.0f : res[t * len + i];
+    res[t * len + i] = prev + v;
 }
 
 // estimates[s] += w_s * (res[s] / shifts) for every source with w_s != 0 (:625-631, the
-// division by shifts of :626 when shifts > 0); the first model adds to 0.0f.
+// division by shifts of :626 when shifts > 0); the first model adds to 0.0f. blockIdx.y = s.
 struct BagArgs {
     float* est;
     const float* res;
     long long plane;             // C * len
-    long long count;             // S * plane
     float w[64];
     float shifts;                // 0: no division
     int first;
@@ -257,34 +341,36 @@ struct BagArgs {
 
 __global__ __launch_bounds__(256) void bag_add_kernel(BagArgs a) {
 #pragma clang fp contract(off)
-    const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
-    if (e >= a.count) return;
-    const int s = (int)(e / a.plane);
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= a.plane) return;
+    const int s = (int)blockIdx.y;
+    const long long e = (long long)s * a.plane + i;
     const float w = a.w[s];
-    const float prev = a.first ? 0.0f : a.est[e];
     if (w == 0.0f) {
-        if (a.first) a.est[e] = prev;
+        if (a.first) a.est[e] = 0.0f;
         return;
     }
+    const float prev = a.first ? 0.0f : a.est[e];
     float v = a.res[e];
     if (a.shifts != 0.0f) v = v / a.shifts;
     const float p = w * v;
     a.est[e] = prev + p;
 }
 
-// out = (float)(est / totals[s] * ref_std + ref_mean) (:633-638).
+// out = (float)(est / totals[s] * ref_std + ref_mean) (:633-638); blockIdx.y = s.
 struct FinalArgs {
     float* est;
-    long long plane, count;
+    long long plane;
     float totals[64];
     const double* stats;
 };
 
 __global__ __launch_bounds__(256) void bag_final_kernel(FinalArgs a) {
 #pragma clang fp contract(off)
-    const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
-    if (e >= a.count) return;
-    const int s = (int)(e / a.plane);
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= a.plane) return;
+    const int s = (int)blockIdx.y;
+    const long long e = (long long)s * a.plane + i;
     const float q = a.est[e] / a.totals[s];
     a.est[e] = (float)((double)q * a.stats[1] + a.stats[0]);
 }
@@ -336,18 +422,26 @@ void check_ws(void* ws, size_t bytes, long long n) {
 }
 
 template <int MK, int NK>
-void normalize(const float* x, long long n_mom, long long count, long long ft, int C, float* y, double* stats,
-               void* ws, hipStream_t s) {
+void normalize(const float* x, long long n_mom, long long count, int C, float* y, double* stats, void* ws,
+               hipStream_t s) {
     double* partial = static_cast<double*>(ws);
     const long long nb = mom_blocks(n_mom);
     STX_REQUIRE(nb < (1LL << 31) && count < (1LL << 40), "normalise: too many elements");
     MomArgs m{x, n_mom, C, partial};
-    hipLaunchKernelGGL((moments_kernel<MK>), dim3((unsigned)nb), dim3(256), 0, s, m);
+    if constexpr (MK == MOM_MONO) {
+        if (C == 1) hipLaunchKernelGGL((moments_kernel<MK, 1>), dim3((unsigned)nb), dim3(256), 0, s, m);
+        else if (C == 2) hipLaunchKernelGGL((moments_kernel<MK, 2>), dim3((unsigned)nb), dim3(256), 0, s, m);
+        else hipLaunchKernelGGL((moments_kernel<MK, 0>), dim3((unsigned)nb), dim3(256), 0, s, m);
+    } else {
+        hipLaunchKernelGGL((moments_kernel<MK, 0>), dim3((unsigned)nb), dim3(256), 0, s, m);
+    }
     launch_check("moments_kernel");
-    NormArgs a{x, y, n_mom, count, ft, C, partial, (int)nb, stats};
-    const long long blocks = (count + 1023) / 1024;
+    hipLaunchKernelGGL((moments_final_kernel<NK>), dim3(1), dim3(256), 0, s, m, (int)nb, stats);
+    launch_check("moments_final_kernel");
+    const long long blocks = (count + 256 * kNormPer - 1) / (256 * kNormPer);
     STX_REQUIRE(blocks < (1LL << 31), "normalise: too many elements");
-    hipLaunchKernelGGL((normalize_kernel<NK>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((normalize_kernel<NK>), dim3((unsigned)blocks, NK == NORM_CAC ? (unsigned)C : 1u), dim3(256),
+                       0, s, x, y, count, stats);
     launch_check("normalize_kernel");
 }
 
@@ -368,9 +462,9 @@ STX_API stx_status stx_htdemucs_cac_normalize(const float* spec, int channels, i
         STX_REQUIRE(spec && mag && stats, "NULL buffer");
         const long long ft = (long long)n_bins * n_frames, n = 2LL * channels * ft;
         STX_REQUIRE(n > 1, "cac_normalize: need at least two values for the unbiased std");
+        STX_REQUIRE(channels < 65536, "cac_normalize: too many channels");
         check_ws(workspace, workspace_bytes, n);
-        normalize<MOM_FLAT, NORM_CAC>(spec, n, (long long)channels * ft, ft, channels, mag, stats, workspace,
-                                      as_stream(stream));
+        normalize<MOM_FLAT, NORM_CAC>(spec, n, ft, channels, mag, stats, workspace, as_stream(stream));
     });
 }
 
@@ -380,7 +474,7 @@ STX_API stx_status stx_htdemucs_wave_normalize(const float* x, int64_t n, float*
         STX_REQUIRE(n > 1, "wave_normalize: need at least two samples for the unbiased std");
         STX_REQUIRE(x && out && stats, "NULL buffer");
         check_ws(workspace, workspace_bytes, n);
-        normalize<MOM_FLAT, NORM_FLAT>(x, n, n, 0, 1, out, stats, workspace, as_stream(stream));
+        normalize<MOM_FLAT, NORM_FLAT>(x, n, n, 1, out, stats, workspace, as_stream(stream));
     });
 }
 
@@ -391,7 +485,7 @@ STX_API stx_status stx_htdemucs_mix_normalize(const float* mix, int channels, in
         STX_REQUIRE(channels > 0, "mix_normalize: channels must be positive");
         STX_REQUIRE(mix && out && stats, "NULL buffer");
         check_ws(workspace, workspace_bytes, len);
-        normalize<MOM_MONO, NORM_MIX>(mix, len, (long long)channels * len, 0, channels, out, stats, workspace,
+        normalize<MOM_MONO, NORM_MIX>(mix, len, (long long)channels * len, channels, out, stats, workspace,
                                       as_stream(stream));
     });
 }
@@ -403,10 +497,10 @@ STX_API stx_status stx_htdemucs_cac_denormalize(const float* ox, int n_sources, 
         const long long ft = (long long)n_bins * n_frames, count = (long long)n_sources * channels * ft;
         if (count == 0) return;
         STX_REQUIRE(ox && spec && stats, "NULL buffer");
-        const long long blocks = (count + 255) / 256;
-        STX_REQUIRE(blocks < (1LL << 31), "cac_denormalize: too many elements");
-        hipLaunchKernelGGL(cac_denorm_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), ox,
-                           reinterpret_cast<float2*>(spec), ft, channels, count, stats);
+        const long long blocks = (ft + 256 * kNormPer - 1) / (256 * kNormPer);
+        STX_REQUIRE(blocks < (1LL << 31) && (long long)n_sources * channels < 65536, "cac_denormalize: too large");
+        hipLaunchKernelGGL(cac_denorm_kernel, dim3((unsigned)blocks, (unsigned)(n_sources * channels)), dim3(256), 0,
+                           as_stream(stream), ox, reinterpret_cast<float2*>(spec), ft, stats);
         launch_check("cac_denorm_kernel");
     });
 }
@@ -449,8 +543,11 @@ STX_API stx_status stx_htdemucs_segments(const float* buf, int channels, int64_t
         STX_REQUIRE(total > 0, "segments: empty buffer");
         STX_REQUIRE(count < 65536 && channels < 65536, "segments: too many chunks or channels");
         SegArgs a{buf, parts, total, offset, length, segment, stride, first, channels};
-        const dim3 grid((unsigned)((segment + 255) / 256), (unsigned)channels, (unsigned)count);
-        hipLaunchKernelGGL(segments_kernel, grid, dim3(256), 0, as_stream(stream), a);
+        const dim3 grid((unsigned)((segment + 1023) / 1024), (unsigned)channels, (unsigned)count);
+        if (segment % 4 == 0 && (reinterpret_cast<uintptr_t>(parts) & 15) == 0)
+            hipLaunchKernelGGL(segments_kernel<true>, grid, dim3(256), 0, as_stream(stream), a);
+        else
+            hipLaunchKernelGGL(segments_kernel<false>, grid, dim3(256), 0, as_stream(stream), a);
         launch_check("segments_kernel");
     });
 }
@@ -472,8 +569,20 @@ STX_API stx_status stx_htdemucs_split_overlap_add(const float* y, int tracks, in
         a.n_chunks = (int)(((long long)length + stride - 1) / stride);
         const int half = segment / 2;
         a.mx = (float)std::max(half, segment - half);
-        const dim3 grid((unsigned)((length + 256 * kOlaPer - 1) / (256 * kOlaPer)), (unsigned)tracks);
-        hipLaunchKernelGGL(split_ola_kernel, grid, dim3(256), 0, as_stream(stream), a);
+        a.sdiv = FastDiv((unsigned)stride);
+        const int cover = (segment + stride - 1) / stride;
+        if (cover > kOlaMaxCover)
+            fail(STX_STATUS_UNSUPPORTED, "split_overlap_add: more than %d segments cover a sample", kOlaMaxCover);
+        const dim3 grid((unsigned)((length + 256 * kOlaPer - 1) / (256 * kOlaPer)),
+                        (unsigned)((tracks + kOlaTracks - 1) / kOlaTracks));
+        const hipStream_t s = as_stream(stream);
+        switch (cover) {
+        case 1: hipLaunchKernelGGL(split_ola_kernel<1>, grid, dim3(256), 0, s, a); break;
+        case 2: hipLaunchKernelGGL(split_ola_kernel<2>, grid, dim3(256), 0, s, a); break;
+        case 3: hipLaunchKernelGGL(split_ola_kernel<3>, grid, dim3(256), 0, s, a); break;
+        case 4: hipLaunchKernelGGL(split_ola_kernel<4>, grid, dim3(256), 0, s, a); break;
+        default: hipLaunchKernelGGL(split_ola_kernel<kOlaMaxCover>, grid, dim3(256), 0, s, a); break;
+        }
         launch_check("split_ola_kernel");
     });
 }
@@ -497,6 +606,7 @@ STX_API stx_status stx_htdemucs_separate(const float* mix, int channels, int64_t
         STX_REQUIRE(len < (1LL << 31) - sample_rate, "separate: input too long");
         STX_REQUIRE(channels >= 1 && n_sources >= 1 && n_sources <= 64 && n_models >= 1 && segment >= 2 && batch >= 1,
                     "separate: bad channels/sources/models/segment/batch");
+        STX_REQUIRE((long long)n_sources * channels < 65536, "separate: too many tracks");
         STX_REQUIRE(mix && out && forward && workspace && bag_weights, "NULL argument");
         const int shifts = std::max(0, opt.shifts);
         STX_REQUIRE(shifts == 0 || sample_rate >= 2, "separate: bad sample rate for shifts");
@@ -513,7 +623,7 @@ STX_API stx_status stx_htdemucs_separate(const float* mix, int channels, int64_t
         const hipStream_t s = as_stream(stream);
         const int S = n_sources, C = channels, tracks = S * C;
         // Normalise by the mono mix (:539-549).
-        normalize<MOM_MONO, NORM_MIX>(mix, len, (long long)C * len, 0, C, d_mix, d_stats, ws + L.mom, s);
+        normalize<MOM_MONO, NORM_MIX>(mix, len, (long long)C * len, C, d_mix, d_stats, ws + L.mom, s);
 
         const int passes_per_split = (int)((len + L.stride - 1) / L.stride);                    // :577
         const int total_passes = n_models * std::max(1, shifts) * passes_per_split;
@@ -554,9 +664,9 @@ STX_API stx_status stx_htdemucs_separate(const float* mix, int channels, int64_t
                         const int offset = dist(rng);
                         const int length = (int)len + max_shift - offset;
                         split(mi, (long long)offset - max_shift, length);
-                        hipLaunchKernelGGL(shift_add_kernel, dim3(grid256((long long)tracks * len)), dim3(256), 0, s,
+                        hipLaunchKernelGGL(shift_add_kernel, dim3(grid256(len), (unsigned)tracks), dim3(256), 0, s,
                                            d_res, d_o, (long long)len, (long long)length,
-                                           (long long)(max_shift - offset), (long long)tracks * len, k == 0 ? 1 : 0);
+                                           (long long)(max_shift - offset), k == 0 ? 1 : 0);
                         launch_check("shift_add_kernel");
                     }
                     res = d_res;
@@ -565,14 +675,13 @@ STX_API stx_status stx_htdemucs_separate(const float* mix, int channels, int64_t
                 b.est = out;
                 b.res = res;
                 b.plane = (long long)C * len;
-                b.count = (long long)S * b.plane;
                 for (int si = 0; si < S; si++) {
                     b.w[si] = bag_weights[(size_t)mi * S + si];
                     totals[si] += b.w[si];                                                       // :627
                 }
                 b.shifts = shifts > 0 ? (float)shifts : 0.0f;
                 b.first = mi == 0 ? 1 : 0;
-                hipLaunchKernelGGL(bag_add_kernel, dim3(grid256(b.count)), dim3(256), 0, s, b);
+                hipLaunchKernelGGL(bag_add_kernel, dim3(grid256(b.plane), (unsigned)S), dim3(256), 0, s, b);
                 launch_check("bag_add_kernel");
             }
         } catch (const Cancelled&) {
@@ -581,10 +690,9 @@ STX_API stx_status stx_htdemucs_separate(const float* mix, int channels, int64_t
         FinalArgs f{};
         f.est = out;
         f.plane = (long long)C * len;
-        f.count = (long long)S * f.plane;
         for (int si = 0; si < S; si++) f.totals[si] = totals[si];
         f.stats = d_stats;
-        hipLaunchKernelGGL(bag_final_kernel, dim3(grid256(f.count)), dim3(256), 0, s, f);
+        hipLaunchKernelGGL(bag_final_kernel, dim3(grid256(f.plane), (unsigned)S), dim3(256), 0, s, f);
         launch_check("bag_final_kernel");
     });
 }
