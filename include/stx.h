@@ -246,14 +246,31 @@ STX_API int stx_demix_step(int chunk, int num_overlap, float overlap);
 STX_API stx_status stx_demix_plan(int64_t len, int chunk, int step, stx_demix_geometry* geom,
                                   stx_chunk* chunks, int64_t capacity);
 
+/* The chunking rules of a plan. STX_DEMIX_MSST is TFCTDF::Impl::demix_msst
+ * (src/tfc_tdf.cpp:447-495), ZFTurbo's loop as the MDX/TFC-TDF models run it: short chunks are
+ * reflect-padded when longer than chunk / 2 (not chunk / 2 + 1), only the chunk after which the
+ * loop ends (start + step >= Lp) keeps full weight at its end, and the fades are
+ * linspace(0, 1, fade) and linspace(1, 0, fade) (:56-63,465-469). */
+typedef int32_t stx_demix_rules;
+enum {
+    STX_DEMIX_ROFORMER = 0,
+    STX_DEMIX_MSST     = 1
+};
+/* stx_demix_plan / stx_demix_window / stx_demix_create with explicit rules. */
+STX_API stx_status stx_demix_plan_rules(int64_t len, int chunk, int step, stx_demix_rules rules,
+                                        stx_demix_geometry* geom, stx_chunk* chunks, int64_t capacity);
+
 /* The fade window of src/roformer.cpp:303-313 (host only): window[chunk] floats, before the
  * first/last chunk edits. */
 STX_API stx_status stx_demix_window(int chunk, float* window);
+STX_API stx_status stx_demix_window_rules(int chunk, stx_demix_rules rules, float* window);
 
 typedef struct stx_demix stx_demix;
 
 /* Device plan for one input length: geometry and window on the device. */
 STX_API stx_status stx_demix_create(int64_t len, int channels, int chunk, int step, stx_demix** out);
+STX_API stx_status stx_demix_create_rules(int64_t len, int channels, int chunk, int step, stx_demix_rules rules,
+                                          stx_demix** out);
 STX_API void       stx_demix_destroy(stx_demix* demix);
 STX_API int64_t    stx_demix_n_chunks(const stx_demix* demix);
 
@@ -302,6 +319,59 @@ STX_API stx_status stx_demix_track(const float* mix, int channels, int64_t len, 
                                    stx_separate_fn separate, void* separate_user,
                                    const stx_separate_options* options, float* out, void* workspace,
                                    size_t workspace_bytes, stx_stream stream);
+
+/* ------------------------------------------------------------------------------------------
+ * TFC-TDF (MDX) chunking. Replaces TFCTDF::Impl::demix_uvr (src/tfc_tdf.cpp:407-441) and
+ * TFCTDF::separate (:569-595); the MSST loop (:447-495) is an stx_demix plan with
+ * STX_DEMIX_MSST rules.
+ * ---------------------------------------------------------------------------------------- */
+typedef struct stx_uvr_demix stx_uvr_demix;
+
+/* UVR's SeperateMDX.demix geometry (src/tfc_tdf.cpp:410-415): trim = n_fft / 2 zeros in front,
+ * gen = chunk - 2 trim, M = trim + len + gen + trim - len % gen samples, step = chunk - n_fft for
+ * overlap < 0, else (int64)((1 - overlap) * chunk); chunks start at 0, step, ... < M. Weights
+ * are np.hanning of each chunk's actual length min(chunk, M - start), or 1 when overlap == 0,
+ * held by the plan on the device. RUNTIME_ERROR "tfc_tdf: chunk shorter than the FFT" for
+ * gen <= 0, INVALID_ARGUMENT "overlap too large for this model" for step <= 0. */
+STX_API stx_status stx_uvr_demix_create(int64_t len, int channels, int chunk, int n_fft, float overlap,
+                                        stx_uvr_demix** out);
+STX_API void       stx_uvr_demix_destroy(stx_uvr_demix* demix);
+STX_API int64_t    stx_uvr_demix_n_chunks(const stx_uvr_demix* demix);
+/* M, step and trim of a plan (each pointer may be NULL). */
+STX_API stx_status stx_uvr_demix_geometry(const stx_uvr_demix* demix, int64_t* padded_len, int64_t* step, int* trim);
+/* Model inputs of chunks first .. first + count - 1 (:416-425): mix device [C][len] ->
+ * parts device [count][C][chunk], zero past each chunk's actual length. */
+STX_API stx_status stx_uvr_demix_chunks(const stx_uvr_demix* demix, const float* mix, int64_t first, int64_t count,
+                                        float* parts, stx_stream stream);
+/* The weighted overlap-add (:427-440): y device [n_chunks][n_stems][C][chunk] -> out device
+ * [n_stems][C][len], double products and sums in chunk order, one division, bit-identical to the
+ * reference for the same model outputs. */
+STX_API stx_status stx_uvr_demix_overlap_add(const stx_uvr_demix* demix, const float* y, int n_stems, float* out,
+                                             stx_stream stream);
+
+typedef int32_t stx_tfc_chunking;
+enum {
+    STX_TFC_MSST = 0,          /* the model's chunking "msst" (ZFTurbo's demix) */
+    STX_TFC_UVR  = 1           /* "uvr_mdx" (UVR's SeperateMDX.demix) */
+};
+
+/* Bytes of device workspace stx_tfc_tdf_separate needs (0 for a geometry it rejects). */
+STX_API size_t stx_tfc_tdf_separate_workspace_size(int channels, int64_t len, int chunk, int n_fft,
+                                                   stx_tfc_chunking chunking, int num_overlap, float overlap,
+                                                   int n_stems, int batch);
+
+/* TFCTDF::separate (src/tfc_tdf.cpp:569-595) around any separator (parts [count][C][chunk] ->
+ * y [count][n_stems][C][chunk], the model's run_chunk): RUNTIME_ERROR for empty or non-finite
+ * input or shifts != 0, INVALID_ARGUMENT for overlap >= 1, CANCELLED when should_cancel returns
+ * non-zero (polled before the loop and before each chunk); MSST or UVR chunking (MSST step:
+ * stx_demix_step(chunk, num_overlap, overlap)); the stems times `compensate` when it is not 1;
+ * with `complement`, one more plane mix - stem 0 - stem 1 - ... in float. out is device
+ * [n_stems + complement][C][len]. Returns after the stream has drained. */
+STX_API stx_status stx_tfc_tdf_separate(const float* mix, int channels, int64_t len, int chunk, int n_fft,
+                                        stx_tfc_chunking chunking, int num_overlap, int n_stems, float compensate,
+                                        int complement, int batch, stx_separate_fn separate, void* separate_user,
+                                        const stx_separate_options* options, float* out, void* workspace,
+                                        size_t workspace_bytes, stx_stream stream);
 
 /* ------------------------------------------------------------------------------------------
  * HTDemucs pre/post-processing around the model graph, and apply_model's split. Replace the

@@ -33,6 +33,10 @@
  *     difference). ggml-specific rounding (the float theta recurrence of ggml's RoPE, its float
  *     softmax and norm arithmetic) is parity unpinned: ggml's sources are not in the reference.
  *   orc_binary: numpy's float32 arithmetic on explicitly tiled operands, bit for bit.
+ *   orc_msst_* / orc_uvr_* / orc_tfc_post: the closed forms of their windows (linspace ends at
+ *     exactly 0 and 1; np.hanning against numpy's own), numpy restatements of both loops on
+ *     small inputs, the identity model (both must return the mix), and the UVR geometry of the
+ *     reference's defaults (trim n_fft / 2, step chunk - n_fft).
  *   orc_mean_std / orc_*normalize / orc_time_add / orc_split_*: torch.std's unbiased estimator
  *     and numpy float32 arithmetic on the same formulas, the weights' closed form (symmetric
  *     up to the centre sample, maximum 1), the identity model (a split of a model that returns
@@ -106,6 +110,18 @@ int orc_demix_chunks(const float* mix, int C, long len, int chunk, int step, flo
 
 /* Overlap-add of src/roformer.cpp:334-350: y [n_chunks][S][C][chunk] -> out [S][C][len]. */
 int orc_demix_ola(const float* y, int S, int C, long len, int chunk, int step, float* out);
+
+/* TFC-TDF chunking (tfc_oracle.c): MSST (src/tfc_tdf.cpp:447-495) and UVR (:407-441) chunk
+ * inputs [n_chunks][C][chunk] and overlap-adds of y [n_chunks][S][C][chunk] -> out [S][C][len],
+ * and separate()'s compensation + complement (:582-595). */
+void orc_msst_window(int chunk, float* window);
+long orc_msst_n_chunks(long len, int chunk, int step);
+int orc_msst_chunks(const float* mix, int C, long len, int chunk, int step, float* parts);
+int orc_msst_ola(const float* y, int S, int C, long len, int chunk, int step, float* out);
+long orc_uvr_geometry(long len, int chunk, int n_fft, float overlap, long* M, long* step);
+int orc_uvr_chunks(const float* mix, int C, long len, int chunk, int n_fft, float overlap, float* parts);
+int orc_uvr_ola(const float* y, int S, int C, long len, int chunk, int n_fft, float overlap, float* out);
+void orc_tfc_post(const float* mix, long plane, int S, float compensate, int complement, float* est);
 
 /* ggml ops (ops_oracle.c). Contiguous tensors, ggml extents ne[4] (ne[0] fastest); broadcast
  * operands repeat into ne. */

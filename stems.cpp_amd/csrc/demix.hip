@@ -1,6 +1,8 @@
 // demix.hip — chunked overlap-add demix on gfx950.
 //
-// Reference: RoFormer::Impl::demix (src/roformer.cpp:286-351). The reference walks the chunks
+// Reference: RoFormer::Impl::demix (src/roformer.cpp:286-351), and with the MSST rules
+// TFCTDF::Impl::demix_msst (src/tfc_tdf.cpp:447-495), which differs in the short-chunk reflect
+// threshold, the chunk that drops its fade-out and the fade window (demix_host.cpp). The reference walks the chunks
 // one by one and read-modify-writes a double accumulator of S*C*Lp values per chunk. Here the
 // whole song stays resident (288 GB of HBM holds every chunk's output many times over) and
 // the overlap-add is a single gather pass: each output sample sums, in chunk order and in
@@ -29,11 +31,15 @@ namespace {
 struct DemixArgs {
     int64_t len, padded_len;
     int chunk, step, border, fade, reflect_border, channels;
+    int tail_min;                // a short chunk is reflect-padded above this length
+    int reach;                   // a chunk drops its fade-out when start + reach >= padded_len
 };
 
 DemixArgs args_of(const stx_demix* d) {
+    const bool msst = d->g.rules == STX_DEMIX_MSST;
     return DemixArgs{d->g.len, d->g.padded_len, d->g.chunk, d->g.step, d->g.border, d->g.fade,
-                     d->g.reflect_border, d->channels};
+                     d->g.reflect_border, d->channels, d->g.chunk / 2 + (msst ? 0 : 1),
+                     msst ? d->g.step : d->g.chunk};
 }
 
 // Sample p of the border-padded signal of channel row xc (src/roformer.cpp:293-301).
@@ -58,7 +64,7 @@ __global__ __launch_bounds__(256) void demix_chunks_kernel(DemixArgs a, const fl
     const int64_t k = first + (int64_t)blockIdx.z;
     const int64_t i = k * a.step;
     const int64_t length = min((int64_t)a.chunk, a.padded_len - i);
-    const bool reflect_tail = length > a.chunk / 2 + 1;
+    const bool reflect_tail = length > a.tail_min;
     const float* xc = mix + (size_t)c * a.len;
     const int64_t lead = a.reflect_border ? a.border : 0;    // padded index p is signal index p - lead
     float v[kChunkGroups][4];
@@ -99,10 +105,10 @@ __global__ __launch_bounds__(256) void demix_chunks_kernel(DemixArgs a, const fl
     }
 }
 
-// Weight of chunk k at offset t (src/roformer.cpp:334-336).
+// Weight of chunk k at offset t (src/roformer.cpp:334-336; src/tfc_tdf.cpp:484-486).
 __device__ __forceinline__ float chunk_weight(const float* __restrict__ window, int64_t k, int t, const DemixArgs& a) {
     if (k == 0) return t < a.fade ? 1.0f : window[t];
-    if (k * a.step + a.chunk >= a.padded_len && t >= a.chunk - a.fade) return 1.0f;
+    if (k * a.step + a.reach >= a.padded_len && t >= a.chunk - a.fade) return 1.0f;
     return window[t];
 }
 
@@ -141,7 +147,7 @@ __global__ __launch_bounds__(256) void demix_ola_kernel(DemixArgs a, const float
         const int64_t k = k_lo + kk;
         const int64_t i = k * a.step;
         const int64_t length = min((int64_t)a.chunk, a.padded_len - i);
-        const bool last = i + a.chunk >= a.padded_len;
+        const bool last = i + a.reach >= a.padded_len;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int64_t tt = p0 + j - i;
@@ -313,14 +319,19 @@ using namespace stx;
 extern "C" {
 
 STX_API stx_status stx_demix_create(int64_t len, int channels, int chunk, int step, stx_demix** out) {
+    return stx_demix_create_rules(len, channels, chunk, step, STX_DEMIX_ROFORMER, out);
+}
+
+STX_API stx_status stx_demix_create_rules(int64_t len, int channels, int chunk, int step, stx_demix_rules rules,
+                                          stx_demix** out) {
     return guard([&] {
         STX_REQUIRE(out != nullptr, "out is NULL");
         *out = nullptr;
         STX_REQUIRE(channels >= 1, "bad channel count");
-        const DemixGeometry g = demix_geometry(len, chunk, step);
+        const DemixGeometry g = demix_geometry(len, chunk, step, rules);
         STX_REQUIRE(g.n_chunks < (1LL << 31), "too many chunks");
         std::vector<float> w(chunk);
-        demix_window(chunk, w.data());
+        demix_window(chunk, w.data(), rules);
         stx_demix* d = new stx_demix;
         d->g = g;
         d->channels = channels;

@@ -15,10 +15,11 @@ struct DemixGeometry {
     int border = 0;              // chunk - step
     int fade = 0;                // chunk / 10
     int reflect_border = 0;      // len > 2 * border && border > 0
+    int rules = 0;               // STX_DEMIX_ROFORMER or STX_DEMIX_MSST
 };
 
-DemixGeometry demix_geometry(int64_t len, int chunk, int step);   // throws stx::Error
+DemixGeometry demix_geometry(int64_t len, int chunk, int step, int rules = STX_DEMIX_ROFORMER);   // throws stx::Error
 stx_chunk demix_chunk(const DemixGeometry& g, int64_t k);
-void demix_window(int chunk, float* window);
+void demix_window(int chunk, float* window, int rules = STX_DEMIX_ROFORMER);
 
 }  // namespace stx

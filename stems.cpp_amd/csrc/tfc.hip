@@ -1,0 +1,395 @@
+// tfc.hip — the TFC-TDF (MDX) chunking on gfx950: UVR's SeperateMDX.demix loop and the
+// TFCTDF::separate driver (MSST or UVR chunking, compensation, complement stem).
+//
+// Reference: TFCTDF::Impl::demix_uvr (src/tfc_tdf.cpp:407-441) and TFCTDF::separate (:569-595).
+// The MSST loop (:447-495) is the demix plan of demix.hip with STX_DEMIX_MSST rules.
+//
+// UVR: `trim` = n_fft / 2 zeros in front of the mix, chunks of `chunk` samples every `step`
+// over M = trim + len + gen + trim - len % gen samples (gen = chunk - 2 trim), each zero-filled
+// past its actual length min(chunk, M - i), weighted by np.hanning(actual) (1 when
+// overlap == 0), accumulated in double and divided at the trim offset. As in demix.hip the
+// whole song stays resident and the overlap-add is a gather: each output sample sums, in chunk
+// order and with the reference's double products, the chunks covering it, then divides once.
+// The hanning tables are computed once per plan on the host with the C library's cos, as the
+// reference computes them, so the weights (and so the results) are bit-identical.
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
+#include "common.hpp"
+#include "demix_host.hpp"
+
+struct stx_uvr_demix {
+    int64_t len = 0, M = 0, step = 0, n_chunks = 0, first_partial = 0;
+    int channels = 0, chunk = 0, n_fft = 0, trim = 0;
+    double* d_w = nullptr;           // [chunk] weights of full chunks, then each partial chunk's
+    int64_t* d_woff = nullptr;       // [n_chunks]: offset of chunk k's weights in d_w
+};
+
+namespace stx {
+namespace {
+
+struct UvrArgs {
+    int64_t len, M, step;
+    int64_t n_chunks;
+    int chunk, trim, channels;
+    FastDiv sdiv;                // division by step (M < 2^32)
+};
+
+UvrArgs uvr_args(const stx_uvr_demix* d) {
+    return UvrArgs{d->len, d->M, d->step, d->n_chunks, d->chunk, d->trim, d->channels, FastDiv((unsigned)d->step)};
+}
+
+// parts[k - first][c][t] = x[c][i + t] for t < actual, else 0, where x is the mix behind `trim`
+// zeros and zeros past its end (src/tfc_tdf.cpp:416-425). Four samples per thread.
+__global__ __launch_bounds__(256) void uvr_chunks_kernel(UvrArgs a, const float* __restrict__ mix, int64_t first,
+                                                         int vec, float* __restrict__ parts) {
+    const int c = (int)blockIdx.y;
+    const int64_t k = first + (int64_t)blockIdx.z;
+    const int64_t i = k * a.step;
+    const int64_t actual = min((int64_t)a.chunk, a.M - i);
+    const int t0 = ((int)blockIdx.x * 256 + (int)threadIdx.x) * 4;
+    if (t0 >= a.chunk) return;
+    const float* xc = mix + (size_t)c * a.len;
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int64_t t = t0 + j;
+        const int64_t s = i + t - a.trim;                    // index into the mix
+        const bool in = t < actual && s >= 0 && s < a.len;
+        const float x = xc[in ? s : 0];
+        v[j] = in ? x : 0.0f;
+    }
+    float* dst = parts + ((size_t)blockIdx.z * a.channels + c) * a.chunk + t0;
+    if (vec && t0 + 3 < a.chunk) {
+        *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (t0 + j < a.chunk) dst[j] = v[j];
+    }
+}
+
+// out[q][t] = sum_k (double)y[k][q][p - i_k] * w_k[p - i_k] / sum_k w_k[p - i_k], p = trim + t,
+// over the chunks covering p in chunk order (src/tfc_tdf.cpp:427-440). NK bounds the chunks
+// covering one sample. A thread takes one sample and kUvrPlanes planes, which share the weights
+// and their sum; loads are clamped to valid addresses and issued together.
+constexpr int kUvrMaxCover = 8;
+constexpr int kUvrPlanes = 4;
+
+template <int NK>
+__global__ __launch_bounds__(256) void uvr_ola_kernel(UvrArgs a, const float* __restrict__ y,
+                                                      const double* __restrict__ w, const int64_t* __restrict__ woff,
+                                                      int planes, float* __restrict__ out) {
+#pragma clang fp contract(off)
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= a.len) return;
+    const int q0 = (int)blockIdx.y * kUvrPlanes;
+    const int64_t p = a.trim + t;
+    const int64_t k_hi = min((int64_t)a.sdiv.div((unsigned)p), a.n_chunks - 1);
+    double wv[NK];
+    int64_t base[NK];
+    bool in[NK];
+#pragma unroll
+    for (int j = 0; j < NK; j++) {                      // chunk k_hi - j
+        const int64_t k = max(k_hi - j, (int64_t)0);
+        const int64_t i = k * a.step;
+        const int64_t actual = min((int64_t)a.chunk, a.M - i);
+        const int64_t r = p - i;
+        in[j] = k_hi - j >= 0 && r < actual;
+        const int64_t rc = min(r, actual - 1);
+        wv[j] = w[woff[k] + rc];
+        base[j] = (int64_t)k * planes * a.chunk + rc;
+    }
+    float yv[kUvrPlanes][NK];
+#pragma unroll
+    for (int u = 0; u < kUvrPlanes; u++) {
+        const int64_t q = min(q0 + u, planes - 1);
+#pragma unroll
+        for (int j = 0; j < NK; j++) yv[u][j] = y[base[j] + q * a.chunk];
+    }
+    double div = 0.0;
+#pragma unroll
+    for (int j = NK - 1; j >= 0; j--)                   // ascending chunk order
+        if (in[j]) div = div + wv[j];
+#pragma unroll
+    for (int u = 0; u < kUvrPlanes; u++) {
+        if (q0 + u >= planes) break;
+        double res = 0.0;
+#pragma unroll
+        for (int j = NK - 1; j >= 0; j--) {
+            if (in[j]) {
+                const double prod = (double)yv[u][j] * wv[j];
+                res = res + prod;
+            }
+        }
+        out[(size_t)(q0 + u) * a.len + t] = (float)(res / div);
+    }
+}
+
+// est *= compensate (when != 1), and with `complement` rest = mix - est_0 - est_1 - ... in float
+// (src/tfc_tdf.cpp:582-593). One thread per sample of the [C][len] plane.
+__global__ __launch_bounds__(256) void tfc_post_kernel(const float* __restrict__ mix, int64_t plane, int n_stems,
+                                                       float compensate, int complement, float* __restrict__ est) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= plane) return;
+    float rest = complement ? mix[i] : 0.0f;
+    for (int k = 0; k < n_stems; k++) {
+        float v = est[(size_t)k * plane + i];
+        if (compensate != 1.0f) {
+            v = v * compensate;
+            est[(size_t)k * plane + i] = v;
+        }
+        rest = rest - v;
+    }
+    if (complement) est[(size_t)n_stems * plane + i] = rest;
+}
+
+// Sets *flag when any value of x [n] is not finite (src/tfc_tdf.cpp:573-574).
+__global__ __launch_bounds__(256) void nonfinite_kernel(const float* __restrict__ x, int64_t n, int* flag) {
+    bool bad = false;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        bad = bad || !isfinite(x[i]);
+    if (bad) flag[0] = 1;                                // plain stores of one value: the order does not matter
+}
+
+void check_uvr(const stx_uvr_demix* d) { STX_REQUIRE(d != nullptr && d->d_w != nullptr, "null UVR plan"); }
+
+unsigned grid_for(int64_t n) { return (unsigned)std::min<int64_t>((n + 255) / 256, 1 << 20); }
+
+}  // namespace
+}  // namespace stx
+
+using namespace stx;
+
+extern "C" {
+
+STX_API stx_status stx_uvr_demix_create(int64_t len, int channels, int chunk, int n_fft, float overlap,
+                                        stx_uvr_demix** out) {
+    return guard([&] {
+        STX_REQUIRE(out != nullptr, "out is NULL");
+        *out = nullptr;
+        STX_REQUIRE(len > 0, "empty input");
+        STX_REQUIRE(channels >= 1 && chunk >= 1 && n_fft >= 1, "bad channels/chunk/n_fft");
+        const int trim = n_fft / 2, gen = chunk - 2 * trim;
+        if (gen <= 0) fail(STX_STATUS_RUNTIME_ERROR, "tfc_tdf: chunk shorter than the FFT");      // :410
+        const int64_t M = (int64_t)trim + len + gen + trim - len % gen;
+        const int64_t step = overlap < 0 ? chunk - n_fft : (int64_t)((1.0 - (double)overlap) * chunk);
+        if (step <= 0) fail(STX_STATUS_INVALID_ARGUMENT, "overlap too large for this model");     // :414
+        const int64_t n = (M + step - 1) / step;
+        STX_REQUIRE(n < (1LL << 31) && M < (1LL << 32), "input too long");
+        // Weights: one table for full chunks, one per partial chunk (np.hanning of its length).
+        auto hanning = [&](int m, std::vector<double>& w) {
+            const size_t o = w.size();
+            w.resize(o + m, 1.0);
+            if (overlap == 0.0f) return;                                                            // :428
+            if (m > 1)
+                for (int i = 0; i < m; i++) w[o + i] = 0.5 - 0.5 * std::cos(2.0 * M_PI * i / (m - 1));
+        };
+        std::vector<double> w;
+        std::vector<int64_t> woff(n);
+        hanning(chunk, w);
+        int64_t first_partial = n;
+        for (int64_t k = 0; k < n; k++) {
+            const int64_t actual = std::min<int64_t>(chunk, M - k * step);
+            if (actual == chunk) {
+                woff[k] = 0;
+            } else {
+                if (first_partial == n) first_partial = k;
+                woff[k] = (int64_t)w.size();
+                hanning((int)actual, w);
+            }
+        }
+        stx_uvr_demix* d = new stx_uvr_demix;
+        d->len = len;
+        d->M = M;
+        d->step = step;
+        d->n_chunks = n;
+        d->first_partial = first_partial;
+        d->channels = channels;
+        d->chunk = chunk;
+        d->n_fft = n_fft;
+        d->trim = trim;
+        hipError_t e = hipMalloc(&d->d_w, sizeof(double) * w.size());
+        if (e == hipSuccess) e = hipMemcpy(d->d_w, w.data(), sizeof(double) * w.size(), hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMalloc(&d->d_woff, sizeof(int64_t) * n);
+        if (e == hipSuccess) e = hipMemcpy(d->d_woff, woff.data(), sizeof(int64_t) * n, hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            stx_uvr_demix_destroy(d);
+            hip_check(e, "stx_uvr_demix_create");
+        }
+        *out = d;
+    });
+}
+
+STX_API void stx_uvr_demix_destroy(stx_uvr_demix* d) {
+    if (!d) return;
+    (void)hipFree(d->d_w);
+    (void)hipFree(d->d_woff);
+    delete d;
+}
+
+STX_API int64_t stx_uvr_demix_n_chunks(const stx_uvr_demix* d) { return d ? d->n_chunks : 0; }
+
+STX_API stx_status stx_uvr_demix_geometry(const stx_uvr_demix* d, int64_t* padded_len, int64_t* step, int* trim) {
+    return guard([&] {
+        check_uvr(d);
+        if (padded_len) *padded_len = d->M;
+        if (step) *step = d->step;
+        if (trim) *trim = d->trim;
+    });
+}
+
+STX_API stx_status stx_uvr_demix_chunks(const stx_uvr_demix* d, const float* mix, int64_t first, int64_t count,
+                                        float* parts, stx_stream stream) {
+    return guard([&] {
+        check_uvr(d);
+        STX_REQUIRE(first >= 0 && count >= 0 && first + count <= d->n_chunks, "chunk range out of the plan");
+        if (count == 0) return;
+        STX_REQUIRE(mix && parts, "NULL buffer");
+        STX_REQUIRE(count < 65536 && d->channels < 65536, "too many chunks or channels in one call");
+        const int vec = d->chunk % 4 == 0 && (reinterpret_cast<uintptr_t>(parts) & 15) == 0;
+        const dim3 grid((unsigned)((d->chunk + 1023) / 1024), (unsigned)d->channels, (unsigned)count);
+        hipLaunchKernelGGL(uvr_chunks_kernel, grid, dim3(256), 0, as_stream(stream), uvr_args(d), mix, first, vec, parts);
+        launch_check("uvr_chunks_kernel");
+    });
+}
+
+STX_API stx_status stx_uvr_demix_overlap_add(const stx_uvr_demix* d, const float* y, int n_stems, float* out,
+                                             stx_stream stream) {
+    return guard([&] {
+        check_uvr(d);
+        STX_REQUIRE(n_stems >= 1, "bad stem count");
+        STX_REQUIRE(y && out, "NULL buffer");
+        STX_REQUIRE((int64_t)n_stems * d->channels < 65536, "too many stems * channels");
+        const int planes = n_stems * d->channels;
+        const int64_t cover = (d->chunk + d->step - 1) / d->step;
+        if (cover > kUvrMaxCover)
+            fail(STX_STATUS_UNSUPPORTED, "UVR overlap-add: more than %d chunks cover a sample", kUvrMaxCover);
+        const dim3 grid((unsigned)((d->len + 255) / 256), (unsigned)((planes + kUvrPlanes - 1) / kUvrPlanes));
+        const hipStream_t s = as_stream(stream);
+        const UvrArgs a = uvr_args(d);
+        switch (cover) {
+        case 1: hipLaunchKernelGGL(uvr_ola_kernel<1>, grid, dim3(256), 0, s, a, y, d->d_w, d->d_woff, planes, out); break;
+        case 2: hipLaunchKernelGGL(uvr_ola_kernel<2>, grid, dim3(256), 0, s, a, y, d->d_w, d->d_woff, planes, out); break;
+        case 3: hipLaunchKernelGGL(uvr_ola_kernel<3>, grid, dim3(256), 0, s, a, y, d->d_w, d->d_woff, planes, out); break;
+        case 4: hipLaunchKernelGGL(uvr_ola_kernel<4>, grid, dim3(256), 0, s, a, y, d->d_w, d->d_woff, planes, out); break;
+        default:
+            hipLaunchKernelGGL(uvr_ola_kernel<kUvrMaxCover>, grid, dim3(256), 0, s, a, y, d->d_w, d->d_woff, planes, out);
+            break;
+        }
+        launch_check("uvr_ola_kernel");
+    });
+}
+
+STX_API size_t stx_tfc_tdf_separate_workspace_size(int channels, int64_t len, int chunk, int n_fft,
+                                                   stx_tfc_chunking chunking, int num_overlap, float overlap,
+                                                   int n_stems, int batch) {
+    try {
+        if (channels < 1 || len < 1 || chunk < 1 || n_stems < 1 || batch < 1) return 0;
+        int64_t n = 0;
+        if (chunking == STX_TFC_UVR) {
+            const int trim = n_fft / 2, gen = chunk - 2 * trim;
+            if (gen <= 0) return 0;
+            const int64_t M = (int64_t)trim + len + gen + trim - len % gen;
+            const int64_t step = overlap < 0 ? chunk - n_fft : (int64_t)((1.0 - (double)overlap) * chunk);
+            if (step <= 0) return 0;
+            n = (M + step - 1) / step;
+        } else {
+            const int step = stx_demix_step(chunk, num_overlap, overlap);
+            if (step < 1) return 0;
+            n = demix_geometry(len, chunk, step, STX_DEMIX_MSST).n_chunks;
+        }
+        auto align = [](size_t b) { return (b + 255) / 256 * 256; };
+        return align(sizeof(float) * (size_t)batch * channels * chunk) +
+               align(sizeof(float) * (size_t)n * n_stems * channels * chunk) + 256;
+    } catch (...) {
+        return 0;
+    }
+}
+
+STX_API stx_status stx_tfc_tdf_separate(const float* mix, int channels, int64_t len, int chunk, int n_fft,
+                                        stx_tfc_chunking chunking, int num_overlap, int n_stems, float compensate,
+                                        int complement, int batch, stx_separate_fn separate, void* separate_user,
+                                        const stx_separate_options* options, float* out, void* workspace,
+                                        size_t workspace_bytes, stx_stream stream) {
+    stx_uvr_demix* uplan = nullptr;
+    stx_demix* mplan = nullptr;
+    const stx_status st = guard([&] {
+        stx_separate_options opt{};
+        opt.overlap = -1.0f;
+        if (options) opt = *options;
+        if (!mix || len <= 0) fail(STX_STATUS_RUNTIME_ERROR, "tfc_tdf: empty input");                // :572
+        STX_REQUIRE(chunking == STX_TFC_MSST || chunking == STX_TFC_UVR, "unknown TFC-TDF chunking %d", chunking);
+        STX_REQUIRE(channels >= 1 && n_stems >= 1 && chunk >= 1 && batch >= 1, "bad channels/stems/chunk/batch");
+        STX_REQUIRE(out && separate && workspace && workspace_bytes >= 256, "NULL argument or no workspace");
+        const hipStream_t s = as_stream(stream);
+        char* ws = static_cast<char*>(workspace);
+        {   // :573-574; the flag borrows the workspace's first bytes before any chunk is built
+            int* d_flag = reinterpret_cast<int*>(ws);
+            int flag = 0;
+            hip_check(hipMemcpyAsync(d_flag, &flag, sizeof(int), hipMemcpyHostToDevice, s), "flag");
+            hipLaunchKernelGGL(nonfinite_kernel, dim3(grid_for((int64_t)channels * len)), dim3(256), 0, s, mix,
+                               (int64_t)channels * len, d_flag);
+            launch_check("nonfinite_kernel");
+            hip_check(hipMemcpyAsync(&flag, d_flag, sizeof(int), hipMemcpyDeviceToHost, s), "flag");
+            hip_check(hipStreamSynchronize(s), "flag");
+            if (flag) fail(STX_STATUS_RUNTIME_ERROR, "tfc_tdf: non-finite input");
+        }
+        if (opt.shifts != 0) fail(STX_STATUS_RUNTIME_ERROR, "tfc_tdf: shifts are unsupported");        // :575
+        if (opt.overlap >= 1.0f) fail(STX_STATUS_INVALID_ARGUMENT, "overlap must be < 1");           // :576
+        if (opt.should_cancel && opt.should_cancel(opt.user)) fail(STX_STATUS_CANCELLED, "cancelled"); // :581
+        int64_t n = 0;
+        if (chunking == STX_TFC_UVR) {                   // the plan reports the reference's errors (:410,:414)
+            const stx_status cs = stx_uvr_demix_create(len, channels, chunk, n_fft, opt.overlap, &uplan);
+            if (cs != STX_STATUS_OK) fail(cs, "%s", stx_last_error());
+            n = uplan->n_chunks;
+        } else {
+            const int step = stx_demix_step(chunk, num_overlap, opt.overlap);
+            STX_REQUIRE(step >= 1, "bad num_overlap");
+            const stx_status cs = stx_demix_create_rules(len, channels, chunk, step, STX_DEMIX_MSST, &mplan);
+            if (cs != STX_STATUS_OK) fail(cs, "%s", stx_last_error());
+            n = stx_demix_n_chunks(mplan);
+        }
+        const size_t need = stx_tfc_tdf_separate_workspace_size(channels, len, chunk, n_fft, chunking, num_overlap,
+                                                                opt.overlap, n_stems, batch);
+        STX_REQUIRE(workspace_bytes >= need, "workspace too small: %zu bytes, need %zu", workspace_bytes, need);
+        const size_t parts_bytes = ((sizeof(float) * (size_t)batch * channels * chunk) + 255) / 256 * 256;
+        float* d_parts = reinterpret_cast<float*>(ws);
+        float* d_y = reinterpret_cast<float*>(ws + parts_bytes);
+        const int total = (int)n;
+        int done = 0;
+        for (int64_t first = 0; first < n; first += batch) {
+            const int64_t count = std::min<int64_t>(batch, n - first);
+            for (int64_t k = 0; k < count; k++)                                                   // :426, :481
+                if (opt.should_cancel && opt.should_cancel(opt.user)) fail(STX_STATUS_CANCELLED, "cancelled");
+            const stx_status cs = uplan ? stx_uvr_demix_chunks(uplan, mix, first, count, d_parts, stream)
+                                        : stx_demix_chunks(mplan, mix, first, count, d_parts, stream);
+            if (cs != STX_STATUS_OK) fail(cs, "%s", stx_last_error());
+            const int32_t rc = separate(separate_user, d_parts, first, count,
+                                        d_y + (size_t)first * n_stems * channels * chunk, stream);
+            if (rc != 0) fail(STX_STATUS_RUNTIME_ERROR, "separator failed with %d", rc);
+            for (int64_t k = 0; k < count; k++)                                                   // :433, :489
+                if (opt.progress) opt.progress(opt.user, ++done, total);
+        }
+        const stx_status os = uplan ? stx_uvr_demix_overlap_add(uplan, d_y, n_stems, out, stream)
+                                    : stx_demix_overlap_add(mplan, d_y, n_stems, out, stream);
+        if (os != STX_STATUS_OK) fail(os, "%s", stx_last_error());
+        if (compensate != 1.0f || complement) {                                                   // :582-593
+            const int64_t plane = (int64_t)channels * len;
+            STX_REQUIRE((plane + 255) / 256 < (1LL << 31), "input too long");
+            hipLaunchKernelGGL(tfc_post_kernel, dim3((unsigned)((plane + 255) / 256)), dim3(256), 0, s, mix, plane,
+                               n_stems, compensate, complement ? 1 : 0, out);
+            launch_check("tfc_post_kernel");
+        }
+        // The plans' tables are freed below: the queued kernels must have finished first.
+        hip_check(hipStreamSynchronize(s), "tfc_tdf_separate");
+    });
+    if (st != STX_STATUS_OK) (void)hipStreamSynchronize(as_stream(stream));
+    stx_uvr_demix_destroy(uplan);
+    stx_demix_destroy(mplan);
+    return st;
+}
+
+}  // extern "C"

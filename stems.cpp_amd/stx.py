@@ -57,6 +57,19 @@ _SIGNATURES = {
     "stx_demix_plan": (_i, [ctypes.c_int64, _i, _i, _vp, _vp, ctypes.c_int64]),
     "stx_demix_window": (_i, [_i, _vp]),
     "stx_demix_create": (_i, [ctypes.c_int64, _i, _i, _i, ctypes.POINTER(_vp)]),
+    "stx_demix_plan_rules": (_i, [ctypes.c_int64, _i, _i, _i, _vp, _vp, ctypes.c_int64]),
+    "stx_demix_window_rules": (_i, [_i, _i, _vp]),
+    "stx_demix_create_rules": (_i, [ctypes.c_int64, _i, _i, _i, _i, ctypes.POINTER(_vp)]),
+    "stx_uvr_demix_create": (_i, [ctypes.c_int64, _i, _i, _i, ctypes.c_float, ctypes.POINTER(_vp)]),
+    "stx_uvr_demix_destroy": (None, [_vp]),
+    "stx_uvr_demix_n_chunks": (ctypes.c_int64, [_vp]),
+    "stx_uvr_demix_geometry": (_i, [_vp, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64), _c_int_p]),
+    "stx_uvr_demix_chunks": (_i, [_vp, _vp, ctypes.c_int64, ctypes.c_int64, _vp, _vp]),
+    "stx_uvr_demix_overlap_add": (_i, [_vp, _vp, _i, _vp, _vp]),
+    "stx_tfc_tdf_separate_workspace_size": (ctypes.c_size_t, [_i, ctypes.c_int64, _i, _i, _i, _i, ctypes.c_float,
+                                                              _i, _i]),
+    "stx_tfc_tdf_separate": (_i, [_vp, _i, ctypes.c_int64, _i, _i, _i, _i, _i, ctypes.c_float, _i, _i, _vp, _vp,
+                                  _vp, _vp, _vp, ctypes.c_size_t, _vp]),
     "stx_demix_destroy": (None, [_vp]),
     "stx_demix_n_chunks": (ctypes.c_int64, [_vp]),
     "stx_demix_chunks": (_i, [_vp, _vp, ctypes.c_int64, ctypes.c_int64, _vp, _vp]),
@@ -413,13 +426,18 @@ def demix_step(chunk, num_overlap, overlap=-1.0):
     return lib().stx_demix_step(int(chunk), int(num_overlap), float(overlap))
 
 
-def demix_plan(length, chunk, step):
+DEMIX_ROFORMER, DEMIX_MSST = 0, 1
+TFC_MSST, TFC_UVR = 0, 1
+
+
+def demix_plan(length, chunk, step, rules=DEMIX_ROFORMER):
     """(geometry dict, numpy structured chunk table) of the overlap-add demix (host only)."""
     import numpy as np
     g = DemixGeometry()
-    check(lib().stx_demix_plan(int(length), int(chunk), int(step), ctypes.byref(g), None, 0))
+    check(lib().stx_demix_plan_rules(int(length), int(chunk), int(step), int(rules), ctypes.byref(g), None, 0))
     table = (Chunk * max(1, g.n_chunks))()
-    check(lib().stx_demix_plan(int(length), int(chunk), int(step), ctypes.byref(g), table, g.n_chunks))
+    check(lib().stx_demix_plan_rules(int(length), int(chunk), int(step), int(rules), ctypes.byref(g), table,
+                                     g.n_chunks))
     geom = {f: getattr(g, f) for f, _ in DemixGeometry._fields_}
     arr = np.array([(c.start, c.length, c.pad_mode, c.fade_in, c.fade_out) for c in table[: g.n_chunks]],
                    dtype=[("start", np.int64), ("length", np.int32), ("pad_mode", np.int32),
@@ -427,19 +445,20 @@ def demix_plan(length, chunk, step):
     return geom, arr
 
 
-def demix_window(chunk):
+def demix_window(chunk, rules=DEMIX_ROFORMER):
     import numpy as np
     w = np.zeros(chunk, dtype=np.float32)
-    check(lib().stx_demix_window(int(chunk), _np_ptr(w)))
+    check(lib().stx_demix_window_rules(int(chunk), int(rules), _np_ptr(w)))
     return w
 
 
 class Demix:
     """Device plan of the overlap-add demix for one input length."""
 
-    def __init__(self, length, channels, chunk, step):
+    def __init__(self, length, channels, chunk, step, rules=DEMIX_ROFORMER):
         h = ctypes.c_void_p()
-        check(lib().stx_demix_create(int(length), int(channels), int(chunk), int(step), ctypes.byref(h)))
+        check(lib().stx_demix_create_rules(int(length), int(channels), int(chunk), int(step), int(rules),
+                                           ctypes.byref(h)))
         self.handle = h
         self.length, self.channels, self.chunk, self.step = int(length), int(channels), int(chunk), int(step)
         self.n_chunks = lib().stx_demix_n_chunks(h)
@@ -474,6 +493,86 @@ class Demix:
             out = torch.empty((S, self.channels, self.length), dtype=torch.float32, device=y.device)
         check(lib().stx_demix_overlap_add(self.handle, _ptr(y), int(S), _ptr(out), _stream(stream)))
         return out
+
+
+class UvrDemix:
+    """Device plan of UVR's SeperateMDX.demix chunking (TFC-TDF "uvr_mdx") for one input length."""
+
+    def __init__(self, length, channels, chunk, n_fft, overlap=-1.0):
+        h = ctypes.c_void_p()
+        check(lib().stx_uvr_demix_create(int(length), int(channels), int(chunk), int(n_fft), float(overlap),
+                                         ctypes.byref(h)))
+        self.handle = h
+        self.length, self.channels, self.chunk = int(length), int(channels), int(chunk)
+        self.n_chunks = lib().stx_uvr_demix_n_chunks(h)
+        M, st, tr = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int()
+        check(lib().stx_uvr_demix_geometry(h, ctypes.byref(M), ctypes.byref(st), ctypes.byref(tr)))
+        self.padded_len, self.step, self.trim = M.value, st.value, tr.value
+
+    def close(self):
+        if getattr(self, "handle", None):
+            lib().stx_uvr_demix_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def chunks(self, mix, first=0, count=None, out=None, stream=None):
+        import torch
+        _require(mix, torch.float32, "mix")
+        count = self.n_chunks - first if count is None else count
+        if out is None:
+            out = torch.empty((count, self.channels, self.chunk), dtype=torch.float32, device=mix.device)
+        check(lib().stx_uvr_demix_chunks(self.handle, _ptr(mix), int(first), int(count), _ptr(out), _stream(stream)))
+        return out
+
+    def overlap_add(self, y, out=None, stream=None):
+        import torch
+        _require(y, torch.float32, "y")
+        S = y.shape[1]
+        if out is None:
+            out = torch.empty((S, self.channels, self.length), dtype=torch.float32, device=y.device)
+        check(lib().stx_uvr_demix_overlap_add(self.handle, _ptr(y), int(S), _ptr(out), _stream(stream)))
+        return out
+
+
+def tfc_tdf_separate(mix, chunk, n_fft, chunking, n_stems, separate, num_overlap=4, compensate=1.0,
+                     complement=False, batch=4, shifts=0, overlap=-1.0, progress=None, should_cancel=None,
+                     stream=None):
+    """TFCTDF::separate around a Python separator (same callback as demix_track)."""
+    import torch
+    _require(mix, torch.float32, "mix")
+    C, L = mix.shape
+    ws_bytes = lib().stx_tfc_tdf_separate_workspace_size(C, L, int(chunk), int(n_fft), int(chunking),
+                                                         int(num_overlap), float(overlap), int(n_stems), int(batch))
+    ws = workspace(max(ws_bytes, 256), mix.device)
+    out = torch.empty((n_stems + (1 if complement else 0), C, L), dtype=torch.float32, device=mix.device)
+
+    def sep(user, parts, first, count, y, st):
+        try:
+            return int(separate(parts, first, count, y, st))
+        except Exception:
+            import traceback
+            traceback.print_exc()
+            return -1
+
+    def prog(user, done, total):
+        progress(done, total)
+
+    def canc(user):
+        return 1 if should_cancel() else 0
+
+    cb = SEPARATE_FN(sep)
+    opt = SeparateOptions(int(shifts), float(overlap), 0, PROGRESS_FN(prog) if progress else PROGRESS_FN(),
+                          CANCEL_FN(canc) if should_cancel else CANCEL_FN(), None)
+    check(lib().stx_tfc_tdf_separate(_ptr(mix), C, L, int(chunk), int(n_fft), int(chunking), int(num_overlap),
+                                     int(n_stems), float(compensate), int(bool(complement)), int(batch),
+                                     ctypes.cast(cb, ctypes.c_void_p), None, ctypes.byref(opt), _ptr(out), _ptr(ws),
+                                     ws.numel() * 4, _stream(stream)))
+    return out
 
 
 def demix_track(mix, chunk, num_overlap, n_stems, separate, complement=False, sample_rate=44100, batch=8,

@@ -188,6 +188,23 @@ class _Demix:
         L.orc_demix_chunks.argtypes = [_vp, _i, ctypes.c_long, _i, _i, _vp]
         L.orc_demix_ola.restype = _i
         L.orc_demix_ola.argtypes = [_vp, _i, _i, ctypes.c_long, _i, _i, _vp]
+        L.orc_msst_window.restype = None
+        L.orc_msst_window.argtypes = [_i, _vp]
+        L.orc_msst_n_chunks.restype = ctypes.c_long
+        L.orc_msst_n_chunks.argtypes = [ctypes.c_long, _i, _i]
+        L.orc_msst_chunks.restype = _i
+        L.orc_msst_chunks.argtypes = [_vp, _i, ctypes.c_long, _i, _i, _vp]
+        L.orc_msst_ola.restype = _i
+        L.orc_msst_ola.argtypes = [_vp, _i, _i, ctypes.c_long, _i, _i, _vp]
+        L.orc_uvr_geometry.restype = ctypes.c_long
+        L.orc_uvr_geometry.argtypes = [ctypes.c_long, _i, _i, ctypes.c_float, ctypes.POINTER(ctypes.c_long),
+                                       ctypes.POINTER(ctypes.c_long)]
+        L.orc_uvr_chunks.restype = _i
+        L.orc_uvr_chunks.argtypes = [_vp, _i, ctypes.c_long, _i, _i, ctypes.c_float, _vp]
+        L.orc_uvr_ola.restype = _i
+        L.orc_uvr_ola.argtypes = [_vp, _i, _i, ctypes.c_long, _i, _i, ctypes.c_float, _vp]
+        L.orc_tfc_post.restype = None
+        L.orc_tfc_post.argtypes = [_vp, ctypes.c_long, _i, ctypes.c_float, _i, _vp]
         self.L = L
 
     def n_chunks(self, length, chunk, step):
@@ -213,6 +230,59 @@ class _Demix:
         n, S, C, _ = y.shape
         out = np.zeros((S, C, length), dtype=np.float32)
         self.L.orc_demix_ola(_np(y), S, C, length, chunk, step, _np(out))
+        return out
+
+    # TFC-TDF: MSST and UVR chunking (oracle/tfc_oracle.c)
+    def msst_window(self, chunk):
+        w = np.zeros(chunk, dtype=np.float32)
+        self.L.orc_msst_window(chunk, _np(w))
+        return w
+
+    def msst_chunks(self, mix, chunk, step):
+        mix = np.ascontiguousarray(mix, dtype=np.float32)
+        C, length = mix.shape
+        n = self.L.orc_msst_n_chunks(length, chunk, step)
+        parts = np.zeros((n, C, chunk), dtype=np.float32)
+        if self.L.orc_msst_chunks(_np(mix), C, length, chunk, step, _np(parts)):
+            raise RuntimeError("msst_chunks")
+        return parts
+
+    def msst_ola(self, y, length, chunk, step):
+        y = np.ascontiguousarray(y, dtype=np.float32)
+        n, S, C, _ = y.shape
+        out = np.zeros((S, C, length), dtype=np.float32)
+        self.L.orc_msst_ola(_np(y), S, C, length, chunk, step, _np(out))
+        return out
+
+    def uvr_geometry(self, length, chunk, n_fft, overlap=-1.0):
+        M, st = ctypes.c_long(), ctypes.c_long()
+        n = self.L.orc_uvr_geometry(length, chunk, n_fft, overlap, ctypes.byref(M), ctypes.byref(st))
+        return n, M.value, st.value
+
+    def uvr_chunks(self, mix, chunk, n_fft, overlap=-1.0):
+        mix = np.ascontiguousarray(mix, dtype=np.float32)
+        C, length = mix.shape
+        n, _, _ = self.uvr_geometry(length, chunk, n_fft, overlap)
+        parts = np.zeros((n, C, chunk), dtype=np.float32)
+        if self.L.orc_uvr_chunks(_np(mix), C, length, chunk, n_fft, overlap, _np(parts)):
+            raise RuntimeError("uvr_chunks")
+        return parts
+
+    def uvr_ola(self, y, length, chunk, n_fft, overlap=-1.0):
+        y = np.ascontiguousarray(y, dtype=np.float32)
+        n, S, C, _ = y.shape
+        out = np.zeros((S, C, length), dtype=np.float32)
+        if self.L.orc_uvr_ola(_np(y), S, C, length, chunk, n_fft, overlap, _np(out)):
+            raise RuntimeError("uvr_ola")
+        return out
+
+    def tfc_post(self, mix, est, compensate, complement):
+        """est float32 [S][C][len] -> [S + complement][C][len]."""
+        mix = np.ascontiguousarray(mix, dtype=np.float32)
+        S = est.shape[0]
+        out = np.zeros((S + (1 if complement else 0),) + est.shape[1:], np.float32)
+        out[:S] = est
+        self.L.orc_tfc_post(_np(mix), mix.size, S, compensate, int(bool(complement)), _np(out))
         return out
 
 
