@@ -624,6 +624,22 @@ def run_rows(torch, stx, dev):
     out["c5_demix_overlap_add"] = time_call(torch, stream, mk_ola, lens * S * C * 4 + S * C * Lsong * 4)
     del plan
 
+    # The same song through the TFC-TDF UVR chunking (Kim_Vocal_2: n_fft 7680, chunk 261,120,
+    # step 253,440, one stem): chunk inputs and the hanning-weighted overlap-add.
+    uvr = stx.UvrDemix(Lsong, C, 261120, 7680)
+
+    def mk_uvr_chunks():
+        m, p = mix.clone(), torch.empty((uvr.n_chunks, C, 261120), device=dev)
+        return lambda: uvr.chunks(m, out=p, stream=stream)
+    out["c5_uvr_chunks"] = time_call(torch, stream, mk_uvr_chunks, C * Lsong * 4 + uvr.n_chunks * C * 261120 * 4)
+
+    def mk_uvr_ola():
+        y, o = rn(uvr.n_chunks, 1, C, 261120), torch.empty((1, C, Lsong), device=dev)
+        return lambda: uvr.overlap_add(y, out=o, stream=stream)
+    uvr_read = sum(min(261120, uvr.padded_len - k * uvr.step) for k in range(uvr.n_chunks))
+    out["c5_uvr_overlap_add"] = time_call(torch, stream, mk_uvr_ola, (uvr_read + Lsong) * C * 4)
+    del uvr
+
     # The same song through HTDemucs' apply_model split: mono-mix normalise, the 31 padded
     # segments of 343,980 samples (stride 257,985) and the triangular-weight overlap-add.
     seg = 343980

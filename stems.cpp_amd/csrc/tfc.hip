@@ -23,7 +23,6 @@ struct stx_uvr_demix {
     int64_t len = 0, M = 0, step = 0, n_chunks = 0, first_partial = 0;
     int channels = 0, chunk = 0, n_fft = 0, trim = 0;
     double* d_w = nullptr;           // [chunk] weights of full chunks, then each partial chunk's
-    int64_t* d_woff = nullptr;       // [n_chunks]: offset of chunk k's weights in d_w
 };
 
 namespace stx {
@@ -31,13 +30,22 @@ namespace {
 
 struct UvrArgs {
     int64_t len, M, step;
-    int64_t n_chunks;
+    int64_t n_chunks, first_partial;
     int chunk, trim, channels;
     FastDiv sdiv;                // division by step (M < 2^32)
 };
 
 UvrArgs uvr_args(const stx_uvr_demix* d) {
-    return UvrArgs{d->len, d->M, d->step, d->n_chunks, d->chunk, d->trim, d->channels, FastDiv((unsigned)d->step)};
+    return UvrArgs{d->len, d->M, d->step, d->n_chunks, d->first_partial, d->chunk, d->trim, d->channels,
+                   FastDiv((unsigned)d->step)};
+}
+
+// Offset of chunk k's weights in the plan's table: 0 for full chunks, then the partial chunks'
+// tables back to back, partial chunk j holding M - j * step weights (the host layout).
+__host__ __device__ __forceinline__ int64_t uvr_woff(const UvrArgs& a, int64_t k) {
+    if (k < a.first_partial) return 0;
+    const int64_t f = a.first_partial;
+    return a.chunk + (k - f) * a.M - a.step * ((k * (k - 1) - f * (f - 1)) / 2);
 }
 
 // parts[k - first][c][t] = x[c][i + t] for t < actual, else 0, where x is the mix behind `trim`
@@ -72,59 +80,72 @@ __global__ __launch_bounds__(256) void uvr_chunks_kernel(UvrArgs a, const float*
 
 // out[q][t] = sum_k (double)y[k][q][p - i_k] * w_k[p - i_k] / sum_k w_k[p - i_k], p = trim + t,
 // over the chunks covering p in chunk order (src/tfc_tdf.cpp:427-440). NK bounds the chunks
-// covering one sample. A thread takes one sample and kUvrPlanes planes, which share the weights
-// and their sum; loads are clamped to valid addresses and issued together.
+// covering one sample. A thread takes kUvrPer samples and P planes, which share the weights and
+// their sum; loads are clamped to valid addresses and issued together.
 constexpr int kUvrMaxCover = 8;
-constexpr int kUvrPlanes = 4;
+constexpr int kUvrPer = 2;
+
+template <int NK, int P>
+__global__ __launch_bounds__(256) void uvr_ola_kernel(UvrArgs a, const float* __restrict__ y,
+                                                      const double* __restrict__ w, int planes,
+                                                      float* __restrict__ out) {
+#pragma clang fp contract(off)
+    const int q0 = (int)blockIdx.y * P;
+    const int64_t t0 = (int64_t)blockIdx.x * kUvrPer * 256 + threadIdx.x;
+    if (t0 >= a.len) return;
+    // Every load of every sample first (clamped addresses), then the sums: a chunk that does not
+    // cover the sample adds +0.0, an exact no-op (the sums start at +0.0 and never become -0.0),
+    // so no load sits behind a branch.
+    double wv[kUvrPer][NK];
+    bool in[kUvrPer][NK];
+    float yv[kUvrPer][P][NK];
+#pragma unroll
+    for (int e = 0; e < kUvrPer; e++) {
+        const int64_t t = min(t0 + 256LL * e, a.len - 1);
+        const int64_t p = a.trim + t;
+        const int64_t k_hi = min((int64_t)a.sdiv.div((unsigned)p), a.n_chunks - 1);
+#pragma unroll
+        for (int j = 0; j < NK; j++) {                  // chunk k_hi - j
+            const int64_t k = max(k_hi - j, (int64_t)0);
+            const int64_t i = k * a.step;
+            const int64_t actual = min((int64_t)a.chunk, a.M - i);
+            const int64_t r = p - i;
+            in[e][j] = k_hi - j >= 0 && r < actual;
+            const int64_t rc = min(r, actual - 1);
+            wv[e][j] = w[uvr_woff(a, k) + rc];
+            const int64_t base = (int64_t)k * planes * a.chunk + rc;
+#pragma unroll
+            for (int u = 0; u < P; u++) yv[e][u][j] = y[base + (int64_t)min(q0 + u, planes - 1) * a.chunk];
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < kUvrPer; e++) {
+        const int64_t t = t0 + 256LL * e;
+        double div = 0.0;
+#pragma unroll
+        for (int j = NK - 1; j >= 0; j--) div = div + (in[e][j] ? wv[e][j] : 0.0);   // ascending chunk order
+#pragma unroll
+        for (int u = 0; u < P; u++) {
+            double res = 0.0;
+#pragma unroll
+            for (int j = NK - 1; j >= 0; j--) {
+                const double prod = (double)yv[e][u][j] * wv[e][j];
+                res = res + (in[e][j] ? prod : 0.0);
+            }
+            if (t < a.len && q0 + u < planes) out[(size_t)(q0 + u) * a.len + t] = (float)(res / div);
+        }
+    }
+}
 
 template <int NK>
-__global__ __launch_bounds__(256) void uvr_ola_kernel(UvrArgs a, const float* __restrict__ y,
-                                                      const double* __restrict__ w, const int64_t* __restrict__ woff,
-                                                      int planes, float* __restrict__ out) {
-#pragma clang fp contract(off)
-    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (t >= a.len) return;
-    const int q0 = (int)blockIdx.y * kUvrPlanes;
-    const int64_t p = a.trim + t;
-    const int64_t k_hi = min((int64_t)a.sdiv.div((unsigned)p), a.n_chunks - 1);
-    double wv[NK];
-    int64_t base[NK];
-    bool in[NK];
-#pragma unroll
-    for (int j = 0; j < NK; j++) {                      // chunk k_hi - j
-        const int64_t k = max(k_hi - j, (int64_t)0);
-        const int64_t i = k * a.step;
-        const int64_t actual = min((int64_t)a.chunk, a.M - i);
-        const int64_t r = p - i;
-        in[j] = k_hi - j >= 0 && r < actual;
-        const int64_t rc = min(r, actual - 1);
-        wv[j] = w[woff[k] + rc];
-        base[j] = (int64_t)k * planes * a.chunk + rc;
-    }
-    float yv[kUvrPlanes][NK];
-#pragma unroll
-    for (int u = 0; u < kUvrPlanes; u++) {
-        const int64_t q = min(q0 + u, planes - 1);
-#pragma unroll
-        for (int j = 0; j < NK; j++) yv[u][j] = y[base[j] + q * a.chunk];
-    }
-    double div = 0.0;
-#pragma unroll
-    for (int j = NK - 1; j >= 0; j--)                   // ascending chunk order
-        if (in[j]) div = div + wv[j];
-#pragma unroll
-    for (int u = 0; u < kUvrPlanes; u++) {
-        if (q0 + u >= planes) break;
-        double res = 0.0;
-#pragma unroll
-        for (int j = NK - 1; j >= 0; j--) {
-            if (in[j]) {
-                const double prod = (double)yv[u][j] * wv[j];
-                res = res + prod;
-            }
-        }
-        out[(size_t)(q0 + u) * a.len + t] = (float)(res / div);
-    }
+void launch_uvr_ola(const UvrArgs& a, const float* y, const double* w, int planes, float* out, hipStream_t s) {
+    const unsigned bx = (unsigned)((a.len + 256 * kUvrPer - 1) / (256 * kUvrPer));
+    if (planes % 4 == 0)
+        hipLaunchKernelGGL((uvr_ola_kernel<NK, 4>), dim3(bx, (unsigned)(planes / 4)), dim3(256), 0, s, a, y, w, planes, out);
+    else if (planes % 2 == 0)
+        hipLaunchKernelGGL((uvr_ola_kernel<NK, 2>), dim3(bx, (unsigned)(planes / 2)), dim3(256), 0, s, a, y, w, planes, out);
+    else
+        hipLaunchKernelGGL((uvr_ola_kernel<NK, 1>), dim3(bx, (unsigned)planes), dim3(256), 0, s, a, y, w, planes, out);
 }
 
 // est *= compensate (when != 1), and with `complement` rest = mix - est_0 - est_1 - ... in float
@@ -188,16 +209,12 @@ STX_API stx_status stx_uvr_demix_create(int64_t len, int channels, int chunk, in
                 for (int i = 0; i < m; i++) w[o + i] = 0.5 - 0.5 * std::cos(2.0 * M_PI * i / (m - 1));
         };
         std::vector<double> w;
-        std::vector<int64_t> woff(n);
         hanning(chunk, w);
         int64_t first_partial = n;
         for (int64_t k = 0; k < n; k++) {
             const int64_t actual = std::min<int64_t>(chunk, M - k * step);
-            if (actual == chunk) {
-                woff[k] = 0;
-            } else {
+            if (actual < chunk) {                   // every chunk after the first partial one is partial
                 if (first_partial == n) first_partial = k;
-                woff[k] = (int64_t)w.size();
                 hanning((int)actual, w);
             }
         }
@@ -211,10 +228,11 @@ STX_API stx_status stx_uvr_demix_create(int64_t len, int channels, int chunk, in
         d->chunk = chunk;
         d->n_fft = n_fft;
         d->trim = trim;
+        for (int64_t k = 0; k < n; k++)             // the device recomputes the offsets in closed form
+            STX_REQUIRE(uvr_woff(uvr_args(d), k) + std::min<int64_t>(chunk, M - k * step) <= (int64_t)w.size(),
+                        "UVR weight table layout");
         hipError_t e = hipMalloc(&d->d_w, sizeof(double) * w.size());
         if (e == hipSuccess) e = hipMemcpy(d->d_w, w.data(), sizeof(double) * w.size(), hipMemcpyHostToDevice);
-        if (e == hipSuccess) e = hipMalloc(&d->d_woff, sizeof(int64_t) * n);
-        if (e == hipSuccess) e = hipMemcpy(d->d_woff, woff.data(), sizeof(int64_t) * n, hipMemcpyHostToDevice);
         if (e != hipSuccess) {
             stx_uvr_demix_destroy(d);
             hip_check(e, "stx_uvr_demix_create");
@@ -226,7 +244,6 @@ STX_API stx_status stx_uvr_demix_create(int64_t len, int channels, int chunk, in
 STX_API void stx_uvr_demix_destroy(stx_uvr_demix* d) {
     if (!d) return;
     (void)hipFree(d->d_w);
-    (void)hipFree(d->d_woff);
     delete d;
 }
 
@@ -267,17 +284,14 @@ STX_API stx_status stx_uvr_demix_overlap_add(const stx_uvr_demix* d, const float
         const int64_t cover = (d->chunk + d->step - 1) / d->step;
         if (cover > kUvrMaxCover)
             fail(STX_STATUS_UNSUPPORTED, "UVR overlap-add: more than %d chunks cover a sample", kUvrMaxCover);
-        const dim3 grid((unsigned)((d->len + 255) / 256), (unsigned)((planes + kUvrPlanes - 1) / kUvrPlanes));
         const hipStream_t s = as_stream(stream);
         const UvrArgs a = uvr_args(d);
         switch (cover) {
-        case 1: hipLaunchKernelGGL(uvr_ola_kernel<1>, grid, dim3(256), 0, s, a, y, d->d_w, d->d_woff, planes, out); break;
-        case 2: hipLaunchKernelGGL(uvr_ola_kernel<2>, grid, dim3(256), 0, s, a, y, d->d_w, d->d_woff, planes, out); break;
-        case 3: hipLaunchKernelGGL(uvr_ola_kernel<3>, grid, dim3(256), 0, s, a, y, d->d_w, d->d_woff, planes, out); break;
-        case 4: hipLaunchKernelGGL(uvr_ola_kernel<4>, grid, dim3(256), 0, s, a, y, d->d_w, d->d_woff, planes, out); break;
-        default:
-            hipLaunchKernelGGL(uvr_ola_kernel<kUvrMaxCover>, grid, dim3(256), 0, s, a, y, d->d_w, d->d_woff, planes, out);
-            break;
+        case 1: launch_uvr_ola<1>(a, y, d->d_w, planes, out, s); break;
+        case 2: launch_uvr_ola<2>(a, y, d->d_w, planes, out, s); break;
+        case 3: launch_uvr_ola<3>(a, y, d->d_w, planes, out, s); break;
+        case 4: launch_uvr_ola<4>(a, y, d->d_w, planes, out, s); break;
+        default: launch_uvr_ola<kUvrMaxCover>(a, y, d->d_w, planes, out, s); break;
         }
         launch_check("uvr_ola_kernel");
     });
