@@ -70,6 +70,13 @@ typedef struct stx_fft stx_fft;
  * build has no kernels for. Allocates the plan's device tables (window, twiddles) on the
  * current device. */
 STX_API stx_status stx_fft_create(int n, stx_fft** out);
+/* st::VRFFT::VRFFT(int n) (src/vr_dsp.h:11-37), the plan the reference uses for sizes that are
+ * not powers of two (TFC-TDF's n_fft 7680, src/tfc_tdf.cpp:85-86,551-552; VR's 320/640/960): any
+ * even n = 2^a 3^b 5^c in [16, 16384] (powers of two in [16, 8192] give the stx_fft_create plan),
+ * UNSUPPORTED otherwise. The plan serves stx_fft_run (complex transforms up to 8192 points),
+ * stx_torch_stft and the workspace iSTFT (stx_torch_istft_ws); the reference's Bluestein
+ * transform is computed exactly (a DFT), so results agree to rounding. */
+STX_API stx_status stx_fft_create_any(int n, stx_fft** out);
 STX_API void       stx_fft_destroy(stx_fft* fft);
 /* st::FFT::size() (src/stft.h:32). */
 STX_API int        stx_fft_size(const stx_fft* fft);

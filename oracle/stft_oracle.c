@@ -64,6 +64,58 @@ int orc_fft(double* a, int n, int inverse) {
     return 0;
 }
 
+/* st::VRFFT (src/vr_dsp.h:11-37): Bluestein's transform for any n on top of the radix-2 FFT of
+ * m >= 2n - 1 points: chirp c[i] = polar(1, -pi i^2 / n), kernel conj(c) wrapped around and
+ * transformed once, then x -> (x c) * FFT -> * kernel -> inverse FFT -> * c / m; the inverse
+ * transform conjugates on the way in and out. Unnormalised, like orc_fft. */
+int orc_vrfft(double* x, int n, int inverse) {
+    if (n < 1) return -1;
+    int m = 1;
+    while (m < 2 * n - 1) m *= 2;
+    double* chirp = (double*)malloc(sizeof(double) * 2 * n);
+    double* kern = (double*)calloc(2 * (size_t)m, sizeof(double));
+    double* a = (double*)calloc(2 * (size_t)m, sizeof(double));
+    for (int i = 0; i < n; i++) {
+        const double th = -M_PI * (double)i * i / n;
+        chirp[2 * i] = 1.0 * cos(th);
+        chirp[2 * i + 1] = 1.0 * sin(th);
+        kern[2 * i] = chirp[2 * i];
+        kern[2 * i + 1] = -chirp[2 * i + 1];
+        if (i) {
+            kern[2 * (m - i)] = kern[2 * i];
+            kern[2 * (m - i) + 1] = kern[2 * i + 1];
+        }
+    }
+    orc_fft(kern, m, 0);
+    for (int i = 0; i < n; i++) {
+        const double xr = x[2 * i], xi = inverse ? -x[2 * i + 1] : x[2 * i + 1];
+        const double cr = chirp[2 * i], ci = chirp[2 * i + 1];
+        a[2 * i] = xr * cr - xi * ci;
+        a[2 * i + 1] = xr * ci + xi * cr;
+    }
+    orc_fft(a, m, 0);
+    for (int i = 0; i < m; i++) {
+        const double ar = a[2 * i], ai = a[2 * i + 1], kr = kern[2 * i], ki = kern[2 * i + 1];
+        a[2 * i] = ar * kr - ai * ki;
+        a[2 * i + 1] = ar * ki + ai * kr;
+    }
+    orc_fft(a, m, 1);
+    for (int i = 0; i < n; i++) {
+        const double ar = a[2 * i], ai = a[2 * i + 1], cr = chirp[2 * i], ci = chirp[2 * i + 1];
+        const double vr = (ar * cr - ai * ci) / (double)m, vi = (ar * ci + ai * cr) / (double)m;
+        x[2 * i] = vr;
+        x[2 * i + 1] = inverse ? -vi : vi;
+    }
+    free(chirp);
+    free(kern);
+    free(a);
+    return 0;
+}
+
+/* The FFT the reference's torch_stft / torch_istft template is instantiated with: st::FFT for
+ * powers of two, st::VRFFT otherwise (src/tfc_tdf.cpp:551-552). */
+static int any_fft(double* a, int n, int inverse) { return is_pow2(n) ? orc_fft(a, n, inverse) : orc_vrfft(a, n, inverse); }
+
 int orc_hann_periodic(double* w, int n) {
     for (int i = 0; i < n; i++) w[i] = 0.5 - 0.5 * cos(2.0 * M_PI * i / n);
     return 0;
@@ -93,7 +145,7 @@ static int frames_fft(const double* xp, int n_fft, int T, long first, long hop, 
             buf[2 * i] = xp[start + i] * win[i];
             buf[2 * i + 1] = 0.0;
         }
-        orc_fft(buf, n_fft, 0);
+        any_fft(buf, n_fft, 0);
         for (int f = 0; f < F; f++) {
             out[2 * ((size_t)f * T + t)] = buf[2 * f] * norm;
             out[2 * ((size_t)f * T + t) + 1] = buf[2 * f + 1] * norm;
@@ -105,7 +157,7 @@ static int frames_fft(const double* xp, int n_fft, int T, long first, long hop, 
 }
 
 int orc_torch_stft(const float* x, int len, int n_fft, int hop, int normalized, double* spec, int* n_frames) {
-    if (!is_pow2(n_fft)) return -1;
+    if (n_fft < 2) return -1;
     const int F = n_fft / 2 + 1;
     double* xp = (double*)malloc(sizeof(double) * ((size_t)len + n_fft));
     if (orc_reflect_pad(x, len, n_fft / 2, n_fft / 2, xp)) {
@@ -146,7 +198,7 @@ int orc_htdemucs_spec(const float* x, int len, int n_fft, double* spec, int* n_f
 }
 
 int orc_torch_istft(const double* spec, int n_frames, int n_fft, int hop, int normalized, float* out) {
-    if (!is_pow2(n_fft)) return -1;
+    if (n_fft < 2 || n_fft % 2) return -1;
     const int F = n_fft / 2 + 1;
     double* win = (double*)malloc(sizeof(double) * n_fft);
     orc_hann_periodic(win, n_fft);
@@ -167,7 +219,7 @@ int orc_torch_istft(const double* spec, int n_frames, int n_fft, int hop, int no
         }
         buf[2 * (F - 1)] = spec[2 * ((size_t)(F - 1) * n_frames + t)];
         buf[2 * (F - 1) + 1] = 0.0;
-        orc_fft(buf, n_fft, 1);
+        any_fft(buf, n_fft, 1);
         const size_t off = (size_t)t * hop;
         for (int i = 0; i < n_fft; i++) {
             y[off + i] += buf[2 * i] * norm * win[i];

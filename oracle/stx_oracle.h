@@ -15,6 +15,8 @@
  *     written by the reference's own src/stft.h (tests/golden/), plus closed forms (impulse
  *     known answer, brute-force DFT, Parseval) and the reference's round-trip tolerances
  *     (tests/dsp_test.cpp:63,76-77,95).
+ *   orc_vrfft: a brute-force DFT in double (closed form) at the reference's sizes 7680, 960, 640
+ *     and 320, and the torch STFT -> iSTFT round trip at n_fft 7680 (Kim_Vocal_2).
  *   orc_mel_band_map: the counts the survey of the reference restated independently (60 bands,
  *     1,979 entries, sizes 7, 6, 6, ..., 122, 130, 71 bins in one band and 954 in two), an
  *     independent vectorised float32 restatement of librosa's filterbank in the test, and the
@@ -64,6 +66,10 @@ extern "C" {
 
 /* st::FFT (src/stft.h:19-55): in-place radix-2 DIT, unnormalised; inverse = conj twiddles. */
 int orc_fft(double* a, int n, int inverse);
+
+/* st::VRFFT (src/vr_dsp.h:11-37): Bluestein for any n, unnormalised. orc_torch_stft and
+ * orc_torch_istft use it for sizes that are not powers of two, as the reference's TFC-TDF does. */
+int orc_vrfft(double* a, int n, int inverse);
 
 /* st::hann_periodic (src/stft.h:70-74). */
 int orc_hann_periodic(double* w, int n);

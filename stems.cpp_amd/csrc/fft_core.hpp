@@ -108,6 +108,42 @@ template <> struct Dft<16> {
     }
 };
 
+// Odd radices of the mixed-radix path (sizes 2^a 3^b 5^c). Dft<3>: X1,2 = a - (b + c)/2 -/+
+// i sqrt(3)/2 (b - c). Dft<5>: with t1 = x1 + x4, t2 = x2 + x3, t3 = x1 - x4, t4 = x2 - x3,
+// X1,4 = x0 + c1 t1 + c2 t2 -/+ i (s1 t3 + s2 t4), X2,3 = x0 + c2 t1 + c1 t2 -/+ i (s2 t3 - s1 t4),
+// c_k = cos(2 pi k / 5), s_k = sin(2 pi k / 5).
+template <> struct Dft<3> {
+    static STX_HD void run(float2* v) {
+        constexpr float h = 0.86602540378443864676f;     // sqrt(3) / 2
+        const float2 a = v[0], t1 = cadd(v[1], v[2]), t2 = csub(v[1], v[2]);
+        const float2 m = make_float2(a.x - 0.5f * t1.x, a.y - 0.5f * t1.y);
+        const float2 q = make_float2(h * t2.y, -h * t2.x);  // -i h t2
+        v[0] = cadd(a, t1);
+        v[1] = cadd(m, q);
+        v[2] = csub(m, q);
+    }
+};
+
+template <> struct Dft<5> {
+    static STX_HD void run(float2* v) {
+        constexpr float c1 = 0.30901699437494742410f, c2 = -0.80901699437494742410f;
+        constexpr float s1 = 0.95105651629515357212f, s2 = 0.58778525229247312917f;
+        const float2 x0 = v[0];
+        const float2 t1 = cadd(v[1], v[4]), t2 = cadd(v[2], v[3]);
+        const float2 t3 = csub(v[1], v[4]), t4 = csub(v[2], v[3]);
+        const float2 a1 = make_float2(x0.x + c1 * t1.x + c2 * t2.x, x0.y + c1 * t1.y + c2 * t2.y);
+        const float2 a2 = make_float2(x0.x + c2 * t1.x + c1 * t2.x, x0.y + c2 * t1.y + c1 * t2.y);
+        const float2 b1 = make_float2(s1 * t3.x + s2 * t4.x, s1 * t3.y + s2 * t4.y);
+        const float2 b2 = make_float2(s2 * t3.x - s1 * t4.x, s2 * t3.y - s1 * t4.y);
+        const float2 ib1 = make_float2(b1.y, -b1.x), ib2 = make_float2(b2.y, -b2.x);   // -i b
+        v[0] = cadd(x0, cadd(t1, t2));
+        v[1] = cadd(a1, ib1);
+        v[4] = csub(a1, ib1);
+        v[2] = cadd(a2, ib2);
+        v[3] = csub(a2, ib2);
+    }
+};
+
 constexpr int ilog2(int n) { return n <= 1 ? 0 : 1 + ilog2(n / 2); }
 
 // Two-level twiddle table for TN points: [L low entries W^m, m < L][H high entries W^(L*h)].
@@ -251,5 +287,79 @@ struct ToLds {
     float2* buf;
     __device__ __forceinline__ void operator()(int n, float2 v) const { buf[n + n / P] = v; }
 };
+
+}  // namespace stx
+
+namespace stx {
+
+// Mixed-radix plan of an M-point complex transform, M = 2^a 3^b 5^c: radix 16 passes while 16
+// divides what is left, then one of 8, 4 or 2, then 3s and 5s.
+struct MixedRadix {
+    int count = 0;
+    int r[24] = {};
+};
+
+inline bool mixed_plan(int m, MixedRadix& p) {
+    p = MixedRadix{};
+    if (m < 1) return false;
+    int left = m;
+    while (left % 16 == 0) { p.r[p.count++] = 16; left /= 16; }
+    for (int q : {8, 4, 2})
+        if (left % q == 0) { p.r[p.count++] = q; left /= q; }
+    while (left % 3 == 0) { p.r[p.count++] = 3; left /= 3; }
+    while (left % 5 == 0) { p.r[p.count++] = 5; left /= 5; }
+    return left == 1 && p.count <= 24;
+}
+
+// One out-of-place Stockham pass of radix R after sub-transforms of length Ns over an M-point
+// transform held in src (natural layout), by the NT threads of a workgroup: butterfly b reads
+// src[b + r M/R], multiplies element r by W_{Ns R}^{(b mod Ns) r} = twn[(b mod Ns) r scale]
+// (twn: W_n^m, scale = n / (Ns R)), takes an R-point DFT and writes
+// dst[(b / Ns) Ns R + b mod Ns + r Ns].
+template <int R>
+__device__ __forceinline__ void mixed_pass(const float2* src, float2* dst, int M, int Ns, int scale,
+                                           const float2* __restrict__ twn, int tid, int nt) {
+    const int B = M / R;
+    for (int b = tid; b < B; b += nt) {
+        const int blk = b / Ns, k = b - blk * Ns;
+        float2 v[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) v[r] = src[b + r * B];
+#pragma unroll
+        for (int r = 1; r < R; r++) v[r] = cmul(v[r], twn[k * r * scale]);
+        Dft<R>::run(v);
+        const int base = blk * Ns * R + k;
+#pragma unroll
+        for (int r = 0; r < R; r++) dst[base + r * Ns] = v[r];
+    }
+}
+
+// All passes of plan p over the M-point transform in buf0 (buf1: scratch of M); returns the
+// buffer holding the result. Every thread of the workgroup must call it (it has barriers).
+// twn holds W_n^m for m < n with n a multiple of M (tw_mul = n / M).
+__device__ __forceinline__ float2* mixed_fft(float2* buf0, float2* buf1, int M, const MixedRadix& p, int tw_mul,
+                                             const float2* __restrict__ twn, int tid, int nt) {
+    float2* src = buf0;
+    float2* dst = buf1;
+    int Ns = 1;
+    for (int i = 0; i < p.count; i++) {
+        const int R = p.r[i];
+        const int scale = (M / (Ns * R)) * tw_mul;
+        switch (R) {
+            case 16: mixed_pass<16>(src, dst, M, Ns, scale, twn, tid, nt); break;
+            case 8: mixed_pass<8>(src, dst, M, Ns, scale, twn, tid, nt); break;
+            case 4: mixed_pass<4>(src, dst, M, Ns, scale, twn, tid, nt); break;
+            case 2: mixed_pass<2>(src, dst, M, Ns, scale, twn, tid, nt); break;
+            case 3: mixed_pass<3>(src, dst, M, Ns, scale, twn, tid, nt); break;
+            default: mixed_pass<5>(src, dst, M, Ns, scale, twn, tid, nt); break;
+        }
+        __syncthreads();
+        float2* t = src;
+        src = dst;
+        dst = t;
+        Ns *= R;
+    }
+    return src;
+}
 
 }  // namespace stx

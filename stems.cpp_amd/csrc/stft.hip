@@ -32,6 +32,10 @@ struct stx_fft {
     int device = 0;
     float2* twt = nullptr;   // device: two-level twiddle table for n points (fft_core.hpp)
     float* win = nullptr;    // device [n]: periodic Hann
+    int mixed = 0;           // n = 2^a 3^b 5^c, not a power of two: the mixed-radix kernels
+    float2* twn = nullptr;   // mixed: device [n], W_n^m
+    stx::MixedRadix half;    // mixed: plan of the n/2-point transform of real frames
+    stx::MixedRadix full;    // mixed: plan of the n-point complex transform
 };
 
 namespace stx {
@@ -211,18 +215,21 @@ __device__ __forceinline__ float2 spec_bin(const IstftArgs& a, const float2* __r
 // conj Z'[k] for k < N/2 from X[k] and X[N/2 - k] of one frame: the inverse split, with the
 // DC and Nyquist imaginary parts ignored (src/stft.h:121,177,182) and the Nyquist bin zeroed
 // for HTDemucs (:126).
-template <int N>
-__device__ __forceinline__ float2 inverse_split(float2 xk, float2 xm, int k, int keep_nyquist,
-                                                const float2* __restrict__ twt) {
+__device__ __forceinline__ float2 inverse_split_w(float2 xk, float2 xm, int k, int keep_nyquist, float2 w) {
     if (k == 0) {
         xk = make_float2(xk.x, 0.f);
         xm = keep_nyquist ? make_float2(xm.x, 0.f) : make_float2(0.f, 0.f);
     }
     const float er = xk.x + xm.x, ei = xk.y - xm.y;          // X[k] + conj X[M-k]
     const float dr = xk.x - xm.x, di = xk.y + xm.y;          // X[k] - conj X[M-k]
-    const float2 w = tw_lookup<N>(twt, k);                   // times conj(W_N^k)
-    const float orr = dr * w.x + di * w.y, oi = di * w.x - dr * w.y;
+    const float orr = dr * w.x + di * w.y, oi = di * w.x - dr * w.y;   // times conj(W_N^k)
     return make_float2(er - oi, -(ei + orr));                // conj(E' + i O')
+}
+
+template <int N>
+__device__ __forceinline__ float2 inverse_split(float2 xk, float2 xm, int k, int keep_nyquist,
+                                                const float2* __restrict__ twt) {
+    return inverse_split_w(xk, xm, k, keep_nyquist, tw_lookup<N>(twt, k));
 }
 
 // Windowed output of the inverse transform: z[n] = conj(fft(conj Z'))[n] holds samples
@@ -498,6 +505,85 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
     });
 }
 
+// ------------------------------------------------------------------ mixed-radix sizes
+// n = 2^a 3^b 5^c that is not a power of two (VRFFT's sizes: Kim_Vocal_2's 7680, VR's 320, 640,
+// 960; src/vr_dsp.h:11-37, src/tfc_tdf.cpp:85-86,551-552). The reference reaches these sizes with
+// Bluestein (three power-of-two transforms of at least 2n - 1 points); here one workgroup runs
+// the n/2-point transform of a real frame directly, radix 16 / 8 / 4 / 2 / 3 / 5 Stockham passes
+// ping-ponging between two LDS buffers with twiddles W_n^m from a table computed in double.
+// Frames are packed and split as in the power-of-two kernels; the iSTFT always takes the
+// two-kernel path (frames to the workspace, then istft_ola_kernel).
+constexpr int kMixedThreads = 256;
+
+__device__ __forceinline__ int padded_index_rt(int m, const StftArgs& a, int n) {
+    int j = reflect(m - n / 2, a.len1) - a.pre_left;
+    j = reflect(j, a.len);
+    return min(max(j, 0), a.len - 1);
+}
+
+template <int MAXM>
+__global__ __launch_bounds__(kMixedThreads) void stft_mixed_kernel(StftArgs a, MixedRadix p,
+                                                                   const float2* __restrict__ twn, int n) {
+    __shared__ float2 b0[MAXM], b1[MAXM];
+    const int M = n / 2, tid = (int)threadIdx.x;
+    const int f = (int)blockIdx.x;                     // channel * T + frame
+    const int c = f / a.T, t = f - c * a.T;
+    const float* xc = a.x + (size_t)c * a.len;
+    const int m0 = a.frame0 + t * a.hop;
+    for (int i = tid; i < M; i += kMixedThreads) {
+        const float x0 = xc[padded_index_rt(m0 + 2 * i, a, n)], x1 = xc[padded_index_rt(m0 + 2 * i + 1, a, n)];
+        b0[i] = make_float2(x0 * a.win[2 * i], x1 * a.win[2 * i + 1]);
+    }
+    __syncthreads();
+    const float2* z = mixed_fft(b0, b1, M, p, 2, twn, tid, kMixedThreads);
+    // X[k] = E[k] + W_n^k O[k], k <= n/2, as in stft_kernel.
+    const float hs = 0.5f * a.scale;
+    for (int k = tid; k < a.F; k += kMixedThreads) {
+        const float2 zk = z[k == M ? 0 : k], zm = z[k == 0 ? 0 : M - k];
+        const float2 w = twn[k];
+        const float er = zk.x + zm.x, ei = zk.y - zm.y;
+        const float orr = zk.y + zm.y, oi = zm.x - zk.x;
+        const float2 val = make_float2((er + w.x * orr - w.y * oi) * hs, (ei + w.x * oi + w.y * orr) * hs);
+        if (a.layout == STX_SPEC_F_MAJOR) a.spec[((size_t)c * a.F + k) * a.T + t] = val;
+        else a.spec[((size_t)c * a.T + t) * a.F + k] = val;
+    }
+}
+
+template <int MAXM>
+__global__ __launch_bounds__(kMixedThreads) void istft_frames_mixed_kernel(IstftArgs a, MixedRadix p,
+                                                                           const float2* __restrict__ twn, int n) {
+    __shared__ float2 b0[MAXM], b1[MAXM];
+    const int M = n / 2, tid = (int)threadIdx.x;
+    const int f = (int)blockIdx.x;
+    const int c = f / a.T, st = f - c * a.T;
+    const float2* sc = a.spec + (size_t)c * a.T * a.F;
+    for (int k = tid; k < M; k += kMixedThreads) {
+        const float2 xk = spec_bin(a, sc, st, k);
+        float2 xm = spec_bin(a, sc, st, min(M - k, a.F - 1));
+        if (k == 0 && !a.keep_nyquist) xm = make_float2(0.f, 0.f);
+        b0[k] = inverse_split_w(xk, xm, k, a.keep_nyquist, twn[k]);
+    }
+    __syncthreads();
+    const float2* r = mixed_fft(b0, b1, M, p, 2, twn, tid, kMixedThreads);
+    float* dst = a.frames + (size_t)f * n;
+    for (int i = tid; i < M; i += kMixedThreads) {     // windowed as WindowPost
+        dst[2 * i] = r[i].x * a.win[2 * i] * a.norm;
+        dst[2 * i + 1] = -r[i].y * a.win[2 * i + 1] * a.norm;
+    }
+}
+
+template <int MAXM>
+__global__ __launch_bounds__(kMixedThreads) void fft_mixed_kernel(float2* data, int inverse, MixedRadix p,
+                                                                  const float2* __restrict__ twn, int n) {
+    __shared__ float2 b0[MAXM], b1[MAXM];
+    const int tid = (int)threadIdx.x;
+    float2* d = data + (size_t)blockIdx.x * n;
+    for (int i = tid; i < n; i += kMixedThreads) b0[i] = inverse ? cconj(d[i]) : d[i];
+    __syncthreads();
+    const float2* r = mixed_fft(b0, b1, n, p, 1, twn, tid, kMixedThreads);
+    for (int i = tid; i < n; i += kMixedThreads) d[i] = inverse ? cconj(r[i]) : r[i];
+}
+
 __global__ __launch_bounds__(256) void zero_kernel(float* out, size_t count) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i < count) out[i] = 0.f;
@@ -671,6 +757,24 @@ size_t istft_workspace_bytes(int n, int channels, int n_frames) {
 // Shared body of the four iSTFT entry points.
 void run_istft(const stx_fft* f, IstftArgs a, int channels, void* workspace, size_t ws_bytes, hipStream_t s) {
     const bool two_step = workspace != nullptr;
+    if (f->mixed) {
+        if (!two_step) fail(STX_STATUS_UNSUPPORTED, "iSTFT of size %d needs the workspace variant", f->n);
+        const size_t need = istft_workspace_bytes(f->n, channels, a.T);
+        STX_REQUIRE(ws_bytes >= need, "workspace too small: %zu bytes, need %zu", ws_bytes, need);
+        check_extent((long long)channels * a.T * f->n, "workspace");
+        a.frames = static_cast<float*>(workspace);
+        const unsigned frames = (unsigned)(channels * a.T);
+        if (f->n / 2 <= 1024)
+            hipLaunchKernelGGL(istft_frames_mixed_kernel<1024>, dim3(frames), dim3(kMixedThreads), 0, s, a, f->half,
+                               f->twn, f->n);
+        else
+            hipLaunchKernelGGL(istft_frames_mixed_kernel<8192>, dim3(frames), dim3(kMixedThreads), 0, s, a, f->half,
+                               f->twn, f->n);
+        launch_check("istft_frames_mixed_kernel");
+        hipLaunchKernelGGL(istft_ola_kernel, dim3((a.out_len + 255) / 256, channels), dim3(256), 0, s, a, f->n);
+        launch_check("istft_ola_kernel");
+        return;
+    }
     if (two_step) {
         const size_t need = istft_workspace_bytes(f->n, channels, a.T);
         STX_REQUIRE(ws_bytes >= need, "workspace too small: %zu bytes, need %zu", ws_bytes, need);
@@ -718,6 +822,7 @@ stx_status htdemucs_ispec_impl(const stx_fft* f, const float* spec, int channels
                                float* out, stx_spec_layout layout, void* ws, size_t ws_bytes, stx_stream stream) {
     return guard([&] {
         check_fft(f);
+        if (f->mixed) fail(STX_STATUS_UNSUPPORTED, "htdemucs_ispec needs a power-of-two FFT size");
         check_layout(layout);
         const int n = f->n, hl = n / 4, pad = hl / 2 * 3;
         STX_REQUIRE(channels >= 0 && n_frames >= 0 && length >= 0, "bad channels/n_frames/length");
@@ -796,10 +901,45 @@ STX_API stx_status stx_fft_create(int n, stx_fft** out) {
     });
 }
 
+STX_API stx_status stx_fft_create_any(int n, stx_fft** out) {
+    if (n >= 16 && n <= 8192 && (n & (n - 1)) == 0) return stx_fft_create(n, out);
+    return guard([&] {
+        STX_REQUIRE(out != nullptr, "out is NULL");
+        *out = nullptr;
+        STX_REQUIRE(n >= 1, "FFT size must be positive");
+        MixedRadix half, full;
+        if (n % 2 != 0 || n < 16 || n > 16384 || !mixed_plan(n / 2, half) || !mixed_plan(n, full))
+            fail(STX_STATUS_UNSUPPORTED, "FFT size %d has no kernel (even sizes 2^a 3^b 5^c from 16 to 16384)", n);
+        std::vector<float2> twn(n);
+        for (int m = 0; m < n; m++) {
+            const double th = 2.0 * M_PI * (double)m / n;
+            twn[m] = make_float2((float)std::cos(th), (float)-std::sin(th));
+        }
+        std::vector<float> win(n);
+        for (int m = 0; m < n; m++) win[m] = (float)(0.5 - 0.5 * std::cos(2.0 * M_PI * m / n));   // hann_periodic (src/stft.h:70-74)
+        stx_fft* f = new stx_fft;
+        f->n = n;
+        f->mixed = 1;
+        f->half = half;
+        f->full = full;
+        hipError_t e = hipGetDevice(&f->device);
+        if (e == hipSuccess) e = hipMalloc(&f->twn, sizeof(float2) * n);
+        if (e == hipSuccess) e = hipMalloc(&f->win, sizeof(float) * n);
+        if (e == hipSuccess) e = hipMemcpy(f->twn, twn.data(), sizeof(float2) * n, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(f->win, win.data(), sizeof(float) * n, hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            stx_fft_destroy(f);
+            hip_check(e, "stx_fft_create_any");
+        }
+        *out = f;
+    });
+}
+
 STX_API void stx_fft_destroy(stx_fft* f) {
     if (!f) return;
     if (f->twt) (void)hipFree(f->twt);
     if (f->win) (void)hipFree(f->win);
+    if (f->twn) (void)hipFree(f->twn);
     delete f;
 }
 
@@ -812,6 +952,19 @@ STX_API stx_status stx_fft_run(const stx_fft* f, float* data, int batch, int inv
         if (batch == 0) return;
         STX_REQUIRE(data != nullptr, "data is NULL");
         check_extent((long long)batch * f->n, "FFT batch");
+        if (f->mixed) {
+            if (f->n > 8192) fail(STX_STATUS_UNSUPPORTED, "complex transforms of %d points (at most 8192)", f->n);
+            if (f->n <= 1024)
+                hipLaunchKernelGGL(fft_mixed_kernel<1024>, dim3((unsigned)batch), dim3(kMixedThreads), 0,
+                                   as_stream(stream), reinterpret_cast<float2*>(data), inverse ? 1 : 0, f->full, f->twn,
+                                   f->n);
+            else
+                hipLaunchKernelGGL(fft_mixed_kernel<8192>, dim3((unsigned)batch), dim3(kMixedThreads), 0,
+                                   as_stream(stream), reinterpret_cast<float2*>(data), inverse ? 1 : 0, f->full, f->twn,
+                                   f->n);
+            launch_check("fft_mixed_kernel");
+            return;
+        }
         by_size<FftL>(f->n, reinterpret_cast<float2*>(data), batch, inverse ? 1 : 0, f->twt, as_stream(stream));
     });
 }
@@ -851,6 +1004,17 @@ STX_API stx_status stx_torch_stft(const stx_fft* f, const float* x, int channels
         a.scale = normalized ? (float)(1.0 / std::sqrt((double)n)) : 1.0f;
         check_extent((long long)channels * a.T * a.F, "spectrum");
         check_extent((long long)channels * len + n, "signal");
+        if (f->mixed) {
+            const unsigned frames = (unsigned)a.jobs;
+            if (n / 2 <= 1024)
+                hipLaunchKernelGGL(stft_mixed_kernel<1024>, dim3(frames), dim3(kMixedThreads), 0, as_stream(stream), a,
+                                   f->half, f->twn, n);
+            else
+                hipLaunchKernelGGL(stft_mixed_kernel<8192>, dim3(frames), dim3(kMixedThreads), 0, as_stream(stream), a,
+                                   f->half, f->twn, n);
+            launch_check("stft_mixed_kernel");
+            return;
+        }
         by_size<StftL>(n, a, as_stream(stream));
     });
 }
@@ -859,6 +1023,7 @@ STX_API stx_status stx_htdemucs_spec(const stx_fft* f, const float* x, int chann
                                      stx_spec_layout layout, stx_stream stream) {
     return guard([&] {
         check_fft(f);
+        if (f->mixed) fail(STX_STATUS_UNSUPPORTED, "htdemucs_spec needs a power-of-two FFT size");
         check_layout(layout);
         const int n = f->n, hl = n / 4;
         STX_REQUIRE(channels >= 0 && len >= 0, "bad channels/len");

@@ -32,6 +32,7 @@ _SIGNATURES = {
     "stx_last_error": (ctypes.c_char_p, []),
     "stx_fft_create": (_i, [_i, ctypes.POINTER(_vp)]),
     "stx_fft_destroy": (None, [_vp]),
+    "stx_fft_create_any": (_i, [_i, ctypes.POINTER(_vp)]),
     "stx_fft_size": (_i, [_vp]),
     "stx_fft_run": (_i, [_vp, _vp, _i, _i, _vp]),
     "stx_torch_stft_frames": (_i, [_i, _i]),
@@ -167,9 +168,11 @@ def _require(t, dtype, what):
 class FFT:
     """st::FFT (src/stft.h:19-55) on the device: plan holding the window and twiddle tables."""
 
-    def __init__(self, n):
+    def __init__(self, n, any_size=False):
+        """any_size: st::VRFFT's sizes as well (even 2^a 3^b 5^c, stx_fft_create_any)."""
         h = ctypes.c_void_p()
-        check(lib().stx_fft_create(int(n), ctypes.byref(h)))
+        create = lib().stx_fft_create_any if any_size else lib().stx_fft_create
+        check(create(int(n), ctypes.byref(h)))
         self.handle = h
         self.n = int(n)
 

@@ -46,6 +46,16 @@ class _Stft:
             raise ValueError(f"fft rc={rc}")
         return a
 
+    def vrfft(self, a, inverse=False):
+        """st::VRFFT (Bluestein, any size) of the oracle."""
+        fn = self.L.orc_vrfft
+        fn.restype = _i
+        fn.argtypes = [_vp, _i, _i]
+        a = np.ascontiguousarray(a, dtype=np.complex128).copy()
+        if fn(_np(a), a.size, int(inverse)):
+            raise ValueError("vrfft")
+        return a
+
     def torch_stft(self, x, n_fft, hop, normalized=False):
         x = np.ascontiguousarray(x, dtype=np.float32)
         T = x.size // hop + 1

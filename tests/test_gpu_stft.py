@@ -225,3 +225,85 @@ def test_workspace_too_small(device):
     with pytest.raises(stx.StxError) as e:
         stx.torch_istft(f, spec, 441, workspace=ws)
     assert e.value.status == stx.STATUS_INVALID_ARGUMENT
+
+
+# ----------------------------------------- st::VRFFT sizes (mixed-radix kernels on the device)
+_any_plans = {}
+
+
+def any_plan(n):
+    if n not in _any_plans:
+        _any_plans[n] = stx.FFT(n, any_size=True)
+    return _any_plans[n]
+
+
+@pytest.mark.parametrize("n", [7680, 3840, 960, 640, 320, 480, 6000])
+def test_fft_run_any_size(device, orc, n):
+    """Complex transforms of VRFFT's sizes against the oracle's Bluestein (src/vr_dsp.h:11-37)."""
+    v = synth.normal(n + 1, (3, 2 * n), 1.0).astype(np.float64)
+    a = (v[:, 0::2] + 1j * v[:, 1::2]).astype(np.complex64)
+    d = to_dev(a, device)
+    any_plan(n).run(d)
+    fw = host(d)
+    any_plan(n).run(d, inverse=True)
+    back = host(d) / n
+    for b in range(3):
+        assert snr_db(fw[b], orc.vrfft(a[b].astype(np.complex128))) >= SNR_DB
+        assert snr_db(back[b], a[b]) >= SNR_DB
+
+
+@pytest.mark.parametrize("layout", [stx.F_MAJOR, stx.T_MAJOR])
+@pytest.mark.parametrize("normalized", [False, True])
+def test_torch_stft_7680_kim_chunk(device, orc, layout, normalized):
+    """Kim_Vocal_2's transform (src/tfc_tdf.cpp:355-359): n_fft 7680, hop 1024, one chunk of
+    1024 x 255 = 261,120 stereo samples -> [2][3841][256]; STFT and the workspace iSTFT."""
+    length, n, hop = 261120, 7680, 1024
+    x = _stereo(7680, length)
+    f = any_plan(n)
+    spec = stx.torch_stft(f, to_dev(x, device), hop, normalized, layout=layout)
+    ws = stx.workspace(stx.istft_workspace_size(f, 2, length // hop + 1), device)
+    y = stx.torch_istft(f, spec, hop, normalized, layout=layout, workspace=ws)
+    spec_h, y_h = host(spec), host(y)
+    if layout == stx.T_MAJOR:
+        spec_h = spec_h.transpose(0, 2, 1)
+    assert spec_h.shape == (2, 3841, 256)
+    for c in range(2):
+        ref = orc.torch_stft(x[c], n, hop, normalized)
+        assert snr_db(spec_h[c], ref) >= SNR_DB
+        assert snr_db(y_h[c], orc.torch_istft(ref, n, hop, normalized)) >= SNR_DB
+
+
+@pytest.mark.parametrize("n,hop", [(320, 80), (640, 160), (960, 240), (1536, 256)])
+def test_torch_stft_vr_sizes_round_trip(device, orc, n, hop):
+    length = 20 * n + 3
+    x = _stereo(n, length, 0.5)
+    f = any_plan(n)
+    spec = stx.torch_stft(f, to_dev(x, device), hop)
+    ws = stx.workspace(stx.istft_workspace_size(f, 2, length // hop + 1), device)
+    y = stx.torch_istft(f, spec, hop, workspace=ws)
+    spec_h, y_h = host(spec), host(y)
+    for c in range(2):
+        ref = orc.torch_stft(x[c], n, hop)
+        assert snr_db(spec_h[c], ref) >= SNR_DB
+        assert snr_db(y_h[c], orc.torch_istft(ref, n, hop)) >= SNR_DB
+
+
+def test_any_size_errors(device):
+    import torch
+    for n in (7, 14, 22, 20000):
+        with pytest.raises(stx.StxError) as e:
+            stx.FFT(n, any_size=True)
+        assert e.value.status == stx.STATUS_UNSUPPORTED
+    with pytest.raises(stx.StxError) as e:
+        stx.FFT(7680)                                              # st::FFT: powers of two only
+    assert e.value.status == stx.STATUS_INVALID_ARGUMENT
+    assert any_plan(2048).n == 2048                                 # a power of two: the radix-16 plan
+    f = any_plan(7680)
+    x = torch.zeros((1, 20000), dtype=torch.float32, device=device)
+    spec = stx.torch_stft(f, x, 1024)
+    with pytest.raises(stx.StxError) as e:
+        stx.torch_istft(f, spec, 1024)                             # needs the workspace variant
+    assert e.value.status == stx.STATUS_UNSUPPORTED
+    with pytest.raises(stx.StxError) as e:
+        stx.htdemucs_spec(f, x)
+    assert e.value.status == stx.STATUS_UNSUPPORTED

@@ -150,3 +150,39 @@ def test_reflect_pad_errors(orc):
         orc.torch_stft(np.zeros(1024, np.float32), 2048, 441)        # len <= n/2
     with pytest.raises(RuntimeError):
         orc.htdemucs_spec(np.zeros(1000, np.float32), 4096)          # len <= pad (1536)
+
+
+# ----------------------------------------------- st::VRFFT (Bluestein) for other sizes
+@pytest.mark.parametrize("n", [7680, 960, 640, 320, 15])
+def test_vrfft_is_a_dft(n):
+    """orc_vrfft (src/vr_dsp.h:11-37) against the DFT by its definition, in double."""
+    o = oracle_lib.oracle()
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal(n) + 1j * rng.standard_normal(n)
+    k = np.arange(n)
+    if n <= 1000:
+        want = np.exp(-2j * np.pi * np.outer(k, k) / n) @ x
+    else:
+        want = np.fft.fft(x)                                 # pinned to the definition at the small sizes
+    got = o.vrfft(x)
+    assert np.max(np.abs(got - want)) <= 1e-9 * np.max(np.abs(want))
+    back = o.vrfft(got, inverse=True) / n
+    assert np.max(np.abs(back - x)) <= 1e-12 * np.max(np.abs(x))
+
+
+def test_torch_stft_istft_7680_round_trip():
+    """torch_stft -> torch_istft with the Kim_Vocal_2 transform (n_fft 7680, hop 1024): the
+    identity away from the edges, as the reference's power-of-two round trips
+    (tests/dsp_test.cpp:63,76-77)."""
+    o = oracle_lib.oracle()
+    x = synth.normal(3, (30000,), 0.3)
+    spec = o.torch_stft(x, 7680, 1024)
+    y = o.torch_istft(spec, 7680, 1024)
+    n = min(len(y), len(x))
+    assert np.max(np.abs(y[:n] - x[:n])) <= 1e-6 * np.max(np.abs(x))
+    # Bin f of frame t is the DFT of the windowed, reflect-padded frame at that bin.
+    xp = np.pad(x.astype(np.float64), (3840, 3840), mode="reflect")
+    w = 0.5 - 0.5 * np.cos(2 * np.pi * np.arange(7680) / 7680)
+    t = 7
+    frame = xp[t * 1024:t * 1024 + 7680] * w
+    assert np.max(np.abs(spec[:, t] - np.fft.rfft(frame))) <= 1e-9 * np.max(np.abs(spec[:, t]))
