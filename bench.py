@@ -554,6 +554,23 @@ def run_rows(torch, stx, dev):
     out["c1_time_add"] = time_call(torch, stream, mk_tadd, 3 * 4 * C * L1 * 4)
 
 
+    # Kim_Vocal_2's transform (n_fft 7680, not a power of two; hop 1024) on one TFC-TDF chunk of
+    # 1024 x 255 = 261,120 stereo samples -> [2][3841][256]: the mixed-radix STFT and iSTFT.
+    fk, Lk, Tk, Fk = stx.FFT(7680, any_size=True), 261120, 256, 3841
+    kim_bytes = C * Lk * 4 + C * Tk * Fk * 8
+
+    def mk_kim_stft():
+        x, y = rn(C, Lk), torch.empty((C, Fk, Tk), dtype=torch.complex64, device=dev)
+        return lambda: stx.torch_stft(fk, x, 1024, out=y, stream=stream)
+    out["kim_stft_7680"] = time_call(torch, stream, mk_kim_stft, kim_bytes)
+
+    def mk_kim_istft():
+        z, y = torch.randn((C, Fk, Tk), dtype=torch.complex64, device=dev), torch.empty((C, 1024 * 255), device=dev)
+        ws = stx.workspace(stx.istft_workspace_size(fk, C, Tk), dev)
+        return lambda: stx.torch_istft(fk, z, 1024, out=y, stream=stream, workspace=ws)
+    out["kim_istft_7680"] = time_call(torch, stream, mk_kim_istft, kim_bytes)
+    del fk
+
     # c4: RoFormer transformer ops (dim 384, 8 heads x 64, 60 bands x 801 frames).
     def mk_rms():
         x, g, y = rn(48060, 384), rn(384), torch.empty((48060, 384), device=dev)

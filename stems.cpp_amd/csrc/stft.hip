@@ -767,6 +767,9 @@ void run_istft(const stx_fft* f, IstftArgs a, int channels, void* workspace, siz
         if (f->n / 2 <= 1024)
             hipLaunchKernelGGL(istft_frames_mixed_kernel<1024>, dim3(frames), dim3(kMixedThreads), 0, s, a, f->half,
                                f->twn, f->n);
+        else if (f->n / 2 <= 4096)
+            hipLaunchKernelGGL(istft_frames_mixed_kernel<4096>, dim3(frames), dim3(kMixedThreads), 0, s, a, f->half,
+                               f->twn, f->n);
         else
             hipLaunchKernelGGL(istft_frames_mixed_kernel<8192>, dim3(frames), dim3(kMixedThreads), 0, s, a, f->half,
                                f->twn, f->n);
@@ -958,6 +961,10 @@ STX_API stx_status stx_fft_run(const stx_fft* f, float* data, int batch, int inv
                 hipLaunchKernelGGL(fft_mixed_kernel<1024>, dim3((unsigned)batch), dim3(kMixedThreads), 0,
                                    as_stream(stream), reinterpret_cast<float2*>(data), inverse ? 1 : 0, f->full, f->twn,
                                    f->n);
+            else if (f->n <= 4096)
+                hipLaunchKernelGGL(fft_mixed_kernel<4096>, dim3((unsigned)batch), dim3(kMixedThreads), 0,
+                                   as_stream(stream), reinterpret_cast<float2*>(data), inverse ? 1 : 0, f->full, f->twn,
+                                   f->n);
             else
                 hipLaunchKernelGGL(fft_mixed_kernel<8192>, dim3((unsigned)batch), dim3(kMixedThreads), 0,
                                    as_stream(stream), reinterpret_cast<float2*>(data), inverse ? 1 : 0, f->full, f->twn,
@@ -1008,6 +1015,9 @@ STX_API stx_status stx_torch_stft(const stx_fft* f, const float* x, int channels
             const unsigned frames = (unsigned)a.jobs;
             if (n / 2 <= 1024)
                 hipLaunchKernelGGL(stft_mixed_kernel<1024>, dim3(frames), dim3(kMixedThreads), 0, as_stream(stream), a,
+                                   f->half, f->twn, n);
+            else if (n / 2 <= 4096)
+                hipLaunchKernelGGL(stft_mixed_kernel<4096>, dim3(frames), dim3(kMixedThreads), 0, as_stream(stream), a,
                                    f->half, f->twn, n);
             else
                 hipLaunchKernelGGL(stft_mixed_kernel<8192>, dim3(frames), dim3(kMixedThreads), 0, as_stream(stream), a,
