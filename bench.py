@@ -641,6 +641,16 @@ def run_rows(torch, stx, dev):
     out["c5_demix_overlap_add"] = time_call(torch, stream, mk_ola, lens * S * C * 4 + S * C * Lsong * 4)
     del plan
 
+    # The song arriving at 48 kHz: resampled to the models' 44.1 kHz (src/audio.h:17-59).
+    rsm = stx.Resampler(48000, 44100)
+    n48 = 8640000
+
+    def mk_resample():
+        x, y = rn(C, n48), torch.empty((C, rsm.length(n48)), device=dev)
+        return lambda: rsm(x, out=y, stream=stream)
+    out["c5_resample_48k"] = time_call(torch, stream, mk_resample, C * (n48 + rsm.length(n48)) * 4)
+    del rsm
+
     # The same song through the TFC-TDF UVR chunking (Kim_Vocal_2: n_fft 7680, chunk 261,120,
     # step 253,440, one stem): chunk inputs and the hanning-weighted overlap-add.
     uvr = stx.UvrDemix(Lsong, C, 261120, 7680)

@@ -381,6 +381,24 @@ STX_API stx_status stx_tfc_tdf_separate(const float* mix, int channels, int64_t 
                                         size_t workspace_bytes, stx_stream stream);
 
 /* ------------------------------------------------------------------------------------------
+ * Resampling. Replaces st::resample_planar (src/audio.h:17-59), used when the input is not at
+ * the model's rate.
+ * ---------------------------------------------------------------------------------------- */
+typedef struct stx_resampler stx_resampler;
+
+/* The reference's Kaiser-windowed sinc (beta 8.6, 32 zero crossings, cutoff 0.95 of the lower
+ * Nyquist), tabulated at 2^15 + 2 points on the device, for src_rate -> dst_rate. */
+STX_API stx_status stx_resampler_create(int src_rate, int dst_rate, stx_resampler** out);
+STX_API void       stx_resampler_destroy(stx_resampler* resampler);
+/* Output samples per channel for n input samples: llround(n * dst / src), n when the rates are
+ * equal (src/audio.h:19-20); -1 for a NULL plan or n < 0. */
+STX_API int64_t    stx_resample_length(const stx_resampler* resampler, int64_t n);
+/* in: device [channels][n]; out: device [channels][stx_resample_length(n)], bit-identical to the
+ * reference (double sums in its order). Equal rates copy. More than 8 channels is UNSUPPORTED. */
+STX_API stx_status stx_resample(const stx_resampler* resampler, const float* in, int channels, int64_t n, float* out,
+                                stx_stream stream);
+
+/* ------------------------------------------------------------------------------------------
  * HTDemucs pre/post-processing around the model graph, and apply_model's split. Replace the
  * host loops of HTDemucs::Impl::run (src/htdemucs.cpp:419-474) and HTDemucs::separate
  * (:534-644). Statistics are device double[2] {mean, sd}, written by the normalise calls and

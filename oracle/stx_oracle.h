@@ -39,6 +39,9 @@
  *     exactly 0 and 1; np.hanning against numpy's own), numpy restatements of both loops on
  *     small inputs, the identity model (both must return the mix), and the UVR geometry of the
  *     reference's defaults (trim n_fft / 2, step chunk - n_fft).
+ *   orc_resample: src == dst returns the input; a numpy restatement of the tabulated kernel,
+ *     bit for bit; the direct Kaiser-sinc formula (no table) to the interpolation error; and
+ *     the closed forms of a band-limited sine (passband gain 1) and of DC.
  *   orc_mean_std / orc_*normalize / orc_time_add / orc_split_*: torch.std's unbiased estimator
  *     and numpy float32 arithmetic on the same formulas, the weights' closed form (symmetric
  *     up to the centre sample, maximum 1), the identity model (a split of a model that returns
@@ -128,6 +131,11 @@ long orc_uvr_geometry(long len, int chunk, int n_fft, float overlap, long* M, lo
 int orc_uvr_chunks(const float* mix, int C, long len, int chunk, int n_fft, float overlap, float* parts);
 int orc_uvr_ola(const float* y, int S, int C, long len, int chunk, int n_fft, float overlap, float* out);
 void orc_tfc_post(const float* mix, long plane, int S, float compensate, int complement, float* est);
+
+/* st::resample_planar (src/audio.h:17-59) (resample_oracle.c). */
+void orc_resample_table(int src_rate, int dst_rate, double* table, double* half);
+long orc_resample_length(long n, int src_rate, int dst_rate);
+int orc_resample(const float* in, int n, int ch, int src_rate, int dst_rate, float* out);
 
 /* ggml ops (ops_oracle.c). Contiguous tensors, ggml extents ne[4] (ne[0] fastest); broadcast
  * operands repeat into ne. */

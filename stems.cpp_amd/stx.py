@@ -33,6 +33,10 @@ _SIGNATURES = {
     "stx_fft_create": (_i, [_i, ctypes.POINTER(_vp)]),
     "stx_fft_destroy": (None, [_vp]),
     "stx_fft_create_any": (_i, [_i, ctypes.POINTER(_vp)]),
+    "stx_resampler_create": (_i, [_i, _i, ctypes.POINTER(_vp)]),
+    "stx_resampler_destroy": (None, [_vp]),
+    "stx_resample_length": (ctypes.c_int64, [_vp, ctypes.c_int64]),
+    "stx_resample": (_i, [_vp, _vp, _i, ctypes.c_int64, _vp, _vp]),
     "stx_fft_size": (_i, [_vp]),
     "stx_fft_run": (_i, [_vp, _vp, _i, _i, _vp]),
     "stx_torch_stft_frames": (_i, [_i, _i]),
@@ -614,6 +618,40 @@ def demix_track(mix, chunk, num_overlap, n_stems, separate, complement=False, sa
                                 int(sample_rate), int(batch), ctypes.cast(cb, ctypes.c_void_p), None,
                                 ctypes.byref(opt), _ptr(out), _ptr(ws), ws.numel() * 4, _stream(stream)))
     return out
+
+
+# ---------------------------------------------------------------------------- resampling
+class Resampler:
+    """st::resample_planar (src/audio.h:17-59) on the device for one pair of rates."""
+
+    def __init__(self, src_rate, dst_rate):
+        h = ctypes.c_void_p()
+        check(lib().stx_resampler_create(int(src_rate), int(dst_rate), ctypes.byref(h)))
+        self.handle = h
+
+    def close(self):
+        if getattr(self, "handle", None):
+            lib().stx_resampler_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def length(self, n):
+        return lib().stx_resample_length(self.handle, int(n))
+
+    def __call__(self, x, out=None, stream=None):
+        """x float32 [C, n] -> [C, length(n)]."""
+        import torch
+        _require(x, torch.float32, "x")
+        C, n = x.shape
+        if out is None:
+            out = torch.empty((C, self.length(n)), dtype=torch.float32, device=x.device)
+        check(lib().stx_resample(self.handle, _ptr(x), C, n, _ptr(out), _stream(stream)))
+        return out
 
 
 # ------------------------------------------------------------ HTDemucs pre/post + split

@@ -642,3 +642,35 @@ def htdemucs():
     if _htd is None:
         _htd = _HTDemucs()
     return _htd
+
+
+class _Resample:
+    """st::resample_planar oracle (oracle/resample_oracle.c)."""
+
+    def __init__(self):
+        L = ctypes.CDLL(ORACLE_PATH)
+        L.orc_resample.restype = _i
+        L.orc_resample.argtypes = [_vp, _i, _i, _i, _i, _vp]
+        L.orc_resample_length.restype = ctypes.c_long
+        L.orc_resample_length.argtypes = [ctypes.c_long, _i, _i]
+        L.orc_resample_table.restype = None
+        L.orc_resample_table.argtypes = [_i, _i, _vp, ctypes.POINTER(ctypes.c_double)]
+        self.L = L
+
+    def table(self, src, dst):
+        t = np.zeros((1 << 15) + 2, np.float64)
+        half = ctypes.c_double()
+        self.L.orc_resample_table(src, dst, _np(t), ctypes.byref(half))
+        return t, half.value
+
+    def __call__(self, x, src, dst):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        C, n = x.shape
+        m = self.L.orc_resample_length(n, src, dst)
+        out = np.zeros((C, m), np.float32)
+        self.L.orc_resample(_np(x), n, C, src, dst, _np(out))
+        return out
+
+
+def resample():
+    return _Resample()
