@@ -25,7 +25,7 @@ namespace stx {
 namespace {
 
 constexpr int kTableN = 1 << 15;
-constexpr int kTapGroup = 4;
+constexpr int kTapGroup = 8;
 
 struct ResampleArgs {
     const float* in;                 // [C][n]
