@@ -513,7 +513,11 @@ typedef struct {
  * normalised over ne0 x ne1 x its channels with the biased variance. weight and bias (either
  * may be NULL) repeat into a; gelu != 0 applies GELU-erf last. a and dst must be contiguous
  * (dst may be a). workspace: device, 256-byte aligned, stx_group_norm_workspace_size() bytes,
- * no initialisation needed; calls that share a workspace must not run concurrently. */
+ * no initialisation needed; it keeps a generation number per group between calls, and calls
+ * that share a workspace must not run concurrently. Groups that fit on the device at once run
+ * as one grid-synchronised kernel whose blocks must all be resident together: do not run
+ * another grid-synchronised kernel concurrently on the same device (its waits are bounded: a
+ * block that cannot complete them writes NaN instead of hanging). */
 STX_API size_t     stx_group_norm_workspace_size(const stx_tensor* a, int n_groups);
 STX_API stx_status stx_group_norm(const stx_tensor* a, const stx_tensor* dst, int n_groups, float eps,
                                   const stx_tensor* weight, const stx_tensor* bias, int gelu, void* workspace,

@@ -20,8 +20,12 @@
 // ADD, MUL and x + h * s round after every operation, exactly as the separate ggml ops do, and
 // are bit-exact with that definition.
 #include <algorithm>
+#include <atomic>
+#include <chrono>
 #include <cmath>
+#include <mutex>
 #include <type_traits>
+#include <vector>
 
 #include "common.hpp"
 #include "tensor.hpp"
@@ -90,30 +94,25 @@ __device__ __forceinline__ float rcp_nr(float d) {
     return fmaf(r, fmaf(-d, r, 1.0f), r);
 }
 
-// erfcx(u) = exp(u^2) erfc(u) for u >= 0.7 in the form of Hastings' approximation
-// (Abramowitz & Stegun 7.1.26): erfcx(u) = t P(t), t = 1 / (1 + 0.47 u), one reciprocal. P has
-// degree 11, fitted for this library by weighted least squares in double, its coefficients
-// rounded to float one at a time from the top with the rest refitted (relative error 6.4e-10
-// on u >= 0.7).
-__device__ __forceinline__ float erfcx_tail(float u) {
-    const float t = rcp_nr(fmaf(0.47f, u, 1.f));
-    float p = 4.219519719e-02f;
-    p = fmaf(p, t, -1.974450797e-01f);
-    p = fmaf(p, t, 3.449501991e-01f);
-    p = fmaf(p, t, -2.401850075e-01f);
-    p = fmaf(p, t, 3.913874179e-02f);
-    p = fmaf(p, t, -5.485558510e-02f);
-    p = fmaf(p, t, 2.373995818e-02f);
-    p = fmaf(p, t, 9.893336892e-02f);
-    p = fmaf(p, t, 1.773130894e-01f);
-    p = fmaf(p, t, 2.358806431e-01f);
-    p = fmaf(p, t, 2.651691437e-01f);
-    p = fmaf(p, t, 2.651691139e-01f);
-    return t * p;
-}
-
-// gelu(x + dx) for |x| >= 1 (see gelu_erf_hl).
-__device__ __forceinline__ float gelu_tail(float x, float dx) {
+// gelu(x) = x Phi(x), Phi(x) = (1 + erf(x/sqrt2)) / 2, without a library erf/erfc/exp call and
+// without branches (~40 VALU instructions), within 9 ulp everywhere (a float32 simulation of
+// these exact steps, with the hardware exp2 and reciprocal taken 1 ulp off, against erfc in
+// double: at most 8.4 ulp on x < 0, 3 ulp on x > 1):
+//   Q = Phi(-|x|) = exp(-x^2/2) erfcx(|x|/sqrt2) / 2, and Phi(x) = Q for x < 0, 1 - Q otherwise.
+//   erfcx(u) = exp(u^2) erfc(u) = t P(t) with t = 1 / (1 + u/2) (the form of Hastings'
+//     approximation, Abramowitz & Stegun 7.1.26), one reciprocal; P has degree 12, fitted for
+//     this library over all u >= 0 by weighted least squares in double, its coefficients
+//     rounded to float one at a time from the top with the rest refitted.
+//   The exponential is 2^y with y = -(x + dx)^2 / (2 ln 2) formed as a head and tail (x^2 split
+//     exactly by an fma, the constant split in two floats), so it costs one ulp instead of
+//     ~x^2 ulps; 2^y = 2^n * 2^f, n = rint(y head), f in [-1/2, 1/2] on the hardware exp2.
+//   x > 10: Phi(x) = 1 to float precision; x < -15: gelu underflows (0 * x keeps -0 and NaN,
+//     and gives NaN at -inf like x * (1 + erf(x/sqrt2)) / 2 does).
+// gelu_erf_hl takes its argument as a float head x plus a small tail dx (x + dx is the value)
+// so that a fused producer can hand over a double result without rounding it first: in the
+// negative tail d ln gelu / d ln x ~ 1 + x^2, so one ulp of input rounding would become ~x^2
+// ulps of output error.
+__device__ __forceinline__ float gelu_erf_hl(float x, float dx) {
     // No contraction here: yh must be the rounded product that the fma residual refers to
     // (hipcc fuses a separate multiply and add by default, which would count the residual twice).
 #pragma clang fp contract(off)
@@ -123,43 +122,25 @@ __device__ __forceinline__ float gelu_tail(float x, float dx) {
     const float l = fmaf(x, x, -h);                       // x^2 = h + l exactly
     const float yh = h * C1;
     const float yl = fmaf(h, C1, -yh) + fmaf(h, C2, fmaf(2.f * x, dx, l) * C1);
-    const float n = rintf(yh);
+    const float n = rintf(fmaxf(yh, -200.f));             // |x| > 15 is selected away below
     const float e = ldexpf(__builtin_amdgcn_exp2f((yh - n) + yl), (int)n);
-    const float g = 0.5f * e * erfcx_tail(fabsf(x) * 0.70710678118654752440f);   // Phi(-|x|)
+    const float t = rcp_nr(fmaf(0.5f, fabsf(x) * 0.70710678118654752440f, 1.f));
+    float p = -3.032274731e-02f;
+    p = fmaf(p, t, 1.836623400e-01f);
+    p = fmaf(p, t, -4.440974593e-01f);
+    p = fmaf(p, t, 5.091602206e-01f);
+    p = fmaf(p, t, -2.279437780e-01f);
+    p = fmaf(p, t, 8.653792553e-03f);
+    p = fmaf(p, t, -6.725899875e-02f);
+    p = fmaf(p, t, -2.435513539e-03f);
+    p = fmaf(p, t, 8.313342929e-02f);
+    p = fmaf(p, t, 1.764382720e-01f);
+    p = fmaf(p, t, 2.468204200e-01f);
+    p = fmaf(p, t, 2.820952535e-01f);
+    p = fmaf(p, t, 2.820947766e-01f);
+    const float g = 0.5f * e * (t * p);                   // Phi(-|x|)
     const float ph = x < 0.f ? g : 1.f - g;
-    // x < -15 (including -inf, where x^2 overflows): 0 * x, keeping -0 and NaN.
     return x > 10.f ? x + dx : x < -15.f ? x * 0.f : fmaf(ph, dx, x * ph);
-}
-
-// gelu(x) = x Phi(x), Phi(x) = (1 + erf(x/sqrt2)) / 2, to a few ulp everywhere, without a
-// library erf/erfc/exp call (one short path per sign, ~12 VALU instructions for |x| < 1 and
-// ~42 beyond).
-//   |x| < 1:  erf(x/sqrt2) = x Q(x^2), Q of degree 5 fitted for this library (relative error
-//             of Phi 1.6e-9 on |x| <= 1).
-//   |x| >= 1: Phi(-|x|) = exp(-x^2/2) erfcx(|x|/sqrt2) / 2; Phi(x) is that or 1 minus it. The
-//             exponential is 2^y with y = -(x + dx)^2 / (2 ln 2) formed as a head and tail
-//             (x^2 split exactly by an fma, the constant split in two floats), so it costs one
-//             ulp instead of ~x^2 ulps; 2^y = 2^n * 2^f, n = rint(y head), f in [-1/2, 1/2] on
-//             the hardware exp2.
-//   x > 10:   Phi(x) = 1 to float precision; x < -15: gelu underflows (0 * x keeps -0, NaN).
-// gelu_erf_hl takes its argument as a float head x plus a small tail dx (x + dx is the value)
-// so that a fused producer can hand over a double result without rounding it first: in the
-// negative tail d ln gelu / d ln x ~ 1 + x^2, so one ulp of input rounding would become ~x^2
-// ulps of output error.
-__device__ __forceinline__ float gelu_erf_hl(float x, float dx) {
-    const float a = fabsf(x);
-    if (a < 1.f) {
-        const float s = x * x;
-        float q = -1.532521674e-05f;
-        q = fmaf(q, s, 2.270149562e-04f);
-        q = fmaf(q, s, -2.372696996e-03f);
-        q = fmaf(q, s, 1.994666085e-02f);
-        q = fmaf(q, s, -1.329807192e-01f);
-        q = fmaf(q, s, 7.978845835e-01f);
-        const float ph = 0.5f * fmaf(x, q, 1.f);
-        return fmaf(ph, dx, x * ph);
-    }
-    return gelu_tail(x, dx);
 }
 
 __device__ __forceinline__ float gelu_erf(float x) { return gelu_erf_hl(x, 0.f); }
@@ -714,13 +695,13 @@ __device__ __forceinline__ void group_span(const GroupNormArgs& a, int gt, long 
 }
 
 // Loads this thread's values of chunk [lo, hi) of base: float4 k covers positions
-// lo + (k * 256 + tid) * 4 .. +3.
-template <int VEC>
+// lo + (k * NT + tid) * 4 .. +3 (NT threads per block).
+template <int VEC, int NT = 256>
 __device__ __forceinline__ void gn_load(const GroupNormArgs& a, const float* base, unsigned lo, unsigned hi,
                                         float (&v)[4 * VEC], bool (&ok)[4 * VEC]) {
 #pragma unroll
     for (int k = 0; k < VEC; k++) {
-        const unsigned p = lo + (k * 256 + threadIdx.x) * 4;
+        const unsigned p = lo + (k * NT + threadIdx.x) * 4;
         if (a.vec && p + 3 < hi) {
             const float4 q = *reinterpret_cast<const float4*>(base + p);
             v[4 * k] = q.x;
@@ -800,7 +781,7 @@ __device__ __forceinline__ float affine_at(const Affine& f, long long c, unsigne
 
 // Affine parameters of this thread's elements: channel c and (i0, i1) inside its plane of
 // element p, advanced element by element.
-template <int AK, int VEC>
+template <int AK, int VEC, int NT = 256>
 __device__ __forceinline__ void gn_affine(const GroupNormArgs& a, unsigned lo, long long c0, long long i3,
                                           const bool (&ok)[4 * VEC], float (&wv)[4 * VEC], float (&bv)[4 * VEC]) {
     if constexpr (AK == AFF_CHANNEL) {
@@ -809,7 +790,7 @@ __device__ __forceinline__ void gn_affine(const GroupNormArgs& a, unsigned lo, l
             // group (clamped to a valid channel, unconditional), then a selection per element.
 #pragma unroll
             for (int k = 0; k < VEC; k++) {
-                const unsigned p = lo + (k * 256 + threadIdx.x) * 4;
+                const unsigned p = lo + (k * NT + threadIdx.x) * 4;
                 const unsigned cp = fast_div(p, a.plane, a.rplane), q = p - cp * a.plane;
                 const long long cl = a.ne2 - 1;
                 const long long c = min(c0 + cp, cl), c1 = min(c0 + cp + 1, cl);
@@ -827,7 +808,7 @@ __device__ __forceinline__ void gn_affine(const GroupNormArgs& a, unsigned lo, l
     }
 #pragma unroll
     for (int k = 0; k < VEC; k++) {
-        const unsigned p = lo + (k * 256 + threadIdx.x) * 4;
+        const unsigned p = lo + (k * NT + threadIdx.x) * 4;
         long long c = 0;
         unsigned i0 = 0, i1 = 0;
         if constexpr (AK == AFF_NE0) {
@@ -856,13 +837,13 @@ __device__ __forceinline__ void gn_affine(const GroupNormArgs& a, unsigned lo, l
     }
 }
 
-template <bool GELU, int VEC>
+template <bool GELU, int VEC, int NT = 256>
 __device__ __forceinline__ void gn_store(const GroupNormArgs& a, float* yg, unsigned lo, unsigned hi, double mean,
                                          double rstd, const float (&v)[4 * VEC], const bool (&ok)[4 * VEC],
                                          const float (&wv)[4 * VEC], const float (&bv)[4 * VEC]) {
 #pragma unroll 1
     for (int k = 0; k < VEC; k++) {
-        const unsigned p = lo + (k * 256 + threadIdx.x) * 4;
+        const unsigned p = lo + (k * NT + threadIdx.x) * 4;
         if (p >= hi) continue;
         float o[4];
 #pragma unroll
@@ -918,6 +899,172 @@ __global__ __launch_bounds__(256) void gn_apply_kernel(GroupNormArgs a) {
     double mean, rstd;
     gn_stats(a, gt, count, a.shift[gt], red, mean, rstd);     // shift from pass 1
     gn_store<GELU, VEC>(a, a.y + begin, lo, hi, mean, rstd, v, ok, wv, bv);
+}
+
+// Sums of two doubles over an NT-thread block: wave sums, then the wave totals added in wave
+// order by every thread (the same order in every block). red holds 2 * NT / 64 doubles.
+template <int NT>
+__device__ __forceinline__ void block_sum2_n(double& a, double& b, double* red) {
+    constexpr int W = NT / kWave;
+    a = group_sum<kWave>(a);
+    b = group_sum<kWave>(b);
+    __syncthreads();
+    if (threadIdx.x % kWave == 0) {
+        red[threadIdx.x / kWave] = a;
+        red[W + threadIdx.x / kWave] = b;
+    }
+    __syncthreads();
+    a = 0.0;
+    b = 0.0;
+#pragma unroll
+    for (int w = 0; w < W; w++) {
+        a += red[w];
+        b += red[W + w];
+    }
+}
+
+// Single-pass GroupNorm (gn_fused_kernel): when every group's blocks fit on the device at once,
+// each block keeps its chunk of x in registers and publishes its partial sums; block 0 of the
+// group waits for all of them (one record per block, polled by one thread each: no
+// same-address atomics), adds them up in block order and publishes the totals; the other
+// blocks wait for the totals and write y from the registers. Every block thus normalises with
+// the same statistics bit for bit, x is read from HBM once and there is one launch.
+// Records are (s1, s2, tag) with tag = a 64-bit hash of s1, s2 and the call's key (token << 32 |
+// gen + 1): the token is a per-call random number from the host, gen a per-group generation
+// number kept in the workspace that block 0 advances once every block has read it. A reader
+// takes a record only when its tag matches the values it read under the current key, so the
+// three words need no write ordering (a torn or stale record fails the check), graph replays
+// of one call (same token) wait for a new gen each time, and neither a record of another call
+// nor garbage in a fresh workspace passes: the workspace needs no initialisation or clearing.
+// Every wait is bounded: a block that gives up (which needs blocks that never become
+// resident, e.g. two such kernels sharing the device) writes NaN instead of hanging.
+constexpr int kGnFusedThreads = 512;
+constexpr int kGnFusedMaxBlocks = 512;               // per group
+constexpr int kGnFusedMaxGroups = 8;
+constexpr int kGnStatCopies = 8;                     // waiters poll copy (block % 8)
+constexpr int kGnStatStride = 128;                   // unsigned long longs between copies (1 KB)
+constexpr unsigned kGnSpinLimit = 1u << 18;          // polls of about 1 us each
+
+struct GnSync {
+    unsigned* gen;                   // [kGnFusedMaxGroups]
+    unsigned long long* stat;        // [kGnStatCopies][kGnStatStride]: group g's totals record at 3g
+    unsigned long long* part;        // [kGnFusedMaxGroups][kGnFusedMaxBlocks][3]: partial sums records
+    unsigned token;
+    unsigned spin_limit;
+};
+
+// Cross-block words are device-scope relaxed atomics, which gfx950 performs at the device's
+// coherence point (sc1), past the XCD's own L2: no L2 write-back or invalidation, which a
+// release/acquire pair would cost per block.
+__device__ __forceinline__ void sync_store(unsigned long long* p, unsigned long long v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long sync_load(const unsigned long long* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// MurmurHash3's 64-bit finaliser.
+__device__ __forceinline__ unsigned long long fmix64(unsigned long long k) {
+    k ^= k >> 33;
+    k *= 0xff51afd7ed558ccdull;
+    k ^= k >> 33;
+    k *= 0xc4ceb9fe1a85ec53ull;
+    k ^= k >> 33;
+    return k;
+}
+__device__ __forceinline__ unsigned long long record_tag(unsigned long long a, unsigned long long b,
+                                                         unsigned long long key) {
+    return fmix64(a ^ fmix64(b ^ fmix64(key)));
+}
+// Publishes (s1, s2) at r[0..2] under key.
+__device__ __forceinline__ void record_store(unsigned long long* r, double s1, double s2, unsigned long long key) {
+    const unsigned long long a = (unsigned long long)__double_as_longlong(s1);
+    const unsigned long long b = (unsigned long long)__double_as_longlong(s2);
+    sync_store(r, a);
+    sync_store(r + 1, b);
+    sync_store(r + 2, record_tag(a, b, key));
+}
+// Polls r (at most limit times) until it holds a record under key; false if it never did.
+__device__ __forceinline__ bool record_wait(const unsigned long long* r, unsigned long long key, unsigned limit,
+                                            double& s1, double& s2) {
+    for (unsigned spins = 0;;) {
+        const unsigned long long a = sync_load(r), b = sync_load(r + 1), h = sync_load(r + 2);
+        if (h == record_tag(a, b, key)) {
+            s1 = __longlong_as_double((long long)a);
+            s2 = __longlong_as_double((long long)b);
+            return true;
+        }
+        if (++spins > limit) return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+template <int AK, bool GELU, int VEC>
+__global__ __launch_bounds__(kGnFusedThreads) void gn_fused_kernel(GroupNormArgs a, GnSync f) {
+    constexpr int NT = kGnFusedThreads;
+    constexpr unsigned CH = NT * 4 * VEC;
+    __shared__ double red[2 * NT / kWave];
+    __shared__ double tot[2];
+    const int gt = (int)blockIdx.y;
+    long long begin, c0, i3;
+    unsigned count;
+    group_span(a, gt, begin, count, c0, i3);
+    const unsigned lo = blockIdx.x * CH;
+    if (lo >= count) return;                                   // past a short group: not one of its blocks
+    const unsigned hi = min(lo + CH, count);
+    const int nch = (int)((count + CH - 1) / CH);
+    const float* xg = a.x + begin;
+    const unsigned gen1 = __hip_atomic_load(f.gen + gt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    const unsigned long long key = (unsigned long long)f.token << 32 | gen1;
+    float v[4 * VEC], wv[4 * VEC], bv[4 * VEC];
+    bool ok[4 * VEC];
+    gn_load<VEC, NT>(a, xg, lo, hi, v, ok);
+    gn_affine<AK, VEC, NT>(a, lo, c0, i3, ok, wv, bv);
+    const double shift = (double)xg[0];                        // read before any block writes y
+    double s1 = 0.0, s2 = 0.0;
+#pragma unroll
+    for (int k = 0; k < 4 * VEC; k++) {
+        const double d = ok[k] ? (double)v[k] - shift : 0.0;
+        s1 += d;
+        s2 += d * d;
+    }
+    block_sum2_n<NT>(s1, s2, red);
+    unsigned long long* part = f.part + 3 * (size_t)gt * kGnFusedMaxBlocks;
+    bool late = false;
+    if (blockIdx.x != 0) {
+        if (threadIdx.x == 0) {
+            record_store(part + 3 * blockIdx.x, s1, s2, key);
+            double t1 = 0.0, t2 = 0.0;                         // the group's totals, from block 0
+            late = !record_wait(f.stat + (blockIdx.x % kGnStatCopies) * kGnStatStride + 3 * gt, key, f.spin_limit,
+                                t1, t2);
+            tot[0] = t1;
+            tot[1] = t2;
+        }
+    } else {
+        // Block 0 collects: thread t waits for the records of blocks t, t + NT, ... and adds
+        // them in that order (block 0's own sums first), then the block adds the threads' sums
+        // in thread order and publishes the totals, one record per copy.
+        double p1 = threadIdx.x == 0 ? s1 : 0.0, p2 = threadIdx.x == 0 ? s2 : 0.0;
+        for (int b = threadIdx.x == 0 ? NT : (int)threadIdx.x; b < nch && !late; b += NT) {
+            double q1 = 0.0, q2 = 0.0;
+            late = !record_wait(part + 3 * b, key, f.spin_limit, q1, q2);
+            p1 += q1;
+            p2 += q2;
+        }
+        block_sum2_n<NT>(p1, p2, red);
+        if (threadIdx.x == 0) {
+            tot[0] = p1;
+            tot[1] = p2;
+#pragma unroll
+            for (int c = 0; c < kGnStatCopies; c++) record_store(f.stat + c * kGnStatStride + 3 * gt, p1, p2, key);
+            // Every block has read gen before it published its record.
+            __hip_atomic_store(f.gen + gt, gen1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    const bool timed_out = __syncthreads_or(late);
+    const double N = (double)count, dm = tot[0] / N;
+    const double mean = timed_out ? __builtin_nan("") : shift + dm;
+    const double rstd = 1.0 / sqrt(fmax(tot[1] / N - dm * dm, 0.0) + (double)a.eps);
+    gn_store<GELU, VEC, NT>(a, a.y + begin, lo, hi, mean, rstd, v, ok, wv, bv);
 }
 
 // ----------------------------------------------------------------------------- ROPE
@@ -1210,11 +1357,21 @@ Affine make_affine(const stx_tensor* t, const stx_tensor* x, const char* what) {
 }
 
 struct GnPlan {
-    long long cpg, groups, groups_total, chunks_partial, chunks_apply;
+    long long cpg, groups, groups_total, span, chunks_partial, chunks_apply;
     int pvec;                                            // pass 1 width
     bool wide;                                           // pass 2 with kGnVecApplyWide
-    size_t shift_off, part_off, bytes;                   // workspace layout
+    size_t sync_off, shift_off, part_off, bytes;         // workspace layout
 };
+
+// The single-pass kernel's area sits at offset 0 of every group-norm workspace with a fixed
+// size, so that a workspace shared by calls of different shapes keeps each group slot's
+// generation number consistent: [8 KB) totals records, 8 per group at 1 KB apart | [256 B)
+// generation numbers | partial sums records, 3 words per block.
+constexpr size_t kGnSyncStat = 0, kGnSyncGen = sizeof(unsigned long long) * kGnStatCopies * kGnStatStride,
+                 kGnSyncPart = kGnSyncGen + 256;
+constexpr size_t kGnSyncBytes =
+    (kGnSyncPart + sizeof(unsigned long long) * 3 * kGnFusedMaxGroups * kGnFusedMaxBlocks + 255) / 256 * 256;
+static_assert(3 * kGnFusedMaxGroups <= kGnStatStride && 4 * kGnFusedMaxGroups <= 256, "group-norm sync area layout");
 
 GnPlan gn_plan(const stx_tensor* a, int n_groups) {
     GnPlan p{};
@@ -1222,6 +1379,7 @@ GnPlan gn_plan(const stx_tensor* a, int n_groups) {
     p.groups = (a->ne[2] + p.cpg - 1) / p.cpg;
     p.groups_total = p.groups * a->ne[3];
     const long long span = p.cpg * a->ne[0] * a->ne[1];
+    p.span = span;
     p.pvec = gn_partial_vec(span);
     p.chunks_partial = (span + 1024LL * p.pvec - 1) / (1024LL * p.pvec);
     p.wide = (span + gn_chunk<kGnVecApplyWide>() - 1) / gn_chunk<kGnVecApplyWide>() * p.groups_total >= kGnWideBlocks;
@@ -1229,14 +1387,70 @@ GnPlan gn_plan(const stx_tensor* a, int n_groups) {
     p.chunks_apply = (span + cha - 1) / cha;
     const size_t g = (size_t)std::max<long long>(1, p.groups_total);
     auto up = [](size_t v) { return (v + 255) / 256 * 256; };
-    p.shift_off = 0;
-    p.part_off = up(sizeof(double) * g);
+    p.sync_off = 0;
+    p.shift_off = kGnSyncBytes;
+    p.part_off = p.shift_off + up(sizeof(double) * g);
     p.bytes = p.part_off + up(sizeof(double) * 2 * g * (size_t)std::max<long long>(1, p.chunks_partial));
     return p;
 }
 
+// A per-call random number: murmur3's 32-bit finaliser of a call counter offset by a
+// per-process seed from the clock.
+unsigned gn_call_token() {
+    static const unsigned seed = (unsigned)std::chrono::steady_clock::now().time_since_epoch().count();
+    static std::atomic<unsigned> calls{0};
+    unsigned h = seed + 0x9e3779b9u * calls.fetch_add(1, std::memory_order_relaxed);
+    h ^= h >> 16;
+    h *= 0x85ebca6bu;
+    h ^= h >> 13;
+    h *= 0xc2b2ae35u;
+    h ^= h >> 16;
+    return h;
+}
+
+// Blocks of `kernel` (kGnFusedThreads threads) that the current device holds at once.
+int resident_blocks(const void* kernel) {
+    struct Entry {
+        const void* k;
+        int dev, blocks;
+    };
+    static std::mutex mu;
+    static std::vector<Entry> cache;
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    std::lock_guard<std::mutex> lock(mu);
+    for (const Entry& e : cache)
+        if (e.k == kernel && e.dev == dev) return e.blocks;
+    int cus = 0, per_cu = 0;
+    hip_check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
+    hip_check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kGnFusedThreads, 0),
+              "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+    cache.push_back({kernel, dev, cus * per_cu});
+    return cus * per_cu;
+}
+
+// Single pass when the groups fit: at most kGnFusedMaxGroups of them, each in at most
+// kGnFusedMaxBlocks blocks, all blocks resident together. VEC is the smallest width that
+// fits (more blocks, shorter per-thread chains). Returns false to take the two passes.
+template <int AK, bool GELU, int VEC>
+bool try_fused(const GroupNormArgs& g, const GnPlan& p, const GnSync& sync, hipStream_t s) {
+    const long long ch = (long long)kGnFusedThreads * 4 * VEC;
+    const long long nch = (p.span + ch - 1) / ch;
+    if (nch > kGnFusedMaxBlocks) return false;
+    const void* k = reinterpret_cast<const void*>(&gn_fused_kernel<AK, GELU, VEC>);
+    if (nch * p.groups_total > resident_blocks(k)) return false;
+    hipLaunchKernelGGL((gn_fused_kernel<AK, GELU, VEC>), dim3((unsigned)nch, (unsigned)p.groups_total),
+                       dim3(kGnFusedThreads), 0, s, g, sync);
+    launch_check("gn_fused_kernel");
+    return true;
+}
+
 template <int AK, bool GELU>
-void launch_group_norm(GroupNormArgs g, const GnPlan& p, hipStream_t s) {
+void launch_group_norm(GroupNormArgs g, const GnPlan& p, const GnSync& sync, hipStream_t s) {
+    if (p.groups_total <= kGnFusedMaxGroups &&
+        (try_fused<AK, GELU, 1>(g, p, sync, s) || try_fused<AK, GELU, 2>(g, p, sync, s) ||
+         try_fused<AK, GELU, 4>(g, p, sync, s)))
+        return;
     g.chunks = (int)p.chunks_partial;
     g.pchunk = 1024 * p.pvec;
     const dim3 grid1((unsigned)p.chunks_partial, (unsigned)p.groups_total);
@@ -1439,6 +1653,12 @@ STX_API stx_status stx_group_norm(const stx_tensor* a, const stx_tensor* dst, in
         g.w = w;
         g.b = b;
         char* ws = static_cast<char*>(workspace);
+        GnSync sync;
+        sync.gen = reinterpret_cast<unsigned*>(ws + p.sync_off + kGnSyncGen);
+        sync.stat = reinterpret_cast<unsigned long long*>(ws + p.sync_off + kGnSyncStat);
+        sync.part = reinterpret_cast<unsigned long long*>(ws + p.sync_off + kGnSyncPart);
+        sync.token = gn_call_token();
+        sync.spin_limit = kGnSpinLimit;
         g.shift = reinterpret_cast<double*>(ws + p.shift_off);
         g.part = reinterpret_cast<double*>(ws + p.part_off);
         g.ne0 = (unsigned)ta.ne[0];
@@ -1461,14 +1681,14 @@ STX_API stx_status stx_group_norm(const stx_tensor* a, const stx_tensor* dst, in
         };
         const int ak = fits(AFF_CHANNEL) ? AFF_CHANNEL : fits(AFF_NE0) ? AFF_NE0 : AFF_GENERAL;
         if (ak == AFF_CHANNEL) {
-            if (gelu) launch_group_norm<AFF_CHANNEL, true>(g, p, s);
-            else launch_group_norm<AFF_CHANNEL, false>(g, p, s);
+            if (gelu) launch_group_norm<AFF_CHANNEL, true>(g, p, sync, s);
+            else launch_group_norm<AFF_CHANNEL, false>(g, p, sync, s);
         } else if (ak == AFF_NE0) {
-            if (gelu) launch_group_norm<AFF_NE0, true>(g, p, s);
-            else launch_group_norm<AFF_NE0, false>(g, p, s);
+            if (gelu) launch_group_norm<AFF_NE0, true>(g, p, sync, s);
+            else launch_group_norm<AFF_NE0, false>(g, p, sync, s);
         } else {
-            if (gelu) launch_group_norm<AFF_GENERAL, true>(g, p, s);
-            else launch_group_norm<AFF_GENERAL, false>(g, p, s);
+            if (gelu) launch_group_norm<AFF_GENERAL, true>(g, p, sync, s);
+            else launch_group_norm<AFF_GENERAL, false>(g, p, sync, s);
         }
     });
 }
