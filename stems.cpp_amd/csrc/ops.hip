@@ -111,19 +111,10 @@ __device__ __forceinline__ float rcp_nr(float d) {
 // gelu_erf_hl takes its argument as a float head x plus a small tail dx (x + dx is the value)
 // so that a fused producer can hand over a double result without rounding it first: in the
 // negative tail d ln gelu / d ln x ~ 1 + x^2, so one ulp of input rounding would become ~x^2
-// ulps of output error.
-__device__ __forceinline__ float gelu_erf_hl(float x, float dx) {
-    // No contraction here: yh must be the rounded product that the fma residual refers to
-    // (hipcc fuses a separate multiply and add by default, which would count the residual twice).
-#pragma clang fp contract(off)
-    constexpr float C1 = -0x1.715476p-1f;                 // -1/(2 ln 2) = C1 + C2 to 3e-16
-    constexpr float C2 = -0x1.4ae0cp-27f;
-    const float h = x * x;
-    const float l = fmaf(x, x, -h);                       // x^2 = h + l exactly
-    const float yh = h * C1;
-    const float yl = fmaf(h, C1, -yh) + fmaf(h, C2, fmaf(2.f * x, dx, l) * C1);
-    const float n = rintf(fmaxf(yh, -200.f));             // |x| > 15 is selected away below
-    const float e = ldexpf(__builtin_amdgcn_exp2f((yh - n) + yl), (int)n);
+// ulps of output error; gelu_erf_d takes the double itself.
+
+// Phi(-|x|) = e erfcx(|x|/sqrt2) / 2, given e = exp(-x^2/2).
+__device__ __forceinline__ float gelu_phi_neg(float x, float e) {
     const float t = rcp_nr(fmaf(0.5f, fabsf(x) * 0.70710678118654752440f, 1.f));
     float p = -3.032274731e-02f;
     p = fmaf(p, t, 1.836623400e-01f);
@@ -138,9 +129,35 @@ __device__ __forceinline__ float gelu_erf_hl(float x, float dx) {
     p = fmaf(p, t, 2.468204200e-01f);
     p = fmaf(p, t, 2.820952535e-01f);
     p = fmaf(p, t, 2.820947766e-01f);
-    const float g = 0.5f * e * (t * p);                   // Phi(-|x|)
+    return 0.5f * e * (t * p);
+}
+
+__device__ __forceinline__ float gelu_erf_hl(float x, float dx) {
+    // No contraction here: yh must be the rounded product that the fma residual refers to
+    // (hipcc fuses a separate multiply and add by default, which would count the residual twice).
+#pragma clang fp contract(off)
+    constexpr float C1 = -0x1.715476p-1f;                 // -1/(2 ln 2) = C1 + C2 to 3e-16
+    constexpr float C2 = -0x1.4ae0cp-27f;
+    const float h = x * x;
+    const float l = fmaf(x, x, -h);                       // x^2 = h + l exactly
+    const float yh = h * C1;
+    const float yl = fmaf(h, C1, -yh) + fmaf(h, C2, fmaf(2.f * x, dx, l) * C1);
+    const float n = rintf(fmaxf(yh, -200.f));             // |x| > 15 is selected away below
+    const float g = gelu_phi_neg(x, ldexpf(__builtin_amdgcn_exp2f((yh - n) + yl), (int)n));
     const float ph = x < 0.f ? g : 1.f - g;
     return x > 10.f ? x + dx : x < -15.f ? x * 0.f : fmaf(ph, dx, x * ph);
+}
+
+// gelu of a double argument (a fused producer's result before rounding), the same
+// approximation with the exponent -t^2 / (2 ln 2) formed in double instead of as a float head
+// and tail, and one rounding of t Phi(t) at the end.
+__device__ __forceinline__ float gelu_erf_d(double t) {
+    const float x = (float)t;
+    const double y = t * t * -0x1.71547652b82fep-1;
+    const double n = rint(fmax(y, -200.0));               // |t| > 15 is selected away below
+    const float g = gelu_phi_neg(x, ldexpf(__builtin_amdgcn_exp2f((float)(y - n)), (int)n));
+    const float ph = x < 0.f ? g : 1.f - g;
+    return x > 10.f ? x : x < -15.f ? x * 0.f : (float)(t * (double)ph);
 }
 
 __device__ __forceinline__ float gelu_erf(float x) { return gelu_erf_hl(x, 0.f); }
@@ -849,9 +866,8 @@ __device__ __forceinline__ void gn_store(const GroupNormArgs& a, float* yg, unsi
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const double t = fma(((double)v[4 * k + j] - mean) * rstd, (double)wv[4 * k + j], (double)bv[4 * k + j]);
-            const float f = (float)t;
-            if constexpr (GELU) o[j] = gelu_erf_hl(f, (float)(t - (double)f));
-            else o[j] = f;
+            if constexpr (GELU) o[j] = gelu_erf_d(t);
+            else o[j] = (float)t;
         }
         if (a.vec && p + 3 < hi) {
             *reinterpret_cast<float4*>(yg + p) = make_float4(o[0], o[1], o[2], o[3]);
