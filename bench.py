@@ -6,7 +6,7 @@ N(0, 1) from a seed, for each (C, T) in (48, 85995), (96, 21499), (192, 5375), (
      stx_group_norm (src/htdemucs.cpp:114-128,136);
   2. GLU over 2C channels of a [1, 2C, T] input, then LayerScale broadcast MUL plus residual
      ADD, x + glu(h) * scale[C], one call: stx_glu_mul_add (src/htdemucs.cpp:105-110,137-139).
-The 8 calls (12 kernels) of a step are captured once into a HIP graph per buffer set and
+The 8 calls (8 kernels) of a step are captured once into a HIP graph per buffer set and
 replayed on one stream; buffer sets rotate so that more than 512 MB is touched between reuses,
 larger than the 256 MB Infinity Cache: cold-cache numbers.
 
@@ -16,7 +16,7 @@ its output once): GroupNorm+affine 8, GELU 8, GLU 12 and LayerScale MUL + residu
 per element of [C, T] (40 in all, plus the parameters). Fusion moves fewer bytes than that:
 config.bytes_moved_per_step gives the minimum these kernels move (24 per element).
 roofline: the op with the largest share of the step (GroupNorm+GELU): its algorithmic bytes
-(8 per element) / its duration (gn_partial_kernel + gn_apply_kernel), from a graph of instances
+(8 per element) / its duration (gn_fused_kernel, one grid-synchronised pass), from a graph of instances
 of that op on more than 512 MB of distinct buffers (cold, like the step) replayed between two
 HIP events on the stream the kernels run on. traffic: HBM bytes of that op
 per step measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter
@@ -158,7 +158,7 @@ def run_ops(args, torch, stx, dev):
     stream = torch.cuda.Stream()
     torch.cuda.synchronize()
 
-    # One graph per buffer set: the 8 calls (12 kernels) of a step.
+    # One graph per buffer set: the 8 calls (8 kernels) of a step.
     graphs = []
     with torch.cuda.stream(stream):
         for k in range(copies):
@@ -220,7 +220,7 @@ def run_ops(args, torch, stx, dev):
     dom_bytes = sum(nbytes[dom])
     achieved = dom_bytes / (share[dom] * 1e-6) / 1e9
     step_bytes = sum(sum(v) for v in op_bytes().values())
-    kernel_names = {"gn": "group_norm+affine+gelu (gn_partial_kernel + gn_apply_kernel<channel,gelu>)",
+    kernel_names = {"gn": "group_norm+affine+gelu (gn_fused_kernel<channel,gelu>: one grid-synchronised pass)",
                     "glu_scale_residual": "glu + layer scale + residual (ew_flat_kernel<GLU_MUL_ADD>)"}
     res = {
         "value": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
@@ -230,7 +230,7 @@ def run_ops(args, torch, stx, dev):
             "shapes_CT": [list(s) for s in SHAPES],
             "bytes_per_step": step_bytes,
             "bytes_moved_per_step": sum(sum(v) for v in moved_bytes().values()),
-            "execution": "one HIP graph per step (12 kernels), one stream",
+            "execution": "one HIP graph per step (8 kernels), one stream",
             "buffer_sets_rotated": copies,
             "input": "N(0,1) fp32 from seed 2025",
         },

@@ -44,7 +44,7 @@ HTDEMUCS_CT = [(48, 85995), (96, 21499), (192, 5375), (384, 1344), (6, 85995)]
 
 
 # ------------------------------------------------------------------- GROUP_NORM
-@pytest.mark.parametrize("C,T", HTDEMUCS_CT + [(47, 85993)])    # last: wide pass 2 on unaligned rows
+@pytest.mark.parametrize("C,T", HTDEMUCS_CT + [(47, 85993)])    # last: odd-sized group (no float4 path)
 @pytest.mark.parametrize("gelu", [False, True])
 def test_group_norm_rows_h1(device, ops, C, T, gelu):
     """group_norm_rows with H == 1 (src/htdemucs.cpp:117-119,127): G = 1 over [T, 1, C], * w[C] + b[C]."""
@@ -99,7 +99,7 @@ def test_group_norm_in_place_and_deterministic(device, ops):
 def test_group_norm_shapes_share_a_workspace(device, ops, gelu):
     """Large groups, many groups and batched groups: one workspace, filled with garbage first,
     serves all of them in turn, twice (no initialisation needed; the single-pass kernel's
-    generation numbers and flags in it stay consistent across shapes)."""
+    generation numbers and records in it stay consistent across shapes)."""
     import torch
     ws = torch.full((1 << 17,), -7.25, device=device)
     shapes = [((96, 1, 85995), 1), ((1000, 1, 8192), 1000), ((48, 1, 85995), 1), ((8, 3, 1, 999), 4)]
@@ -111,6 +111,32 @@ def test_group_norm_shapes_share_a_workspace(device, ops, gelu):
             assert stx.group_norm_workspace_size(x, G) <= ws.numel() * 4
             y = host(stx.group_norm(x, G, 1e-5, w, b, gelu=gelu, workspace=ws))
             assert rel_err(y, ops.group_norm(host(x), G, 1e-5, host(w), host(b), gelu=gelu)) <= TOL
+
+
+def test_group_norm_graph_replays(device, ops):
+    """Replays of one captured call (one call token) on new data each time: the single-pass
+    kernel must wait for a new generation of records per replay, not take the last replay's."""
+    import torch
+    C, T = 96, 21499
+    x = randn(device, (C, 1, T), 40)
+    w, b = randn(device, (C, 1, 1), 41), randn(device, (C, 1, 1), 42)
+    y = torch.empty_like(x)
+    ws = stx.workspace(stx.group_norm_workspace_size(x, 1), device)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        stx.group_norm(x, 1, 1e-5, w, b, gelu=True, out=y, workspace=ws, stream=s)
+        s.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            stx.group_norm(x, 1, 1e-5, w, b, gelu=True, out=y, workspace=ws, stream=s)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        xn = randn(device, (C, 1, T), 50 + rep, 1.0 + rep, 0.1 * rep)
+        x.copy_(xn)
+        torch.cuda.synchronize()
+        g.replay()
+        want = ops.group_norm(host(xn), 1, 1e-5, host(w), host(b), gelu=True)
+        assert rel_err(host(y), want) <= TOL
 
 
 def test_group_norm_errors(device):
