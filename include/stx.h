@@ -413,7 +413,9 @@ STX_API size_t stx_htdemucs_norm_workspace_size(int64_t n);
  * stx_htdemucs_spec writes it); mag is device [2C][F][T] with mag[2c] = re and mag[2c+1] = im,
  * each (v - mean) / (1e-5 + sd) over all 2 C F T values (mean_of and the unbiased std_of,
  * :293-302, in double). stats gets {mean, sd}. workspace: device, 16-byte aligned,
- * stx_htdemucs_norm_workspace_size(2 C F T) bytes; calls that share one must not overlap. */
+ * stx_htdemucs_norm_workspace_size(2 C F T) bytes, no initialisation needed; calls that share one
+ * must not overlap. A segment that fits on the device at once is normalised by one
+ * grid-synchronised kernel (do not run another such kernel concurrently on the device). */
 STX_API stx_status stx_htdemucs_cac_normalize(const float* spec, int channels, int n_bins, int n_frames, float* mag,
                                               double* stats, void* workspace, size_t workspace_bytes,
                                               stx_stream stream);

@@ -9,10 +9,13 @@
 //   * split(): TensorChunk padding (:552-561), triangular weights (:566-573), center_trim and
 //     the weighted overlap-add (:589-607).
 //
-// The moments (mean_of / std_of, :293-302: double sums, unbiased std) take two kernels:
-// pass 1 writes one (sum d, sum d^2) pair in double per 8192 floats, with d = x - x[0] so
-// no cancellation occurs; pass 2 has every block add all pairs in one fixed order (so every
-// block gets bit-identical statistics) and then normalise its own chunk. The split's
+// The moments (mean_of / std_of, :293-302: double sums of d = x - x[0], so no cancellation
+// occurs, and the unbiased std) and the normalisation run as one grid-synchronised kernel when
+// the input fits in the registers of blocks that are all resident at once (one segment's
+// spectrum or waveform): each block loads its chunk once, the blocks exchange their partial
+// sums (grid_sync.hpp) and normalise from registers. Otherwise (the whole mix of separate())
+// three kernels: pass 1 writes one (sum d, sum d^2) pair in double per 8192 floats, one block
+// adds them in a fixed order into {mean, sd}, and a third kernel normalises. The split's
 // overlap-add is in gather form: each output sample sums, in chunk order and in float like the
 // reference's `out += weight * seg_out`, the <= ceil(seg / stride) chunks covering it, and
 // divides by the summed weights, so it is bit-exact.
@@ -22,6 +25,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "grid_sync.hpp"
 
 namespace stx {
 namespace {
@@ -169,6 +173,92 @@ __global__ __launch_bounds__(256) void normalize_kernel(const float* x, float* y
         for (int k = 0; k < kNormPer; k++) {
             const long long e = e0 + 256LL * k;
             if (e < count) y[e] = (float)(((double)v[k] - mean) / den);
+        }
+    }
+}
+
+// One launch of moments + normalise for NORM_CAC / NORM_FLAT: x is n floats (CAC: the complex64
+// spectrum [C][ft] read as 2 C ft floats), VEC float4 per thread in chunks of kGridThreads * 4 *
+// VEC floats. Same statistics formulas as moments_final_kernel and the same per-element division
+// as normalize_kernel; block 0 writes {mean, sd} to stats.
+template <int KIND, int VEC>
+__global__ __launch_bounds__(kGridThreads) void norm_fused_kernel(const float* x, float* y, long long n, long long ft,
+                                                                  double* stats, GridSync f) {
+    constexpr int NT = kGridThreads;
+    constexpr long long CH = NT * 4 * VEC;
+    __shared__ double red[2 * NT / 64];
+    __shared__ double tot[2];
+    const long long lo = (long long)blockIdx.x * CH;
+    const int nch = (int)((n + CH - 1) / CH);
+    const unsigned gen1 = grid_gen1(f, 0);
+    const bool vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && n % 4 == 0;
+    float v[VEC][4];
+#pragma unroll
+    for (int k = 0; k < VEC; k++) {
+        const long long p = lo + (k * NT + (long long)threadIdx.x) * 4;
+        if (vec && p + 3 < n) {
+            const float4 q = *reinterpret_cast<const float4*>(x + p);
+            v[k][0] = q.x;
+            v[k][1] = q.y;
+            v[k][2] = q.z;
+            v[k][3] = q.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++) v[k][j] = x[min(p + j, n - 1)];      // clamped; counted only if p + j < n
+        }
+    }
+    const double shift = (double)x[0];                         // read before any block writes y
+    double s1 = 0.0, s2 = 0.0;
+#pragma unroll
+    for (int k = 0; k < VEC; k++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const bool in = lo + (k * NT + (long long)threadIdx.x) * 4 + j < n;
+            const double d = in ? (double)v[k][j] - shift : 0.0;
+            s1 += d;
+            s2 += d * d;
+        }
+    block_sum2_n<NT>(s1, s2, red);
+    const bool timed_out = grid_totals<NT>(f, 0, nch, gen1, s1, s2, red, tot);
+    const double nn = (double)n, s = tot[0], q = tot[1];
+    const double mean = timed_out ? __builtin_nan("") : shift + s / nn;
+    const double sd = sqrt(fmax(q - s * (s / nn), 0.0) / (nn - 1.0));
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        stats[0] = mean;
+        stats[1] = sd;
+    }
+    const double den = 1e-5 + sd, rden = 1.0 / den;
+    // CAC: float e of the spectrum is channel c = e / (2 ft), bin i = (e % (2 ft)) / 2, re or im
+    // by its parity, and goes to plane 2 c (re) or 2 c + 1 (im) at i.
+    const bool pairs = KIND == NORM_CAC && vec && ft % 2 == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0;
+#pragma unroll
+    for (int k = 0; k < VEC; k++) {
+        const long long p = lo + (k * NT + (long long)threadIdx.x) * 4;
+        if (p >= n) continue;
+        float o[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) o[j] = (float)div_rn((double)v[k][j] - mean, den, rden);   // = (v - mean) / den
+        if (KIND == NORM_FLAT) {
+            if (vec && p + 3 < n) {
+                *reinterpret_cast<float4*>(y + p) = make_float4(o[0], o[1], o[2], o[3]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if (p + j < n) y[p + j] = o[j];
+            }
+        } else if (pairs && p + 3 < n) {
+            // Two whole complex values of one channel (2 ft is a multiple of 4 and p of 4).
+            const long long c = p / (2 * ft), i = (p - c * 2 * ft) / 2;
+            *reinterpret_cast<float2*>(y + 2 * c * ft + i) = make_float2(o[0], o[2]);
+            *reinterpret_cast<float2*>(y + (2 * c + 1) * ft + i) = make_float2(o[1], o[3]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const long long e = p + j;
+                if (e >= n) continue;
+                const long long c = e / (2 * ft), r = e - c * 2 * ft;
+                y[(2 * c + (r & 1)) * ft + r / 2] = o[j];
+            }
         }
     }
 }
@@ -401,7 +491,7 @@ SepLayout sep_layout(int C, long long len, int seg, int S, int batch, int shifts
     L.stats = o;
     o += align(2 * sizeof(double));
     L.mom = o;
-    o += align((size_t)mom_blocks(len) * 16);
+    o += align(kGridSyncBytes + (size_t)mom_blocks(len) * 16);
     L.parts = o;
     o += align(sizeof(float) * (size_t)batch * C * seg);
     L.y = o;
@@ -414,17 +504,39 @@ SepLayout sep_layout(int C, long long len, int seg, int S, int batch, int shifts
     return L;
 }
 
+// Normalisation workspace: the single-pass kernel's area (kGridSyncBytes), then the pass-1 pairs.
+size_t norm_ws_bytes(long long n) { return kGridSyncBytes + (size_t)mom_blocks(n) * 16; }
+
 void check_ws(void* ws, size_t bytes, long long n) {
     STX_REQUIRE(ws != nullptr, "normalise: workspace is NULL");
     STX_REQUIRE((reinterpret_cast<uintptr_t>(ws) & 15) == 0, "normalise: workspace must be 16-byte aligned");
-    STX_REQUIRE(bytes >= (size_t)mom_blocks(n) * 16, "normalise: workspace too small (%zu < %zu bytes)", bytes,
-                (size_t)mom_blocks(n) * 16);
+    STX_REQUIRE(bytes >= norm_ws_bytes(n), "normalise: workspace too small (%zu < %zu bytes)", bytes,
+                norm_ws_bytes(n));
+}
+
+// The single-pass kernel at the smallest width whose blocks (at most kGridMaxBlocks) are all
+// resident at once; false when none is.
+template <int NK, int VEC>
+bool try_norm_fused(const float* x, float* y, long long n, long long ft, double* stats, void* ws, hipStream_t s) {
+    const long long ch = (long long)kGridThreads * 4 * VEC;
+    const long long nch = (n + ch - 1) / ch;
+    if (nch > kGridMaxBlocks) return false;
+    if (nch > resident_blocks(reinterpret_cast<const void*>(&norm_fused_kernel<NK, VEC>))) return false;
+    hipLaunchKernelGGL((norm_fused_kernel<NK, VEC>), dim3((unsigned)nch), dim3(kGridThreads), 0, s, x, y, n, ft, stats,
+                       grid_sync_at(ws));
+    launch_check("norm_fused_kernel");
+    return true;
 }
 
 template <int MK, int NK>
 void normalize(const float* x, long long n_mom, long long count, int C, float* y, double* stats, void* ws,
                hipStream_t s) {
-    double* partial = static_cast<double*>(ws);
+    if constexpr (NK != NORM_MIX) {
+        if (try_norm_fused<NK, 1>(x, y, n_mom, count, stats, ws, s) || try_norm_fused<NK, 2>(x, y, n_mom, count, stats, ws, s) ||
+            try_norm_fused<NK, 4>(x, y, n_mom, count, stats, ws, s))
+            return;
+    }
+    double* partial = reinterpret_cast<double*>(static_cast<char*>(ws) + kGridSyncBytes);
     const long long nb = mom_blocks(n_mom);
     STX_REQUIRE(nb < (1LL << 31) && count < (1LL << 40), "normalise: too many elements");
     MomArgs m{x, n_mom, C, partial};
@@ -452,7 +564,7 @@ using namespace stx;
 
 extern "C" {
 
-STX_API size_t stx_htdemucs_norm_workspace_size(int64_t n) { return n > 0 ? (size_t)mom_blocks(n) * 16 : 16; }
+STX_API size_t stx_htdemucs_norm_workspace_size(int64_t n) { return norm_ws_bytes(n > 0 ? n : 1); }
 
 STX_API stx_status stx_htdemucs_cac_normalize(const float* spec, int channels, int n_bins, int n_frames, float* mag,
                                               double* stats, void* workspace, size_t workspace_bytes,

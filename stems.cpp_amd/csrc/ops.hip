@@ -20,14 +20,12 @@
 // ADD, MUL and x + h * s round after every operation, exactly as the separate ggml ops do, and
 // are bit-exact with that definition.
 #include <algorithm>
-#include <atomic>
-#include <chrono>
 #include <cmath>
-#include <mutex>
 #include <type_traits>
 #include <vector>
 
 #include "common.hpp"
+#include "grid_sync.hpp"
 #include "tensor.hpp"
 
 namespace stx {
@@ -917,106 +915,14 @@ __global__ __launch_bounds__(256) void gn_apply_kernel(GroupNormArgs a) {
     gn_store<GELU, VEC>(a, a.y + begin, lo, hi, mean, rstd, v, ok, wv, bv);
 }
 
-// Sums of two doubles over an NT-thread block: wave sums, then the wave totals added in wave
-// order by every thread (the same order in every block). red holds 2 * NT / 64 doubles.
-template <int NT>
-__device__ __forceinline__ void block_sum2_n(double& a, double& b, double* red) {
-    constexpr int W = NT / kWave;
-    a = group_sum<kWave>(a);
-    b = group_sum<kWave>(b);
-    __syncthreads();
-    if (threadIdx.x % kWave == 0) {
-        red[threadIdx.x / kWave] = a;
-        red[W + threadIdx.x / kWave] = b;
-    }
-    __syncthreads();
-    a = 0.0;
-    b = 0.0;
-#pragma unroll
-    for (int w = 0; w < W; w++) {
-        a += red[w];
-        b += red[W + w];
-    }
-}
-
-// Single-pass GroupNorm (gn_fused_kernel): when every group's blocks fit on the device at once,
-// each block keeps its chunk of x in registers and publishes its partial sums; block 0 of the
-// group waits for all of them (one record per block, polled by one thread each: no
-// same-address atomics), adds them up in block order and publishes the totals; the other
-// blocks wait for the totals and write y from the registers. Every block thus normalises with
-// the same statistics bit for bit, x is read from HBM once and there is one launch.
-// Records are (s1, s2, tag) with tag = a 64-bit hash of s1, s2 and the call's key (token << 32 |
-// gen + 1): the token is a per-call random number from the host, gen a per-group generation
-// number kept in the workspace that block 0 advances once every block has read it. A reader
-// takes a record only when its tag matches the values it read under the current key, so the
-// three words need no write ordering (a torn or stale record fails the check), graph replays
-// of one call (same token) wait for a new gen each time, and neither a record of another call
-// nor garbage in a fresh workspace passes: the workspace needs no initialisation or clearing.
-// Every wait is bounded: a block that gives up (which needs blocks that never become
-// resident, e.g. two such kernels sharing the device) writes NaN instead of hanging.
-constexpr int kGnFusedThreads = 512;
-constexpr int kGnFusedMaxBlocks = 512;               // per group
-constexpr int kGnFusedMaxGroups = 8;
-constexpr int kGnStatCopies = 8;                     // waiters poll copy (block % 8)
-constexpr int kGnStatStride = 128;                   // unsigned long longs between copies (1 KB)
-constexpr unsigned kGnSpinLimit = 1u << 18;          // polls of about 1 us each
-
-struct GnSync {
-    unsigned* gen;                   // [kGnFusedMaxGroups]
-    unsigned long long* stat;        // [kGnStatCopies][kGnStatStride]: group g's totals record at 3g
-    unsigned long long* part;        // [kGnFusedMaxGroups][kGnFusedMaxBlocks][3]: partial sums records
-    unsigned token;
-    unsigned spin_limit;
-};
-
-// Cross-block words are device-scope relaxed atomics, which gfx950 performs at the device's
-// coherence point (sc1), past the XCD's own L2: no L2 write-back or invalidation, which a
-// release/acquire pair would cost per block.
-__device__ __forceinline__ void sync_store(unsigned long long* p, unsigned long long v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ unsigned long long sync_load(const unsigned long long* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// MurmurHash3's 64-bit finaliser.
-__device__ __forceinline__ unsigned long long fmix64(unsigned long long k) {
-    k ^= k >> 33;
-    k *= 0xff51afd7ed558ccdull;
-    k ^= k >> 33;
-    k *= 0xc4ceb9fe1a85ec53ull;
-    k ^= k >> 33;
-    return k;
-}
-__device__ __forceinline__ unsigned long long record_tag(unsigned long long a, unsigned long long b,
-                                                         unsigned long long key) {
-    return fmix64(a ^ fmix64(b ^ fmix64(key)));
-}
-// Publishes (s1, s2) at r[0..2] under key.
-__device__ __forceinline__ void record_store(unsigned long long* r, double s1, double s2, unsigned long long key) {
-    const unsigned long long a = (unsigned long long)__double_as_longlong(s1);
-    const unsigned long long b = (unsigned long long)__double_as_longlong(s2);
-    sync_store(r, a);
-    sync_store(r + 1, b);
-    sync_store(r + 2, record_tag(a, b, key));
-}
-// Polls r (at most limit times) until it holds a record under key; false if it never did.
-__device__ __forceinline__ bool record_wait(const unsigned long long* r, unsigned long long key, unsigned limit,
-                                            double& s1, double& s2) {
-    for (unsigned spins = 0;;) {
-        const unsigned long long a = sync_load(r), b = sync_load(r + 1), h = sync_load(r + 2);
-        if (h == record_tag(a, b, key)) {
-            s1 = __longlong_as_double((long long)a);
-            s2 = __longlong_as_double((long long)b);
-            return true;
-        }
-        if (++spins > limit) return false;
-        __builtin_amdgcn_s_sleep(1);
-    }
-}
-
+// Single-pass GroupNorm (gn_fused_kernel): when every group's blocks fit on the device at once
+// (at most kGridMaxGroups groups of at most kGridMaxBlocks blocks), each block keeps its chunk
+// of x and its affine parameters in registers, sums d and d^2 (d = x - x[group start]) and
+// gets the group's totals from the other blocks through grid_totals (grid_sync.hpp), then
+// writes y from the registers: x is read from HBM once, in one launch.
 template <int AK, bool GELU, int VEC>
-__global__ __launch_bounds__(kGnFusedThreads) void gn_fused_kernel(GroupNormArgs a, GnSync f) {
-    constexpr int NT = kGnFusedThreads;
+__global__ __launch_bounds__(kGridThreads) void gn_fused_kernel(GroupNormArgs a, GridSync f) {
+    constexpr int NT = kGridThreads;
     constexpr unsigned CH = NT * 4 * VEC;
     __shared__ double red[2 * NT / kWave];
     __shared__ double tot[2];
@@ -1029,8 +935,7 @@ __global__ __launch_bounds__(kGnFusedThreads) void gn_fused_kernel(GroupNormArgs
     const unsigned hi = min(lo + CH, count);
     const int nch = (int)((count + CH - 1) / CH);
     const float* xg = a.x + begin;
-    const unsigned gen1 = __hip_atomic_load(f.gen + gt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
-    const unsigned long long key = (unsigned long long)f.token << 32 | gen1;
+    const unsigned gen1 = grid_gen1(f, gt);
     float v[4 * VEC], wv[4 * VEC], bv[4 * VEC];
     bool ok[4 * VEC];
     gn_load<VEC, NT>(a, xg, lo, hi, v, ok);
@@ -1044,39 +949,7 @@ __global__ __launch_bounds__(kGnFusedThreads) void gn_fused_kernel(GroupNormArgs
         s2 += d * d;
     }
     block_sum2_n<NT>(s1, s2, red);
-    unsigned long long* part = f.part + 3 * (size_t)gt * kGnFusedMaxBlocks;
-    bool late = false;
-    if (blockIdx.x != 0) {
-        if (threadIdx.x == 0) {
-            record_store(part + 3 * blockIdx.x, s1, s2, key);
-            double t1 = 0.0, t2 = 0.0;                         // the group's totals, from block 0
-            late = !record_wait(f.stat + (blockIdx.x % kGnStatCopies) * kGnStatStride + 3 * gt, key, f.spin_limit,
-                                t1, t2);
-            tot[0] = t1;
-            tot[1] = t2;
-        }
-    } else {
-        // Block 0 collects: thread t waits for the records of blocks t, t + NT, ... and adds
-        // them in that order (block 0's own sums first), then the block adds the threads' sums
-        // in thread order and publishes the totals, one record per copy.
-        double p1 = threadIdx.x == 0 ? s1 : 0.0, p2 = threadIdx.x == 0 ? s2 : 0.0;
-        for (int b = threadIdx.x == 0 ? NT : (int)threadIdx.x; b < nch && !late; b += NT) {
-            double q1 = 0.0, q2 = 0.0;
-            late = !record_wait(part + 3 * b, key, f.spin_limit, q1, q2);
-            p1 += q1;
-            p2 += q2;
-        }
-        block_sum2_n<NT>(p1, p2, red);
-        if (threadIdx.x == 0) {
-            tot[0] = p1;
-            tot[1] = p2;
-#pragma unroll
-            for (int c = 0; c < kGnStatCopies; c++) record_store(f.stat + c * kGnStatStride + 3 * gt, p1, p2, key);
-            // Every block has read gen before it published its record.
-            __hip_atomic_store(f.gen + gt, gen1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
-    const bool timed_out = __syncthreads_or(late);
+    const bool timed_out = grid_totals<NT>(f, gt, nch, gen1, s1, s2, red, tot);
     const double N = (double)count, dm = tot[0] / N;
     const double mean = timed_out ? __builtin_nan("") : shift + dm;
     const double rstd = 1.0 / sqrt(fmax(tot[1] / N - dm * dm, 0.0) + (double)a.eps);
@@ -1379,16 +1252,7 @@ struct GnPlan {
     size_t sync_off, shift_off, part_off, bytes;         // workspace layout
 };
 
-// The single-pass kernel's area sits at offset 0 of every group-norm workspace with a fixed
-// size, so that a workspace shared by calls of different shapes keeps each group slot's
-// generation number consistent: [8 KB) totals records, 8 per group at 1 KB apart | [256 B)
-// generation numbers | partial sums records, 3 words per block.
-constexpr size_t kGnSyncStat = 0, kGnSyncGen = sizeof(unsigned long long) * kGnStatCopies * kGnStatStride,
-                 kGnSyncPart = kGnSyncGen + 256;
-constexpr size_t kGnSyncBytes =
-    (kGnSyncPart + sizeof(unsigned long long) * 3 * kGnFusedMaxGroups * kGnFusedMaxBlocks + 255) / 256 * 256;
-static_assert(3 * kGnFusedMaxGroups <= kGnStatStride && 4 * kGnFusedMaxGroups <= 256, "group-norm sync area layout");
-
+// Every group-norm workspace starts with the single-pass kernel's area (kGridSyncBytes).
 GnPlan gn_plan(const stx_tensor* a, int n_groups) {
     GnPlan p{};
     p.cpg = std::max<long long>(1, (a->ne[2] + n_groups - 1) / n_groups);
@@ -1404,66 +1268,31 @@ GnPlan gn_plan(const stx_tensor* a, int n_groups) {
     const size_t g = (size_t)std::max<long long>(1, p.groups_total);
     auto up = [](size_t v) { return (v + 255) / 256 * 256; };
     p.sync_off = 0;
-    p.shift_off = kGnSyncBytes;
+    p.shift_off = kGridSyncBytes;
     p.part_off = p.shift_off + up(sizeof(double) * g);
     p.bytes = p.part_off + up(sizeof(double) * 2 * g * (size_t)std::max<long long>(1, p.chunks_partial));
     return p;
 }
 
-// A per-call random number: murmur3's 32-bit finaliser of a call counter offset by a
-// per-process seed from the clock.
-unsigned gn_call_token() {
-    static const unsigned seed = (unsigned)std::chrono::steady_clock::now().time_since_epoch().count();
-    static std::atomic<unsigned> calls{0};
-    unsigned h = seed + 0x9e3779b9u * calls.fetch_add(1, std::memory_order_relaxed);
-    h ^= h >> 16;
-    h *= 0x85ebca6bu;
-    h ^= h >> 13;
-    h *= 0xc2b2ae35u;
-    h ^= h >> 16;
-    return h;
-}
-
-// Blocks of `kernel` (kGnFusedThreads threads) that the current device holds at once.
-int resident_blocks(const void* kernel) {
-    struct Entry {
-        const void* k;
-        int dev, blocks;
-    };
-    static std::mutex mu;
-    static std::vector<Entry> cache;
-    int dev = 0;
-    hip_check(hipGetDevice(&dev), "hipGetDevice");
-    std::lock_guard<std::mutex> lock(mu);
-    for (const Entry& e : cache)
-        if (e.k == kernel && e.dev == dev) return e.blocks;
-    int cus = 0, per_cu = 0;
-    hip_check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
-    hip_check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kGnFusedThreads, 0),
-              "hipOccupancyMaxActiveBlocksPerMultiprocessor");
-    cache.push_back({kernel, dev, cus * per_cu});
-    return cus * per_cu;
-}
-
-// Single pass when the groups fit: at most kGnFusedMaxGroups of them, each in at most
-// kGnFusedMaxBlocks blocks, all blocks resident together. VEC is the smallest width that
+// Single pass when the groups fit: at most kGridMaxGroups of them, each in at most
+// kGridMaxBlocks blocks, all blocks resident together. VEC is the smallest width that
 // fits (more blocks, shorter per-thread chains). Returns false to take the two passes.
 template <int AK, bool GELU, int VEC>
-bool try_fused(const GroupNormArgs& g, const GnPlan& p, const GnSync& sync, hipStream_t s) {
-    const long long ch = (long long)kGnFusedThreads * 4 * VEC;
+bool try_fused(const GroupNormArgs& g, const GnPlan& p, const GridSync& sync, hipStream_t s) {
+    const long long ch = (long long)kGridThreads * 4 * VEC;
     const long long nch = (p.span + ch - 1) / ch;
-    if (nch > kGnFusedMaxBlocks) return false;
+    if (nch > kGridMaxBlocks) return false;
     const void* k = reinterpret_cast<const void*>(&gn_fused_kernel<AK, GELU, VEC>);
     if (nch * p.groups_total > resident_blocks(k)) return false;
     hipLaunchKernelGGL((gn_fused_kernel<AK, GELU, VEC>), dim3((unsigned)nch, (unsigned)p.groups_total),
-                       dim3(kGnFusedThreads), 0, s, g, sync);
+                       dim3(kGridThreads), 0, s, g, sync);
     launch_check("gn_fused_kernel");
     return true;
 }
 
 template <int AK, bool GELU>
-void launch_group_norm(GroupNormArgs g, const GnPlan& p, const GnSync& sync, hipStream_t s) {
-    if (p.groups_total <= kGnFusedMaxGroups &&
+void launch_group_norm(GroupNormArgs g, const GnPlan& p, const GridSync& sync, hipStream_t s) {
+    if (p.groups_total <= kGridMaxGroups &&
         (try_fused<AK, GELU, 1>(g, p, sync, s) || try_fused<AK, GELU, 2>(g, p, sync, s) ||
          try_fused<AK, GELU, 4>(g, p, sync, s)))
         return;
@@ -1669,12 +1498,7 @@ STX_API stx_status stx_group_norm(const stx_tensor* a, const stx_tensor* dst, in
         g.w = w;
         g.b = b;
         char* ws = static_cast<char*>(workspace);
-        GnSync sync;
-        sync.gen = reinterpret_cast<unsigned*>(ws + p.sync_off + kGnSyncGen);
-        sync.stat = reinterpret_cast<unsigned long long*>(ws + p.sync_off + kGnSyncStat);
-        sync.part = reinterpret_cast<unsigned long long*>(ws + p.sync_off + kGnSyncPart);
-        sync.token = gn_call_token();
-        sync.spin_limit = kGnSpinLimit;
+        const GridSync sync = grid_sync_at(ws + p.sync_off);
         g.shift = reinterpret_cast<double*>(ws + p.shift_off);
         g.part = reinterpret_cast<double*>(ws + p.part_off);
         g.ne0 = (unsigned)ta.ne[0];

@@ -39,12 +39,6 @@ struct ResampleArgs {
     int n, out_n, C;
 };
 
-// x / h correctly rounded, given r = RN(1/h) (x >= 0 and no overflow or underflow).
-__device__ __forceinline__ double div_rn(double x, double h, double r) {
-#pragma clang fp contract(off)
-    const double q0 = x * r;
-    return fma(fma(-q0, h, x), r, q0);
-}
 
 template <int NC>
 __global__ __launch_bounds__(256) void resample_kernel(ResampleArgs a) {

@@ -65,7 +65,7 @@ def test_wave_normalize_c1(device, htd):
     assert np.array_equal(host(y), htd.normalize(xh, st[0], st[1]))
 
 
-@pytest.mark.parametrize("n", [2, 3, 8191, 8192, 8193, 100003])
+@pytest.mark.parametrize("n", [2, 3, 8191, 8192, 8193, 100003, 5000001])   # last: too large for one pass
 def test_wave_normalize_ragged(device, htd, n):
     xh = synth.normal(3, (n,), 1.0) * 5 + 2
     y, stats = stx.htdemucs_wave_normalize(dev(xh, device))
