@@ -512,7 +512,10 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
 // the n/2-point transform of a real frame directly, radix 16 / 8 / 4 / 2 / 3 / 5 Stockham passes
 // ping-ponging between two LDS buffers with twiddles W_n^m from a table computed in double.
 // Frames are packed and split as in the power-of-two kernels; the iSTFT always takes the
-// two-kernel path (frames to the workspace, then istft_ola_kernel).
+// two-kernel path (frames to the workspace, then istft_ola_kernel). One frame per workgroup,
+// numbered XCD-aware (xcd_block): consecutive frames run on one XCD, so the F-major spectrum's
+// rows, where each frame owns 8 bytes of a 128-byte line, are written (or read) through one L2
+// that merges the 16 frames of a line, instead of as partial lines from eight XCDs.
 constexpr int kMixedThreads = 256;
 
 __device__ __forceinline__ int padded_index_rt(int m, const StftArgs& a, int n) {
@@ -526,7 +529,8 @@ __global__ __launch_bounds__(kMixedThreads) void stft_mixed_kernel(StftArgs a, M
                                                                    const float2* __restrict__ twn, int n) {
     __shared__ float2 b0[MAXM], b1[MAXM];
     const int M = n / 2, tid = (int)threadIdx.x;
-    const int f = (int)blockIdx.x;                     // channel * T + frame
+    const int f = xcd_block();                         // channel * T + frame
+    if (f >= a.jobs) return;                           // whole block idle: no barrier reached
     const int c = f / a.T, t = f - c * a.T;
     const float* xc = a.x + (size_t)c * a.len;
     const int m0 = a.frame0 + t * a.hop;
@@ -551,10 +555,12 @@ __global__ __launch_bounds__(kMixedThreads) void stft_mixed_kernel(StftArgs a, M
 
 template <int MAXM>
 __global__ __launch_bounds__(kMixedThreads) void istft_frames_mixed_kernel(IstftArgs a, MixedRadix p,
-                                                                           const float2* __restrict__ twn, int n) {
+                                                                           const float2* __restrict__ twn, int n,
+                                                                           int jobs) {
     __shared__ float2 b0[MAXM], b1[MAXM];
     const int M = n / 2, tid = (int)threadIdx.x;
-    const int f = (int)blockIdx.x;
+    const int f = xcd_block();                         // channel * T + frame
+    if (f >= jobs) return;                             // whole block idle: no barrier reached
     const int c = f / a.T, st = f - c * a.T;
     const float2* sc = a.spec + (size_t)c * a.T * a.F;
     for (int k = tid; k < M; k += kMixedThreads) {
@@ -763,16 +769,17 @@ void run_istft(const stx_fft* f, IstftArgs a, int channels, void* workspace, siz
         STX_REQUIRE(ws_bytes >= need, "workspace too small: %zu bytes, need %zu", ws_bytes, need);
         check_extent((long long)channels * a.T * f->n, "workspace");
         a.frames = static_cast<float*>(workspace);
-        const unsigned frames = (unsigned)(channels * a.T);
+        const int jobs = channels * a.T;
+        const unsigned grid = (unsigned)((jobs + kXcds - 1) / kXcds * kXcds);   // xcd_block's multiple
         if (f->n / 2 <= 1024)
-            hipLaunchKernelGGL(istft_frames_mixed_kernel<1024>, dim3(frames), dim3(kMixedThreads), 0, s, a, f->half,
-                               f->twn, f->n);
+            hipLaunchKernelGGL(istft_frames_mixed_kernel<1024>, dim3(grid), dim3(kMixedThreads), 0, s, a, f->half,
+                               f->twn, f->n, jobs);
         else if (f->n / 2 <= 4096)
-            hipLaunchKernelGGL(istft_frames_mixed_kernel<4096>, dim3(frames), dim3(kMixedThreads), 0, s, a, f->half,
-                               f->twn, f->n);
+            hipLaunchKernelGGL(istft_frames_mixed_kernel<4096>, dim3(grid), dim3(kMixedThreads), 0, s, a, f->half,
+                               f->twn, f->n, jobs);
         else
-            hipLaunchKernelGGL(istft_frames_mixed_kernel<8192>, dim3(frames), dim3(kMixedThreads), 0, s, a, f->half,
-                               f->twn, f->n);
+            hipLaunchKernelGGL(istft_frames_mixed_kernel<8192>, dim3(grid), dim3(kMixedThreads), 0, s, a, f->half,
+                               f->twn, f->n, jobs);
         launch_check("istft_frames_mixed_kernel");
         hipLaunchKernelGGL(istft_ola_kernel, dim3((a.out_len + 255) / 256, channels), dim3(256), 0, s, a, f->n);
         launch_check("istft_ola_kernel");
@@ -1012,15 +1019,15 @@ STX_API stx_status stx_torch_stft(const stx_fft* f, const float* x, int channels
         check_extent((long long)channels * a.T * a.F, "spectrum");
         check_extent((long long)channels * len + n, "signal");
         if (f->mixed) {
-            const unsigned frames = (unsigned)a.jobs;
+            const unsigned grid = (unsigned)((a.jobs + kXcds - 1) / kXcds * kXcds);   // xcd_block's multiple
             if (n / 2 <= 1024)
-                hipLaunchKernelGGL(stft_mixed_kernel<1024>, dim3(frames), dim3(kMixedThreads), 0, as_stream(stream), a,
+                hipLaunchKernelGGL(stft_mixed_kernel<1024>, dim3(grid), dim3(kMixedThreads), 0, as_stream(stream), a,
                                    f->half, f->twn, n);
             else if (n / 2 <= 4096)
-                hipLaunchKernelGGL(stft_mixed_kernel<4096>, dim3(frames), dim3(kMixedThreads), 0, as_stream(stream), a,
+                hipLaunchKernelGGL(stft_mixed_kernel<4096>, dim3(grid), dim3(kMixedThreads), 0, as_stream(stream), a,
                                    f->half, f->twn, n);
             else
-                hipLaunchKernelGGL(stft_mixed_kernel<8192>, dim3(frames), dim3(kMixedThreads), 0, as_stream(stream), a,
+                hipLaunchKernelGGL(stft_mixed_kernel<8192>, dim3(grid), dim3(kMixedThreads), 0, as_stream(stream), a,
                                    f->half, f->twn, n);
             launch_check("stft_mixed_kernel");
             return;
