@@ -311,34 +311,67 @@ inline bool mixed_plan(int m, MixedRadix& p) {
     return left == 1 && p.count <= 24;
 }
 
+// LDS layout of the mixed-radix buffers: element i at i + i / 16, so that the first pass's
+// stride-16 writes (and every other power-of-two stride of 16 or more) spread over the banks.
+// A buffer for M elements holds mixed_padded(M) float2.
+__host__ __device__ constexpr int mixed_pad(int i) { return i + (i >> 4); }
+__host__ __device__ constexpr int mixed_padded(int m) { return m + m / 16 + 1; }
+
 // One out-of-place Stockham pass of radix R after sub-transforms of length Ns over an M-point
-// transform held in src (natural layout), by the NT threads of a workgroup: butterfly b reads
-// src[b + r M/R], multiplies element r by W_{Ns R}^{(b mod Ns) r} = twn[(b mod Ns) r scale]
-// (twn: W_n^m, scale = n / (Ns R)), takes an R-point DFT and writes
-// dst[(b / Ns) Ns R + b mod Ns + r Ns].
-template <int R>
+// transform held in src (natural order, padded layout), by the NT threads of a workgroup:
+// butterfly b reads src[b + r M/R], multiplies element r by W_{Ns R}^{(b mod Ns) r} =
+// twn[(b mod Ns) r scale] (twn: W_n^m, scale = n / (Ns R); all ones when Ns = 1), takes an
+// R-point DFT and writes dst[(b / Ns) Ns R + b mod Ns + r Ns]. A thread takes butterflies
+// tid + i NT in batches of IT whose LDS reads and twiddle loads are all issued before the first
+// is used (clamped to a valid butterfly; the extra ones are not written), so a pass costs one
+// twiddle round trip per batch rather than one per butterfly. b / Ns is umulhi(b, inv) with
+// inv = ceil(2^32 / Ns), exact for b, Ns < 2^18.
+template <int R, int IT, int NT>
 __device__ __forceinline__ void mixed_pass(const float2* src, float2* dst, int M, int Ns, int scale,
-                                           const float2* __restrict__ twn, int tid, int nt) {
+                                           const float2* __restrict__ twn, int tid) {
     const int B = M / R;
-    for (int b = tid; b < B; b += nt) {
-        const int blk = b / Ns, k = b - blk * Ns;
-        float2 v[R];
+    const unsigned inv = Ns > 1 ? 0xffffffffu / (unsigned)Ns + 1u : 0u;
+    for (int b0 = tid; b0 < B; b0 += IT * NT) {
+        float2 v[IT][R];
+        int base[IT];
 #pragma unroll
-        for (int r = 0; r < R; r++) v[r] = src[b + r * B];
+        for (int it = 0; it < IT; it++) {
+            const int b = min(b0 + it * NT, B - 1);
+            const int blk = Ns > 1 ? (int)__umulhi((unsigned)b, inv) : b, k = b - blk * Ns;
 #pragma unroll
-        for (int r = 1; r < R; r++) v[r] = cmul(v[r], twn[k * r * scale]);
-        Dft<R>::run(v);
-        const int base = blk * Ns * R + k;
+            for (int r = 0; r < R; r++) v[it][r] = src[mixed_pad(b + r * B)];
+            if (Ns > 1) {
 #pragma unroll
-        for (int r = 0; r < R; r++) dst[base + r * Ns] = v[r];
+                for (int r = 1; r < R; r++) v[it][r] = cmul(v[it][r], twn[k * r * scale]);
+            }
+            base[it] = blk * Ns * R + k;
+        }
+#pragma unroll
+        for (int it = 0; it < IT; it++) {
+            if (b0 + it * NT >= B) break;
+            Dft<R>::run(v[it]);
+#pragma unroll
+            for (int r = 0; r < R; r++) dst[mixed_pad(base[it] + r * Ns)] = v[it][r];
+        }
     }
 }
 
-// All passes of plan p over the M-point transform in buf0 (buf1: scratch of M); returns the
-// buffer holding the result. Every thread of the workgroup must call it (it has barriers).
-// twn holds W_n^m for m < n with n a multiple of M (tw_mul = n / M).
+// Butterflies per thread and batch for radix R: all of a pass of MAXM points at once, capped
+// so that a batch holds at most 32 complex values.
+template <int R, int MAXM, int NT>
+constexpr int mixed_batch() {
+    const int all = (MAXM / R + NT - 1) / NT;
+    const int cap = 32 / R > 0 ? 32 / R : 1;
+    return all < cap ? (all > 0 ? all : 1) : cap;
+}
+
+// All passes of plan p over the M-point transform (M <= MAXM) in buf0 (buf1: scratch; both
+// padded, see mixed_pad) by NT threads; returns the buffer holding the result. Every thread of
+// the workgroup must call it (it has barriers). twn holds W_n^m for m < n with n a multiple of
+// M (tw_mul = n / M).
+template <int MAXM, int NT>
 __device__ __forceinline__ float2* mixed_fft(float2* buf0, float2* buf1, int M, const MixedRadix& p, int tw_mul,
-                                             const float2* __restrict__ twn, int tid, int nt) {
+                                             const float2* __restrict__ twn, int tid) {
     float2* src = buf0;
     float2* dst = buf1;
     int Ns = 1;
@@ -346,12 +379,12 @@ __device__ __forceinline__ float2* mixed_fft(float2* buf0, float2* buf1, int M, 
         const int R = p.r[i];
         const int scale = (M / (Ns * R)) * tw_mul;
         switch (R) {
-            case 16: mixed_pass<16>(src, dst, M, Ns, scale, twn, tid, nt); break;
-            case 8: mixed_pass<8>(src, dst, M, Ns, scale, twn, tid, nt); break;
-            case 4: mixed_pass<4>(src, dst, M, Ns, scale, twn, tid, nt); break;
-            case 2: mixed_pass<2>(src, dst, M, Ns, scale, twn, tid, nt); break;
-            case 3: mixed_pass<3>(src, dst, M, Ns, scale, twn, tid, nt); break;
-            default: mixed_pass<5>(src, dst, M, Ns, scale, twn, tid, nt); break;
+            case 16: mixed_pass<16, mixed_batch<16, MAXM, NT>(), NT>(src, dst, M, Ns, scale, twn, tid); break;
+            case 8: mixed_pass<8, mixed_batch<8, MAXM, NT>(), NT>(src, dst, M, Ns, scale, twn, tid); break;
+            case 4: mixed_pass<4, mixed_batch<4, MAXM, NT>(), NT>(src, dst, M, Ns, scale, twn, tid); break;
+            case 2: mixed_pass<2, mixed_batch<2, MAXM, NT>(), NT>(src, dst, M, Ns, scale, twn, tid); break;
+            case 3: mixed_pass<3, mixed_batch<3, MAXM, NT>(), NT>(src, dst, M, Ns, scale, twn, tid); break;
+            default: mixed_pass<5, mixed_batch<5, MAXM, NT>(), NT>(src, dst, M, Ns, scale, twn, tid); break;
         }
         __syncthreads();
         float2* t = src;

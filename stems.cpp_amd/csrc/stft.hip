@@ -516,7 +516,7 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
 // numbered XCD-aware (xcd_block): consecutive frames run on one XCD, so the F-major spectrum's
 // rows, where each frame owns 8 bytes of a 128-byte line, are written (or read) through one L2
 // that merges the 16 frames of a line, instead of as partial lines from eight XCDs.
-constexpr int kMixedThreads = 256;
+constexpr int kMixedThreads = 512;
 
 __device__ __forceinline__ int padded_index_rt(int m, const StftArgs& a, int n) {
     int j = reflect(m - n / 2, a.len1) - a.pre_left;
@@ -527,7 +527,7 @@ __device__ __forceinline__ int padded_index_rt(int m, const StftArgs& a, int n) 
 template <int MAXM>
 __global__ __launch_bounds__(kMixedThreads) void stft_mixed_kernel(StftArgs a, MixedRadix p,
                                                                    const float2* __restrict__ twn, int n) {
-    __shared__ float2 b0[MAXM], b1[MAXM];
+    __shared__ float2 b0[mixed_padded(MAXM)], b1[mixed_padded(MAXM)];
     const int M = n / 2, tid = (int)threadIdx.x;
     const int f = xcd_block();                         // channel * T + frame
     if (f >= a.jobs) return;                           // whole block idle: no barrier reached
@@ -536,14 +536,14 @@ __global__ __launch_bounds__(kMixedThreads) void stft_mixed_kernel(StftArgs a, M
     const int m0 = a.frame0 + t * a.hop;
     for (int i = tid; i < M; i += kMixedThreads) {
         const float x0 = xc[padded_index_rt(m0 + 2 * i, a, n)], x1 = xc[padded_index_rt(m0 + 2 * i + 1, a, n)];
-        b0[i] = make_float2(x0 * a.win[2 * i], x1 * a.win[2 * i + 1]);
+        b0[mixed_pad(i)] = make_float2(x0 * a.win[2 * i], x1 * a.win[2 * i + 1]);
     }
     __syncthreads();
-    const float2* z = mixed_fft(b0, b1, M, p, 2, twn, tid, kMixedThreads);
+    const float2* z = mixed_fft<MAXM, kMixedThreads>(b0, b1, M, p, 2, twn, tid);
     // X[k] = E[k] + W_n^k O[k], k <= n/2, as in stft_kernel.
     const float hs = 0.5f * a.scale;
     for (int k = tid; k < a.F; k += kMixedThreads) {
-        const float2 zk = z[k == M ? 0 : k], zm = z[k == 0 ? 0 : M - k];
+        const float2 zk = z[mixed_pad(k == M ? 0 : k)], zm = z[mixed_pad(k == 0 ? 0 : M - k)];
         const float2 w = twn[k];
         const float er = zk.x + zm.x, ei = zk.y - zm.y;
         const float orr = zk.y + zm.y, oi = zm.x - zk.x;
@@ -557,7 +557,7 @@ template <int MAXM>
 __global__ __launch_bounds__(kMixedThreads) void istft_frames_mixed_kernel(IstftArgs a, MixedRadix p,
                                                                            const float2* __restrict__ twn, int n,
                                                                            int jobs) {
-    __shared__ float2 b0[MAXM], b1[MAXM];
+    __shared__ float2 b0[mixed_padded(MAXM)], b1[mixed_padded(MAXM)];
     const int M = n / 2, tid = (int)threadIdx.x;
     const int f = xcd_block();                         // channel * T + frame
     if (f >= jobs) return;                             // whole block idle: no barrier reached
@@ -567,27 +567,28 @@ __global__ __launch_bounds__(kMixedThreads) void istft_frames_mixed_kernel(Istft
         const float2 xk = spec_bin(a, sc, st, k);
         float2 xm = spec_bin(a, sc, st, min(M - k, a.F - 1));
         if (k == 0 && !a.keep_nyquist) xm = make_float2(0.f, 0.f);
-        b0[k] = inverse_split_w(xk, xm, k, a.keep_nyquist, twn[k]);
+        b0[mixed_pad(k)] = inverse_split_w(xk, xm, k, a.keep_nyquist, twn[k]);
     }
     __syncthreads();
-    const float2* r = mixed_fft(b0, b1, M, p, 2, twn, tid, kMixedThreads);
+    const float2* r = mixed_fft<MAXM, kMixedThreads>(b0, b1, M, p, 2, twn, tid);
     float* dst = a.frames + (size_t)f * n;
     for (int i = tid; i < M; i += kMixedThreads) {     // windowed as WindowPost
-        dst[2 * i] = r[i].x * a.win[2 * i] * a.norm;
-        dst[2 * i + 1] = -r[i].y * a.win[2 * i + 1] * a.norm;
+        const float2 ri = r[mixed_pad(i)];
+        dst[2 * i] = ri.x * a.win[2 * i] * a.norm;
+        dst[2 * i + 1] = -ri.y * a.win[2 * i + 1] * a.norm;
     }
 }
 
 template <int MAXM>
 __global__ __launch_bounds__(kMixedThreads) void fft_mixed_kernel(float2* data, int inverse, MixedRadix p,
                                                                   const float2* __restrict__ twn, int n) {
-    __shared__ float2 b0[MAXM], b1[MAXM];
+    __shared__ float2 b0[mixed_padded(MAXM)], b1[mixed_padded(MAXM)];
     const int tid = (int)threadIdx.x;
     float2* d = data + (size_t)blockIdx.x * n;
-    for (int i = tid; i < n; i += kMixedThreads) b0[i] = inverse ? cconj(d[i]) : d[i];
+    for (int i = tid; i < n; i += kMixedThreads) b0[mixed_pad(i)] = inverse ? cconj(d[i]) : d[i];
     __syncthreads();
-    const float2* r = mixed_fft(b0, b1, n, p, 1, twn, tid, kMixedThreads);
-    for (int i = tid; i < n; i += kMixedThreads) d[i] = inverse ? cconj(r[i]) : r[i];
+    const float2* r = mixed_fft<MAXM, kMixedThreads>(b0, b1, n, p, 1, twn, tid);
+    for (int i = tid; i < n; i += kMixedThreads) d[i] = inverse ? cconj(r[mixed_pad(i)]) : r[mixed_pad(i)];
 }
 
 __global__ __launch_bounds__(256) void zero_kernel(float* out, size_t count) {
