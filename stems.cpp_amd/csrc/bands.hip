@@ -66,6 +66,8 @@ struct GatherArgs {
     const int* pair_off;     // [n_bands + 1]
     const int* pair_code;    // [total_feat / 2]
     const int* freq_lo;      // [n_bands]: first bin of each band when every band is a bin range
+    const stx::FastDiv* pair_div;   // [n_bands]: division by the band's pairs per frame
+    stx::FastDiv cdiv;       // division by C
     int C, F, T;
     int n_bands;
     long long total_feat;    // floats per frame of one batch item
@@ -82,12 +84,16 @@ constexpr int kGatherPer = 8;                        // T-major: outputs per thr
 // bin freq_lo[b] + q / C and the pair table is not read.
 template <bool RANGES>
 __global__ __launch_bounds__(256) void band_gather_t_kernel(GatherArgs a) {
-    extern __shared__ int po[];                      // [n_bands + 1] pair offsets, [n_bands] first bins
+    // LDS: [n_bands + 1] pair offsets, [n_bands] first bins, [n_bands] dividers by the pairs.
+    extern __shared__ int po[];
     int* flo = po + a.n_bands + 1;
+    stx::FastDiv* fd = reinterpret_cast<stx::FastDiv*>(flo + a.n_bands);
     const int tid = (int)threadIdx.x;
     for (int b = tid; b <= a.n_bands; b += 256) po[b] = a.pair_off[b];
-    if constexpr (RANGES)
-        for (int b = tid; b < a.n_bands; b += 256) flo[b] = a.freq_lo[b];
+    for (int b = tid; b < a.n_bands; b += 256) {
+        if constexpr (RANGES) flo[b] = a.freq_lo[b];
+        fd[b] = a.pair_div[b];
+    }
     __syncthreads();
     const int bt = (int)blockIdx.y;
     const int n = po[a.n_bands] * a.T;
@@ -107,11 +113,11 @@ __global__ __launch_bounds__(256) void band_gather_t_kernel(GatherArgs a) {
         while (po[b + 1] * a.T <= e) b++;
         const int pairs = po[b + 1] - po[b];
         const int r = e - po[b] * a.T;
-        t[k] = r / pairs;
+        t[k] = (int)fd[b].div((unsigned)r);                   // r / pairs
         const int q = r - t[k] * pairs;
         pair[k] = po[b] + q;
         if constexpr (RANGES) {
-            const int j = q / a.C;
+            const int j = (int)a.cdiv.div((unsigned)q);       // q / C
             code[k] = ((q - j * a.C) << 16) | (flo[b] + j);
         }
     }
@@ -557,7 +563,9 @@ STX_API stx_status stx_band_gather(const stx_bands* h, const float* spec, int ba
             STX_REQUIRE(n < (1LL << 31) - 256 * kGatherPer, "band gather: too many features per chunk");
             if (h->n_bands > 8191) fail(STX_STATUS_UNSUPPORTED, "T-major band gather: more than 8191 bands");
             dim3 grid((unsigned)((n + 256 * kGatherPer - 1) / (256 * kGatherPer)), batch);
-            const size_t lds = sizeof(int) * (2 * (size_t)h->n_bands + 1);
+            const size_t lds = sizeof(int) * (2 * (size_t)h->n_bands + 1) + sizeof(FastDiv) * (size_t)h->n_bands;
+            a.pair_div = h->d_pair_div;
+            a.cdiv = FastDiv((unsigned)a.C);
             if (h->ranges) hipLaunchKernelGGL(band_gather_t_kernel<true>, grid, dim3(256), lds, s, a);
             else hipLaunchKernelGGL(band_gather_t_kernel<false>, grid, dim3(256), lds, s, a);
             launch_check("band_gather_t_kernel");
