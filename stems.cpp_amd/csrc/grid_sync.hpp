@@ -25,6 +25,7 @@
 
 #include <atomic>
 #include <chrono>
+#include <cstdlib>
 #include <mutex>
 #include <vector>
 
@@ -200,8 +201,21 @@ inline GridSync grid_sync_at(void* ws) {
     return f;
 }
 
-// Blocks of `kernel` (kGridThreads threads, no dynamic LDS) that the current device holds at once.
+// Whether the single-pass kernels may run: not when STX_NO_GRID_SYNC is set to anything but
+// "0" (read at every call, for callers that run such kernels concurrently on one device), and
+// not when the process's queues carry a CU mask (HSA_CU_MASK, ROC_GLOBAL_CU_MASK), which would
+// leave fewer CUs than the occupancy check counts.
+inline bool grid_sync_enabled() {
+    const char* off = std::getenv("STX_NO_GRID_SYNC");
+    if (off && off[0] && !(off[0] == '0' && off[1] == 0)) return false;
+    static const bool masked = std::getenv("HSA_CU_MASK") || std::getenv("ROC_GLOBAL_CU_MASK");
+    return !masked;
+}
+
+// Blocks of `kernel` (kGridThreads threads, no dynamic LDS) that the current device holds at
+// once; 0 when grid_sync_enabled() is false, so that callers take their multi-kernel path.
 inline int resident_blocks(const void* kernel) {
+    if (!grid_sync_enabled()) return 0;
     struct Entry {
         const void* k;
         int dev, blocks;

@@ -74,6 +74,22 @@ def test_wave_normalize_ragged(device, htd, n):
     assert np.array_equal(host(y), htd.normalize(xh, st[0], st[1]))
 
 
+def test_normalize_without_grid_sync(device, htd, monkeypatch):
+    """STX_NO_GRID_SYNC=1 sends one segment's normalisations to the three-kernel path."""
+    monkeypatch.setenv("STX_NO_GRID_SYNC", "1")
+    xh = synth.normal(9, (2, SEG), 0.1) - 0.02
+    y, stats = stx.htdemucs_wave_normalize(dev(xh, device))
+    st = host(stats)
+    assert close_stats(st, htd.mean_std(xh))
+    assert np.array_equal(host(y), htd.normalize(xh, st[0], st[1]))
+    x = dev(synth.normal(10, (2, SEG), 0.1), device)
+    spec = stx.htdemucs_spec(stx.FFT(NFFT), x)
+    mag, stats = stx.htdemucs_cac_normalize(spec)
+    sh, st = host(spec), host(stats)
+    assert close_stats(st, htd.mean_std(htd.cac_pack(sh)))
+    assert np.array_equal(host(mag), htd.cac_normalize(sh, st[0], st[1]))
+
+
 def test_mix_normalize_song(device, htd):
     """src/htdemucs.cpp:539-549 on the 180 s stereo song."""
     mix = synth.sines_plus_pink(5, 2, SONG)

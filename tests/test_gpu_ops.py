@@ -139,6 +139,19 @@ def test_group_norm_graph_replays(device, ops):
         assert rel_err(host(y), want) <= TOL
 
 
+@pytest.mark.parametrize("C,T", [(48, 85995), (384, 1344)])
+def test_group_norm_without_grid_sync(device, ops, C, T, monkeypatch):
+    """STX_NO_GRID_SYNC=1 sends shapes that take the single pass to the two-kernel path: both
+    paths give the oracle's result."""
+    x = randn(device, (C, 1, T), 60 + C, 1.3, -0.4)
+    w, b = randn(device, (C, 1, 1), 61), randn(device, (C, 1, 1), 62)
+    want = ops.group_norm(host(x), 1, 1e-5, host(w), host(b), gelu=True)
+    y1 = host(stx.group_norm(x, 1, 1e-5, w, b, gelu=True))
+    monkeypatch.setenv("STX_NO_GRID_SYNC", "1")
+    y2 = host(stx.group_norm(x, 1, 1e-5, w, b, gelu=True))
+    assert rel_err(y1, want) <= TOL and rel_err(y2, want) <= TOL
+
+
 def test_group_norm_errors(device):
     import torch
     x = randn(device, (4, 1, 100), 10)
