@@ -647,26 +647,27 @@ __global__ __launch_bounds__(256) void ew_flat_kernel(const float* __restrict__ 
 // ----------------------------------------------------------------------- GROUP_NORM
 // Groups: for each i3, channels (ne2) [g*cpg, min((g+1)*cpg, ne2)) with cpg = ceil(ne2 / G),
 // normalised together over ne0 x ne1 x channels (ggml_group_norm). Contiguous tensors only,
-// so a group is one contiguous span of floats (fewer than 2^32 of them).
-//   pass 1 (gn_partial_kernel): one block per chunk of a group writes the chunk's sums of d
-//     and d^2 in double, d = x - K with K the group's first element (the shift removes a
-//     common offset, so S2 - S1^2/N loses only ~1e-16 ((mean - K)/sigma)^2 relative); the
+// so a group is one contiguous span of floats (fewer than 2^32 of them). Statistics are the
+// double sums of d and d^2, d = x - K with K the group's first element (the shift removes a
+// common offset, so S2 - S1^2/N loses only ~1e-16 ((mean - K)/sigma)^2 relative), added in a
+// fixed order so that every block gets the same statistics bit for bit, deterministically and
+// without atomics; the output ((x - mean) / sqrt(M2/N + eps)) [* w + b] [-> gelu] is formed in
+// double up to the GELU, which takes the double itself.
+//   Single pass (gn_fused_kernel, below) when every group's blocks fit on the device at once:
+//     x is read once, the blocks exchange their partial sums (grid_sync.hpp).
+//   Otherwise two passes:
+//   pass 1 (gn_partial_kernel): one block per chunk of a group writes the chunk's sums; the
 //     first block also stores K, so that pass 2 does not re-read x[0] (x may be y);
 //   pass 2 (gn_apply_kernel): every block issues its chunk's loads and its affine parameters
-//     first, then adds up all of its group's partial sums in a fixed order (so every block gets
-//     the same statistics bit for bit, deterministically, without atomics) and writes
-//     ((x - mean) / sqrt(M2/N + eps)) [* w + b] [-> gelu], in double up to the GELU, which
-//     takes the double as a float head and tail.
-// A single pass would need a grid-wide barrier; same-address atomics serialise across the
-// eight XCDs (about 0.1 us per arriving block, measured), which costs more than the second
-// read of x at these sizes.
+//     first, then adds up all of its group's partial sums and writes its chunk.
 //
-// Workspace: [groups] shift | [groups][partial chunks][2] partial sums.
-// VEC float4 per thread: chunks of 1024 * VEC floats, chosen per launch by the group span
-// (measured at the HTDemucs shapes): pass 1 uses 4 from 2M floats, 2 from 768K, else 1 (more,
-// shorter blocks for small groups); pass 2 uses 1 (more blocks, shorter latency chains) unless
-// a launch has at least kGnWideBlocks chunks of 4096 floats, where 4 amortises each block's
-// statistics over four times as many elements.
+// Workspace: the single pass's area (kGridSyncBytes) | [groups] shift | [groups][partial
+// chunks][2] partial sums.
+// Two-pass VEC float4 per thread: chunks of 1024 * VEC floats, chosen per launch by the group
+// span (measured at the HTDemucs shapes): pass 1 uses 4 from 2M floats, 2 from 768K, else 1
+// (more, shorter blocks for small groups); pass 2 uses 1 (more blocks, shorter latency chains)
+// unless a launch has at least kGnWideBlocks chunks of 4096 floats, where 4 amortises each
+// block's statistics over four times as many elements.
 constexpr int kGnVecApplyNarrow = 1, kGnVecApplyWide = 4;
 constexpr long long kGnWideBlocks = 768;
 inline int gn_partial_vec(long long span) { return span >= (2LL << 20) ? 4 : span >= (768LL << 10) ? 2 : 1; }
