@@ -124,6 +124,9 @@ __global__ __launch_bounds__(256) void uvr_ola_kernel(UvrArgs a, const float* __
         double div = 0.0;
 #pragma unroll
         for (int j = NK - 1; j >= 0; j--) div = div + (in[e][j] ? wv[e][j] : 0.0);   // ascending chunk order
+        // res / div for every plane as div_rn with one reciprocal per sample (the IEEE quotient);
+        // a zero weight sum keeps the plain division, whose inf / NaN the identity does not give.
+        const double rdiv = 1.0 / div;
 #pragma unroll
         for (int u = 0; u < P; u++) {
             double res = 0.0;
@@ -132,7 +135,8 @@ __global__ __launch_bounds__(256) void uvr_ola_kernel(UvrArgs a, const float* __
                 const double prod = (double)yv[e][u][j] * wv[e][j];
                 res = res + (in[e][j] ? prod : 0.0);
             }
-            if (t < a.len && q0 + u < planes) out[(size_t)(q0 + u) * a.len + t] = (float)(res / div);
+            const double q = div != 0.0 ? div_rn(res, div, rdiv) : res / div;
+            if (t < a.len && q0 + u < planes) out[(size_t)(q0 + u) * a.len + t] = (float)q;
         }
     }
 }
