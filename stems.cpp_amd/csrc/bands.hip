@@ -189,8 +189,8 @@ __device__ __forceinline__ float2 masked_bin(const ScatterArgs& a, const float* 
         ar += (double)m.x;
         ai += (double)m.y;
     }
-    const double d = a.denom[f];
-    const double qr = ar / d, qi = ai / d;
+    const double d = a.denom[f], rd = 1.0 / d;
+    const double qr = div_rn(ar, d, rd), qi = div_rn(ai, d, rd);   // = ar / d, ai / d
     const double zr = z.x, zi = z.y;
     return make_float2((float)(zr * qr - zi * qi), (float)(zr * qi + zi * qr));
 }
@@ -246,14 +246,15 @@ __global__ __launch_bounds__(256) void band_scatter_t_kernel(ScatterArgs a) {
             }
         }
     }
-    const double d = a.denom[f];
+    // ar / d and ai / d as div_rn with one reciprocal per thread (the IEEE quotients).
+    const double d = a.denom[f], rd = 1.0 / d;
     float2* oc = a.out + (((size_t)bt * a.S + s) * a.C + c) * a.T * a.F + f;
 #pragma unroll
     for (int k = 0; k < kScatterFrames; k++) {
         if (t0 + k >= a.T) break;
         float2 o = make_float2(0.f, 0.f);
         if (!(a.zero_dc && f == 0)) {
-            const double qr = ar[k] / d, qi = ai[k] / d;
+            const double qr = div_rn(ar[k], d, rd), qi = div_rn(ai[k], d, rd);
             const double zr = z[k].x, zi = z[k].y;
             o = make_float2((float)(zr * qr - zi * qi), (float)(zr * qi + zi * qr));
         }
