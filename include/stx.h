@@ -414,8 +414,9 @@ STX_API size_t stx_htdemucs_norm_workspace_size(int64_t n);
  * each (v - mean) / (1e-5 + sd) over all 2 C F T values (mean_of and the unbiased std_of,
  * :293-302, in double). stats gets {mean, sd}. workspace: device, 16-byte aligned,
  * stx_htdemucs_norm_workspace_size(2 C F T) bytes, no initialisation needed; calls that share one
- * must not overlap. A segment that fits on the device at once is normalised by one
- * grid-synchronised kernel (do not run another such kernel concurrently on the device). */
+ * must not overlap. A segment that fits on the device at once (and whose output does not
+ * overlap its input) is normalised by one grid-synchronised kernel, with the bounded waits and
+ * the same-bits fallback of stx_group_norm; the rest take three kernels. */
 STX_API stx_status stx_htdemucs_cac_normalize(const float* spec, int channels, int n_bins, int n_frames, float* mag,
                                               double* stats, void* workspace, size_t workspace_bytes,
                                               stx_stream stream);
@@ -515,15 +516,27 @@ typedef struct {
  * normalised over ne0 x ne1 x its channels with the biased variance. weight and bias (either
  * may be NULL) repeat into a; gelu != 0 applies GELU-erf last. a and dst must be contiguous
  * (dst may be a). workspace: device, 256-byte aligned, stx_group_norm_workspace_size() bytes,
- * no initialisation needed; it keeps a generation number per group between calls, and calls
- * that share a workspace must not run concurrently. Groups that fit on the device at once run
- * as one grid-synchronised kernel whose blocks must all be resident together: do not run
- * another grid-synchronised kernel concurrently on the same device (its waits are bounded: a
- * block that cannot complete them writes NaN instead of hanging). */
+ * no initialisation needed; calls that share a workspace must not run concurrently.
+ * Results are deterministic and the same bits whichever path a call takes:
+ *   - groups that fit on the device at once (at most 8 groups, all blocks resident together)
+ *     with dst not overlapping a run as one grid-synchronised kernel. Its blocks wait for one
+ *     another with bounded waits; a block whose wait gives up (blocks that never became
+ *     resident: another process or a concurrent kernel holding CUs) computes its group's
+ *     statistics itself from a, in the same order, and counts itself in the workspace's
+ *     fallback word (stx_grid_sync_fallbacks). Streams created with a CU mask, HSA_CU_MASK,
+ *     ROC_GLOBAL_CU_MASK and STX_NO_GRID_SYNC=1 select the two-kernel path;
+ *   - everything else runs as two kernels (three for groups of more than 2^21 floats at
+ *     VEC 4). */
 STX_API size_t     stx_group_norm_workspace_size(const stx_tensor* a, int n_groups);
 STX_API stx_status stx_group_norm(const stx_tensor* a, const stx_tensor* dst, int n_groups, float eps,
                                   const stx_tensor* weight, const stx_tensor* bias, int gelu, void* workspace,
                                   size_t workspace_bytes, stx_stream stream);
+
+/* Blocks of grid-synchronised kernels that ran on `workspace` (a group-norm or HTDemucs
+ * normalisation workspace) and computed their statistics themselves because a wait gave up: a sticky count, read
+ * synchronously (the caller synchronises the streams that used the workspace first). Not
+ * part of the reference; a diagnostic for callers that share the device. */
+STX_API stx_status stx_grid_sync_fallbacks(const void* workspace, uint32_t* count);
 
 /* ggml_norm(a, eps) over ne0 (src/htdemucs.cpp:215): (x - mean) / sqrt(var + eps). */
 STX_API stx_status stx_norm(const stx_tensor* a, const stx_tensor* dst, float eps, stx_stream stream);

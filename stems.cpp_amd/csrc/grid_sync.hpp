@@ -4,72 +4,75 @@
 //
 // Every block of a group publishes its partial sums (s1, s2); block 0 of the group waits for
 // all of them (one record per block, polled by one thread each: no same-address atomics), adds
-// them in block order and publishes the totals; the other blocks wait for the totals. Every
+// them in a fixed order and publishes the totals; the other blocks wait for the totals. Every
 // block thus gets the same totals bit for bit, and the data is read from HBM once in one launch.
-// All blocks of a launch must be resident at once: the host checks the occupancy first
-// (resident_blocks) and takes another path when they would not be.
+// The host checks first that all blocks of a launch can be resident at once (resident_blocks)
+// and takes a multi-kernel path when they cannot.
 //
-// Records are (s1, s2, tag) with tag = a 64-bit hash of s1, s2 and the call's key (token << 32 |
-// gen + 1): the token is a per-call random number from the host, gen a per-group generation
-// number kept in the workspace that block 0 advances once every block has read it. A reader
-// takes a record only when its tag matches the values it read under the current key, so the
-// three words need no write ordering (a torn or stale record fails the check), graph replays
-// of one call (same token) wait for a new gen each time, and neither a record of another call
-// nor garbage in a fresh workspace passes: the workspace needs no initialisation or clearing.
-// Cross-block words are device-scope relaxed atomics, which gfx950 performs at the device's
-// coherence point (sc1), past the XCD's own L2: no L2 write-back or invalidation, which a
-// release/acquire pair would cost per block. Every wait is bounded: a block that gives up
-// (which needs blocks that never become resident, e.g. two such kernels sharing the device)
-// reports it, and the kernels then write NaN instead of hanging.
+// Records are (s1, s2, tag) with tag = a 64-bit hash of s1, s2 and the launch's key. The key is
+// the hardware's name for this dispatch: the AQL packet's dispatch id (its index in its queue,
+// 64 bits, never reused by that queue) hashed with the queue's address. Every block of a launch
+// reads the same key, graph replays get new ones, and a record of an earlier launch, a torn
+// record or garbage in a fresh workspace fails the check: the workspace needs no initialisation
+// and no per-launch state. Cross-block words are device-scope relaxed atomics, which gfx950
+// performs at the device's coherence point, past the XCD's own L2.
+//
+// Every wait is bounded (spin_limit polls). A block whose wait gives up (blocks that never
+// became resident: another process or a concurrent kernel holding CUs, a CU-masked queue)
+// computes its group's totals itself from the input, chunk by chunk in the same order and with
+// the same arithmetic as the blocks and the collector, so its output is bit-identical to the
+// normal path's; it counts itself in the workspace's fallback word (stx_grid_sync_fallbacks).
+// That needs the input unchanged until every block has read it: the callers take the single
+// pass only when the output does not overlap the input.
 #pragma once
 
 #include <atomic>
-#include <chrono>
 #include <cstdlib>
 #include <mutex>
 #include <vector>
 
 #include "common.hpp"
 
+// The AQL packet's dispatch id (user SGPRs set up by the command processor).
+extern "C" __device__ unsigned long long stx_amdgcn_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
+
 namespace stx {
 
 constexpr int kGridThreads = 512;                    // threads per block of the single-pass kernels
-constexpr int kGridMaxBlocks = 512;                  // per group
+constexpr int kGridMaxBlocks = 512;                  // per group (one collector thread per block)
 constexpr int kGridMaxGroups = 8;
 constexpr int kGridStatCopies = 8;                   // waiters poll copy (block % 8)
 constexpr int kGridStatStride = 128;                 // unsigned long longs between copies (1 KB)
-constexpr unsigned kGridSpinLimit = 1u << 18;        // polls of about 1 us each
+constexpr unsigned kGridSpinLimit = 1u << 16;        // polls of about 1 us each
 
-// Workspace area, at a fixed offset with a fixed size so that a workspace shared by calls of
-// different shapes keeps each group slot's generation number consistent: [8 KB) totals
-// records, 8 per group at 1 KB apart | [256 B) generation numbers | partial sums records,
-// 3 words per block.
+// Workspace area: [8 KB) totals records, 8 per group at 1 KB apart | [256 B) the fallback
+// counter | partial sums records, 3 words per block.
 constexpr size_t kGridSyncStat = 0;
-constexpr size_t kGridSyncGen = sizeof(unsigned long long) * kGridStatCopies * kGridStatStride;
-constexpr size_t kGridSyncPart = kGridSyncGen + 256;
+constexpr size_t kGridSyncFallback = sizeof(unsigned long long) * kGridStatCopies * kGridStatStride;
+constexpr size_t kGridSyncPart = kGridSyncFallback + 256;
 constexpr size_t kGridSyncBytes =
     (kGridSyncPart + sizeof(unsigned long long) * 3 * kGridMaxGroups * kGridMaxBlocks + 255) / 256 * 256;
-static_assert(3 * kGridMaxGroups <= kGridStatStride && 4 * kGridMaxGroups <= 256, "grid sync area layout");
+static_assert(3 * kGridMaxGroups <= kGridStatStride, "grid sync area layout");
 
 struct GridSync {
-    unsigned* gen;                   // [kGridMaxGroups]
     unsigned long long* stat;        // [kGridStatCopies][kGridStatStride]: group g's totals record at 3g
     unsigned long long* part;        // [kGridMaxGroups][kGridMaxBlocks][3]: partial sums records
-    unsigned token;
+    unsigned* fallbacks;             // blocks that computed their totals themselves (sticky)
     unsigned spin_limit;
 };
 
 // Sums of two doubles over an NT-thread block: wave sums, then the wave totals added in wave
 // order by every thread (the same order in every block). red holds 2 * NT / 64 doubles.
+// Returns the OR of `flag` over the block (folded into the first barrier).
 template <int NT>
-__device__ __forceinline__ void block_sum2_n(double& a, double& b, double* red) {
+__device__ __forceinline__ bool block_sum2_or(double& a, double& b, double* red, bool flag) {
     constexpr int W = NT / 64;
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) {
         a += __shfl_xor(a, m, 64);
         b += __shfl_xor(b, m, 64);
     }
-    __syncthreads();
+    const bool any = __syncthreads_or(flag);
     if (threadIdx.x % 64 == 0) {
         red[threadIdx.x / 64] = a;
         red[W + threadIdx.x / 64] = b;
@@ -82,6 +85,12 @@ __device__ __forceinline__ void block_sum2_n(double& a, double& b, double* red) 
         a += red[w];
         b += red[W + w];
     }
+    return any;
+}
+
+template <int NT>
+__device__ __forceinline__ void block_sum2_n(double& a, double& b, double* red) {
+    (void)block_sum2_or<NT>(a, b, red, false);
 }
 
 __device__ __forceinline__ void sync_store(unsigned long long* p, unsigned long long v) {
@@ -99,6 +108,11 @@ __device__ __forceinline__ unsigned long long fmix64(unsigned long long k) {
     k ^= k >> 33;
     return k;
 }
+// Key of group gt in this launch.
+__device__ __forceinline__ unsigned long long launch_key(int gt) {
+    const unsigned long long q = (unsigned long long)__builtin_amdgcn_queue_ptr();
+    return fmix64(stx_amdgcn_dispatch_id() ^ fmix64(q)) + (unsigned long long)gt;
+}
 __device__ __forceinline__ unsigned long long record_tag(unsigned long long a, unsigned long long b,
                                                          unsigned long long key) {
     return fmix64(a ^ fmix64(b ^ fmix64(key)));
@@ -111,7 +125,8 @@ __device__ __forceinline__ void record_store(unsigned long long* r, double s1, d
     sync_store(r + 1, b);
     sync_store(r + 2, record_tag(a, b, key));
 }
-// Polls r (at most limit times) until it holds a record under key; false if it never did.
+// Polls r (at most limit times after the first look) until it holds a record under key;
+// false if it never did.
 __device__ __forceinline__ bool record_wait(const unsigned long long* r, unsigned long long key, unsigned limit,
                                             double& s1, double& s2) {
     for (unsigned spins = 0;;) {
@@ -126,19 +141,18 @@ __device__ __forceinline__ bool record_wait(const unsigned long long* r, unsigne
     }
 }
 
-// Generation number of group gt for this call, plus one (read at the start of the kernel,
-// before the block publishes anything).
-__device__ __forceinline__ unsigned grid_gen1(const GridSync& f, int gt) {
-    return __hip_atomic_load(f.gen + gt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
-}
-
 // Totals over the nblk blocks of group gt (this block is blockIdx.x) of the block sums s1, s2
-// (the same values in every thread): tot[0..1] (shared) gets them in every block. gen1 is
-// grid_gen1() read at the start. Returns true when a wait gave up (every thread agrees).
-template <int NT>
-__device__ __forceinline__ bool grid_totals(const GridSync& f, int gt, int nblk, unsigned gen1, double s1, double s2,
-                                            double* red, double* tot) {
-    const unsigned long long key = (unsigned long long)f.token << 32 | gen1;
+// (the same values in every thread): tot[0..1] (shared) holds them in every block on return.
+// The collector's order: thread t adds the sums of blocks t, t + NT, t + 2 NT, ... in that
+// order, starting from +0.0, then the block adds the threads' sums (block_sum2_or).
+// recompute(tot) is called by every thread of a block whose wait gave up: it must leave the
+// same totals in tot[0..1] from the input, in that order, and end with a barrier. Returns
+// whether it was called (uniform over the block), so that the caller can reload what it kept
+// in registers instead of holding it across the recompute.
+template <int NT, class Recompute>
+__device__ __forceinline__ bool grid_totals(const GridSync& f, int gt, int nblk, double s1, double s2, double* red,
+                                            double* tot, Recompute&& recompute) {
+    const unsigned long long key = launch_key(gt);
     unsigned long long* part = f.part + 3 * (size_t)gt * kGridMaxBlocks;
     bool late = false;
     if (blockIdx.x != 0) {
@@ -150,72 +164,92 @@ __device__ __forceinline__ bool grid_totals(const GridSync& f, int gt, int nblk,
             tot[0] = t1;
             tot[1] = t2;
         }
+        late = __syncthreads_or(late);
     } else {
-        // Block 0 collects: thread t waits for the records of blocks t, t + NT, ... and adds
-        // them in that order (block 0's own sums first), then the block adds the threads' sums
-        // in thread order and publishes the totals, one record per copy.
-        double p1 = threadIdx.x == 0 ? s1 : 0.0, p2 = threadIdx.x == 0 ? s2 : 0.0;
+        double p1 = 0.0, p2 = 0.0;
+        if (threadIdx.x == 0) {
+            p1 += s1;
+            p2 += s2;
+        }
         for (int b = threadIdx.x == 0 ? NT : (int)threadIdx.x; b < nblk && !late; b += NT) {
             double q1 = 0.0, q2 = 0.0;
             late = !record_wait(part + 3 * b, key, f.spin_limit, q1, q2);
             p1 += q1;
             p2 += q2;
         }
-        block_sum2_n<NT>(p1, p2, red);
-        if (threadIdx.x == 0) {
-            tot[0] = p1;
-            tot[1] = p2;
+        late = block_sum2_or<NT>(p1, p2, red, late);
+        if (!late) {
+            if (threadIdx.x == 0) {
+                tot[0] = p1;
+                tot[1] = p2;
 #pragma unroll
-            for (int c = 0; c < kGridStatCopies; c++)
-                record_store(f.stat + c * kGridStatStride + 3 * gt, p1, p2, key);
-            // Every block has read gen before it published its record.
-            __hip_atomic_store(f.gen + gt, gen1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                for (int c = 0; c < kGridStatCopies; c++)
+                    record_store(f.stat + c * kGridStatStride + 3 * gt, p1, p2, key);
+            }
+            __syncthreads();
         }
     }
-    return __syncthreads_or(late);
+    if (late) {                                                // uniform over the block
+        recompute(tot);
+        if (threadIdx.x == 0) {
+            if (blockIdx.x == 0) {                             // blocks still waiting take these
+#pragma unroll
+                for (int c = 0; c < kGridStatCopies; c++)
+                    record_store(f.stat + c * kGridStatStride + 3 * gt, tot[0], tot[1], key);
+            }
+            __hip_atomic_fetch_add(f.fallbacks, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+    }
+    return late;
 }
 
-// A per-call random number: murmur3's 32-bit finaliser of a call counter offset by a
-// per-process seed from the clock.
-inline unsigned grid_call_token() {
-    static const unsigned seed = (unsigned)std::chrono::steady_clock::now().time_since_epoch().count();
-    static std::atomic<unsigned> calls{0};
-    unsigned h = seed + 0x9e3779b9u * calls.fetch_add(1, std::memory_order_relaxed);
-    h ^= h >> 16;
-    h *= 0x85ebca6bu;
-    h ^= h >> 13;
-    h *= 0xc2b2ae35u;
-    h ^= h >> 16;
-    return h;
+// Polls per wait: kGridSpinLimit, or STX_GRID_SYNC_SPIN_LIMIT when set (read at every call;
+// a small value forces the recompute path, for tests).
+inline unsigned grid_spin_limit() {
+    const char* s = std::getenv("STX_GRID_SYNC_SPIN_LIMIT");
+    if (!s || !s[0]) return kGridSpinLimit;
+    char* end = nullptr;
+    const unsigned long v = std::strtoul(s, &end, 10);
+    return end && *end == 0 ? (unsigned)std::min<unsigned long>(v, 1ul << 30) : kGridSpinLimit;
 }
 
 // The sync area of a workspace that starts at ws (8-byte aligned), for one call.
 inline GridSync grid_sync_at(void* ws) {
     char* b = static_cast<char*>(ws);
     GridSync f;
-    f.gen = reinterpret_cast<unsigned*>(b + kGridSyncGen);
     f.stat = reinterpret_cast<unsigned long long*>(b + kGridSyncStat);
+    f.fallbacks = reinterpret_cast<unsigned*>(b + kGridSyncFallback);
     f.part = reinterpret_cast<unsigned long long*>(b + kGridSyncPart);
-    f.token = grid_call_token();
-    f.spin_limit = kGridSpinLimit;
+    f.spin_limit = grid_spin_limit();
     return f;
 }
 
-// Whether the single-pass kernels may run: not when STX_NO_GRID_SYNC is set to anything but
-// "0" (read at every call, for callers that run such kernels concurrently on one device), and
-// not when the process's queues carry a CU mask (HSA_CU_MASK, ROC_GLOBAL_CU_MASK), which would
-// leave fewer CUs than the occupancy check counts.
-inline bool grid_sync_enabled() {
+// Whether the single-pass kernels may run on `stream`: not when STX_NO_GRID_SYNC is set to
+// anything but "0" (read at every call), not when the process's queues carry a CU mask
+// (HSA_CU_MASK, ROC_GLOBAL_CU_MASK), and not on a stream created with a CU mask
+// (hipExtStreamCreateWithCUMask): those leave fewer CUs than the occupancy check counts. The
+// single pass stays correct without them (see above), only slower.
+inline bool grid_sync_enabled(hipStream_t stream) {
     const char* off = std::getenv("STX_NO_GRID_SYNC");
     if (off && off[0] && !(off[0] == '0' && off[1] == 0)) return false;
     static const bool masked = std::getenv("HSA_CU_MASK") || std::getenv("ROC_GLOBAL_CU_MASK");
-    return !masked;
+    if (masked) return false;
+    if (stream == nullptr) return true;
+    uint32_t mask[32] = {};
+    if (hipExtStreamGetCUMask(stream, 32, mask) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    int set = 0;
+    for (uint32_t m : mask) set += __builtin_popcount(m);
+    return set >= device_cus();
 }
 
 // Blocks of `kernel` (kGridThreads threads, no dynamic LDS) that the current device holds at
 // once; 0 when grid_sync_enabled() is false, so that callers take their multi-kernel path.
-inline int resident_blocks(const void* kernel) {
-    if (!grid_sync_enabled()) return 0;
+inline int resident_blocks(const void* kernel, hipStream_t stream) {
+    if (!grid_sync_enabled(stream)) return 0;
     struct Entry {
         const void* k;
         int dev, blocks;
@@ -233,6 +267,12 @@ inline int resident_blocks(const void* kernel) {
               "hipOccupancyMaxActiveBlocksPerMultiprocessor");
     cache.push_back({kernel, dev, cus * per_cu});
     return cus * per_cu;
+}
+
+// Whether [a, a + an) and [b, b + bn) (bytes) overlap.
+inline bool overlaps(const void* a, size_t an, const void* b, size_t bn) {
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    return x < y + bn && y < x + an;
 }
 
 }  // namespace stx

@@ -12,8 +12,9 @@
 // The moments (mean_of / std_of, :293-302: double sums of d = x - x[0], so no cancellation
 // occurs, and the unbiased std) and the normalisation run as one grid-synchronised kernel when
 // the input fits in the registers of blocks that are all resident at once (one segment's
-// spectrum or waveform): each block loads its chunk once, the blocks exchange their partial
-// sums (grid_sync.hpp) and normalise from registers. Otherwise (the whole mix of separate())
+// spectrum or waveform) and the output does not overlap the input: each block loads its chunk
+// once, the blocks exchange their partial sums (grid_sync.hpp) and normalise from registers.
+// Otherwise (the whole mix of separate())
 // three kernels: pass 1 writes one (sum d, sum d^2) pair in double per 8192 floats, one block
 // adds them in a fixed order into {mean, sd}, and a third kernel normalises. The split's
 // overlap-add is in gather form: each output sample sums, in chunk order and in float like the
@@ -181,18 +182,11 @@ __global__ __launch_bounds__(256) void normalize_kernel(const float* x, float* y
 // spectrum [C][ft] read as 2 C ft floats), VEC float4 per thread in chunks of kGridThreads * 4 *
 // VEC floats. Same statistics formulas as moments_final_kernel and the same per-element division
 // as normalize_kernel; block 0 writes {mean, sd} to stats.
-template <int KIND, int VEC>
-__global__ __launch_bounds__(kGridThreads) void norm_fused_kernel(const float* x, float* y, long long n, long long ft,
-                                                                  double* stats, GridSync f) {
+//
+// This thread's values of the chunk at lo (clamped loads past n; counted only where in range).
+template <int VEC>
+__device__ __forceinline__ void norm_load(const float* x, long long n, long long lo, bool vec, float (&v)[VEC][4]) {
     constexpr int NT = kGridThreads;
-    constexpr long long CH = NT * 4 * VEC;
-    __shared__ double red[2 * NT / 64];
-    __shared__ double tot[2];
-    const long long lo = (long long)blockIdx.x * CH;
-    const int nch = (int)((n + CH - 1) / CH);
-    const unsigned gen1 = grid_gen1(f, 0);
-    const bool vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && n % 4 == 0;
-    float v[VEC][4];
 #pragma unroll
     for (int k = 0; k < VEC; k++) {
         const long long p = lo + (k * NT + (long long)threadIdx.x) * 4;
@@ -204,24 +198,68 @@ __global__ __launch_bounds__(kGridThreads) void norm_fused_kernel(const float* x
             v[k][3] = q.w;
         } else {
 #pragma unroll
-            for (int j = 0; j < 4; j++) v[k][j] = x[min(p + j, n - 1)];      // clamped; counted only if p + j < n
+            for (int j = 0; j < 4; j++) v[k][j] = x[min(p + j, n - 1)];
         }
     }
-    const double shift = (double)x[0];                         // read before any block writes y
-    double s1 = 0.0, s2 = 0.0;
+}
+
+// Block sums of d = v - shift over the chunk at lo, in every thread: each thread adds its
+// values in (k, j) order, then block_sum2_n.
+template <int VEC>
+__device__ __forceinline__ void norm_sums(const float (&v)[VEC][4], long long n, long long lo, double shift, double* red,
+                                          double& s1, double& s2) {
+    constexpr int NT = kGridThreads;
+    s1 = 0.0;
+    s2 = 0.0;
 #pragma unroll
     for (int k = 0; k < VEC; k++)
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const bool in = lo + (k * NT + (long long)threadIdx.x) * 4 + j < n;
             const double d = in ? (double)v[k][j] - shift : 0.0;
-            s1 += d;
-            s2 += d * d;
+            s1 = s1 + d;
+            s2 = fma(d, d, s2);
         }
     block_sum2_n<NT>(s1, s2, red);
-    const bool timed_out = grid_totals<NT>(f, 0, nch, gen1, s1, s2, red, tot);
+}
+
+template <int KIND, int VEC>
+__global__ __launch_bounds__(kGridThreads) void norm_fused_kernel(const float* x, float* y, long long n, long long ft,
+                                                                  double* stats, GridSync f) {
+    constexpr int NT = kGridThreads;
+    constexpr long long CH = NT * 4 * VEC;
+    __shared__ double red[2 * NT / 64];
+    __shared__ double tot[2];
+    const long long lo = (long long)blockIdx.x * CH;
+    const int nch = (int)((n + CH - 1) / CH);
+    const bool vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && n % 4 == 0;
+    float v[VEC][4];
+    norm_load<VEC>(x, n, lo, vec, v);
+    const double shift = (double)x[0];
+    double s1, s2;
+    norm_sums<VEC>(v, n, lo, shift, red, s1, s2);
+    // A block whose wait gave up adds every chunk's sums itself, in the collector's order.
+    grid_totals<NT>(f, 0, nch, s1, s2, red, tot, [&](double* t) {
+        double p1 = 0.0, p2 = 0.0;
+        for (int m = 0; m < nch; m++) {
+            float w[VEC][4];
+            norm_load<VEC>(x, n, m * CH, vec, w);
+            double q1, q2;
+            norm_sums<VEC>(w, n, m * CH, shift, red, q1, q2);
+            if ((int)threadIdx.x == m % NT) {
+                p1 += q1;
+                p2 += q2;
+            }
+        }
+        block_sum2_n<NT>(p1, p2, red);
+        if (threadIdx.x == 0) {
+            t[0] = p1;
+            t[1] = p2;
+        }
+        __syncthreads();
+    });
     const double nn = (double)n, s = tot[0], q = tot[1];
-    const double mean = timed_out ? __builtin_nan("") : shift + s / nn;
+    const double mean = shift + s / nn;
     const double sd = sqrt(fmax(q - s * (s / nn), 0.0) / (nn - 1.0));
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         stats[0] = mean;
@@ -521,7 +559,10 @@ bool try_norm_fused(const float* x, float* y, long long n, long long ft, double*
     const long long ch = (long long)kGridThreads * 4 * VEC;
     const long long nch = (n + ch - 1) / ch;
     if (nch > kGridMaxBlocks) return false;
-    if (nch > resident_blocks(reinterpret_cast<const void*>(&norm_fused_kernel<NK, VEC>))) return false;
+    // The single pass needs x unchanged until every block has read it (a block whose wait gives
+    // up re-reads all of x): y must not overlap x (y has as many floats as x).
+    if (overlaps(x, sizeof(float) * (size_t)n, y, sizeof(float) * (size_t)n)) return false;
+    if (nch > resident_blocks(reinterpret_cast<const void*>(&norm_fused_kernel<NK, VEC>), s)) return false;
     hipLaunchKernelGGL((norm_fused_kernel<NK, VEC>), dim3((unsigned)nch), dim3(kGridThreads), 0, s, x, y, n, ft, stats,
                        grid_sync_at(ws));
     launch_check("norm_fused_kernel");

@@ -109,7 +109,7 @@ __device__ __forceinline__ float rcp_nr(float d) {
 // gelu_erf_hl takes its argument as a float head x plus a small tail dx (x + dx is the value)
 // so that a fused producer can hand over a double result without rounding it first: in the
 // negative tail d ln gelu / d ln x ~ 1 + x^2, so one ulp of input rounding would become ~x^2
-// ulps of output error; gelu_erf_d takes the double itself.
+// ulps of output error; gelu_erf_dt takes the double itself.
 
 // Phi(-|x|) = e erfcx(|x|/sqrt2) / 2, given e = exp(-x^2/2).
 __device__ __forceinline__ float gelu_phi_neg(float x, float e) {
@@ -146,16 +146,37 @@ __device__ __forceinline__ float gelu_erf_hl(float x, float dx) {
     return x > 10.f ? x + dx : x < -15.f ? x * 0.f : fmaf(ph, dx, x * ph);
 }
 
-// gelu of a double argument (a fused producer's result before rounding), the same
+// gelu of a double argument t (a fused producer's result before rounding), the same
 // approximation with the exponent -t^2 / (2 ln 2) formed in double instead of as a float head
-// and tail, and one rounding of t Phi(t) at the end.
-__device__ __forceinline__ float gelu_erf_d(double t) {
+// and tail, and one rounding of t Phi(t) at the end. Branch- and select-free in the ranges the
+// float formula has to clamp: the 1/2 is folded into P's coefficients (exact), t > ~5.3 gives
+// Q < 2^-25, so Phi = 1 - Q = 1 exactly and the result is t rounded; t < ~-13.2 underflows Q to
+// 0 (the exponent is floored at -200 so that 2^n stays finite), giving t * 0 = -0 as the float
+// formula's x * 0; |t| is capped at 1e30 in the reciprocal's argument so that +inf gives inf
+// (not 0 * inf in the Newton step), -inf gives NaN like x * (1 + erf(x/sqrt2)) / 2, NaN stays NaN.
+// About 30 VALU instructions; the float32 simulation of these steps (hardware exp2 and rcp
+// taken 1 ulp off) against erfc in double stays within 8.3 ulp on [-15, 10].
+__device__ __forceinline__ float gelu_erf_dt(double t) {
     const float x = (float)t;
     const double y = t * t * -0x1.71547652b82fep-1;
-    const double n = rint(fmax(y, -200.0));               // |t| > 15 is selected away below
-    const float g = gelu_phi_neg(x, ldexpf(__builtin_amdgcn_exp2f((float)(y - n)), (int)n));
-    const float ph = x < 0.f ? g : 1.f - g;
-    return x > 10.f ? x : x < -15.f ? x * 0.f : (float)(t * (double)ph);
+    const double n = rint(fmax(y, -200.0));
+    const float e = ldexpf(__builtin_amdgcn_exp2f((float)(y - n)), (int)n);
+    const float r = rcp_nr(fmaf(fminf(fabsf(x), 1e30f), 0.35355339059327376220f, 1.f));   // 1 / (1 + |x| / (2 sqrt2))
+    float p = -1.5161373655e-02f;                         // P / 2 (see gelu_phi_neg)
+    p = fmaf(p, r, 9.183117002e-02f);
+    p = fmaf(p, r, -2.2204872965e-01f);
+    p = fmaf(p, r, 2.545801103e-01f);
+    p = fmaf(p, r, -1.139718890e-01f);
+    p = fmaf(p, r, 4.3268962765e-03f);
+    p = fmaf(p, r, -3.3629499375e-02f);
+    p = fmaf(p, r, -1.2177567695e-03f);
+    p = fmaf(p, r, 4.1566714645e-02f);
+    p = fmaf(p, r, 8.82191360e-02f);
+    p = fmaf(p, r, 1.234102100e-01f);
+    p = fmaf(p, r, 1.4104762675e-01f);
+    p = fmaf(p, r, 1.410473883e-01f);
+    const float g = e * (r * p);                          // Phi(-|t|)
+    return (float)(t * (double)(x < 0.f ? g : 1.f - g));
 }
 
 __device__ __forceinline__ float gelu_erf(float x) { return gelu_erf_hl(x, 0.f); }
@@ -647,57 +668,73 @@ __global__ __launch_bounds__(256) void ew_flat_kernel(const float* __restrict__ 
 // ----------------------------------------------------------------------- GROUP_NORM
 // Groups: for each i3, channels (ne2) [g*cpg, min((g+1)*cpg, ne2)) with cpg = ceil(ne2 / G),
 // normalised together over ne0 x ne1 x channels (ggml_group_norm). Contiguous tensors only,
-// so a group is one contiguous span of floats (fewer than 2^32 of them). Statistics are the
-// double sums of d and d^2, d = x - K with K the group's first element (the shift removes a
-// common offset, so S2 - S1^2/N loses only ~1e-16 ((mean - K)/sigma)^2 relative), added in a
-// fixed order so that every block gets the same statistics bit for bit, deterministically and
-// without atomics; the output ((x - mean) / sqrt(M2/N + eps)) [* w + b] [-> gelu] is formed in
-// double up to the GELU, which takes the double itself.
-//   Single pass (gn_fused_kernel, below) when every group's blocks fit on the device at once:
-//     x is read once, the blocks exchange their partial sums (grid_sync.hpp).
-//   Otherwise two passes:
-//   pass 1 (gn_partial_kernel): one block per chunk of a group writes the chunk's sums; the
-//     first block also stores K, so that pass 2 does not re-read x[0] (x may be y);
-//   pass 2 (gn_apply_kernel): every block issues its chunk's loads and its affine parameters
-//     first, then adds up all of its group's partial sums and writes its chunk.
+// so a group is one contiguous span of floats (fewer than 2^32 of them).
 //
-// Workspace: the single pass's area (kGridSyncBytes) | [groups] shift | [groups][partial
-// chunks][2] partial sums.
-// Two-pass VEC float4 per thread: chunks of 1024 * VEC floats, chosen per launch by the group
-// span (measured at the HTDemucs shapes): pass 1 uses 4 from 2M floats, 2 from 768K, else 1
-// (more, shorter blocks for small groups); pass 2 uses 1 (more blocks, shorter latency chains)
-// unless a launch has at least kGnWideBlocks chunks of 4096 floats, where 4 amortises each
-// block's statistics over four times as many elements.
-constexpr int kGnVecApplyNarrow = 1, kGnVecApplyWide = 4;
-constexpr long long kGnWideBlocks = 768;
-inline int gn_partial_vec(long long span) { return span >= (2LL << 20) ? 4 : span >= (768LL << 10) ? 2 : 1; }
-template <int VEC> constexpr int gn_chunk() { return 256 * 4 * VEC; }
+// Statistics: the double sums of d and d^2, d = x - K with K the group's first element (the
+// shift removes a common offset, so S2 - S1^2/N loses only ~1e-16 ((mean - K)/sigma)^2
+// relative). They are added in ONE order that every path shares, so that every path gives
+// the same statistics bit for bit, deterministically and without atomics:
+//   - a group is cut into chunks of kGnThreads * 4 * VEC floats, VEC in {1, 2, 4} chosen from
+//     the group's span alone (gn_vec); thread t of a chunk holds float4 k at
+//     chunk start + (k * kGnThreads + t) * 4 and adds its values in (k, j) order;
+//   - a chunk's partial sums are the threads' sums added by block_sum2_n;
+//   - the totals: thread t adds the partials of chunks t, t + kGnThreads, ... from +0.0, then
+//     block_sum2_n over the threads (the collector of grid_totals, gn_fold).
+// The output is t = x * a + d with a = rstd * w, d = b - mean * a in double, then rounded, or
+// GELU of the double t (its negative tail is ill-conditioned: d ln gelu / d ln t ~ 1 + t^2).
+//
+// Paths, by shape:
+//   single pass (gn_fused_kernel) when the groups fit on the device at once and y does not
+//     overlap x: x is read once, the blocks exchange their partial sums (grid_sync.hpp);
+//   two passes otherwise: gn_partial_kernel writes each chunk's partial sums (and K), then
+//     gn_apply_kernel folds its group's partials itself (or reads gn_fold_kernel's totals when
+//     a group has more than kGnFoldDirect chunks) and writes its chunk.
+// Affine per channel with planes of at least 256 floats (the HTDemucs shapes) takes a
+// per-wave path: a wave's 256 consecutive elements lie in at most two channels, whose
+// parameters it loads once (wave-uniform) before the statistics are known and turns into
+// (a, d) once after; every element then costs one conversion and one fma before its GELU.
+//
+// Workspace: the single pass's area (kGridSyncBytes) | shift [groups] | totals [groups][2] |
+// chunk partials [groups][chunks][2].
+constexpr int kGnThreads = kGridThreads;
+constexpr int kGnFoldDirect = 1024;
+template <int VEC> constexpr unsigned gn_chunk() { return kGnThreads * 4u * VEC; }
+// The smallest width whose chunks cover the group in at most kGridMaxBlocks chunks (the single
+// pass's limit), else 4.
+inline int gn_vec(long long span) {
+    if (span <= (long long)kGridMaxBlocks * gn_chunk<1>()) return 1;
+    if (span <= (long long)kGridMaxBlocks * gn_chunk<2>()) return 2;
+    return 4;
+}
 
-enum AffineKind { AFF_NONE = 0, AFF_CHANNEL = 1, AFF_NE0 = 2, AFF_GENERAL = 3 };
+// CHANNEL: p[c]; NE0: p[i0]; GENERAL: broadcast over all four dimensions; CHANNEL_WAVE:
+// p[c] taken once per wave (per channel affine, planes of >= 256 floats).
+enum AffineKind { AFF_NONE = 0, AFF_CHANNEL = 1, AFF_NE0 = 2, AFF_GENERAL = 3, AFF_CHANNEL_WAVE = 4 };
 
 struct Affine {
     const float* p;
     long long ne[4];                     // broadcast extents (elements)
     long long nb[4];                     // strides in floats
-    int kind;                            // CHANNEL: p[c]; NE0: p[i0]; GENERAL: broadcast
+    int kind;
 };
 
 struct GroupNormArgs {
     const float* x;
     float* y;
     Affine w, b;
-    double* shift;           // [groups_total]
-    double* part;            // [groups_total][partial chunks][2]
+    double* shift;           // [groups_total] (two passes)
+    double* tot;             // [groups_total][2] (two passes, separate fold)
+    double* part;            // [groups_total][nch][2] (two passes)
     unsigned ne0, ne1;       // dims of x (ne3 is folded into the group index)
     long long ne2;
     unsigned plane;          // ne0 * ne1
     double rplane, rne0;     // 1/plane, 1/ne0
+    FastDiv plane_div;       // division by plane on the scalar unit
     long long cpg;           // channels per group
     int groups;              // groups per ne3 slice
-    int chunks;              // partial chunks per group (max over groups)
-    int pchunk;              // floats per partial chunk
+    int nch;                 // chunks per group (of the largest group)
     float eps;
-    int vec;                 // all group spans 16-byte aligned
+    int vec;                 // every group span is 16-byte aligned and a multiple of 4 floats
 };
 
 __device__ __forceinline__ void group_span(const GroupNormArgs& a, int gt, long long& begin, unsigned& count,
@@ -710,15 +747,16 @@ __device__ __forceinline__ void group_span(const GroupNormArgs& a, int gt, long 
     count = (unsigned)((c1 - c0) * a.plane);
 }
 
-// Loads this thread's values of chunk [lo, hi) of base: float4 k covers positions
-// lo + (k * NT + tid) * 4 .. +3 (NT threads per block).
-template <int VEC, int NT = 256>
-__device__ __forceinline__ void gn_load(const GroupNormArgs& a, const float* base, unsigned lo, unsigned hi,
-                                        float (&v)[4 * VEC], bool (&ok)[4 * VEC]) {
+// This thread's values of chunk [lo, hi) of base. FULL (a whole chunk of an aligned span):
+// unconditional float4 loads. Otherwise clamped scalar loads (always-valid addresses, so they
+// issue together) and a mask.
+template <int VEC, bool FULL>
+__device__ __forceinline__ void gn_load(const float* base, unsigned lo, unsigned hi, float (&v)[4 * VEC],
+                                        bool (&ok)[4 * VEC]) {
 #pragma unroll
     for (int k = 0; k < VEC; k++) {
-        const unsigned p = lo + (k * NT + threadIdx.x) * 4;
-        if (a.vec && p + 3 < hi) {
+        const unsigned p = lo + (k * kGnThreads + threadIdx.x) * 4;
+        if constexpr (FULL) {
             const float4 q = *reinterpret_cast<const float4*>(base + p);
             v[4 * k] = q.x;
             v[4 * k + 1] = q.y;
@@ -729,65 +767,82 @@ __device__ __forceinline__ void gn_load(const GroupNormArgs& a, const float* bas
         } else {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                ok[4 * k + j] = p + j < hi;
-                v[4 * k + j] = ok[4 * k + j] ? base[p + j] : 0.f;
+                const unsigned e = p + j;
+                const float t = base[min(e, hi - 1)];
+                ok[4 * k + j] = e < hi;
+                v[4 * k + j] = ok[4 * k + j] ? t : 0.f;
             }
         }
     }
 }
 
-// Sums of two doubles over a 256-thread block in a fixed order. red holds 8 doubles.
-__device__ __forceinline__ void block_sum2(double& a, double& b, double* red) {
-    a = group_sum<kWave>(a);
-    b = group_sum<kWave>(b);
-    __syncthreads();
-    if (threadIdx.x % kWave == 0) {
-        red[threadIdx.x / kWave] = a;
-        red[4 + threadIdx.x / kWave] = b;
-    }
-    __syncthreads();
-    a = (red[0] + red[1]) + (red[2] + red[3]);
-    b = (red[4] + red[5]) + (red[6] + red[7]);
-}
-
-// Block partial sums of d = v - shift over this thread's valid values, written to part.
-template <int VEC>
-__device__ __forceinline__ void gn_write_partial(const GroupNormArgs& a, int gt, const float (&v)[4 * VEC],
-                                                 const bool (&ok)[4 * VEC], double shift, double* red) {
-    double s1 = 0.0, s2 = 0.0;
+// The thread's sums of d = v - shift over its valid values, in (k, j) order.
+template <int N>
+__device__ __forceinline__ void gn_thread_sums(const float (&v)[N], const bool (&ok)[N], double shift, double& s1,
+                                               double& s2) {
+    s1 = 0.0;
+    s2 = 0.0;
 #pragma unroll
-    for (int k = 0; k < 4 * VEC; k++) {
+    for (int k = 0; k < N; k++) {
         const double d = ok[k] ? (double)v[k] - shift : 0.0;
-        s1 += d;
-        s2 += d * d;
+        s1 = s1 + d;
+        s2 = fma(d, d, s2);
     }
-    block_sum2(s1, s2, red);
+}
+
+// Partial sums of chunk m of a group (count floats at xg), in every thread.
+template <int VEC>
+__device__ __forceinline__ void gn_chunk_sums(const float* xg, unsigned m, unsigned count, double shift, double* red,
+                                              double& s1, double& s2) {
+    const unsigned lo = m * gn_chunk<VEC>(), hi = min(lo + gn_chunk<VEC>(), count);
+    float v[4 * VEC];
+    bool ok[4 * VEC];
+    gn_load<VEC, false>(xg, lo, hi, v, ok);
+    gn_thread_sums(v, ok, shift, s1, s2);
+    block_sum2_n<kGnThreads>(s1, s2, red);
+}
+
+// A group's totals from x alone, in the collector's order (a single-pass block whose wait
+// gave up): tot[0..1] (shared), then a barrier.
+template <int VEC>
+__device__ __forceinline__ void gn_recompute(const float* xg, unsigned count, int nblk, double shift, double* red, double* tot) {
+    double p1 = 0.0, p2 = 0.0;
+    for (int m = 0; m < nblk; m++) {
+        double q1, q2;
+        gn_chunk_sums<VEC>(xg, (unsigned)m, count, shift, red, q1, q2);
+        if ((int)threadIdx.x == m % kGnThreads) {
+            p1 += q1;
+            p2 += q2;
+        }
+    }
+    block_sum2_n<kGnThreads>(p1, p2, red);
     if (threadIdx.x == 0) {
-        double* p = a.part + ((size_t)gt * a.chunks + blockIdx.x) * 2;
-        p[0] = s1;
-        p[1] = s2;
-        if (blockIdx.x == 0) a.shift[gt] = shift;
+        tot[0] = p1;
+        tot[1] = p2;
     }
+    __syncthreads();
 }
 
-// mean and 1/sqrt(var + eps) of group gt from its partial sums (fixed order).
-__device__ __forceinline__ void gn_stats(const GroupNormArgs& a, int gt, unsigned count, double shift, double* red,
-                                         double& mean, double& rstd) {
-    const int nch = (int)((count + (unsigned)a.pchunk - 1) / (unsigned)a.pchunk);
-    const double* part = a.part + (size_t)gt * a.chunks * 2;
-    double s1 = 0.0, s2 = 0.0;
-    for (int k = threadIdx.x; k < nch; k += 256) {
-        s1 += part[2 * k];
-        s2 += part[2 * k + 1];
+// A group's totals from its nblk chunk partials (two passes), in the collector's order.
+__device__ __forceinline__ void gn_fold(const double* part, int nblk, double* red, double& t1, double& t2) {
+    double p1 = 0.0, p2 = 0.0;
+    for (int m = threadIdx.x; m < nblk; m += kGnThreads) {
+        p1 += part[2 * m];
+        p2 += part[2 * m + 1];
     }
-    block_sum2(s1, s2, red);
-    const double N = (double)count, dm = s1 / N;
+    block_sum2_n<kGnThreads>(p1, p2, red);
+    t1 = p1;
+    t2 = p2;
+}
+
+__device__ __forceinline__ void gn_moments(double t1, double t2, unsigned count, double shift, float eps, double& mean,
+                                           double& rstd) {
+    const double N = (double)count, dm = t1 / N;
     mean = shift + dm;
-    rstd = 1.0 / sqrt(fmax(s2 / N - dm * dm, 0.0) + (double)a.eps);
+    rstd = 1.0 / sqrt(fmax(t2 / N - dm * dm, 0.0) + (double)eps);
 }
 
-// One affine operand at element (channel c, i0, i1, i3) under the kernel's affine mode AK:
-// CHANNEL reads p[c], NE0 reads p[i0], GENERAL broadcasts over all four dimensions.
+// One affine operand at element (channel c, i0, i1, i3) under the per-element kinds.
 template <int AK>
 __device__ __forceinline__ float affine_at(const Affine& f, long long c, unsigned i0, unsigned i1, long long i3) {
     if constexpr (AK == AFF_CHANNEL) return f.p[c];
@@ -795,57 +850,63 @@ __device__ __forceinline__ float affine_at(const Affine& f, long long c, unsigne
     return f.p[(i0 % f.ne[0]) * f.nb[0] + (i1 % f.ne[1]) * f.nb[1] + (c % f.ne[2]) * f.nb[2] + (i3 % f.ne[3]) * f.nb[3]];
 }
 
-// Affine parameters of this thread's elements: channel c and (i0, i1) inside its plane of
-// element p, advanced element by element.
-template <int AK, int VEC, int NT = 256>
-__device__ __forceinline__ void gn_affine(const GroupNormArgs& a, unsigned lo, long long c0, long long i3,
-                                          const bool (&ok)[4 * VEC], float (&wv)[4 * VEC], float (&bv)[4 * VEC]) {
-    if constexpr (AK == AFF_CHANNEL) {
-        if (a.plane >= 4) {
-            // Four consecutive elements lie in channel c or c + 1: two loads of each operand per
-            // group (clamped to a valid channel, unconditional), then a selection per element.
+// Affine parameters of this thread's elements.
+//   CHANNEL_WAVE: per float4 k, the two channels the wave's run [pw, pw + 256) can touch:
+//     w0/b0 of the channel of pw, w1/b1 of the next one (clamped), and bnd, the first element
+//     of the next channel (all wave-uniform).
+//   other kinds: one (w, b) per element.
+template <int AK, int VEC>
+struct GnParams {
+    static constexpr bool kWave = AK == AFF_CHANNEL_WAVE;
+    float w0[kWave ? VEC : 1], w1[kWave ? VEC : 1], b0[kWave ? VEC : 1], b1[kWave ? VEC : 1];
+    unsigned bnd[kWave ? VEC : 1];
+    float w[kWave ? 1 : 4 * VEC], b[kWave ? 1 : 4 * VEC];
+};
+
+template <int AK, int VEC>
+__device__ __forceinline__ void gn_params(const GroupNormArgs& a, unsigned lo, long long c0, long long i3,
+                                          const bool (&ok)[4 * VEC], GnParams<AK, VEC>& pr) {
+    constexpr int NT = kGnThreads;
+    if constexpr (AK == AFF_CHANNEL_WAVE) {
+        const unsigned w64 = (unsigned)__builtin_amdgcn_readfirstlane((int)threadIdx.x) & ~63u;
+        const long long cl = a.ne2 - 1;
 #pragma unroll
-            for (int k = 0; k < VEC; k++) {
-                const unsigned p = lo + (k * NT + threadIdx.x) * 4;
+        for (int k = 0; k < VEC; k++) {
+            const unsigned pw = lo + (k * NT + w64) * 4;
+            const unsigned ca = a.plane_div.div(pw);
+            pr.bnd[k] = (ca + 1) * a.plane;
+            const long long cA = min(c0 + (long long)ca, cl), cB = min(c0 + (long long)ca + 1, cl);
+            pr.w0[k] = a.w.p ? a.w.p[cA] : 1.f;
+            pr.w1[k] = a.w.p ? a.w.p[cB] : 1.f;
+            pr.b0[k] = a.b.p ? a.b.p[cA] : 0.f;
+            pr.b1[k] = a.b.p ? a.b.p[cB] : 0.f;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < VEC; k++) {
+            const unsigned p = lo + (k * NT + threadIdx.x) * 4;
+            long long c = 0;
+            unsigned i0 = 0, i1 = 0;
+            if constexpr (AK == AFF_NE0) {
+                i0 = fast_mod(p, a.ne0, a.rne0);
+            } else {
                 const unsigned cp = fast_div(p, a.plane, a.rplane), q = p - cp * a.plane;
-                const long long cl = a.ne2 - 1;
-                const long long c = min(c0 + cp, cl), c1 = min(c0 + cp + 1, cl);
-                const float w0 = a.w.p ? a.w.p[c] : 1.f, w1 = a.w.p ? a.w.p[c1] : 1.f;
-                const float b0 = a.b.p ? a.b.p[c] : 0.f, b1 = a.b.p ? a.b.p[c1] : 0.f;
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const bool in = ok[4 * k + j], next = q + j >= a.plane;
-                    wv[4 * k + j] = in ? (next ? w1 : w0) : 1.f;
-                    bv[4 * k + j] = in ? (next ? b1 : b0) : 0.f;
-                }
+                c = c0 + cp;
+                i1 = fast_div(q, a.ne0, a.rne0);
+                i0 = q - i1 * a.ne0;
             }
-            return;
-        }
-    }
 #pragma unroll
-    for (int k = 0; k < VEC; k++) {
-        const unsigned p = lo + (k * NT + threadIdx.x) * 4;
-        long long c = 0;
-        unsigned i0 = 0, i1 = 0;
-        if constexpr (AK == AFF_NE0) {
-            i0 = fast_mod(p, a.ne0, a.rne0);
-        } else {
-            const unsigned cp = fast_div(p, a.plane, a.rplane), q = p - cp * a.plane;
-            c = c0 + cp;
-            i1 = fast_div(q, a.ne0, a.rne0);
-            i0 = q - i1 * a.ne0;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const bool in = ok[4 * k + j];
-            wv[4 * k + j] = a.w.p && in ? affine_at<AK>(a.w, c, i0, i1, i3) : 1.f;
-            bv[4 * k + j] = a.b.p && in ? affine_at<AK>(a.b, c, i0, i1, i3) : 0.f;
-            if (++i0 == a.ne0) {
-                i0 = 0;
-                if constexpr (AK != AFF_NE0) {
-                    if (++i1 == a.ne1) {
-                        i1 = 0;
-                        ++c;
+            for (int j = 0; j < 4; j++) {
+                const bool in = ok[4 * k + j];
+                pr.w[4 * k + j] = a.w.p && in ? affine_at<AK>(a.w, c, i0, i1, i3) : 1.f;
+                pr.b[4 * k + j] = a.b.p && in ? affine_at<AK>(a.b, c, i0, i1, i3) : 0.f;
+                if (++i0 == a.ne0) {
+                    i0 = 0;
+                    if constexpr (AK != AFF_NE0) {
+                        if (++i1 == a.ne1) {
+                            i1 = 0;
+                            ++c;
+                        }
                     }
                 }
             }
@@ -853,108 +914,190 @@ __device__ __forceinline__ void gn_affine(const GroupNormArgs& a, unsigned lo, l
     }
 }
 
-template <bool GELU, int VEC, int NT = 256>
-__device__ __forceinline__ void gn_store(const GroupNormArgs& a, float* yg, unsigned lo, unsigned hi, double mean,
-                                         double rstd, const float (&v)[4 * VEC], const bool (&ok)[4 * VEC],
-                                         const float (&wv)[4 * VEC], const float (&bv)[4 * VEC]) {
-#pragma unroll 1
+template <bool GELU>
+__device__ __forceinline__ float gn_out(double t) {
+    if constexpr (GELU) return gelu_erf_dt(t);
+    else return (float)t;
+}
+
+// Writes this thread's outputs of chunk [lo, hi) at yg.
+template <int AK, bool GELU, int VEC, bool FULL>
+__device__ __forceinline__ void gn_write(float* yg, unsigned lo, unsigned hi, double mean, double rstd,
+                                         const float (&v)[4 * VEC], const bool (&ok)[4 * VEC],
+                                         const GnParams<AK, VEC>& pr) {
+    constexpr int NT = kGnThreads;
+#pragma unroll
     for (int k = 0; k < VEC; k++) {
         const unsigned p = lo + (k * NT + threadIdx.x) * 4;
-        if (p >= hi) continue;
         float o[4];
+        if constexpr (AK == AFF_CHANNEL_WAVE) {
+            const double a0 = rstd * (double)pr.w0[k], d0 = fma(-mean, a0, (double)pr.b0[k]);
+            const unsigned pw = (unsigned)__builtin_amdgcn_readfirstlane((int)p);
+            if (pw + 255 < pr.bnd[k]) {                        // the wave's run is in one channel
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const double t = fma(((double)v[4 * k + j] - mean) * rstd, (double)wv[4 * k + j], (double)bv[4 * k + j]);
-            if constexpr (GELU) o[j] = gelu_erf_d(t);
-            else o[j] = (float)t;
+                for (int j = 0; j < 4; j++) o[j] = gn_out<GELU>(fma((double)v[4 * k + j], a0, d0));
+            } else {
+                const double a1 = rstd * (double)pr.w1[k], d1 = fma(-mean, a1, (double)pr.b1[k]);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const bool nx = p + j >= pr.bnd[k];
+                    o[j] = gn_out<GELU>(fma((double)v[4 * k + j], nx ? a1 : a0, nx ? d1 : d0));
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const double aj = rstd * (double)pr.w[4 * k + j];
+                o[j] = gn_out<GELU>(fma((double)v[4 * k + j], aj, fma(-mean, aj, (double)pr.b[4 * k + j])));
+            }
         }
-        if (a.vec && p + 3 < hi) {
+        if constexpr (FULL) {
             *reinterpret_cast<float4*>(yg + p) = make_float4(o[0], o[1], o[2], o[3]);
         } else {
 #pragma unroll
             for (int j = 0; j < 4; j++)
                 if (ok[4 * k + j]) yg[p + j] = o[j];
         }
+        // One float4 at a time: interleaving the GELUs of several would need more than the
+        // 128 VGPRs that two blocks per CU leave.
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
-template <int VEC>
-__global__ __launch_bounds__(256) void gn_partial_kernel(GroupNormArgs a) {
-    constexpr int CH = gn_chunk<VEC>();
-    __shared__ double red[8];
-    const int gt = (int)blockIdx.y;
-    long long begin, c0, i3;
-    unsigned count;
-    group_span(a, gt, begin, count, c0, i3);
-    const unsigned lo = blockIdx.x * (unsigned)CH;
-    if (lo >= count) return;                                   // uniform over the block
-    const unsigned hi = min(lo + (unsigned)CH, count);
+// Single pass: a block keeps its chunk of x and its affine parameters in registers, sums d
+// and d^2 and gets the group's totals from the other blocks through grid_totals, then writes
+// y from the registers: x is read from HBM once, in one launch.
+template <int AK, bool GELU, int VEC, bool FULL>
+__device__ __forceinline__ void gn_fused_body(const GroupNormArgs& a, const GridSync& f, int gt, long long begin,
+                                              unsigned count, long long c0, long long i3, unsigned lo, double* red,
+                                              double* tot) {
+    const unsigned hi = min(lo + gn_chunk<VEC>(), count);
+    const int nblk = (int)((count + gn_chunk<VEC>() - 1) / gn_chunk<VEC>());
     const float* xg = a.x + begin;
     float v[4 * VEC];
     bool ok[4 * VEC];
-    gn_load<VEC>(a, xg, lo, hi, v, ok);
-    gn_write_partial<VEC>(a, gt, v, ok, (double)xg[0], red);
-}
-
-template <int AK, bool GELU, int VEC>
-__global__ __launch_bounds__(256) void gn_apply_kernel(GroupNormArgs a) {
-    constexpr int CH = gn_chunk<VEC>();
-    __shared__ double red[8];
-    const int gt = (int)blockIdx.y;
-    long long begin, c0, i3;
-    unsigned count;
-    group_span(a, gt, begin, count, c0, i3);
-    const unsigned lo = blockIdx.x * (unsigned)CH;
-    if (lo >= count) return;                                   // uniform over the block
-    const unsigned hi = min(lo + (unsigned)CH, count);
-    float v[4 * VEC], wv[4 * VEC], bv[4 * VEC];
-    bool ok[4 * VEC];
-    gn_load<VEC>(a, a.x + begin, lo, hi, v, ok);               // in flight while the stats add up
-    gn_affine<AK, VEC>(a, lo, c0, i3, ok, wv, bv);
+    gn_load<VEC, FULL>(xg, lo, hi, v, ok);
+    const double shift = (double)xg[0];
+    GnParams<AK, VEC> pr;
+    gn_params<AK, VEC>(a, lo, c0, i3, ok, pr);
+    double s1, s2;
+    gn_thread_sums(v, ok, shift, s1, s2);
+    block_sum2_n<kGnThreads>(s1, s2, red);
+    if (grid_totals<kGnThreads>(f, gt, nblk, s1, s2, red, tot,
+                                [&](double* t) { gn_recompute<VEC>(xg, count, nblk, shift, red, t); })) {
+        gn_load<VEC, FULL>(xg, lo, hi, v, ok);                 // x is unchanged (y does not overlap it)
+        gn_params<AK, VEC>(a, lo, c0, i3, ok, pr);
+    }
     double mean, rstd;
-    gn_stats(a, gt, count, a.shift[gt], red, mean, rstd);     // shift from pass 1
-    gn_store<GELU, VEC>(a, a.y + begin, lo, hi, mean, rstd, v, ok, wv, bv);
+    gn_moments(tot[0], tot[1], count, shift, a.eps, mean, rstd);
+    gn_write<AK, GELU, VEC, FULL>(a.y + begin, lo, hi, mean, rstd, v, ok, pr);
 }
 
-// Single-pass GroupNorm (gn_fused_kernel): when every group's blocks fit on the device at once
-// (at most kGridMaxGroups groups of at most kGridMaxBlocks blocks), each block keeps its chunk
-// of x and its affine parameters in registers, sums d and d^2 (d = x - x[group start]) and
-// gets the group's totals from the other blocks through grid_totals (grid_sync.hpp), then
-// writes y from the registers: x is read from HBM once, in one launch.
+// Two blocks per CU must fit (the C = 48 op-set shape has 504 blocks of VEC 4 for 256 CUs):
+// at least 4 waves per SIMD, i.e. at most 128 VGPRs.
 template <int AK, bool GELU, int VEC>
-__global__ __launch_bounds__(kGridThreads) void gn_fused_kernel(GroupNormArgs a, GridSync f) {
-    constexpr int NT = kGridThreads;
-    constexpr unsigned CH = NT * 4 * VEC;
-    __shared__ double red[2 * NT / kWave];
+__global__ __launch_bounds__(kGnThreads) __attribute__((amdgpu_waves_per_eu(4))) void gn_fused_kernel(GroupNormArgs a,
+                                                                                                     GridSync f) {
+    __shared__ double red[2 * kGnThreads / kWave];
     __shared__ double tot[2];
     const int gt = (int)blockIdx.y;
     long long begin, c0, i3;
     unsigned count;
     group_span(a, gt, begin, count, c0, i3);
-    const unsigned lo = blockIdx.x * CH;
+    const unsigned lo = blockIdx.x * gn_chunk<VEC>();
     if (lo >= count) return;                                   // past a short group: not one of its blocks
-    const unsigned hi = min(lo + CH, count);
-    const int nch = (int)((count + CH - 1) / CH);
-    const float* xg = a.x + begin;
-    const unsigned gen1 = grid_gen1(f, gt);
-    float v[4 * VEC], wv[4 * VEC], bv[4 * VEC];
+    if (a.vec && lo + gn_chunk<VEC>() <= count)
+        gn_fused_body<AK, GELU, VEC, true>(a, f, gt, begin, count, c0, i3, lo, red, tot);
+    else
+        gn_fused_body<AK, GELU, VEC, false>(a, f, gt, begin, count, c0, i3, lo, red, tot);
+}
+
+// Two passes, pass 1: chunk m's partial sums to part[gt][m]; chunk 0 also stores K (x may be y,
+// so pass 2 must not read it back from x).
+template <int VEC, bool FULL>
+__device__ __forceinline__ void gn_partial_body(const GroupNormArgs& a, int gt, const float* xg, unsigned count,
+                                                unsigned lo, double* red) {
+    const unsigned hi = min(lo + gn_chunk<VEC>(), count);
+    float v[4 * VEC];
     bool ok[4 * VEC];
-    gn_load<VEC, NT>(a, xg, lo, hi, v, ok);
-    gn_affine<AK, VEC, NT>(a, lo, c0, i3, ok, wv, bv);
-    const double shift = (double)xg[0];                        // read before any block writes y
-    double s1 = 0.0, s2 = 0.0;
-#pragma unroll
-    for (int k = 0; k < 4 * VEC; k++) {
-        const double d = ok[k] ? (double)v[k] - shift : 0.0;
-        s1 += d;
-        s2 += d * d;
+    gn_load<VEC, FULL>(xg, lo, hi, v, ok);
+    const double shift = (double)xg[0];
+    double s1, s2;
+    gn_thread_sums(v, ok, shift, s1, s2);
+    block_sum2_n<kGnThreads>(s1, s2, red);
+    if (threadIdx.x == 0) {
+        double* p = a.part + ((size_t)gt * a.nch + blockIdx.x) * 2;
+        p[0] = s1;
+        p[1] = s2;
+        if (blockIdx.x == 0) a.shift[gt] = shift;
     }
-    block_sum2_n<NT>(s1, s2, red);
-    const bool timed_out = grid_totals<NT>(f, gt, nch, gen1, s1, s2, red, tot);
-    const double N = (double)count, dm = tot[0] / N;
-    const double mean = timed_out ? __builtin_nan("") : shift + dm;
-    const double rstd = 1.0 / sqrt(fmax(tot[1] / N - dm * dm, 0.0) + (double)a.eps);
-    gn_store<GELU, VEC, NT>(a, a.y + begin, lo, hi, mean, rstd, v, ok, wv, bv);
+}
+
+template <int VEC>
+__global__ __launch_bounds__(kGnThreads) void gn_partial_kernel(GroupNormArgs a) {
+    __shared__ double red[2 * kGnThreads / kWave];
+    const int gt = (int)blockIdx.y;
+    long long begin, c0, i3;
+    unsigned count;
+    group_span(a, gt, begin, count, c0, i3);
+    const unsigned lo = blockIdx.x * gn_chunk<VEC>();
+    if (lo >= count) return;
+    if (a.vec && lo + gn_chunk<VEC>() <= count) gn_partial_body<VEC, true>(a, gt, a.x + begin, count, lo, red);
+    else gn_partial_body<VEC, false>(a, gt, a.x + begin, count, lo, red);
+}
+
+// Two passes, for groups of more than kGnFoldDirect chunks: one block per group folds its
+// partials into tot[gt].
+__global__ __launch_bounds__(kGnThreads) void gn_fold_kernel(GroupNormArgs a, int vec) {
+    __shared__ double red[2 * kGnThreads / kWave];
+    const int gt = (int)blockIdx.x;
+    long long begin, c0, i3;
+    unsigned count;
+    group_span(a, gt, begin, count, c0, i3);
+    const unsigned ch = kGnThreads * 4u * (unsigned)vec;
+    double t1, t2;
+    gn_fold(a.part + (size_t)gt * a.nch * 2, (int)((count + ch - 1) / ch), red, t1, t2);
+    if (threadIdx.x == 0) {
+        a.tot[2 * gt] = t1;
+        a.tot[2 * gt + 1] = t2;
+    }
+}
+
+// Two passes, pass 2: loads its chunk and parameters first, then the group's totals (folded
+// here from the partials, or gn_fold_kernel's), then writes its chunk.
+template <int AK, bool GELU, int VEC, bool FULL>
+__device__ __forceinline__ void gn_apply_body(const GroupNormArgs& a, int gt, long long begin, unsigned count,
+                                              long long c0, long long i3, unsigned lo, double* red) {
+    const unsigned hi = min(lo + gn_chunk<VEC>(), count);
+    const int nblk = (int)((count + gn_chunk<VEC>() - 1) / gn_chunk<VEC>());
+    float v[4 * VEC];
+    bool ok[4 * VEC];
+    gn_load<VEC, FULL>(a.x + begin, lo, hi, v, ok);
+    GnParams<AK, VEC> pr;
+    gn_params<AK, VEC>(a, lo, c0, i3, ok, pr);
+    double t1, t2;
+    if (nblk <= kGnFoldDirect) {
+        gn_fold(a.part + (size_t)gt * a.nch * 2, nblk, red, t1, t2);
+    } else {
+        t1 = a.tot[2 * gt];
+        t2 = a.tot[2 * gt + 1];
+    }
+    double mean, rstd;
+    gn_moments(t1, t2, count, a.shift[gt], a.eps, mean, rstd);
+    gn_write<AK, GELU, VEC, FULL>(a.y + begin, lo, hi, mean, rstd, v, ok, pr);
+}
+
+template <int AK, bool GELU, int VEC>
+__global__ __launch_bounds__(kGnThreads) void gn_apply_kernel(GroupNormArgs a) {
+    __shared__ double red[2 * kGnThreads / kWave];
+    const int gt = (int)blockIdx.y;
+    long long begin, c0, i3;
+    unsigned count;
+    group_span(a, gt, begin, count, c0, i3);
+    const unsigned lo = blockIdx.x * gn_chunk<VEC>();
+    if (lo >= count) return;
+    if (a.vec && lo + gn_chunk<VEC>() <= count) gn_apply_body<AK, GELU, VEC, true>(a, gt, begin, count, c0, i3, lo, red);
+    else gn_apply_body<AK, GELU, VEC, false>(a, gt, begin, count, c0, i3, lo, red);
 }
 
 // ----------------------------------------------------------------------------- ROPE
@@ -1247,10 +1390,9 @@ Affine make_affine(const stx_tensor* t, const stx_tensor* x, const char* what) {
 }
 
 struct GnPlan {
-    long long cpg, groups, groups_total, span, chunks_partial, chunks_apply;
-    int pvec;                                            // pass 1 width
-    bool wide;                                           // pass 2 with kGnVecApplyWide
-    size_t sync_off, shift_off, part_off, bytes;         // workspace layout
+    long long cpg, groups, groups_total, span;
+    int vec, nch;
+    size_t shift_off, tot_off, part_off, bytes;          // workspace layout
 };
 
 // Every group-norm workspace starts with the single-pass kernel's area (kGridSyncBytes).
@@ -1259,58 +1401,117 @@ GnPlan gn_plan(const stx_tensor* a, int n_groups) {
     p.cpg = std::max<long long>(1, (a->ne[2] + n_groups - 1) / n_groups);
     p.groups = (a->ne[2] + p.cpg - 1) / p.cpg;
     p.groups_total = p.groups * a->ne[3];
-    const long long span = p.cpg * a->ne[0] * a->ne[1];
-    p.span = span;
-    p.pvec = gn_partial_vec(span);
-    p.chunks_partial = (span + 1024LL * p.pvec - 1) / (1024LL * p.pvec);
-    p.wide = (span + gn_chunk<kGnVecApplyWide>() - 1) / gn_chunk<kGnVecApplyWide>() * p.groups_total >= kGnWideBlocks;
-    const long long cha = p.wide ? gn_chunk<kGnVecApplyWide>() : gn_chunk<kGnVecApplyNarrow>();
-    p.chunks_apply = (span + cha - 1) / cha;
+    p.span = p.cpg * a->ne[0] * a->ne[1];
+    p.vec = gn_vec(p.span);
+    const long long ch = (long long)kGnThreads * 4 * p.vec;
+    p.nch = (int)std::max<long long>(1, (p.span + ch - 1) / ch);
     const size_t g = (size_t)std::max<long long>(1, p.groups_total);
     auto up = [](size_t v) { return (v + 255) / 256 * 256; };
-    p.sync_off = 0;
     p.shift_off = kGridSyncBytes;
-    p.part_off = p.shift_off + up(sizeof(double) * g);
-    p.bytes = p.part_off + up(sizeof(double) * 2 * g * (size_t)std::max<long long>(1, p.chunks_partial));
+    p.tot_off = p.shift_off + up(sizeof(double) * g);
+    p.part_off = p.tot_off + up(sizeof(double) * 2 * g);
+    p.bytes = p.part_off + up(sizeof(double) * 2 * g * (size_t)p.nch);
     return p;
 }
 
-// Single pass when the groups fit: at most kGridMaxGroups of them, each in at most
-// kGridMaxBlocks blocks, all blocks resident together. VEC is the smallest width that
-// fits (more blocks, shorter per-thread chains). Returns false to take the two passes.
 template <int AK, bool GELU, int VEC>
-bool try_fused(const GroupNormArgs& g, const GnPlan& p, const GridSync& sync, hipStream_t s) {
-    const long long ch = (long long)kGridThreads * 4 * VEC;
-    const long long nch = (p.span + ch - 1) / ch;
-    if (nch > kGridMaxBlocks) return false;
-    const void* k = reinterpret_cast<const void*>(&gn_fused_kernel<AK, GELU, VEC>);
-    if (nch * p.groups_total > resident_blocks(k)) return false;
-    hipLaunchKernelGGL((gn_fused_kernel<AK, GELU, VEC>), dim3((unsigned)nch, (unsigned)p.groups_total),
-                       dim3(kGridThreads), 0, s, g, sync);
-    launch_check("gn_fused_kernel");
-    return true;
+void launch_gn_vec(const GroupNormArgs& g, const GnPlan& p, const GridSync& sync, bool single, hipStream_t s) {
+    const dim3 grid((unsigned)p.nch, (unsigned)p.groups_total);
+    // The per-element parameter kinds hold 16 weights and 16 biases per thread at VEC 4, more
+    // than the 128 VGPRs of two blocks per CU leave without spilling: two passes for them.
+    if (single && (AK == AFF_CHANNEL_WAVE || VEC < 4)) {
+        const void* k = reinterpret_cast<const void*>(&gn_fused_kernel<AK, GELU, VEC>);
+        if ((long long)p.nch * p.groups_total <= resident_blocks(k, s)) {
+            hipLaunchKernelGGL((gn_fused_kernel<AK, GELU, VEC>), grid, dim3(kGnThreads), 0, s, g, sync);
+            launch_check("gn_fused_kernel");
+            return;
+        }
+    }
+    hipLaunchKernelGGL(gn_partial_kernel<VEC>, grid, dim3(kGnThreads), 0, s, g);
+    launch_check("gn_partial_kernel");
+    if (p.nch > kGnFoldDirect) {
+        hipLaunchKernelGGL(gn_fold_kernel, dim3((unsigned)p.groups_total), dim3(kGnThreads), 0, s, g, VEC);
+        launch_check("gn_fold_kernel");
+    }
+    hipLaunchKernelGGL((gn_apply_kernel<AK, GELU, VEC>), grid, dim3(kGnThreads), 0, s, g);
+    launch_check("gn_apply_kernel");
 }
 
+// Single pass when the groups fit (at most kGridMaxGroups of at most kGridMaxBlocks chunks,
+// all resident together) and y does not overlap x; otherwise two passes. Both give the same
+// bits.
 template <int AK, bool GELU>
-void launch_group_norm(GroupNormArgs g, const GnPlan& p, const GridSync& sync, hipStream_t s) {
-    if (p.groups_total <= kGridMaxGroups &&
-        (try_fused<AK, GELU, 1>(g, p, sync, s) || try_fused<AK, GELU, 2>(g, p, sync, s) ||
-         try_fused<AK, GELU, 4>(g, p, sync, s)))
-        return;
-    g.chunks = (int)p.chunks_partial;
-    g.pchunk = 1024 * p.pvec;
-    const dim3 grid1((unsigned)p.chunks_partial, (unsigned)p.groups_total);
-    if (p.pvec == 4) hipLaunchKernelGGL(gn_partial_kernel<4>, grid1, dim3(256), 0, s, g);
-    else if (p.pvec == 2) hipLaunchKernelGGL(gn_partial_kernel<2>, grid1, dim3(256), 0, s, g);
-    else hipLaunchKernelGGL(gn_partial_kernel<1>, grid1, dim3(256), 0, s, g);
-    launch_check("gn_partial_kernel");
-    if (p.wide)
-        hipLaunchKernelGGL((gn_apply_kernel<AK, GELU, kGnVecApplyWide>),
-                           dim3((unsigned)p.chunks_apply, (unsigned)p.groups_total), dim3(256), 0, s, g);
-    else
-        hipLaunchKernelGGL((gn_apply_kernel<AK, GELU, kGnVecApplyNarrow>),
-                           dim3((unsigned)p.chunks_apply, (unsigned)p.groups_total), dim3(256), 0, s, g);
-    launch_check("gn_apply_kernel");
+void launch_group_norm(const GroupNormArgs& g, const GnPlan& p, const GridSync& sync, bool single, hipStream_t s) {
+    single = single && p.groups_total <= kGridMaxGroups && p.nch <= kGridMaxBlocks;
+    if (p.vec == 1) launch_gn_vec<AK, GELU, 1>(g, p, sync, single, s);
+    else if (p.vec == 2) launch_gn_vec<AK, GELU, 2>(g, p, sync, single, s);
+    else launch_gn_vec<AK, GELU, 4>(g, p, sync, single, s);
+}
+
+// stx_group_norm on a workspace of ws_bytes at ws (checked by the caller).
+void group_norm(const stx_tensor* a, const stx_tensor* dst, int n_groups, float eps, const stx_tensor* weight,
+                const stx_tensor* bias, int gelu, void* ws, const GnPlan& p, hipStream_t s) {
+    const T4 ta = view(a), td = view(dst);
+    GroupNormArgs g{};
+    g.x = reinterpret_cast<const float*>(ta.data);
+    g.y = reinterpret_cast<float*>(td.data);
+    g.w = make_affine(weight, a, "weight");
+    g.b = make_affine(bias, a, "bias");
+    char* w = static_cast<char*>(ws);
+    const GridSync sync = grid_sync_at(w);
+    g.shift = reinterpret_cast<double*>(w + p.shift_off);
+    g.tot = reinterpret_cast<double*>(w + p.tot_off);
+    g.part = reinterpret_cast<double*>(w + p.part_off);
+    g.ne0 = (unsigned)ta.ne[0];
+    g.ne1 = (unsigned)ta.ne[1];
+    g.ne2 = ta.ne[2];
+    g.plane = (unsigned)(ta.ne[0] * ta.ne[1]);
+    g.rplane = 1.0 / (double)g.plane;
+    g.rne0 = 1.0 / (double)g.ne0;
+    g.plane_div = FastDiv(g.plane);
+    g.cpg = p.cpg;
+    g.groups = (int)p.groups;
+    g.nch = p.nch;
+    g.eps = eps;
+    // Every group span starts at (i3 * ne2 + g * cpg) * plane floats.
+    g.vec = aligned16(ta.data) && aligned16(td.data) && (g.cpg * (long long)g.plane) % 4 == 0 &&
+                    (ta.ne[3] == 1 || (g.ne2 * (long long)g.plane) % 4 == 0)
+                ? 1
+                : 0;
+    const size_t nbytes = (size_t)nelem(ta) * 4;
+    const bool single = !overlaps(ta.data, nbytes, td.data, nbytes);
+    auto fits = [&](int kind) {
+        return (g.w.kind == AFF_NONE || g.w.kind == kind) && (g.b.kind == AFF_NONE || g.b.kind == kind);
+    };
+    int ak = fits(AFF_CHANNEL) ? AFF_CHANNEL : fits(AFF_NE0) ? AFF_NE0 : AFF_GENERAL;
+    if (ak == AFF_CHANNEL && g.plane >= 256) ak = AFF_CHANNEL_WAVE;
+    switch (ak * 2 + (gelu ? 1 : 0)) {
+        case AFF_CHANNEL_WAVE * 2 + 1: launch_group_norm<AFF_CHANNEL_WAVE, true>(g, p, sync, single, s); break;
+        case AFF_CHANNEL_WAVE * 2: launch_group_norm<AFF_CHANNEL_WAVE, false>(g, p, sync, single, s); break;
+        case AFF_CHANNEL * 2 + 1: launch_group_norm<AFF_CHANNEL, true>(g, p, sync, single, s); break;
+        case AFF_CHANNEL * 2: launch_group_norm<AFF_CHANNEL, false>(g, p, sync, single, s); break;
+        case AFF_NE0 * 2 + 1: launch_group_norm<AFF_NE0, true>(g, p, sync, single, s); break;
+        case AFF_NE0 * 2: launch_group_norm<AFF_NE0, false>(g, p, sync, single, s); break;
+        case AFF_GENERAL * 2 + 1: launch_group_norm<AFF_GENERAL, true>(g, p, sync, single, s); break;
+        default: launch_group_norm<AFF_GENERAL, false>(g, p, sync, single, s); break;
+    }
+}
+
+// Checks shared by the group-norm entry points; the plan of a call that has work, else false.
+bool group_norm_check(const stx_tensor* a, const stx_tensor* dst, int n_groups, const stx_tensor* weight,
+                      const stx_tensor* bias, GnPlan& p) {
+    check_tensor(a, "a");
+    check_tensor(dst, "dst");
+    check_same_shape(a, dst, "group_norm");
+    STX_REQUIRE(n_groups >= 1, "group_norm: n_groups < 1");
+    STX_REQUIRE(contiguous(view(a)) && contiguous(view(dst)), "group_norm: tensors must be contiguous");
+    (void)make_affine(weight, a, "weight");
+    (void)make_affine(bias, a, "bias");
+    if (nelem(view(a)) == 0) return false;
+    p = gn_plan(a, n_groups);
+    STX_REQUIRE(p.groups_total < 65536, "group_norm: more than 65535 groups");
+    STX_REQUIRE(p.span < (1LL << 32) - gn_chunk<4>(), "group_norm: groups of 2^32 floats or more are not supported");
+    return true;
 }
 
 }  // namespace
@@ -1477,60 +1678,21 @@ STX_API stx_status stx_group_norm(const stx_tensor* a, const stx_tensor* dst, in
                                   const stx_tensor* weight, const stx_tensor* bias, int gelu, void* workspace,
                                   size_t workspace_bytes, stx_stream stream) {
     return guard([&] {
-        check_tensor(a, "a");
-        check_tensor(dst, "dst");
-        check_same_shape(a, dst, "group_norm");
-        STX_REQUIRE(n_groups >= 1, "group_norm: n_groups < 1");
-        const T4 ta = view(a), td = view(dst);
-        STX_REQUIRE(contiguous(ta) && contiguous(td), "group_norm: tensors must be contiguous");
-        const Affine w = make_affine(weight, a, "weight");
-        const Affine b = make_affine(bias, a, "bias");
-        if (nelem(ta) == 0) return;
-        const GnPlan p = gn_plan(a, n_groups);
-        STX_REQUIRE(p.groups_total < 65536, "group_norm: more than 65535 groups");
-        STX_REQUIRE(p.cpg * a->ne[0] * a->ne[1] < (1LL << 32) - gn_chunk<16>(),
-                    "group_norm: groups of 2^32 floats or more are not supported");
+        GnPlan p;
+        if (!group_norm_check(a, dst, n_groups, weight, bias, p)) return;
         STX_REQUIRE(workspace != nullptr && workspace_bytes >= p.bytes, "group_norm: workspace too small (%zu, need %zu)",
                     workspace_bytes, p.bytes);
         STX_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0, "group_norm: workspace must be 256-byte aligned");
-        GroupNormArgs g{};
-        g.x = reinterpret_cast<const float*>(ta.data);
-        g.y = reinterpret_cast<float*>(td.data);
-        g.w = w;
-        g.b = b;
-        char* ws = static_cast<char*>(workspace);
-        const GridSync sync = grid_sync_at(ws + p.sync_off);
-        g.shift = reinterpret_cast<double*>(ws + p.shift_off);
-        g.part = reinterpret_cast<double*>(ws + p.part_off);
-        g.ne0 = (unsigned)ta.ne[0];
-        g.ne1 = (unsigned)ta.ne[1];
-        g.ne2 = ta.ne[2];
-        g.plane = (unsigned)(ta.ne[0] * ta.ne[1]);
-        g.rplane = 1.0 / (double)g.plane;
-        g.rne0 = 1.0 / (double)g.ne0;
-        g.cpg = p.cpg;
-        g.groups = (int)p.groups;
-        g.eps = eps;
-        // Every group span starts at (i3 * ne2 + g * cpg) * plane floats.
-        g.vec = aligned16(ta.data) && aligned16(td.data) && (g.cpg * (long long)g.plane) % 4 == 0 &&
-                        (ta.ne[3] == 1 || (g.ne2 * (long long)g.plane) % 4 == 0)
-                    ? 1
-                    : 0;
-        const hipStream_t s = as_stream(stream);
-        auto fits = [&](int kind) {
-            return (g.w.kind == AFF_NONE || g.w.kind == kind) && (g.b.kind == AFF_NONE || g.b.kind == kind);
-        };
-        const int ak = fits(AFF_CHANNEL) ? AFF_CHANNEL : fits(AFF_NE0) ? AFF_NE0 : AFF_GENERAL;
-        if (ak == AFF_CHANNEL) {
-            if (gelu) launch_group_norm<AFF_CHANNEL, true>(g, p, sync, s);
-            else launch_group_norm<AFF_CHANNEL, false>(g, p, sync, s);
-        } else if (ak == AFF_NE0) {
-            if (gelu) launch_group_norm<AFF_NE0, true>(g, p, sync, s);
-            else launch_group_norm<AFF_NE0, false>(g, p, sync, s);
-        } else {
-            if (gelu) launch_group_norm<AFF_GENERAL, true>(g, p, sync, s);
-            else launch_group_norm<AFF_GENERAL, false>(g, p, sync, s);
-        }
+        group_norm(a, dst, n_groups, eps, weight, bias, gelu, workspace, p, as_stream(stream));
+    });
+}
+
+STX_API stx_status stx_grid_sync_fallbacks(const void* workspace, uint32_t* count) {
+    return guard([&] {
+        STX_REQUIRE(count != nullptr, "grid_sync_fallbacks: count is NULL");
+        STX_REQUIRE(workspace != nullptr, "grid_sync_fallbacks: workspace is NULL");
+        const char* src = static_cast<const char*>(workspace) + kGridSyncFallback;
+        hip_check(hipMemcpy(count, src, sizeof(uint32_t), hipMemcpyDeviceToHost), "hipMemcpy");
     });
 }
 

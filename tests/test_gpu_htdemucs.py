@@ -90,6 +90,36 @@ def test_normalize_without_grid_sync(device, htd, monkeypatch):
     assert np.array_equal(host(mag), htd.cac_normalize(sh, st[0], st[1]))
 
 
+def test_normalize_forced_fallback(device, htd, monkeypatch):
+    """STX_GRID_SYNC_SPIN_LIMIT=0 makes the single-pass blocks give up their waits at the first
+    look; each then computes the totals from the input itself, in the same order: the same bits
+    as the normal run, and the workspace counts the fallbacks."""
+    xh = synth.normal(11, (2, SEG), 0.1) + 0.01
+    x = dev(xh, device)
+    y1, st1 = stx.htdemucs_wave_normalize(x)
+    spec = stx.htdemucs_spec(stx.FFT(NFFT), dev(synth.normal(12, (2, SEG), 0.1), device))
+    m1, sc1 = stx.htdemucs_cac_normalize(spec)
+    ws = stx.workspace(stx.lib().stx_htdemucs_norm_workspace_size(2 * 2 * 2048 * 336), device)
+    monkeypatch.setenv("STX_GRID_SYNC_SPIN_LIMIT", "0")
+    y2, st2 = stx.htdemucs_wave_normalize(x, workspace=ws)
+    m2, sc2 = stx.htdemucs_cac_normalize(spec, workspace=ws)
+    monkeypatch.delenv("STX_GRID_SYNC_SPIN_LIMIT")
+    assert stx.grid_sync_fallbacks(ws) > 0
+    assert np.array_equal(host(y1), host(y2)) and np.array_equal(host(st1), host(st2))
+    assert np.array_equal(host(m1), host(m2)) and np.array_equal(host(sc1), host(sc2))
+    assert close_stats(host(st1), htd.mean_std(xh))
+
+
+def test_normalize_in_place(device, htd):
+    """Output over its input: the three-kernel path (a single-pass block may re-read x)."""
+    xh = synth.normal(13, (2, SEG), 0.1) - 0.005
+    x = dev(xh, device)
+    y, stats = stx.htdemucs_wave_normalize(x, out=x)
+    st = host(stats)
+    assert close_stats(st, htd.mean_std(xh))
+    assert np.array_equal(host(y), htd.normalize(xh, st[0], st[1]))
+
+
 def test_mix_normalize_song(device, htd):
     """src/htdemucs.cpp:539-549 on the 180 s stereo song."""
     mix = synth.sines_plus_pink(5, 2, SONG)

@@ -98,8 +98,8 @@ def test_group_norm_in_place_and_deterministic(device, ops):
 @pytest.mark.parametrize("gelu", [False, True])
 def test_group_norm_shapes_share_a_workspace(device, ops, gelu):
     """Large groups, many groups and batched groups: one workspace, filled with garbage first,
-    serves all of them in turn, twice (no initialisation needed; the single-pass kernel's
-    generation numbers and records in it stay consistent across shapes)."""
+    serves all of them in turn, twice (no initialisation needed: the single-pass kernel's
+    records are keyed by the dispatch, and the two-pass areas are written before they are read)."""
     import torch
     ws = torch.full((1 << 17,), -7.25, device=device)
     shapes = [((96, 1, 85995), 1), ((1000, 1, 8192), 1000), ((48, 1, 85995), 1), ((8, 3, 1, 999), 4)]
@@ -114,8 +114,8 @@ def test_group_norm_shapes_share_a_workspace(device, ops, gelu):
 
 
 def test_group_norm_graph_replays(device, ops):
-    """Replays of one captured call (one call token) on new data each time: the single-pass
-    kernel must wait for a new generation of records per replay, not take the last replay's."""
+    """Replays of one captured call on new data each time: the single-pass kernel's records are
+    keyed by the dispatch, so a replay must wait for its own records, not take the last one's."""
     import torch
     C, T = 96, 21499
     x = randn(device, (C, 1, T), 40)
@@ -150,6 +150,49 @@ def test_group_norm_without_grid_sync(device, ops, C, T, monkeypatch):
     monkeypatch.setenv("STX_NO_GRID_SYNC", "1")
     y2 = host(stx.group_norm(x, 1, 1e-5, w, b, gelu=True))
     assert rel_err(y1, want) <= TOL and rel_err(y2, want) <= TOL
+
+
+GN_PATH_SHAPES = [((96, 1, 21499), 1), ((384, 1, 1344), 1), ((8, 1, 3000), 4), ((64, 1, 100), 1),
+                  ((47, 1, 85993), 1), ((2, 6, 1, 700), 3)]
+
+
+@pytest.mark.parametrize("shape,G", GN_PATH_SHAPES)
+@pytest.mark.parametrize("gelu", [False, True])
+def test_group_norm_paths_same_bits(device, ops, shape, G, gelu, monkeypatch):
+    """Every path gives the same bits: the single pass; two passes (STX_NO_GRID_SYNC=1); in
+    place (two passes, since a single-pass block may have to re-read x); and the single pass
+    with every wait given up at its first look (STX_GRID_SYNC_SPIN_LIMIT=0), where each block
+    that gives up computes its group's totals from x itself. Only the forced run counts
+    fallbacks in its workspace. Shapes: per-wave channel parameters (planes >= 256), per-element
+    ones (plane 100), an unaligned group span (no float4 loads), several groups per launch and
+    a batch (ne3 = 2) of ragged groups."""
+    import torch
+    x = randn(device, shape, sum(shape) + G, 1.3, 0.7)
+    C = shape[-3]
+    w, b = randn(device, (C, 1, 1), 70), randn(device, (C, 1, 1), 71)
+    ws = stx.workspace(stx.group_norm_workspace_size(x, G), device)
+    y1 = host(stx.group_norm(x, G, 1e-5, w, b, gelu=gelu, workspace=ws))
+    assert stx.grid_sync_fallbacks(ws) == 0
+    assert rel_err(y1, ops.group_norm(host(x), G, 1e-5, host(w), host(b), gelu=gelu)) <= TOL
+    monkeypatch.setenv("STX_NO_GRID_SYNC", "1")
+    y2 = host(stx.group_norm(x, G, 1e-5, w, b, gelu=gelu))
+    monkeypatch.delenv("STX_NO_GRID_SYNC")
+    xc = x.clone()
+    stx.group_norm(xc, G, 1e-5, w, b, gelu=gelu, out=xc)
+    y3 = host(xc)
+    ws0 = stx.workspace(stx.group_norm_workspace_size(x, G), device)
+    monkeypatch.setenv("STX_GRID_SYNC_SPIN_LIMIT", "0")
+    y4 = host(stx.group_norm(x, G, 1e-5, w, b, gelu=gelu, workspace=ws0))
+    monkeypatch.delenv("STX_GRID_SYNC_SPIN_LIMIT")
+    forced = stx.grid_sync_fallbacks(ws0)
+    assert np.array_equal(y1, y2) and np.array_equal(y1, y3) and np.array_equal(y1, y4)
+    ne = list(shape[::-1]) + [1] * (4 - len(shape))
+    cpg = -(-ne[2] // G)
+    span, groups_total = cpg * ne[0] * ne[1], -(-ne[2] // cpg) * ne[3]
+    vec = 1 if span <= 512 * 2048 else 2 if span <= 512 * 4096 else 4
+    chunks = -(-span // (2048 * vec))
+    if groups_total <= 8 and chunks <= 512 and chunks > 1:       # a single pass whose blocks wait
+        assert forced > 0
 
 
 def test_group_norm_errors(device):
