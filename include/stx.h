@@ -532,8 +532,23 @@ STX_API stx_status stx_group_norm(const stx_tensor* a, const stx_tensor* dst, in
                                   const stx_tensor* weight, const stx_tensor* bias, int gelu, void* workspace,
                                   size_t workspace_bytes, stx_stream stream);
 
+/* Bytes of the static scratch of stx_group_norm_noalloc, per GPU. */
+#define STX_GROUP_NORM_SCRATCH_BYTES (1u << 20)
+
+/* stx_group_norm without a workspace argument and without any allocation: no counterpart in
+ * the reference. It is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Its scratch is a static
+ * device array of STX_GROUP_NORM_SCRATCH_BYTES per GPU, held until the process ends; shapes
+ * whose stx_group_norm_workspace_size() exceeds it return INVALID_ARGUMENT. Every call on a
+ * GPU shares that GPU's scratch: calls that overlap on one GPU (other streams, other threads)
+ * race; calls in one stream are ordered and safe. Same kernels and results as stx_group_norm. */
+STX_API stx_status stx_group_norm_noalloc(const stx_tensor* a, const stx_tensor* dst, int n_groups, float eps,
+                                          const stx_tensor* weight, const stx_tensor* bias, int gelu,
+                                          stx_stream stream);
+
 /* Blocks of grid-synchronised kernels that ran on `workspace` (a group-norm or HTDemucs
- * normalisation workspace) and computed their statistics themselves because a wait gave up: a sticky count, read
+ * normalisation workspace; NULL: the calling GPU's stx_group_norm_noalloc scratch) and
+ * computed their statistics themselves because a wait gave up: a sticky count, read
  * synchronously (the caller synchronises the streams that used the workspace first). Not
  * part of the reference; a diagnostic for callers that share the device. */
 STX_API stx_status stx_grid_sync_fallbacks(const void* workspace, uint32_t* count);

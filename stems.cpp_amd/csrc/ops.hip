@@ -21,6 +21,7 @@
 // are bit-exact with that definition.
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <type_traits>
 #include <vector>
 
@@ -1514,6 +1515,28 @@ bool group_norm_check(const stx_tensor* a, const stx_tensor* dst, int n_groups, 
     return true;
 }
 
+// Scratch of stx_group_norm_noalloc: a static device array, one per GPU, whose address
+// hipGetSymbolAddress gives once per device (the array's name is not a device address in
+// host code).
+constexpr size_t kGnScratchBytes = STX_GROUP_NORM_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kGnScratchBytes];
+
+void* scratch_address() {
+    static std::mutex mu;
+    static void* addr[64] = {};
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    STX_REQUIRE(dev >= 0 && dev < 64, "group_norm_noalloc: device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void* ptr = nullptr;
+        hip_check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        STX_REQUIRE(ptr != nullptr, "group_norm_noalloc: no scratch address");
+        addr[dev] = ptr;
+    }
+    return addr[dev];
+}
+
 }  // namespace
 }  // namespace stx
 
@@ -1687,11 +1710,25 @@ STX_API stx_status stx_group_norm(const stx_tensor* a, const stx_tensor* dst, in
     });
 }
 
+STX_API stx_status stx_group_norm_noalloc(const stx_tensor* a, const stx_tensor* dst, int n_groups, float eps,
+                                          const stx_tensor* weight, const stx_tensor* bias, int gelu,
+                                          stx_stream stream) {
+    return guard([&] {
+        GnPlan p;
+        if (!group_norm_check(a, dst, n_groups, weight, bias, p)) return;
+        STX_REQUIRE(p.bytes <= kGnScratchBytes,
+                    "group_norm_noalloc: this shape needs %zu bytes of scratch, more than the %zu of the static "
+                    "scratch (use stx_group_norm with a workspace)",
+                    p.bytes, kGnScratchBytes);
+        group_norm(a, dst, n_groups, eps, weight, bias, gelu, scratch_address(), p, as_stream(stream));
+    });
+}
+
 STX_API stx_status stx_grid_sync_fallbacks(const void* workspace, uint32_t* count) {
     return guard([&] {
         STX_REQUIRE(count != nullptr, "grid_sync_fallbacks: count is NULL");
-        STX_REQUIRE(workspace != nullptr, "grid_sync_fallbacks: workspace is NULL");
-        const char* src = static_cast<const char*>(workspace) + kGridSyncFallback;
+        const void* ws = workspace ? workspace : scratch_address();
+        const char* src = static_cast<const char*>(ws) + kGridSyncFallback;
         hip_check(hipMemcpy(count, src, sizeof(uint32_t), hipMemcpyDeviceToHost), "hipMemcpy");
     });
 }

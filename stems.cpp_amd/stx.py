@@ -97,6 +97,7 @@ _SIGNATURES = {
                                    ctypes.c_size_t, _vp]),
     "stx_group_norm_workspace_size": (ctypes.c_size_t, [_vp, _i]),
     "stx_group_norm": (_i, [_vp, _vp, _i, ctypes.c_float, _vp, _vp, _i, _vp, ctypes.c_size_t, _vp]),
+    "stx_group_norm_noalloc": (_i, [_vp, _vp, _i, ctypes.c_float, _vp, _vp, _i, _vp]),
     "stx_grid_sync_fallbacks": (_i, [_vp, ctypes.POINTER(ctypes.c_uint32)]),
     "stx_norm": (_i, [_vp, _vp, ctypes.c_float, _vp]),
     "stx_norm_affine": (_i, [_vp, _vp, _vp, _vp, ctypes.c_float, _vp]),
@@ -845,10 +846,19 @@ def group_norm(x, n_groups, eps=1e-5, weight=None, bias=None, gelu=False, out=No
     return out
 
 
-def grid_sync_fallbacks(workspace):
-    """Sticky count of grid-synchronised blocks that recomputed their statistics on `workspace`."""
+def group_norm_noalloc(x, n_groups, eps=1e-5, weight=None, bias=None, gelu=False, out=None, stream=None):
+    """group_norm on the library's static per-GPU scratch (stx_group_norm_noalloc): no workspace."""
+    out = _out(out, x)
+    check(lib().stx_group_norm_noalloc(_t(x), _t(out), int(n_groups), float(eps), _t(weight), _t(bias),
+                                       int(bool(gelu)), _stream(stream)))
+    return out
+
+
+def grid_sync_fallbacks(workspace=None):
+    """Sticky count of grid-synchronised blocks that recomputed their statistics on `workspace`
+    (None: the static scratch of group_norm_noalloc on the current GPU)."""
     n = ctypes.c_uint32(0)
-    check(lib().stx_grid_sync_fallbacks(_ptr(workspace), ctypes.byref(n)))
+    check(lib().stx_grid_sync_fallbacks(None if workspace is None else _ptr(workspace), ctypes.byref(n)))
     return int(n.value)
 
 
