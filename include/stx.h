@@ -18,6 +18,12 @@
  *     frame contiguous and is what the device pipeline prefers.
  *   - Handles (stx_fft, stx_bands) are immutable after creation and may be shared between
  *     threads and streams, as st::FFT is (src/stft.h:19-55).
+ *   - Versioned table (libstems V1's model, src/libstems_v1.h:146-189): a consumer that loads
+ *     the library at run time resolves only stx_get_api(STX_ABI_VERSION_1) and calls every
+ *     entry point through the returned table. Structs that may grow (stx_separate_options,
+ *     stx_demix_geometry) are size tagged and checked against frozen *_MIN_SIZE prefixes;
+ *     stx_tensor (ggml's descriptor) and stx_chunk (an element of a caller-sized array) are
+ *     frozen by-value types.
  */
 #ifndef STX_H
 #define STX_H
@@ -237,19 +243,23 @@ typedef struct {
     int32_t fade_out;          /* 1: the weight keeps its fade-out (0 for chunks reaching the end) */
 } stx_chunk;
 
+/* Size tagged: set size = sizeof(stx_demix_geometry) before the call; the library writes the
+ * fields that fit in `size` (at least STX_DEMIX_GEOMETRY_MIN_SIZE). */
 typedef struct {
+    uint32_t size;
+    int32_t chunk, step, border, fade, reflect_border;
     int64_t len;               /* samples per channel */
     int64_t padded_len;        /* Lp */
     int64_t n_chunks;
-    int32_t chunk, step, border, fade, reflect_border;
 } stx_demix_geometry;
 
 /* Step of RoFormer::separate (src/roformer.cpp:442-443): chunk / num_overlap for overlap < 0,
  * else max(1, lround(chunk * (1 - overlap))); 0 for overlap >= 1 (the reference rejects it). */
 STX_API int stx_demix_step(int chunk, int num_overlap, float overlap);
 
-/* The integer chunk table (host only): geometry, and chunks[n_chunks] unless chunks is NULL.
- * INVALID_ARGUMENT for len <= 0 ("empty input") or chunk/step <= 0. */
+/* The integer chunk table (host only): geometry (unless NULL), and chunks[n_chunks] unless
+ * chunks is NULL. INVALID_ARGUMENT for len <= 0 ("empty input"), chunk/step <= 0 or a geometry
+ * whose size is below STX_DEMIX_GEOMETRY_MIN_SIZE. */
 STX_API stx_status stx_demix_plan(int64_t len, int chunk, int step, stx_demix_geometry* geom,
                                   stx_chunk* chunks, int64_t capacity);
 
@@ -300,8 +310,11 @@ typedef int32_t (*stx_separate_fn)(void* user, const float* parts, int64_t first
 typedef void (*stx_progress_fn)(void* user, int32_t done, int32_t total);
 typedef int32_t (*stx_cancel_fn)(void* user);
 
-/* st::SeparateOptions (src/separator.h:19-32). */
+/* st::SeparateOptions (src/separator.h:19-32). Size tagged: zero it, set size = sizeof,
+ * call stx_separate_options_init for the defaults, then set fields. A NULL options pointer
+ * means the defaults; a size below STX_SEPARATE_OPTIONS_MIN_SIZE is INVALID_ARGUMENT. */
 typedef struct {
+    uint32_t size;
     int32_t shifts;                /* random time shifts averaged; 0 = one deterministic pass */
     float overlap;                 /* [0, 1); negative = the model's num_overlap */
     uint32_t seed;                 /* for the shift offsets (std::mt19937) */
@@ -309,6 +322,11 @@ typedef struct {
     stx_cancel_fn should_cancel;   /* polled before every chunk; non-zero cancels; may be NULL */
     void* user;
 } stx_separate_options;
+
+/* Writes the defaults (no shifts, overlap -1: the model's own, seed 0, no callbacks) into the
+ * fields that fit in options->size. INVALID_ARGUMENT for NULL or a size below
+ * STX_SEPARATE_OPTIONS_MIN_SIZE. Host only. */
+STX_API stx_status stx_separate_options_init(stx_separate_options* options);
 
 /* Bytes of device workspace stx_demix_track needs (batch = chunks per separator call). */
 STX_API size_t stx_demix_track_workspace_size(int channels, int64_t len, int chunk, int step, int n_stems,
@@ -641,6 +659,202 @@ STX_API stx_status stx_cont_permute(const stx_tensor* a, int ax0, int ax1, int a
  * and their extents along dim add up to dst's. srcs is a host array of n_srcs descriptors. */
 STX_API stx_status stx_concat(const stx_tensor* const* srcs, int n_srcs, int dim, const stx_tensor* dst,
                               stx_stream stream);
+
+
+/* ------------------------------------------------------------------------------------------
+ * Versioned function table (after libstems V1, src/libstems_v1.h:146-189). Every entry point
+ * above, in header order; a later revision of V1 may append entries (never reorder them), so
+ * a consumer checks `size` against the prefix it needs.
+ * ---------------------------------------------------------------------------------------- */
+#define STX_ABI_VERSION_1 1u
+
+typedef struct stx_api_v1 {
+    uint32_t size;                 /* sizeof the library's table */
+    uint32_t abi_version;          /* STX_ABI_VERSION_1 */
+    const char*(*version)(void);
+    const char*(*last_error)(void);
+    stx_status (*fft_create)(int n, stx_fft** out);
+    stx_status (*fft_create_any)(int n, stx_fft** out);
+    void (*fft_destroy)(stx_fft* fft);
+    int (*fft_size)(const stx_fft* fft);
+    stx_status (*fft_run)(const stx_fft* fft, float* data, int batch, int inverse,
+                          stx_stream stream);
+    int (*torch_stft_frames)(int len, int hop);
+    int (*htdemucs_frames)(int n_fft, int len);
+    stx_status (*torch_stft)(const stx_fft* fft, const float* x, int channels, int len, int hop,
+                             int normalized, float* spec, stx_spec_layout layout,
+                             stx_stream stream);
+    stx_status (*torch_istft)(const stx_fft* fft, const float* spec, int channels, int n_frames,
+                              int hop, int normalized, float* out, stx_spec_layout layout,
+                              stx_stream stream);
+    stx_status (*htdemucs_spec)(const stx_fft* fft, const float* x, int channels, int len,
+                                float* spec, stx_spec_layout layout, stx_stream stream);
+    stx_status (*htdemucs_ispec)(const stx_fft* fft, const float* spec, int channels, int n_frames,
+                                 int length, float* out, stx_spec_layout layout, stx_stream stream);
+    size_t (*istft_workspace_size)(const stx_fft* fft, int channels, int n_frames);
+    stx_status (*torch_istft_ws)(const stx_fft* fft, const float* spec, int channels, int n_frames,
+                                 int hop, int normalized, float* out, stx_spec_layout layout,
+                                 void* workspace, size_t workspace_bytes, stx_stream stream);
+    stx_status (*htdemucs_ispec_ws)(const stx_fft* fft, const float* spec, int channels,
+                                    int n_frames, int length, float* out, stx_spec_layout layout,
+                                    void* workspace, size_t workspace_bytes, stx_stream stream);
+    stx_status (*mel_band_map)(int sample_rate, int n_fft, int n_mels, int32_t* band_sizes,
+                               int32_t* band_freqs, int64_t capacity, int64_t* n_freqs);
+    stx_status (*bs_band_map)(const int32_t* freqs_per_bands, int n_bands, int n_fft,
+                              int32_t* band_freqs, int64_t capacity, int64_t* n_freqs);
+    stx_status (*bands_layout)(const int32_t* band_sizes, int n_bands, const int32_t* band_freqs,
+                               int64_t n_freqs, int n_bins, int channels, int64_t* band_freq_off,
+                               int64_t* band_feat_off, int32_t* bands_per_freq);
+    stx_status (*bands_create)(const int32_t* band_sizes, int n_bands, const int32_t* band_freqs,
+                               int64_t n_freqs, int n_bins, int channels, stx_bands** out);
+    void (*bands_destroy)(stx_bands* bands);
+    int64_t (*bands_total_feat)(const stx_bands* bands);
+    stx_status (*band_gather)(const stx_bands* bands, const float* spec, int batch, int n_frames,
+                              stx_spec_layout layout, float* feat, stx_stream stream);
+    stx_status (*band_scatter_apply)(const stx_bands* bands, const float* masks, int n_stems,
+                                     const float* spec, int batch, int n_frames,
+                                     stx_spec_layout layout, int zero_dc, float* out,
+                                     stx_stream stream);
+    stx_status (*band_rms_norm)(const stx_bands* bands, const float* feat, int batch, int n_frames,
+                                const float* const* gammas, float eps, float* out,
+                                stx_stream stream);
+    stx_status (*band_mask_glu)(const stx_bands* bands, const float* const* heads, int n_stems,
+                                int n_frames, float* masks, stx_stream stream);
+    int (*demix_step)(int chunk, int num_overlap, float overlap);
+    stx_status (*demix_plan)(int64_t len, int chunk, int step, stx_demix_geometry* geom,
+                             stx_chunk* chunks, int64_t capacity);
+    stx_status (*demix_plan_rules)(int64_t len, int chunk, int step, stx_demix_rules rules,
+                                   stx_demix_geometry* geom, stx_chunk* chunks, int64_t capacity);
+    stx_status (*demix_window)(int chunk, float* window);
+    stx_status (*demix_window_rules)(int chunk, stx_demix_rules rules, float* window);
+    stx_status (*demix_create)(int64_t len, int channels, int chunk, int step, stx_demix** out);
+    stx_status (*demix_create_rules)(int64_t len, int channels, int chunk, int step,
+                                     stx_demix_rules rules, stx_demix** out);
+    void (*demix_destroy)(stx_demix* demix);
+    int64_t (*demix_n_chunks)(const stx_demix* demix);
+    stx_status (*demix_chunks)(const stx_demix* demix, const float* mix, int64_t first,
+                               int64_t count, float* parts, stx_stream stream);
+    stx_status (*demix_overlap_add)(const stx_demix* demix, const float* y, int n_stems,
+                                    float* out, stx_stream stream);
+    stx_status (*separate_options_init)(stx_separate_options* options);
+    size_t (*demix_track_workspace_size)(int channels, int64_t len, int chunk, int step,
+                                         int n_stems, int batch, int shifts, int sample_rate);
+    stx_status (*demix_track)(const float* mix, int channels, int64_t len, int chunk,
+                              int num_overlap, int n_stems, int complement, int sample_rate,
+                              int batch, stx_separate_fn separate, void* separate_user,
+                              const stx_separate_options* options, float* out, void* workspace,
+                              size_t workspace_bytes, stx_stream stream);
+    stx_status (*uvr_demix_create)(int64_t len, int channels, int chunk, int n_fft, float overlap,
+                                   stx_uvr_demix** out);
+    void (*uvr_demix_destroy)(stx_uvr_demix* demix);
+    int64_t (*uvr_demix_n_chunks)(const stx_uvr_demix* demix);
+    stx_status (*uvr_demix_geometry)(const stx_uvr_demix* demix, int64_t* padded_len,
+                                     int64_t* step, int* trim);
+    stx_status (*uvr_demix_chunks)(const stx_uvr_demix* demix, const float* mix, int64_t first,
+                                   int64_t count, float* parts, stx_stream stream);
+    stx_status (*uvr_demix_overlap_add)(const stx_uvr_demix* demix, const float* y, int n_stems,
+                                        float* out, stx_stream stream);
+    size_t (*tfc_tdf_separate_workspace_size)(int channels, int64_t len, int chunk, int n_fft,
+                                              stx_tfc_chunking chunking, int num_overlap,
+                                              float overlap, int n_stems, int batch);
+    stx_status (*tfc_tdf_separate)(const float* mix, int channels, int64_t len, int chunk,
+                                   int n_fft, stx_tfc_chunking chunking, int num_overlap,
+                                   int n_stems, float compensate, int complement, int batch,
+                                   stx_separate_fn separate, void* separate_user,
+                                   const stx_separate_options* options, float* out,
+                                   void* workspace, size_t workspace_bytes, stx_stream stream);
+    stx_status (*resampler_create)(int src_rate, int dst_rate, stx_resampler** out);
+    void (*resampler_destroy)(stx_resampler* resampler);
+    int64_t (*resample_length)(const stx_resampler* resampler, int64_t n);
+    stx_status (*resample)(const stx_resampler* resampler, const float* in, int channels,
+                           int64_t n, float* out, stx_stream stream);
+    size_t (*htdemucs_norm_workspace_size)(int64_t n);
+    stx_status (*htdemucs_cac_normalize)(const float* spec, int channels, int n_bins, int n_frames,
+                                         float* mag, double* stats, void* workspace,
+                                         size_t workspace_bytes, stx_stream stream);
+    stx_status (*htdemucs_wave_normalize)(const float* x, int64_t n, float* out, double* stats,
+                                          void* workspace, size_t workspace_bytes,
+                                          stx_stream stream);
+    stx_status (*htdemucs_mix_normalize)(const float* mix, int channels, int64_t len, float* out,
+                                         double* stats, void* workspace, size_t workspace_bytes,
+                                         stx_stream stream);
+    stx_status (*htdemucs_cac_denormalize)(const float* ox, int n_sources, int channels,
+                                           int n_bins, int n_frames, const double* stats,
+                                           float* spec, stx_stream stream);
+    stx_status (*htdemucs_time_add)(const float* xt, const float* y, int64_t n,
+                                    const double* stats, float* out, stx_stream stream);
+    stx_status (*htdemucs_split_plan)(int length, int segment, float overlap, int* stride,
+                                      int* n_chunks);
+    stx_status (*htdemucs_segments)(const float* buf, int channels, int64_t total, int64_t offset,
+                                    int length, int segment, int stride, int first, int count,
+                                    float* parts, stx_stream stream);
+    stx_status (*htdemucs_split_overlap_add)(const float* y, int tracks, int length, int segment,
+                                             int stride, float* out, stx_stream stream);
+    size_t (*htdemucs_separate_workspace_size)(int channels, int64_t len, int segment,
+                                               int n_sources, int batch, int shifts,
+                                               int sample_rate, float overlap);
+    stx_status (*htdemucs_separate)(const float* mix, int channels, int64_t len, int segment,
+                                    int n_sources, int n_models, const float* bag_weights,
+                                    int sample_rate, int batch, stx_model_fn forward,
+                                    void* forward_user, const stx_separate_options* options,
+                                    float* out, void* workspace, size_t workspace_bytes,
+                                    stx_stream stream);
+    size_t (*group_norm_workspace_size)(const stx_tensor* a, int n_groups);
+    stx_status (*group_norm)(const stx_tensor* a, const stx_tensor* dst, int n_groups, float eps,
+                             const stx_tensor* weight, const stx_tensor* bias, int gelu,
+                             void* workspace, size_t workspace_bytes, stx_stream stream);
+    stx_status (*group_norm_noalloc)(const stx_tensor* a, const stx_tensor* dst, int n_groups,
+                                     float eps, const stx_tensor* weight, const stx_tensor* bias,
+                                     int gelu, stx_stream stream);
+    stx_status (*grid_sync_fallbacks)(const void* workspace, uint32_t* count);
+    stx_status (*norm)(const stx_tensor* a, const stx_tensor* dst, float eps, stx_stream stream);
+    stx_status (*norm_affine)(const stx_tensor* a, const float* weight, const float* bias,
+                              const stx_tensor* dst, float eps, stx_stream stream);
+    stx_status (*rms_norm)(const stx_tensor* a, const stx_tensor* dst, float eps,
+                           stx_stream stream);
+    stx_status (*rms_norm_mul)(const stx_tensor* a, const float* gamma, const stx_tensor* dst,
+                               float eps, stx_stream stream);
+    stx_status (*soft_max_ext)(const stx_tensor* a, const stx_tensor* mask, const stx_tensor* dst,
+                               float scale, float max_bias, stx_stream stream);
+    stx_status (*gelu_erf)(const stx_tensor* a, const stx_tensor* dst, stx_stream stream);
+    stx_status (*add_gelu_erf)(const stx_tensor* a, const stx_tensor* b, const stx_tensor* dst,
+                               stx_stream stream);
+    stx_status (*glu)(const stx_tensor* a, const stx_tensor* dst, int dim, stx_stream stream);
+    stx_status (*add)(const stx_tensor* a, const stx_tensor* b, const stx_tensor* dst,
+                      stx_stream stream);
+    stx_status (*mul)(const stx_tensor* a, const stx_tensor* b, const stx_tensor* dst,
+                      stx_stream stream);
+    stx_status (*mul_add)(const stx_tensor* x, const stx_tensor* h, const stx_tensor* s,
+                          const stx_tensor* dst, stx_stream stream);
+    stx_status (*glu_mul_add)(const stx_tensor* x, const stx_tensor* a, int dim,
+                              const stx_tensor* s, const stx_tensor* dst, stx_stream stream);
+    stx_status (*rope_ext)(const stx_tensor* a, const int32_t* pos, const stx_tensor* dst,
+                           int n_dims, int mode, int n_ctx_orig, float freq_base, float freq_scale,
+                           float ext_factor, float attn_factor, float beta_fast, float beta_slow,
+                           stx_stream stream);
+    stx_status (*qkv_rope_split)(const stx_tensor* qkv, const int32_t* pos, int n_head,
+                                 float freq_base, float freq_scale, float attn_factor,
+                                 const stx_tensor* q, const stx_tensor* k, const stx_tensor* vt,
+                                 stx_stream stream);
+    stx_status (*merge_heads)(const stx_tensor* o, const stx_tensor* gates, const stx_tensor* dst,
+                              stx_stream stream);
+    stx_status (*cont_permute)(const stx_tensor* a, int ax0, int ax1, int ax2, int ax3,
+                               const stx_tensor* dst, stx_stream stream);
+    stx_status (*concat)(const stx_tensor* const* srcs, int n_srcs, int dim, const stx_tensor* dst,
+                         stx_stream stream);
+    void (*reserved[16])(void);
+} stx_api_v1;
+
+/* Frozen V1 prefixes: each names the last field of the initial V1 contract. */
+#define STX_FIELD_END(type, field) ((uint32_t)(offsetof(type, field) + sizeof(((type*)0)->field)))
+#define STX_SEPARATE_OPTIONS_MIN_SIZE STX_FIELD_END(stx_separate_options, user)
+#define STX_DEMIX_GEOMETRY_MIN_SIZE   STX_FIELD_END(stx_demix_geometry, n_chunks)
+#define STX_API_V1_MIN_SIZE           STX_FIELD_END(stx_api_v1, concat)
+
+/* The one symbol a dynamically loading consumer resolves: the static V1 table (owned by the
+ * library for the lifetime of the module) for abi_version STX_ABI_VERSION_1, NULL for any other
+ * version. */
+STX_API const stx_api_v1* stx_get_api(uint32_t abi_version);
 
 #ifdef __cplusplus
 }

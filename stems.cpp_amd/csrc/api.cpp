@@ -12,6 +12,6 @@ const char* last_error() { return g_last_error.c_str(); }
 }  // namespace stx
 
 extern "C" {
-STX_API const char* stx_version(void) { return "0.1.0"; }
+STX_API const char* stx_version(void) { return "0.2.0"; }
 STX_API const char* stx_last_error(void) { return stx::last_error(); }
 }

@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <cstring>
 #include <new>
 #include <stdexcept>
 #include <string>
@@ -120,6 +121,26 @@ struct FastDiv {
     }
     __host__ __device__ __forceinline__ unsigned mod(unsigned n) const { return n - div(n) * d; }
 };
+
+// The defaults of stx_separate_options (src/separator.h:19-32): no shifts, the model's overlap.
+inline stx_separate_options default_separate_options() {
+    stx_separate_options o{};
+    o.size = sizeof o;
+    o.overlap = -1.0f;
+    return o;
+}
+
+// A caller's separate options (NULL: the defaults), checked against the frozen V1 prefix; the
+// fields past the caller's size keep their defaults.
+inline stx_separate_options separate_options(const stx_separate_options* in) {
+    stx_separate_options o = default_separate_options();
+    if (!in) return o;
+    STX_REQUIRE(in->size >= STX_SEPARATE_OPTIONS_MIN_SIZE, "separate options: size %u is below the V1 minimum %u",
+                in->size, STX_SEPARATE_OPTIONS_MIN_SIZE);
+    std::memcpy(&o, in, in->size < sizeof o ? in->size : sizeof o);
+    o.size = sizeof o;
+    return o;
+}
 
 // Compute units of the current device (cached per device id).
 inline int device_cus() {

@@ -429,9 +429,7 @@ STX_API stx_status stx_demix_track(const float* mix, int channels, int64_t len, 
                                    void* separate_user, const stx_separate_options* options, float* out,
                                    void* workspace, size_t workspace_bytes, stx_stream stream) {
     stx_status st = guard([&] {
-        stx_separate_options opt{};
-        opt.overlap = -1.0f;
-        if (options) opt = *options;
+        const stx_separate_options opt = separate_options(options);
         if (len <= 0) fail(STX_STATUS_INVALID_ARGUMENT, "empty input");                   // :439
         if (opt.overlap >= 1.0f) fail(STX_STATUS_INVALID_ARGUMENT, "overlap must be < 1"); // :440
         STX_REQUIRE(channels >= 1 && n_stems >= 1 && chunk >= 1 && batch >= 1, "bad channels/stems/chunk/batch");

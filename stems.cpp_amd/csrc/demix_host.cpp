@@ -105,14 +105,19 @@ STX_API stx_status stx_demix_plan_rules(int64_t len, int chunk, int step, stx_de
     return guard([&] {
         const DemixGeometry g = demix_geometry(len, chunk, step, rules);
         if (geom) {
-            geom->len = g.len;
-            geom->padded_len = g.padded_len;
-            geom->chunk = g.chunk;
-            geom->step = g.step;
-            geom->border = g.border;
-            geom->fade = g.fade;
-            geom->reflect_border = g.reflect_border;
-            geom->n_chunks = g.n_chunks;
+            STX_REQUIRE(geom->size >= STX_DEMIX_GEOMETRY_MIN_SIZE, "demix geometry: size %u is below the V1 minimum %u",
+                        geom->size, STX_DEMIX_GEOMETRY_MIN_SIZE);
+            stx_demix_geometry o{};
+            o.size = geom->size;
+            o.len = g.len;
+            o.padded_len = g.padded_len;
+            o.chunk = g.chunk;
+            o.step = g.step;
+            o.border = g.border;
+            o.fade = g.fade;
+            o.reflect_border = g.reflect_border;
+            o.n_chunks = g.n_chunks;
+            std::memcpy(geom, &o, std::min<size_t>(geom->size, sizeof o));
         }
         if (!chunks) return;
         STX_REQUIRE(capacity >= g.n_chunks, "chunk table capacity %lld < %lld", (long long)capacity,

@@ -752,9 +752,7 @@ STX_API stx_status stx_htdemucs_separate(const float* mix, int channels, int64_t
                                          const stx_separate_options* options, float* out, void* workspace,
                                          size_t workspace_bytes, stx_stream stream) {
     return guard([&] {
-        stx_separate_options opt{};
-        opt.overlap = -1.0f;
-        if (options) opt = *options;
+        const stx_separate_options opt = separate_options(options);
         if (len <= 0) fail(STX_STATUS_INVALID_ARGUMENT, "empty input");                        // :537
         STX_REQUIRE(len < (1LL << 31) - sample_rate, "separate: input too long");
         STX_REQUIRE(channels >= 1 && n_sources >= 1 && n_sources <= 64 && n_models >= 1 && segment >= 2 && batch >= 1,

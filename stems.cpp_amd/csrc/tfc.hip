@@ -335,9 +335,7 @@ STX_API stx_status stx_tfc_tdf_separate(const float* mix, int channels, int64_t 
     stx_uvr_demix* uplan = nullptr;
     stx_demix* mplan = nullptr;
     const stx_status st = guard([&] {
-        stx_separate_options opt{};
-        opt.overlap = -1.0f;
-        if (options) opt = *options;
+        const stx_separate_options opt = separate_options(options);
         if (!mix || len <= 0) fail(STX_STATUS_RUNTIME_ERROR, "tfc_tdf: empty input");                // :572
         STX_REQUIRE(chunking == STX_TFC_MSST || chunking == STX_TFC_UVR, "unknown TFC-TDF chunking %d", chunking);
         STX_REQUIRE(channels >= 1 && n_stems >= 1 && chunk >= 1 && batch >= 1, "bad channels/stems/chunk/batch");

@@ -95,6 +95,8 @@ _SIGNATURES = {
                                                                ctypes.c_float]),
     "stx_htdemucs_separate": (_i, [_vp, _i, ctypes.c_int64, _i, _i, _i, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp,
                                    ctypes.c_size_t, _vp]),
+    "stx_separate_options_init": (_i, [_vp]),
+    "stx_get_api": (_vp, [ctypes.c_uint32]),
     "stx_group_norm_workspace_size": (ctypes.c_size_t, [_vp, _i]),
     "stx_group_norm": (_i, [_vp, _vp, _i, ctypes.c_float, _vp, _vp, _i, _vp, ctypes.c_size_t, _vp]),
     "stx_group_norm_noalloc": (_i, [_vp, _vp, _i, ctypes.c_float, _vp, _vp, _i, _vp]),
@@ -410,9 +412,10 @@ CHUNK_FULL, CHUNK_REFLECT, CHUNK_ZERO = 0, 1, 2
 
 
 class DemixGeometry(ctypes.Structure):
-    _fields_ = [("len", ctypes.c_int64), ("padded_len", ctypes.c_int64), ("n_chunks", ctypes.c_int64),
-                ("chunk", ctypes.c_int32), ("step", ctypes.c_int32), ("border", ctypes.c_int32),
-                ("fade", ctypes.c_int32), ("reflect_border", ctypes.c_int32)]
+    """stx_demix_geometry (size tagged)."""
+    _fields_ = [("size", ctypes.c_uint32), ("chunk", ctypes.c_int32), ("step", ctypes.c_int32),
+                ("border", ctypes.c_int32), ("fade", ctypes.c_int32), ("reflect_border", ctypes.c_int32),
+                ("len", ctypes.c_int64), ("padded_len", ctypes.c_int64), ("n_chunks", ctypes.c_int64)]
 
 
 class Chunk(ctypes.Structure):
@@ -427,8 +430,15 @@ CANCEL_FN = ctypes.CFUNCTYPE(ctypes.c_int32, ctypes.c_void_p)
 
 
 class SeparateOptions(ctypes.Structure):
-    _fields_ = [("shifts", ctypes.c_int32), ("overlap", ctypes.c_float), ("seed", ctypes.c_uint32),
-                ("progress", PROGRESS_FN), ("should_cancel", CANCEL_FN), ("user", ctypes.c_void_p)]
+    """stx_separate_options (size tagged: size is set to the struct's size)."""
+    _fields_ = [("size", ctypes.c_uint32), ("shifts", ctypes.c_int32), ("overlap", ctypes.c_float),
+                ("seed", ctypes.c_uint32), ("progress", PROGRESS_FN), ("should_cancel", CANCEL_FN),
+                ("user", ctypes.c_void_p)]
+
+    def __init__(self, shifts=0, overlap=-1.0, seed=0, progress=None, should_cancel=None, user=None):
+        super().__init__(ctypes.sizeof(SeparateOptions), shifts, overlap, seed,
+                         progress if progress is not None else PROGRESS_FN(),
+                         should_cancel if should_cancel is not None else CANCEL_FN(), user)
 
 
 def demix_step(chunk, num_overlap, overlap=-1.0):
@@ -443,11 +453,12 @@ def demix_plan(length, chunk, step, rules=DEMIX_ROFORMER):
     """(geometry dict, numpy structured chunk table) of the overlap-add demix (host only)."""
     import numpy as np
     g = DemixGeometry()
+    g.size = ctypes.sizeof(DemixGeometry)
     check(lib().stx_demix_plan_rules(int(length), int(chunk), int(step), int(rules), ctypes.byref(g), None, 0))
     table = (Chunk * max(1, g.n_chunks))()
     check(lib().stx_demix_plan_rules(int(length), int(chunk), int(step), int(rules), ctypes.byref(g), table,
                                      g.n_chunks))
-    geom = {f: getattr(g, f) for f, _ in DemixGeometry._fields_}
+    geom = {f: getattr(g, f) for f, _ in DemixGeometry._fields_ if f != "size"}
     arr = np.array([(c.start, c.length, c.pad_mode, c.fade_in, c.fade_out) for c in table[: g.n_chunks]],
                    dtype=[("start", np.int64), ("length", np.int32), ("pad_mode", np.int32),
                           ("fade_in", np.int32), ("fade_out", np.int32)])

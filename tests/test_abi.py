@@ -109,3 +109,30 @@ def test_layout_argument_checks():
     md = _desc([4, 6, 5, 1], 0x900000)
     assert L.stx_merge_heads(ctypes.byref(o), ctypes.byref(gates), ctypes.byref(md), None) == \
         stx.STATUS_INVALID_ARGUMENT
+
+
+def test_versioned_table_from_c(tmp_path):
+    """tests/cpp/abi_check.c, pure C: dlopen libstx.so, resolve only stx_get_api for the calls,
+    check the V1 table (every entry is the exported function of its name), NULL for other
+    versions, the size-tagged structs' frozen minimums and a few host-only calls through the
+    table (src/libstems_v1.h:146-189 and tests/abi_test.c:63-101 are the model)."""
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("no C compiler")
+    exe = tmp_path / "abi_check"
+    subprocess.run([gcc, "-std=c11", "-Wall", "-Wextra", "-Werror", "-I", os.path.join(ROOT, "include"),
+                    os.path.join(ROOT, "tests", "cpp", "abi_check.c"), "-o", str(exe), "-ldl"], check=True)
+    r = subprocess.run([str(exe), os.path.abspath(stx.LIB_PATH)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "all ok" in r.stdout
+
+
+def test_table_lists_every_entry_point_in_header_order():
+    """The stx_api_v1 members are the declared entry points (minus stx_get_api), in header order."""
+    text = open(os.path.join(ROOT, "include", "stx.h")).read()
+    head, table = text.split("typedef struct stx_api_v1 {", 1)
+    decl = re.findall(r"STX_API\s+[\w\s\*]+?\b(stx_\w+)\s*\(", head)
+    members = re.findall(r"\(\*(\w+)\)\(", table.split("} stx_api_v1;")[0])
+    assert members == [d[4:] for d in decl]
