@@ -90,13 +90,16 @@ __device__ __forceinline__ int xcd_block() {
 
 inline bool is_pow2(long long n) { return n >= 1 && (n & (n - 1)) == 0; }
 
-// x / h correctly rounded, given r = RN(1/h): q0 = RN(x r), then RN(q0 + r RN(x - q0 h)), which
-// by Markstein's theorem (r within half an ulp of 1/h, q0 within one ulp of x/h, the residual
-// exact by the fma) is the IEEE quotient, for x and h with no overflow or underflow on the way.
+// x / h correctly rounded, for h finite and nonzero, given r = RN(1/h): q0 = RN(x r), then
+// RN(q0 + r RN(x - q0 h)), which by Markstein's theorem (r within half an ulp of 1/h, q0 within
+// one ulp of x/h, the residual exact by the fma) is the IEEE quotient when nothing overflows or
+// underflows on the way. When q0 is not finite (x infinite or NaN, or x/h overflowing) the
+// residual would be inf - inf = NaN; the IEEE quotient is then q0 itself (+-inf or NaN).
 __device__ __forceinline__ double div_rn(double x, double h, double r) {
 #pragma clang fp contract(off)
     const double q0 = x * r;
-    return fma(fma(-q0, h, x), r, q0);
+    const double q = fma(fma(-q0, h, x), r, q0);
+    return isfinite(q0) ? q : q0;
 }
 
 // Division of any n < 2^32 by a fixed d >= 1 with one high multiply, one add and one shift:

@@ -79,6 +79,27 @@ def test_scatter_apply_bit_exact(device, ob, mel, kind, layout, S, zero_dc):
         assert np.array_equal(out[b], ref.astype(np.complex64))
 
 
+def test_scatter_apply_non_finite_masks(device, ob, mel):
+    """Masks holding inf and NaN (a diverged model): the average of a bin's band values divides
+    by the band count like the reference (src/roformer.cpp:270-275), inf stays inf, NaN stays
+    NaN, and the complex multiply follows; the same bits as the oracle, NaNs in place."""
+    sizes, freqs = mel
+    C, F, T = 2, 1025, 33
+    z = rand_spec(14, 1, C, F, T)[0]
+    tf = int(sizes.sum()) * C * 2
+    masks = synth.uniform(15, (1, tf * T))
+    masks[0, 11] = np.inf
+    masks[0, 5 * tf + 2] = -np.inf
+    masks[0, 9 * tf + 40] = np.nan
+    masks[0, 20 * tf + 1001] = np.inf
+    bands = stx.Bands(sizes, freqs, F, C)
+    out = host(bands.scatter_apply(dev(masks[None], device), dev(z[None], device), T, layout=stx.F_MAJOR))[0, 0]
+    ref = ob.scatter_apply(sizes, freqs, masks, z.astype(np.complex128), False).astype(np.complex64)[0]
+    a, b = out.view(np.float32), ref.view(np.float32)
+    assert np.isinf(a).any() and np.isnan(a).any()
+    assert np.array_equal(a, b, equal_nan=True)
+
+
 def test_small_random_table_bit_exact(device, ob):
     from test_oracle_bands import random_table
     sizes, freqs = random_table(5, 33, 9)

@@ -80,6 +80,25 @@ def test_uvr_chunks_and_ola_bit_exact(device, od, length, chunk, n_fft, overlap)
     assert np.array_equal(got, od.uvr_ola(y, length, chunk, n_fft, overlap))
 
 
+def test_uvr_ola_non_finite_outputs(device, od):
+    """Model outputs holding inf, -inf and NaN: the overlap-add divides by the weight sum as the
+    reference does (src/tfc_tdf.cpp:427, no nan_to_num), so an infinite sum stays infinite (the
+    correctly rounded quotient's residual would be inf - inf) and NaN stays NaN."""
+    length, chunk, n_fft, overlap = 5000, 512, 128, -1.0
+    plan = stx.UvrDemix(length, 2, chunk, n_fft, overlap)
+    y = synth.uniform(31, (plan.n_chunks, 2, 2, chunk))
+    y[1, 0, 0, 100] = np.inf
+    y[2, 1, 1, 7] = -np.inf
+    y[3, 0, 1, 300] = np.nan
+    assert plan.step == 384
+    y[4, 1, 0, 450] = np.inf
+    y[5, 1, 0, 450 - 384] = -np.inf                     # the same sample from two chunks: inf - inf
+    got = host(plan.overlap_add(dev(y, device)))
+    want = od.uvr_ola(y, length, chunk, n_fft, overlap)
+    assert np.isposinf(got).any() and np.isneginf(got).any() and np.isnan(got).any()
+    assert np.array_equal(got, want, equal_nan=True)
+
+
 def test_uvr_errors(device):
     with pytest.raises(stx.StxError) as e:
         stx.UvrDemix(1000, 2, 100, 128)
