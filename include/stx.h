@@ -72,9 +72,12 @@ STX_API const char* stx_last_error(void);
 typedef struct stx_fft stx_fft;
 
 /* st::FFT::FFT(int n) (src/stft.h:21-31): INVALID_ARGUMENT unless n is a power of two >= 2,
- * exactly like the reference; UNSUPPORTED for powers of two outside [16, 8192], which this
- * build has no kernels for. Allocates the plan's device tables (window, twiddles) on the
- * current device. */
+ * exactly like the reference; every such n up to 2^24 gives a plan (UNSUPPORTED above: the
+ * plan's scratch). Sizes 16..8192 serve every call below; 2, 4, 8 (register transforms) and
+ * sizes above 8192 (four steps: n1 x n2 transforms around transposes, scratch of n complex
+ * values owned by the plan) serve stx_fft_run only, and the STFT/iSTFT calls return
+ * UNSUPPORTED for them (the reference frames only at 2048 and 4096). Allocates the plan's
+ * device tables on the current device. */
 STX_API stx_status stx_fft_create(int n, stx_fft** out);
 /* st::VRFFT::VRFFT(int n) (src/vr_dsp.h:11-37), the plan the reference uses for sizes that are
  * not powers of two (TFC-TDF's n_fft 7680, src/tfc_tdf.cpp:85-86,551-552; VR's 320/640/960): any
@@ -88,7 +91,8 @@ STX_API void       stx_fft_destroy(stx_fft* fft);
 STX_API int        stx_fft_size(const stx_fft* fft);
 
 /* st::FFT::run(a, inverse) (src/stft.h:34-49), batched: data is device [batch][n] complex,
- * transformed in place, unnormalised; inverse uses conjugate twiddles (no 1/n). */
+ * transformed in place, unnormalised; inverse uses conjugate twiddles (no 1/n). Calls with a
+ * plan above 8192 points must not overlap (they share the plan's scratch). */
 STX_API stx_status stx_fft_run(const stx_fft* fft, float* data, int batch, int inverse,
                                stx_stream stream);
 

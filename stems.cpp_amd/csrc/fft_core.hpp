@@ -186,6 +186,26 @@ __device__ __forceinline__ void stage_twiddles(float2* twt, const float2* __rest
     stage_lds<TwTable<TN>::SIZE, NT>(twt, g, tid);
 }
 
+// stage_lds in two halves: load() issues a thread's share of a table into registers (at the top
+// of a kernel, so that the table's round trip overlaps the data loads), store() writes it to
+// LDS after the data loads have been issued; the caller's next barrier publishes it.
+template <int COUNT, int NT, class T>
+struct Staged {
+    static constexpr int R = (COUNT + NT - 1) / NT;
+    T v[R];
+    __device__ __forceinline__ void load(const T* __restrict__ src, int tid) {
+#pragma unroll
+        for (int r = 0; r < R; r++) v[r] = src[min(tid + r * NT, COUNT - 1)];
+    }
+    __device__ __forceinline__ void store(T* dst, int tid) const {
+#pragma unroll
+        for (int r = 0; r < R; r++)
+            if (tid + r * NT < COUNT) dst[tid + r * NT] = v[r];
+    }
+};
+template <int TN, int NT>
+using StagedTwiddles = Staged<TwTable<TN>::SIZE, NT, float2>;
+
 // Shape of an M-point transform with P points per thread.
 template <int M, int P, int TN_> struct FftCfg {
     static_assert(P == 8 || P == 16, "P must be 8 or 16");

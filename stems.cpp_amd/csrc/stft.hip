@@ -21,6 +21,7 @@
 //         once and writes it windowed to the workspace, the next sums and divides. This
 //         keeps every CU busy when there are few frames.
 #include <algorithm>
+#include <memory>
 #include <cmath>
 #include <vector>
 
@@ -36,6 +37,14 @@ struct stx_fft {
     float2* twn = nullptr;   // mixed: device [n], W_n^m
     stx::MixedRadix half;    // mixed: plan of the n/2-point transform of real frames
     stx::MixedRadix full;    // mixed: plan of the n-point complex transform
+    // Powers of two without STFT kernels (stx_fft_run only): 2, 4, 8 are register transforms;
+    // above 8192 the transform runs in four steps as n1 x n2 with the plans sub1, sub2 and a
+    // scratch of n complex values.
+    int run_only = 0;
+    int n1 = 0, n2 = 0;
+    stx_fft* sub1 = nullptr;
+    stx_fft* sub2 = nullptr;
+    float2* scratch = nullptr;
 };
 
 namespace stx {
@@ -101,6 +110,8 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void stft_kernel(StftArgs a) {
     const bool active = f < a.jobs;
     float2* buf = lds + slot * C::PADN;
 
+    StagedTwiddles<N, NT> tws;
+    tws.load(a.twt, tid);                              // overlaps the frame's loads
     const int c = active ? f / a.T : 0;
     const int t = active ? f - c * a.T : 0;
     const float* xc = a.x + (size_t)c * a.len;
@@ -135,7 +146,7 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void stft_kernel(StftArgs a) {
     for (int r = 0; r < P; r++) w[r] = win2[j + r * TPJ];
 #pragma unroll
     for (int r = 0; r < P; r++) v[r] = make_float2(v[r].x * w[r].x, v[r].y * w[r].y);
-    stage_twiddles<N, NT>(twt, a.twt, tid);
+    tws.store(twt, tid);
     fft_first_pass<M, P, N>(v, buf, j, NoPost{}, ToLds<P>{buf});
     __syncthreads();
     fft_rest_passes<M, P, N, P>(buf, j, twt, NoPost{}, ToLds<P>{buf});
@@ -262,6 +273,10 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_frames_kernel(IstftA
     const int f = lb * JOBS + slot;
     const bool active = f < a.jobs;
     float2* buf = lds + slot * C::PADN;
+    StagedTwiddles<N, NT> tws;
+    Staged<N, NT, float> wins;
+    tws.load(a.twt, tid);                              // overlap the spectrum loads
+    wins.load(a.win, tid);
     const int c = active ? f / a.T : 0;
     const int st = active ? f - c * a.T : 0;
     const float2* sc = a.spec + (size_t)c * a.T * a.F;
@@ -281,8 +296,8 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_frames_kernel(IstftA
         if (!active) xk[r] = make_float2(0.f, 0.f);
         if (!active || (km == M && !a.keep_nyquist)) xm[r] = make_float2(0.f, 0.f);
     }
-    stage_twiddles<N, NT>(twt, a.twt, tid);
-    stage_lds<N, NT>(wl, a.win, tid);
+    tws.store(twt, tid);
+    wins.store(wl, tid);
     __syncthreads();
     float2 v[P];
 #pragma unroll
@@ -613,19 +628,71 @@ __global__ __launch_bounds__(JOBS * (N / P)) void fft_kernel(float2* data, int b
     const bool active = job < batch;
     float2* buf = lds + slot * C::PADN;
     float2* d = data + (size_t)(active ? job : 0) * N;
+    StagedTwiddles<N, JOBS * TPJ> tws;
+    tws.load(gtw, tid);
     float2 v[P];
 #pragma unroll
     for (int r = 0; r < P; r++) {
         const float2 x = active ? d[j + r * TPJ] : make_float2(0.f, 0.f);
         v[r] = inverse ? cconj(x) : x;
     }
-    stage_twiddles<N, JOBS * TPJ>(twt, gtw, tid);
+    tws.store(twt, tid);
     auto sink = [&](int k, float2 y) {
         if (active) d[k] = inverse ? cconj(y) : y;
     };
     fft_first_pass<N, P, N>(v, buf, j, NoPost{}, sink);
     __syncthreads();
     fft_rest_passes<N, P, N, P>(buf, j, twt, NoPost{}, sink);
+}
+
+// Transforms of N = 2, 4 or 8 points, one per thread, in registers (the inverse as conj, forward
+// DFT, conj).
+template <int N>
+__global__ __launch_bounds__(256) void fft_small_kernel(float2* data, int batch, int inverse) {
+    const int b = (int)(blockIdx.x * 256 + threadIdx.x);
+    if (b >= batch) return;
+    float2* d = data + (size_t)b * N;
+    float2 v[N];
+#pragma unroll
+    for (int r = 0; r < N; r++) v[r] = inverse ? cconj(d[r]) : d[r];
+    Dft<N>::run(v);
+#pragma unroll
+    for (int r = 0; r < N; r++) d[r] = inverse ? cconj(v[r]) : v[r];
+}
+
+// Four-step transforms (n = n1 n2 > 8192): dst[c][r] = src[r][c] for a rows x cols complex
+// matrix, times W_n^(r c) (conjugated for the inverse) when `twiddle`, with W evaluated in
+// double; 32 x 32 tiles through LDS (one float2 of padding per row).
+__global__ __launch_bounds__(256) void transpose_c64_kernel(const float2* __restrict__ src, float2* __restrict__ dst,
+                                                            int rows, int cols, int twiddle, int n, int inverse) {
+    __shared__ float2 tile[32][33];
+    const int c0 = (int)blockIdx.x * 32, r0 = (int)blockIdx.y * 32;
+    const int tx = (int)threadIdx.x % 32, ty = (int)threadIdx.x / 32;
+#pragma unroll
+    for (int i = ty; i < 32; i += 8) {
+        const int r = r0 + i, c = c0 + tx;
+        if (r < rows && c < cols) {
+            float2 v = src[(size_t)r * cols + c];
+            if (twiddle) {
+                double sn, cs;
+                sincospi(2.0 * (double)((long long)r * c % n) / (double)n, &sn, &cs);
+                v = cmul(v, make_float2((float)cs, inverse ? (float)sn : (float)-sn));
+            }
+            tile[i][tx] = v;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = ty; i < 32; i += 8) {
+        const int c = c0 + i, r = r0 + tx;
+        if (r < rows && c < cols) dst[(size_t)c * rows + r] = tile[tx][i];
+    }
+}
+
+__global__ __launch_bounds__(256) void copy_c64_kernel(const float2* __restrict__ src, float2* __restrict__ dst,
+                                                       long long count) {
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i < count) dst[i] = src[i];
 }
 
 // ------------------------------------------------------------------------ dispatch
@@ -638,15 +705,23 @@ constexpr int kIstftPer = 6;                           // fused: output samples 
 constexpr int kStftP = 8;
 constexpr int fused_p(int n) { return n / 2 >= 16 ? 16 : 8; }
 
-template <int N>
-void launch_stft(const StftArgs& a0, hipStream_t s) {
-    constexpr int P = N >= 4096 ? 16 : kStftP;
+// One frame per workgroup in the T-major layout (the most workgroups); two in the F-major
+// layout, whose bins then leave as 16-byte runs of two frames per row instead of 8.
+template <int N, int JOBS>
+void launch_stft_jobs(StftArgs a, hipStream_t s) {
+    constexpr int P = kStftP;
     constexpr int TPJ = N / 2 / P;
-    constexpr int JOBS = block_jobs(TPJ, 256);
-    StftArgs a = a0;
     a.nblocks = (a.jobs + JOBS - 1) / JOBS;
     hipLaunchKernelGGL((stft_kernel<N, P, JOBS>), dim3(xcd_grid(a.nblocks)), dim3(JOBS * TPJ), 0, s, a);
     launch_check("stft_kernel");
+}
+
+template <int N>
+void launch_stft(const StftArgs& a, hipStream_t s) {
+    constexpr int TPJ = N / 2 / kStftP;
+    constexpr int J2 = TPJ * 2 <= 1024 ? 2 : 1;
+    if (a.layout == STX_SPEC_T_MAJOR) launch_stft_jobs<N, 1>(a, s);
+    else launch_stft_jobs<N, J2>(a, s);
 }
 
 // Tiles of m hops need m + ceil(N/hop) - 1 frames; m is chosen so that they fit one round of
@@ -744,8 +819,18 @@ template <int N> struct FftL {
     static void go(float2* d, int b, int inv, const float2* tw, hipStream_t s) { launch_fft<N>(d, b, inv, tw, s); }
 };
 
+// Largest power of two stx_fft_create accepts (its four-step scratch is n complex values).
+constexpr int kFftMaxRun = 1 << 24;
+
 void check_fft(const stx_fft* f) {
-    STX_REQUIRE(f != nullptr && f->n >= 16, "null FFT plan");
+    STX_REQUIRE(f != nullptr && f->n >= 2, "null FFT plan");
+}
+
+// A plan the STFT / iSTFT kernels can use (n_fft from 16 to 8192, or a mixed-radix size).
+void check_stft_plan(const stx_fft* f) {
+    check_fft(f);
+    if (f->run_only)
+        fail(STX_STATUS_UNSUPPORTED, "no STFT kernel for n_fft %d (power-of-two STFT sizes: 16..8192)", f->n);
 }
 
 void check_layout(int layout) {
@@ -799,7 +884,7 @@ stx_status torch_istft_impl(const stx_fft* f, const float* spec, int channels, i
                             int normalized, float* out, stx_spec_layout layout, void* ws, size_t ws_bytes,
                             stx_stream stream) {
     return guard([&] {
-        check_fft(f);
+        check_stft_plan(f);
         check_layout(layout);
         const int n = f->n;
         STX_REQUIRE(channels >= 0 && hop > 0 && n_frames >= 1, "bad channels/hop/n_frames");
@@ -832,7 +917,7 @@ stx_status torch_istft_impl(const stx_fft* f, const float* spec, int channels, i
 stx_status htdemucs_ispec_impl(const stx_fft* f, const float* spec, int channels, int n_frames, int length,
                                float* out, stx_spec_layout layout, void* ws, size_t ws_bytes, stx_stream stream) {
     return guard([&] {
-        check_fft(f);
+        check_stft_plan(f);
         if (f->mixed) fail(STX_STATUS_UNSUPPORTED, "htdemucs_ispec needs a power-of-two FFT size");
         check_layout(layout);
         const int n = f->n, hl = n / 4, pad = hl / 2 * 3;
@@ -886,7 +971,30 @@ STX_API stx_status stx_fft_create(int n, stx_fft** out) {
         *out = nullptr;
         // st::FFT's own check (src/stft.h:22).
         if (n < 2 || (n & (n - 1))) fail(STX_STATUS_INVALID_ARGUMENT, "FFT size must be a power of two");
-        if (n < 16 || n > 8192) fail(STX_STATUS_UNSUPPORTED, "FFT size %d has no kernel (supported: 16..8192)", n);
+        if (n > kFftMaxRun)
+            fail(STX_STATUS_UNSUPPORTED, "FFT size %d is above %d (the four-step scratch limit)", n, kFftMaxRun);
+        if (n < 16 || n > 8192) {
+            std::unique_ptr<stx_fft, void (*)(stx_fft*)> f(new stx_fft, stx_fft_destroy);
+            f->n = n;
+            f->run_only = 1;
+            hip_check(hipGetDevice(&f->device), "hipGetDevice");
+            if (n > 8192) {
+                const int b = ilog2(n);
+                f->n1 = 1 << ((b + 1) / 2);
+                f->n2 = n / f->n1;
+                stx_fft* s1 = nullptr;
+                stx_fft* s2 = nullptr;
+                const stx_status st1 = stx_fft_create(f->n1, &s1);
+                f->sub1 = s1;
+                if (st1 != STX_STATUS_OK) fail(st1, "%s", stx_last_error());
+                const stx_status st2 = stx_fft_create(f->n2, &s2);
+                f->sub2 = s2;
+                if (st2 != STX_STATUS_OK) fail(st2, "%s", stx_last_error());
+                hip_check(hipMalloc(&f->scratch, sizeof(float2) * (size_t)n), "hipMalloc(FFT scratch)");
+            }
+            *out = f.release();
+            return;
+        }
         const int lbits = (ilog2(n) + 1) / 2, L = 1 << lbits, H = n / L;
         std::vector<float2> twt(L + H);
         auto w_n = [n](long long m) {
@@ -948,6 +1056,9 @@ STX_API stx_status stx_fft_create_any(int n, stx_fft** out) {
 
 STX_API void stx_fft_destroy(stx_fft* f) {
     if (!f) return;
+    if (f->sub1) stx_fft_destroy(f->sub1);
+    if (f->sub2) stx_fft_destroy(f->sub2);
+    if (f->scratch) (void)hipFree(f->scratch);
     if (f->twt) (void)hipFree(f->twt);
     if (f->win) (void)hipFree(f->win);
     if (f->twn) (void)hipFree(f->twn);
@@ -963,6 +1074,39 @@ STX_API stx_status stx_fft_run(const stx_fft* f, float* data, int batch, int inv
         if (batch == 0) return;
         STX_REQUIRE(data != nullptr, "data is NULL");
         check_extent((long long)batch * f->n, "FFT batch");
+        const hipStream_t st = as_stream(stream);
+        float2* d2 = reinterpret_cast<float2*>(data);
+        const int inv = inverse ? 1 : 0;
+        if (f->run_only && f->n <= 8) {
+            const unsigned grid = (unsigned)((batch + 255) / 256);
+            if (f->n == 2) hipLaunchKernelGGL(fft_small_kernel<2>, dim3(grid), dim3(256), 0, st, d2, batch, inv);
+            else if (f->n == 4) hipLaunchKernelGGL(fft_small_kernel<4>, dim3(grid), dim3(256), 0, st, d2, batch, inv);
+            else hipLaunchKernelGGL(fft_small_kernel<8>, dim3(grid), dim3(256), 0, st, d2, batch, inv);
+            launch_check("fft_small_kernel");
+            return;
+        }
+        if (f->run_only) {
+            // x[n2 m1 + m2] as A[m1][m2] (n1 x n2): transpose, n2 transforms of n1 points, twiddle
+            // W_n^(m2 k1) and transpose, n1 transforms of n2 points, transpose: X[k1 + n1 k2].
+            const int n1 = f->n1, n2 = f->n2;
+            auto transpose = [&](const float2* src, float2* dst, int rows, int cols, int tw) {
+                hipLaunchKernelGGL(transpose_c64_kernel, dim3((unsigned)((cols + 31) / 32), (unsigned)((rows + 31) / 32)),
+                                   dim3(256), 0, st, src, dst, rows, cols, tw, f->n, inv);
+                launch_check("transpose_c64_kernel");
+            };
+            for (int b = 0; b < batch; b++) {
+                float2* d = d2 + (size_t)b * f->n;
+                transpose(d, f->scratch, n1, n2, 0);
+                by_size<FftL>(n1, f->scratch, n2, inv, f->sub1->twt, st);
+                transpose(f->scratch, d, n2, n1, 1);
+                by_size<FftL>(n2, d, n1, inv, f->sub2->twt, st);
+                transpose(d, f->scratch, n1, n2, 0);
+                hipLaunchKernelGGL(copy_c64_kernel, dim3((unsigned)((f->n + 255) / 256)), dim3(256), 0, st,
+                                   f->scratch, d, (long long)f->n);
+                launch_check("copy_c64_kernel");
+            }
+            return;
+        }
         if (f->mixed) {
             if (f->n > 8192) fail(STX_STATUS_UNSUPPORTED, "complex transforms of %d points (at most 8192)", f->n);
             if (f->n <= 1024)
@@ -994,7 +1138,7 @@ STX_API int stx_htdemucs_frames(int n_fft, int len) {
 STX_API stx_status stx_torch_stft(const stx_fft* f, const float* x, int channels, int len, int hop,
                                   int normalized, float* spec, stx_spec_layout layout, stx_stream stream) {
     return guard([&] {
-        check_fft(f);
+        check_stft_plan(f);
         check_layout(layout);
         const int n = f->n;
         STX_REQUIRE(channels >= 0 && hop > 0 && len >= 0, "bad channels/hop/len");
@@ -1040,7 +1184,7 @@ STX_API stx_status stx_torch_stft(const stx_fft* f, const float* x, int channels
 STX_API stx_status stx_htdemucs_spec(const stx_fft* f, const float* x, int channels, int len, float* spec,
                                      stx_spec_layout layout, stx_stream stream) {
     return guard([&] {
-        check_fft(f);
+        check_stft_plan(f);
         if (f->mixed) fail(STX_STATUS_UNSUPPORTED, "htdemucs_spec needs a power-of-two FFT size");
         check_layout(layout);
         const int n = f->n, hl = n / 4;

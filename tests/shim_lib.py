@@ -17,6 +17,8 @@ def lib():
         if not os.path.exists(PATH):
             raise OSError(f"{PATH} not built (make -C tests/cpp)")
         L = ctypes.CDLL(PATH)
+        L.shim_time_htdemucs_round_trip.restype = ctypes.c_double
+        L.shim_time_htdemucs_round_trip.argtypes = [_i, _vp, _i, _i, _i]
         for name, args in {
             "shim_fft_create": [_i],
             "shim_fft_run": [_i, _vp, _i, _i],
@@ -25,6 +27,8 @@ def lib():
             "shim_torch_stft": [_i, _vp, _i, _i, _i, _vp, _vp],
             "shim_torch_istft": [_i, _vp, _i, _i, _i, _vp],
             "shim_istft_short_spectrum": [_i],
+            "shim_fft_run_prefix": [_i, _vp, _i, _i],
+            "shim_fft_run_short": [_i],
         }.items():
             fn = getattr(L, name)
             fn.restype = _i
@@ -41,6 +45,13 @@ def fft(a, inverse=False):
     a = np.ascontiguousarray(a, dtype=np.complex128).copy()
     n = a.shape[-1]
     rc = lib().shim_fft_run(n, _p(a), a.size // n, int(inverse))
+    return rc, a
+
+
+def fft_prefix(a, n, inverse=False):
+    """st::FFT(n).run on the whole vector a (len >= n)."""
+    a = np.ascontiguousarray(a, dtype=np.complex128).copy()
+    rc = lib().shim_fft_run_prefix(n, _p(a), a.size, int(inverse))
     return rc, a
 
 

@@ -37,7 +37,7 @@ def test_version_and_error():
 
 
 @pytest.mark.parametrize("n,status", [(12, stx.STATUS_INVALID_ARGUMENT), (0, stx.STATUS_INVALID_ARGUMENT),
-                                      (4, stx.STATUS_UNSUPPORTED), (16384, stx.STATUS_UNSUPPORTED)])
+                                      (1, stx.STATUS_INVALID_ARGUMENT), (1 << 25, stx.STATUS_UNSUPPORTED)])
 def test_fft_create_rejects(n, status):
     h = ctypes.c_void_p()
     assert stx.lib().stx_fft_create(n, ctypes.byref(h)) == status

@@ -43,7 +43,7 @@ def test_shim_torch_round_trip_c3(device, orc, normalized):
     assert snr_db(y, orc.torch_istft(want, 2048, 441, normalized)) >= SNR_DB
 
 
-@pytest.mark.parametrize("n", [16, 1024, 4096])
+@pytest.mark.parametrize("n", [2, 8, 16, 1024, 4096, 16384])
 def test_shim_fft(device, orc, n):
     a = (synth.normal(n, (3, n), 1.0) + 1j * synth.normal(n + 1, (3, n), 1.0)).astype(np.complex128)
     for inverse in (False, True):
@@ -51,6 +51,18 @@ def test_shim_fft(device, orc, n):
         assert rc == 0
         want = np.stack([orc.fft(row, inverse) for row in a])
         assert snr_db(got, want) >= SNR_DB
+
+
+def test_shim_fft_transforms_exactly_n_points(device, orc):
+    """src/stft.h:35-49 transforms a[0..n) and leaves the rest of the vector alone."""
+    n, extra = 1024, 77
+    a = (synth.normal(5, (n + extra,), 1.0) + 1j * synth.normal(6, (n + extra,), 1.0)).astype(np.complex128)
+    for inverse in (False, True):
+        rc, got = shim_lib.fft_prefix(a, n, inverse)
+        assert rc == 0
+        assert snr_db(got[:n], orc.fft(a[:n], inverse)) >= SNR_DB
+        assert np.array_equal(got[n:], a[n:])
+    assert shim_lib.lib().shim_fft_run_short(n) == 1          # shorter than n: std::invalid_argument
 
 
 def test_shim_exceptions(device):

@@ -165,7 +165,9 @@ def test_every_fft_size_stft_round_trip(device, orc, n, use_ws):
             assert snr_db(y2h[c], orc.htdemucs_ispec(ref, n, length)) >= SNR_DB
 
 
-@pytest.mark.parametrize("n", [16, 256, 2048, 4096, 8192])
+# Every power of two st::FFT accepts (src/stft.h:21-22): 2, 4, 8 as register transforms, 16 to
+# 8192 as LDS kernels, and above 8192 in four steps (n1 x n2 transforms around transposes).
+@pytest.mark.parametrize("n", [2, 4, 8, 16, 256, 2048, 4096, 8192, 16384, 32768, 1 << 20])
 def test_fft_run_against_oracle(device, orc, n):
     import torch
     v = synth.normal(n, (3, 2 * n), 1.0).astype(np.float64)
@@ -179,6 +181,19 @@ def test_fft_run_against_oracle(device, orc, n):
         assert snr_db(fw[b], orc.fft(a[b].astype(np.complex64).astype(np.complex128))) >= SNR_DB
         assert snr_db(back[b], a[b].astype(np.complex64)) >= SNR_DB
     del torch
+
+
+def test_fft_run_only_sizes_have_no_stft(device):
+    """Sizes with only a complex transform (2, 4, 8 and above 8192) report UNSUPPORTED for the
+    STFT/iSTFT; the reference never frames at those sizes."""
+    import torch
+    x = torch.zeros((1, 100000), dtype=torch.float32, device=device)
+    for n in (8, 16384):
+        f = plan(n)
+        assert f.size() == n
+        with pytest.raises(stx.StxError) as e:
+            stx.torch_stft(f, x, n // 4)
+        assert e.value.status == stx.STATUS_UNSUPPORTED
 
 
 def test_fft_impulse_known_answer(device):

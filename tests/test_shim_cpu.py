@@ -7,4 +7,4 @@ def test_shim_helper_loads_and_rejects_bad_sizes():
     L = shim_lib.lib()
     assert L.shim_fft_create(3) == 1       # not a power of two: std::invalid_argument
     assert L.shim_fft_create(0) == 1
-    assert L.shim_fft_create(1 << 20) == 2   # a power of two with no kernel here: runtime_error
+    assert L.shim_fft_create(1 << 25) == 2   # a power of two above the plan limit: runtime_error
