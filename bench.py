@@ -10,11 +10,13 @@ The 8 calls (8 kernels) of a step are captured once into a HIP graph per buffer 
 replayed on one stream; buffer sets rotate so that more than 512 MB is touched between reuses,
 larger than the 256 MB Infinity Cache: cold-cache numbers.
 
-value = algorithmic bytes per step / step time, in GB/s, with the algorithmic bytes of the
+value = algorithmic bytes per step / step time, in GB/s (cold), with the algorithmic bytes of the
 reference's decomposition of the op set (one unit per op, each reading its inputs and writing
 its output once): GroupNorm+affine 8, GELU 8, GLU 12 and LayerScale MUL + residual ADD 12 bytes
 per element of [C, T] (40 in all, plus the parameters). Fusion moves fewer bytes than that:
-config.bytes_moved_per_step gives the minimum these kernels move (24 per element).
+config.bytes_moved_per_step gives the minimum these kernels move (24 per element); moved_GBps is
+that over the same step time (the bytes the kernels really move), warm the same step replayed on
+one buffer set that stays in the Infinity Cache.
 roofline: the op with the largest share of the step (GroupNorm+GELU): its algorithmic bytes
 (8 per element) / its duration (gn_fused_kernel, one grid-synchronised pass), from a graph of instances
 of that op on more than 512 MB of distinct buffers (cold, like the step) replayed between two
@@ -42,6 +44,7 @@ its algorithmic bytes and against a plain device copy of the same bytes at the s
 (copy_us; frac_of_copy = copy_us / us), the practical ceiling for small, launch-bound sizes.
 """
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -183,6 +186,13 @@ def run_ops(args, torch, stx, dev):
     t1.record(cur)
     torch.cuda.synchronize()
     ms_per_step = t0.elapsed_time(t1) / args.steps
+    # Warm: the same step replayed on one buffer set (its 155 MB stay in the Infinity Cache).
+    t0.record(cur)
+    for i in range(args.steps):
+        graphs[0].replay()
+    t1.record(cur)
+    torch.cuda.synchronize()
+    ms_per_step_warm = t0.elapsed_time(t1) / args.steps
 
     # Per-op durations, cold like the step: per (op, shape), one graph of instances on their
     # own buffers, more than 512 MB of them, replayed between two HIP events on the stream the
@@ -222,9 +232,15 @@ def run_ops(args, torch, stx, dev):
     step_bytes = sum(sum(v) for v in op_bytes().values())
     kernel_names = {"gn": "group_norm+affine+gelu (gn_fused_kernel<channel,gelu>: one grid-synchronised pass)",
                     "glu_scale_residual": "glu + layer scale + residual (ew_flat_kernel<GLU_MUL_ADD>)"}
+    moved = sum(sum(v) for v in moved_bytes().values())
     res = {
         "value": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
         "ms_per_step": round(ms_per_step, 6),
+        "moved_GBps": round(moved / (ms_per_step * 1e-3) / 1e9, 1),
+        "moved_frac_of_peak": round(moved / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "warm": {"ms_per_step": round(ms_per_step_warm, 6),
+                 "value": round(step_bytes / (ms_per_step_warm * 1e-3) / 1e9, 1),
+                 "moved_GBps": round(moved / (ms_per_step_warm * 1e-3) / 1e9, 1)},
         "config": {
             "workload": "htdemucs_op_set: GroupNorm(1)+affine then GELU on [1,C,T]; GLU 2C->C then LayerScale MUL + residual ADD",
             "shapes_CT": [list(s) for s in SHAPES],
@@ -251,16 +267,48 @@ def run_ops(args, torch, stx, dev):
     return res, ops
 
 
-def cpu_threads():
-    """Physical cores, capped by the job's OMP_NUM_THREADS share when it is set."""
+def physical_cores():
+    """Physical cores as the reference counts them (src/backend_loader.cpp:57-95, Linux branch):
+    one per distinct thread_siblings_list over the logical CPUs, else the logical count."""
+    logical = os.cpu_count() or 1
+    cores = set()
+    for i in range(logical):
+        try:
+            with open(f"/sys/devices/system/cpu/cpu{i}/topology/thread_siblings_list") as f:
+                cores.add(f.readline().strip())
+        except OSError:
+            pass
+    return len(cores) if cores else logical
+
+
+def host_cpu():
+    """The CPU baseline's host: model name, physical cores, logical CPUs, the CPUs this process
+    may run on and the job's thread cap (OMP_NUM_THREADS)."""
+    model = "unknown"
     try:
-        import psutil
-        n = psutil.cpu_count(logical=False) or os.cpu_count() or 1
-    except ImportError:
-        n = os.cpu_count() or 1
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = os.cpu_count() or 1
     omp = os.environ.get("OMP_NUM_THREADS")
-    if omp and omp.isdigit() and int(omp) > 0:
-        n = min(n, int(omp))
+    return {"cpu_model": model, "physical_cores": physical_cores(), "logical_cpus": os.cpu_count() or 1,
+            "affinity_cpus": affinity, "thread_cap": int(omp) if omp and omp.isdigit() else None}
+
+
+def cpu_threads():
+    """Threads for the multi-core CPU figures: the physical cores (ggml's default thread count in
+    the reference), capped by the CPUs this process may use and the job's OMP_NUM_THREADS."""
+    h = host_cpu()
+    n = min(h["physical_cores"], h["affinity_cpus"])
+    if h["thread_cap"]:
+        n = min(n, h["thread_cap"])
     return max(1, n)
 
 
@@ -319,6 +367,7 @@ def cpu_ops_baseline(budget_s):
                   "from the reference)",
         "single_thread": {"value": round(steps1 * step_bytes / el1 / 1e9, 3), "unit": "GB/s", "cores": 1,
                           "sample": f"{steps1} steps in {el1:.1f} s"},
+        "host": host_cpu(),
     }
 
 
@@ -366,6 +415,20 @@ def run_spectral(args, torch, stx, dev):
         out["htdemucs_round_trip"][f"{name}_us"] = round(t, 3)
         out["htdemucs_round_trip"][f"{name}_GBps"] = round(alg / (t * 1e-6) / 1e9, 1)
     del xs, specs, ys
+    # The same round trip through the drop-in C++ shim (include/stx_st.hpp) on host buffers, as
+    # src/htdemucs.cpp:428,470 call src/stft.h: one st::FFT reused, per channel htdemucs_spec then
+    # htdemucs_ispec; includes the PCIe copies and the complex<double> <-> complex64 conversion.
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    try:
+        import shim_lib
+        sec = shim_lib.lib().shim_time_htdemucs_round_trip(n_fft, x_host.ctypes.data_as(ctypes.c_void_p), C, L, 10)
+        if sec > 0:
+            out["htdemucs_round_trip_st_shim"] = {
+                "metric": "Msamples/s", "value": round(C * L / sec / 1e6, 3), "ms_per_step": round(sec * 1e3, 6),
+                "note": "stx_st.hpp on host vectors: st::htdemucs_spec + st::htdemucs_ispec per channel, one FFT "
+                        "object reused, PCIe copies and complex<double> conversion included"}
+    except OSError as e:
+        out["htdemucs_round_trip_st_shim"] = {"skipped": str(e)}
 
     # RoFormer chunk: STFT -> mask scatter-average + apply -> iSTFT.
     n_fft, hop, L, C, S = 2048, 441, 352800, 2, 1
@@ -416,8 +479,15 @@ def time_graphs(torch, stream, fn, copies, steps, samples, warmup):
     t1.record(cur)
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / steps
+    t0.record(cur)
+    for i in range(steps):
+        graphs[0].replay()                             # warm: one buffer set, kept in the Infinity Cache
+    t1.record(cur)
+    torch.cuda.synchronize()
+    warm = t0.elapsed_time(t1) / steps
     return {"metric": "Msamples/s", "value": round(samples / (ms * 1e-3) / 1e6, 3), "ms_per_step": round(ms, 6),
-            "steps": steps}
+            "steps": steps, "warm_value": round(samples / (warm * 1e-3) / 1e6, 3),
+            "warm_ms_per_step": round(warm, 6)}
 
 
 def time_call(torch, stream, make, nbytes, replays=3):
@@ -440,10 +510,26 @@ def time_call(torch, stream, make, nbytes, replays=3):
         e1.record(stream)
     e1.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / (replays * n_inst)
-    del gr, calls
+    del gr
+    # Warm: one instance's buffers, which stay in the 256 MB Infinity Cache when they fit,
+    # captured WARM_REPS times into one graph and replayed.
+    WARM_REPS = 20
+    with torch.cuda.stream(stream):
+        gw = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gw, stream=stream):
+            for _ in range(WARM_REPS):
+                calls[0]()
+        gw.replay()
+        e0.record(stream)
+        for _ in range(replays):
+            gw.replay()
+        e1.record(stream)
+    e1.synchronize()
+    warm = e0.elapsed_time(e1) * 1e3 / (replays * WARM_REPS)
+    del gw, calls
     torch.cuda.empty_cache()
     return {"us": round(us, 3), "algorithmic_bytes": int(nbytes), "GBps": round(nbytes / us / 1e3, 1),
-            "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+            "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "warm_us": round(warm, 3)}
 
 
 def run_rows(torch, stx, dev):
@@ -465,6 +551,11 @@ def run_rows(torch, stx, dev):
         x, y = rn(C, L), torch.empty((C, T, F), dtype=torch.complex64, device=dev)
         return lambda: stx.torch_stft(fft, x, hop, layout=stx.T_MAJOR, out=y, stream=stream)
     out["c3_stft_t_major"] = time_call(torch, stream, mk_stft, C * L * 4 + C * T * F * 8)
+
+    def mk_stft_f():
+        x, y = rn(C, L), torch.empty((C, F, T), dtype=torch.complex64, device=dev)
+        return lambda: stx.torch_stft(fft, x, hop, layout=stx.F_MAJOR, out=y, stream=stream)
+    out["c3_stft_f_major"] = time_call(torch, stream, mk_stft_f, C * L * 4 + C * T * F * 8)
 
     def mk_gather():
         z, f = torch.randn((1, C, T, F), dtype=torch.complex64, device=dev), torch.empty((1, feat), device=dev)
@@ -496,6 +587,11 @@ def run_rows(torch, stx, dev):
         z, y = torch.randn((C, T, F), dtype=torch.complex64, device=dev), torch.empty((C, hop * (T - 1)), device=dev)
         return lambda: stx.torch_istft(fft, z, hop, layout=stx.T_MAJOR, out=y, stream=stream)
     out["c3_istft_t_major"] = time_call(torch, stream, mk_istft, C * L * 4 + C * T * F * 8)
+
+    def mk_istft_f():
+        z, y = torch.randn((C, F, T), dtype=torch.complex64, device=dev), torch.empty((C, hop * (T - 1)), device=dev)
+        return lambda: stx.torch_istft(fft, z, hop, layout=stx.F_MAJOR, out=y, stream=stream)
+    out["c3_istft_f_major"] = time_call(torch, stream, mk_istft_f, C * L * 4 + C * T * F * 8)
 
     def mk_istft_ws():
         z, y = torch.randn((C, T, F), dtype=torch.complex64, device=dev), torch.empty((C, hop * (T - 1)), device=dev)
@@ -727,7 +823,8 @@ def cpu_spectral_baseline(budget_s):
             "sample": f"{reps1} single-channel HTDemucs-spec STFT->iSTFT round trips of {L} samples ({el1:.1f} s, "
                       f"single thread, double precision, {what})",
             "multi_core": {"value": round(repsn * L / eln / 1e6, 3), "unit": "Msamples/s", "cores": n,
-                           "sample": f"{repsn} channel round trips in {eln:.1f} s on {n} threads"}}
+                           "sample": f"{repsn} channel round trips in {eln:.1f} s on {n} threads"},
+            "host": host_cpu()}
 
 
 def main():
@@ -758,6 +855,9 @@ def main():
         "config": res["config"],
         "roofline": res["roofline"],
         "hbm_frac_of_peak": round(res["value"] / HBM_PEAK_GBS, 4),
+        "moved_GBps": res["moved_GBps"],
+        "moved_frac_of_peak": res["moved_frac_of_peak"],
+        "warm": res["warm"],
         "ops_us": res["ops_us"],
         "ops_share_us": res["ops_share_us"],
     }
