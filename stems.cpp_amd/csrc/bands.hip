@@ -4,19 +4,22 @@
 // average, apply, zero_dc). Both are rewritten in gather form so that no two threads write
 // one element:
 //   * band gather: band b's features are one contiguous block [T][size_b * C] of complex
-//     values (feat[t][(j*C + c)*2 + {re,im}]). T-major spectra: the output is walked flat,
-//     8 values per thread, each thread finding its band by a binary search over the band
-//     starts staged in LDS and its (channel, bin) in a per-pair table built once per band
-//     table; all loads are issued before the first store. F-major spectra: one workgroup per
-//     (band, tile of frames) through an LDS transpose, so that both sides stay coalesced.
+//     values (feat[t][(j*C + c)*2 + {re,im}]). T-major spectra: one workgroup per frame stages
+//     the frame's C rows in LDS with its first loads and writes every (band, position) entry's
+//     C values from there, guided by one 8-byte record per entry (no table search before the
+//     spectrum loads); frames too wide for LDS walk the output flat, 8 values per thread,
+//     finding their band by a binary search over the band starts. F-major spectra: one
+//     workgroup per (band, tile of frames) through an LDS transpose, so that both sides stay
+//     coalesced.
 //   * scatter + apply: a thread per (bin, channel) and tile of frames (T-major) or per frame
-//     (F-major) walks the list of (band, position) pairs that cover its bin (a CSR table
-//     built once per band table, in the reference's band-then-position order), sums their
-//     mask values in double, divides by the band count and multiplies the spectrum, all in
-//     double like the reference, and rounds once. Neighbouring lanes take neighbouring
-//     (bin, channel) pairs, which are neighbouring floats of the mask rows, so mask reads are
-//     coalesced in T-major layout; the T-major thread reads its CSR entries once for all of
-//     its frames and issues the frames' loads together.
+//     (F-major) sums the mask values of the (band, position) pairs that cover its bin in the
+//     reference's band-then-position order, in double, divides by the band count and
+//     multiplies the spectrum, all in double like the reference, and rounds once. The pairs
+//     come from one 16-byte record per bin when no bin has more than two (the mel and
+//     band-split maps), else from a CSR table built once per band table. Neighbouring lanes
+//     take neighbouring (bin, channel) pairs, which are neighbouring floats of the mask rows,
+//     so mask reads are coalesced in T-major layout, and each thread issues its frames' loads
+//     together.
 #include <algorithm>
 #include <type_traits>
 #include <vector>
@@ -35,6 +38,23 @@ struct CsrEntry {
     int din;                 // dim_in(b) = size * C * 2
     int col;                 // j * C * 2: the bin's column inside the band's rows
 };
+// A bin's covering (band, position) pairs when there are at most two, in CSR order: one 16-byte
+// load instead of the CSR offsets, the entries and the denominator. din[1] == 0: one pair;
+// din[0] == 0: none. A missing pair repeats a valid address (entry 0, or the first mask value)
+// and is not added.
+struct BinBands {
+    int feat_off[2];
+    unsigned short din[2];
+    unsigned short col[2];
+};
+static_assert(sizeof(BinBands) == 16, "BinBands is one 16-byte load");
+// One (band, position) entry of the band table, in feature order.
+struct GatherRec {
+    int first;               // freq_off[b]: the band's first entry
+    unsigned short size;     // band_sizes[b]
+    unsigned short bin;      // band_freqs[entry]
+};
+static_assert(sizeof(GatherRec) == 8, "GatherRec is one 8-byte load");
 }  // namespace stx
 
 struct stx_bands {
@@ -48,6 +68,8 @@ struct stx_bands {
     int* d_csr_off = nullptr;                        // [n_bins + 1]
     stx::CsrEntry* d_csr = nullptr;                  // [n_freqs]
     double* d_denom = nullptr;                       // [n_bins]: max(bands_per_freq, 1)
+    stx::BinBands* d_bin_bands = nullptr;            // [n_bins] when every bin has at most two pairs
+    stx::GatherRec* d_gather_rec = nullptr;          // [n_freqs] when sizes and bins fit 16 bits
     int* d_pair_off = nullptr;                       // [n_bands + 1]: first (bin, channel) pair of band b
     int* d_pair_code = nullptr;                      // [total_feat / 2]: (channel << 16) | bin of each pair
     int* d_freq_lo = nullptr;                        // [n_bands]: first bin of each band
@@ -68,6 +90,9 @@ struct GatherArgs {
     const int* freq_lo;      // [n_bands]: first bin of each band when every band is a bin range
     const stx::FastDiv* pair_div;   // [n_bands]: division by the band's pairs per frame
     stx::FastDiv cdiv;       // division by C
+    const GatherRec* rec;    // [n_entries] (band_gather_frame_kernel)
+    int n_entries;           // n_freqs
+    stx::FastDiv fdiv;       // division by F
     int C, F, T;
     int n_bands;
     long long total_feat;    // floats per frame of one batch item
@@ -136,6 +161,70 @@ __global__ __launch_bounds__(256) void band_gather_t_kernel(GatherArgs a) {
         if (e0 + k * 256 < n) fb[e0 + k * 256] = v[k];
 }
 
+// T-major, one workgroup per frame: the frame's C rows of F bins (contiguous in this layout)
+// are loaded into LDS with the first loads of the kernel, together with the thread's entry
+// records; each thread then takes entries e (band b, position j) and writes the C values of
+// bin band_freqs[e] to feat[C * (first_b * T + t * size_b + j) + c], one contiguous C * 8-byte
+// store (16 bytes at C = 2). Nothing waits on a table lookup before the spectrum is in flight,
+// and each spectrum value is read from HBM once however many bands cover its bin.
+// Workgroups are dealt to the XCDs in runs of consecutive frames, so the partial lines where
+// band rows of neighbouring frames meet merge in one L2.
+template <int CC, int NT, int ROW, int OUT>          // channels (0: a.C at run time); threads;
+__global__ __launch_bounds__(NT) void band_gather_frame_kernel(GatherArgs a) {   // per thread
+    extern __shared__ float2 row[];                  // [C][F]
+    const int t = xcd_block();
+    if (t >= a.T) return;                            // uniform per workgroup
+    const int C = CC > 0 ? CC : a.C;
+    const int tid = (int)threadIdx.x;
+    const int F = a.F, E = a.n_entries, n = C * F;
+    const size_t plane = (size_t)a.T * F;
+    const size_t bt = blockIdx.y;
+    const float2* sb = a.spec + bt * C * plane + (size_t)t * F;
+    GatherRec r[OUT];
+    auto load_recs = [&](int e0) {
+#pragma unroll
+        for (int k = 0; k < OUT; k++) r[k] = a.rec[min(e0 + tid + k * NT, E - 1)];
+    };
+    load_recs(0);
+    for (int i0 = 0; i0 < n; i0 += NT * ROW) {
+        float2 v[ROW];
+#pragma unroll
+        for (int k = 0; k < ROW; k++) {
+            const int i = min(i0 + tid + k * NT, n - 1);
+            const int c = CC == 1 ? 0 : CC == 2 ? (i >= F ? 1 : 0) : (int)a.fdiv.div((unsigned)i);
+            v[k] = sb[(size_t)c * plane + (i - c * F)];
+        }
+#pragma unroll
+        for (int k = 0; k < ROW; k++)
+            if (i0 + tid + k * NT < n) row[i0 + tid + k * NT] = v[k];
+    }
+    __syncthreads();
+    float2* fb = a.feat + bt * ((size_t)E * C * a.T);
+    for (int e0 = 0; e0 < E; e0 += NT * OUT) {
+        if (e0 > 0) load_recs(e0);
+#pragma unroll
+        for (int k = 0; k < OUT; k++) {
+            const int e = e0 + tid + k * NT;
+            if (e >= E) break;
+            const GatherRec R = r[k];
+            float2* d = fb + (size_t)C * ((size_t)R.first * a.T + (size_t)t * R.size + (e - R.first));
+            if constexpr (CC == 2) {
+                const float2 v0 = row[R.bin], v1 = row[F + R.bin];
+                store_stream(reinterpret_cast<float4*>(d), make_float4(v0.x, v0.y, v1.x, v1.y));
+            } else {
+                for (int c = 0; c < C; c++) store_stream(d + c, row[c * F + R.bin]);
+            }
+        }
+    }
+}
+
+// The frame gather's shape: 256 threads, 9 row values (C * F = 2050 at n_fft 2048 stereo in one
+// batch of 2304) and 8 entries (2048 >= the 1,979 of the 60-band mel map) per thread per batch.
+template <int CC>
+void launch_gather_frame(const GatherArgs& a, dim3 grid, size_t lds, hipStream_t s) {
+    hipLaunchKernelGGL((band_gather_frame_kernel<CC, 256, 9, 8>), grid, dim3(256), lds, s, a);
+}
+
 // F-major: a tile [pairs][TT] is read along t (coalesced) into LDS and written along the
 // band rows (coalesced).
 __global__ __launch_bounds__(256) void band_gather_f_kernel(GatherArgs a) {
@@ -172,6 +261,8 @@ struct ScatterArgs {
     const int* csr_off;
     const CsrEntry* csr;
     const double* denom;
+    const BinBands* rec;     // per-bin pairs (band_scatter_rec_kernel)
+    stx::FastDiv fc_div, c_div;   // by F * C and by C (band_scatter_rec_kernel)
     int C, F, T, S, zero_dc;
     long long total_feat;
 };
@@ -259,6 +350,67 @@ __global__ __launch_bounds__(256) void band_scatter_t_kernel(ScatterArgs a) {
             o = make_float2((float)(zr * qr - zi * qi), (float)(zr * qi + zi * qr));
         }
         oc[(size_t)(t0 + k) * a.F] = o;
+    }
+}
+
+// T-major with per-bin records (every bin in at most two (band, position) pairs, as in the mel
+// and band-split maps): thread = (tile of kScatterRecFrames frames, bin, channel), numbered with
+// (bin, channel) fastest so that no workgroup idles at the end of a tile. The record load is
+// issued with the spectrum loads, so the masks are one memory trip behind, not two. With no
+// table walk to amortise, 2 frames per thread (twice the workgroups of 4, 4x those of 8) hides
+// the most latency; the output is stored with the non-temporal hint.
+constexpr int kScatterRecFrames = 2;
+
+__global__ __launch_bounds__(256) void band_scatter_rec_kernel(ScatterArgs a, unsigned n) {
+#pragma clang fp contract(off)
+    const unsigned i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= n) return;
+    const int tile = (int)a.fc_div.div(i);
+    const int fc = (int)(i - (unsigned)tile * a.fc_div.d);
+    const int f = (int)a.c_div.div((unsigned)fc), c = fc - f * a.C;
+    const int t0 = tile * kScatterRecFrames;
+    const int bt = (int)blockIdx.y / a.S, s = (int)blockIdx.y % a.S;
+    const BinBands R = a.rec[f];
+    const float* mb = a.masks + ((size_t)bt * a.S + s) * a.total_feat * a.T + 2 * c;
+    const float2* zc = a.spec + (((size_t)bt * a.C + c) * a.T) * a.F + f;
+    int tt[kScatterRecFrames];
+    float2 z[kScatterRecFrames];
+#pragma unroll
+    for (int k = 0; k < kScatterRecFrames; k++) {
+        tt[k] = min(t0 + k, a.T - 1);
+        z[k] = zc[(size_t)tt[k] * a.F];
+    }
+    const float* r0 = mb + (size_t)R.feat_off[0] * a.T + R.col[0];
+    const float* r1 = mb + (size_t)R.feat_off[1] * a.T + R.col[1];
+    float2 m0[kScatterRecFrames], m1[kScatterRecFrames];
+#pragma unroll
+    for (int k = 0; k < kScatterRecFrames; k++) {
+        m0[k] = *reinterpret_cast<const float2*>(r0 + (size_t)tt[k] * R.din[0]);
+        m1[k] = *reinterpret_cast<const float2*>(r1 + (size_t)tt[k] * R.din[1]);
+    }
+    const int count = R.din[0] == 0 ? 0 : R.din[1] == 0 ? 1 : 2;
+    // The sums in CSR order from +0.0; the quotient by max(count, 1) as div_rn, the IEEE quotient.
+    const double d = count > 1 ? 2.0 : 1.0, rd = count > 1 ? 0.5 : 1.0;
+    float2* oc = a.out + (((size_t)bt * a.S + s) * a.C + c) * a.T * a.F + f;
+#pragma unroll
+    for (int k = 0; k < kScatterRecFrames; k++) {
+        if (t0 + k >= a.T) break;
+        double ar = 0.0, ai = 0.0;
+        if (count > 0) {
+            ar += (double)m0[k].x;
+            ai += (double)m0[k].y;
+        }
+        if (count > 1) {
+            ar += (double)m1[k].x;
+            ai += (double)m1[k].y;
+        }
+        float2 o = make_float2(0.f, 0.f);
+        if (!(a.zero_dc && f == 0)) {
+            const double qr = div_rn(ar, d, rd), qi = div_rn(ai, d, rd);
+            const double zr = z[k].x, zi = z[k].y;
+            o = make_float2((float)(zr * qr - zi * qi), (float)(zr * qi + zi * qr));
+        }
+        store_stream(oc + (size_t)(t0 + k) * a.F, o);
     }
 }
 
@@ -481,6 +633,34 @@ STX_API stx_status stx_bands_create(const int32_t* band_sizes, int n_bands, cons
         }
         std::vector<double> denom(n_bins);
         for (int f = 0; f < n_bins; f++) denom[f] = (double)std::max(bpf[f], 1);   // src/roformer.cpp:272
+        // Per-bin records when every bin has at most two pairs and the offsets fit their fields.
+        bool records = fe.back() >= 2LL * channels && fe.back() < (1LL << 31);
+        for (int f = 0; f < n_bins && records; f++) records = bpf[f] <= 2;
+        for (int b = 0; b < n_bands && records; b++) records = band_sizes[b] * (long long)channels * 2 < 65536;
+        std::vector<GatherRec> grec;
+        bool gather_records = fe.back() / 2 / channels < (1LL << 31);
+        for (int b = 0; b < n_bands && gather_records; b++) gather_records = band_sizes[b] < 65536;
+        if (gather_records) {
+            grec.reserve((size_t)n_freqs);
+            for (int b = 0; b < n_bands; b++)
+                for (int j = 0; j < band_sizes[b]; j++)
+                    grec.push_back(GatherRec{(int)fo[b], (unsigned short)band_sizes[b],
+                                             (unsigned short)band_freqs[fo[b] + j]});
+        }
+        std::vector<BinBands> rec;
+        if (records) {
+            rec.assign(n_bins, BinBands{{0, 0}, {0, 0}, {0, 0}});
+            for (int f = 0; f < n_bins; f++) {
+                BinBands& r = rec[f];
+                for (int k = 0; k < 2; k++) {
+                    const int e = std::min(csr_off[f] + k, csr_off[f + 1] - 1);   // a missing pair repeats entry 0
+                    if (e < csr_off[f]) break;
+                    r.feat_off[k] = (int)csr[e].feat_off;
+                    r.col[k] = (unsigned short)csr[e].col;
+                    r.din[k] = csr_off[f] + k < csr_off[f + 1] ? (unsigned short)csr[e].din : 0;
+                }
+            }
+        }
 
         stx_bands* h = new stx_bands;
         h->n_bands = n_bands;
@@ -505,6 +685,8 @@ STX_API stx_status stx_bands_create(const int32_t* band_sizes, int n_bands, cons
         up(&h->d_csr_off, csr_off);
         up(&h->d_csr, csr);
         up(&h->d_denom, denom);
+        if (records) up(&h->d_bin_bands, rec);
+        if (gather_records && n_freqs > 0) up(&h->d_gather_rec, grec);
         up(&h->d_pair_off, pair_off);
         up(&h->d_pair_code, pair_code);
         up(&h->d_freq_lo, freq_lo);
@@ -527,6 +709,8 @@ STX_API void stx_bands_destroy(stx_bands* h) {
     (void)hipFree(h->d_csr_off);
     (void)hipFree(h->d_csr);
     (void)hipFree(h->d_denom);
+    (void)hipFree(h->d_bin_bands);
+    (void)hipFree(h->d_gather_rec);
     (void)hipFree(h->d_pair_off);
     (void)hipFree(h->d_pair_code);
     (void)hipFree(h->d_freq_lo);
@@ -559,6 +743,19 @@ STX_API stx_status stx_band_gather(const stx_bands* h, const float* spec, int ba
         a.freq_lo = h->d_freq_lo;
         a.n_bands = h->n_bands;
         const hipStream_t s = as_stream(stream);
+        const size_t row_bytes = sizeof(float2) * (size_t)a.C * a.F;
+        const bool aligned = a.C != 2 || reinterpret_cast<uintptr_t>(feat) % 16 == 0;
+        if (layout == STX_SPEC_T_MAJOR && h->d_gather_rec && row_bytes <= 65536 && aligned) {
+            a.rec = h->d_gather_rec;
+            a.n_entries = (int)h->n_freqs;
+            a.fdiv = FastDiv((unsigned)a.F);
+            const dim3 grid(xcd_grid(n_frames), batch);
+            if (a.C == 1) launch_gather_frame<1>(a, grid, row_bytes, s);
+            else if (a.C == 2) launch_gather_frame<2>(a, grid, row_bytes, s);
+            else launch_gather_frame<0>(a, grid, row_bytes, s);
+            launch_check("band_gather_frame_kernel");
+            return;
+        }
         if (layout == STX_SPEC_T_MAJOR) {
             const long long n = h->total_feat / 2 * (long long)n_frames;
             STX_REQUIRE(n < (1LL << 31) - 256 * kGatherPer, "band gather: too many features per chunk");
@@ -610,8 +807,18 @@ STX_API stx_status stx_band_scatter_apply(const stx_bands* h, const float* masks
         a.zero_dc = zero_dc ? 1 : 0;
         a.total_feat = h->total_feat;
         const hipStream_t s = as_stream(stream);
-        if (layout == STX_SPEC_T_MAJOR) {
-            dim3 grid((a.F * a.C + 255) / 256, (n_frames + kScatterFrames - 1) / kScatterFrames, batch * n_stems);
+        const long long tiles = (n_frames + kScatterFrames - 1) / kScatterFrames;
+        const long long rec_tiles = (n_frames + kScatterRecFrames - 1) / kScatterRecFrames;
+        if (layout == STX_SPEC_T_MAJOR && h->d_bin_bands && rec_tiles * a.F * a.C < (1LL << 32) - 256) {
+            const unsigned n = (unsigned)(rec_tiles * a.F * a.C);
+            a.rec = h->d_bin_bands;
+            a.fc_div = FastDiv((unsigned)(a.F * a.C));
+            a.c_div = FastDiv((unsigned)a.C);
+            const dim3 grid((n + 255) / 256, batch * n_stems);
+            hipLaunchKernelGGL(band_scatter_rec_kernel, grid, dim3(256), 0, s, a, n);
+            launch_check("band_scatter_rec_kernel");
+        } else if (layout == STX_SPEC_T_MAJOR) {
+            dim3 grid((a.F * a.C + 255) / 256, (unsigned)tiles, batch * n_stems);
             hipLaunchKernelGGL(band_scatter_t_kernel, grid, dim3(256), 0, s, a);
             launch_check("band_scatter_t_kernel");
         } else {

@@ -90,6 +90,20 @@ __device__ __forceinline__ int xcd_block() {
 
 inline bool is_pow2(long long n) { return n >= 1 && (n & (n - 1)) == 0; }
 
+// Vector stores with the non-temporal hint (the store's nt bit), for outputs the kernel does not
+// read back. Measured on outputs of tens of MB written once (the band gather's features): the
+// cold call is ~20 % faster, since the written lines no longer displace dirty lines of earlier
+// work from the caches; when the same buffers are rewritten while still cached it costs ~2 %.
+typedef float stx_v2f __attribute__((ext_vector_type(2)));
+typedef float stx_v4f __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void store_stream(float* p, float v) { __builtin_nontemporal_store(v, p); }
+__device__ __forceinline__ void store_stream(float2* p, float2 v) {
+    __builtin_nontemporal_store(stx_v2f{v.x, v.y}, reinterpret_cast<stx_v2f*>(p));
+}
+__device__ __forceinline__ void store_stream(float4* p, float4 v) {
+    __builtin_nontemporal_store(stx_v4f{v.x, v.y, v.z, v.w}, reinterpret_cast<stx_v4f*>(p));
+}
+
 // x / h correctly rounded, for h finite and nonzero, given r = RN(1/h): q0 = RN(x r), then
 // RN(q0 + r RN(x - q0 h)), which by Markstein's theorem (r within half an ulp of 1/h, q0 within
 // one ulp of x/h, the residual exact by the fma) is the IEEE quotient when nothing overflows or

@@ -657,13 +657,13 @@ __global__ __launch_bounds__(256) void ew_flat_kernel(const float* __restrict__ 
         if constexpr (has_b<OP>()) flat_load(b, i, vb);
         if constexpr (has_c<OP>()) flat_load(c, i, vc);
         if constexpr (has_d<OP>()) flat_load(d, i, vd);
-        *reinterpret_cast<float4*>(y + i) =
-            make_float4(ew_apply<OP>(p.x, vb[0], vc[0], vd[0]), ew_apply<OP>(p.y, vb[1], vc[1], vd[1]),
-                        ew_apply<OP>(p.z, vb[2], vc[2], vd[2]), ew_apply<OP>(p.w, vb[3], vc[3], vd[3]));
+        store_stream(reinterpret_cast<float4*>(y + i),
+                     make_float4(ew_apply<OP>(p.x, vb[0], vc[0], vd[0]), ew_apply<OP>(p.y, vb[1], vc[1], vd[1]),
+                                 ew_apply<OP>(p.z, vb[2], vc[2], vd[2]), ew_apply<OP>(p.w, vb[3], vc[3], vd[3])));
     }
     for (unsigned i = 4 * n4 + blockIdx.x * 256 + threadIdx.x; i < n; i += stride)
-        y[i] = ew_apply<OP>(xa[i], has_b<OP>() ? flat_at(b, i) : 0.f, has_c<OP>() ? flat_at(c, i) : 0.f,
-                            has_d<OP>() ? flat_at(d, i) : 0.f);
+        store_stream(y + i, ew_apply<OP>(xa[i], has_b<OP>() ? flat_at(b, i) : 0.f, has_c<OP>() ? flat_at(c, i) : 0.f,
+                                         has_d<OP>() ? flat_at(d, i) : 0.f));
 }
 
 // ----------------------------------------------------------------------- GROUP_NORM
@@ -953,11 +953,11 @@ __device__ __forceinline__ void gn_write(float* yg, unsigned lo, unsigned hi, do
             }
         }
         if constexpr (FULL) {
-            *reinterpret_cast<float4*>(yg + p) = make_float4(o[0], o[1], o[2], o[3]);
+            store_stream(reinterpret_cast<float4*>(yg + p), make_float4(o[0], o[1], o[2], o[3]));
         } else {
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                if (ok[4 * k + j]) yg[p + j] = o[j];
+                if (ok[4 * k + j]) store_stream(yg + p + j, o[j]);
         }
         // One float4 at a time: interleaving the GELUs of several would need more than the
         // 128 VGPRs that two blocks per CU leave.

@@ -119,6 +119,81 @@ def test_small_random_table_bit_exact(device, ob):
             assert np.array_equal(out[b], ob.scatter_apply(sizes, freqs, masks[b], zb).astype(np.complex64))
 
 
+def two_pair_table():
+    """Every bin in at most two (band, position) pairs: overlapping bands, unordered bins, a
+    repeated bin, and bins no band covers (the scatter's per-bin record path, not the CSR one)."""
+    sizes = [5, 5, 5, 3, 2, 3]
+    freqs = [0, 1, 2, 3, 4, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 20, 18, 19, 25, 25, 30, 31, 32]
+    return np.array(sizes, np.int32), np.array(freqs, np.int32)
+
+
+@pytest.mark.parametrize("T,zero_dc", [(1, False), (21, True), (8, False)])
+def test_two_pair_table_bit_exact(device, ob, T, zero_dc):
+    sizes, freqs = two_pair_table()
+    assert np.bincount(freqs, minlength=40).max() == 2
+    C, F, S, batch = 3, 40, 3, 2
+    z = rand_spec(16, batch, C, F, T)
+    bands = stx.Bands(sizes, freqs, F, C)
+    masks = synth.uniform(17, (batch, S, bands.total_feat * T))
+    for layout in (stx.F_MAJOR, stx.T_MAJOR):
+        zd = z if layout == stx.F_MAJOR else np.ascontiguousarray(z.transpose(0, 1, 3, 2))
+        feat = host(bands.gather(dev(zd, device), T, layout=layout))
+        out = host(bands.scatter_apply(dev(masks, device), dev(zd, device), T, layout=layout, zero_dc=zero_dc))
+        if layout == stx.T_MAJOR:
+            out = out.transpose(0, 1, 2, 4, 3)
+        for b in range(batch):
+            zb = z[b].astype(np.complex128)
+            assert np.array_equal(feat[b], ob.gather(sizes, freqs, zb))
+            ref = ob.scatter_apply(sizes, freqs, masks[b], zb, zero_dc).astype(np.complex64)
+            assert np.array_equal(out[b], ref)
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_mel_gather_scatter_few_frames(device, ob, mel, T):
+    """One or three frames: the T-major gather's workgroups are (pair chunk, frame), 2 chunks
+    of the 3,958 pairs per frame here; the scatter's last frame tile is partial."""
+    sizes, freqs = mel
+    C, F, S, batch = 2, 1025, 2, 3
+    z = rand_spec(18, batch, C, F, T)
+    bands = stx.Bands(sizes, freqs, F, C)
+    masks = synth.uniform(19, (batch, S, bands.total_feat * T))
+    zd = np.ascontiguousarray(z.transpose(0, 1, 3, 2))
+    feat = host(bands.gather(dev(zd, device), T, layout=stx.T_MAJOR))
+    out = host(bands.scatter_apply(dev(masks, device), dev(zd, device), T, layout=stx.T_MAJOR, zero_dc=True))
+    out = out.transpose(0, 1, 2, 4, 3)
+    for b in range(batch):
+        zb = z[b].astype(np.complex128)
+        assert np.array_equal(feat[b], ob.gather(sizes, freqs, zb))
+        assert np.array_equal(out[b], ob.scatter_apply(sizes, freqs, masks[b], zb, True).astype(np.complex64))
+
+
+@pytest.mark.parametrize("case", ["mono", "unaligned_out", "wide_frame"])
+def test_gather_kernel_paths(device, ob, case):
+    """The T-major gather stages a frame in LDS when its C * F complex values fit 64 KB and, at
+    C = 2, the output is 16-byte aligned; otherwise it walks the output flat. Both, bit-exact:
+    mono (one channel), an output 8 bytes past a 16-byte boundary, and n_fft 8192 stereo
+    (2 * 4097 bins, 65.5 KB per frame)."""
+    import torch
+    n_fft = 8192 if case == "wide_frame" else 2048
+    C = 1 if case == "mono" else 2
+    F, T, batch = n_fft // 2 + 1, 37, 2
+    sizes, freqs = stx.mel_band_map(SR, n_fft, NMELS)
+    z = rand_spec(20, batch, C, F, T)
+    bands = stx.Bands(sizes, freqs, F, C)
+    n = bands.total_feat * T
+    zd = dev(np.ascontiguousarray(z.transpose(0, 1, 3, 2)), device)
+    if case == "unaligned_out":
+        buf = torch.empty(batch * n + 2, dtype=torch.float32, device=device)
+        out = buf[2:].view(batch, n)
+        assert out.data_ptr() % 16 == 8
+        bands.gather(zd, T, layout=stx.T_MAJOR, out=out)
+    else:
+        out = bands.gather(zd, T, layout=stx.T_MAJOR)
+    feat = host(out)
+    for b in range(batch):
+        assert np.array_equal(feat[b], ob.gather(sizes, freqs, z[b].astype(np.complex128)))
+
+
 @pytest.mark.parametrize("S", [1, 4])
 def test_roformer_spectral_path_c3(device, mel, S):
     # One RoFormer chunk: stereo 352,800 samples, n_fft 2048, hop 441, 60 mel bands; per-band
