@@ -489,7 +489,7 @@ __global__ __launch_bounds__(256) void band_rms_norm_kernel(BandNormArgs a) {
     for (int k = 0; k < V; k++) {
         if (lane + (k << lg) < d) ss += (double)v[k].x * v[k].x + (double)v[k].y * v[k].y;
     }
-    for (int m = L >> 1; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);   // stays inside the row's lanes
+    ss = lane_sum_dyn(ss, L);                        // stays inside the row's lanes
     const float scale = (float)(1.0 / sqrt(ss / (2.0 * d) + (double)a.eps));
     if (t >= a.T) return;
     float2* y = reinterpret_cast<float2*>(a.out + base);

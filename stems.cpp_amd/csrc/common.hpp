@@ -90,6 +90,72 @@ __device__ __forceinline__ int xcd_block() {
 
 inline bool is_pow2(long long n) { return n >= 1 && (n & (n - 1)) == 0; }
 
+// Wave reductions on DPP lane permutations (VALU moves, no LDS round trip). The controls used
+// here read lanes of the same 16-lane row only, so every source lane exists:
+//   0xB1 quad_perm [1,0,3,2] (lane ^ 1), 0x4E quad_perm [2,3,0,1] (lane ^ 2),
+//   0x141 row_half_mirror (7 - i within 8 lanes), 0x140 row_mirror (15 - i within 16 lanes).
+// Each step adds a lane's value to its partner's; IEEE addition is commutative, so both
+// partners hold the same bits after every step and the result is the same in every lane.
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(unsigned)b, CTRL, 0xf, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(unsigned)(b >> 32), CTRL, 0xf, 0xf, false);
+    return __longlong_as_double((long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+    const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, lane);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(b >> 32), lane);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
+// Sum over aligned groups of LANES lanes (a power of two <= 64), the same bits in every lane of
+// a group. Up to 16 lanes: DPP steps inside the row. 32: the row sums, then one exchange
+// between the two rows of the group. 64: the four row sums read into scalars and added as
+// (r0 + r1) + (r2 + r3), uniform over the wave.
+template <int LANES>
+__device__ __forceinline__ double lane_sum(double v) {
+    static_assert(LANES >= 1 && LANES <= 64 && (LANES & (LANES - 1)) == 0, "lane_sum: LANES");
+    if constexpr (LANES >= 2) v += dpp_f64<0xB1>(v);
+    if constexpr (LANES >= 4) v += dpp_f64<0x4E>(v);
+    if constexpr (LANES >= 8) v += dpp_f64<0x141>(v);
+    if constexpr (LANES >= 16) v += dpp_f64<0x140>(v);
+    if constexpr (LANES == 32) v += __shfl_xor(v, 16, 32);
+    if constexpr (LANES == 64)
+        v = (readlane_f64(v, 0) + readlane_f64(v, 16)) + (readlane_f64(v, 32) + readlane_f64(v, 48));
+    return v;
+}
+
+// lane_sum with a run-time group size L (a power of two <= 64, uniform over the wave).
+__device__ __forceinline__ double lane_sum_dyn(double v, int L) {
+    if (L >= 2) v += dpp_f64<0xB1>(v);
+    if (L >= 4) v += dpp_f64<0x4E>(v);
+    if (L >= 8) v += dpp_f64<0x141>(v);
+    if (L >= 16) v += dpp_f64<0x140>(v);
+    if (L >= 32) v += __shfl_xor(v, 16, 64);
+    if (L >= 64) v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+// Maximum over aligned groups of LANES lanes, in every lane of a group (max is exact, so any
+// order gives the same value).
+template <int LANES>
+__device__ __forceinline__ float lane_max(float v) {
+    static_assert(LANES >= 1 && LANES <= 64 && (LANES & (LANES - 1)) == 0, "lane_max: LANES");
+    if constexpr (LANES >= 2) v = fmaxf(v, dpp_f32<0xB1>(v));
+    if constexpr (LANES >= 4) v = fmaxf(v, dpp_f32<0x4E>(v));
+    if constexpr (LANES >= 8) v = fmaxf(v, dpp_f32<0x141>(v));
+    if constexpr (LANES >= 16) v = fmaxf(v, dpp_f32<0x140>(v));
+    if constexpr (LANES >= 32) v = fmaxf(v, __shfl_xor(v, 16, LANES));
+    if constexpr (LANES == 64) v = fmaxf(v, __shfl_xor(v, 32, 64));
+    return v;
+}
+
 // Vector stores with the non-temporal hint (the store's nt bit), for outputs the kernel does not
 // read back. Measured on outputs of tens of MB written once (the band gather's features): the
 // cold call is ~20 % faster, since the written lines no longer displace dirty lines of earlier

@@ -43,7 +43,7 @@ constexpr int kGridMaxBlocks = 512;                  // per group (one collector
 constexpr int kGridMaxGroups = 8;
 constexpr int kGridStatCopies = 8;                   // waiters poll copy (block % 8)
 constexpr int kGridStatStride = 128;                 // unsigned long longs between copies (1 KB)
-constexpr unsigned kGridSpinLimit = 1u << 16;        // polls of about 1 us each
+constexpr unsigned kGridSpinLimit = 1u << 16;        // polls of 0.1 to 1 us each
 
 // Workspace area: [8 KB) totals records, 8 per group at 1 KB apart | [256 B) the fallback
 // counter | partial sums records, 3 words per block.
@@ -61,31 +61,33 @@ struct GridSync {
     unsigned spin_limit;
 };
 
-// Sums of two doubles over an NT-thread block: wave sums, then the wave totals added in wave
-// order by every thread (the same order in every block). red holds 2 * NT / 64 doubles.
-// Returns the OR of `flag` over the block (folded into the first barrier).
+// Sums of two doubles over an NT-thread block: wave sums (lane_sum<64>), then the wave totals
+// added in wave order by every thread (the same order in every block). red holds 2 * NT / 64
+// doubles. Returns the OR of `flag` over the block (a ballot per wave, passed beside the sums).
 template <int NT>
 __device__ __forceinline__ bool block_sum2_or(double& a, double& b, double* red, bool flag) {
     constexpr int W = NT / 64;
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        a += __shfl_xor(a, m, 64);
-        b += __shfl_xor(b, m, 64);
-    }
-    const bool any = __syncthreads_or(flag);
+    __shared__ int wflag[W];
+    a = lane_sum<64>(a);
+    b = lane_sum<64>(b);
+    const bool wany = __ballot(flag) != 0;
+    __syncthreads();                                   // readers of a previous call's red are done
     if (threadIdx.x % 64 == 0) {
         red[threadIdx.x / 64] = a;
         red[W + threadIdx.x / 64] = b;
+        wflag[threadIdx.x / 64] = wany ? 1 : 0;
     }
     __syncthreads();
     a = 0.0;
     b = 0.0;
+    int any = 0;
 #pragma unroll
     for (int w = 0; w < W; w++) {
         a += red[w];
         b += red[W + w];
+        any |= wflag[w];
     }
-    return any;
+    return any != 0;
 }
 
 template <int NT>
@@ -125,8 +127,10 @@ __device__ __forceinline__ void record_store(unsigned long long* r, double s1, d
     sync_store(r + 1, b);
     sync_store(r + 2, record_tag(a, b, key));
 }
-// Polls r (at most limit times after the first look) until it holds a record under key;
-// false if it never did.
+// Polls r (at most limit times after the first look) until it holds a record under key; false
+// if it never did. One poll in flight with a short pause between polls: with every block of a
+// launch polling, a second poll in flight or no pause measured slower (the device-scope loads
+// of all blocks share the coherence point).
 __device__ __forceinline__ bool record_wait(const unsigned long long* r, unsigned long long key, unsigned limit,
                                             double& s1, double& s2) {
     for (unsigned spins = 0;;) {
@@ -137,7 +141,7 @@ __device__ __forceinline__ bool record_wait(const unsigned long long* r, unsigne
             return true;
         }
         if (++spins > limit) return false;
-        __builtin_amdgcn_s_sleep(1);
+        __builtin_amdgcn_s_sleep(2);
     }
 }
 
@@ -156,15 +160,18 @@ __device__ __forceinline__ bool grid_totals(const GridSync& f, int gt, int nblk,
     unsigned long long* part = f.part + 3 * (size_t)gt * kGridMaxBlocks;
     bool late = false;
     if (blockIdx.x != 0) {
+        __shared__ int wait_late;
         if (threadIdx.x == 0) {
             record_store(part + 3 * blockIdx.x, s1, s2, key);
             double t1 = 0.0, t2 = 0.0;                         // the group's totals, from block 0
-            late = !record_wait(f.stat + (blockIdx.x % kGridStatCopies) * kGridStatStride + 3 * gt, key,
-                                f.spin_limit, t1, t2);
+            const bool l = !record_wait(f.stat + (blockIdx.x % kGridStatCopies) * kGridStatStride + 3 * gt, key,
+                                        f.spin_limit, t1, t2);
             tot[0] = t1;
             tot[1] = t2;
+            wait_late = l ? 1 : 0;
         }
-        late = __syncthreads_or(late);
+        __syncthreads();
+        late = wait_late != 0;
     } else {
         double p1 = 0.0, p2 = 0.0;
         if (threadIdx.x == 0) {

@@ -73,8 +73,7 @@ __device__ __forceinline__ void mono_batch(const float* x, long long n, int C, c
 }
 
 __device__ __forceinline__ double block_sum(double v, double* red) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    v = lane_sum<64>(v);
     const int w = (int)threadIdx.x / 64, lane = (int)threadIdx.x % 64;
     __syncthreads();                             // red may still be read by a previous call
     if (lane == 0) red[w] = v;

@@ -64,23 +64,9 @@ long long row_spacing(const T4& t) {
     return rs > 0 ? rs : 4 * t.ne[0];          // a single row: any positive spacing works
 }
 
-template <int LANES>
-__device__ __forceinline__ double group_sum(double v) {
-#pragma unroll
-    for (int m = LANES / 2; m >= 1; m /= 2) v += __shfl_xor(v, m, LANES);
-    return v;
-}
-
-template <int LANES>
-__device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-    for (int m = LANES / 2; m >= 1; m /= 2) v = fmaxf(v, __shfl_xor(v, m, LANES));
-    return v;
-}
-
 // Sum over a 256-thread block in a fixed order (deterministic). red holds 4 doubles.
 __device__ __forceinline__ double block_sum(double v, double* red) {
-    v = group_sum<kWave>(v);
+    v = lane_sum<kWave>(v);
     __syncthreads();
     if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = v;
     __syncthreads();
@@ -222,14 +208,14 @@ __global__ __launch_bounds__(256) void row_norm_kernel(RowNormArgs a) {
             double s = 0.0;
 #pragma unroll
             for (int k = 0; k < VPL; k++) s += (double)v[k];
-            mean = group_sum<LANES>(s) / n;
+            mean = lane_sum<LANES>(s) / n;
         }
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
             const double d = (double)v[k] - mean;
             ss += lane + k * LANES < n ? d * d : 0.0;
         }
-        ss = group_sum<LANES>(ss);
+        ss = lane_sum<LANES>(ss);
         const double scale = 1.0 / sqrt(ss / n + (double)a.eps);
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
@@ -303,7 +289,7 @@ __global__ __launch_bounds__(256) void softmax_kernel(SoftmaxArgs a) {
             v[k] = i < n ? x[i] : 0.f;
             if (i < n) m = fmaxf(m, sgn * v[k]);
         }
-        const double ms = (double)(sgn * group_max<LANES>(m)) * sc;
+        const double ms = (double)(sgn * lane_max<LANES>(m)) * sc;
         double sum = 0.0;
         float e[VPL];
 #pragma unroll
@@ -311,7 +297,7 @@ __global__ __launch_bounds__(256) void softmax_kernel(SoftmaxArgs a) {
             e[k] = lane + k * LANES < n ? exp_split((double)v[k] * sc - ms) : 0.f;
             sum += (double)e[k];
         }
-        const double inv = 1.0 / group_sum<LANES>(sum);
+        const double inv = 1.0 / lane_sum<LANES>(sum);
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
             const int i = lane + k * LANES;
@@ -408,7 +394,7 @@ __global__ __launch_bounds__(256) void row_norm_v4_kernel(RowNormArgs a) {
             double s = ei >= 0 ? (double)e : 0.0;
 #pragma unroll
             for (int k = 0; k < 4 * V4; k++) s += (double)v[k];       // invalid slots hold 0
-            mean = group_sum<LANES>(s) / n;
+            mean = lane_sum<LANES>(s) / n;
         }
         double ss = 0.0;
         if (ei >= 0) ss = ((double)e - mean) * ((double)e - mean);
@@ -422,7 +408,7 @@ __global__ __launch_bounds__(256) void row_norm_v4_kernel(RowNormArgs a) {
                 }
             }
         }
-        ss = group_sum<LANES>(ss);
+        ss = lane_sum<LANES>(ss);
         const double scale = 1.0 / sqrt(ss / n + (double)a.eps);
         const float scale_f = (float)scale;
         float4* yb = reinterpret_cast<float4*>(y + sp.h);
@@ -484,7 +470,7 @@ __global__ __launch_bounds__(256) void softmax_v4_kernel(SoftmaxArgs a) {
             if (lane + LANES * k < sp.nb4)
 #pragma unroll
                 for (int j = 0; j < 4; j++) m = fmaxf(m, sgn * v[4 * k + j]);
-        const double ms = (double)(sgn * group_max<LANES>(m)) * sc;
+        const double ms = (double)(sgn * lane_max<LANES>(m)) * sc;
         double sum = 0.0;
 #pragma unroll
         for (int k = 0; k < V4; k++) {
@@ -499,7 +485,7 @@ __global__ __launch_bounds__(256) void softmax_v4_kernel(SoftmaxArgs a) {
             e = exp_split((double)e * sc - ms);
             sum += (double)e;
         }
-        const double inv = 1.0 / group_sum<LANES>(sum);
+        const double inv = 1.0 / lane_sum<LANES>(sum);
         float4* yb = reinterpret_cast<float4*>(y + sp.h);
 #pragma unroll
         for (int k = 0; k < V4; k++) {
@@ -856,6 +842,9 @@ __device__ __forceinline__ float affine_at(const Affine& f, long long c, unsigne
 //     w0/b0 of the channel of pw, w1/b1 of the next one (clamped), and bnd, the first element
 //     of the next channel (all wave-uniform).
 //   other kinds: one (w, b) per element.
+// The identities of a missing weight (1) and bias (0).
+__device__ const float kAffineUnit[2] = {1.f, 0.f};
+
 template <int AK, int VEC>
 struct GnParams {
     static constexpr bool kWave = AK == AFF_CHANNEL_WAVE;
@@ -877,10 +866,18 @@ __device__ __forceinline__ void gn_params(const GroupNormArgs& a, unsigned lo, l
             const unsigned ca = a.plane_div.div(pw);
             pr.bnd[k] = (ca + 1) * a.plane;
             const long long cA = min(c0 + (long long)ca, cl), cB = min(c0 + (long long)ca + 1, cl);
-            pr.w0[k] = a.w.p ? a.w.p[cA] : 1.f;
-            pr.w1[k] = a.w.p ? a.w.p[cB] : 1.f;
-            pr.b0[k] = a.b.p ? a.b.p[cA] : 0.f;
-            pr.b1[k] = a.b.p ? a.b.p[cB] : 0.f;
+            // Unconditional loads (a missing operand reads its identity from kAffineUnit), so that
+            // they issue with the chunk's loads instead of after a wait in a branch.
+            // Global-space pointers: a generic (flat) load would also count on the LDS counter
+            // and hold up the reductions' LDS waits.
+            using gfloat = __attribute__((address_space(1))) const float;
+            gfloat* wp = (gfloat*)(a.w.p ? a.w.p : kAffineUnit);
+            gfloat* bp = (gfloat*)(a.b.p ? a.b.p : kAffineUnit + 1);
+            const long long mw = a.w.p ? -1 : 0, mb = a.b.p ? -1 : 0;
+            pr.w0[k] = wp[cA & mw];
+            pr.w1[k] = wp[cB & mw];
+            pr.b0[k] = bp[cA & mb];
+            pr.b1[k] = bp[cB & mb];
         }
     } else {
 #pragma unroll
