@@ -22,6 +22,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 namespace stx {
 
 #define STX_HD __host__ __device__ __forceinline__
@@ -240,17 +242,33 @@ __device__ __forceinline__ void twiddle_powers(const float2* __restrict__ twt, i
     }
 }
 
+struct NoPost {
+    __device__ __forceinline__ float2 operator()(int, float2 v) const { return v; }
+};
+
+// Sink writing into the transform's own LDS buffer (natural order).
+template <int P>
+struct ToLds {
+    float2* buf;
+    __device__ __forceinline__ void operator()(int n, float2 v) const { buf[n + n / P] = v; }
+};
+
+// LDS addressing: element i of a transform lives at idx(i) = i + i / P. For a base b and a
+// multiple s of P, idx(b + r s) = idx(b) + r (s + s / P), so every LDS access of a butterfly is
+// one base index plus a compile-time offset (an immediate of the ds instruction) instead of an
+// index computation per element.
+
 // First pass (Ns = 1, radix P): v holds a[j + r*M/P] for r < P on entry. Writes to the LDS
-// buffer, or, when it is also the last pass (M == P), to `sink` through `post`.
+// buffer (elements j*P + r, at idx = j*(P + 1) + r), or, when it is also the last pass
+// (M == P), to `sink` through `post`.
 template <int M, int P, int TN, class Post, class Sink>
 __device__ __forceinline__ void fft_first_pass(float2* v, float2* buf, int j, const Post& post, const Sink& sink) {
-    using C = FftCfg<M, P, TN>;
     Dft<P>::run(v);
+    float2* w = buf + j * (P + 1);
 #pragma unroll
     for (int r = 0; r < P; r++) {
-        const int n = j * P + r;
-        if constexpr (M == P) sink(n, post(n, v[r]));
-        else buf[C::idx(n)] = v[r];
+        if constexpr (M == P) sink(j * P + r, post(j * P + r, v[r]));
+        else w[r] = v[r];
     }
 }
 
@@ -267,12 +285,16 @@ __device__ __forceinline__ void fft_rest_passes(float2* buf, int j, const float2
         constexpr int BPT = P / R;                    // butterflies per thread
         constexpr int SCALE = C::TN / (Ns * R);       // W_{Ns*R}^e = W_TN^(e*SCALE)
         constexpr bool LAST = (Ns * R == M);
+        static_assert((M / R) % P == 0 && Ns % P == 0, "strides of the rest passes are multiples of P");
+        constexpr int RS = M / R + M / R / P;         // LDS distance between a butterfly's inputs
+        constexpr int WS = Ns + Ns / P;               // ... and between its outputs
+        constexpr bool TO_LDS = std::is_same<Sink, ToLds<P>>::value;
         float2 v[P];
 #pragma unroll
         for (int q = 0; q < BPT; q++) {
-            const int jj = j + q * TPJ;
+            const float2* rd = buf + C::idx(j + q * TPJ);
 #pragma unroll
-            for (int r = 0; r < R; r++) v[q * R + r] = buf[C::idx(jj + r * (M / R))];
+            for (int r = 0; r < R; r++) v[q * R + r] = rd[r * RS];
         }
         __syncthreads();
 #pragma unroll
@@ -285,28 +307,19 @@ __device__ __forceinline__ void fft_rest_passes(float2* buf, int j, const float2
             for (int r = 1; r < R; r++) v[q * R + r] = cmul(v[q * R + r], w[r]);
             Dft<R>::run(&v[q * R]);
             const int base = (jj / Ns) * Ns * R + k;
+            float2* wr = buf + C::idx(base);
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 const int n = base + r * Ns;
-                if constexpr (LAST) sink(n, post(n, v[q * R + r]));
-                else buf[C::idx(n)] = v[q * R + r];
+                if constexpr (LAST && TO_LDS) wr[r * WS] = post(n, v[q * R + r]);
+                else if constexpr (LAST) sink(n, post(n, v[q * R + r]));
+                else wr[r * WS] = v[q * R + r];
             }
         }
         __syncthreads();
         fft_rest_passes<M, P, TN, Ns * R>(buf, j, twt, post, sink);
     }
 }
-
-struct NoPost {
-    __device__ __forceinline__ float2 operator()(int, float2 v) const { return v; }
-};
-
-// Sink writing into the transform's own LDS buffer (natural order).
-template <int P>
-struct ToLds {
-    float2* buf;
-    __device__ __forceinline__ void operator()(int n, float2 v) const { buf[n + n / P] = v; }
-};
 
 }  // namespace stx
 

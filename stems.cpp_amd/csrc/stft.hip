@@ -21,6 +21,7 @@
 //         once and writes it windowed to the workspace, the next sums and divides. This
 //         keeps every CU busy when there are few frames.
 #include <algorithm>
+#include <type_traits>
 #include <memory>
 #include <cmath>
 #include <vector>
@@ -151,14 +152,19 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void stft_kernel(StftArgs a) {
     __syncthreads();
     fft_rest_passes<M, P, N, P>(buf, j, twt, NoPost{}, ToLds<P>{buf});
 
-    // X[k] = E[k] + W_N^k O[k] for frame g of the block, k <= N/2.
+    // X[k] = E[k] + W_N^k O[k] for frame g of the block, k <= N/2. Bins k = k0 + i*KS (KS a
+    // multiple of P) are read at idx(k) = idx(k0) + i*(KS + KS/P), their mirrors M - k at
+    // idx(M - k0) - i*(KS + KS/P); k = 0 and k = M pair with element 0 (k & (M - 1)).
     const float hs = 0.5f * a.scale;
     const int f0 = lb * JOBS;
     const int c0 = f0 / a.T, t0 = f0 - c0 * a.T;
-    auto bin = [&](int k, int g, float2 w) {
-        const float2* bs = lds + g * C::PADN;
-        const float2 zk = bs[C::idx(k & (M - 1))];
-        const float2 zm = bs[C::idx((M - k) & (M - 1))];
+    constexpr int MP = M + M / P;
+    // ik, im: idx(k) and idx(M - k) kept incrementally when the bin stride KS is a multiple of
+    // P (every size from 32 up), computed directly otherwise.
+    auto bin = [&](const float2* bs, int k, int ik, int im, float2 w, auto ks) {
+        const bool inc = decltype(ks)::value % P == 0;
+        const float2 zk = bs[inc ? (k < M ? ik : ik - MP) : C::idx(k & (M - 1))];
+        const float2 zm = bs[(k & (M - 1)) == 0 ? 0 : inc ? im : C::idx(M - k)];
         const float er = zk.x + zm.x, ei = zk.y - zm.y;       // 2E
         const float orr = zk.y + zm.y, oi = zm.x - zk.x;      // 2O
         return make_float2((er + w.x * orr - w.y * oi) * hs, (ei + w.x * oi + w.y * orr) * hs);
@@ -167,16 +173,23 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void stft_kernel(StftArgs a) {
         // Element e = k*JOBS + g: with NT a multiple of JOBS every thread keeps one frame
         // g = tid % JOBS and takes bins tid / JOBS + i * NT / JOBS, so that the JOBS lanes of a
         // bin write consecutive frames of its row.
-        const int g = tid % JOBS;
+        constexpr int KS = NT / JOBS, KSP = KS + KS / P;
+        const int g = tid % JOBS, k0 = tid / JOBS;
         int tt = t0 + g, cc = c0;
         while (tt >= a.T) { tt -= a.T; cc++; }
         if (f0 + g < a.jobs) {
+            const float2* bs = lds + g * C::PADN;
             float2* col = a.spec + (size_t)cc * a.F * a.T + tt;
+            const unsigned rs = (unsigned)a.T * KS;           // row step of one bin stride
+            unsigned off = (unsigned)k0 * a.T;
+            int ik = C::idx(k0), im = C::idx(M - k0);
 #pragma unroll 4
-            for (int k = tid / JOBS; k < a.F; k += NT / JOBS) col[(size_t)k * a.T] = bin(k, g, tw_lookup<N>(twt, k));
+            for (int k = k0; k < a.F; k += KS, off += rs, ik += KSP, im -= KSP)
+                col[off] = bin(bs, k, ik, im, tw_lookup<N>(twt, k), std::integral_constant<int, KS>{});
         }
     } else {
         // Row of frame g, then each bin's twiddle once for all JOBS frames.
+        constexpr int KSP = NT + NT / P;
         float2* rows[JOBS];
 #pragma unroll
         for (int g = 0; g < JOBS; g++) {
@@ -184,12 +197,13 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void stft_kernel(StftArgs a) {
             while (tt >= a.T) { tt -= a.T; cc++; }
             rows[g] = f0 + g < a.jobs ? a.spec + ((size_t)cc * a.T + tt) * a.F : nullptr;
         }
+        int ik = C::idx(tid), im = C::idx(M - tid);
 #pragma unroll 4
-        for (int k = tid; k < a.F; k += NT) {
+        for (int k = tid; k < a.F; k += NT, ik += KSP, im -= KSP) {
             const float2 w = tw_lookup<N>(twt, k);
 #pragma unroll
             for (int g = 0; g < JOBS; g++)
-                if (rows[g]) rows[g][k] = bin(k, g, w);
+                if (rows[g]) rows[g][k] = bin(lds + g * C::PADN, k, ik, im, w, std::integral_constant<int, NT>{});
         }
     }
 }
@@ -368,9 +382,13 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
     float2* buf = lds + slot * C::PADN;
     const int hop = a.hop;
 
-    stage_twiddles<N, NT>(twt, a.twt, tid);
-    if constexpr (WIN_LDS)
-        stage_lds<N, NT>(wl, a.win, tid);
+    // The twiddle and window tables are loaded into registers here and written to LDS after the
+    // first round's spectrum loads are issued, so that their round trips overlap.
+    StagedTwiddles<N, NT> tws;
+    Staged<WIN_LDS ? N : 1, NT, float> wins;
+    tws.load(a.twt, tid);
+    if constexpr (WIN_LDS) wins.load(a.win, tid);
+    bool staged = false;
     const float* win = WIN_LDS ? wl : a.win;
 
     const int J0 = max(a.out_off, a.tile_origin + tile * a.tile_len);
@@ -424,6 +442,11 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
 #pragma unroll
             for (int i = 0; i < P; i++) sv[i] = col[(size_t)(k0 + i * TPJ) * a.T];
             const float2 nyq = sc[(size_t)min(M, a.F - 1) * a.T + min(s0 + min(tr, JOBS - 1), st_hi)];
+            if (!staged) {
+                tws.store(twt, tid);
+                if constexpr (WIN_LDS) wins.store(wl, tid);
+                staged = true;
+            }
             const bool live = s0 + g <= st_hi;
 #pragma unroll
             for (int i = 0; i < P; i++) lds[g * C::PADN + k0 + i * TPJ] = live ? sv[i] : make_float2(0.f, 0.f);
@@ -444,6 +467,11 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
 #pragma unroll
             for (int i = 0; i < P; i++) sv[i] = sc[(size_t)min(s0 + slot_of(i), st_hi) * a.F + bin_of(i)];
             const float2 nyq = sc[(size_t)min(s0 + min(tr, JOBS - 1), st_hi) * a.F + min(M, a.F - 1)];
+            if (!staged) {
+                tws.store(twt, tid);
+                if constexpr (WIN_LDS) wins.store(wl, tid);
+                staged = true;
+            }
 #pragma unroll
             for (int i = 0; i < P; i++)
                 lds[slot_of(i) * C::PADN + bin_of(i)] = s0 + slot_of(i) <= st_hi ? sv[i] : make_float2(0.f, 0.f);
@@ -477,6 +505,11 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
                 sum += sl[pos + 2 * (pos / (2 * P))];
             acc[q] = sum;
         });
+        __syncthreads();
+    }
+    if (!staged) {                                  // no frame overlaps the tile (uniform)
+        tws.store(twt, tid);
+        if constexpr (WIN_LDS) wins.store(wl, tid);
         __syncthreads();
     }
 
