@@ -232,6 +232,40 @@ def test_small_hop_needs_several_rounds(device, orc):
         assert snr_db(y[c], orc.torch_istft(ref, n, hop)) >= SNR_DB
 
 
+@pytest.mark.parametrize("case", ["c1_htdemucs", "c3_torch"])
+@pytest.mark.parametrize("layout", [stx.F_MAJOR, stx.T_MAJOR])
+def test_istft_ws_spill_forced_fallback(device, orc, case, layout, monkeypatch):
+    """The workspace iSTFT transforms each frame once and hands each block's spill (its frames'
+    sums past its own range) to the next block as tagged records. STX_GRID_SYNC_SPIN_LIMIT=0
+    makes every block give up its wait at the first look and transform its predecessor's frames
+    itself: the same bits. Against the fused path (frames shared by two tiles transformed
+    twice) the sums differ only in rounding."""
+    if case == "c1_htdemucs":
+        n, hop, length = 4096, 1024, 343980
+        x = _stereo(41, length, 0.1)
+        f = plan(n)
+        spec = stx.htdemucs_spec(f, to_dev(x, device), layout=layout)
+        frames = spec.shape[2] if layout == stx.F_MAJOR else spec.shape[1]
+        run = lambda ws: stx.htdemucs_ispec(f, spec, length, layout=layout, workspace=ws)
+    else:
+        n, hop, length = 2048, 441, 352800
+        x = _stereo(42, length, 0.1)
+        f = plan(n)
+        spec = stx.torch_stft(f, to_dev(x, device), hop, layout=layout)
+        frames = length // hop + 1
+        run = lambda ws: stx.torch_istft(f, spec, hop, layout=layout, workspace=ws)
+    ws = ws_for(f, 2, frames, device, True)
+    y_ws = host(run(ws))
+    monkeypatch.setenv("STX_GRID_SYNC_SPIN_LIMIT", "0")
+    y_forced = host(run(ws))
+    monkeypatch.delenv("STX_GRID_SYNC_SPIN_LIMIT")
+    y_fused = host(run(None))
+    assert np.array_equal(y_ws, y_forced)
+    assert np.max(np.abs(y_ws - y_fused)) <= 1e-6 * np.max(np.abs(y_fused))
+    if case == "c3_torch":                                  # torch_stft -> torch_istft is the identity
+        assert snr_db(y_ws, x) >= SNR_DB
+
+
 def test_workspace_too_small(device):
     f = plan(2048)
     x = to_dev(_stereo(56, 20000), device)
