@@ -136,11 +136,12 @@ STX_API stx_status stx_htdemucs_ispec(const stx_fft* fft, const float* spec, int
 STX_API size_t stx_istft_workspace_size(const stx_fft* fft, int channels, int n_frames);
 
 /* stx_torch_istft / stx_htdemucs_ispec with a caller-owned device workspace of at least
- * stx_istft_workspace_size() bytes (INVALID_ARGUMENT if smaller). They inverse-transform each
- * frame once into the workspace and overlap-add in a second kernel, which keeps every CU busy
- * when there are few frames (one segment); the plain entry points need no workspace and
- * transform frames shared by two output tiles twice. Results are the same to rounding.
- * A NULL workspace selects the plain path. */
+ * stx_istft_workspace_size() bytes (INVALID_ARGUMENT if smaller). Sizes that are not powers of
+ * two (stx_fft_create_any) need it: they inverse-transform each frame once into the workspace
+ * and overlap-add in a second kernel. Power-of-two sizes run the same single kernel as the plain
+ * entry points (the workspace is checked, not used): at every size measured that kernel, which
+ * transforms frames shared by two output tiles twice, was faster than writing and re-reading
+ * every windowed frame. A NULL workspace selects the plain path. */
 STX_API stx_status stx_torch_istft_ws(const stx_fft* fft, const float* spec, int channels,
                                       int n_frames, int hop, int normalized, float* out,
                                       stx_spec_layout layout, void* workspace,

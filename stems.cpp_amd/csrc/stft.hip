@@ -28,7 +28,6 @@
 
 #include "common.hpp"
 #include "fft_core.hpp"
-#include "grid_sync.hpp"
 
 struct stx_fft {
     int n = 0;
@@ -269,66 +268,7 @@ struct WindowPost {
     }
 };
 
-// Two-kernel path, step 1: one inverse transform per frame, written windowed to the workspace.
-template <int N, int P, int JOBS>
-__global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_frames_kernel(IstftArgs a) {
-    constexpr int M = N / 2;
-    using C = FftCfg<M, P, N>;
-    constexpr int TPJ = C::TPJ;
-    constexpr int NT = JOBS * TPJ;
-    __shared__ float2 lds[JOBS * C::PADN];
-    __shared__ float2 twt[TwTable<N>::SIZE];
-    __shared__ float wl[N];
-
-    const int lb = xcd_block();
-    if (lb >= a.nblocks) return;
-    const int tid = (int)threadIdx.x;
-    const int slot = tid / TPJ;
-    const int j = tid % TPJ;
-    const int f = lb * JOBS + slot;
-    const bool active = f < a.jobs;
-    float2* buf = lds + slot * C::PADN;
-    StagedTwiddles<N, NT> tws;
-    Staged<N, NT, float> wins;
-    tws.load(a.twt, tid);                              // overlap the spectrum loads
-    wins.load(a.win, tid);
-    const int c = active ? f / a.T : 0;
-    const int st = active ? f - c * a.T : 0;
-    const float2* sc = a.spec + (size_t)c * a.T * a.F;
-
-    // Unconditional loads (an inactive job reads frame 0, a missing Nyquist bin bin F - 1),
-    // zeroed afterwards, so that no branch separates them.
-    float2 xk[P], xm[P];
-#pragma unroll
-    for (int r = 0; r < P; r++) {
-        const int k = j + r * TPJ;
-        xk[r] = spec_bin(a, sc, st, k);
-        xm[r] = spec_bin(a, sc, st, min(M - k, a.F - 1));
-    }
-#pragma unroll
-    for (int r = 0; r < P; r++) {
-        const int km = M - (j + r * TPJ);
-        if (!active) xk[r] = make_float2(0.f, 0.f);
-        if (!active || (km == M && !a.keep_nyquist)) xm[r] = make_float2(0.f, 0.f);
-    }
-    tws.store(twt, tid);
-    wins.store(wl, tid);
-    __syncthreads();
-    float2 v[P];
-#pragma unroll
-    for (int r = 0; r < P; r++) v[r] = inverse_split<N>(xk[r], xm[r], j + r * TPJ, a.keep_nyquist, twt);
-
-    const WindowPost post{reinterpret_cast<const float2*>(wl), a.norm};
-    float2* dst = reinterpret_cast<float2*>(a.frames + (size_t)f * N);
-    auto sink = [&](int n, float2 val) {
-        if (active) dst[n] = val;
-    };
-    fft_first_pass<M, P, N>(v, buf, j, post, sink);
-    __syncthreads();
-    fft_rest_passes<M, P, N, P>(buf, j, twt, post, sink);
-}
-
-// Two-kernel path, step 2: out = sum of the windowed frames over the frames covering each
+// Two-kernel path (mixed-radix sizes), step 2: out = sum of the windowed frames over the frames covering each
 // sample, in frame order, divided by the window-squared envelope.
 __global__ __launch_bounds__(256) void istft_ola_kernel(IstftArgs a, int N) {
     const int i = (int)(blockIdx.x * 256 + threadIdx.x);
@@ -552,244 +492,6 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
         }
         oc[J - a.out_off] = y;
     });
-}
-
-// ------------------------------------------------- iSTFT: every frame once, spill records
-// Workspace path for power-of-two sizes (stx_*_istft_ws). Block (channel c, b) owns spectrum
-// frames [bK, bK + K) and inverse-transforms each of them once. With K >= ceil(N / hop) - 1 its
-// frames reach past its own output range [Jo0, Jo1) = [(bK + off) hop, ((b + 1)K + off) hop)
-// by SP = N - hop samples (its spill), into the next block's range only. The block sums its own
-// frames, in frame order, over its range and its spill; it hands the spill sums to block b + 1
-// as records (two samples, tag) in the workspace, the tag being record_tag (grid_sync.hpp) of
-// the data over the launch key and the record's index, so that stale or torn records fail the
-// check and the workspace needs no initialisation; and it takes block b - 1's spill for the
-// first SP samples of its range: y = (sum over b - 1's frames) + (sum over its own frames), then
-// the envelope division. A block waits only for its predecessor, which the hardware dispatched
-// before it, so the wait ends; should it still give up (the spin limit), the block transforms
-// the predecessor's frames itself and forms the same sums bit for bit.
-struct SpillArgs {
-    unsigned long long* rec;   // [blocks][rpb][2]: (two samples as 64 bits, tag)
-    int nbc;                   // blocks per channel
-    int K;                     // frames per block
-    int rpb;                   // records per block: ceil((N - hop) / 2)
-    int per;                   // two-sample units per thread
-    FastDiv hop_div;           // J / hop
-    unsigned spin_limit;
-};
-
-__device__ __forceinline__ bool spill_wait(const unsigned long long* r, unsigned long long idx, unsigned long long key,
-                                           unsigned limit, unsigned long long& data) {
-    for (unsigned spins = 0;;) {
-        const unsigned long long d = sync_load(r), h = sync_load(r + 1);
-        if (h == record_tag(d, idx, key)) {
-            data = d;
-            return true;
-        }
-        if (++spins > limit) return false;
-        __builtin_amdgcn_s_sleep(2);
-    }
-}
-
-template <int N, int P>
-__global__ __launch_bounds__(1024) void istft_spill_kernel(IstftArgs a, SpillArgs sp) {
-    constexpr int M = N / 2;
-    using C = FftCfg<M, P, N>;
-    constexpr int TPJ = C::TPJ;
-    constexpr int TWS = TwTable<N>::SIZE;
-    constexpr int PERMAX = P;                            // ((K - 1) hop + N) / (K N / P) <= P
-    constexpr int RT = (TWS + TPJ - 1) / TPJ;            // table values per thread (NT >= TPJ)
-    constexpr int RW = (N + TPJ - 1) / TPJ;
-    extern __shared__ float2 dyn_lds[];
-    const int K = sp.K, NT = K * TPJ;
-    float2* lds = dyn_lds;                               // [K][PADN] frames
-    float2* twt = lds + K * C::PADN;                     // [TWS]
-    float* wl = reinterpret_cast<float*>(twt + TWS);     // [N] window
-    float* inv_env = wl + N;                             // [N] reciprocal envelope by J mod hop
-    const float* ldsf = reinterpret_cast<const float*>(lds);
-
-    const int tid = (int)threadIdx.x;
-    const int blk = (int)blockIdx.x;
-    const int c = blk / sp.nbc, b = blk - c * sp.nbc;
-    const bool first = b == 0, last = b == sp.nbc - 1;
-    const int hop = a.hop, off = a.frame_off;
-    const int s_lo = b * K, s_hi = min(s_lo + K, a.T) - 1;
-    const int Jo0 = (s_lo + off) * hop, Jo1 = (s_lo + K + off) * hop;
-    const int out_end = a.out_off + a.out_len;
-    const float2* sc = a.spec + (size_t)c * a.T * a.F;
-    const int slot = tid / TPJ, j = tid % TPJ;
-    float2* buf = lds + slot * C::PADN;
-    const unsigned long long key = launch_key(0);
-
-    float2 tv[RT];
-    float wv[RW];
-#pragma unroll
-    for (int r = 0; r < RT; r++) tv[r] = a.twt[min(tid + r * NT, TWS - 1)];
-#pragma unroll
-    for (int r = 0; r < RW; r++) wv[r] = a.win[min(tid + r * NT, N - 1)];
-
-    // Stages spectrum frames [s0, s0 + cnt) (cnt <= K) into slots 0.. (zeros past cnt), every
-    // load issued before the first LDS write, and inverse-transforms them: slot g then holds
-    // samples (2n, 2n + 1) of frame s0 + g at LDS index idx(n), times window * norm. Called by
-    // every thread of the block.
-    const WindowPost post{reinterpret_cast<const float2*>(wl), a.norm};
-    auto transform = [&](int s0, int cnt, bool tables) {
-        float2 sv[P];
-        int sl[P], bn[P];
-        if (a.layout == STX_SPEC_F_MAJOR) {
-            const int g = tid % K, k0 = tid / K;         // element e = tid + i NT: slot e % K, bin e / K
-#pragma unroll
-            for (int i = 0; i < P; i++) {
-                sl[i] = g;
-                bn[i] = k0 + i * TPJ;
-                sv[i] = sc[(size_t)bn[i] * a.T + s0 + min(g, cnt - 1)];
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < P; i++) {                // element e = tid + i NT: slot e / M, bin e % M
-                const int e = tid + i * NT;
-                sl[i] = e / M;
-                bn[i] = e % M;
-                sv[i] = sc[(size_t)(s0 + min(sl[i], cnt - 1)) * a.F + bn[i]];
-            }
-        }
-        const int gy = min(tid, K - 1);
-        const float2 nyq = a.layout == STX_SPEC_F_MAJOR ? sc[(size_t)min(M, a.F - 1) * a.T + s0 + min(gy, cnt - 1)]
-                                                        : sc[(size_t)(s0 + min(gy, cnt - 1)) * a.F + min(M, a.F - 1)];
-        if (tables) {
-#pragma unroll
-            for (int r = 0; r < RT; r++)
-                if (tid + r * NT < TWS) twt[tid + r * NT] = tv[r];
-#pragma unroll
-            for (int r = 0; r < RW; r++)
-                if (tid + r * NT < N) wl[tid + r * NT] = wv[r];
-        }
-#pragma unroll
-        for (int i = 0; i < P; i++) lds[sl[i] * C::PADN + bn[i]] = sl[i] < cnt ? sv[i] : make_float2(0.f, 0.f);
-        if (tid < K) lds[tid * C::PADN + M] = (tid < cnt && M < a.F) ? nyq : make_float2(0.f, 0.f);
-        __syncthreads();
-        float2 v[P];
-#pragma unroll
-        for (int r = 0; r < P; r++) {
-            const int k = j + r * TPJ;
-            v[r] = inverse_split<N>(buf[k], buf[M - k], k, a.keep_nyquist, twt);
-        }
-        __syncthreads();                                 // staging read before the FFT overwrites it
-        fft_first_pass<M, P, N>(v, buf, j, post, ToLds<P>{buf});
-        __syncthreads();
-        fft_rest_passes<M, P, N, P>(buf, j, twt, post, ToLds<P>{buf});
-    };
-
-    // Sum over the transformed frames [s0, s0 + cnt) that cover sample J, in frame order.
-    const int K0 = (N - 1) / hop, rK = N - 1 - K0 * hop;
-    auto frame_sum = [&](int J, int s0, int cnt, float acc) {
-        const int A = (int)sp.hop_div.div((unsigned)J), R = J - A * hop;
-        const int lo = max(A - (R <= rK ? K0 : K0 - 1) - off, s0), hi = min(A - off, s0 + cnt - 1);
-        unsigned pos = (unsigned)(J - (lo + off) * hop);
-        const float* sl = ldsf + 2 * C::PADN * (lo - s0);
-        for (int s = lo; s <= hi; s++, pos -= (unsigned)hop, sl += 2 * C::PADN) acc += sl[pos + 2 * (pos / (2 * P))];
-        return acc;
-    };
-    // Envelope division of sample J's sum (src/stft.h:130-136,187-190): win^2 over the
-    // envelope frames covering J, in frame order; the reciprocal from the table where every
-    // covering frame exists, else summed here; 0 where env <= 1e-11 or J >= valid_end.
-    auto finish = [&](int J, float acc) {
-        if (J >= a.valid_end) return 0.f;
-        const int A = (int)sp.hop_div.div((unsigned)J), R = J - A * hop;
-        const int Kc = R <= rK ? K0 : K0 - 1, tf0 = A - Kc;
-        if (tf0 >= 0 && A < a.env_frames) {
-            const float r = inv_env[R];
-            return r > 0.f ? acc * r : 0.f;
-        }
-        const int i0 = max(0, -tf0), i1 = min(Kc, a.env_frames - 1 - tf0);
-        unsigned pos = (unsigned)(R + (Kc - i0) * hop);
-        float env = 0.f;
-        for (int i = i0; i <= i1; i++, pos -= (unsigned)hop) {
-            const float w = wl[pos];
-            env += w * w;
-        }
-        return env > 1e-11f ? acc / env : 0.f;
-    };
-
-    transform(s_lo, s_hi - s_lo + 1, true);
-    for (int R = tid; R < min(hop, N); R += NT) {        // (published by the next barrier)
-        const int Kc = R <= rK ? K0 : K0 - 1;
-        float env = 0.f;
-        for (int i = Kc; i >= 0; i--) {                  // frame order: position R + Kc hop first
-            const float w = wl[R + i * hop];
-            env += w * w;
-        }
-        inv_env[R] = env > 1e-11f ? 1.f / env : 0.f;
-    }
-    __syncthreads();
-
-    // Two-sample units u = tid + q NT: samples Jo0 + 2u and Jo0 + 2u + 1.
-    const int cnt = s_hi - s_lo + 1;
-    const int u_out = (K * hop) / 2;                     // first spill-out unit (Jo1)
-    const int ob = max(Jo0, a.out_off), oe = last ? out_end : min(Jo1, out_end);
-    float* oc = a.out + (size_t)c * a.out_len - a.out_off;
-    float2 own[PERMAX];
-#pragma unroll
-    for (int q = 0; q < PERMAX; q++) {
-        own[q] = make_float2(0.f, 0.f);
-        if (q >= sp.per) continue;
-        const int J = Jo0 + 2 * (tid + q * NT);
-        own[q] = make_float2(frame_sum(J, s_lo, cnt, 0.f), frame_sum(J + 1, s_lo, cnt, 0.f));
-        const int u = tid + q * NT;
-        if (!last && u >= u_out) {                       // spill-out record
-            const unsigned long long d = ((unsigned long long)__float_as_uint(own[q].y) << 32) | __float_as_uint(own[q].x);
-            const unsigned long long idx = (unsigned long long)blk * sp.rpb + (u - u_out);
-            if (u - u_out < sp.rpb) {
-                unsigned long long* r = sp.rec + 2 * idx;
-                sync_store(r, d);
-                sync_store(r + 1, record_tag(d, idx, key));
-            }
-        } else if (first || u >= sp.rpb) {              // no incoming spill: final
-            if (J >= ob && J < oe) oc[J] = finish(J, own[q].x);
-            if (J + 1 >= ob && J + 1 < oe) oc[J + 1] = finish(J + 1, own[q].y);
-        }
-    }
-    if (first) return;
-
-    // Incoming spill: units u < rpb.
-    __shared__ int gave_up;
-    if (tid == 0) gave_up = 0;
-    __syncthreads();
-    float2 in[PERMAX];
-#pragma unroll
-    for (int q = 0; q < PERMAX; q++) {
-        in[q] = make_float2(0.f, 0.f);
-        const int u = tid + q * NT;
-        if (q < sp.per && u < sp.rpb) {
-            const unsigned long long idx = (unsigned long long)(blk - 1) * sp.rpb + u;
-            unsigned long long d = 0;
-            if (spill_wait(sp.rec + 2 * idx, idx, key, sp.spin_limit, d))
-                in[q] = make_float2(__uint_as_float((unsigned)d), __uint_as_float((unsigned)(d >> 32)));
-            else
-                gave_up = 1;
-        }
-    }
-    __syncthreads();
-    if (gave_up) {                                       // uniform: the predecessor's frames here
-        const int S = min(s_lo, (N + hop - 1) / hop - 1);
-        transform(s_lo - S, S, false);
-#pragma unroll
-        for (int q = 0; q < PERMAX; q++) {
-            const int u = tid + q * NT;
-            if (q < sp.per && u < sp.rpb) {
-                const int J = Jo0 + 2 * u;
-                in[q] = make_float2(frame_sum(J, s_lo - S, S, 0.f), frame_sum(J + 1, s_lo - S, S, 0.f));
-            }
-        }
-    }
-#pragma unroll
-    for (int q = 0; q < PERMAX; q++) {
-        const int u = tid + q * NT;
-        if (q < sp.per && u < sp.rpb && !(u >= u_out && !last)) {
-            const int J = Jo0 + 2 * u;
-            if (J >= ob && J < oe) oc[J] = finish(J, in[q].x + own[q].x);
-            if (J + 1 >= ob && J + 1 < oe) oc[J + 1] = finish(J + 1, in[q].y + own[q].y);
-        }
-    }
 }
 
 // ------------------------------------------------------------------ mixed-radix sizes
@@ -1041,87 +743,6 @@ void launch_istft_fused(IstftArgs a, int channels, hipStream_t s) {
 }
 
 template <int N>
-void launch_istft_two_step(IstftArgs a, int channels, hipStream_t s) {
-    constexpr int P = kStftP;
-    constexpr int TPJ = N / 2 / P;
-    constexpr int JOBS = block_jobs(TPJ, 256);
-    a.jobs = channels * a.T;
-    a.nblocks = (a.jobs + JOBS - 1) / JOBS;
-    hipLaunchKernelGGL((istft_frames_kernel<N, P, JOBS>), dim3(xcd_grid(a.nblocks)), dim3(JOBS * TPJ), 0, s, a);
-    launch_check("istft_frames_kernel");
-    hipLaunchKernelGGL(istft_ola_kernel, dim3((a.out_len + 255) / 256, channels), dim3(256), 0, s, a, N);
-    launch_check("istft_ola_kernel");
-}
-
-// The spill path's shape for hop and the points per thread P: frames per block K (K hop even,
-// so that records of two samples start at the next block's first sample), its threads and LDS.
-struct SpillShape {
-    int K = 0, P = 0, threads = 0, per = 0;
-    size_t lds = 0;
-};
-
-template <int N, int P>
-bool spill_shape(int hop, SpillShape& sh) {
-    constexpr int M = N / 2;
-    if constexpr (M < P) {
-        return false;
-    } else {
-        using C = FftCfg<M, P, N>;
-        int K = std::max(1, (N + hop - 1) / hop - 1);
-        if ((K * hop) % 2) K++;
-        const int threads = K * C::TPJ;
-        const size_t lds = ((size_t)K * C::PADN + TwTable<N>::SIZE) * sizeof(float2) + 2 * (size_t)N * sizeof(float);
-        if (threads > 1024 || lds > 160 * 1024) return false;
-        const int per = (((K - 1) * hop + N + 1) / 2 + threads - 1) / threads;
-        if (per > P) return false;
-        sh.K = K;
-        sh.P = P;
-        sh.threads = threads;
-        sh.per = per;
-        sh.lds = lds;
-        return true;
-    }
-}
-
-// Launches the spill path when the shape fits and the workspace holds its records; false
-// otherwise (the caller takes the two-kernel path).
-template <int N>
-bool launch_istft_spill(IstftArgs a, int channels, void* ws, size_t ws_bytes, hipStream_t s) {
-    const int hop = a.hop;
-    if (hop <= 0 || hop > N) return false;
-    // Every output sample lies in [first frame's start, last frame's end].
-    if (a.out_off < a.frame_off * hop) return false;
-    if ((long long)a.out_off + a.out_len > (long long)(a.T - 1 + a.frame_off) * hop + N) return false;
-    SpillShape sh;
-    if (!spill_shape<N, 8>(hop, sh) && !spill_shape<N, 16>(hop, sh)) return false;
-    SpillArgs sp{};
-    sp.nbc = (a.T + sh.K - 1) / sh.K;
-    sp.K = sh.K;
-    sp.rpb = (N - hop + 1) / 2;
-    sp.per = sh.per;
-    sp.hop_div = FastDiv((unsigned)hop);
-    sp.spin_limit = grid_spin_limit();
-    const long long blocks = (long long)channels * sp.nbc;
-    if (blocks <= 0 || blocks > (1LL << 31) - 1) return false;
-    if ((size_t)blocks * sp.rpb * 16 > ws_bytes) return false;
-    sp.rec = static_cast<unsigned long long*>(ws);
-    auto go = [&](auto kernel) {
-        if (sh.lds > 64 * 1024)                          // dynamic LDS past the default limit
-            hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)sh.lds),
-                      "hipFuncSetAttribute");
-        hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(sh.threads), sh.lds, s, a, sp);
-        launch_check("istft_spill_kernel");
-    };
-    if (sh.P == 8) {
-        if constexpr (N / 2 >= 8) go(istft_spill_kernel<N, 8>);
-    } else {
-        if constexpr (N / 2 >= 16) go(istft_spill_kernel<N, 16>);
-    }
-    return true;
-}
-
-template <int N>
 void launch_fft(float2* data, int batch, int inverse, const float2* twt, hipStream_t s) {
     constexpr int P = N >= 16 ? 16 : 8;
     constexpr int TPJ = N / P;
@@ -1150,13 +771,7 @@ void by_size(int n, Args&&... args) {
 }
 template <int N> struct StftL { static void go(const StftArgs& a, hipStream_t s) { launch_stft<N>(a, s); } };
 template <int N> struct IstftL {
-    static void go(const IstftArgs& a, int ch, bool two_step, void* ws, size_t ws_bytes, hipStream_t s) {
-        if (two_step) {
-            if (!launch_istft_spill<N>(a, ch, ws, ws_bytes, s)) launch_istft_two_step<N>(a, ch, s);
-        } else {
-            launch_istft_fused<N>(a, ch, s);
-        }
-    }
+    static void go(const IstftArgs& a, int ch, hipStream_t s) { launch_istft_fused<N>(a, ch, s); }
 };
 template <int N> struct FftL {
     static void go(float2* d, int b, int inv, const float2* tw, hipStream_t s) { launch_fft<N>(d, b, inv, tw, s); }
@@ -1214,13 +829,14 @@ void run_istft(const stx_fft* f, IstftArgs a, int channels, void* workspace, siz
         launch_check("istft_ola_kernel");
         return;
     }
+    // Power-of-two sizes: the fused kernel with or without a workspace (a two-kernel path that
+    // transforms each frame once into the workspace measured slower at every size here: it
+    // writes and re-reads every windowed frame). A workspace passed in is still checked.
     if (two_step) {
         const size_t need = istft_workspace_bytes(f->n, channels, a.T);
         STX_REQUIRE(ws_bytes >= need, "workspace too small: %zu bytes, need %zu", ws_bytes, need);
-        check_extent((long long)channels * a.T * f->n, "workspace");
-        a.frames = static_cast<float*>(workspace);
     }
-    by_size<IstftL>(f->n, a, channels, two_step, workspace, ws_bytes, s);
+    by_size<IstftL>(f->n, a, channels, s);
 }
 
 stx_status torch_istft_impl(const stx_fft* f, const float* spec, int channels, int n_frames, int hop,

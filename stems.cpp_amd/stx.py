@@ -247,8 +247,9 @@ def _ws(workspace):
 
 
 def torch_istft(fft, spec, hop, normalized=False, layout=F_MAJOR, out=None, stream=None, workspace=None):
-    """spec: complex64 [C, F, T] or [C, T, F] -> float32 [C, hop * (T - 1)]. With a workspace
-    tensor of at least istft_workspace_size() bytes the two-kernel path runs."""
+    """spec: complex64 [C, F, T] or [C, T, F] -> float32 [C, hop * (T - 1)]. A workspace tensor
+    of at least istft_workspace_size() bytes is required for sizes that are not powers of two
+    (two kernels); power-of-two sizes check it and run the single fused kernel."""
     import torch
     _require(spec, torch.complex64, "spec")
     C = spec.shape[0]

@@ -53,7 +53,7 @@ def ws_for(fft, channels, frames, device, use):
 
 @pytest.mark.parametrize("path", SPEC_GOLDEN, ids=[os.path.basename(p)[5:-4] for p in SPEC_GOLDEN])
 @pytest.mark.parametrize("layout", [stx.F_MAJOR, stx.T_MAJOR])
-@pytest.mark.parametrize("use_ws", [False, True], ids=["fused", "two_step"])
+@pytest.mark.parametrize("use_ws", [False, True], ids=["plain", "workspace"])
 def test_golden_spectrum_and_inverse(device, path, layout, use_ws):
     d = np.load(path)
     n = int(d["n_fft"])
@@ -86,7 +86,7 @@ def _stereo(seed, length, sigma=0.1):
     return synth.normal(seed, (2, length), sigma)
 
 
-@pytest.mark.parametrize("use_ws", [False, True], ids=["fused", "two_step"])
+@pytest.mark.parametrize("use_ws", [False, True], ids=["plain", "workspace"])
 def test_htdemucs_spec_c1_full_size(device, orc, use_ws):
     # HTDemucs spec: stereo 343,980 samples, n_fft 4096, hop 1024 -> [2][2048][336].
     length = 343980
@@ -119,7 +119,7 @@ def test_torch_stft_c1_plain_call(device, orc):
 
 
 @pytest.mark.parametrize("normalized", [False, True])
-@pytest.mark.parametrize("use_ws", [False, True], ids=["fused", "two_step"])
+@pytest.mark.parametrize("use_ws", [False, True], ids=["plain", "workspace"])
 def test_roformer_stft_c3_full_size(device, orc, normalized, use_ws):
     # RoFormer chunk: stereo 352,800 samples, n_fft 2048, hop 441 -> [2][1025][801] (odd T).
     length = 352800
@@ -142,7 +142,7 @@ def test_roformer_stft_c3_full_size(device, orc, normalized, use_ws):
 
 
 @pytest.mark.parametrize("n", [16, 32, 64, 128, 256, 512, 1024, 2048, 4096, 8192])
-@pytest.mark.parametrize("use_ws", [False, True], ids=["fused", "two_step"])
+@pytest.mark.parametrize("use_ws", [False, True], ids=["plain", "workspace"])
 def test_every_fft_size_stft_round_trip(device, orc, n, use_ws):
     hop = max(1, n // 4 - 1)
     length = 3 * n + 5
@@ -230,40 +230,6 @@ def test_small_hop_needs_several_rounds(device, orc):
         ref = orc.torch_stft(x[c], n, hop)
         assert snr_db(spec_h[c], ref) >= SNR_DB
         assert snr_db(y[c], orc.torch_istft(ref, n, hop)) >= SNR_DB
-
-
-@pytest.mark.parametrize("case", ["c1_htdemucs", "c3_torch"])
-@pytest.mark.parametrize("layout", [stx.F_MAJOR, stx.T_MAJOR])
-def test_istft_ws_spill_forced_fallback(device, orc, case, layout, monkeypatch):
-    """The workspace iSTFT transforms each frame once and hands each block's spill (its frames'
-    sums past its own range) to the next block as tagged records. STX_GRID_SYNC_SPIN_LIMIT=0
-    makes every block give up its wait at the first look and transform its predecessor's frames
-    itself: the same bits. Against the fused path (frames shared by two tiles transformed
-    twice) the sums differ only in rounding."""
-    if case == "c1_htdemucs":
-        n, hop, length = 4096, 1024, 343980
-        x = _stereo(41, length, 0.1)
-        f = plan(n)
-        spec = stx.htdemucs_spec(f, to_dev(x, device), layout=layout)
-        frames = spec.shape[2] if layout == stx.F_MAJOR else spec.shape[1]
-        run = lambda ws: stx.htdemucs_ispec(f, spec, length, layout=layout, workspace=ws)
-    else:
-        n, hop, length = 2048, 441, 352800
-        x = _stereo(42, length, 0.1)
-        f = plan(n)
-        spec = stx.torch_stft(f, to_dev(x, device), hop, layout=layout)
-        frames = length // hop + 1
-        run = lambda ws: stx.torch_istft(f, spec, hop, layout=layout, workspace=ws)
-    ws = ws_for(f, 2, frames, device, True)
-    y_ws = host(run(ws))
-    monkeypatch.setenv("STX_GRID_SYNC_SPIN_LIMIT", "0")
-    y_forced = host(run(ws))
-    monkeypatch.delenv("STX_GRID_SYNC_SPIN_LIMIT")
-    y_fused = host(run(None))
-    assert np.array_equal(y_ws, y_forced)
-    assert np.max(np.abs(y_ws - y_fused)) <= 1e-6 * np.max(np.abs(y_fused))
-    if case == "c3_torch":                                  # torch_stft -> torch_istft is the identity
-        assert snr_db(y_ws, x) >= SNR_DB
 
 
 def test_workspace_too_small(device):
