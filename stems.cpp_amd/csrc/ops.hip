@@ -135,7 +135,9 @@ __device__ __forceinline__ float gelu_erf_hl(float x, float dx) {
 
 // gelu of a double argument t (a fused producer's result before rounding), the same
 // approximation with the exponent -t^2 / (2 ln 2) formed in double instead of as a float head
-// and tail, and one rounding of t Phi(t) at the end. Branch- and select-free in the ranges the
+// and tail, and the product of the rounded t and Phi at the end (a float multiply: in the
+// simulation below the bound is unchanged, the conditioning of the tail lies in the exponent,
+// which stays in double). Branch- and select-free in the ranges the
 // float formula has to clamp: the 1/2 is folded into P's coefficients (exact), t > ~5.3 gives
 // Q < 2^-25, so Phi = 1 - Q = 1 exactly and the result is t rounded; t < ~-13.2 underflows Q to
 // 0 (the exponent is floored at -200 so that 2^n stays finite), giving t * 0 = -0 as the float
@@ -163,7 +165,7 @@ __device__ __forceinline__ float gelu_erf_dt(double t) {
     p = fmaf(p, r, 1.4104762675e-01f);
     p = fmaf(p, r, 1.410473883e-01f);
     const float g = e * (r * p);                          // Phi(-|t|)
-    return (float)(t * (double)(x < 0.f ? g : 1.f - g));
+    return x * (x < 0.f ? g : 1.f - g);                   // rounded t times Phi: at most 1 ulp more
 }
 
 __device__ __forceinline__ float gelu_erf(float x) { return gelu_erf_hl(x, 0.f); }
@@ -822,11 +824,27 @@ __device__ __forceinline__ void gn_fold(const double* part, int nblk, double* re
     t2 = p2;
 }
 
+// mean and 1/sqrt(var + eps) from the group's totals. Every path calls this one function on the
+// same totals, so every path gets the same bits. 1/N and the reciprocal square root come from
+// the hardware's double approximations refined by Newton steps (each doubles the correct bits
+// of the ~2^-22 start, so two reach double precision), not from IEEE division and square root:
+// about 20 instructions instead of 60, on the path between a block's release and its stores.
+__device__ __forceinline__ double rcp_f64_nr(double d) {
+    double r = __builtin_amdgcn_rcp(d);
+    r = fma(r, fma(-d, r, 1.0), r);
+    return fma(r, fma(-d, r, 1.0), r);
+}
 __device__ __forceinline__ void gn_moments(double t1, double t2, unsigned count, double shift, float eps, double& mean,
                                            double& rstd) {
-    const double N = (double)count, dm = t1 / N;
+    const double rn = rcp_f64_nr((double)count), dm = t1 * rn;
     mean = shift + dm;
-    rstd = 1.0 / sqrt(fmax(t2 / N - dm * dm, 0.0) + (double)eps);
+    const double v = fmax(t2 * rn - dm * dm, 0.0) + (double)eps;
+    double y = __builtin_amdgcn_rsq(v);
+    if (v > 0.0 && v < 1e300) {                       // y = y (3 - v y^2) / 2, twice
+        y = y * fma(-0.5 * v, y * y, 1.5);
+        y = y * fma(-0.5 * v, y * y, 1.5);
+    }
+    rstd = y;
 }
 
 // One affine operand at element (channel c, i0, i1, i3) under the per-element kinds.
