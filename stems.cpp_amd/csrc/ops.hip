@@ -673,8 +673,8 @@ __global__ __launch_bounds__(256) void ew_flat_kernel(const float* __restrict__ 
 // GELU of the double t (its negative tail is ill-conditioned: d ln gelu / d ln t ~ 1 + t^2).
 //
 // Paths, by shape:
-//   single pass (gn_fused_kernel) when the groups fit on the device at once and y does not
-//     overlap x: x is read once, the blocks exchange their partial sums (grid_sync.hpp);
+//   single pass (gn_fused_kernel) when the groups fit on the device at once, VEC < 4 and y
+//     does not overlap x: x is read once, the blocks exchange their partial sums (grid_sync.hpp);
 //   two passes otherwise: gn_partial_kernel writes each chunk's partial sums (and K), then
 //     gn_apply_kernel folds its group's partials itself (or reads gn_fold_kernel's totals when
 //     a group has more than kGnFoldDirect chunks) and writes its chunk.
@@ -1009,7 +1009,7 @@ __device__ __forceinline__ void gn_fused_body(const GroupNormArgs& a, const Grid
     gn_write<AK, GELU, VEC, FULL>(a.y + begin, lo, hi, mean, rstd, v, ok, pr);
 }
 
-// Two blocks per CU must fit (the C = 48 op-set shape has 504 blocks of VEC 4 for 256 CUs):
+// Two blocks per CU must fit (the C = 96 and 192 op-set shapes have 504 blocks for 256 CUs):
 // at least 4 waves per SIMD, i.e. at most 128 VGPRs.
 template <int AK, bool GELU, int VEC>
 __global__ __launch_bounds__(kGnThreads) __attribute__((amdgpu_waves_per_eu(4))) void gn_fused_kernel(GroupNormArgs a,
@@ -1433,9 +1433,14 @@ GnPlan gn_plan(const stx_tensor* a, int n_groups) {
 template <int AK, bool GELU, int VEC>
 void launch_gn_vec(const GroupNormArgs& g, const GnPlan& p, const GridSync& sync, bool single, hipStream_t s) {
     const dim3 grid((unsigned)p.nch, (unsigned)p.groups_total);
-    // The per-element parameter kinds hold 16 weights and 16 biases per thread at VEC 4, more
-    // than the 128 VGPRs of two blocks per CU leave without spilling: two passes for them.
-    if (single && (AK == AFF_CHANNEL_WAVE || VEC < 4)) {
+    // VEC 4 (groups of more than kGridMaxBlocks * gn_chunk<2>() floats) takes two passes: the
+    // per-element parameter kinds would hold 16 weights and 16 biases per thread, more than the
+    // 128 VGPRs of two blocks per CU leave without spilling, and for the per-wave kind the two
+    // passes measured faster (15.2 against 16.1 us for 48 x 85995 floats, cold): the second
+    // pass's block m runs on the XCD that read chunk m in the first, so it re-reads x from that
+    // XCD's L2, and the kernel boundary costs less than the single pass's exchange plus the
+    // spread in its blocks' release at 504 blocks of 16 values per thread.
+    if constexpr (VEC < 4) if (single) {
         const void* k = reinterpret_cast<const void*>(&gn_fused_kernel<AK, GELU, VEC>);
         if ((long long)p.nch * p.groups_total <= resident_blocks(k, s)) {
             hipLaunchKernelGGL((gn_fused_kernel<AK, GELU, VEC>), grid, dim3(kGnThreads), 0, s, g, sync);
