@@ -14,6 +14,7 @@
 // reference computes them, so the weights (and so the results) are bit-identical.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <vector>
 
 #include "common.hpp"
@@ -23,6 +24,7 @@ struct stx_uvr_demix {
     int64_t len = 0, M = 0, step = 0, n_chunks = 0, first_partial = 0;
     int channels = 0, chunk = 0, n_fft = 0, trim = 0;
     double* d_w = nullptr;           // [chunk] weights of full chunks, then each partial chunk's
+    uint64_t w_count = 0;            // entries of d_w
 };
 
 namespace stx {
@@ -81,18 +83,36 @@ __global__ __launch_bounds__(256) void uvr_chunks_kernel(UvrArgs a, const float*
 // out[q][t] = sum_k (double)y[k][q][p - i_k] * w_k[p - i_k] / sum_k w_k[p - i_k], p = trim + t,
 // over the chunks covering p in chunk order (src/tfc_tdf.cpp:427-440). NK bounds the chunks
 // covering one sample. A thread takes kUvrPer samples and P planes, which share the weights and
-// their sum; loads are clamped to valid addresses and issued together.
+// their sum; loads are clamped to valid addresses and issued together. U is the index type:
+// uint32_t when every index fits (the usual case: 64-bit index products cost several VALU
+// instructions each, which made the kernel issue-bound), uint64_t otherwise.
 constexpr int kUvrMaxCover = 8;
 constexpr int kUvrPer = 2;
 
-template <int NK, int P>
+template <class U>
+__device__ __forceinline__ U umin(U x, U y) { return x < y ? x : y; }
+
+// uvr_woff in U's arithmetic. With U = uint32_t the host has checked that the table has fewer
+// than 2^32 entries and k < 65536: the halvings are then exact (k (k - 1) < 2^32) and the rest
+// is ring arithmetic, so intermediate wrap-around leaves the (representable) result exact.
+template <class U>
+__device__ __forceinline__ U uvr_woff_u(const UvrArgs& a, U k) {
+    const U f = (U)a.first_partial;
+    if (k < f) return 0;
+    return (U)a.chunk + (k - f) * (U)a.M - (U)a.step * (k * (k - 1) / 2 - f * (f - 1) / 2);
+}
+
+template <int NK, int P, class U>
 __global__ __launch_bounds__(256) void uvr_ola_kernel(UvrArgs a, const float* __restrict__ y,
                                                       const double* __restrict__ w, int planes,
                                                       float* __restrict__ out) {
 #pragma clang fp contract(off)
     const int q0 = (int)blockIdx.y * P;
-    const int64_t t0 = (int64_t)blockIdx.x * kUvrPer * 256 + threadIdx.x;
-    if (t0 >= a.len) return;
+    const U len = (U)a.len;
+    const U t0 = (U)blockIdx.x * (kUvrPer * 256) + threadIdx.x;
+    if (t0 >= len) return;
+    const U step = (U)a.step, M = (U)a.M, chunk = (U)a.chunk, pc = (U)planes * chunk;
+    const int last = (int)a.n_chunks - 1;
     // Every load of every sample first (clamped addresses), then the sums: a chunk that does not
     // cover the sample adds +0.0, an exact no-op (the sums start at +0.0 and never become -0.0),
     // so no load sits behind a branch.
@@ -101,26 +121,27 @@ __global__ __launch_bounds__(256) void uvr_ola_kernel(UvrArgs a, const float* __
     float yv[kUvrPer][P][NK];
 #pragma unroll
     for (int e = 0; e < kUvrPer; e++) {
-        const int64_t t = min(t0 + 256LL * e, a.len - 1);
-        const int64_t p = a.trim + t;
-        const int64_t k_hi = min((int64_t)a.sdiv.div((unsigned)p), a.n_chunks - 1);
+        const U t = umin<U>(t0 + (U)(256 * e), len - 1);
+        const U p = (U)a.trim + t;
+        const int k_hi = min((int)a.sdiv.div((unsigned)p), last);
 #pragma unroll
         for (int j = 0; j < NK; j++) {                  // chunk k_hi - j
-            const int64_t k = max(k_hi - j, (int64_t)0);
-            const int64_t i = k * a.step;
-            const int64_t actual = min((int64_t)a.chunk, a.M - i);
-            const int64_t r = p - i;
-            in[e][j] = k_hi - j >= 0 && r < actual;
-            const int64_t rc = min(r, actual - 1);
-            wv[e][j] = w[uvr_woff(a, k) + rc];
-            const int64_t base = (int64_t)k * planes * a.chunk + rc;
+            const int kk = k_hi - j;
+            const U k = (U)max(kk, 0);
+            const U i = k * step;                       // <= p: k <= p / step
+            const U actual = umin<U>(chunk, M - i);
+            const U r = p - i;
+            in[e][j] = kk >= 0 && r < actual;
+            const U rc = umin<U>(r, actual - 1);
+            wv[e][j] = w[uvr_woff_u<U>(a, k) + rc];
+            const U base = k * pc + rc;
 #pragma unroll
-            for (int u = 0; u < P; u++) yv[e][u][j] = y[base + (int64_t)min(q0 + u, planes - 1) * a.chunk];
+            for (int u = 0; u < P; u++) yv[e][u][j] = y[base + (U)min(q0 + u, planes - 1) * chunk];
         }
     }
 #pragma unroll
     for (int e = 0; e < kUvrPer; e++) {
-        const int64_t t = t0 + 256LL * e;
+        const U t = t0 + (U)(256 * e);
         double div = 0.0;
 #pragma unroll
         for (int j = NK - 1; j >= 0; j--) div = div + (in[e][j] ? wv[e][j] : 0.0);   // ascending chunk order
@@ -136,20 +157,27 @@ __global__ __launch_bounds__(256) void uvr_ola_kernel(UvrArgs a, const float* __
                 res = res + (in[e][j] ? prod : 0.0);
             }
             const double q = div != 0.0 ? div_rn(res, div, rdiv) : res / div;
-            if (t < a.len && q0 + u < planes) out[(size_t)(q0 + u) * a.len + t] = (float)q;
+            if (t < len && q0 + u < planes) out[(size_t)(q0 + u) * a.len + t] = (float)q;
         }
     }
 }
 
-template <int NK>
-void launch_uvr_ola(const UvrArgs& a, const float* y, const double* w, int planes, float* out, hipStream_t s) {
+template <int NK, class U>
+void launch_uvr_ola_u(const UvrArgs& a, const float* y, const double* w, int planes, float* out, hipStream_t s) {
     const unsigned bx = (unsigned)((a.len + 256 * kUvrPer - 1) / (256 * kUvrPer));
     if (planes % 4 == 0)
-        hipLaunchKernelGGL((uvr_ola_kernel<NK, 4>), dim3(bx, (unsigned)(planes / 4)), dim3(256), 0, s, a, y, w, planes, out);
+        hipLaunchKernelGGL((uvr_ola_kernel<NK, 4, U>), dim3(bx, (unsigned)(planes / 4)), dim3(256), 0, s, a, y, w, planes, out);
     else if (planes % 2 == 0)
-        hipLaunchKernelGGL((uvr_ola_kernel<NK, 2>), dim3(bx, (unsigned)(planes / 2)), dim3(256), 0, s, a, y, w, planes, out);
+        hipLaunchKernelGGL((uvr_ola_kernel<NK, 2, U>), dim3(bx, (unsigned)(planes / 2)), dim3(256), 0, s, a, y, w, planes, out);
     else
-        hipLaunchKernelGGL((uvr_ola_kernel<NK, 1>), dim3(bx, (unsigned)planes), dim3(256), 0, s, a, y, w, planes, out);
+        hipLaunchKernelGGL((uvr_ola_kernel<NK, 1, U>), dim3(bx, (unsigned)planes), dim3(256), 0, s, a, y, w, planes, out);
+}
+
+template <int NK>
+void launch_uvr_ola(const UvrArgs& a, const float* y, const double* w, int planes, bool narrow, float* out,
+                    hipStream_t s) {
+    if (narrow) launch_uvr_ola_u<NK, uint32_t>(a, y, w, planes, out, s);
+    else launch_uvr_ola_u<NK, uint64_t>(a, y, w, planes, out, s);
 }
 
 // est *= compensate (when != 1), and with `complement` rest = mix - est_0 - est_1 - ... in float
@@ -235,6 +263,7 @@ STX_API stx_status stx_uvr_demix_create(int64_t len, int channels, int chunk, in
         for (int64_t k = 0; k < n; k++)             // the device recomputes the offsets in closed form
             STX_REQUIRE(uvr_woff(uvr_args(d), k) + std::min<int64_t>(chunk, M - k * step) <= (int64_t)w.size(),
                         "UVR weight table layout");
+        d->w_count = w.size();
         hipError_t e = hipMalloc(&d->d_w, sizeof(double) * w.size());
         if (e == hipSuccess) e = hipMemcpy(d->d_w, w.data(), sizeof(double) * w.size(), hipMemcpyHostToDevice);
         if (e != hipSuccess) {
@@ -290,12 +319,18 @@ STX_API stx_status stx_uvr_demix_overlap_add(const stx_uvr_demix* d, const float
             fail(STX_STATUS_UNSUPPORTED, "UVR overlap-add: more than %d chunks cover a sample", kUvrMaxCover);
         const hipStream_t s = as_stream(stream);
         const UvrArgs a = uvr_args(d);
+        // 32-bit indices when the chunk outputs, the weight table and the chunk count allow;
+        // STX_UVR_WIDE_INDEX=1 (read at each call) takes the 64-bit ones for every size, so that
+        // the two kernels can be compared.
+        const char* wide = std::getenv("STX_UVR_WIDE_INDEX");
+        const bool narrow = d->n_chunks < 65536 && (uint64_t)d->n_chunks * planes * d->chunk < (1ull << 32) &&
+                            d->w_count < (1ull << 32) && !(wide && wide[0] == '1');
         switch (cover) {
-        case 1: launch_uvr_ola<1>(a, y, d->d_w, planes, out, s); break;
-        case 2: launch_uvr_ola<2>(a, y, d->d_w, planes, out, s); break;
-        case 3: launch_uvr_ola<3>(a, y, d->d_w, planes, out, s); break;
-        case 4: launch_uvr_ola<4>(a, y, d->d_w, planes, out, s); break;
-        default: launch_uvr_ola<kUvrMaxCover>(a, y, d->d_w, planes, out, s); break;
+        case 1: launch_uvr_ola<1>(a, y, d->d_w, planes, narrow, out, s); break;
+        case 2: launch_uvr_ola<2>(a, y, d->d_w, planes, narrow, out, s); break;
+        case 3: launch_uvr_ola<3>(a, y, d->d_w, planes, narrow, out, s); break;
+        case 4: launch_uvr_ola<4>(a, y, d->d_w, planes, narrow, out, s); break;
+        default: launch_uvr_ola<kUvrMaxCover>(a, y, d->d_w, planes, narrow, out, s); break;
         }
         launch_check("uvr_ola_kernel");
     });

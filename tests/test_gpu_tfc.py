@@ -67,7 +67,9 @@ UVR_CASES = [(SONG, CHUNK, 7680, -1.0), (SONG, CHUNK, 7680, 0.5), (SONG, CHUNK, 
 
 
 @pytest.mark.parametrize("length,chunk,n_fft,overlap", UVR_CASES)
-def test_uvr_chunks_and_ola_bit_exact(device, od, length, chunk, n_fft, overlap):
+def test_uvr_chunks_and_ola_bit_exact(device, od, length, chunk, n_fft, overlap, monkeypatch):
+    """Chunks and overlap-add against the oracle, bit for bit; the overlap-add with 32-bit
+    indices (every case here) and with 64-bit ones (STX_UVR_WIDE_INDEX=1) alike."""
     mix = synth.normal(length % 1000 + 7, (2, length), 0.3)
     plan = stx.UvrDemix(length, 2, chunk, n_fft, overlap)
     n, M, step = od.uvr_geometry(length, chunk, n_fft, overlap)
@@ -76,8 +78,11 @@ def test_uvr_chunks_and_ola_bit_exact(device, od, length, chunk, n_fft, overlap)
     assert np.array_equal(parts, od.uvr_chunks(mix, chunk, n_fft, overlap))
     S = 1 if length > 1000000 else 3
     y = synth.uniform(length % 991, (n, S, 2, chunk))
-    got = host(plan.overlap_add(dev(y, device)))
+    yd = dev(y, device)
+    got = host(plan.overlap_add(yd))
     assert np.array_equal(got, od.uvr_ola(y, length, chunk, n_fft, overlap))
+    monkeypatch.setenv("STX_UVR_WIDE_INDEX", "1")
+    assert np.array_equal(host(plan.overlap_add(yd)), got)
 
 
 def test_uvr_ola_non_finite_outputs(device, od):
