@@ -148,6 +148,9 @@ template <int KIND>
 __global__ __launch_bounds__(256) void normalize_kernel(const float* x, float* y, long long count, const double* stats) {
     const double mean = stats[0];
     const double den = KIND == NORM_MIX ? stats[1] : 1e-5 + stats[1];
+    // den is positive (or NaN): the moments of finite floats cannot overflow, so div_rn gives the
+    // IEEE quotient with one reciprocal per thread.
+    const double rden = 1.0 / den;
     const long long e0 = (long long)blockIdx.x * (256 * kNormPer) + threadIdx.x;
     if (KIND == NORM_CAC) {
         const long long c = blockIdx.y;
@@ -161,8 +164,8 @@ __global__ __launch_bounds__(256) void normalize_kernel(const float* x, float* y
         for (int k = 0; k < kNormPer; k++) {
             const long long e = e0 + 256LL * k;
             if (e < count) {
-                re[e] = (float)(((double)v[k].x - mean) / den);
-                im[e] = (float)(((double)v[k].y - mean) / den);
+                store_stream(re + e, (float)div_rn((double)v[k].x - mean, den, rden));
+                store_stream(im + e, (float)div_rn((double)v[k].y - mean, den, rden));
             }
         }
     } else {
@@ -172,24 +175,21 @@ __global__ __launch_bounds__(256) void normalize_kernel(const float* x, float* y
 #pragma unroll
         for (int k = 0; k < kNormPer; k++) {
             const long long e = e0 + 256LL * k;
-            if (e < count) y[e] = (float)(((double)v[k] - mean) / den);
+            if (e < count) store_stream(y + e, (float)div_rn((double)v[k] - mean, den, rden));
         }
     }
 }
 
-// One launch of moments + normalise for NORM_CAC / NORM_FLAT: x is n floats (CAC: the complex64
-// spectrum [C][ft] read as 2 C ft floats), VEC float4 per thread in chunks of kGridThreads * 4 *
-// VEC floats. Same statistics formulas as moments_final_kernel and the same per-element division
-// as normalize_kernel; block 0 writes {mean, sd} to stats.
-//
-// This thread's values of the chunk at lo (clamped loads past n; counted only where in range).
-template <int VEC>
-__device__ __forceinline__ void norm_load(const float* x, long long n, long long lo, bool vec, float (&v)[VEC][4]) {
-    constexpr int NT = kGridThreads;
+// This thread's values of the chunk at lo. FULL (a whole chunk, x 16-byte aligned): unconditional
+// float4 loads; otherwise clamped scalar loads (always-valid addresses, issued together), counted
+// only where in range. Indices are 32-bit: the single pass covers fewer than 2^32 floats.
+template <int VEC, bool FULL>
+__device__ __forceinline__ void norm_load(const float* x, unsigned n, unsigned lo, float (&v)[VEC][4]) {
+    constexpr unsigned NT = kGridThreads;
 #pragma unroll
     for (int k = 0; k < VEC; k++) {
-        const long long p = lo + (k * NT + (long long)threadIdx.x) * 4;
-        if (vec && p + 3 < n) {
+        const unsigned p = lo + (k * NT + threadIdx.x) * 4;
+        if constexpr (FULL) {
             const float4 q = *reinterpret_cast<const float4*>(x + p);
             v[k][0] = q.x;
             v[k][1] = q.y;
@@ -204,17 +204,17 @@ __device__ __forceinline__ void norm_load(const float* x, long long n, long long
 
 // Block sums of d = v - shift over the chunk at lo, in every thread: each thread adds its
 // values in (k, j) order, then block_sum2_n.
-template <int VEC>
-__device__ __forceinline__ void norm_sums(const float (&v)[VEC][4], long long n, long long lo, double shift, double* red,
+template <int VEC, bool FULL>
+__device__ __forceinline__ void norm_sums(const float (&v)[VEC][4], unsigned n, unsigned lo, double shift, double* red,
                                           double& s1, double& s2) {
-    constexpr int NT = kGridThreads;
+    constexpr unsigned NT = kGridThreads;
     s1 = 0.0;
     s2 = 0.0;
 #pragma unroll
     for (int k = 0; k < VEC; k++)
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const bool in = lo + (k * NT + (long long)threadIdx.x) * 4 + j < n;
+            const bool in = FULL || lo + (k * NT + threadIdx.x) * 4 + j < n;
             const double d = in ? (double)v[k][j] - shift : 0.0;
             s1 = s1 + d;
             s2 = fma(d, d, s2);
@@ -222,30 +222,29 @@ __device__ __forceinline__ void norm_sums(const float (&v)[VEC][4], long long n,
     block_sum2_n<NT>(s1, s2, red);
 }
 
-template <int KIND, int VEC>
-__global__ __launch_bounds__(kGridThreads) void norm_fused_kernel(const float* x, float* y, long long n, long long ft,
-                                                                  double* stats, GridSync f) {
-    constexpr int NT = kGridThreads;
-    constexpr long long CH = NT * 4 * VEC;
-    __shared__ double red[2 * NT / 64];
-    __shared__ double tot[2];
-    const long long lo = (long long)blockIdx.x * CH;
+// CAC: float e of the spectrum is channel c = e / (2 ft), bin i = (e % (2 ft)) / 2, re or im by
+// its parity, and goes to plane 2 c (re) or 2 c + 1 (im) at i (cdiv divides by 2 ft).
+template <int KIND, int VEC, bool FULL>
+__device__ __forceinline__ void norm_fused_body(const float* x, float* y, unsigned n, unsigned ft, FastDiv cdiv,
+                                                bool vec, double* stats, const GridSync& f, double* red, double* tot) {
+    constexpr unsigned NT = kGridThreads;
+    constexpr unsigned CH = NT * 4 * VEC;
+    const unsigned lo = blockIdx.x * CH;
     const int nch = (int)((n + CH - 1) / CH);
-    const bool vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && n % 4 == 0;
-    float v[VEC][4];
-    norm_load<VEC>(x, n, lo, vec, v);
     const double shift = (double)x[0];
+    float v[VEC][4];
+    norm_load<VEC, FULL>(x, n, lo, v);
     double s1, s2;
-    norm_sums<VEC>(v, n, lo, shift, red, s1, s2);
+    norm_sums<VEC, FULL>(v, n, lo, shift, red, s1, s2);
     // A block whose wait gave up adds every chunk's sums itself, in the collector's order.
     grid_totals<NT>(f, 0, nch, s1, s2, red, tot, [&](double* t) {
         double p1 = 0.0, p2 = 0.0;
         for (int m = 0; m < nch; m++) {
             float w[VEC][4];
-            norm_load<VEC>(x, n, m * CH, vec, w);
+            norm_load<VEC, false>(x, n, m * CH, w);
             double q1, q2;
-            norm_sums<VEC>(w, n, m * CH, shift, red, q1, q2);
-            if ((int)threadIdx.x == m % NT) {
+            norm_sums<VEC, false>(w, n, m * CH, shift, red, q1, q2);
+            if ((int)threadIdx.x == m % (int)NT) {
                 p1 += q1;
                 p2 += q2;
             }
@@ -265,39 +264,55 @@ __global__ __launch_bounds__(kGridThreads) void norm_fused_kernel(const float* x
         stats[1] = sd;
     }
     const double den = 1e-5 + sd, rden = 1.0 / den;
-    // CAC: float e of the spectrum is channel c = e / (2 ft), bin i = (e % (2 ft)) / 2, re or im
-    // by its parity, and goes to plane 2 c (re) or 2 c + 1 (im) at i.
     const bool pairs = KIND == NORM_CAC && vec && ft % 2 == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0;
+    const unsigned ft2 = 2 * ft;
 #pragma unroll
     for (int k = 0; k < VEC; k++) {
-        const long long p = lo + (k * NT + (long long)threadIdx.x) * 4;
-        if (p >= n) continue;
+        const unsigned p = lo + (k * NT + threadIdx.x) * 4;
+        if (!FULL && p >= n) continue;
         float o[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) o[j] = (float)div_rn((double)v[k][j] - mean, den, rden);   // = (v - mean) / den
         if (KIND == NORM_FLAT) {
-            if (vec && p + 3 < n) {
-                *reinterpret_cast<float4*>(y + p) = make_float4(o[0], o[1], o[2], o[3]);
+            if (FULL || (vec && p + 3 < n)) {
+                store_stream(reinterpret_cast<float4*>(y + p), make_float4(o[0], o[1], o[2], o[3]));
             } else {
 #pragma unroll
                 for (int j = 0; j < 4; j++)
-                    if (p + j < n) y[p + j] = o[j];
+                    if (p + j < n) store_stream(y + p + j, o[j]);
             }
-        } else if (pairs && p + 3 < n) {
+        } else if (pairs && (FULL || p + 3 < n)) {
             // Two whole complex values of one channel (2 ft is a multiple of 4 and p of 4).
-            const long long c = p / (2 * ft), i = (p - c * 2 * ft) / 2;
-            *reinterpret_cast<float2*>(y + 2 * c * ft + i) = make_float2(o[0], o[2]);
-            *reinterpret_cast<float2*>(y + (2 * c + 1) * ft + i) = make_float2(o[1], o[3]);
+            const unsigned c = cdiv.div(p), i = (p - c * ft2) / 2;
+            store_stream(reinterpret_cast<float2*>(y + 2 * c * ft + i), make_float2(o[0], o[2]));
+            store_stream(reinterpret_cast<float2*>(y + (2 * c + 1) * ft + i), make_float2(o[1], o[3]));
         } else {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const long long e = p + j;
+                const unsigned e = p + j;
                 if (e >= n) continue;
-                const long long c = e / (2 * ft), r = e - c * 2 * ft;
-                y[(2 * c + (r & 1)) * ft + r / 2] = o[j];
+                const unsigned c = cdiv.div(e), r = e - c * ft2;
+                store_stream(y + (2 * c + (r & 1)) * ft + r / 2, o[j]);
             }
         }
     }
+}
+
+// One launch of moments + normalise for NORM_CAC / NORM_FLAT: x is n floats (CAC: the complex64
+// spectrum [C][ft] read as 2 C ft floats), VEC float4 per thread in chunks of kGridThreads * 4 *
+// VEC floats. Same statistics formulas as moments_final_kernel and the same per-element division
+// as normalize_kernel; block 0 writes {mean, sd} to stats.
+template <int KIND, int VEC>
+__global__ __launch_bounds__(kGridThreads) void norm_fused_kernel(const float* x, float* y, unsigned n, unsigned ft,
+                                                                  FastDiv cdiv, double* stats, GridSync f) {
+    __shared__ double red[2 * kGridThreads / 64];
+    __shared__ double tot[2];
+    constexpr unsigned CH = kGridThreads * 4 * VEC;
+    const bool vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && n % 4 == 0;
+    if (vec && blockIdx.x * CH + CH <= n)
+        norm_fused_body<KIND, VEC, true>(x, y, n, ft, cdiv, vec, stats, f, red, tot);
+    else
+        norm_fused_body<KIND, VEC, false>(x, y, n, ft, cdiv, vec, stats, f, red, tot);
 }
 
 // Spectral branch denormalise: ox [S][2C][FT] -> complex64 spec [S][C][FT]; blockIdx.y = s * C + c.
@@ -562,8 +577,9 @@ bool try_norm_fused(const float* x, float* y, long long n, long long ft, double*
     // up re-reads all of x): y must not overlap x (y has as many floats as x).
     if (overlaps(x, sizeof(float) * (size_t)n, y, sizeof(float) * (size_t)n)) return false;
     if (nch > resident_blocks(reinterpret_cast<const void*>(&norm_fused_kernel<NK, VEC>), s)) return false;
-    hipLaunchKernelGGL((norm_fused_kernel<NK, VEC>), dim3((unsigned)nch), dim3(kGridThreads), 0, s, x, y, n, ft, stats,
-                       grid_sync_at(ws));
+    // n <= kGridMaxBlocks chunks of at most 8192 floats: every index fits 32 bits.
+    hipLaunchKernelGGL((norm_fused_kernel<NK, VEC>), dim3((unsigned)nch), dim3(kGridThreads), 0, s, x, y, (unsigned)n,
+                       (unsigned)ft, FastDiv((unsigned)(2 * ft)), stats, grid_sync_at(ws));
     launch_check("norm_fused_kernel");
     return true;
 }

@@ -57,6 +57,19 @@ def test_cac_normalize_c1(device, htd):
     assert rel_err(host(mag), htd.cac_normalize(sh, *want_stats)) <= 1e-6
 
 
+@pytest.mark.parametrize("C,F,T", [(2, 33, 77), (2, 64, 51), (3, 2049, 5), (1, 7, 3)])
+def test_cac_normalize_ragged(device, htd, C, F, T):
+    """Spectra whose float count is not a multiple of a block's chunk, with an odd bins x frames
+    product (each float placed on its own) and an even one (re/im pairs)."""
+    import torch
+    z = synth.normal(C * F + T, (C, F, T, 2), 1.0) * 3 + 0.5
+    sh = (z[..., 0] + 1j * z[..., 1]).astype(np.complex64)
+    mag, stats = stx.htdemucs_cac_normalize(torch.from_numpy(sh).to(device))
+    st = host(stats)
+    assert close_stats(st, htd.mean_std(htd.cac_pack(sh)))
+    assert np.array_equal(host(mag), htd.cac_normalize(sh, st[0], st[1]))
+
+
 def test_wave_normalize_c1(device, htd):
     xh = synth.normal(2, (2, SEG), 0.1) + 0.003
     y, stats = stx.htdemucs_wave_normalize(dev(xh, device))
