@@ -160,6 +160,8 @@ __device__ __forceinline__ float lane_max(float v) {
 // read back. Measured on outputs of tens of MB written once (the band gather's features): the
 // cold call is ~20 % faster, since the written lines no longer displace dirty lines of earlier
 // work from the caches; when the same buffers are rewritten while still cached it costs ~2 %.
+// Not for stores of short runs that other workgroups complete to whole lines (the F-major STFT
+// rows): those must meet in L2 first, and streamed they cost 1.4-2.4x.
 typedef float stx_v2f __attribute__((ext_vector_type(2)));
 typedef float stx_v4f __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void store_stream(float* p, float v) { __builtin_nontemporal_store(v, p); }

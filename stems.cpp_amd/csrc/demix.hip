@@ -96,11 +96,11 @@ __global__ __launch_bounds__(256) void demix_chunks_kernel(DemixArgs a, const fl
         const int t0 = ((int)blockIdx.x * kChunkGroups + g) * 1024 + (int)threadIdx.x * 4;
         if (t0 >= a.chunk) break;
         if ((vec & 1) && t0 + 3 < a.chunk) {
-            *reinterpret_cast<float4*>(dst + t0) = make_float4(v[g][0], v[g][1], v[g][2], v[g][3]);
+            store_stream(reinterpret_cast<float4*>(dst + t0), make_float4(v[g][0], v[g][1], v[g][2], v[g][3]));
         } else {
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                if (t0 + j < a.chunk) dst[t0 + j] = v[g][j];
+                if (t0 + j < a.chunk) store_stream(dst + t0 + j, v[g][j]);
         }
     }
 }
@@ -213,11 +213,11 @@ __global__ __launch_bounds__(256) void demix_ola_kernel(DemixArgs a, const float
         }
         float* dst = out + (size_t)sc * a.len + t0;
         if (vec && t0 + 3 < a.len) {
-            *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+            store_stream(reinterpret_cast<float4*>(dst), make_float4(o[0], o[1], o[2], o[3]));
         } else {
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                if (t0 + j < a.len) dst[j] = o[j];
+                if (t0 + j < a.len) store_stream(dst + j, o[j]);
         }
     }
 }

@@ -379,11 +379,11 @@ __global__ __launch_bounds__(256) void segments_kernel(SegArgs a) {
     }
     float* dst = a.parts + ((long long)k * a.C + c) * a.seg + i0;
     if (V4) {
-        *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+        store_stream(reinterpret_cast<float4*>(dst), make_float4(v[0], v[1], v[2], v[3]));
     } else {
 #pragma unroll
         for (int q = 0; q < 4; q++)
-            if (i0 + q < a.seg) dst[q] = v[q];
+            if (i0 + q < a.seg) store_stream(dst + q, v[q]);
     }
 }
 
@@ -451,7 +451,7 @@ __global__ __launch_bounds__(256) void split_ola_kernel(OlaArgs a) {
                     acc = acc + prod;
                 }
             }
-            a.out[(long long)(sc0 + t) * a.length + i] = acc / sw;
+            store_stream(a.out + (long long)(sc0 + t) * a.length + i, acc / sw);
         }
     }
 }

@@ -72,11 +72,11 @@ __global__ __launch_bounds__(256) void uvr_chunks_kernel(UvrArgs a, const float*
     }
     float* dst = parts + ((size_t)blockIdx.z * a.channels + c) * a.chunk + t0;
     if (vec && t0 + 3 < a.chunk) {
-        *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+        store_stream(reinterpret_cast<float4*>(dst), make_float4(v[0], v[1], v[2], v[3]));
     } else {
 #pragma unroll
         for (int j = 0; j < 4; j++)
-            if (t0 + j < a.chunk) dst[j] = v[j];
+            if (t0 + j < a.chunk) store_stream(dst + j, v[j]);
     }
 }
 
@@ -157,7 +157,7 @@ __global__ __launch_bounds__(256) void uvr_ola_kernel(UvrArgs a, const float* __
                 res = res + (in[e][j] ? prod : 0.0);
             }
             const double q = div != 0.0 ? div_rn(res, div, rdiv) : res / div;
-            if (t < len && q0 + u < planes) out[(size_t)(q0 + u) * a.len + t] = (float)q;
+            if (t < len && q0 + u < planes) store_stream(out + (size_t)(q0 + u) * a.len + t, (float)q);
         }
     }
 }
