@@ -496,7 +496,7 @@ __global__ __launch_bounds__(256) void band_rms_norm_kernel(BandNormArgs a) {
 #pragma unroll
     for (int k = 0; k < V; k++) {
         const int q = lane + (k << lg);
-        if (k < nk && q < d) y[q] = make_float2((v[k].x * scale) * gv[k].x, (v[k].y * scale) * gv[k].y);
+        if (k < nk && q < d) store_stream(y + q, make_float2((v[k].x * scale) * gv[k].x, (v[k].y * scale) * gv[k].y));
     }
 }
 
@@ -576,7 +576,7 @@ __global__ __launch_bounds__(256) void band_mask_glu_kernel(BandGluArgs a) {
 #pragma unroll
     for (int k = 0; k < kGluPer; k++) {
         const int e = e0 + 256 * k;
-        if (e < n) out[e] = make_float2(glu_gate(h0[k].x, h1[k].x), glu_gate(h0[k].y, h1[k].y));
+        if (e < n) store_stream(out + e, make_float2(glu_gate(h0[k].x, h1[k].x), glu_gate(h0[k].y, h1[k].y)));
     }
 }
 

@@ -131,8 +131,8 @@ __global__ __launch_bounds__(256) void qkv_rope_split_kernel(QkvArgs a) {
         for (int p = 0; p < P; p++) {
             const int n = n0 + rr + RPP * p;
             if (ok[p]) {
-                *reinterpret_cast<float4*>(qo + (long long)n * DH) = rotate_pairs(xq[p], c0[p], s0[p], c1[p], s1[p]);
-                *reinterpret_cast<float4*>(ko + (long long)n * DH) = rotate_pairs(xk[p], c0[p], s0[p], c1[p], s1[p]);
+                store_stream(reinterpret_cast<float4*>(qo + (long long)n * DH), rotate_pairs(xq[p], c0[p], s0[p], c1[p], s1[p]));
+                store_stream(reinterpret_cast<float4*>(ko + (long long)n * DH), rotate_pairs(xk[p], c0[p], s0[p], c1[p], s1[p]));
             }
             tile[buf][4 * q4 + 0][rr + RPP * p] = xv[p].x;
             tile[buf][4 * q4 + 1][rr + RPP * p] = xv[p].y;
@@ -145,7 +145,7 @@ __global__ __launch_bounds__(256) void qkv_rope_split_kernel(QkvArgs a) {
 #pragma unroll
             for (int j = 0; j < DH / 4; j++) {
                 const int d = dd + 4 * j;
-                vo[(long long)d * N] = tile[buf][d][nn];
+                store_stream(vo + (long long)d * N, tile[buf][d][nn]);
             }
         }
         if (NBUF == 1) __syncthreads();
@@ -217,7 +217,7 @@ __global__ __launch_bounds__(256) void permute_rows_kernel(RowPermArgs a) {
                 o *= g[u];
             }
         }
-        *reinterpret_cast<U*>(a.dst + doff[u]) = o;
+        store_stream(reinterpret_cast<U*>(a.dst + doff[u]), o);
     }
 }
 
@@ -269,7 +269,7 @@ __global__ __launch_bounds__(256) void transpose_kernel(TransArgs a) {
 #pragma unroll
         for (int j = 0; j < kTile / 4; j++) {
             const int oa = a0 + w + 4 * j;
-            if (oa < a.na) *reinterpret_cast<float*>(d + oa * a.da + (long long)ob * 4) = tile[lane][w + 4 * j];
+            if (oa < a.na) store_stream(reinterpret_cast<float*>(d + oa * a.da + (long long)ob * 4), tile[lane][w + 4 * j]);
         }
     }
 }
@@ -327,7 +327,7 @@ __global__ __launch_bounds__(256) void concat_kernel(ConcatArgs a) {
 #pragma unroll
     for (int u = 0; u < kConcatUnits; u++) {
         if (e0 + 256u * u >= s.count) break;
-        *reinterpret_cast<U*>(a.dst + doff[u]) = v[u];
+        store_stream(reinterpret_cast<U*>(a.dst + doff[u]), v[u]);
     }
 }
 

@@ -443,10 +443,10 @@ __global__ __launch_bounds__(256) void row_norm_v4_kernel(RowNormArgs a) {
 #pragma unroll
                     for (int j = 0; j < 4; j++) o[j] = norm_out(a, v[4 * k + j], mean, scale, i0 + j);
                 }
-                yb[q] = make_float4(o[0], o[1], o[2], o[3]);
+                store_stream(yb + q, make_float4(o[0], o[1], o[2], o[3]));
             }
         }
-        if (ei >= 0) y[ei] = norm_out(a, e, mean, scale, ei);
+        if (ei >= 0) store_stream(y + ei, norm_out(a, e, mean, scale, ei));
     }
 }
 
@@ -493,10 +493,10 @@ __global__ __launch_bounds__(256) void softmax_v4_kernel(SoftmaxArgs a) {
         for (int k = 0; k < V4; k++) {
             const int q = lane + LANES * k;
             if (q < sp.nb4)
-                yb[q] = make_float4((float)((double)v[4 * k] * inv), (float)((double)v[4 * k + 1] * inv),
-                                    (float)((double)v[4 * k + 2] * inv), (float)((double)v[4 * k + 3] * inv));
+                store_stream(yb + q, make_float4((float)((double)v[4 * k] * inv), (float)((double)v[4 * k + 1] * inv),
+                                                 (float)((double)v[4 * k + 2] * inv), (float)((double)v[4 * k + 3] * inv)));
         }
-        if (ei >= 0) y[ei] = (float)((double)e * inv);
+        if (ei >= 0) store_stream(y + ei, (float)((double)e * inv));
     }
 }
 
@@ -1218,7 +1218,7 @@ __global__ __launch_bounds__(256) void rope_v4_kernel(RopeArgs a) {
             o.z = (float)((double)v.z * c1 - (double)v.w * s1);
             o.w = (float)((double)v.z * s1 + (double)v.w * c1);
         }
-        reinterpret_cast<float4*>(ys + i1 * a.dst.nb[1] + i3 * a.dst.nb[3])[q] = o;
+        store_stream(reinterpret_cast<float4*>(ys + i1 * a.dst.nb[1] + i3 * a.dst.nb[3]) + q, o);
     }
 }
 
