@@ -277,7 +277,7 @@ __global__ __launch_bounds__(256) void shift_accumulate_kernel(const float* __re
 __global__ __launch_bounds__(256) void complement_kernel(const float* __restrict__ mix, const float* __restrict__ est0,
                                                          int64_t n, float* __restrict__ out) {
     for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256)
-        out[e] = mix[e] - est0[e];
+        store_stream(out + e, mix[e] - est0[e]);
 }
 
 unsigned grid_for(int64_t n) { return (unsigned)std::min<int64_t>((n + 255) / 256, 1 << 20); }

@@ -335,7 +335,7 @@ __global__ __launch_bounds__(256) void cac_denorm_kernel(const float* ox, float2
 #pragma unroll
     for (int k = 0; k < kNormPer; k++) {
         const long long e = e0 + 256LL * k;
-        if (e < ft) out[e] = make_float2((float)((double)vr[k] * sd + mean), (float)((double)vi[k] * sd + mean));
+        if (e < ft) store_stream(out + e, make_float2((float)((double)vr[k] * sd + mean), (float)((double)vi[k] * sd + mean)));
     }
 }
 
@@ -347,7 +347,7 @@ __global__ __launch_bounds__(256) void time_add_kernel(const float* t, const flo
     if (e >= n) return;
     const double mean = stats[0], sd = stats[1];
     const float a = (float)((double)t[e] * sd + mean);
-    out[e] = a + y[e];
+    store_stream(out + e, a + y[e]);
 }
 
 // ------------------------------------------------------------------------------- split

@@ -78,7 +78,7 @@ __global__ __launch_bounds__(256) void resample_kernel(ResampleArgs a) {
     }
 #pragma unroll
     for (int k = 0; k < MC; k++)
-        if (k < C) a.out[(size_t)k * a.out_n + i] = (float)acc[k];
+        if (k < C) store_stream(a.out + (size_t)k * a.out_n + i, (float)acc[k]);
 }
 
 __global__ __launch_bounds__(256) void copy_kernel(const float* __restrict__ in, float* __restrict__ out, size_t n) {

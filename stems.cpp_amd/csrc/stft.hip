@@ -294,7 +294,7 @@ __global__ __launch_bounds__(256) void istft_ola_kernel(IstftArgs a, int N) {
         }
         y = env > 1e-11f ? sum / env : 0.f;
     }
-    a.out[(size_t)c * a.out_len + i] = y;
+    store_stream(a.out + (size_t)c * a.out_len + i, y);
 }
 
 // Fused path: one workgroup owns a tile of output samples and inverse-transforms, JOBS frames
@@ -541,7 +541,7 @@ __global__ __launch_bounds__(kMixedThreads) void stft_mixed_kernel(StftArgs a, M
         const float orr = zk.y + zm.y, oi = zm.x - zk.x;
         const float2 val = make_float2((er + w.x * orr - w.y * oi) * hs, (ei + w.x * oi + w.y * orr) * hs);
         if (a.layout == STX_SPEC_F_MAJOR) a.spec[((size_t)c * a.F + k) * a.T + t] = val;
-        else a.spec[((size_t)c * a.T + t) * a.F + k] = val;
+        else store_stream(a.spec + ((size_t)c * a.T + t) * a.F + k, val);
     }
 }
 
