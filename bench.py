@@ -18,7 +18,8 @@ config.bytes_moved_per_step gives the minimum these kernels move (24 per element
 that over the same step time (the bytes the kernels really move), warm the same step replayed on
 one buffer set that stays in the Infinity Cache.
 roofline: the op with the largest share of the step (GroupNorm+GELU): its algorithmic bytes
-(8 per element) / its duration (gn_fused_kernel, one grid-synchronised pass), from a graph of instances
+(8 per element) / its duration (gn_fused_kernel, one grid-synchronised pass, at C = 96, 192, 384;
+gn_partial_kernel + gn_apply_kernel at C = 48), from a graph of instances
 of that op on more than 512 MB of distinct buffers (cold, like the step) replayed between two
 HIP events on the stream the kernels run on. traffic: HBM bytes of that op
 per step measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter
@@ -243,7 +244,8 @@ def run_ops(args, torch, stx, dev):
     dom_bytes = sum(nbytes[dom])
     achieved = dom_bytes / (share[dom] * 1e-6) / 1e9
     step_bytes = sum(sum(v) for v in op_bytes().values())
-    kernel_names = {"gn": "group_norm+affine+gelu (gn_fused_kernel<channel,gelu>: one grid-synchronised pass)",
+    kernel_names = {"gn": "group_norm+affine+gelu (gn_fused_kernel<channel,gelu>, one grid-synchronised pass, at "
+                          "C = 96, 192, 384; gn_partial_kernel + gn_apply_kernel at C = 48)",
                     "glu_scale_residual": "glu + layer scale + residual (ew_flat_kernel<GLU_MUL_ADD>)"}
     moved = sum(sum(v) for v in moved_bytes().values())
     res = {
