@@ -526,6 +526,8 @@ __global__ __launch_bounds__(kMixedThreads) void stft_mixed_kernel(StftArgs a, M
     const int c = f / a.T, t = f - c * a.T;
     const float* xc = a.x + (size_t)c * a.len;
     const int m0 = a.frame0 + t * a.hop;
+    // (Loads batched into registers before the LDS writes, as the iSTFT does, measured no
+    // faster here: the passes' twiddle round trips dominate.)
     for (int i = tid; i < M; i += kMixedThreads) {
         const float x0 = xc[padded_index_rt(m0 + 2 * i, a, n)], x1 = xc[padded_index_rt(m0 + 2 * i + 1, a, n)];
         b0[mixed_pad(i)] = make_float2(x0 * a.win[2 * i], x1 * a.win[2 * i + 1]);
@@ -555,19 +557,37 @@ __global__ __launch_bounds__(kMixedThreads) void istft_frames_mixed_kernel(Istft
     if (f >= jobs) return;                             // whole block idle: no barrier reached
     const int c = f / a.T, st = f - c * a.T;
     const float2* sc = a.spec + (size_t)c * a.T * a.F;
-    for (int k = tid; k < M; k += kMixedThreads) {
-        const float2 xk = spec_bin(a, sc, st, k);
-        float2 xm = spec_bin(a, sc, st, min(M - k, a.F - 1));
-        if (k == 0 && !a.keep_nyquist) xm = make_float2(0.f, 0.f);
-        b0[mixed_pad(k)] = inverse_split_w(xk, xm, k, a.keep_nyquist, twn[k]);
+    // Every spectrum and twiddle load (clamped to valid bins) before the first LDS write.
+    constexpr int RL = (MAXM + kMixedThreads - 1) / kMixedThreads;
+    float2 xk[RL], xm[RL], tw[RL];
+#pragma unroll
+    for (int q = 0; q < RL; q++) {
+        const int k = min(tid + q * kMixedThreads, M - 1);
+        xk[q] = spec_bin(a, sc, st, k);
+        xm[q] = spec_bin(a, sc, st, min(M - k, a.F - 1));
+        tw[q] = twn[k];
+    }
+#pragma unroll
+    for (int q = 0; q < RL; q++) {
+        const int k = tid + q * kMixedThreads;
+        if (k >= M) break;
+        const float2 m = k == 0 && !a.keep_nyquist ? make_float2(0.f, 0.f) : xm[q];
+        b0[mixed_pad(k)] = inverse_split_w(xk[q], m, k, a.keep_nyquist, tw[q]);
     }
     __syncthreads();
     const float2* r = mixed_fft<MAXM, kMixedThreads>(b0, b1, M, p, 2, twn, tid);
     float* dst = a.frames + (size_t)f * n;
-    for (int i = tid; i < M; i += kMixedThreads) {     // windowed as WindowPost
+    const float2* win2 = reinterpret_cast<const float2*>(a.win);
+    float2 wv[RL];
+#pragma unroll
+    for (int q = 0; q < RL; q++) wv[q] = win2[min(tid + q * kMixedThreads, M - 1)];
+#pragma unroll
+    for (int q = 0; q < RL; q++) {                     // windowed as WindowPost
+        const int i = tid + q * kMixedThreads;
+        if (i >= M) break;
         const float2 ri = r[mixed_pad(i)];
-        dst[2 * i] = ri.x * a.win[2 * i] * a.norm;
-        dst[2 * i + 1] = -ri.y * a.win[2 * i + 1] * a.norm;
+        dst[2 * i] = ri.x * wv[q].x * a.norm;
+        dst[2 * i + 1] = -ri.y * wv[q].y * a.norm;
     }
 }
 
@@ -577,7 +597,13 @@ __global__ __launch_bounds__(kMixedThreads) void fft_mixed_kernel(float2* data, 
     __shared__ float2 b0[mixed_padded(MAXM)], b1[mixed_padded(MAXM)];
     const int tid = (int)threadIdx.x;
     float2* d = data + (size_t)blockIdx.x * n;
-    for (int i = tid; i < n; i += kMixedThreads) b0[mixed_pad(i)] = inverse ? cconj(d[i]) : d[i];
+    constexpr int RL = (MAXM + kMixedThreads - 1) / kMixedThreads;
+    float2 v[RL];
+#pragma unroll
+    for (int q = 0; q < RL; q++) v[q] = d[min(tid + q * kMixedThreads, n - 1)];   // every load first
+#pragma unroll
+    for (int q = 0; q < RL; q++)
+        if (tid + q * kMixedThreads < n) b0[mixed_pad(tid + q * kMixedThreads)] = inverse ? cconj(v[q]) : v[q];
     __syncthreads();
     const float2* r = mixed_fft<MAXM, kMixedThreads>(b0, b1, n, p, 1, twn, tid);
     for (int i = tid; i < n; i += kMixedThreads) d[i] = inverse ? cconj(r[mixed_pad(i)]) : r[mixed_pad(i)];
