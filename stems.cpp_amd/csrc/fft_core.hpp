@@ -350,18 +350,29 @@ inline bool mixed_plan(int m, MixedRadix& p) {
 __host__ __device__ constexpr int mixed_pad(int i) { return i + (i >> 4); }
 __host__ __device__ constexpr int mixed_padded(int m) { return m + m / 16 + 1; }
 
+// Twiddles of the mixed-radix passes: a two-level table of W_n^m staged in LDS, lo[j] = W_n^j
+// for j < kMixedTwL, then hi[h] = W_n^(h kMixedTwL) for h < ceil(n / kMixedTwL), every entry
+// computed in double and rounded once; W_n^m = lo[m mod kMixedTwL] * hi[m / kMixedTwL]. Two LDS
+// reads and a complex product per twiddle instead of a global load per pass (a memory round trip
+// on every pass's critical path). n <= 16384.
+constexpr int kMixedTwL = 128;
+constexpr int kMixedTwMax = kMixedTwL + 16384 / kMixedTwL;
+__device__ __forceinline__ float2 mixed_tw(const float2* twl, int m) {
+    return cmul(twl[m & (kMixedTwL - 1)], twl[kMixedTwL + (m >> 7)]);
+}
+static_assert(kMixedTwL == 128, "mixed_tw shifts by log2(kMixedTwL)");
+
 // One out-of-place Stockham pass of radix R after sub-transforms of length Ns over an M-point
 // transform held in src (natural order, padded layout), by the NT threads of a workgroup:
 // butterfly b reads src[b + r M/R], multiplies element r by W_{Ns R}^{(b mod Ns) r} =
-// twn[(b mod Ns) r scale] (twn: W_n^m, scale = n / (Ns R); all ones when Ns = 1), takes an
-// R-point DFT and writes dst[(b / Ns) Ns R + b mod Ns + r Ns]. A thread takes butterflies
-// tid + i NT in batches of IT whose LDS reads and twiddle loads are all issued before the first
-// is used (clamped to a valid butterfly; the extra ones are not written), so a pass costs one
-// twiddle round trip per batch rather than one per butterfly. b / Ns is umulhi(b, inv) with
-// inv = ceil(2^32 / Ns), exact for b, Ns < 2^18.
+// W_n^{(b mod Ns) r scale} (from the LDS table twl, see mixed_tw; scale = n / (Ns R); all ones
+// when Ns = 1), takes an R-point DFT and writes dst[(b / Ns) Ns R + b mod Ns + r Ns]. A thread
+// takes butterflies tid + i NT in batches of IT whose LDS reads are all issued before the first
+// is used (clamped to a valid butterfly; the extra ones are not written). b / Ns is
+// umulhi(b, inv) with inv = ceil(2^32 / Ns), exact for b, Ns < 2^18.
 template <int R, int IT, int NT>
 __device__ __forceinline__ void mixed_pass(const float2* src, float2* dst, int M, int Ns, int scale,
-                                           const float2* __restrict__ twn, int tid) {
+                                           const float2* twl, int tid) {
     const int B = M / R;
     const unsigned inv = Ns > 1 ? 0xffffffffu / (unsigned)Ns + 1u : 0u;
     for (int b0 = tid; b0 < B; b0 += IT * NT) {
@@ -375,7 +386,7 @@ __device__ __forceinline__ void mixed_pass(const float2* src, float2* dst, int M
             for (int r = 0; r < R; r++) v[it][r] = src[mixed_pad(b + r * B)];
             if (Ns > 1) {
 #pragma unroll
-                for (int r = 1; r < R; r++) v[it][r] = cmul(v[it][r], twn[k * r * scale]);
+                for (int r = 1; r < R; r++) v[it][r] = cmul(v[it][r], mixed_tw(twl, k * r * scale));
             }
             base[it] = blk * Ns * R + k;
         }
@@ -400,11 +411,11 @@ constexpr int mixed_batch() {
 
 // All passes of plan p over the M-point transform (M <= MAXM) in buf0 (buf1: scratch; both
 // padded, see mixed_pad) by NT threads; returns the buffer holding the result. Every thread of
-// the workgroup must call it (it has barriers). twn holds W_n^m for m < n with n a multiple of
-// M (tw_mul = n / M).
+// the workgroup must call it (it has barriers), after the LDS table twl (mixed_tw) of W_n^m, with
+// n a multiple of M (tw_mul = n / M), has been published by a barrier.
 template <int MAXM, int NT>
 __device__ __forceinline__ float2* mixed_fft(float2* buf0, float2* buf1, int M, const MixedRadix& p, int tw_mul,
-                                             const float2* __restrict__ twn, int tid) {
+                                             const float2* twl, int tid) {
     float2* src = buf0;
     float2* dst = buf1;
     int Ns = 1;
@@ -412,12 +423,12 @@ __device__ __forceinline__ float2* mixed_fft(float2* buf0, float2* buf1, int M, 
         const int R = p.r[i];
         const int scale = (M / (Ns * R)) * tw_mul;
         switch (R) {
-            case 16: mixed_pass<16, mixed_batch<16, MAXM, NT>(), NT>(src, dst, M, Ns, scale, twn, tid); break;
-            case 8: mixed_pass<8, mixed_batch<8, MAXM, NT>(), NT>(src, dst, M, Ns, scale, twn, tid); break;
-            case 4: mixed_pass<4, mixed_batch<4, MAXM, NT>(), NT>(src, dst, M, Ns, scale, twn, tid); break;
-            case 2: mixed_pass<2, mixed_batch<2, MAXM, NT>(), NT>(src, dst, M, Ns, scale, twn, tid); break;
-            case 3: mixed_pass<3, mixed_batch<3, MAXM, NT>(), NT>(src, dst, M, Ns, scale, twn, tid); break;
-            default: mixed_pass<5, mixed_batch<5, MAXM, NT>(), NT>(src, dst, M, Ns, scale, twn, tid); break;
+            case 16: mixed_pass<16, mixed_batch<16, MAXM, NT>(), NT>(src, dst, M, Ns, scale, twl, tid); break;
+            case 8: mixed_pass<8, mixed_batch<8, MAXM, NT>(), NT>(src, dst, M, Ns, scale, twl, tid); break;
+            case 4: mixed_pass<4, mixed_batch<4, MAXM, NT>(), NT>(src, dst, M, Ns, scale, twl, tid); break;
+            case 2: mixed_pass<2, mixed_batch<2, MAXM, NT>(), NT>(src, dst, M, Ns, scale, twl, tid); break;
+            case 3: mixed_pass<3, mixed_batch<3, MAXM, NT>(), NT>(src, dst, M, Ns, scale, twl, tid); break;
+            default: mixed_pass<5, mixed_batch<5, MAXM, NT>(), NT>(src, dst, M, Ns, scale, twl, tid); break;
         }
         __syncthreads();
         float2* t = src;

@@ -36,6 +36,7 @@ struct stx_fft {
     float* win = nullptr;    // device [n]: periodic Hann
     int mixed = 0;           // n = 2^a 3^b 5^c, not a power of two: the mixed-radix kernels
     float2* twn = nullptr;   // mixed: device [n], W_n^m
+    float2* twm = nullptr;   // mixed: device [kMixedTwMax], the passes' two-level table (fft_core.hpp)
     stx::MixedRadix half;    // mixed: plan of the n/2-point transform of real frames
     stx::MixedRadix full;    // mixed: plan of the n-point complex transform
     // Powers of two without STFT kernels (stx_fft_run only): 2, 4, 8 are register transforms;
@@ -518,22 +519,25 @@ __device__ __forceinline__ int padded_index_rt(int m, const StftArgs& a, int n) 
 
 template <int MAXM>
 __global__ __launch_bounds__(kMixedThreads) void stft_mixed_kernel(StftArgs a, MixedRadix p,
-                                                                   const float2* __restrict__ twn, int n) {
+                                                                   const float2* __restrict__ twn,
+                                                                   const float2* __restrict__ twm, int n) {
     __shared__ float2 b0[mixed_padded(MAXM)], b1[mixed_padded(MAXM)];
+    __shared__ float2 twl[kMixedTwMax];
     const int M = n / 2, tid = (int)threadIdx.x;
     const int f = xcd_block();                         // channel * T + frame
     if (f >= a.jobs) return;                           // whole block idle: no barrier reached
+    Staged<kMixedTwMax, kMixedThreads, float2> tws;
+    tws.load(twm, tid);
     const int c = f / a.T, t = f - c * a.T;
     const float* xc = a.x + (size_t)c * a.len;
     const int m0 = a.frame0 + t * a.hop;
-    // (Loads batched into registers before the LDS writes, as the iSTFT does, measured no
-    // faster here: the passes' twiddle round trips dominate.)
     for (int i = tid; i < M; i += kMixedThreads) {
         const float x0 = xc[padded_index_rt(m0 + 2 * i, a, n)], x1 = xc[padded_index_rt(m0 + 2 * i + 1, a, n)];
         b0[mixed_pad(i)] = make_float2(x0 * a.win[2 * i], x1 * a.win[2 * i + 1]);
     }
+    tws.store(twl, tid);
     __syncthreads();
-    const float2* z = mixed_fft<MAXM, kMixedThreads>(b0, b1, M, p, 2, twn, tid);
+    const float2* z = mixed_fft<MAXM, kMixedThreads>(b0, b1, M, p, 2, twl, tid);
     // X[k] = E[k] + W_n^k O[k], k <= n/2, as in stft_kernel.
     const float hs = 0.5f * a.scale;
     for (int k = tid; k < a.F; k += kMixedThreads) {
@@ -549,12 +553,16 @@ __global__ __launch_bounds__(kMixedThreads) void stft_mixed_kernel(StftArgs a, M
 
 template <int MAXM>
 __global__ __launch_bounds__(kMixedThreads) void istft_frames_mixed_kernel(IstftArgs a, MixedRadix p,
-                                                                           const float2* __restrict__ twn, int n,
+                                                                           const float2* __restrict__ twn,
+                                                                           const float2* __restrict__ twm, int n,
                                                                            int jobs) {
     __shared__ float2 b0[mixed_padded(MAXM)], b1[mixed_padded(MAXM)];
+    __shared__ float2 twl[kMixedTwMax];
     const int M = n / 2, tid = (int)threadIdx.x;
     const int f = xcd_block();                         // channel * T + frame
     if (f >= jobs) return;                             // whole block idle: no barrier reached
+    Staged<kMixedTwMax, kMixedThreads, float2> tws;
+    tws.load(twm, tid);
     const int c = f / a.T, st = f - c * a.T;
     const float2* sc = a.spec + (size_t)c * a.T * a.F;
     // Every spectrum and twiddle load (clamped to valid bins) before the first LDS write.
@@ -574,8 +582,9 @@ __global__ __launch_bounds__(kMixedThreads) void istft_frames_mixed_kernel(Istft
         const float2 m = k == 0 && !a.keep_nyquist ? make_float2(0.f, 0.f) : xm[q];
         b0[mixed_pad(k)] = inverse_split_w(xk[q], m, k, a.keep_nyquist, tw[q]);
     }
+    tws.store(twl, tid);
     __syncthreads();
-    const float2* r = mixed_fft<MAXM, kMixedThreads>(b0, b1, M, p, 2, twn, tid);
+    const float2* r = mixed_fft<MAXM, kMixedThreads>(b0, b1, M, p, 2, twl, tid);
     float* dst = a.frames + (size_t)f * n;
     const float2* win2 = reinterpret_cast<const float2*>(a.win);
     float2 wv[RL];
@@ -593,9 +602,12 @@ __global__ __launch_bounds__(kMixedThreads) void istft_frames_mixed_kernel(Istft
 
 template <int MAXM>
 __global__ __launch_bounds__(kMixedThreads) void fft_mixed_kernel(float2* data, int inverse, MixedRadix p,
-                                                                  const float2* __restrict__ twn, int n) {
+                                                                  const float2* __restrict__ twm, int n) {
     __shared__ float2 b0[mixed_padded(MAXM)], b1[mixed_padded(MAXM)];
+    __shared__ float2 twl[kMixedTwMax];
     const int tid = (int)threadIdx.x;
+    Staged<kMixedTwMax, kMixedThreads, float2> tws;
+    tws.load(twm, tid);
     float2* d = data + (size_t)blockIdx.x * n;
     constexpr int RL = (MAXM + kMixedThreads - 1) / kMixedThreads;
     float2 v[RL];
@@ -604,8 +616,9 @@ __global__ __launch_bounds__(kMixedThreads) void fft_mixed_kernel(float2* data, 
 #pragma unroll
     for (int q = 0; q < RL; q++)
         if (tid + q * kMixedThreads < n) b0[mixed_pad(tid + q * kMixedThreads)] = inverse ? cconj(v[q]) : v[q];
+    tws.store(twl, tid);
     __syncthreads();
-    const float2* r = mixed_fft<MAXM, kMixedThreads>(b0, b1, n, p, 1, twn, tid);
+    const float2* r = mixed_fft<MAXM, kMixedThreads>(b0, b1, n, p, 1, twl, tid);
     for (int i = tid; i < n; i += kMixedThreads) d[i] = inverse ? cconj(r[mixed_pad(i)]) : r[mixed_pad(i)];
 }
 
@@ -846,13 +859,13 @@ void run_istft(const stx_fft* f, IstftArgs a, int channels, void* workspace, siz
         const unsigned grid = (unsigned)((jobs + kXcds - 1) / kXcds * kXcds);   // xcd_block's multiple
         if (f->n / 2 <= 1024)
             hipLaunchKernelGGL(istft_frames_mixed_kernel<1024>, dim3(grid), dim3(kMixedThreads), 0, s, a, f->half,
-                               f->twn, f->n, jobs);
+                               f->twn, f->twm, f->n, jobs);
         else if (f->n / 2 <= 4096)
             hipLaunchKernelGGL(istft_frames_mixed_kernel<4096>, dim3(grid), dim3(kMixedThreads), 0, s, a, f->half,
-                               f->twn, f->n, jobs);
+                               f->twn, f->twm, f->n, jobs);
         else
             hipLaunchKernelGGL(istft_frames_mixed_kernel<8192>, dim3(grid), dim3(kMixedThreads), 0, s, a, f->half,
-                               f->twn, f->n, jobs);
+                               f->twn, f->twm, f->n, jobs);
         launch_check("istft_frames_mixed_kernel");
         hipLaunchKernelGGL(istft_ola_kernel, dim3((a.out_len + 255) / 256, channels), dim3(256), 0, s, a, f->n);
         launch_check("istft_ola_kernel");
@@ -1022,6 +1035,10 @@ STX_API stx_status stx_fft_create_any(int n, stx_fft** out) {
             const double th = 2.0 * M_PI * (double)m / n;
             twn[m] = make_float2((float)std::cos(th), (float)-std::sin(th));
         }
+        // The passes' two-level table: W_n^j for j < kMixedTwL, then W_n^(h kMixedTwL).
+        std::vector<float2> twm(kMixedTwMax, make_float2(0.f, 0.f));
+        for (int j = 0; j < kMixedTwL; j++) twm[j] = twn[j % n];
+        for (int h = 0; h * kMixedTwL < n; h++) twm[kMixedTwL + h] = twn[h * kMixedTwL];
         std::vector<float> win(n);
         for (int m = 0; m < n; m++) win[m] = (float)(0.5 - 0.5 * std::cos(2.0 * M_PI * m / n));   // hann_periodic (src/stft.h:70-74)
         stx_fft* f = new stx_fft;
@@ -1033,6 +1050,8 @@ STX_API stx_status stx_fft_create_any(int n, stx_fft** out) {
         if (e == hipSuccess) e = hipMalloc(&f->twn, sizeof(float2) * n);
         if (e == hipSuccess) e = hipMalloc(&f->win, sizeof(float) * n);
         if (e == hipSuccess) e = hipMemcpy(f->twn, twn.data(), sizeof(float2) * n, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMalloc(&f->twm, sizeof(float2) * twm.size());
+        if (e == hipSuccess) e = hipMemcpy(f->twm, twm.data(), sizeof(float2) * twm.size(), hipMemcpyHostToDevice);
         if (e == hipSuccess) e = hipMemcpy(f->win, win.data(), sizeof(float) * n, hipMemcpyHostToDevice);
         if (e != hipSuccess) {
             stx_fft_destroy(f);
@@ -1050,6 +1069,7 @@ STX_API void stx_fft_destroy(stx_fft* f) {
     if (f->twt) (void)hipFree(f->twt);
     if (f->win) (void)hipFree(f->win);
     if (f->twn) (void)hipFree(f->twn);
+    if (f->twm) (void)hipFree(f->twm);
     delete f;
 }
 
@@ -1099,15 +1119,15 @@ STX_API stx_status stx_fft_run(const stx_fft* f, float* data, int batch, int inv
             if (f->n > 8192) fail(STX_STATUS_UNSUPPORTED, "complex transforms of %d points (at most 8192)", f->n);
             if (f->n <= 1024)
                 hipLaunchKernelGGL(fft_mixed_kernel<1024>, dim3((unsigned)batch), dim3(kMixedThreads), 0,
-                                   as_stream(stream), reinterpret_cast<float2*>(data), inverse ? 1 : 0, f->full, f->twn,
+                                   as_stream(stream), reinterpret_cast<float2*>(data), inverse ? 1 : 0, f->full, f->twm,
                                    f->n);
             else if (f->n <= 4096)
                 hipLaunchKernelGGL(fft_mixed_kernel<4096>, dim3((unsigned)batch), dim3(kMixedThreads), 0,
-                                   as_stream(stream), reinterpret_cast<float2*>(data), inverse ? 1 : 0, f->full, f->twn,
+                                   as_stream(stream), reinterpret_cast<float2*>(data), inverse ? 1 : 0, f->full, f->twm,
                                    f->n);
             else
                 hipLaunchKernelGGL(fft_mixed_kernel<8192>, dim3((unsigned)batch), dim3(kMixedThreads), 0,
-                                   as_stream(stream), reinterpret_cast<float2*>(data), inverse ? 1 : 0, f->full, f->twn,
+                                   as_stream(stream), reinterpret_cast<float2*>(data), inverse ? 1 : 0, f->full, f->twm,
                                    f->n);
             launch_check("fft_mixed_kernel");
             return;
@@ -1155,13 +1175,13 @@ STX_API stx_status stx_torch_stft(const stx_fft* f, const float* x, int channels
             const unsigned grid = (unsigned)((a.jobs + kXcds - 1) / kXcds * kXcds);   // xcd_block's multiple
             if (n / 2 <= 1024)
                 hipLaunchKernelGGL(stft_mixed_kernel<1024>, dim3(grid), dim3(kMixedThreads), 0, as_stream(stream), a,
-                                   f->half, f->twn, n);
+                                   f->half, f->twn, f->twm, n);
             else if (n / 2 <= 4096)
                 hipLaunchKernelGGL(stft_mixed_kernel<4096>, dim3(grid), dim3(kMixedThreads), 0, as_stream(stream), a,
-                                   f->half, f->twn, n);
+                                   f->half, f->twn, f->twm, n);
             else
                 hipLaunchKernelGGL(stft_mixed_kernel<8192>, dim3(grid), dim3(kMixedThreads), 0, as_stream(stream), a,
-                                   f->half, f->twn, n);
+                                   f->half, f->twn, f->twm, n);
             launch_check("stft_mixed_kernel");
             return;
         }
