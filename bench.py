@@ -642,6 +642,11 @@ def run_rows(torch, stx, dev):
         return lambda: stx.htdemucs_spec(fft1, x, out=y, stream=stream)
     row(out, "c1_htdemucs_spec", torch, stream, mk_spec1, c1_bytes)
 
+    def mk_spec1_t():
+        x, y = rn(C, L1), torch.empty((C, T1, F1), dtype=torch.complex64, device=dev)
+        return lambda: stx.htdemucs_spec(fft1, x, layout=stx.T_MAJOR, out=y, stream=stream)
+    row(out, "c1_htdemucs_spec_t_major", torch, stream, mk_spec1_t, c1_bytes)
+
     def mk_ispec1(with_ws):
         def mk():
             z, y = torch.randn((C, F1, T1), dtype=torch.complex64, device=dev), torch.empty((C, L1), device=dev)
@@ -650,6 +655,11 @@ def run_rows(torch, stx, dev):
         return mk
     row(out, "c1_htdemucs_ispec", torch, stream, mk_ispec1(False), c1_bytes)
     row(out, "c1_htdemucs_ispec_ws", torch, stream, mk_ispec1(True), c1_bytes)
+
+    def mk_ispec1_t():
+        z, y = torch.randn((C, T1, F1), dtype=torch.complex64, device=dev), torch.empty((C, L1), device=dev)
+        return lambda: stx.htdemucs_ispec(fft1, z, L1, layout=stx.T_MAJOR, out=y, stream=stream)
+    row(out, "c1_htdemucs_ispec_t_major", torch, stream, mk_ispec1_t, c1_bytes)
     del fft1
 
     # c1 pre/post-processing around the HTDemucs graph (4 sources): CaC pack + normalise of the

@@ -1436,10 +1436,10 @@ void launch_gn_vec(const GroupNormArgs& g, const GnPlan& p, const GridSync& sync
     // VEC 4 (groups of more than kGridMaxBlocks * gn_chunk<2>() floats) takes two passes: the
     // per-element parameter kinds would hold 16 weights and 16 biases per thread, more than the
     // 128 VGPRs of two blocks per CU leave without spilling, and for the per-wave kind the two
-    // passes measured faster (15.2 against 16.1 us for 48 x 85995 floats, cold): the second
-    // pass's block m runs on the XCD that read chunk m in the first, so it re-reads x from that
-    // XCD's L2, and the kernel boundary costs less than the single pass's exchange plus the
-    // spread in its blocks' release at 504 blocks of 16 values per thread.
+    // passes measured faster (15.2 against 16.1 us for 48 x 85995 floats, cold). The second
+    // pass fetches x again (PMC: 2.0x its algorithmic bytes), from the Infinity Cache where the
+    // first left it, and its loads, the fold and the VALU-bound GELU overlap across blocks
+    // better than the single pass's epilogue, which every block starts at its release.
     if constexpr (VEC < 4) if (single) {
         const void* k = reinterpret_cast<const void*>(&gn_fused_kernel<AK, GELU, VEC>);
         if ((long long)p.nch * p.groups_total <= resident_blocks(k, s)) {
