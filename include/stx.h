@@ -375,7 +375,8 @@ STX_API stx_status stx_uvr_demix_chunks(const stx_uvr_demix* demix, const float*
                                         float* parts, stx_stream stream);
 /* The weighted overlap-add (:427-440): y device [n_chunks][n_stems][C][chunk] -> out device
  * [n_stems][C][len], double products and sums in chunk order, one division, bit-identical to the
- * reference for the same model outputs. */
+ * reference for the same model outputs. Indices are 32-bit when every one fits, else 64-bit;
+ * STX_UVR_WIDE_INDEX=1 (read at each call) forces the 64-bit kernel, which gives the same bits. */
 STX_API stx_status stx_uvr_demix_overlap_add(const stx_uvr_demix* demix, const float* y, int n_stems, float* out,
                                              stx_stream stream);
 
@@ -541,15 +542,14 @@ typedef struct {
  * (dst may be a). workspace: device, 256-byte aligned, stx_group_norm_workspace_size() bytes,
  * no initialisation needed; calls that share a workspace must not run concurrently.
  * Results are deterministic and the same bits whichever path a call takes:
- *   - groups that fit on the device at once (at most 8 groups, all blocks resident together)
- *     with dst not overlapping a run as one grid-synchronised kernel. Its blocks wait for one
+ *   - groups of at most 2^21 floats that fit on the device at once (at most 8 groups, all
+ *     blocks resident together) with dst not overlapping a run as one grid-synchronised kernel. Its blocks wait for one
  *     another with bounded waits; a block whose wait gives up (blocks that never became
  *     resident: another process or a concurrent kernel holding CUs) computes its group's
  *     statistics itself from a, in the same order, and counts itself in the workspace's
  *     fallback word (stx_grid_sync_fallbacks). Streams created with a CU mask, HSA_CU_MASK,
  *     ROC_GLOBAL_CU_MASK and STX_NO_GRID_SYNC=1 select the two-kernel path;
- *   - everything else runs as two kernels (three for groups of more than 2^21 floats at
- *     VEC 4). */
+ *   - everything else runs as two kernels (three for groups of more than 2^23 floats). */
 STX_API size_t     stx_group_norm_workspace_size(const stx_tensor* a, int n_groups);
 STX_API stx_status stx_group_norm(const stx_tensor* a, const stx_tensor* dst, int n_groups, float eps,
                                   const stx_tensor* weight, const stx_tensor* bias, int gelu, void* workspace,
