@@ -439,4 +439,85 @@ __device__ __forceinline__ float2* mixed_fft(float2* buf0, float2* buf1, int M, 
     return src;
 }
 
+// mixed_pass with the whole pass known at compile time (M, Ns and the twiddle scale), all of a
+// thread's butterflies in one batch. Every LDS access is then one padded base plus immediate
+// offsets wherever the layout allows it: reads when M / R is a multiple of 16
+// (pad(b + r B) = pad(b) + r (B + B / 16)), writes when Ns is (the same identity), or when
+// Ns = 1 and R divides 16 (pad(b R + r) = pad(b R) + r, the run staying inside one 16-block).
+// The runtime pass computes a padded index, a product and a quotient per element instead.
+template <int R, int NT, int M, int Ns, int SCALE>
+__device__ __forceinline__ void mixed_pass_ct(const float2* src, float2* dst, const float2* twl, int tid) {
+    constexpr int B = M / R;
+    constexpr int IT = (B + NT - 1) / NT;
+    constexpr bool SRC_LIN = B % 16 == 0;
+    constexpr bool DST_LIN = Ns % 16 == 0 || (Ns == 1 && 16 % R == 0);
+    constexpr int SRC_STEP = B + B / 16, DST_STEP = Ns + Ns / 16;
+    float2 v[IT][R];
+    int base[IT];
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
+        const int b = min(tid + it * NT, B - 1);
+        const int blk = b / Ns, k = b - blk * Ns;
+        if constexpr (SRC_LIN) {
+            const float2* sp = src + mixed_pad(b);
+#pragma unroll
+            for (int r = 0; r < R; r++) v[it][r] = sp[r * SRC_STEP];
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; r++) v[it][r] = src[mixed_pad(b + r * B)];
+        }
+        if constexpr (Ns > 1) {
+            const int ks = k * SCALE;
+#pragma unroll
+            for (int r = 1; r < R; r++) v[it][r] = cmul(v[it][r], mixed_tw(twl, r * ks));
+        }
+        base[it] = blk * Ns * R + k;
+    }
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
+        if (tid + it * NT >= B) break;
+        Dft<R>::run(v[it]);
+        if constexpr (DST_LIN) {
+            float2* dp = dst + mixed_pad(base[it]);
+#pragma unroll
+            for (int r = 0; r < R; r++) dp[r * (Ns == 1 ? 1 : DST_STEP)] = v[it][r];
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; r++) dst[mixed_pad(base[it] + r * Ns)] = v[it][r];
+        }
+    }
+}
+
+// The passes of radices R, Rest... after sub-transforms of length Ns, ping-ponging between
+// src and dst (barrier after each); returns the buffer holding the result.
+template <int NT, int M, int TWMUL, int Ns, int R, int... Rest>
+__device__ __forceinline__ float2* mixed_fft_ct(float2* src, float2* dst, const float2* twl, int tid) {
+    mixed_pass_ct<R, NT, M, Ns, (M / (Ns * R)) * TWMUL>(src, dst, twl, tid);
+    __syncthreads();
+    if constexpr (sizeof...(Rest) == 0) return dst;
+    else return mixed_fft_ct<NT, M, TWMUL, Ns * R, Rest...>(dst, src, twl, tid);
+}
+
+// A transform size whose plan (the radices mixed_plan gives) is compiled in: mixed_fft_ct over
+// M points. The host checks that the plan object it built has the same radices.
+template <int M_, int... Rs>
+struct MixedCt {
+    static constexpr int M = M_;
+    static constexpr int count = sizeof...(Rs);
+    static constexpr int radix[sizeof...(Rs)] = {Rs...};
+    template <int NT, int TWMUL>
+    static __device__ __forceinline__ float2* run(float2* b0, float2* b1, const float2* twl, int tid) {
+        return mixed_fft_ct<NT, M, TWMUL, 1, Rs...>(b0, b1, twl, tid);
+    }
+};
+// Kim_Vocal_2's n_fft 7680: the real transform's 3840-point half.
+using MixedCt3840 = MixedCt<3840, 16, 16, 3, 5>;
+
+inline bool mixed_plan_is(const MixedRadix& p, const int* radix, int count) {
+    if (p.count != count) return false;
+    for (int i = 0; i < count; i++)
+        if (p.r[i] != radix[i]) return false;
+    return true;
+}
+
 }  // namespace stx

@@ -517,12 +517,19 @@ __device__ __forceinline__ int padded_index_rt(int m, const StftArgs& a, int n) 
     return min(max(j, 0), a.len - 1);
 }
 
-template <int MAXM>
+// CT: a size whose plan is compiled in (MixedCt: constant trip counts, LDS offsets as
+// immediates), or void for the plan p at run time.
+template <class CT> struct MixedM { static constexpr int value = CT::M; };
+template <> struct MixedM<void> { static constexpr int value = 0; };
+
+template <int MAXM, class CT>
 __global__ __launch_bounds__(kMixedThreads) void stft_mixed_kernel(StftArgs a, MixedRadix p,
                                                                    const float2* __restrict__ twn,
-                                                                   const float2* __restrict__ twm, int n) {
+                                                                   const float2* __restrict__ twm, int n_rt) {
     __shared__ float2 b0[mixed_padded(MAXM)], b1[mixed_padded(MAXM)];
     __shared__ float2 twl[kMixedTwMax];
+    constexpr int CTM = MixedM<CT>::value;
+    const int n = CTM ? 2 * CTM : n_rt;
     const int M = n / 2, tid = (int)threadIdx.x;
     const int f = xcd_block();                         // channel * T + frame
     if (f >= a.jobs) return;                           // whole block idle: no barrier reached
@@ -537,7 +544,9 @@ __global__ __launch_bounds__(kMixedThreads) void stft_mixed_kernel(StftArgs a, M
     }
     tws.store(twl, tid);
     __syncthreads();
-    const float2* z = mixed_fft<MAXM, kMixedThreads>(b0, b1, M, p, 2, twl, tid);
+    const float2* z;
+    if constexpr (CTM != 0) z = CT::template run<kMixedThreads, 2>(b0, b1, twl, tid);
+    else z = mixed_fft<MAXM, kMixedThreads>(b0, b1, M, p, 2, twl, tid);
     // X[k] = E[k] + W_n^k O[k], k <= n/2, as in stft_kernel.
     const float hs = 0.5f * a.scale;
     for (int k = tid; k < a.F; k += kMixedThreads) {
@@ -551,13 +560,15 @@ __global__ __launch_bounds__(kMixedThreads) void stft_mixed_kernel(StftArgs a, M
     }
 }
 
-template <int MAXM>
+template <int MAXM, class CT>
 __global__ __launch_bounds__(kMixedThreads) void istft_frames_mixed_kernel(IstftArgs a, MixedRadix p,
                                                                            const float2* __restrict__ twn,
-                                                                           const float2* __restrict__ twm, int n,
+                                                                           const float2* __restrict__ twm, int n_rt,
                                                                            int jobs) {
     __shared__ float2 b0[mixed_padded(MAXM)], b1[mixed_padded(MAXM)];
     __shared__ float2 twl[kMixedTwMax];
+    constexpr int CTM = MixedM<CT>::value;
+    const int n = CTM ? 2 * CTM : n_rt;
     const int M = n / 2, tid = (int)threadIdx.x;
     const int f = xcd_block();                         // channel * T + frame
     if (f >= jobs) return;                             // whole block idle: no barrier reached
@@ -584,7 +595,9 @@ __global__ __launch_bounds__(kMixedThreads) void istft_frames_mixed_kernel(Istft
     }
     tws.store(twl, tid);
     __syncthreads();
-    const float2* r = mixed_fft<MAXM, kMixedThreads>(b0, b1, M, p, 2, twl, tid);
+    const float2* r;
+    if constexpr (CTM != 0) r = CT::template run<kMixedThreads, 2>(b0, b1, twl, tid);
+    else r = mixed_fft<MAXM, kMixedThreads>(b0, b1, M, p, 2, twl, tid);
     float* dst = a.frames + (size_t)f * n;
     const float2* win2 = reinterpret_cast<const float2*>(a.win);
     float2 wv[RL];
@@ -857,14 +870,17 @@ void run_istft(const stx_fft* f, IstftArgs a, int channels, void* workspace, siz
         a.frames = static_cast<float*>(workspace);
         const int jobs = channels * a.T;
         const unsigned grid = (unsigned)((jobs + kXcds - 1) / kXcds * kXcds);   // xcd_block's multiple
-        if (f->n / 2 <= 1024)
-            hipLaunchKernelGGL(istft_frames_mixed_kernel<1024>, dim3(grid), dim3(kMixedThreads), 0, s, a, f->half,
+        if (f->n == 2 * MixedCt3840::M && mixed_plan_is(f->half, MixedCt3840::radix, MixedCt3840::count))
+            hipLaunchKernelGGL((istft_frames_mixed_kernel<4096, MixedCt3840>), dim3(grid), dim3(kMixedThreads), 0, s, a,
+                               f->half, f->twn, f->twm, f->n, jobs);
+        else if (f->n / 2 <= 1024)
+            hipLaunchKernelGGL((istft_frames_mixed_kernel<1024, void>), dim3(grid), dim3(kMixedThreads), 0, s, a, f->half,
                                f->twn, f->twm, f->n, jobs);
         else if (f->n / 2 <= 4096)
-            hipLaunchKernelGGL(istft_frames_mixed_kernel<4096>, dim3(grid), dim3(kMixedThreads), 0, s, a, f->half,
+            hipLaunchKernelGGL((istft_frames_mixed_kernel<4096, void>), dim3(grid), dim3(kMixedThreads), 0, s, a, f->half,
                                f->twn, f->twm, f->n, jobs);
         else
-            hipLaunchKernelGGL(istft_frames_mixed_kernel<8192>, dim3(grid), dim3(kMixedThreads), 0, s, a, f->half,
+            hipLaunchKernelGGL((istft_frames_mixed_kernel<8192, void>), dim3(grid), dim3(kMixedThreads), 0, s, a, f->half,
                                f->twn, f->twm, f->n, jobs);
         launch_check("istft_frames_mixed_kernel");
         hipLaunchKernelGGL(istft_ola_kernel, dim3((a.out_len + 255) / 256, channels), dim3(256), 0, s, a, f->n);
@@ -1173,14 +1189,17 @@ STX_API stx_status stx_torch_stft(const stx_fft* f, const float* x, int channels
         check_extent((long long)channels * len + n, "signal");
         if (f->mixed) {
             const unsigned grid = (unsigned)((a.jobs + kXcds - 1) / kXcds * kXcds);   // xcd_block's multiple
-            if (n / 2 <= 1024)
-                hipLaunchKernelGGL(stft_mixed_kernel<1024>, dim3(grid), dim3(kMixedThreads), 0, as_stream(stream), a,
+            if (n == 2 * MixedCt3840::M && mixed_plan_is(f->half, MixedCt3840::radix, MixedCt3840::count))
+                hipLaunchKernelGGL((stft_mixed_kernel<4096, MixedCt3840>), dim3(grid), dim3(kMixedThreads), 0,
+                                   as_stream(stream), a, f->half, f->twn, f->twm, n);
+            else if (n / 2 <= 1024)
+                hipLaunchKernelGGL((stft_mixed_kernel<1024, void>), dim3(grid), dim3(kMixedThreads), 0, as_stream(stream), a,
                                    f->half, f->twn, f->twm, n);
             else if (n / 2 <= 4096)
-                hipLaunchKernelGGL(stft_mixed_kernel<4096>, dim3(grid), dim3(kMixedThreads), 0, as_stream(stream), a,
+                hipLaunchKernelGGL((stft_mixed_kernel<4096, void>), dim3(grid), dim3(kMixedThreads), 0, as_stream(stream), a,
                                    f->half, f->twn, f->twm, n);
             else
-                hipLaunchKernelGGL(stft_mixed_kernel<8192>, dim3(grid), dim3(kMixedThreads), 0, as_stream(stream), a,
+                hipLaunchKernelGGL((stft_mixed_kernel<8192, void>), dim3(grid), dim3(kMixedThreads), 0, as_stream(stream), a,
                                    f->half, f->twn, f->twm, n);
             launch_check("stft_mixed_kernel");
             return;
