@@ -17,9 +17,10 @@
 //         transforms every frame that overlaps it (frames shared by two tiles are transformed
 //         by both), sums the windowed frames in frame order in registers and divides by the
 //         window-squared envelope, evaluated in closed form per sample;
-//       - two kernels (with a workspace of C*T*N floats): one inverse-transforms each frame
-//         once and writes it windowed to the workspace, the next sums and divides. This
-//         keeps every CU busy when there are few frames.
+//       - two kernels (the mixed-radix sizes, with a workspace of C*T*N floats): one
+//         inverse-transforms each frame once and writes it windowed to the workspace, the
+//         next sums and divides. Power-of-two sizes run the fused kernel with or without a
+//         workspace (measured faster at every size).
 #include <algorithm>
 #include <type_traits>
 #include <memory>
