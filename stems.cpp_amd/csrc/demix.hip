@@ -252,24 +252,26 @@ __global__ __launch_bounds__(256) void demix_ola_generic_kernel(DemixArgs a, con
 void check_demix(const stx_demix* d) { STX_REQUIRE(d != nullptr && d->d_window != nullptr, "null demix plan"); }
 
 // shifted[c][t] = mix[c][t + offset - max_shift] inside the input, else 0 (src/roformer.cpp:466-472).
-__global__ __launch_bounds__(256) void shift_kernel(const float* __restrict__ mix, int64_t len, int channels,
-                                                    int64_t n, int64_t delta, float* __restrict__ shifted) {
-    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < (int64_t)channels * n; e += (int64_t)gridDim.x * 256) {
-        const int64_t c = e / n, t = e - c * n;
+// blockIdx.y is the channel, so no element needs a division.
+__global__ __launch_bounds__(256) void shift_kernel(const float* __restrict__ mix, int64_t len, int64_t n,
+                                                    int64_t delta, float* __restrict__ shifted) {
+    const int64_t c = blockIdx.y;
+    for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < n; t += (int64_t)gridDim.x * 256) {
         const int64_t src = t + delta;
-        shifted[e] = (src >= 0 && src < len) ? mix[c * len + src] : 0.0f;
+        shifted[c * n + t] = (src >= 0 && src < len) ? mix[c * len + src] : 0.0f;
     }
 }
 
 // est[i][t] += y[i][t + lead] / shifts, float as the reference (:474-476); est starts at 0.
+// blockIdx.y is the plane i.
 __global__ __launch_bounds__(256) void shift_accumulate_kernel(const float* __restrict__ y, int64_t n, int64_t lead,
-                                                               int64_t len, int planes, int shifts, int first,
+                                                               int64_t len, int shifts, int first,
                                                                float* __restrict__ est) {
 #pragma clang fp contract(off)
-    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < (int64_t)planes * len; e += (int64_t)gridDim.x * 256) {
-        const int64_t i = e / len, t = e - i * len;
+    const int64_t i = blockIdx.y;
+    for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < len; t += (int64_t)gridDim.x * 256) {
         const float v = y[i * n + lead + t] / (float)shifts;
-        est[e] = first ? 0.0f + v : est[e] + v;
+        est[i * len + t] = first ? 0.0f + v : est[i * len + t] + v;
     }
 }
 
@@ -433,6 +435,7 @@ STX_API stx_status stx_demix_track(const float* mix, int channels, int64_t len, 
         if (len <= 0) fail(STX_STATUS_INVALID_ARGUMENT, "empty input");                   // :439
         if (opt.overlap >= 1.0f) fail(STX_STATUS_INVALID_ARGUMENT, "overlap must be < 1"); // :440
         STX_REQUIRE(channels >= 1 && n_stems >= 1 && chunk >= 1 && batch >= 1, "bad channels/stems/chunk/batch");
+        STX_REQUIRE((int64_t)n_stems * channels < 65536, "too many stems * channels");
         STX_REQUIRE(mix && out && separate && workspace, "NULL argument");
         STX_REQUIRE(opt.shifts <= 0 || sample_rate >= 2, "bad sample rate for shifts");
         const int step = stx_demix_step(chunk, num_overlap, opt.overlap);
@@ -490,13 +493,13 @@ STX_API stx_status stx_demix_track(const float* mix, int channels, int64_t len, 
                 for (int k = 0; k < opt.shifts; k++) {
                     const int offset = dist(rng);
                     const int64_t n = len + max_shift - offset;
-                    hipLaunchKernelGGL(shift_kernel, dim3(grid_for(channels * n)), dim3(256), 0, s, mix, len, channels,
-                                       n, (int64_t)offset - max_shift, d_shifted);
+                    hipLaunchKernelGGL(shift_kernel, dim3(grid_for(n), (unsigned)channels), dim3(256), 0, s, mix, len, n,
+                                       (int64_t)offset - max_shift, d_shifted);
                     launch_check("shift_kernel");
                     demix(d_shifted, n, d_yk);
-                    hipLaunchKernelGGL(shift_accumulate_kernel, dim3(grid_for((int64_t)n_stems * channels * len)),
-                                       dim3(256), 0, s, d_yk, n, (int64_t)max_shift - offset, len, n_stems * channels,
-                                       opt.shifts, k == 0 ? 1 : 0, out);
+                    hipLaunchKernelGGL(shift_accumulate_kernel, dim3(grid_for(len), (unsigned)(n_stems * channels)),
+                                       dim3(256), 0, s, d_yk, n, (int64_t)max_shift - offset, len, opt.shifts,
+                                       k == 0 ? 1 : 0, out);
                     launch_check("shift_accumulate_kernel");
                 }
             }
