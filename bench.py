@@ -786,6 +786,17 @@ def run_rows(torch, stx, dev):
         x, y = rn(C, n48), torch.empty((C, rsm.length(n48)), device=dev)
         return lambda: rsm(x, out=y, stream=stream)
     row(out, "c5_resample_48k", torch, stream, mk_resample, C * (n48 + rsm.length(n48)) * 4)
+    # The per-tap kernel, bit-identical to the reference (chosen by the variable at each call,
+    # so also when a graph is captured).
+    prev = os.environ.get("STX_RESAMPLE_EXACT")
+    os.environ["STX_RESAMPLE_EXACT"] = "1"
+    try:
+        row(out, "c5_resample_48k_exact", torch, stream, mk_resample, C * (n48 + rsm.length(n48)) * 4)
+    finally:
+        if prev is None:
+            del os.environ["STX_RESAMPLE_EXACT"]
+        else:
+            os.environ["STX_RESAMPLE_EXACT"] = prev
     del rsm
 
     # The same song through the TFC-TDF UVR chunking (Kim_Vocal_2: n_fft 7680, chunk 261,120,

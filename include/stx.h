@@ -417,8 +417,14 @@ STX_API void       stx_resampler_destroy(stx_resampler* resampler);
 /* Output samples per channel for n input samples: llround(n * dst / src), n when the rates are
  * equal (src/audio.h:19-20); -1 for a NULL plan or n < 0. */
 STX_API int64_t    stx_resample_length(const stx_resampler* resampler, int64_t n);
-/* in: device [channels][n]; out: device [channels][stx_resample_length(n)], bit-identical to the
- * reference (double sums in its order). Equal rates copy. More than 8 channels is UNSUPPORTED. */
+/* in: device [channels][n]; out: device [channels][stx_resample_length(n)]. By default each output
+ * uses the weights of its exact phase (dst / gcd rows computed once by the reference's formula),
+ * which differ from the reference's per-output weights by the rounding of its position i / ratio:
+ * measured within 2.0e-7 of the output's rms, 167 dB SNR, on 180 s of stereo at 48 kHz.
+ * STX_RESAMPLE_EXACT=1 in the environment (read at each call) selects the per-tap kernel,
+ * bit-identical to the reference (double sums in its order). That kernel is also used when the
+ * phase path does not fit: more than 2^18 phase-table weights, or more than 64 KB of staged input
+ * per 64 phase cycles. Equal rates copy. More than 8 channels is UNSUPPORTED. */
 STX_API stx_status stx_resample(const stx_resampler* resampler, const float* in, int channels, int64_t n, float* out,
                                 stx_stream stream);
 

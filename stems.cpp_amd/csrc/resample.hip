@@ -3,9 +3,11 @@
 // Reference: st::resample_planar (src/audio.h:17-59): a Kaiser-windowed sinc (beta 8.6, 32 zero
 // crossings, cutoff 0.95 of the lower Nyquist), tabulated once over |x| in [0, half] at 2^15 + 2
 // points and interpolated linearly; each output sample sums, in double and in input order, the
-// weighted input samples within `half` of its position. The table is computed on the host with
-// the reference's formula (so it is bit-identical), kept on the device, and every per-tap
-// operation is the reference's double operation in the reference's order, so the output is
+// weighted input samples within `half` of its position. Two kernels. The default one,
+// resample_phase_kernel (below), weights each output by its exact phase; the per-tap one,
+// resample_kernel, chosen by STX_RESAMPLE_EXACT=1, computes the table on the host with the
+// reference's formula (so it is bit-identical), keeps it on the device, and does every per-tap
+// operation as the reference's double operation in the reference's order, so its output is
 // bit-identical. One thread per output sample and every channel; taps go in groups of eight
 // whose loads are issued together (clamped addresses; a tap past the window, or one the
 // reference skips, adds +0.0, an exact no-op on a sum that starts at +0.0). The per-tap
@@ -15,6 +17,8 @@
 // exact by the fma), so bit-identical to IEEE division at a fraction of its cost.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
+#include <numeric>
 #include <vector>
 
 #include "common.hpp"
@@ -23,6 +27,12 @@ struct stx_resampler {
     int src = 0, dst = 0;
     double ratio = 1.0, half = 0.0;
     double* d_table = nullptr;       // [kTableN + 2]
+    // Phase table (see resample_phase_kernel): dst = up * g, src = down * g.
+    int up = 0, down = 0;
+    int ntap = 0, omin = 0;          // taps per phase row; offset of tap 0 from floor(c)
+    int pad = 0, staged = 0, lds_words = 0;  // staged input tile of resample_phase_kernel
+    double* d_phase = nullptr;       // [up][ntap] weights, 0 where a tap is not used
+    int2* d_range = nullptr;         // [up]: first and last used tap of each phase
 };
 
 namespace stx {
@@ -81,6 +91,106 @@ __global__ __launch_bounds__(256) void resample_kernel(ResampleArgs a) {
         if (k < C) store_stream(a.out + (size_t)k * a.out_n + i, (float)acc[k]);
 }
 
+// The same sums over weights that depend only on the output's phase. With dst = up g and
+// src = down g, output i = q + M up sits at c = i down / up = fq + M down + p / up, where
+// fq = floor(q down / up) and p = q down mod up, so its taps j = fq + M down + omin + k and their
+// weights (the reference's table interpolation at |j - c|) are row p of a table of up rows
+// computed once on the host. Those weights differ from the reference's, which it computes per
+// output from c = i / ratio with ratio rounded to double, by the rounding of c (below 1e-9 for
+// three hours of 48 kHz audio), so the output is within a few float ulps of the reference's
+// (SNR above 160 dB) instead of bit-identical; the per-tap division, table lookup and
+// interpolation of resample_kernel are gone, leaving a conversion and an fma per tap.
+//
+// A workgroup takes one channel and the 64 output groups M = m0 + lane, m0 = 64 blockIdx.x: all
+// outputs in [m0 up, (m0 + 64) up). It stages the input they read, j = m0 down + omin + s for
+// s < 64 down + ntap, in LDS (zeros outside the input, which add nothing), then each of its
+// eight waves takes the phases q = wave, wave + 8, ...: the phase, hence the weight row, is the
+// same for the whole wave and is read through scalar loads, and lane l reads its taps at
+// s = l down + fq + k. Lanes
+// `down` words apart would share LDS banks when down has a large power of two, so then
+// (down % 8 == 0) a pad word follows every `down` staged samples: the lane stride is down + 1,
+// odd, and a lane's window crosses at most one pad every `down` taps, at the same tap for the
+// whole wave. Taps outside a phase's window are not summed.
+struct PhaseArgs {
+    const float* in;                 // [C][n]
+    float* out;                      // [C][out_n]
+    const double* w;                 // [up][ntap]
+    const int2* range;               // [up]: first and last tap of each phase row
+    long long n, out_n;
+    int up, down, ntap, omin;
+    int pad;                         // 1: a pad word after every `down` staged samples
+    int staged;                      // samples staged per workgroup: 64 down + ntap
+    FastDiv fup, fdown;              // q down / up (below 2^26) and s / down (below 2^15)
+};
+
+constexpr int kPhaseTile = 64;                       // output groups per workgroup, one per lane
+constexpr int kPhaseWaves = 8;                       // waves per workgroup, each over up / 8 phases
+constexpr int kPhaseStage = 4;                       // staged loads in flight per thread
+constexpr long long kPhaseMaxWeights = 1 << 18;      // up * ntap above this: per-tap kernel
+constexpr int kPhaseMaxLds = 64 * 1024;              // staged tile above this: per-tap kernel
+
+__global__ __launch_bounds__(kPhaseWaves * 64) void resample_phase_kernel(PhaseArgs a) {
+    extern __shared__ float xs[];
+    constexpr int NT = kPhaseWaves * 64;
+    const int c = (int)blockIdx.y;
+    const long long m0 = (long long)blockIdx.x * kPhaseTile;
+    const float* in = a.in + (size_t)c * a.n;
+    const long long j0 = m0 * a.down + a.omin;
+    for (int s0 = (int)threadIdx.x; s0 < a.staged; s0 += NT * kPhaseStage) {
+        float v[kPhaseStage];
+#pragma unroll
+        for (int u = 0; u < kPhaseStage; u++) {
+            const long long j = j0 + s0 + u * NT;
+            v[u] = s0 + u * NT < a.staged && j >= 0 && j < a.n ? in[j] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kPhaseStage; u++) {
+            const int st = s0 + u * NT;
+            if (st < a.staged) xs[a.pad ? st + (int)a.fdown.div((unsigned)st) : st] = v[u];
+        }
+    }
+    __syncthreads();
+    const int lane = (int)threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const float* xl = xs + lane * (a.down + a.pad);
+    float* outc = a.out + (size_t)c * a.out_n;
+    const long long i0 = (m0 + lane) * a.up;
+    for (int q = wave; q < a.up; q += kPhaseWaves) {
+        const unsigned qd = (unsigned)q * (unsigned)a.down;
+        const int fq = (int)a.fup.div(qd), p = (int)(qd - (unsigned)fq * (unsigned)a.up);
+        const int2 rg = a.range[p];
+        const double* wr = a.w + (size_t)p * a.ntap - fq;       // indexed by s = fq + k
+        double acc = 0.0;
+        int s = fq + rg.x;
+        const int e = fq + rg.y;
+        if (a.pad) {
+            for (int row = (int)a.fdown.div((unsigned)s); s <= e; row++) {
+                const int se = min(e, (row + 1) * a.down - 1);    // last tap before the next pad
+                const float* xr = xl + row;
+#pragma unroll 8
+                for (; s <= se; s++) acc = fma(wr[s], (double)xr[s], acc);
+            }
+        } else {
+#pragma unroll 8
+            for (; s <= e; s++) acc = fma(wr[s], (double)xl[s], acc);
+        }
+        const long long i = i0 + q;
+        if (i < a.out_n) outc[i] = (float)acc;
+    }
+}
+
+// LDS words of one staged tile (zero: the tile does not fit and the per-tap kernel is used).
+int phase_lds_words(int down, int ntap, int* pad, int* staged) {
+    const long long st = (long long)kPhaseTile * down + ntap;
+    const int pd = down % 8 == 0 ? 1 : 0;
+    const long long words = st + (pd ? (st - 1) / down + 1 : 0);
+    if (words * 4 > kPhaseMaxLds) return 0;
+    *pad = pd;
+    *staged = (int)st;
+    return (int)words;
+}
+
+
 __global__ __launch_bounds__(256) void copy_kernel(const float* __restrict__ in, float* __restrict__ out, size_t n) {
     for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (size_t)gridDim.x * 256) out[e] = in[e];
 }
@@ -127,9 +237,55 @@ STX_API stx_status stx_resampler_create(int src_rate, int dst_rate, stx_resample
                 table[t] = rr >= 1 ? 0.0 : sinc * bessel_i0(beta * std::sqrt(1 - rr * rr)) / i0b * cutoff;
             }
             r->half = half;
+            // Phase table: output i = q + M up has c = i down / up = floor(q down / up) + M down
+            // + p / up with p = q down mod up; its taps are j = floor(c) + o for o in
+            // [ceil(p/up - half), floor(p/up + half)], each weighted as the reference weights
+            // |j - c| (src/audio.h:47-52), skipped where the table index reaches table_n.
+            const int g = std::gcd(src_rate, dst_rate);
+            const int up = dst_rate / g, down = src_rate / g;
+            const int omin = -(int)std::floor(half), omax = (int)std::floor(half) + 1;
+            const int ntap = omax - omin + 1;
+            std::vector<double> phase;
+            std::vector<int2> range;
+            int pad = 0, staged = 0;
+            const int lds_words = phase_lds_words(down, ntap, &pad, &staged);
+            if ((long long)up * ntap <= kPhaseMaxWeights && lds_words > 0) {
+                phase.assign((size_t)up * ntap, 0.0);
+                range.assign(up, make_int2(0, -1));
+                for (int p = 0; p < up; p++) {
+                    const double frac = (double)p / up;
+                    int lo = ntap, hi = -1;
+                    for (int k = 0; k < ntap; k++) {
+                        const int o = omin + k;
+                        if (o < (int)std::ceil(frac - half) || o > (int)std::floor(frac + half)) continue;
+                        const double pos = std::fabs(o - frac) / half * kTableN;
+                        const int t = (int)pos;
+                        if (t >= kTableN) continue;
+                        phase[(size_t)p * ntap + k] = table[t] + (table[t + 1] - table[t]) * (pos - t);
+                        lo = std::min(lo, k);
+                        hi = std::max(hi, k);
+                    }
+                    range[p] = make_int2(lo, hi);
+                }
+                r->up = up;
+                r->down = down;
+                r->ntap = ntap;
+                r->omin = omin;
+                r->pad = pad;
+                r->staged = staged;
+                r->lds_words = lds_words;
+            }
             hipError_t e = hipMalloc(&r->d_table, sizeof(double) * table.size());
             if (e == hipSuccess)
                 e = hipMemcpy(r->d_table, table.data(), sizeof(double) * table.size(), hipMemcpyHostToDevice);
+            if (e == hipSuccess && !phase.empty()) {
+                e = hipMalloc(&r->d_phase, sizeof(double) * phase.size());
+                if (e == hipSuccess) e = hipMalloc(&r->d_range, sizeof(int2) * range.size());
+                if (e == hipSuccess)
+                    e = hipMemcpy(r->d_phase, phase.data(), sizeof(double) * phase.size(), hipMemcpyHostToDevice);
+                if (e == hipSuccess)
+                    e = hipMemcpy(r->d_range, range.data(), sizeof(int2) * range.size(), hipMemcpyHostToDevice);
+            }
             if (e != hipSuccess) {
                 stx_resampler_destroy(r);
                 hip_check(e, "stx_resampler_create");
@@ -142,6 +298,8 @@ STX_API stx_status stx_resampler_create(int src_rate, int dst_rate, stx_resample
 STX_API void stx_resampler_destroy(stx_resampler* r) {
     if (!r) return;
     if (r->d_table) (void)hipFree(r->d_table);
+    if (r->d_phase) (void)hipFree(r->d_phase);
+    if (r->d_range) (void)hipFree(r->d_range);
     delete r;
 }
 
@@ -171,6 +329,20 @@ STX_API stx_status stx_resample(const stx_resampler* r, const float* in, int cha
         STX_REQUIRE(out_n < (1LL << 31), "output too long");
         if (out_n == 0) return;
         if (channels > 8) fail(STX_STATUS_UNSUPPORTED, "resample: more than 8 channels");
+        // The phase table unless STX_RESAMPLE_EXACT=1 (read at each call) asks for the per-tap
+        // kernel, which gives the reference's bits.
+        const char* exact = std::getenv("STX_RESAMPLE_EXACT");
+        if (r->d_phase && !(exact && exact[0] == '1')) {
+            PhaseArgs pa{in, out, r->d_phase, r->d_range, n, out_n, r->up, r->down, r->ntap, r->omin, r->pad, r->staged,
+                         FastDiv((unsigned)r->up), FastDiv((unsigned)r->down)};
+            const long long groups = (out_n + r->up - 1) / r->up;                // output groups M
+            STX_REQUIRE(channels < 65536, "too many channels");
+            const long long tiles = (groups + kPhaseTile - 1) / kPhaseTile;
+            const dim3 pg((unsigned)tiles, (unsigned)channels);
+            hipLaunchKernelGGL(resample_phase_kernel, pg, dim3(kPhaseWaves * 64), sizeof(float) * r->lds_words, s, pa);
+            launch_check("resample_phase_kernel");
+            return;
+        }
         ResampleArgs a{in, out, r->d_table, r->ratio, r->half, 1.0 / r->half, (int)n, (int)out_n, channels};
         const dim3 grid((unsigned)((out_n + 255) / 256));
         if (channels == 1) hipLaunchKernelGGL(resample_kernel<1>, grid, dim3(256), 0, s, a);

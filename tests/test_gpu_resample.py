@@ -1,8 +1,13 @@
 """GPU parity of the resampler (resample.hip) against the oracle (src/audio.h:17-59).
 
-Bar: bit-exact (the device sums the reference's double products in the reference's order over
-a table computed by the reference's formula). Shapes: a 180 s stereo song at 48 kHz to the
-models' 44.1 kHz, and short inputs for other rate pairs, mono and 3 channels.
+Bars: the per-tap kernel (STX_RESAMPLE_EXACT=1) is bit-exact (the device sums the reference's
+double products in the reference's order over a table computed by the reference's formula);
+the default phase-table kernel, whose weights come from the output's exact rational position
+instead of the reference's rounded one, has SNR >= 110 dB and every sample within 1e-6 of the
+output's rms. Rate pairs whose staged tile does not fit in LDS (44.1 -> 16 kHz, 96 -> 44.1 kHz
+here) take the per-tap kernel by default and are bit-exact either way. Shapes: a 180 s stereo
+song at 48 kHz to the models' 44.1 kHz, and short inputs for other rate pairs, mono and 3
+channels.
 """
 import numpy as np
 import pytest
@@ -10,6 +15,7 @@ import pytest
 import oracle_lib
 import stx
 import synth
+from metrics import snr_db
 
 pytestmark = pytest.mark.gpu
 
@@ -32,13 +38,22 @@ def host(t):
 
 @pytest.mark.parametrize("src,dst,C,n", [(48000, 44100, 2, 8640000), (22050, 44100, 2, 30001), (44100, 16000, 1, 44100),
                                          (96000, 44100, 3, 9601), (44100, 48000, 2, 100), (8000, 44100, 1, 37)])
-def test_resample_bit_exact(device, rs, src, dst, C, n):
+def test_resample_parity(device, rs, src, dst, C, n, monkeypatch):
     x = synth.sines_plus_pink(src % 1000, C, n) if n > 1000 else synth.normal(src % 1000, (C, n), 0.3)
     r = stx.Resampler(src, dst)
-    got = host(r(dev(x, device)))
+    xd = dev(x, device)
     want = rs(x, src, dst)
+    got = host(r(xd))
     assert got.shape == want.shape and r.length(n) == want.shape[1]
-    assert np.array_equal(got, want)
+    # A filter's output: SNR >= 110 dB, and every sample within 1e-6 of the signal's rms (measured
+    # 167 dB and 2.0e-7 rms for the 180 s song). An elementwise relative bound does not apply:
+    # outputs that cancel to near zero carry the weights' 1e-9 difference times the inputs' scale.
+    rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
+    assert snr_db(got, want) >= 110.0
+    assert float(np.max(np.abs(got.astype(np.float64) - want))) <= 1e-6 * rms
+    monkeypatch.setenv("STX_RESAMPLE_EXACT", "1")
+    exact = host(r(xd))
+    assert np.array_equal(exact, want)
 
 
 def test_equal_rates_copy(device):
