@@ -423,8 +423,9 @@ STX_API int64_t    stx_resample_length(const stx_resampler* resampler, int64_t n
  * measured within 2.0e-7 of the output's rms, 167 dB SNR, on 180 s of stereo at 48 kHz.
  * STX_RESAMPLE_EXACT=1 in the environment (read at each call) selects the per-tap kernel,
  * bit-identical to the reference (double sums in its order). That kernel is also used when the
- * phase path does not fit: more than 2^18 phase-table weights, or more than 64 KB of staged input
- * per 64 phase cycles. Equal rates copy. More than 8 channels is UNSUPPORTED. */
+ * phase path does not fit: more than 2^18 phase-table weights, or a staged input tile (64 rows of
+ * down + taps + 8 samples) above the device's LDS per workgroup. Equal rates copy. More than 8
+ * channels is UNSUPPORTED. */
 STX_API stx_status stx_resample(const stx_resampler* resampler, const float* in, int channels, int64_t n, float* out,
                                 stx_stream stream);
 

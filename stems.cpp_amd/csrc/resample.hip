@@ -30,7 +30,7 @@ struct stx_resampler {
     // Phase table (see resample_phase_kernel): dst = up * g, src = down * g.
     int up = 0, down = 0;
     int ntap = 0, omin = 0;          // taps per phase row; offset of tap 0 from floor(c)
-    int pad = 0, staged = 0, lds_words = 0;  // staged input tile of resample_phase_kernel
+    int width = 0, pitch = 0, lds_bytes = 0;  // staged input tile of resample_phase_kernel
     double* d_phase = nullptr;       // [up][ntap] weights, 0 where a tap is not used
     int2* d_range = nullptr;         // [up]: first and last used tap of each phase
 };
@@ -102,32 +102,37 @@ __global__ __launch_bounds__(256) void resample_kernel(ResampleArgs a) {
 // interpolation of resample_kernel are gone, leaving a conversion and an fma per tap.
 //
 // A workgroup takes one channel and the 64 output groups M = m0 + lane, m0 = 64 blockIdx.x: all
-// outputs in [m0 up, (m0 + 64) up). It stages the input they read, j = m0 down + omin + s for
-// s < 64 down + ntap, in LDS (zeros outside the input, which add nothing), then each of its
-// eight waves takes the phases q = wave, wave + 8, ...: the phase, hence the weight row, is the
-// same for the whole wave and is read through scalar loads, and lane l reads its taps at
-// s = l down + fq + k. Lanes
-// `down` words apart would share LDS banks when down has a large power of two, so then
-// (down % 8 == 0) a pad word follows every `down` staged samples: the lane stride is down + 1,
-// odd, and a lane's window crosses at most one pad every `down` taps, at the same tap for the
-// whole wave. Taps outside a phase's window are not summed.
+// outputs in [m0 up, (m0 + 64) up). It stages in LDS, for each lane, the input its outputs read:
+// row l holds j = (m0 + l) down + omin + r for r < width = down + ntap + kPhaseOverread (zeros
+// outside the input, which add nothing; neighbouring rows overlap by ntap + kPhaseOverread). Rows
+// are `pitch` floats apart, width rounded up to odd, so the lanes of a read fall in different
+// banks. 48 -> 44.1 kHz stages 62 KB: two workgroups of 16 waves, the most waves a CU holds,
+// which the time depends on (8-wave workgroups: 196 us, 4: 358 us). Each of its 16 waves takes the phases q = wave, wave + 16, ...: the phase,
+// hence the weight row, is the same for the whole wave and is read through scalar loads, and
+// lane l reads its taps at row l, r = fq + k. Taps go eight at a time, one 64-byte scalar load of
+// weights and four paired LDS reads each; the last 1-7 taps of a window load a whole chunk (at
+// most 7 samples and weights past the window, inside the row and the padded table) and sum only
+// their own, under uniform branches. Taps outside a phase's window are not summed.
 struct PhaseArgs {
     const float* in;                 // [C][n]
     float* out;                      // [C][out_n]
-    const double* w;                 // [up][ntap]
+    const double* w;                 // [up][ntap] + kPhaseOverread
     const int2* range;               // [up]: first and last tap of each phase row
     long long n, out_n;
     int up, down, ntap, omin;
-    int pad;                         // 1: a pad word after every `down` staged samples
-    int staged;                      // samples staged per workgroup: 64 down + ntap
-    FastDiv fup, fdown;              // q down / up (below 2^26) and s / down (below 2^15)
+    int width, pitch;                // staged samples per lane row; floats between rows (odd)
+    FastDiv fup, fwidth;             // q down / up (below 2^20) and staging index / width (below 2^15)
 };
 
 constexpr int kPhaseTile = 64;                       // output groups per workgroup, one per lane
-constexpr int kPhaseWaves = 8;                       // waves per workgroup, each over up / 8 phases
+constexpr int kPhaseWaves = 16;                      // waves per workgroup, each over up / 16 phases
 constexpr int kPhaseStage = 4;                       // staged loads in flight per thread
 constexpr long long kPhaseMaxWeights = 1 << 18;      // up * ntap above this: per-tap kernel
-constexpr int kPhaseMaxLds = 64 * 1024;              // staged tile above this: per-tap kernel
+constexpr int kPhaseOverread = 8;                    // staged samples and table weights past the last used
+
+// The weight table does not change while the kernel runs: read through the constant address
+// space, a wave-uniform load of it is a scalar load into SGPRs.
+typedef const __attribute__((address_space(4))) double* ConstDoubles;
 
 __global__ __launch_bounds__(kPhaseWaves * 64) void resample_phase_kernel(PhaseArgs a) {
     extern __shared__ float xs[];
@@ -135,59 +140,67 @@ __global__ __launch_bounds__(kPhaseWaves * 64) void resample_phase_kernel(PhaseA
     const int c = (int)blockIdx.y;
     const long long m0 = (long long)blockIdx.x * kPhaseTile;
     const float* in = a.in + (size_t)c * a.n;
-    const long long j0 = m0 * a.down + a.omin;
-    for (int s0 = (int)threadIdx.x; s0 < a.staged; s0 += NT * kPhaseStage) {
+    const int staged = kPhaseTile * a.width;
+    for (int s0 = (int)threadIdx.x; s0 < staged; s0 += NT * kPhaseStage) {
         float v[kPhaseStage];
-#pragma unroll
-        for (int u = 0; u < kPhaseStage; u++) {
-            const long long j = j0 + s0 + u * NT;
-            v[u] = s0 + u * NT < a.staged && j >= 0 && j < a.n ? in[j] : 0.0f;
-        }
+        int at[kPhaseStage];
 #pragma unroll
         for (int u = 0; u < kPhaseStage; u++) {
             const int st = s0 + u * NT;
-            if (st < a.staged) xs[a.pad ? st + (int)a.fdown.div((unsigned)st) : st] = v[u];
+            const int l = (int)a.fwidth.div((unsigned)st), r = st - l * a.width;
+            const long long j = (m0 + l) * a.down + a.omin + r;
+            v[u] = st < staged && j >= 0 && j < a.n ? in[j] : 0.0f;
+            at[u] = l * a.pitch + r;
         }
+#pragma unroll
+        for (int u = 0; u < kPhaseStage; u++)
+            if (s0 + u * NT < staged) xs[at[u]] = v[u];
     }
     __syncthreads();
     const int lane = (int)threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
-    const float* xl = xs + lane * (a.down + a.pad);
+    const float* xl = xs + lane * a.pitch;
     float* outc = a.out + (size_t)c * a.out_n;
     const long long i0 = (m0 + lane) * a.up;
     for (int q = wave; q < a.up; q += kPhaseWaves) {
         const unsigned qd = (unsigned)q * (unsigned)a.down;
         const int fq = (int)a.fup.div(qd), p = (int)(qd - (unsigned)fq * (unsigned)a.up);
         const int2 rg = a.range[p];
-        const double* wr = a.w + (size_t)p * a.ntap - fq;       // indexed by s = fq + k
-        double acc = 0.0;
-        int s = fq + rg.x;
+        const ConstDoubles wr = (ConstDoubles)(a.w + (size_t)p * a.ntap - fq);   // indexed by r = fq + k
         const int e = fq + rg.y;
-        if (a.pad) {
-            for (int row = (int)a.fdown.div((unsigned)s); s <= e; row++) {
-                const int se = min(e, (row + 1) * a.down - 1);    // last tap before the next pad
-                const float* xr = xl + row;
-#pragma unroll 8
-                for (; s <= se; s++) acc = fma(wr[s], (double)xr[s], acc);
+        int r = fq + rg.x;
+        double acc = 0.0;
+        for (; r + 7 <= e; r += 8) {
+#pragma unroll
+            for (int t = 0; t < 8; t++) acc = fma(wr[r + t], (double)xl[r + t], acc);
+        }
+        if (r <= e) {
+            float x[8];
+            double w[8];
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                x[t] = xl[r + t];
+                w[t] = wr[r + t];
             }
-        } else {
-#pragma unroll 8
-            for (; s <= e; s++) acc = fma(wr[s], (double)xl[s], acc);
+#pragma unroll
+            for (int t = 0; t < 7; t++)
+                if (r + t <= e) acc = fma(w[t], (double)x[t], acc);
         }
         const long long i = i0 + q;
         if (i < a.out_n) outc[i] = (float)acc;
     }
 }
 
-// LDS words of one staged tile (zero: the tile does not fit and the per-tap kernel is used).
-int phase_lds_words(int down, int ntap, int* pad, int* staged) {
-    const long long st = (long long)kPhaseTile * down + ntap;
-    const int pd = down % 8 == 0 ? 1 : 0;
-    const long long words = st + (pd ? (st - 1) / down + 1 : 0);
-    if (words * 4 > kPhaseMaxLds) return 0;
-    *pad = pd;
-    *staged = (int)st;
-    return (int)words;
+// LDS bytes of one staged tile (zero: the tile does not fit in `budget` bytes, the device's LDS
+// per workgroup, and the per-tap kernel is used).
+int phase_lds_bytes(int down, int ntap, long long budget, int* width, int* pitch) {
+    const long long wd = (long long)down + ntap + kPhaseOverread;
+    const long long pt = wd | 1;
+    const long long bytes = kPhaseTile * pt * (long long)sizeof(float);
+    if (bytes > budget) return 0;
+    *width = (int)wd;
+    *pitch = (int)pt;
+    return (int)bytes;
 }
 
 
@@ -218,6 +231,11 @@ STX_API stx_status stx_resampler_create(int src_rate, int dst_rate, stx_resample
         STX_REQUIRE(out != nullptr, "out is NULL");
         *out = nullptr;
         STX_REQUIRE(src_rate > 0 && dst_rate > 0, "sample rates must be positive");
+        // LDS per workgroup of the current device: the phase kernel's staged tile must fit.
+        int dev = 0, lds_max = 0;
+        hip_check(hipGetDevice(&dev), "hipGetDevice");
+        hip_check(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, dev),
+                  "hipDeviceGetAttribute");
         stx_resampler* r = new stx_resampler;
         r->src = src_rate;
         r->dst = dst_rate;
@@ -247,10 +265,18 @@ STX_API stx_status stx_resampler_create(int src_rate, int dst_rate, stx_resample
             const int ntap = omax - omin + 1;
             std::vector<double> phase;
             std::vector<int2> range;
-            int pad = 0, staged = 0;
-            const int lds_words = phase_lds_words(down, ntap, &pad, &staged);
-            if ((long long)up * ntap <= kPhaseMaxWeights && lds_words > 0) {
-                phase.assign((size_t)up * ntap, 0.0);
+            // The staged tile must fit in the device's LDS per workgroup; above 64 KB the kernel
+            // is allowed that much dynamic LDS first.
+            int width = 0, pitch = 0;
+            int lds_bytes = phase_lds_bytes(down, ntap, lds_max, &width, &pitch);
+            if (lds_bytes > 64 * 1024 &&
+                hipFuncSetAttribute((const void*)resample_phase_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    lds_max) != hipSuccess) {
+                (void)hipGetLastError();
+                lds_bytes = 0;
+            }
+            if ((long long)up * ntap <= kPhaseMaxWeights && lds_bytes > 0) {
+                phase.assign((size_t)up * ntap + kPhaseOverread, 0.0);
                 range.assign(up, make_int2(0, -1));
                 for (int p = 0; p < up; p++) {
                     const double frac = (double)p / up;
@@ -271,9 +297,9 @@ STX_API stx_status stx_resampler_create(int src_rate, int dst_rate, stx_resample
                 r->down = down;
                 r->ntap = ntap;
                 r->omin = omin;
-                r->pad = pad;
-                r->staged = staged;
-                r->lds_words = lds_words;
+                r->width = width;
+                r->pitch = pitch;
+                r->lds_bytes = lds_bytes;
             }
             hipError_t e = hipMalloc(&r->d_table, sizeof(double) * table.size());
             if (e == hipSuccess)
@@ -333,13 +359,13 @@ STX_API stx_status stx_resample(const stx_resampler* r, const float* in, int cha
         // kernel, which gives the reference's bits.
         const char* exact = std::getenv("STX_RESAMPLE_EXACT");
         if (r->d_phase && !(exact && exact[0] == '1')) {
-            PhaseArgs pa{in, out, r->d_phase, r->d_range, n, out_n, r->up, r->down, r->ntap, r->omin, r->pad, r->staged,
-                         FastDiv((unsigned)r->up), FastDiv((unsigned)r->down)};
+            PhaseArgs pa{in, out, r->d_phase, r->d_range, n, out_n, r->up, r->down, r->ntap, r->omin, r->width, r->pitch,
+                         FastDiv((unsigned)r->up), FastDiv((unsigned)r->width)};
             const long long groups = (out_n + r->up - 1) / r->up;                // output groups M
             STX_REQUIRE(channels < 65536, "too many channels");
             const long long tiles = (groups + kPhaseTile - 1) / kPhaseTile;
             const dim3 pg((unsigned)tiles, (unsigned)channels);
-            hipLaunchKernelGGL(resample_phase_kernel, pg, dim3(kPhaseWaves * 64), sizeof(float) * r->lds_words, s, pa);
+            hipLaunchKernelGGL(resample_phase_kernel, pg, dim3(kPhaseWaves * 64), (unsigned)r->lds_bytes, s, pa);
             launch_check("resample_phase_kernel");
             return;
         }

@@ -4,10 +4,10 @@ Bars: the per-tap kernel (STX_RESAMPLE_EXACT=1) is bit-exact (the device sums th
 double products in the reference's order over a table computed by the reference's formula);
 the default phase-table kernel, whose weights come from the output's exact rational position
 instead of the reference's rounded one, has SNR >= 110 dB and every sample within 1e-6 of the
-output's rms. Rate pairs whose staged tile does not fit in LDS (44.1 -> 16 kHz, 96 -> 44.1 kHz
-here) take the per-tap kernel by default and are bit-exact either way. Shapes: a 180 s stereo
-song at 48 kHz to the models' 44.1 kHz, and short inputs for other rate pairs, mono and 3
-channels.
+output's rms. A rate pair whose staged input tile exceeds the device's LDS per workgroup
+(44.1 -> 8 kHz here: 210 KB) takes the per-tap kernel by default and is bit-exact either way.
+Shapes: a 180 s stereo song at 48 kHz to the models' 44.1 kHz, and short inputs for other rate
+pairs, mono, stereo and 3 channels.
 """
 import numpy as np
 import pytest
@@ -37,7 +37,8 @@ def host(t):
 
 
 @pytest.mark.parametrize("src,dst,C,n", [(48000, 44100, 2, 8640000), (22050, 44100, 2, 30001), (44100, 16000, 1, 44100),
-                                         (96000, 44100, 3, 9601), (44100, 48000, 2, 100), (8000, 44100, 1, 37)])
+                                         (96000, 44100, 3, 9601), (44100, 48000, 2, 100), (8000, 44100, 1, 37),
+                                         (44100, 8000, 2, 20001)])
 def test_resample_parity(device, rs, src, dst, C, n, monkeypatch):
     x = synth.sines_plus_pink(src % 1000, C, n) if n > 1000 else synth.normal(src % 1000, (C, n), 0.3)
     r = stx.Resampler(src, dst)
