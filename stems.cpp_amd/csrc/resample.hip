@@ -29,10 +29,11 @@ struct stx_resampler {
     double* d_table = nullptr;       // [kTableN + 2]
     // Phase table (see resample_phase_kernel): dst = up * g, src = down * g.
     int up = 0, down = 0;
-    int ntap = 0, omin = 0;          // taps per phase row; offset of tap 0 from floor(c)
+    int omin = 0;                    // offset of tap 0 from floor(c)
+    int npairs = 0, rs = 0;          // phase pairs (up + 1) / 2; doubles per pair row
     int width = 0, pitch = 0, lds_bytes = 0;  // staged input tile of resample_phase_kernel
-    double* d_phase = nullptr;       // [up][ntap] weights, 0 where a tap is not used
-    int2* d_range = nullptr;         // [up]: first and last used tap of each phase
+    double* d_pair = nullptr;        // [npairs][rs]: the pair's two weight rows interleaved
+    int4* d_prange = nullptr;        // [npairs]: each row's first and last tap
 };
 
 namespace stx {
@@ -106,26 +107,31 @@ __global__ __launch_bounds__(256) void resample_kernel(ResampleArgs a) {
 // row l holds j = (m0 + l) down + omin + r for r < width = down + ntap + kPhaseOverread (zeros
 // outside the input, which add nothing; neighbouring rows overlap by ntap + kPhaseOverread). Rows
 // are `pitch` floats apart, width rounded up to odd, so the lanes of a read fall in different
-// banks. 48 -> 44.1 kHz stages 62 KB: two workgroups of 16 waves, the most waves a CU holds,
-// which the time depends on (8-wave workgroups: 196 us, 4: 358 us). Each of its 16 waves takes the phases q = wave, wave + 16, ...: the phase,
-// hence the weight row, is the same for the whole wave and is read through scalar loads, and
-// lane l reads its taps at row l, r = fq + k. Taps go eight at a time, one 64-byte scalar load of
-// weights and four paired LDS reads each; the last 1-7 taps of a window load a whole chunk (at
-// most 7 samples and weights past the window, inside the row and the padded table) and sum only
-// their own, under uniform branches. Taps outside a phase's window are not summed.
+// banks. 48 -> 44.1 kHz stages 62 KB: two workgroups of 16 waves, the most waves a CU holds.
+//
+// Each wave takes pairs of neighbouring phases q0 = 2 jp, q1 = q0 + 1 (jp = wave, wave + 16, ...).
+// Their windows, at r = fq0 + s and r = fq1 + k, overlap but for a tap or two at each end, so a
+// lane converts each staged sample it reads once and feeds both sums. The host interleaves the
+// pair's weight rows by s (w0(s), w1(s)): eight common taps are two 64-byte scalar loads from one
+// row and four paired LDS reads. Taps in only one window (the pair's ranges, lo0..hi0 and
+// lo1..hi1 in s) go through a guarded loop, so no tap is summed that its phase's window lacks;
+// each sum still takes its taps in order. The last 1-7 common taps load one whole chunk (at most
+// 7 samples and weight pairs past them, inside the row and the padded table) and sum only their
+// own under uniform branches. An odd last phase is paired with itself; its second sum is not
+// stored.
 struct PhaseArgs {
     const float* in;                 // [C][n]
     float* out;                      // [C][out_n]
-    const double* w;                 // [up][ntap] + kPhaseOverread
-    const int2* range;               // [up]: first and last tap of each phase row
+    const double* w;                 // [npairs][rs]: (w0(s), w1(s)) for s < rs / 2
+    const int4* range;               // [npairs]: lo0, hi0, lo1, hi1 in s
     long long n, out_n;
-    int up, down, ntap, omin;
+    int up, down, omin, npairs, rs;
     int width, pitch;                // staged samples per lane row; floats between rows (odd)
     FastDiv fup, fwidth;             // q down / up (below 2^20) and staging index / width (below 2^15)
 };
 
 constexpr int kPhaseTile = 64;                       // output groups per workgroup, one per lane
-constexpr int kPhaseWaves = 16;                      // waves per workgroup, each over up / 16 phases
+constexpr int kPhaseWaves = 16;                      // waves per workgroup, each over up / 32 phase pairs
 constexpr int kPhaseStage = 4;                       // staged loads in flight per thread
 constexpr long long kPhaseMaxWeights = 1 << 18;      // up * ntap above this: per-tap kernel
 constexpr int kPhaseOverread = 8;                    // staged samples and table weights past the last used
@@ -133,6 +139,16 @@ constexpr int kPhaseOverread = 8;                    // staged samples and table
 // The weight table does not change while the kernel runs: read through the constant address
 // space, a wave-uniform load of it is a scalar load into SGPRs.
 typedef const __attribute__((address_space(4))) double* ConstDoubles;
+
+// Taps s0..s1 of which only some lie in each window: each summed where its window has it.
+__device__ __forceinline__ void pair_edge(const float* xr, ConstDoubles wp, int4 rg, int s0, int s1, double& a0,
+                                          double& a1) {
+    for (int s = s0; s <= s1; s++) {
+        const double x = (double)xr[s];
+        if (s >= rg.x && s <= rg.y) a0 = fma(wp[2 * s], x, a0);
+        if (s >= rg.z && s <= rg.w) a1 = fma(wp[2 * s + 1], x, a1);
+    }
+}
 
 __global__ __launch_bounds__(kPhaseWaves * 64) void resample_phase_kernel(PhaseArgs a) {
     extern __shared__ float xs[];
@@ -159,35 +175,52 @@ __global__ __launch_bounds__(kPhaseWaves * 64) void resample_phase_kernel(PhaseA
     __syncthreads();
     const int lane = (int)threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
-    const float* xl = xs + lane * a.pitch;
     float* outc = a.out + (size_t)c * a.out_n;
     const long long i0 = (m0 + lane) * a.up;
-    for (int q = wave; q < a.up; q += kPhaseWaves) {
-        const unsigned qd = (unsigned)q * (unsigned)a.down;
-        const int fq = (int)a.fup.div(qd), p = (int)(qd - (unsigned)fq * (unsigned)a.up);
-        const int2 rg = a.range[p];
-        const ConstDoubles wr = (ConstDoubles)(a.w + (size_t)p * a.ntap - fq);   // indexed by r = fq + k
-        const int e = fq + rg.y;
-        int r = fq + rg.x;
-        double acc = 0.0;
-        for (; r + 7 <= e; r += 8) {
-#pragma unroll
-            for (int t = 0; t < 8; t++) acc = fma(wr[r + t], (double)xl[r + t], acc);
-        }
-        if (r <= e) {
-            float x[8];
-            double w[8];
+    for (int jp = wave; jp < a.npairs; jp += kPhaseWaves) {
+        const int q0 = 2 * jp;
+        const int fq0 = (int)a.fup.div((unsigned)q0 * (unsigned)a.down);
+        const int4 rg = a.range[jp];
+        const ConstDoubles wp = (ConstDoubles)(a.w + (size_t)jp * a.rs);
+        const float* xr = xs + lane * a.pitch + fq0;
+        const int lo_u = min(rg.x, rg.z), hi_u = max(rg.y, rg.w);
+        int lo_i = max(rg.x, rg.z), hi_i = min(rg.y, rg.w);
+        if (lo_i > hi_i) lo_i = hi_u + 1, hi_i = hi_u;            // no common taps: all on the edge path
+        double a0 = 0.0, a1 = 0.0;
+        pair_edge(xr, wp, rg, lo_u, lo_i - 1, a0, a1);
+        int s = lo_i;
+        for (; s + 7 <= hi_i; s += 8) {
+            const ConstDoubles wc = wp + 2 * s;                  // one base, constant offsets: two 64-byte loads
+            const float* xc = xr + s;
 #pragma unroll
             for (int t = 0; t < 8; t++) {
-                x[t] = xl[r + t];
-                w[t] = wr[r + t];
+                const double x = (double)xc[t];
+                a0 = fma(wc[2 * t], x, a0);
+                a1 = fma(wc[2 * t + 1], x, a1);
+            }
+        }
+        if (s <= hi_i) {
+            const ConstDoubles wc = wp + 2 * s;
+            const float* xc = xr + s;
+            float x[8];
+            double w[16];
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                x[t] = xc[t];
+                w[2 * t] = wc[2 * t];
+                w[2 * t + 1] = wc[2 * t + 1];
             }
 #pragma unroll
             for (int t = 0; t < 7; t++)
-                if (r + t <= e) acc = fma(w[t], (double)x[t], acc);
+                if (s + t <= hi_i) {
+                    a0 = fma(w[2 * t], (double)x[t], a0);
+                    a1 = fma(w[2 * t + 1], (double)x[t], a1);
+                }
         }
-        const long long i = i0 + q;
-        if (i < a.out_n) outc[i] = (float)acc;
+        pair_edge(xr, wp, rg, hi_i + 1, hi_u, a0, a1);
+        const long long i = i0 + q0;
+        if (i < a.out_n) outc[i] = (float)a0;
+        if (q0 + 1 < a.up && i + 1 < a.out_n) outc[i + 1] = (float)a1;
     }
 }
 
@@ -275,8 +308,10 @@ STX_API stx_status stx_resampler_create(int src_rate, int dst_rate, stx_resample
                 (void)hipGetLastError();
                 lds_bytes = 0;
             }
+            std::vector<double> pair;
+            std::vector<int4> prange;
             if ((long long)up * ntap <= kPhaseMaxWeights && lds_bytes > 0) {
-                phase.assign((size_t)up * ntap + kPhaseOverread, 0.0);
+                phase.assign((size_t)up * ntap, 0.0);
                 range.assign(up, make_int2(0, -1));
                 for (int p = 0; p < up; p++) {
                     const double frac = (double)p / up;
@@ -293,10 +328,33 @@ STX_API stx_status stx_resampler_create(int src_rate, int dst_rate, stx_resample
                     }
                     range[p] = make_int2(lo, hi);
                 }
+                // Pairs of neighbouring phases q0 = 2 jp and q1 = q0 + 1, whose taps start at
+                // floor(q down / up) + omin: q1's are d = fq1 - fq0 later, so its row goes in at
+                // s = k + d. An odd last phase is paired with itself.
+                auto fq = [&](int q) { return (int)((long long)q * down / up); };
+                const int npairs = (up + 1) / 2;
+                int dmax = 0;
+                for (int jp = 0; jp < npairs; jp++)
+                    if (2 * jp + 1 < up) dmax = std::max(dmax, fq(2 * jp + 1) - fq(2 * jp));
+                const int rs = 2 * (ntap + dmax + kPhaseOverread);
+                pair.assign((size_t)npairs * rs, 0.0);
+                prange.resize(npairs);
+                for (int jp = 0; jp < npairs; jp++) {
+                    const int q0 = 2 * jp, q1 = q0 + 1 < up ? q0 + 1 : q0;
+                    const int p0 = (int)((long long)q0 * down % up), p1 = (int)((long long)q1 * down % up);
+                    const int d = fq(q1) - fq(q0);
+                    double* row = pair.data() + (size_t)jp * rs;
+                    for (int k = range[p0].x; k <= range[p0].y; k++) row[2 * k] = phase[(size_t)p0 * ntap + k];
+                    if (q1 != q0)
+                        for (int k = range[p1].x; k <= range[p1].y; k++)
+                            row[2 * (k + d) + 1] = phase[(size_t)p1 * ntap + k];
+                    prange[jp] = make_int4(range[p0].x, range[p0].y, d + range[p1].x, d + range[p1].y);
+                }
                 r->up = up;
                 r->down = down;
-                r->ntap = ntap;
                 r->omin = omin;
+                r->npairs = npairs;
+                r->rs = rs;
                 r->width = width;
                 r->pitch = pitch;
                 r->lds_bytes = lds_bytes;
@@ -304,13 +362,13 @@ STX_API stx_status stx_resampler_create(int src_rate, int dst_rate, stx_resample
             hipError_t e = hipMalloc(&r->d_table, sizeof(double) * table.size());
             if (e == hipSuccess)
                 e = hipMemcpy(r->d_table, table.data(), sizeof(double) * table.size(), hipMemcpyHostToDevice);
-            if (e == hipSuccess && !phase.empty()) {
-                e = hipMalloc(&r->d_phase, sizeof(double) * phase.size());
-                if (e == hipSuccess) e = hipMalloc(&r->d_range, sizeof(int2) * range.size());
+            if (e == hipSuccess && !pair.empty()) {
+                e = hipMalloc(&r->d_pair, sizeof(double) * pair.size());
+                if (e == hipSuccess) e = hipMalloc(&r->d_prange, sizeof(int4) * prange.size());
                 if (e == hipSuccess)
-                    e = hipMemcpy(r->d_phase, phase.data(), sizeof(double) * phase.size(), hipMemcpyHostToDevice);
+                    e = hipMemcpy(r->d_pair, pair.data(), sizeof(double) * pair.size(), hipMemcpyHostToDevice);
                 if (e == hipSuccess)
-                    e = hipMemcpy(r->d_range, range.data(), sizeof(int2) * range.size(), hipMemcpyHostToDevice);
+                    e = hipMemcpy(r->d_prange, prange.data(), sizeof(int4) * prange.size(), hipMemcpyHostToDevice);
             }
             if (e != hipSuccess) {
                 stx_resampler_destroy(r);
@@ -324,8 +382,8 @@ STX_API stx_status stx_resampler_create(int src_rate, int dst_rate, stx_resample
 STX_API void stx_resampler_destroy(stx_resampler* r) {
     if (!r) return;
     if (r->d_table) (void)hipFree(r->d_table);
-    if (r->d_phase) (void)hipFree(r->d_phase);
-    if (r->d_range) (void)hipFree(r->d_range);
+    if (r->d_pair) (void)hipFree(r->d_pair);
+    if (r->d_prange) (void)hipFree(r->d_prange);
     delete r;
 }
 
@@ -358,8 +416,8 @@ STX_API stx_status stx_resample(const stx_resampler* r, const float* in, int cha
         // The phase table unless STX_RESAMPLE_EXACT=1 (read at each call) asks for the per-tap
         // kernel, which gives the reference's bits.
         const char* exact = std::getenv("STX_RESAMPLE_EXACT");
-        if (r->d_phase && !(exact && exact[0] == '1')) {
-            PhaseArgs pa{in, out, r->d_phase, r->d_range, n, out_n, r->up, r->down, r->ntap, r->omin, r->width, r->pitch,
+        if (r->d_pair && !(exact && exact[0] == '1')) {
+            PhaseArgs pa{in, out, r->d_pair, r->d_prange, n, out_n, r->up, r->down, r->omin, r->npairs, r->rs, r->width, r->pitch,
                          FastDiv((unsigned)r->up), FastDiv((unsigned)r->width)};
             const long long groups = (out_n + r->up - 1) / r->up;                // output groups M
             STX_REQUIRE(channels < 65536, "too many channels");
