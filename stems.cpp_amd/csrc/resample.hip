@@ -127,18 +127,19 @@ struct PhaseArgs {
     long long n, out_n;
     int up, down, omin, npairs, rs;
     int width, pitch;                // staged samples per lane row; floats between rows (odd)
-    FastDiv fup, fwidth;             // q down / up (below 2^20) and staging index / width (below 2^15)
+    FastDiv fup;                     // q down / up (below 2^20)
 };
 
 constexpr int kPhaseTile = 64;                       // output groups per workgroup, one per lane
 constexpr int kPhaseWaves = 16;                      // waves per workgroup, each over up / 32 phase pairs
-constexpr int kPhaseStage = 4;                       // staged loads in flight per thread
+constexpr int kPhaseStage = 4;                       // staged loads in flight per lane
 constexpr long long kPhaseMaxWeights = 1 << 18;      // up * ntap above this: per-tap kernel
 constexpr int kPhaseOverread = 8;                    // staged samples and table weights past the last used
 
-// The weight table does not change while the kernel runs: read through the constant address
-// space, a wave-uniform load of it is a scalar load into SGPRs.
+// The weight table and the pair ranges do not change while the kernel runs: read through the
+// constant address space, a wave-uniform load of them is a scalar load into SGPRs.
 typedef const __attribute__((address_space(4))) double* ConstDoubles;
+typedef const __attribute__((address_space(4))) int* ConstInts;
 
 // Taps s0..s1 of which only some lie in each window: each summed where its window has it.
 __device__ __forceinline__ void pair_edge(const float* xr, ConstDoubles wp, int4 rg, int s0, int s1, double& a0,
@@ -152,35 +153,41 @@ __device__ __forceinline__ void pair_edge(const float* xr, ConstDoubles wp, int4
 
 __global__ __launch_bounds__(kPhaseWaves * 64) void resample_phase_kernel(PhaseArgs a) {
     extern __shared__ float xs[];
-    constexpr int NT = kPhaseWaves * 64;
     const int c = (int)blockIdx.y;
     const long long m0 = (long long)blockIdx.x * kPhaseTile;
     const float* in = a.in + (size_t)c * a.n;
-    const int staged = kPhaseTile * a.width;
-    for (int s0 = (int)threadIdx.x; s0 < staged; s0 += NT * kPhaseStage) {
-        float v[kPhaseStage];
-        int at[kPhaseStage];
-#pragma unroll
-        for (int u = 0; u < kPhaseStage; u++) {
-            const int st = s0 + u * NT;
-            const int l = (int)a.fwidth.div((unsigned)st), r = st - l * a.width;
-            const long long j = (m0 + l) * a.down + a.omin + r;
-            v[u] = st < staged && j >= 0 && j < a.n ? in[j] : 0.0f;
-            at[u] = l * a.pitch + r;
-        }
-#pragma unroll
-        for (int u = 0; u < kPhaseStage; u++)
-            if (s0 + u * NT < staged) xs[at[u]] = v[u];
-    }
-    __syncthreads();
     const int lane = (int)threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    // Each wave stages whole rows: the row's first input index and its bounds are the same for
+    // the wave, so a sample costs an offset and, at the input's ends only, a bounds test.
+    for (int l = wave; l < kPhaseTile; l += kPhaseWaves) {
+        const long long jb = (m0 + l) * a.down + a.omin;        // input index of r = 0
+        const float* src = in + jb;
+        float* dst = xs + l * a.pitch;
+        const bool inside = jb >= 0 && jb + a.width <= a.n;
+        const int rlo = (int)max(-jb, 0LL), rhi = (int)min(a.n - jb, (long long)a.width);   // r in [rlo, rhi) is input
+        for (int r0 = 0; r0 < a.width; r0 += 64 * kPhaseStage) {
+            float v[kPhaseStage];
+#pragma unroll
+            for (int u = 0; u < kPhaseStage; u++) {
+                const int r = r0 + u * 64 + lane;
+                v[u] = r < a.width && (inside || (r >= rlo && r < rhi)) ? src[r] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < kPhaseStage; u++) {
+                const int r = r0 + u * 64 + lane;
+                if (r < a.width) dst[r] = v[u];
+            }
+        }
+    }
+    __syncthreads();
     float* outc = a.out + (size_t)c * a.out_n;
     const long long i0 = (m0 + lane) * a.up;
     for (int jp = wave; jp < a.npairs; jp += kPhaseWaves) {
         const int q0 = 2 * jp;
         const int fq0 = (int)a.fup.div((unsigned)q0 * (unsigned)a.down);
-        const int4 rg = a.range[jp];
+        const ConstInts rgp = (ConstInts)a.range + 4 * jp;
+        const int4 rg = make_int4(rgp[0], rgp[1], rgp[2], rgp[3]);
         const ConstDoubles wp = (ConstDoubles)(a.w + (size_t)jp * a.rs);
         const float* xr = xs + lane * a.pitch + fq0;
         const int lo_u = min(rg.x, rg.z), hi_u = max(rg.y, rg.w);
@@ -418,7 +425,7 @@ STX_API stx_status stx_resample(const stx_resampler* r, const float* in, int cha
         const char* exact = std::getenv("STX_RESAMPLE_EXACT");
         if (r->d_pair && !(exact && exact[0] == '1')) {
             PhaseArgs pa{in, out, r->d_pair, r->d_prange, n, out_n, r->up, r->down, r->omin, r->npairs, r->rs, r->width, r->pitch,
-                         FastDiv((unsigned)r->up), FastDiv((unsigned)r->width)};
+                         FastDiv((unsigned)r->up)};
             const long long groups = (out_n + r->up - 1) / r->up;                // output groups M
             STX_REQUIRE(channels < 65536, "too many channels");
             const long long tiles = (groups + kPhaseTile - 1) / kPhaseTile;
