@@ -57,6 +57,37 @@ def test_resample_parity(device, rs, src, dst, C, n, monkeypatch):
     assert np.array_equal(exact, want)
 
 
+@pytest.mark.parametrize("src,dst,C,n", [(48000, 44100, 2, 48001), (44100, 48000, 1, 44101), (22050, 44100, 2, 3001),
+                                         (96000, 44100, 3, 9601)])
+def test_resample_nonfinite(device, rs, src, dst, C, n, monkeypatch):
+    """NaN, +inf and -inf samples (NaN at each end) reach exactly the outputs whose window holds
+    them in the reference (src/audio.h:44-52): the phase kernel's pair loop sums a tap only where
+    its own phase's window has it, so the NaN and infinite outputs are the oracle's and the finite
+    outputs keep the usual bound; the per-tap kernel is bit-identical, NaNs included.
+
+    An infinite output's sign is its tap's weight's. At a zero of the kernel the reference's weight
+    and the exact phase's are both below 1e-14 and may differ in sign (a restatement of both
+    weight formulas finds 2, 0, 0 and 3 such taps for these cases), so up to one sign per infinite
+    input sample may differ."""
+    x = synth.normal(src % 997, (C, n), 0.3)
+    for c in range(C):
+        x[c, [0, n // 3 + c, n // 2 + 7 * c, n - 1]] = [np.nan, np.inf, -np.inf, np.nan]
+    r = stx.Resampler(src, dst)
+    xd = dev(x, device)
+    want = rs(x, src, dst)
+    got = host(r(xd))
+    assert np.isnan(want).any() and np.isinf(want).any()
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    inf = np.isinf(want)
+    assert np.array_equal(np.isinf(got), inf)
+    assert int(np.sum(np.sign(got[inf]) != np.sign(want[inf]))) <= 2 * C     # 2 infinite samples per channel
+    fin = np.isfinite(want)
+    rms = float(np.sqrt(np.mean(want[fin].astype(np.float64) ** 2)))
+    assert float(np.max(np.abs(got[fin].astype(np.float64) - want[fin]))) <= 1e-6 * rms
+    monkeypatch.setenv("STX_RESAMPLE_EXACT", "1")
+    assert np.array_equal(host(r(xd)), want, equal_nan=True)
+
+
 def test_equal_rates_copy(device):
     x = synth.normal(3, (2, 1000), 1.0)
     r = stx.Resampler(44100, 44100)
