@@ -447,7 +447,8 @@ STX_API size_t stx_htdemucs_norm_workspace_size(int64_t n);
  * stx_htdemucs_norm_workspace_size(2 C F T) bytes, no initialisation needed; calls that share one
  * must not overlap. A segment that fits on the device at once (and whose output does not
  * overlap its input) is normalised by one grid-synchronised kernel, with the bounded waits and
- * the same-bits fallback of stx_group_norm; the rest take three kernels. */
+ * the same-bits fallback of stx_group_norm; the rest take two kernels (moments, then the
+ * normalisation, each of whose blocks adds the moments' partial sums itself). */
 STX_API stx_status stx_htdemucs_cac_normalize(const float* spec, int channels, int n_bins, int n_frames, float* mag,
                                               double* stats, void* workspace, size_t workspace_bytes,
                                               stx_stream stream);

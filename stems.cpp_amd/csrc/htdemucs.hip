@@ -117,11 +117,13 @@ __global__ __launch_bounds__(256) void moments_kernel(MomArgs a) {
 
 enum NormKind { NORM_CAC = 0, NORM_FLAT = 1, NORM_MIX = 2 };
 
-// One block adds the pass-1 pairs in a fixed order and writes {mean, sd}: the unbiased std,
-// floored at 1e-8 for the mix (std::max(std, 1e-8) keeps a NaN, as here).
+// {mean, den} from the pass-1 pairs, added in a fixed order (thread t takes pairs t, t + 256, ...,
+// then the block sum), so every block that calls it gets the same bits; the unbiased std,
+// floored at 1e-8 for the mix (std::max(std, 1e-8) keeps a NaN, as here); den = 1e-5 + sd
+// (spectrum, waveform) or the floored sd (mix). Block (0, 0) writes {mean, sd} to stats.
 template <int KIND>
-__global__ __launch_bounds__(256) void moments_final_kernel(MomArgs a, int n_partial, double* stats) {
-    __shared__ double red[4];
+__device__ __forceinline__ void fold_stats(const MomArgs& a, int n_partial, double* stats, double& mean, double& den,
+                                           double* red) {
     double s = 0.0, q = 0.0;
     for (int b = (int)threadIdx.x; b < n_partial; b += 256) {
         s += a.partial[2 * b];
@@ -129,39 +131,45 @@ __global__ __launch_bounds__(256) void moments_final_kernel(MomArgs a, int n_par
     }
     s = block_sum(s, red);
     q = block_sum(q, red);
-    if (threadIdx.x == 0) {
-        const double shift = KIND == NORM_MIX ? (double)mono_at(a.x, a.n, a.C, 0) : (double)a.x[0];
-        const double n = (double)a.n;
-        double sd = sqrt(fmax(q - s * (s / n), 0.0) / (n - 1.0));
-        if (KIND == NORM_MIX) sd = sd < 1e-8 ? 1e-8 : sd;
-        stats[0] = shift + s / n;
+    const double shift = KIND == NORM_MIX ? (double)mono_at(a.x, a.n, a.C, 0) : (double)a.x[0];
+    const double n = (double)a.n;
+    double sd = sqrt(fmax(q - s * (s / n), 0.0) / (n - 1.0));
+    if (KIND == NORM_MIX) sd = sd < 1e-8 ? 1e-8 : sd;
+    mean = shift + s / n;
+    den = KIND == NORM_MIX ? sd : 1e-5 + sd;
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
+        stats[0] = mean;
         stats[1] = sd;
     }
 }
 
-constexpr int kNormPer = 8;
+constexpr int kNormPer = 8;                      // elementwise kernels: values per thread
+constexpr int kFoldPer = 32;                     // normalize_kernel: values per thread (8192 per block)
 
-// (v - mean) / den with den = 1e-5 + sd (spectrum, waveform) or the floored sd (mix), in
-// double and rounded once. CAC: blockIdx.y is the channel, its re and im go to planes 2c and
+// Pass 2: (v - mean) / den in double, rounded once. Each block issues its loads, then folds the
+// pass-1 pairs itself (fold_stats: the same bits in every block, from the L2), so no kernel
+// runs between the passes. CAC: blockIdx.y is the channel, its re and im go to planes 2c and
 // 2c + 1. FLAT / MIX: a flat walk.
 template <int KIND>
-__global__ __launch_bounds__(256) void normalize_kernel(const float* x, float* y, long long count, const double* stats) {
-    const double mean = stats[0];
-    const double den = KIND == NORM_MIX ? stats[1] : 1e-5 + stats[1];
-    // den is positive (or NaN): the moments of finite floats cannot overflow, so div_rn gives the
-    // IEEE quotient with one reciprocal per thread.
-    const double rden = 1.0 / den;
-    const long long e0 = (long long)blockIdx.x * (256 * kNormPer) + threadIdx.x;
+__global__ __launch_bounds__(256) void normalize_kernel(MomArgs m, int n_partial, const float* x, float* y,
+                                                        long long count, double* stats) {
+    __shared__ double red[4];
+    const long long e0 = (long long)blockIdx.x * (256 * kFoldPer) + threadIdx.x;
     if (KIND == NORM_CAC) {
         const long long c = blockIdx.y;
         const float2* src = reinterpret_cast<const float2*>(x) + c * count;
         float* re = y + 2 * c * count;
         float* im = re + count;
-        float2 v[kNormPer];
+        float2 v[kFoldPer];
 #pragma unroll
-        for (int k = 0; k < kNormPer; k++) v[k] = src[min(e0 + 256LL * k, count - 1)];
+        for (int k = 0; k < kFoldPer; k++) v[k] = src[min(e0 + 256LL * k, count - 1)];
+        double mean, den;
+        fold_stats<KIND>(m, n_partial, stats, mean, den, red);
+        // den is positive (or NaN): the moments of finite floats cannot overflow, so div_rn
+        // gives the IEEE quotient with one reciprocal per thread.
+        const double rden = 1.0 / den;
 #pragma unroll
-        for (int k = 0; k < kNormPer; k++) {
+        for (int k = 0; k < kFoldPer; k++) {
             const long long e = e0 + 256LL * k;
             if (e < count) {
                 store_stream(re + e, (float)div_rn((double)v[k].x - mean, den, rden));
@@ -169,11 +177,14 @@ __global__ __launch_bounds__(256) void normalize_kernel(const float* x, float* y
             }
         }
     } else {
-        float v[kNormPer];
+        float v[kFoldPer];
 #pragma unroll
-        for (int k = 0; k < kNormPer; k++) v[k] = x[min(e0 + 256LL * k, count - 1)];
+        for (int k = 0; k < kFoldPer; k++) v[k] = x[min(e0 + 256LL * k, count - 1)];
+        double mean, den;
+        fold_stats<KIND>(m, n_partial, stats, mean, den, red);
+        const double rden = 1.0 / den;
 #pragma unroll
-        for (int k = 0; k < kNormPer; k++) {
+        for (int k = 0; k < kFoldPer; k++) {
             const long long e = e0 + 256LL * k;
             if (e < count) store_stream(y + e, (float)div_rn((double)v[k] - mean, den, rden));
         }
@@ -300,8 +311,8 @@ __device__ __forceinline__ void norm_fused_body(const float* x, float* y, unsign
 
 // One launch of moments + normalise for NORM_CAC / NORM_FLAT: x is n floats (CAC: the complex64
 // spectrum [C][ft] read as 2 C ft floats), VEC float4 per thread in chunks of kGridThreads * 4 *
-// VEC floats. Same statistics formulas as moments_final_kernel and the same per-element division
-// as normalize_kernel; block 0 writes {mean, sd} to stats.
+// VEC floats. Same statistics formulas as fold_stats and the same per-element division as
+// normalize_kernel; block 0 writes {mean, sd} to stats.
 template <int KIND, int VEC>
 __global__ __launch_bounds__(kGridThreads) void norm_fused_kernel(const float* x, float* y, unsigned n, unsigned ft,
                                                                   FastDiv cdiv, double* stats, GridSync f) {
@@ -604,12 +615,10 @@ void normalize(const float* x, long long n_mom, long long count, int C, float* y
         hipLaunchKernelGGL((moments_kernel<MK, 0>), dim3((unsigned)nb), dim3(256), 0, s, m);
     }
     launch_check("moments_kernel");
-    hipLaunchKernelGGL((moments_final_kernel<NK>), dim3(1), dim3(256), 0, s, m, (int)nb, stats);
-    launch_check("moments_final_kernel");
-    const long long blocks = (count + 256 * kNormPer - 1) / (256 * kNormPer);
+    const long long blocks = (count + 256 * kFoldPer - 1) / (256 * kFoldPer);
     STX_REQUIRE(blocks < (1LL << 31), "normalise: too many elements");
     hipLaunchKernelGGL((normalize_kernel<NK>), dim3((unsigned)blocks, NK == NORM_CAC ? (unsigned)C : 1u), dim3(256),
-                       0, s, x, y, count, stats);
+                       0, s, m, (int)nb, x, y, count, stats);
     launch_check("normalize_kernel");
 }
 
