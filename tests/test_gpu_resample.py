@@ -38,7 +38,8 @@ def host(t):
 
 @pytest.mark.parametrize("src,dst,C,n", [(48000, 44100, 2, 8640000), (22050, 44100, 2, 30001), (44100, 16000, 1, 44100),
                                          (96000, 44100, 3, 9601), (44100, 48000, 2, 100), (8000, 44100, 1, 37),
-                                         (44100, 8000, 2, 20001)])
+                                         (44100, 8000, 2, 20001), (48000, 44100, 2, 1), (44100, 48000, 1, 2),
+                                         (22050, 44100, 1, 1)])
 def test_resample_parity(device, rs, src, dst, C, n, monkeypatch):
     x = synth.sines_plus_pink(src % 1000, C, n) if n > 1000 else synth.normal(src % 1000, (C, n), 0.3)
     r = stx.Resampler(src, dst)
