@@ -577,25 +577,33 @@ __global__ __launch_bounds__(kMixedThreads) void istft_frames_mixed_kernel(Istft
     tws.load(twm, tid);
     const int c = f / a.T, st = f - c * a.T;
     const float2* sc = a.spec + (size_t)c * a.T * a.F;
-    // Every spectrum and twiddle load (clamped to valid bins) before the first LDS write.
+    // Bins 0..M, each loaded once (clamped to valid bins) and staged in b1, and the twiddles, all
+    // issued before the first LDS write; the inverse split then takes X[k] and X[M - k] from
+    // LDS. In the f-major layout each bin is its own 8-byte request to the L2, so loading X[k]
+    // and X[M - k] from memory, as two loads per bin, doubled the requests the kernel waits on.
     constexpr int RL = (MAXM + kMixedThreads - 1) / kMixedThreads;
-    float2 xk[RL], xm[RL], tw[RL];
+    constexpr int RB = (MAXM + 1 + kMixedThreads - 1) / kMixedThreads;
+    float2 xb[RB], tw[RL];
 #pragma unroll
-    for (int q = 0; q < RL; q++) {
-        const int k = min(tid + q * kMixedThreads, M - 1);
-        xk[q] = spec_bin(a, sc, st, k);
-        xm[q] = spec_bin(a, sc, st, min(M - k, a.F - 1));
-        tw[q] = twn[k];
+    for (int q = 0; q < RB; q++) xb[q] = spec_bin(a, sc, st, min(min(tid + q * kMixedThreads, M), a.F - 1));
+#pragma unroll
+    for (int q = 0; q < RL; q++) tw[q] = twn[min(tid + q * kMixedThreads, M - 1)];
+#pragma unroll
+    for (int q = 0; q < RB; q++) {
+        const int k = tid + q * kMixedThreads;
+        if (k > M) break;
+        b1[mixed_pad(k)] = xb[q];
     }
+    tws.store(twl, tid);
+    __syncthreads();
 #pragma unroll
     for (int q = 0; q < RL; q++) {
         const int k = tid + q * kMixedThreads;
         if (k >= M) break;
-        const float2 m = k == 0 && !a.keep_nyquist ? make_float2(0.f, 0.f) : xm[q];
-        b0[mixed_pad(k)] = inverse_split_w(xk[q], m, k, a.keep_nyquist, tw[q]);
+        const float2 m = k == 0 && !a.keep_nyquist ? make_float2(0.f, 0.f) : b1[mixed_pad(M - k)];
+        b0[mixed_pad(k)] = inverse_split_w(b1[mixed_pad(k)], m, k, a.keep_nyquist, tw[q]);
     }
-    tws.store(twl, tid);
-    __syncthreads();
+    __syncthreads();                                   // b1 read before the first pass writes it
     const float2* r;
     if constexpr (CTM != 0) r = CT::template run<kMixedThreads, 2>(b0, b1, twl, tid);
     else r = mixed_fft<MAXM, kMixedThreads>(b0, b1, M, p, 2, twl, tid);
