@@ -561,60 +561,89 @@ __global__ __launch_bounds__(kMixedThreads) void stft_mixed_kernel(StftArgs a, M
     }
 }
 
-template <int MAXM, class CT>
-__global__ __launch_bounds__(kMixedThreads) void istft_frames_mixed_kernel(IstftArgs a, MixedRadix p,
-                                                                           const float2* __restrict__ twn,
-                                                                           const float2* __restrict__ twm, int n_rt,
-                                                                           int jobs) {
-    __shared__ float2 b0[mixed_padded(MAXM)], b1[mixed_padded(MAXM)];
+// FPB frames per block. FPB = 2 (f-major, T even, 16-byte aligned spectrum): the block's frames
+// are st and st + 1 of one channel, adjacent in every bin row, so each bin of both arrives in one
+// 16-byte load, half the L2 requests of one frame per block; each half of the block (512 threads)
+// then runs its frame's inverse split, transform and windowed store in its own buffers.
+template <int MAXM, class CT, int FPB>
+__global__ __launch_bounds__(kMixedThreads * FPB) void istft_frames_mixed_kernel(IstftArgs a, MixedRadix p,
+                                                                                 const float2* __restrict__ twn,
+                                                                                 const float2* __restrict__ twm,
+                                                                                 int n_rt, int jobs) {
+    __shared__ float2 b0s[FPB][mixed_padded(MAXM)], b1s[FPB][mixed_padded(MAXM)];
     __shared__ float2 twl[kMixedTwMax];
+    constexpr int NT = kMixedThreads;
     constexpr int CTM = MixedM<CT>::value;
     const int n = CTM ? 2 * CTM : n_rt;
-    const int M = n / 2, tid = (int)threadIdx.x;
-    const int f = xcd_block();                         // channel * T + frame
-    if (f >= jobs) return;                             // whole block idle: no barrier reached
-    Staged<kMixedTwMax, kMixedThreads, float2> tws;
-    tws.load(twm, tid);
+    const int M = n / 2, tall = (int)threadIdx.x, half = tall / NT, tid = tall - half * NT;
+    const int f0 = xcd_block() * FPB;                  // first frame (channel * T + frame) of the block
+    if (f0 >= jobs) return;                            // whole block idle: no barrier reached
+    const int f = f0 + half;
+    float2* b0 = b0s[half];
+    float2* b1 = b1s[half];
+    Staged<kMixedTwMax, NT * FPB, float2> tws;
+    tws.load(twm, tall);
     const int c = f / a.T, st = f - c * a.T;
     const float2* sc = a.spec + (size_t)c * a.T * a.F;
     // Bins 0..M, each loaded once (clamped to valid bins) and staged in b1, and the twiddles, all
     // issued before the first LDS write; the inverse split then takes X[k] and X[M - k] from
-    // LDS. In the f-major layout each bin is its own 8-byte request to the L2, so loading X[k]
-    // and X[M - k] from memory, as two loads per bin, doubled the requests the kernel waits on.
-    constexpr int RL = (MAXM + kMixedThreads - 1) / kMixedThreads;
-    constexpr int RB = (MAXM + 1 + kMixedThreads - 1) / kMixedThreads;
-    float2 xb[RB], tw[RL];
+    // LDS. In the f-major layout each bin is its own request to the L2, so loading X[k] and
+    // X[M - k] from memory, as two loads per bin, doubled the requests the kernel waits on.
+    constexpr int RL = (MAXM + NT - 1) / NT;
+    float2 tw[RL];
+    if constexpr (FPB == 2) {
+        constexpr int RB = (MAXM + 1 + 2 * NT - 1) / (2 * NT);
+        const float2* sp = sc + st - half;             // frame st of half 0 (even)
+        float4 xb[RB];
 #pragma unroll
-    for (int q = 0; q < RB; q++) xb[q] = spec_bin(a, sc, st, min(min(tid + q * kMixedThreads, M), a.F - 1));
+        for (int q = 0; q < RB; q++) {
+            const int k = min(min(tall + q * 2 * NT, M), a.F - 1);
+            xb[q] = *reinterpret_cast<const float4*>(sp + (size_t)k * a.T);
+        }
 #pragma unroll
-    for (int q = 0; q < RL; q++) tw[q] = twn[min(tid + q * kMixedThreads, M - 1)];
+        for (int q = 0; q < RL; q++) tw[q] = twn[min(tid + q * NT, M - 1)];
 #pragma unroll
-    for (int q = 0; q < RB; q++) {
-        const int k = tid + q * kMixedThreads;
-        if (k > M) break;
-        b1[mixed_pad(k)] = xb[q];
+        for (int q = 0; q < RB; q++) {
+            const int k = tall + q * 2 * NT;
+            if (k > M) break;
+            b1s[0][mixed_pad(k)] = make_float2(xb[q].x, xb[q].y);
+            b1s[1][mixed_pad(k)] = make_float2(xb[q].z, xb[q].w);
+        }
+    } else {
+        constexpr int RB = (MAXM + 1 + NT - 1) / NT;
+        float2 xb[RB];
+#pragma unroll
+        for (int q = 0; q < RB; q++) xb[q] = spec_bin(a, sc, st, min(min(tid + q * NT, M), a.F - 1));
+#pragma unroll
+        for (int q = 0; q < RL; q++) tw[q] = twn[min(tid + q * NT, M - 1)];
+#pragma unroll
+        for (int q = 0; q < RB; q++) {
+            const int k = tid + q * NT;
+            if (k > M) break;
+            b1[mixed_pad(k)] = xb[q];
+        }
     }
-    tws.store(twl, tid);
+    tws.store(twl, tall);
     __syncthreads();
 #pragma unroll
     for (int q = 0; q < RL; q++) {
-        const int k = tid + q * kMixedThreads;
+        const int k = tid + q * NT;
         if (k >= M) break;
         const float2 m = k == 0 && !a.keep_nyquist ? make_float2(0.f, 0.f) : b1[mixed_pad(M - k)];
         b0[mixed_pad(k)] = inverse_split_w(b1[mixed_pad(k)], m, k, a.keep_nyquist, tw[q]);
     }
     __syncthreads();                                   // b1 read before the first pass writes it
     const float2* r;
-    if constexpr (CTM != 0) r = CT::template run<kMixedThreads, 2>(b0, b1, twl, tid);
-    else r = mixed_fft<MAXM, kMixedThreads>(b0, b1, M, p, 2, twl, tid);
+    if constexpr (CTM != 0) r = CT::template run<NT, 2>(b0, b1, twl, tid);
+    else r = mixed_fft<MAXM, NT>(b0, b1, M, p, 2, twl, tid);
     float* dst = a.frames + (size_t)f * n;
     const float2* win2 = reinterpret_cast<const float2*>(a.win);
     float2 wv[RL];
 #pragma unroll
-    for (int q = 0; q < RL; q++) wv[q] = win2[min(tid + q * kMixedThreads, M - 1)];
+    for (int q = 0; q < RL; q++) wv[q] = win2[min(tid + q * NT, M - 1)];
 #pragma unroll
     for (int q = 0; q < RL; q++) {                     // windowed as WindowPost
-        const int i = tid + q * kMixedThreads;
+        const int i = tid + q * NT;
         if (i >= M) break;
         const float2 ri = r[mixed_pad(i)];
         dst[2 * i] = ri.x * wv[q].x * a.norm;
@@ -878,19 +907,35 @@ void run_istft(const stx_fft* f, IstftArgs a, int channels, void* workspace, siz
         check_extent((long long)channels * a.T * f->n, "workspace");
         a.frames = static_cast<float*>(workspace);
         const int jobs = channels * a.T;
-        const unsigned grid = (unsigned)((jobs + kXcds - 1) / kXcds * kXcds);   // xcd_block's multiple
-        if (f->n == 2 * MixedCt3840::M && mixed_plan_is(f->half, MixedCt3840::radix, MixedCt3840::count))
-            hipLaunchKernelGGL((istft_frames_mixed_kernel<4096, MixedCt3840>), dim3(grid), dim3(kMixedThreads), 0, s, a,
-                               f->half, f->twn, f->twm, f->n, jobs);
+        // Two frames per block where a bin's two frames are one aligned 16-byte load (f-major, T
+        // even) and both frames' buffers fit in LDS (n / 2 <= 4096).
+        const bool pair = a.layout == STX_SPEC_F_MAJOR && a.T % 2 == 0 && f->n / 2 <= 4096 &&
+                          (reinterpret_cast<uintptr_t>(a.spec) & 15) == 0;
+        const int blocks = pair ? jobs / 2 : jobs;
+        const unsigned grid = (unsigned)((blocks + kXcds - 1) / kXcds * kXcds);   // xcd_block's multiple
+        const dim3 bd(kMixedThreads * (pair ? 2 : 1));
+        const bool ct = f->n == 2 * MixedCt3840::M && mixed_plan_is(f->half, MixedCt3840::radix, MixedCt3840::count);
+        if (ct && pair)
+            hipLaunchKernelGGL((istft_frames_mixed_kernel<4096, MixedCt3840, 2>), dim3(grid), bd, 0, s, a, f->half, f->twn,
+                               f->twm, f->n, jobs);
+        else if (ct)
+            hipLaunchKernelGGL((istft_frames_mixed_kernel<4096, MixedCt3840, 1>), dim3(grid), bd, 0, s, a, f->half, f->twn,
+                               f->twm, f->n, jobs);
+        else if (f->n / 2 <= 1024 && pair)
+            hipLaunchKernelGGL((istft_frames_mixed_kernel<1024, void, 2>), dim3(grid), bd, 0, s, a, f->half, f->twn,
+                               f->twm, f->n, jobs);
         else if (f->n / 2 <= 1024)
-            hipLaunchKernelGGL((istft_frames_mixed_kernel<1024, void>), dim3(grid), dim3(kMixedThreads), 0, s, a, f->half,
-                               f->twn, f->twm, f->n, jobs);
+            hipLaunchKernelGGL((istft_frames_mixed_kernel<1024, void, 1>), dim3(grid), bd, 0, s, a, f->half, f->twn,
+                               f->twm, f->n, jobs);
+        else if (f->n / 2 <= 4096 && pair)
+            hipLaunchKernelGGL((istft_frames_mixed_kernel<4096, void, 2>), dim3(grid), bd, 0, s, a, f->half, f->twn,
+                               f->twm, f->n, jobs);
         else if (f->n / 2 <= 4096)
-            hipLaunchKernelGGL((istft_frames_mixed_kernel<4096, void>), dim3(grid), dim3(kMixedThreads), 0, s, a, f->half,
-                               f->twn, f->twm, f->n, jobs);
+            hipLaunchKernelGGL((istft_frames_mixed_kernel<4096, void, 1>), dim3(grid), bd, 0, s, a, f->half, f->twn,
+                               f->twm, f->n, jobs);
         else
-            hipLaunchKernelGGL((istft_frames_mixed_kernel<8192, void>), dim3(grid), dim3(kMixedThreads), 0, s, a, f->half,
-                               f->twn, f->twm, f->n, jobs);
+            hipLaunchKernelGGL((istft_frames_mixed_kernel<8192, void, 1>), dim3(grid), bd, 0, s, a, f->half, f->twn,
+                               f->twm, f->n, jobs);
         launch_check("istft_frames_mixed_kernel");
         hipLaunchKernelGGL(istft_ola_kernel, dim3((a.out_len + 255) / 256, channels), dim3(256), 0, s, a, f->n);
         launch_check("istft_ola_kernel");

@@ -289,8 +289,11 @@ def test_torch_stft_7680_kim_chunk(device, orc, layout, normalized):
 
 
 @pytest.mark.parametrize("n,hop", [(320, 80), (640, 160), (960, 240), (1536, 256)])
-def test_torch_stft_vr_sizes_round_trip(device, orc, n, hop):
-    length = 20 * n + 3
+@pytest.mark.parametrize("extra", [3, "hop"])
+def test_torch_stft_vr_sizes_round_trip(device, orc, n, hop, extra):
+    """An odd frame count (length 20 n + 3) and an even one (20 n + hop): the f-major iSTFT
+    transforms two frames per block when the count is even."""
+    length = 20 * n + (hop if extra == "hop" else extra)
     x = _stereo(n, length, 0.5)
     f = any_plan(n)
     spec = stx.torch_stft(f, to_dev(x, device), hop)
