@@ -523,41 +523,64 @@ __device__ __forceinline__ int padded_index_rt(int m, const StftArgs& a, int n) 
 template <class CT> struct MixedM { static constexpr int value = CT::M; };
 template <> struct MixedM<void> { static constexpr int value = 0; };
 
-template <int MAXM, class CT>
-__global__ __launch_bounds__(kMixedThreads) void stft_mixed_kernel(StftArgs a, MixedRadix p,
-                                                                   const float2* __restrict__ twn,
-                                                                   const float2* __restrict__ twm, int n_rt) {
-    __shared__ float2 b0[mixed_padded(MAXM)], b1[mixed_padded(MAXM)];
+// FPB frames per block, as in istft_frames_mixed_kernel: with FPB = 2 (f-major, T even, 16-byte
+// aligned spectrum) the two frames t and t + 1 of one channel are transformed by the two halves
+// of the block, and every bin row gets both frames' values as one 16-byte store.
+template <int MAXM, class CT, int FPB>
+__global__ __launch_bounds__(kMixedThreads * FPB) void stft_mixed_kernel(StftArgs a, MixedRadix p,
+                                                                         const float2* __restrict__ twn,
+                                                                         const float2* __restrict__ twm, int n_rt) {
+    __shared__ float2 b0s[FPB][mixed_padded(MAXM)], b1s[FPB][mixed_padded(MAXM)];
     __shared__ float2 twl[kMixedTwMax];
+    constexpr int NT = kMixedThreads;
     constexpr int CTM = MixedM<CT>::value;
     const int n = CTM ? 2 * CTM : n_rt;
-    const int M = n / 2, tid = (int)threadIdx.x;
-    const int f = xcd_block();                         // channel * T + frame
-    if (f >= a.jobs) return;                           // whole block idle: no barrier reached
-    Staged<kMixedTwMax, kMixedThreads, float2> tws;
-    tws.load(twm, tid);
+    const int M = n / 2, tall = (int)threadIdx.x, half = tall / NT, tid = tall - half * NT;
+    const int f0 = xcd_block() * FPB;                  // first frame (channel * T + frame) of the block
+    if (f0 >= a.jobs) return;                          // whole block idle: no barrier reached
+    const int f = f0 + half;
+    float2* b0 = b0s[half];
+    float2* b1 = b1s[half];
+    Staged<kMixedTwMax, NT * FPB, float2> tws;
+    tws.load(twm, tall);
     const int c = f / a.T, t = f - c * a.T;
     const float* xc = a.x + (size_t)c * a.len;
     const int m0 = a.frame0 + t * a.hop;
-    for (int i = tid; i < M; i += kMixedThreads) {
+    for (int i = tid; i < M; i += NT) {
         const float x0 = xc[padded_index_rt(m0 + 2 * i, a, n)], x1 = xc[padded_index_rt(m0 + 2 * i + 1, a, n)];
         b0[mixed_pad(i)] = make_float2(x0 * a.win[2 * i], x1 * a.win[2 * i + 1]);
     }
-    tws.store(twl, tid);
+    tws.store(twl, tall);
     __syncthreads();
     const float2* z;
-    if constexpr (CTM != 0) z = CT::template run<kMixedThreads, 2>(b0, b1, twl, tid);
-    else z = mixed_fft<MAXM, kMixedThreads>(b0, b1, M, p, 2, twl, tid);
+    if constexpr (CTM != 0) z = CT::template run<NT, 2>(b0, b1, twl, tid);
+    else z = mixed_fft<MAXM, NT>(b0, b1, M, p, 2, twl, tid);
     // X[k] = E[k] + W_n^k O[k], k <= n/2, as in stft_kernel.
     const float hs = 0.5f * a.scale;
-    for (int k = tid; k < a.F; k += kMixedThreads) {
-        const float2 zk = z[mixed_pad(k == M ? 0 : k)], zm = z[mixed_pad(k == 0 ? 0 : M - k)];
-        const float2 w = twn[k];
+    auto bin = [&](const float2* zz, int k, float2 w) {
+        const float2 zk = zz[mixed_pad(k == M ? 0 : k)], zm = zz[mixed_pad(k == 0 ? 0 : M - k)];
         const float er = zk.x + zm.x, ei = zk.y - zm.y;
         const float orr = zk.y + zm.y, oi = zm.x - zk.x;
-        const float2 val = make_float2((er + w.x * orr - w.y * oi) * hs, (ei + w.x * oi + w.y * orr) * hs);
-        if (a.layout == STX_SPEC_F_MAJOR) a.spec[((size_t)c * a.F + k) * a.T + t] = val;
-        else store_stream(a.spec + ((size_t)c * a.T + t) * a.F + k, val);
+        return make_float2((er + w.x * orr - w.y * oi) * hs, (ei + w.x * oi + w.y * orr) * hs);
+    };
+    if constexpr (FPB == 2) {
+        // Both halves ran the same passes, so both results are in the same buffer of their half;
+        // the last pass ended with a barrier.
+        const bool in0 = z == b0;
+        const float2* z0 = in0 ? b0s[0] : b1s[0];
+        const float2* z1 = in0 ? b0s[1] : b1s[1];
+        const int t0 = t - half;                       // even
+        for (int k = tall; k < a.F; k += 2 * NT) {
+            const float2 w = twn[k];
+            const float2 v0 = bin(z0, k, w), v1 = bin(z1, k, w);
+            *reinterpret_cast<float4*>(a.spec + ((size_t)c * a.F + k) * a.T + t0) = make_float4(v0.x, v0.y, v1.x, v1.y);
+        }
+    } else {
+        for (int k = tid; k < a.F; k += NT) {
+            const float2 val = bin(z, k, twn[k]);
+            if (a.layout == STX_SPEC_F_MAJOR) a.spec[((size_t)c * a.F + k) * a.T + t] = val;
+            else store_stream(a.spec + ((size_t)c * a.T + t) * a.F + k, val);
+        }
     }
 }
 
@@ -1242,19 +1265,31 @@ STX_API stx_status stx_torch_stft(const stx_fft* f, const float* x, int channels
         check_extent((long long)channels * a.T * a.F, "spectrum");
         check_extent((long long)channels * len + n, "signal");
         if (f->mixed) {
-            const unsigned grid = (unsigned)((a.jobs + kXcds - 1) / kXcds * kXcds);   // xcd_block's multiple
-            if (n == 2 * MixedCt3840::M && mixed_plan_is(f->half, MixedCt3840::radix, MixedCt3840::count))
-                hipLaunchKernelGGL((stft_mixed_kernel<4096, MixedCt3840>), dim3(grid), dim3(kMixedThreads), 0,
-                                   as_stream(stream), a, f->half, f->twn, f->twm, n);
+            // Two frames per block where a bin row's two values are one aligned 16-byte store
+            // (f-major, T even) and both frames' buffers fit in LDS (n / 2 <= 4096).
+            const bool pair = layout == STX_SPEC_F_MAJOR && a.T % 2 == 0 && n / 2 <= 4096 &&
+                              (reinterpret_cast<uintptr_t>(spec) & 15) == 0;
+            const int blocks = pair ? a.jobs / 2 : a.jobs;
+            const unsigned grid = (unsigned)((blocks + kXcds - 1) / kXcds * kXcds);   // xcd_block's multiple
+            const dim3 bd(kMixedThreads * (pair ? 2 : 1));
+            const hipStream_t st = as_stream(stream);
+            const bool ct = n == 2 * MixedCt3840::M && mixed_plan_is(f->half, MixedCt3840::radix, MixedCt3840::count);
+            if (ct && pair)
+                hipLaunchKernelGGL((stft_mixed_kernel<4096, MixedCt3840, 2>), dim3(grid), bd, 0, st, a, f->half, f->twn,
+                                   f->twm, n);
+            else if (ct)
+                hipLaunchKernelGGL((stft_mixed_kernel<4096, MixedCt3840, 1>), dim3(grid), bd, 0, st, a, f->half, f->twn,
+                                   f->twm, n);
+            else if (n / 2 <= 1024 && pair)
+                hipLaunchKernelGGL((stft_mixed_kernel<1024, void, 2>), dim3(grid), bd, 0, st, a, f->half, f->twn, f->twm, n);
             else if (n / 2 <= 1024)
-                hipLaunchKernelGGL((stft_mixed_kernel<1024, void>), dim3(grid), dim3(kMixedThreads), 0, as_stream(stream), a,
-                                   f->half, f->twn, f->twm, n);
+                hipLaunchKernelGGL((stft_mixed_kernel<1024, void, 1>), dim3(grid), bd, 0, st, a, f->half, f->twn, f->twm, n);
+            else if (n / 2 <= 4096 && pair)
+                hipLaunchKernelGGL((stft_mixed_kernel<4096, void, 2>), dim3(grid), bd, 0, st, a, f->half, f->twn, f->twm, n);
             else if (n / 2 <= 4096)
-                hipLaunchKernelGGL((stft_mixed_kernel<4096, void>), dim3(grid), dim3(kMixedThreads), 0, as_stream(stream), a,
-                                   f->half, f->twn, f->twm, n);
+                hipLaunchKernelGGL((stft_mixed_kernel<4096, void, 1>), dim3(grid), bd, 0, st, a, f->half, f->twn, f->twm, n);
             else
-                hipLaunchKernelGGL((stft_mixed_kernel<8192, void>), dim3(grid), dim3(kMixedThreads), 0, as_stream(stream), a,
-                                   f->half, f->twn, f->twm, n);
+                hipLaunchKernelGGL((stft_mixed_kernel<8192, void, 1>), dim3(grid), bd, 0, st, a, f->half, f->twn, f->twm, n);
             launch_check("stft_mixed_kernel");
             return;
         }
