@@ -100,7 +100,8 @@ __global__ __launch_bounds__(256) void resample_kernel(ResampleArgs a) {
 // output from c = i / ratio with ratio rounded to double, by the rounding of c (below 1e-9 for
 // three hours of 48 kHz audio), so the output is within a few float ulps of the reference's
 // (SNR above 160 dB) instead of bit-identical; the per-tap division, table lookup and
-// interpolation of resample_kernel are gone, leaving a conversion and an fma per tap.
+// interpolation of resample_kernel are gone, leaving an fma per tap and a conversion per staged
+// sample read (shared by a pair of phases, below).
 //
 // A workgroup takes one channel and the 64 output groups M = m0 + lane, m0 = 64 blockIdx.x: all
 // outputs in [m0 up, (m0 + 64) up). It stages in LDS, for each lane, the input its outputs read:
@@ -131,7 +132,7 @@ struct PhaseArgs {
 };
 
 constexpr int kPhaseTile = 64;                       // output groups per workgroup, one per lane
-constexpr int kPhaseWaves = 16;                      // waves per workgroup, each over up / 32 phase pairs
+constexpr int kPhaseWaves = 16;                      // waves per workgroup, each over every 16th phase pair
 constexpr int kPhaseStage = 4;                       // staged loads in flight per lane
 constexpr long long kPhaseMaxWeights = 1 << 18;      // up * ntap above this: per-tap kernel
 constexpr int kPhaseOverread = 8;                    // staged samples and table weights past the last used
