@@ -287,12 +287,26 @@ __global__ __launch_bounds__(256) void istft_ola_kernel(IstftArgs a, int N) {
         const int hi = min(a.env_frames - 1, J / hop);
         const float* fc = a.frames + (size_t)c * a.T * N;
         float env = 0.f, sum = 0.f;
-        for (int tf = lo; tf <= hi; tf++) {
-            const int s = J - tf * hop;
-            const float w = a.win[s];
-            env += w * w;
-            const int st = tf - a.frame_off;
-            if (st >= 0 && st < a.T) sum += fc[(size_t)st * N + s];
+        // Up to 8 covering frames per step, every load issued before the first sum (the frame
+        // count varies, so a plain loop would wait for each load in turn); the sums stay in
+        // frame order and skip what the loop skipped.
+        for (int tf0 = lo; tf0 <= hi; tf0 += 8) {
+            float wv[8], xv[8];
+            bool in[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int tf = tf0 + u, st = tf - a.frame_off;
+                const bool ok = tf <= hi;
+                const int s = ok ? J - tf * hop : 0;
+                in[u] = ok && st >= 0 && st < a.T;
+                wv[u] = ok ? a.win[s] : 0.f;
+                xv[u] = in[u] ? fc[(size_t)st * N + s] : 0.f;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                if (tf0 + u <= hi) env += wv[u] * wv[u];
+                if (in[u]) sum += xv[u];
+            }
         }
         y = env > 1e-11f ? sum / env : 0.f;
     }
