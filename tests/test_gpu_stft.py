@@ -306,6 +306,30 @@ def test_torch_stft_vr_sizes_round_trip(device, orc, n, hop, extra):
         assert snr_db(y_h[c], orc.torch_istft(ref, n, hop)) >= SNR_DB
 
 
+@pytest.mark.parametrize("n,hop,frames", [(960, 240, 82), (7680, 1024, 32)])
+def test_mixed_pairs_unaligned_spectrum(device, n, hop, frames):
+    """The mixed-radix STFT and iSTFT transform two f-major frames per block when the frame count
+    is even and the spectrum 16-byte aligned; a spectrum 8 bytes off that takes one frame per
+    block. Both give the same bits (the run-time plan at 960 and the compiled one at 7680)."""
+    import torch
+    length = (frames - 1) * hop
+    x = to_dev(_stereo(n, length, 0.5), device)
+    f = any_plan(n)
+    F, T = n // 2 + 1, length // hop + 1
+    assert T == frames
+    a = stx.torch_stft(f, x, hop)
+    assert a.data_ptr() % 16 == 0
+    buf = torch.empty(2 * 2 * F * T + 2, dtype=torch.float32, device=x.device)
+    b = buf[2:].view(torch.complex64).view(2, F, T)
+    assert b.data_ptr() % 16 == 8
+    stx.torch_stft(f, x, hop, out=b)
+    assert np.array_equal(host(a), host(b))
+    ws = stx.workspace(stx.istft_workspace_size(f, 2, T), device)
+    ya = host(stx.torch_istft(f, a, hop, workspace=ws))
+    yb = host(stx.torch_istft(f, b, hop, workspace=ws))
+    assert np.array_equal(ya, yb)
+
+
 def test_any_size_errors(device):
     import torch
     for n in (7, 14, 22, 20000):
