@@ -14,9 +14,9 @@
 // the input fits in the registers of blocks that are all resident at once (one segment's
 // spectrum or waveform) and the output does not overlap the input: each block loads its chunk
 // once, the blocks exchange their partial sums (grid_sync.hpp) and normalise from registers.
-// Otherwise (the whole mix of separate())
-// three kernels: pass 1 writes one (sum d, sum d^2) pair in double per 8192 floats, one block
-// adds them in a fixed order into {mean, sd}, and a third kernel normalises. The split's
+// Otherwise (the whole mix of separate()) two kernels: pass 1 writes one (sum d, sum d^2) pair
+// in double per 8192 floats, and every block of pass 2 adds them in one fixed order into
+// {mean, sd} (the same bits in every block) and normalises its 8192 values. The split's
 // overlap-add is in gather form: each output sample sums, in chunk order and in float like the
 // reference's `out += weight * seg_out`, the <= ceil(seg / stride) chunks covering it, and
 // divides by the summed weights, so it is bit-exact.

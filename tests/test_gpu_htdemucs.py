@@ -88,7 +88,7 @@ def test_wave_normalize_ragged(device, htd, n):
 
 
 def test_normalize_without_grid_sync(device, htd, monkeypatch):
-    """STX_NO_GRID_SYNC=1 sends one segment's normalisations to the three-kernel path."""
+    """STX_NO_GRID_SYNC=1 sends one segment's normalisations to the two-kernel path."""
     monkeypatch.setenv("STX_NO_GRID_SYNC", "1")
     xh = synth.normal(9, (2, SEG), 0.1) - 0.02
     y, stats = stx.htdemucs_wave_normalize(dev(xh, device))
@@ -124,7 +124,7 @@ def test_normalize_forced_fallback(device, htd, monkeypatch):
 
 
 def test_normalize_in_place(device, htd):
-    """Output over its input: the three-kernel path (a single-pass block may re-read x)."""
+    """Output over its input: the two-kernel path (a single-pass block may re-read x)."""
     xh = synth.normal(13, (2, SEG), 0.1) - 0.005
     x = dev(xh, device)
     y, stats = stx.htdemucs_wave_normalize(x, out=x)
