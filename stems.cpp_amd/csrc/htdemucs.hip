@@ -112,13 +112,17 @@ __global__ __launch_bounds__(256) void moments_kernel(MomArgs a) {
     if (threadIdx.x == 0) {
         a.partial[2 * blockIdx.x] = s;
         a.partial[2 * blockIdx.x + 1] = q;
+        // The shift goes after the pairs, so pass 2 never reads it from x: pass 2 may write
+        // its output over x, and a block that starts late would see normalised values there.
+        if (blockIdx.x == 0) a.partial[2 * gridDim.x] = (double)shift;
     }
 }
 
 enum NormKind { NORM_CAC = 0, NORM_FLAT = 1, NORM_MIX = 2 };
 
 // {mean, den} from the pass-1 pairs, added in a fixed order (thread t takes pairs t, t + 256, ...,
-// then the block sum), so every block that calls it gets the same bits; the unbiased std,
+// then the block sum), so every block that calls it gets the same bits; the shift is the one
+// pass 1 stored after its pairs (never x[0], which an in-place call may have overwritten); the unbiased std,
 // floored at 1e-8 for the mix (std::max(std, 1e-8) keeps a NaN, as here); den = 1e-5 + sd
 // (spectrum, waveform) or the floored sd (mix). Block (0, 0) writes {mean, sd} to stats.
 template <int KIND>
@@ -131,7 +135,7 @@ __device__ __forceinline__ void fold_stats(const MomArgs& a, int n_partial, doub
     }
     s = block_sum(s, red);
     q = block_sum(q, red);
-    const double shift = KIND == NORM_MIX ? (double)mono_at(a.x, a.n, a.C, 0) : (double)a.x[0];
+    const double shift = a.partial[2 * n_partial];
     const double n = (double)a.n;
     double sd = sqrt(fmax(q - s * (s / n), 0.0) / (n - 1.0));
     if (KIND == NORM_MIX) sd = sd < 1e-8 ? 1e-8 : sd;
@@ -530,6 +534,10 @@ __global__ __launch_bounds__(256) void bag_final_kernel(FinalArgs a) {
 
 long long mom_blocks(long long n) { return (n + kMomChunk - 1) / kMomChunk; }
 
+// Normalisation workspace: the single-pass kernel's area (kGridSyncBytes), then the pass-1 pairs
+// and the shift (one double, padded to 16 bytes).
+size_t norm_ws_bytes(long long n) { return kGridSyncBytes + (size_t)mom_blocks(n) * 16 + 16; }
+
 unsigned grid256(long long n) { return (unsigned)((n + 255) / 256); }
 
 struct Cancelled {};
@@ -554,7 +562,7 @@ SepLayout sep_layout(int C, long long len, int seg, int S, int batch, int shifts
     L.stats = o;
     o += align(2 * sizeof(double));
     L.mom = o;
-    o += align(kGridSyncBytes + (size_t)mom_blocks(len) * 16);
+    o += align(norm_ws_bytes(len));
     L.parts = o;
     o += align(sizeof(float) * (size_t)batch * C * seg);
     L.y = o;
@@ -566,9 +574,6 @@ SepLayout sep_layout(int C, long long len, int seg, int S, int batch, int shifts
     L.total = o;
     return L;
 }
-
-// Normalisation workspace: the single-pass kernel's area (kGridSyncBytes), then the pass-1 pairs.
-size_t norm_ws_bytes(long long n) { return kGridSyncBytes + (size_t)mom_blocks(n) * 16; }
 
 void check_ws(void* ws, size_t bytes, long long n) {
     STX_REQUIRE(ws != nullptr, "normalise: workspace is NULL");
@@ -598,6 +603,12 @@ bool try_norm_fused(const float* x, float* y, long long n, long long ft, double*
 template <int MK, int NK>
 void normalize(const float* x, long long n_mom, long long count, int C, float* y, double* stats, void* ws,
                hipStream_t s) {
+    // Pass 2 reads and writes the same indices for FLAT and MIX, so y == x is safe there; any
+    // other overlap is refused, and so is any for CAC, whose planes move every value.
+    const size_t bytes = sizeof(float) * (size_t)(NK == NORM_CAC ? n_mom : count);
+    if (overlaps(x, bytes, y, bytes))
+        STX_REQUIRE(NK != NORM_CAC && x == y, "normalise: the output overlaps the input%s",
+                    NK == NORM_CAC ? "" : " without being the same buffer");
     if constexpr (NK != NORM_MIX) {
         if (try_norm_fused<NK, 1>(x, y, n_mom, count, stats, ws, s) || try_norm_fused<NK, 2>(x, y, n_mom, count, stats, ws, s) ||
             try_norm_fused<NK, 4>(x, y, n_mom, count, stats, ws, s))

@@ -133,6 +133,43 @@ def test_normalize_in_place(device, htd):
     assert np.array_equal(host(y), htd.normalize(xh, st[0], st[1]))
 
 
+def test_normalize_in_place_many_waves(device, htd):
+    """In-place calls large enough that the normalising blocks run in several waves (2 x 180 s
+    stereo waveforms: 3,876 blocks; the 180 s stereo mix: 1,938 blocks of 8,192 values, 32 per
+    thread): output and statistics bit-equal to the out-of-place call, whose blocks never see
+    their own output. A late block must not take an already-normalised x[0] as its shift."""
+    import torch
+    xh = synth.normal(14, (2, 2 * SONG), 0.1) + 0.02
+    x = dev(xh, device)
+    y_ref, st_ref = stx.htdemucs_wave_normalize(x)
+    y, st = stx.htdemucs_wave_normalize(x, out=x)
+    assert y.data_ptr() == x.data_ptr()
+    assert np.array_equal(host(st), host(st_ref)) and np.array_equal(host(y), host(y_ref))
+    assert close_stats(host(st), htd.mean_std(xh))
+    del x, y, y_ref
+    mix = synth.sines_plus_pink(5, 2, SONG)
+    m = dev(mix, device)
+    o_ref, s_ref = stx.htdemucs_mix_normalize(m)
+    o, s = stx.htdemucs_mix_normalize(m, out=m)
+    assert np.array_equal(host(s), host(s_ref)) and np.array_equal(host(o), host(o_ref))
+    torch.cuda.synchronize()
+
+
+def test_normalize_overlap_refused(device):
+    """An output that overlaps its input without being the same buffer is refused (blocks would
+    overwrite values other blocks have yet to read), and so is any overlap for the CaC pack,
+    whose planes move every value."""
+    import torch
+    x = torch.zeros(2 * 100000, dtype=torch.float32, device=device)
+    with pytest.raises(stx.StxError) as e:
+        stx.htdemucs_wave_normalize(x[:100000], out=x[1:100001])
+    assert e.value.status == stx.STATUS_INVALID_ARGUMENT and "overlaps" in e.value.message
+    spec = torch.zeros((2, 64, 100), dtype=torch.complex64, device=device)
+    with pytest.raises(stx.StxError) as e:
+        stx.htdemucs_cac_normalize(spec, out=torch.view_as_real(spec).reshape(4, 64, 100))
+    assert e.value.status == stx.STATUS_INVALID_ARGUMENT and "overlaps" in e.value.message
+
+
 def test_mix_normalize_song(device, htd):
     """src/htdemucs.cpp:539-549 on the 180 s stereo song."""
     mix = synth.sines_plus_pink(5, 2, SONG)
