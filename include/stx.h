@@ -436,7 +436,8 @@ STX_API stx_status stx_resample(const stx_resampler* resampler, const float* in,
  * read by the denormalise calls, so nothing returns to the host between them.
  * ---------------------------------------------------------------------------------------- */
 
-/* Bytes of device workspace for a normalise call over n values (16 per 8192 values). */
+/* Bytes of device workspace for a normalise call over n values (a fixed area for the
+ * single-pass kernel, 16 bytes per 8192 values and 16 more). */
 STX_API size_t stx_htdemucs_norm_workspace_size(int64_t n);
 
 /* Complex-as-channels pack and normalisation of one segment's spectrum
@@ -445,8 +446,8 @@ STX_API size_t stx_htdemucs_norm_workspace_size(int64_t n);
  * each (v - mean) / (1e-5 + sd) over all 2 C F T values (mean_of and the unbiased std_of,
  * :293-302, in double). stats gets {mean, sd}. workspace: device, 16-byte aligned,
  * stx_htdemucs_norm_workspace_size(2 C F T) bytes, no initialisation needed; calls that share one
- * must not overlap. A segment that fits on the device at once (and whose output does not
- * overlap its input) is normalised by one grid-synchronised kernel, with the bounded waits and
+ * must not overlap. mag must not overlap spec (INVALID_ARGUMENT). A segment that fits on the
+ * device at once is normalised by one grid-synchronised kernel, with the bounded waits and
  * the same-bits fallback of stx_group_norm; the rest take two kernels (moments, then the
  * normalisation, each of whose blocks adds the moments' partial sums itself). */
 STX_API stx_status stx_htdemucs_cac_normalize(const float* spec, int channels, int n_bins, int n_frames, float* mag,
@@ -454,14 +455,16 @@ STX_API stx_status stx_htdemucs_cac_normalize(const float* spec, int channels, i
                                               stx_stream stream);
 
 /* The waveform branch's normalisation (src/htdemucs.cpp:438-441): out = (x - mean) / (1e-5 + sd)
- * over n values. stats gets {mean, sd}. */
+ * over n values. stats gets {mean, sd}. out may be x (in place, two kernels); any other
+ * overlap of out and x is INVALID_ARGUMENT. */
 STX_API stx_status stx_htdemucs_wave_normalize(const float* x, int64_t n, float* out, double* stats, void* workspace,
                                                size_t workspace_bytes, stx_stream stream);
 
 /* separate()'s normalisation by the mono mix (src/htdemucs.cpp:539-549): mono = sum_c x / C
  * (rounded to float), ref_mean and ref_std = max(std, 1e-8) of mono, out = (x - ref_mean) /
  * ref_std for every channel of mix [C][len]. stats gets {ref_mean, ref_std}. INVALID_ARGUMENT
- * "empty input" when len <= 0, as the reference throws. workspace: norm_workspace_size(len). */
+ * "empty input" when len <= 0, as the reference throws. workspace: norm_workspace_size(len).
+ * out may be mix (in place); any other overlap is INVALID_ARGUMENT. */
 STX_API stx_status stx_htdemucs_mix_normalize(const float* mix, int channels, int64_t len, float* out, double* stats,
                                               void* workspace, size_t workspace_bytes, stx_stream stream);
 
@@ -580,8 +583,12 @@ STX_API stx_status stx_group_norm_noalloc(const stx_tensor* a, const stx_tensor*
 /* Blocks of grid-synchronised kernels that ran on `workspace` (a group-norm or HTDemucs
  * normalisation workspace; NULL: the calling GPU's stx_group_norm_noalloc scratch) and
  * computed their statistics themselves because a wait gave up: a sticky count, read
- * synchronously (the caller synchronises the streams that used the workspace first). Not
- * part of the reference; a diagnostic for callers that share the device. */
+ * synchronously (the caller synchronises the streams that used the workspace first). The
+ * count is a 32-bit word inside the workspace that no call clears: it starts from whatever the
+ * workspace held, so it means something only from a workspace the caller zeroed (all of it:
+ * the kernels accept a zeroed workspace) before the calls to be counted. The noalloc scratch
+ * starts zeroed when the library loads. Not part of the reference; a diagnostic for callers
+ * that share the device. */
 STX_API stx_status stx_grid_sync_fallbacks(const void* workspace, uint32_t* count);
 
 /* ggml_norm(a, eps) over ne0 (src/htdemucs.cpp:215): (x - mean) / sqrt(var + eps). */
@@ -599,7 +606,10 @@ STX_API stx_status stx_rms_norm_mul(const stx_tensor* a, const float* gamma, con
 
 /* ggml_soft_max_ext(a, mask, scale, max_bias) along ne0 (src/roformer.cpp:127,
  * src/htdemucs.cpp:238): softmax(scale * x). The reference passes mask = NULL and
- * max_bias = 0; anything else is UNSUPPORTED, as are rows longer than 2048. */
+ * max_bias = 0; anything else is UNSUPPORTED. Any row length: rows of up to 2048 floats share
+ * a wave, rows of up to 8192 (the HTDemucs scores, Nk = 1,344 or 2,688 tokens) take one block
+ * each with the row in registers, longer or unevenly aligned ones one block and three passes.
+ * dst may be a. */
 STX_API stx_status stx_soft_max_ext(const stx_tensor* a, const stx_tensor* mask, const stx_tensor* dst, float scale,
                                     float max_bias, stx_stream stream);
 

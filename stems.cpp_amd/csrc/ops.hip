@@ -500,6 +500,92 @@ __global__ __launch_bounds__(256) void softmax_v4_kernel(SoftmaxArgs a) {
     }
 }
 
+// Maximum over a 256-thread block (exact in any order). red holds 4 floats.
+__device__ __forceinline__ float block_max(float v, float* red) {
+    v = lane_max<kWave>(v);
+    __syncthreads();
+    if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// Rows of 2049..8192 floats (the HTDemucs attention scores: Nk = 2,688 frequency tokens): one
+// 256-thread block per row, the row held in registers (V4 float4 per thread, split as in
+// softmax_v4_kernel), the maximum and the double sum reduced over the block's four waves.
+template <int V4>
+__global__ __launch_bounds__(256) void softmax_block_kernel(SoftmaxArgs a) {
+    __shared__ float redf[4];
+    __shared__ double redd[4];
+    const int lane = (int)threadIdx.x;
+    const long long rows = a.src.ne[1] * a.src.ne[2] * a.src.ne[3];
+    const int n = (int)a.src.ne[0];
+    const double sc = (double)a.scale;
+    const float sgn = a.scale < 0.f ? -1.f : 1.f;
+    for (long long r = blockIdx.x; r < rows; r += gridDim.x) {
+        const float* x = reinterpret_cast<const float*>(row_ptr_flat(a.src, r, a.rs_src));
+        float* y = reinterpret_cast<float*>(row_ptr_flat(a.dst, r, a.rs_dst));
+        const RowSplit sp = row_split(x, n);
+        float v[4 * V4], e;
+        int ei;
+        row_load<256, V4>(x, sp, lane, v, e, ei);
+        float m = ei >= 0 ? sgn * e : -INFINITY;
+#pragma unroll
+        for (int k = 0; k < V4; k++)
+            if (lane + 256 * k < sp.nb4)
+#pragma unroll
+                for (int j = 0; j < 4; j++) m = fmaxf(m, sgn * v[4 * k + j]);
+        const double ms = (double)(sgn * block_max(m, redf)) * sc;
+        double sum = 0.0;
+#pragma unroll
+        for (int k = 0; k < V4; k++) {
+            const bool ok = lane + 256 * k < sp.nb4;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                v[4 * k + j] = ok ? exp_split((double)v[4 * k + j] * sc - ms) : 0.f;
+                sum += (double)v[4 * k + j];
+            }
+        }
+        if (ei >= 0) {
+            e = exp_split((double)e * sc - ms);
+            sum += (double)e;
+        }
+        const double inv = 1.0 / block_sum(sum, redd);
+        float4* yb = reinterpret_cast<float4*>(y + sp.h);
+#pragma unroll
+        for (int k = 0; k < V4; k++) {
+            const int q = lane + 256 * k;
+            if (q < sp.nb4)
+                store_stream(yb + q, make_float4((float)((double)v[4 * k] * inv), (float)((double)v[4 * k + 1] * inv),
+                                                 (float)((double)v[4 * k + 2] * inv), (float)((double)v[4 * k + 3] * inv)));
+        }
+        if (ei >= 0) store_stream(y + ei, (float)((double)e * inv));
+    }
+}
+
+// Any row length and alignment: one block per row and three passes over it (maximum, sum,
+// output), the second and third re-reading the row from the cache. Each exp is recomputed in
+// the third pass from the same operands, so it has the bits the sum added.
+__global__ __launch_bounds__(256) void softmax_big_kernel(SoftmaxArgs a) {
+    __shared__ float redf[4];
+    __shared__ double redd[4];
+    const long long rows = a.src.ne[1] * a.src.ne[2] * a.src.ne[3];
+    const long long n = a.src.ne[0];
+    const double sc = (double)a.scale;
+    const float sgn = a.scale < 0.f ? -1.f : 1.f;
+    for (long long r = blockIdx.x; r < rows; r += gridDim.x) {
+        const float* x = reinterpret_cast<const float*>(row_ptr(a.src, r));
+        float* y = reinterpret_cast<float*>(row_ptr(a.dst, r));
+        float m = -INFINITY;
+        for (long long i = threadIdx.x; i < n; i += 256) m = fmaxf(m, sgn * x[i]);
+        const double ms = (double)(sgn * block_max(m, redf)) * sc;
+        double sum = 0.0;
+        for (long long i = threadIdx.x; i < n; i += 256) sum += (double)exp_split((double)x[i] * sc - ms);
+        const double inv = 1.0 / block_sum(sum, redd);
+        __syncthreads();                         // every thread has read the row before y overwrites it
+        for (long long i = threadIdx.x; i < n; i += 256) y[i] = (float)((double)exp_split((double)x[i] * sc - ms) * inv);
+    }
+}
+
 // --------------------------------------------------------------------- elementwise
 enum EwOp { EW_GELU = 0, EW_GLU = 1, EW_ADD = 2, EW_MUL = 3, EW_MUL_ADD = 4, EW_ADD_GELU = 5, EW_GLU_MUL_ADD = 6 };
 
@@ -1598,9 +1684,25 @@ STX_API stx_status stx_soft_max_ext(const stx_tensor* a, const stx_tensor* mask,
         args.rs_dst = row_spacing(args.dst);
         const long long rows = nrows(args.src), n = args.src.ne[0];
         if (rows == 0 || n == 0) return;
-        if (n > kMaxRowShapeN) fail(STX_STATUS_UNSUPPORTED, "soft_max_ext: rows longer than 2048 are not supported");
+        STX_REQUIRE(n < (1LL << 31), "soft_max_ext: row too long");
         const hipStream_t s = as_stream(stream);
-        if (same_row_alignment(args.src, args.dst)) {
+        const unsigned row_grid = (unsigned)std::min<long long>(rows, 1 << 20);
+        if (n > kMaxRowShapeN && n <= 4 * kMaxRowShapeN && same_row_alignment(args.src, args.dst)) {
+            const long long v4 = ((n + 3) / 4 + 255) / 256;
+            auto go = [&](auto k) {
+                constexpr int V = decltype(k)::value;
+                hipLaunchKernelGGL((softmax_block_kernel<V>), dim3(row_grid), dim3(256), 0, s, args);
+            };
+            using std::integral_constant;
+            if (v4 <= 3) go(integral_constant<int, 3>{});
+            else if (v4 == 4) go(integral_constant<int, 4>{});
+            else if (v4 <= 6) go(integral_constant<int, 6>{});
+            else go(integral_constant<int, 8>{});
+            launch_check("softmax_block_kernel");
+        } else if (n > kMaxRowShapeN) {
+            hipLaunchKernelGGL(softmax_big_kernel, dim3(row_grid), dim3(256), 0, s, args);
+            launch_check("softmax_big_kernel");
+        } else if (same_row_alignment(args.src, args.dst)) {
             pick_v4_shape(n, [&](auto lanes, auto v4) {
                 constexpr int L = decltype(lanes)::value, V = decltype(v4)::value;
                 hipLaunchKernelGGL((softmax_v4_kernel<L, V>), dim3(row_blocks(rows, L)), dim3(256), 0, s, args);

@@ -6,7 +6,8 @@ MUL and the LayerScale + residual x + h*s, which round after every operation.
 
 Shapes: HTDemucs GroupNorm/GELU/GLU/LayerScale at [T, 1, C] for (C, T) in {(48, 85995),
 (96, 21499), (192, 5375), (384, 1344)}; RoFormer RMSNorm at 48,060 rows x 384 and the band-split
-widths, softmax at one 256 MiB score group [801, 801, 8, 13] and [60, 60, 8, 801], the FF bias +
+widths, softmax at one 256 MiB score group [801, 801, 8, 13] and [60, 60, 8, 801] and the HTDemucs
+scores [Nk, Nq, 8] for Nk, Nq in {1344, 2688}, the FF bias +
 GELU at [1536, 801, 60], RoPE at [64, 8, 801, 60] and [64, 8, 60, 801] (ggml order, ne0 first;
 numpy shapes below are reversed).
 """
@@ -287,9 +288,43 @@ def test_soft_max_negative_scale_and_errors(device, ops):
     with pytest.raises(stx.StxError) as e:
         stx.soft_max_ext(x, 0.125, max_bias=8.0)
     assert e.value.status == stx.STATUS_UNSUPPORTED
-    with pytest.raises(stx.StxError) as e:
-        stx.soft_max_ext(randn(device, (2, 2049), 1), 1.0)
-    assert e.value.status == stx.STATUS_UNSUPPORTED
+
+
+HTDEMUCS_KQ = [(2688, 2688), (1344, 2688), (2688, 1344), (1344, 1344)]
+
+
+@pytest.mark.parametrize("nk,nq", HTDEMUCS_KQ)
+@pytest.mark.parametrize("hd", [48, 64])
+def test_soft_max_htdemucs(device, ops, nk, nq, hd):
+    """ggml_soft_max_ext(kq, NULL, 1/sqrt((float)hd), 0) over kq [Nk, Nq, 8] (src/htdemucs.cpp:236-238):
+    Nk and Nq are the 8 x 336 = 2,688 frequency tokens (:354-358) or the 1,344 time tokens, hd =
+    D / 8 with D = 384 or 512 (the widened bottom). Rows of 2,688 take one block per row."""
+    x = randn(device, (8, nq, nk), nk + nq + hd, 6.0)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    y = stx.soft_max_ext(x, scale)
+    want = ops.soft_max(host(x).reshape(-1, nk), scale)
+    assert rel_err(host(y).reshape(-1, nk), want) <= TOL
+
+
+@pytest.mark.parametrize("n", [2049, 2688, 3072, 3073, 4096, 5000, 6144, 8192, 8193, 20000])
+def test_soft_max_long_rows(device, ops, n):
+    """Rows longer than 2048: aligned rows, rows starting 4 bytes past a 16-byte boundary (a
+    head of 3 floats), an output misaligned with the input (the three-pass kernel) and the
+    call in place."""
+    import torch
+    rows = 37
+    buf = randn(device, (rows * n + 8,), n, 5.0)
+    for off in (0, 1):
+        x = buf[off:off + rows * n].view(rows, n)
+        xh = host(x)
+        want = ops.soft_max(xh, 0.2)
+        assert rel_err(host(stx.soft_max_ext(x, 0.2)), want) <= TOL
+        out = torch.empty(rows * n + 1, device=device)[1 - off:1 - off + rows * n].view(rows, n)
+        assert rel_err(host(stx.soft_max_ext(x, 0.2, out=out)), want) <= TOL
+        xc = x.clone()
+        assert rel_err(host(stx.soft_max_ext(xc, 0.2, out=xc)), want) <= TOL
+    neg = buf[:rows * n].view(rows, n)
+    assert rel_err(host(stx.soft_max_ext(neg, -0.3)), ops.soft_max(host(neg), -0.3)) <= TOL
 
 
 # ---------------------------------------------------------------------------- GELU
