@@ -629,6 +629,25 @@ def run_rows(torch, stx, dev):
         ws = stx.workspace(stx.istft_workspace_size(fft, C, T), dev)
         return lambda: stx.torch_istft(fft, z, hop, layout=stx.T_MAJOR, out=y, stream=stream, workspace=ws)
     row(out, "c3_istft_t_major_ws", torch, stream, mk_istft_ws, C * L * 4 + C * T * F * 8)
+
+    # Launch-amortised: one call over the 180 s song's 96 chunks x 2 channels at the c3 geometry
+    # (192 channels of 352,800 samples, T-major, the device pipeline's layout): the kernels'
+    # throughput once launch and ramp costs vanish.
+    CB = 96 * C
+
+    def mk_stft_b():
+        x, y = rn(CB, L), torch.empty((CB, T, F), dtype=torch.complex64, device=dev)
+        return lambda: stx.torch_stft(fft, x, hop, layout=stx.T_MAJOR, out=y, stream=stream)
+    row(out, "c5_stft_batched", torch, stream, mk_stft_b, CB * L * 4 + CB * T * F * 8)
+
+    def mk_istft_b(with_ws):
+        def mk():
+            z = torch.randn((CB, T, F), dtype=torch.complex64, device=dev)
+            y = torch.empty((CB, hop * (T - 1)), device=dev)
+            ws = stx.workspace(stx.istft_workspace_size(fft, CB, T), dev) if with_ws else None
+            return lambda: stx.torch_istft(fft, z, hop, layout=stx.T_MAJOR, out=y, stream=stream, workspace=ws)
+        return mk
+    row(out, "c5_istft_batched", torch, stream, mk_istft_b(False), CB * L * 4 + CB * T * F * 8)
     del bands, fft
 
     # c1: HTDemucs spectrogram of one stereo segment (343,980 samples, n_fft 4096, hop 1024).

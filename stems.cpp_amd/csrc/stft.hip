@@ -474,10 +474,11 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
     }
 
     // Envelope: win^2 summed over the envelope frames 0 <= tf < env_frames covering J, in frame
-    // order (src/stft.h:130,187); out = acc / env where env > 1e-11, else 0. Where all K + 1
-    // frames of J exist, env depends on R = J mod hop only: its reciprocal (0 for env <= 1e-11)
-    // comes from a table built once per workgroup (the product differs from the quotient by at
-    // most an ulp); elsewhere (the signal's ends) the sum runs here.
+    // order (src/stft.h:130,187); out = acc * (1 / env) where env > 1e-11, else 0 (within an ulp
+    // of the quotient). Where all K + 1 frames of J exist, env depends on R = J mod hop only: its
+    // reciprocal (0 for env <= 1e-11) comes from a table built once per workgroup when the LDS
+    // has room; elsewhere (and at the signal's ends) the same sum and reciprocal run here, so
+    // the table changes no bit.
     if constexpr (ENV_LDS) {
         const int nr = min(hop, N);
         for (int R = tid; R < nr; R += NT) {
@@ -507,7 +508,7 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
                 const float w = win[pos];
                 env += w * w;
             }
-            y = env > 1e-11f ? acc[q] / env : 0.f;
+            y = env > 1e-11f ? acc[q] * (1.f / env) : 0.f;   // as the table's product
         }
         store_stream(oc + (J - a.out_off), y);
     });

@@ -12,7 +12,7 @@ import pytest
 import oracle_lib
 import stx
 import synth
-from metrics import snr_db
+from metrics import rel_err, snr_db
 
 pytestmark = pytest.mark.gpu
 
@@ -277,7 +277,7 @@ def test_band_rms_norm(device, mel, kind, T, batch):
             x = feat[bi, off:off + din * T].reshape(T, din)
             want = ops.norm(x, 1e-24, rms=True, w=g)
             got = y[bi, off:off + din * T].reshape(T, din)
-            assert np.max(np.abs(got - want)) <= 1e-6 * np.max(np.abs(want))
+            assert rel_err(got, want) <= 1e-6
     # In place, and equal to stx_rms_norm_mul on one band's view.
     fd = dev(feat, device)
     bands.rms_norm(fd, T, gd, out=fd)
@@ -285,7 +285,7 @@ def test_band_rms_norm(device, mel, kind, T, batch):
     off, din = band_blocks(sizes, C, T)[5]
     view = dev(feat[0, off:off + din * T].reshape(T, din), device)
     one = host(stx.rms_norm(view, 1e-24, gamma=gd[5]))
-    assert np.max(np.abs(one - y[0, off:off + din * T].reshape(T, din))) <= 1e-6 * np.max(np.abs(one))
+    assert rel_err(y[0, off:off + din * T].reshape(T, din), one) <= 1e-6
 
 
 @pytest.mark.parametrize("kind,S,T", [("mel", 4, 801), ("bs", 2, 801), ("mel", 9, 33)])
@@ -305,7 +305,7 @@ def test_band_mask_glu(device, mel, kind, S, T):
             h = heads_h[s * len(sizes) + b]
             got = m[s, off:off + din * T].reshape(T, din)
             want = ops.glu(h, 0)
-            assert np.max(np.abs(got - want)) <= 1e-6 * max(np.max(np.abs(want)), 1e-30)
+            assert rel_err(got, want) <= 1e-6
             if b % 17 == 0:
                 assert np.array_equal(got, host(stx.glu(heads[s * len(sizes) + b], 0)))
 
@@ -323,4 +323,4 @@ def test_band_mask_glu_many_stems(device):
     for s in range(S):
         for b, (off, din) in enumerate(blocks):
             want = ops.glu(heads_h[s * 60 + b], 0)
-            assert np.max(np.abs(m[s, off:off + din * T].reshape(T, din) - want)) <= 1e-6 * np.max(np.abs(want))
+            assert rel_err(m[s, off:off + din * T].reshape(T, din), want) <= 1e-6
