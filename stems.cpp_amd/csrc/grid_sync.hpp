@@ -9,12 +9,12 @@
 // The host checks first that all blocks of a launch can be resident at once (resident_blocks)
 // and takes a multi-kernel path when they cannot.
 //
-// Records are (s1, s2, tag) with tag = a 64-bit hash of s1, s2 and the launch's key. The key is
-// the hardware's name for this dispatch: the AQL packet's dispatch id (its index in its queue,
-// 64 bits, never reused by that queue) hashed with the queue's address. Every block of a launch
-// reads the same key, graph replays get new ones, and a record of an earlier launch, a torn
-// record or garbage in a fresh workspace fails the check: the workspace needs no initialisation
-// and no per-launch state. Cross-block words are device-scope relaxed atomics, which gfx950
+// Records are (s1, s2, tag) with tag = s1 ^ rotl(s2, 29) ^ the launch's key (as bits). The key
+// is a 64-bit hash of the hardware's name for this dispatch: the AQL packet's dispatch id (its
+// index in its queue, 64 bits, never reused by that queue) and the queue's address, and of the
+// group. Every block of a launch reads the same key, graph replays get new ones, and a record
+// of an earlier launch, a torn record or garbage in a fresh workspace fails the check: the
+// workspace needs no initialisation and no per-launch state. Cross-block words are device-scope relaxed atomics, which gfx950
 // performs at the device's coherence point, past the XCD's own L2.
 //
 // Every wait is bounded (spin_limit polls). A block whose wait gives up (blocks that never
@@ -113,11 +113,15 @@ __device__ __forceinline__ unsigned long long fmix64(unsigned long long k) {
 // Key of group gt in this launch.
 __device__ __forceinline__ unsigned long long launch_key(int gt) {
     const unsigned long long q = (unsigned long long)__builtin_amdgcn_queue_ptr();
-    return fmix64(stx_amdgcn_dispatch_id() ^ fmix64(q)) + (unsigned long long)gt;
+    return fmix64(fmix64(stx_amdgcn_dispatch_id() ^ fmix64(q)) + (unsigned long long)gt);
 }
+// A record's check word. The key is already a 64-bit hash, so the check needs no mixing of its
+// own: a record of another launch, or one whose words come from two launches, passes only if
+// the two launches' keys differ by exactly what their words differ by (probability 2^-64), and
+// the check costs three instructions per poll instead of three 64-bit multiply chains.
 __device__ __forceinline__ unsigned long long record_tag(unsigned long long a, unsigned long long b,
                                                          unsigned long long key) {
-    return fmix64(a ^ fmix64(b ^ fmix64(key)));
+    return a ^ ((b << 29) | (b >> 35)) ^ key;
 }
 // Publishes (s1, s2) at r[0..2] under key.
 __device__ __forceinline__ void record_store(unsigned long long* r, double s1, double s2, unsigned long long key) {
@@ -186,12 +190,10 @@ __device__ __forceinline__ bool grid_totals(const GridSync& f, int gt, int nblk,
         }
         late = block_sum2_or<NT>(p1, p2, red, late);
         if (!late) {
-            if (threadIdx.x == 0) {
+            if (threadIdx.x < kGridStatCopies) {              // one copy per thread
                 tot[0] = p1;
                 tot[1] = p2;
-#pragma unroll
-                for (int c = 0; c < kGridStatCopies; c++)
-                    record_store(f.stat + c * kGridStatStride + 3 * gt, p1, p2, key);
+                record_store(f.stat + threadIdx.x * kGridStatStride + 3 * gt, p1, p2, key);
             }
             __syncthreads();
         }
@@ -254,9 +256,8 @@ inline bool grid_sync_enabled(hipStream_t stream) {
 }
 
 // Blocks of `kernel` (kGridThreads threads, no dynamic LDS) that the current device holds at
-// once; 0 when grid_sync_enabled() is false, so that callers take their multi-kernel path.
-inline int resident_blocks(const void* kernel, hipStream_t stream) {
-    if (!grid_sync_enabled(stream)) return 0;
+// once (occupancy times CUs, cached per kernel and device).
+inline int device_blocks(const void* kernel) {
     struct Entry {
         const void* k;
         int dev, blocks;
@@ -274,6 +275,13 @@ inline int resident_blocks(const void* kernel, hipStream_t stream) {
               "hipOccupancyMaxActiveBlocksPerMultiprocessor");
     cache.push_back({kernel, dev, cus * per_cu});
     return cus * per_cu;
+}
+
+// device_blocks for the single-pass kernels; 0 when grid_sync_enabled() is false, so that
+// callers take their multi-kernel path.
+inline int resident_blocks(const void* kernel, hipStream_t stream) {
+    if (!grid_sync_enabled(stream)) return 0;
+    return device_blocks(kernel);
 }
 
 // Whether [a, a + an) and [b, b + bn) (bytes) overlap.
