@@ -685,6 +685,61 @@ STX_API stx_status stx_concat(const stx_tensor* const* srcs, int n_srcs, int dim
 
 
 /* ------------------------------------------------------------------------------------------
+ * libstems' separate() data path (src/libstems.cpp:135-196) around a model's separate: the
+ * request's audio (planar or interleaved, any channel count and rate) is brought to the model's
+ * channels (st::to_channels, src/audio.h:62-71) and rate (st::resample_planar, :17-59), the
+ * model separates it, and the stems are resampled back with their length pinned to the input's.
+ * The GGUF loader and the model graphs stay with the caller, behind the callback.
+ * ---------------------------------------------------------------------------------------- */
+typedef int32_t stx_audio_layout;
+enum {
+    STX_AUDIO_PLANAR      = 0,     /* samples[channel * n_samples + sample] (STEMS_AUDIO_PLANAR_V1) */
+    STX_AUDIO_INTERLEAVED = 1      /* samples[sample * n_channels + channel] (STEMS_AUDIO_INTERLEAVED_V1) */
+};
+
+/* stems_audio_view_v1 (src/libstems_v1.h:84-93) over device samples. Size tagged like the
+ * reference's view: a size below STX_AUDIO_VIEW_MIN_SIZE is INVALID_ARGUMENT. */
+typedef struct {
+    uint32_t size;
+    const float* samples;          /* device */
+    uint64_t n_samples;            /* per channel */
+    uint32_t n_channels;
+    uint32_t sample_rate;
+    stx_audio_layout layout;
+    uint32_t reserved;
+} stx_audio_view;
+
+/* The model's Separator::separate at its own rate and channel count (src/separator.h:53,
+ * src/libstems.cpp:184): audio device [channels][len] -> stems device [n_sources][channels][len],
+ * e.g. stx_demix_track, stx_htdemucs_separate or stx_tfc_tdf_separate around the model's graph.
+ * options carries the request's shifts, overlap, seed and callbacks. Work may be enqueued on
+ * `stream`. Return STX_STATUS_OK, or a status that stx_separate_audio returns as it is. */
+typedef stx_status (*stx_model_separate_fn)(void* user, const float* audio, int channels, int64_t len,
+                                            const stx_separate_options* options, float* stems,
+                                            stx_stream stream);
+
+/* Bytes of device workspace stx_separate_audio needs for this input and model (0 for an input
+ * it rejects). */
+STX_API size_t stx_separate_audio_workspace_size(const stx_audio_view* input, int model_channels, int model_rate,
+                                                 int n_sources);
+
+/* separate() of libstems V1 (src/libstems.cpp:135-196) on the device. Checks as the reference's
+ * (:141-155): INVALID_ARGUMENT for a missing or short view, no samples, a zero count, channel count
+ * or rate, an unknown layout, more than INT32_MAX / 4 samples, shifts outside 0..10 or
+ * overlap >= 1. Then: the input in planar model channels (:160-167; input channel
+ * min(c, n_channels - 1) for model channel c, channel 0 for mono), resampled to model_rate when
+ * the rates differ through to_model (a plan for sample_rate -> model_rate), the model's separate,
+ * and each stem resampled back through from_model (model_rate -> sample_rate), its length pinned
+ * to n_samples: cut, or padded with zeros (:186-196). The plans are unused (may be NULL) when
+ * the rates are equal. out: device [n_sources][model_channels][n_samples]. The resampling is
+ * stx_resample's (STX_RESAMPLE_EXACT=1 gives the reference's bits). */
+STX_API stx_status stx_separate_audio(const stx_audio_view* input, int model_channels, int model_rate, int n_sources,
+                                      const stx_resampler* to_model, const stx_resampler* from_model,
+                                      stx_model_separate_fn separate, void* separate_user,
+                                      const stx_separate_options* options, float* out, void* workspace,
+                                      size_t workspace_bytes, stx_stream stream);
+
+/* ------------------------------------------------------------------------------------------
  * Versioned function table (after libstems V1, src/libstems_v1.h:146-189). Every entry point
  * above, in header order; a later revision of V1 may append entries (never reorder them), so
  * a consumer checks `size` against the prefix it needs.
@@ -865,6 +920,15 @@ typedef struct stx_api_v1 {
                                const stx_tensor* dst, stx_stream stream);
     stx_status (*concat)(const stx_tensor* const* srcs, int n_srcs, int dim, const stx_tensor* dst,
                          stx_stream stream);
+    /* Appended to V1 after STX_API_V1_MIN_SIZE: check `size` before using these. */
+    size_t (*separate_audio_workspace_size)(const stx_audio_view* input, int model_channels,
+                                            int model_rate, int n_sources);
+    stx_status (*separate_audio)(const stx_audio_view* input, int model_channels, int model_rate,
+                                 int n_sources, const stx_resampler* to_model,
+                                 const stx_resampler* from_model, stx_model_separate_fn separate,
+                                 void* separate_user, const stx_separate_options* options,
+                                 float* out, void* workspace, size_t workspace_bytes,
+                                 stx_stream stream);
     void (*reserved[16])(void);
 } stx_api_v1;
 
@@ -873,6 +937,7 @@ typedef struct stx_api_v1 {
 #define STX_SEPARATE_OPTIONS_MIN_SIZE STX_FIELD_END(stx_separate_options, user)
 #define STX_DEMIX_GEOMETRY_MIN_SIZE   STX_FIELD_END(stx_demix_geometry, n_chunks)
 #define STX_API_V1_MIN_SIZE           STX_FIELD_END(stx_api_v1, concat)
+#define STX_AUDIO_VIEW_MIN_SIZE       STX_FIELD_END(stx_audio_view, reserved)
 
 /* The one symbol a dynamically loading consumer resolves: the static V1 table (owned by the
  * library for the lifetime of the module) for abi_version STX_ABI_VERSION_1, NULL for any other

@@ -77,3 +77,22 @@ int orc_resample(const float* in, int n, int ch, int src_rate, int dst_rate, flo
     free(acc);
     return 0;
 }
+
+/* The request's audio in planar model channels (src/libstems.cpp:160-167, then st::to_channels,
+ * src/audio.h:62-71): planar in[c * n + i] or interleaved in[i * ch + c] copied to a planar
+ * buffer, then model channel c takes input channel 0 when the input is mono, else
+ * min(c, ch - 1) (an unchanged copy when ch == want). */
+void orc_to_channels(const float* in, long n, int ch, int layout, int want, float* out) {
+    for (int c = 0; c < want; c++) {
+        const int src = ch == want ? c : (ch == 1 ? 0 : (c < ch - 1 ? c : ch - 1));
+        for (long i = 0; i < n; i++)
+            out[(size_t)c * n + i] = layout == 0 ? in[(size_t)src * n + i] : in[(size_t)i * ch + src];
+    }
+}
+
+/* Each of `planes` planes of `back` samples cut or zero-padded to n samples
+ * (src/libstems.cpp:188-193). */
+void orc_pin_length(const float* in, long planes, long back, long n, float* out) {
+    for (long k = 0; k < planes; k++)
+        for (long i = 0; i < n; i++) out[(size_t)k * n + i] = i < back ? in[(size_t)k * back + i] : 0.0f;
+}

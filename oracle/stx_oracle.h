@@ -39,6 +39,8 @@
  *     exactly 0 and 1; np.hanning against numpy's own), numpy restatements of both loops on
  *     small inputs, the identity model (both must return the mix), and the UVR geometry of the
  *     reference's defaults (trim n_fft / 2, step chunk - n_fft).
+ *   orc_to_channels / orc_pin_length: numpy's transpose (interleaved to planar), fancy indexing
+ *     by the channel map and slicing / zero padding, on every layout and channel count case.
  *   orc_resample: src == dst returns the input; a numpy restatement of the tabulated kernel,
  *     bit for bit; the direct Kaiser-sinc formula (no table) to the interpolation error; and
  *     the closed forms of a band-limited sine (passband gain 1) and of DC.
@@ -136,6 +138,10 @@ void orc_tfc_post(const float* mix, long plane, int S, float compensate, int com
 void orc_resample_table(int src_rate, int dst_rate, double* table, double* half);
 long orc_resample_length(long n, int src_rate, int dst_rate);
 int orc_resample(const float* in, int n, int ch, int src_rate, int dst_rate, float* out);
+/* libstems separate()'s audio steps (src/libstems.cpp:160-196) (resample_oracle.c): layout 0
+ * planar, 1 interleaved. */
+void orc_to_channels(const float* in, long n, int ch, int layout, int want, float* out);
+void orc_pin_length(const float* in, long planes, long back, long n, float* out);
 
 /* ggml ops (ops_oracle.c). Contiguous tensors, ggml extents ne[4] (ne[0] fastest); broadcast
  * operands repeat into ne. */

@@ -93,6 +93,8 @@ const stx_api_v1 kApiV1 = {
     &stx_merge_heads,
     &stx_cont_permute,
     &stx_concat,
+    &stx_separate_audio_workspace_size,
+    &stx_separate_audio,
     {},
 };
 }  // namespace

@@ -132,9 +132,8 @@ __device__ __forceinline__ void record_store(unsigned long long* r, double s1, d
     sync_store(r + 2, record_tag(a, b, key));
 }
 // Polls r (at most limit times after the first look) until it holds a record under key; false
-// if it never did. One poll in flight with a short pause between polls: with every block of a
-// launch polling, a second poll in flight or no pause measured slower (the device-scope loads
-// of all blocks share the coherence point).
+// if it never did. One poll in flight, issued as soon as the previous one has been checked (a
+// pause of 64 or 128 clocks between polls, or a second poll in flight, measured slower).
 __device__ __forceinline__ bool record_wait(const unsigned long long* r, unsigned long long key, unsigned limit,
                                             double& s1, double& s2) {
     for (unsigned spins = 0;;) {
@@ -145,7 +144,6 @@ __device__ __forceinline__ bool record_wait(const unsigned long long* r, unsigne
             return true;
         }
         if (++spins > limit) return false;
-        __builtin_amdgcn_s_sleep(2);
     }
 }
 

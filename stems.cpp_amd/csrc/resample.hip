@@ -22,6 +22,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "resample.hpp"
 
 struct stx_resampler {
     int src = 0, dst = 0;
@@ -261,6 +262,13 @@ double bessel_i0(double x) {
 void check_resampler(const stx_resampler* r) { STX_REQUIRE(r != nullptr, "null resampler"); }
 
 }  // namespace
+
+void resampler_rates(const stx_resampler* r, int& src, int& dst) {
+    check_resampler(r);
+    src = r->src;
+    dst = r->dst;
+}
+
 }  // namespace stx
 
 using namespace stx;

@@ -119,6 +119,8 @@ _SIGNATURES = {
     "stx_merge_heads": (_i, [_vp, _vp, _vp, _vp]),
     "stx_cont_permute": (_i, [_vp, _i, _i, _i, _i, _vp, _vp]),
     "stx_concat": (_i, [_vp, _i, _i, _vp, _vp]),
+    "stx_separate_audio_workspace_size": (ctypes.c_size_t, [_vp, _i, _i, _i]),
+    "stx_separate_audio": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
 }
 
 
@@ -666,6 +668,70 @@ class Resampler:
             out = torch.empty((C, self.length(n)), dtype=torch.float32, device=x.device)
         check(lib().stx_resample(self.handle, _ptr(x), C, n, _ptr(out), _stream(stream)))
         return out
+
+
+# ------------------------------------------------------------ libstems separate() data path
+AUDIO_PLANAR, AUDIO_INTERLEAVED = 0, 1
+MODEL_SEPARATE_FN = ctypes.CFUNCTYPE(ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64,
+                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p)
+
+
+class AudioView(ctypes.Structure):
+    """stx_audio_view (size tagged), over device samples."""
+    _fields_ = [("size", ctypes.c_uint32), ("samples", ctypes.c_void_p), ("n_samples", ctypes.c_uint64),
+                ("n_channels", ctypes.c_uint32), ("sample_rate", ctypes.c_uint32), ("layout", ctypes.c_int32),
+                ("reserved", ctypes.c_uint32)]
+
+
+def audio_view(samples, n_samples, n_channels, sample_rate, layout):
+    v = AudioView()
+    v.size = ctypes.sizeof(AudioView)
+    v.samples = samples if isinstance(samples, int) or samples is None else _ptr(samples)
+    v.n_samples, v.n_channels, v.sample_rate, v.layout = int(n_samples), int(n_channels), int(sample_rate), int(layout)
+    return v
+
+
+def separate_audio(samples, n_channels, sample_rate, layout, model_channels, model_rate, n_sources, separate,
+                   to_model=None, from_model=None, shifts=0, overlap=-1.0, seed=0, progress=None,
+                   should_cancel=None, stream=None):
+    """libstems separate() (src/libstems.cpp:135-196) around a Python model separate.
+
+    samples: float32 device tensor, planar [n_channels, n] or interleaved [n, n_channels] (flat
+    is fine). separate(audio_ptr, channels, length, options_ptr, stems_ptr, stream_ptr) -> status
+    gets raw device pointers: audio [channels][length] and stems [n_sources][channels][length].
+    Returns float32 [n_sources, model_channels, n]."""
+    import torch
+    _require(samples, torch.float32, "samples")
+    n = samples.numel() // int(n_channels)
+    view = audio_view(samples, n, n_channels, sample_rate, layout)
+    need = lib().stx_separate_audio_workspace_size(ctypes.byref(view), int(model_channels), int(model_rate),
+                                                   int(n_sources))
+    ws = workspace(max(need, 4), samples.device)
+    out = torch.empty((int(n_sources), int(model_channels), n), dtype=torch.float32, device=samples.device)
+
+    def sep(user, audio, channels, length, opt, stems, st):
+        try:
+            return int(separate(audio, channels, length, opt, stems, st))
+        except Exception:
+            import traceback
+            traceback.print_exc()
+            return STATUS_RUNTIME_ERROR
+
+    def prog(user, done, total):
+        progress(done, total)
+
+    def canc(user):
+        return 1 if should_cancel() else 0
+
+    cb = MODEL_SEPARATE_FN(sep)
+    opt = SeparateOptions(int(shifts), float(overlap), int(seed),
+                          PROGRESS_FN(prog) if progress else PROGRESS_FN(),
+                          CANCEL_FN(canc) if should_cancel else CANCEL_FN(), None)
+    h = lambda r: None if r is None else r.handle
+    check(lib().stx_separate_audio(ctypes.byref(view), int(model_channels), int(model_rate), int(n_sources),
+                                   h(to_model), h(from_model), ctypes.cast(cb, ctypes.c_void_p), None,
+                                   ctypes.byref(opt), _ptr(out), _ptr(ws), ws.numel() * 4, _stream(stream)))
+    return out
 
 
 # ------------------------------------------------------------ HTDemucs pre/post + split

@@ -138,6 +138,25 @@ int main(int argc, char** argv) {
     CHECK_FN(cont_permute, "stx_cont_permute");
     CHECK_FN(concat, "stx_concat");
     check(all, "every entry is set and is the exported function of its name");
+    /* Entries appended after the frozen V1 prefix: present when size covers them. */
+    check(api->size >= offsetof(stx_api_v1, separate_audio) + sizeof(api->separate_audio),
+          "the table covers the appended separate_audio entries");
+    all = 1;
+    CHECK_FN(separate_audio_workspace_size, "stx_separate_audio_workspace_size");
+    CHECK_FN(separate_audio, "stx_separate_audio");
+    check(all, "appended entries are the exported functions of their names");
+    {
+        stx_audio_view view;
+        memset(&view, 0, sizeof view);
+        view.size = sizeof view;
+        check(api->separate_audio_workspace_size(&view, 2, 44100, 4) == 0,
+              "separate_audio_workspace_size is 0 for an empty view");
+        view.size = 4;
+        check(api->separate_audio(&view, 2, 44100, 4, NULL, NULL, NULL, NULL, NULL, NULL, NULL, 0, NULL) ==
+                  STX_STATUS_INVALID_ARGUMENT && api->last_error()[0] != '\0',
+              "separate_audio with a too-small view is INVALID_ARGUMENT");
+        check(STX_AUDIO_VIEW_MIN_SIZE == sizeof view, "STX_AUDIO_VIEW_MIN_SIZE is the V1 view");
+    }
     const char* v = api->version();
     check(v != NULL && strchr(v, '.') != NULL, "version() through the table");
     printf("  version: %s\n", v ? v : "(null)");

@@ -655,7 +655,39 @@ class _Resample:
         L.orc_resample_length.argtypes = [ctypes.c_long, _i, _i]
         L.orc_resample_table.restype = None
         L.orc_resample_table.argtypes = [_i, _i, _vp, ctypes.POINTER(ctypes.c_double)]
+        L.orc_to_channels.restype = None
+        L.orc_to_channels.argtypes = [_vp, ctypes.c_long, _i, _i, _i, _vp]
+        L.orc_pin_length.restype = None
+        L.orc_pin_length.argtypes = [_vp, ctypes.c_long, ctypes.c_long, ctypes.c_long, _vp]
         self.L = L
+
+    def to_channels(self, samples, n, ch, layout, want):
+        """samples: flat float32 (planar [ch][n] or interleaved [n][ch]) -> [want][n]."""
+        x = np.ascontiguousarray(samples, dtype=np.float32).reshape(-1)
+        out = np.zeros((want, n), np.float32)
+        self.L.orc_to_channels(_np(x), n, ch, layout, want, _np(out))
+        return out
+
+    def pin_length(self, x, n):
+        """x [planes][back] -> [planes][n], cut or zero-padded."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        planes, back = x.shape
+        out = np.zeros((planes, n), np.float32)
+        self.L.orc_pin_length(_np(x), planes, back, n, _np(out))
+        return out
+
+    def separate_audio(self, samples, n, ch, layout, sr, C, R, model):
+        """libstems separate() (src/libstems.cpp:160-196) around model(audio [C][len]) ->
+        stems [S][C][len], composed from the oracle's steps."""
+        a = self.to_channels(samples, n, ch, layout, C)
+        if sr != R:
+            a = self(a, sr, R)
+        stems = np.ascontiguousarray(model(a), dtype=np.float32)
+        if sr == R:
+            return stems
+        S = stems.shape[0]
+        back = self(stems.reshape(S * C, -1), R, sr)
+        return self.pin_length(back, n).reshape(S, C, n)
 
     def table(self, src, dst):
         t = np.zeros((1 << 15) + 2, np.float64)

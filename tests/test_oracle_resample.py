@@ -71,3 +71,25 @@ def test_passband_sine_and_dc(rs):
     mid = slice(200, m - 200)
     assert np.max(np.abs(y[0, mid] - np.sin(2 * np.pi * 1000 * ty[mid]))) <= 2e-3
     assert np.max(np.abs(y[1, mid] - 1.0)) <= 2e-3
+
+
+@pytest.mark.parametrize("ch,layout,want", [(2, 0, 2), (2, 1, 2), (1, 0, 2), (1, 1, 2), (3, 1, 2), (3, 0, 2),
+                                             (2, 1, 1), (4, 1, 6)])
+def test_to_channels_against_numpy(rs, ch, layout, want):
+    """libstems' de-interleave (src/libstems.cpp:160-167) and st::to_channels (src/audio.h:62-71)
+    against numpy's transpose and a fancy index by the channel map."""
+    n = 37
+    x = synth.normal(ch * 10 + layout, (ch * n,), 1.0).astype(np.float32)
+    planar = x.reshape(n, ch).T if layout == 1 else x.reshape(ch, n)
+    src = list(range(want)) if ch == want else [0 if ch == 1 else min(c, ch - 1) for c in range(want)]
+    assert np.array_equal(rs.to_channels(x, n, ch, layout, want), planar[src])
+
+
+@pytest.mark.parametrize("back,n", [(10, 10), (12, 10), (7, 10), (1, 3)])
+def test_pin_length_against_numpy(rs, back, n):
+    """The length pinning of src/libstems.cpp:188-193: cut to n, or padded with zeros."""
+    x = synth.normal(back + n, (3, back), 1.0).astype(np.float32)
+    want = np.zeros((3, n), np.float32)
+    m = min(back, n)
+    want[:, :m] = x[:, :m]
+    assert np.array_equal(rs.pin_length(x, n), want)
