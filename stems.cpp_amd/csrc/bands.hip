@@ -500,6 +500,61 @@ __global__ __launch_bounds__(256) void band_rms_norm_kernel(BandNormArgs a) {
     }
 }
 
+// The same with 16-byte accesses, for an even channel count (every row and band block then
+// starts on a float4) and 16-byte aligned buffers: L_b lanes per frame with at most
+// kBandNormPer / 2 float4 per lane. Half the memory instructions of the float2 form for the same
+// payload per lane; the sum of squares is added in (lane, float4) order instead of (lane,
+// float2), so its rounding differs from that form's.
+template <int V>
+__global__ __launch_bounds__(256) void band_rms_norm_v4_kernel(BandNormArgs a) {
+    const int blk = (int)blockIdx.x;
+    int lo = 0, hi = a.nb - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (a.first_block[mid] <= blk) lo = mid;
+        else hi = mid - 1;
+    }
+    const int bi = lo;
+    const BandInfo info = a.bands[a.b0 + bi];
+    const int d = info.size * a.C / 2;               // float4 per row
+    const int lg = a.lanes_log2[bi], L = 1 << lg;
+    const int lane = (int)threadIdx.x & (L - 1), rr = (int)threadIdx.x >> lg;
+    const int t = (blk - a.first_block[bi]) * (256 >> lg) + rr;
+    const long long base = (long long)blockIdx.y * a.total_feat * a.T + info.feat_off * a.T +
+                           (long long)min(t, a.T - 1) * 4 * d;
+    const float4* x = reinterpret_cast<const float4*>(a.feat + base);
+    const float4* g = reinterpret_cast<const float4*>(a.gamma[bi]);
+    const int nk = (d + L - 1) >> lg;
+    float4 v[V], gv[V];
+#pragma unroll
+    for (int k = 0; k < V; k++) {
+        if (k < nk) {
+            const int q = min(lane + (k << lg), d - 1);
+            v[k] = x[q];
+            gv[k] = g[q];
+        } else {
+            v[k] = gv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int k = 0; k < V; k++) {
+        if (lane + (k << lg) < d)
+            ss += ((double)v[k].x * v[k].x + (double)v[k].y * v[k].y) + ((double)v[k].z * v[k].z + (double)v[k].w * v[k].w);
+    }
+    ss = lane_sum_dyn(ss, L);
+    const float scale = (float)(1.0 / sqrt(ss / (4.0 * d) + (double)a.eps));
+    if (t >= a.T) return;
+    float4* y = reinterpret_cast<float4*>(a.out + base);
+#pragma unroll
+    for (int k = 0; k < V; k++) {
+        const int q = lane + (k << lg);
+        if (k < nk && q < d)
+            store_stream(y + q, make_float4((v[k].x * scale) * gv[k].x, (v[k].y * scale) * gv[k].y,
+                                            (v[k].z * scale) * gv[k].z, (v[k].w * scale) * gv[k].w));
+    }
+}
+
 // ------------------------------------------------------------------- mask-head GLU
 // The GLU that ends every mask estimator (src/roformer.cpp:199-204): for stem s and band b the
 // last layer's output h [T][2 * dim_in(b)] becomes m[t][i] = h[t][i] * sigmoid(h[t][dim_in + i]),
@@ -858,10 +913,17 @@ STX_API stx_status stx_band_rms_norm(const stx_bands* h, const float* feat, int 
             long long blocks = 0;
             int max_nk = 1;
             const int nb = std::min(kBandTable, h->n_bands - b0);
+            // 16-byte accesses when every row starts on a float4 (an even channel count) and
+            // every buffer is 16-byte aligned.
+            bool v4 = h->channels % 2 == 0 && (reinterpret_cast<uintptr_t>(feat) & 15) == 0 &&
+                      (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+            for (int i = 0; i < nb; i++) v4 = v4 && (reinterpret_cast<uintptr_t>(gammas[b0 + i]) & 15) == 0;
+            const int unit = v4 ? 4 : 2;                 // floats per access
+            const int per = v4 ? kBandNormPer / 2 : kBandNormPer;
             for (int i = 0; i < nb; i++) {
-                const int d = (int)((h->feat_off[b0 + i + 1] - h->feat_off[b0 + i]) / 2);
+                const int d = (int)((h->feat_off[b0 + i + 1] - h->feat_off[b0 + i]) / unit);
                 int lg = 0;
-                while ((1 << lg) < 64 && (1 << lg) * kBandNormPer < d) lg++;
+                while ((1 << lg) < 64 && (1 << lg) * per < d) lg++;
                 a.gamma[i] = gammas[b0 + i];
                 a.lanes_log2[i] = (unsigned char)lg;
                 a.first_block[i] = (int)blocks;      // an empty band gets no blocks: the search skips it
@@ -873,9 +935,17 @@ STX_API stx_status stx_band_rms_norm(const stx_bands* h, const float* feat, int 
             a.first_block[nb] = (int)blocks;
             a.nb = nb;
             const dim3 grid((unsigned)blocks, (unsigned)batch);
-            if (max_nk <= 4) hipLaunchKernelGGL(band_rms_norm_kernel<4>, grid, dim3(256), 0, s, a);
-            else if (max_nk <= 8) hipLaunchKernelGGL(band_rms_norm_kernel<8>, grid, dim3(256), 0, s, a);
-            else hipLaunchKernelGGL(band_rms_norm_kernel<16>, grid, dim3(256), 0, s, a);
+            if (v4) {
+                if (max_nk <= 2) hipLaunchKernelGGL(band_rms_norm_v4_kernel<2>, grid, dim3(256), 0, s, a);
+                else if (max_nk <= 4) hipLaunchKernelGGL(band_rms_norm_v4_kernel<4>, grid, dim3(256), 0, s, a);
+                else hipLaunchKernelGGL(band_rms_norm_v4_kernel<8>, grid, dim3(256), 0, s, a);
+            } else if (max_nk <= 4) {
+                hipLaunchKernelGGL(band_rms_norm_kernel<4>, grid, dim3(256), 0, s, a);
+            } else if (max_nk <= 8) {
+                hipLaunchKernelGGL(band_rms_norm_kernel<8>, grid, dim3(256), 0, s, a);
+            } else {
+                hipLaunchKernelGGL(band_rms_norm_kernel<16>, grid, dim3(256), 0, s, a);
+            }
             launch_check("band_rms_norm_kernel");
         }
     });

@@ -288,6 +288,31 @@ def test_band_rms_norm(device, mel, kind, T, batch):
     assert rel_err(y[0, off:off + din * T].reshape(T, din), one) <= 1e-6
 
 
+@pytest.mark.parametrize("C,misalign", [(1, False), (2, True), (3, False)])
+def test_band_rms_norm_float2_kernel(device, mel, C, misalign):
+    """The float2 kernel, taken for an odd channel count or a buffer that is not 16-byte aligned
+    (the float4 kernel needs neither): the same oracle bound."""
+    import torch
+    ops = oracle_lib.ops()
+    sizes, freqs = mel
+    T = 37
+    bands = stx.Bands(sizes, freqs, 1025, C)
+    feat = synth.normal(31 + C, (1, bands.total_feat * T), 0.7)
+    gam = [synth.normal(200 + b, (int(s) * C * 2,), 1.0) for b, s in enumerate(sizes)]
+    if misalign:       # gamma of band 3 one float past a 16-byte boundary
+        g3 = torch.zeros(gam[3].size + 1, dtype=torch.float32, device=device)
+        g3[1:] = dev(gam[3], device)
+        gd = [dev(g, device) for g in gam]
+        gd[3] = g3[1:]
+        assert gd[3].data_ptr() % 16 != 0
+    else:
+        gd = [dev(g, device) for g in gam]
+    y = host(bands.rms_norm(dev(feat, device), T, gd, eps=1e-24))
+    for (off, din), g in zip(band_blocks(sizes, C, T), gam):
+        x = feat[0, off:off + din * T].reshape(T, din)
+        assert rel_err(y[0, off:off + din * T].reshape(T, din), ops.norm(x, 1e-24, rms=True, w=g)) <= 1e-6
+
+
 @pytest.mark.parametrize("kind,S,T", [("mel", 4, 801), ("bs", 2, 801), ("mel", 9, 33)])
 def test_band_mask_glu(device, mel, kind, S, T):
     """src/roformer.cpp:199-204: GLU on dim 0 of every (stem, band) head into the mask layout
