@@ -104,6 +104,30 @@ def test_uvr_ola_non_finite_outputs(device, od):
     assert np.array_equal(got, want, equal_nan=True)
 
 
+def test_uvr_ola_extreme_magnitudes(device, od):
+    """Where one chunk covers a sample with a non-zero weight, the kernel copies the model's value
+    (the reference's (0 + y w) / (0 + w) rounds back to y); checked bit for bit at the float
+    extremes: subnormals down to 2^-149, values up to 3.4e38, signed zeros and non-finite values,
+    in single-cover samples and in the overlaps."""
+    length, chunk, n_fft, overlap = 20000, 2048, 512, -1.0
+    plan = stx.UvrDemix(length, 2, chunk, n_fft, overlap)
+    rng = np.random.default_rng(5)
+    y = synth.uniform(41, (plan.n_chunks, 2, 2, chunk))
+    y *= np.exp2(rng.integers(-149, 127, y.shape)).astype(np.float32)
+    flat = y.reshape(-1)
+    idx = rng.choice(flat.size, 64, replace=False)
+    flat[idx[:16]] = np.float32(2.0 ** -149)
+    flat[idx[16:24]] = -0.0
+    flat[idx[24:32]] = np.float32(3.4e38)
+    flat[idx[32:36]] = np.inf
+    flat[idx[36:40]] = np.nan
+    got = host(plan.overlap_add(dev(y, device)))
+    want = od.uvr_ola(y, length, chunk, n_fft, overlap)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    m = ~np.isnan(got)
+    assert np.array_equal(got[m].view(np.uint32), want[m].view(np.uint32))          # signed zeros too
+
+
 def test_uvr_errors(device):
     with pytest.raises(stx.StxError) as e:
         stx.UvrDemix(1000, 2, 100, 128)
