@@ -244,8 +244,8 @@ def run_ops(args, torch, stx, dev):
     dom_bytes = sum(nbytes[dom])
     achieved = dom_bytes / (share[dom] * 1e-6) / 1e9
     step_bytes = sum(sum(v) for v in op_bytes().values())
-    kernel_names = {"gn": "group_norm+affine+gelu (gn_fused_kernel<channel,gelu>, one grid-synchronised pass, at "
-                          "C = 96, 192, 384; gn_partial_kernel + gn_apply_kernel at C = 48)",
+    kernel_names = {"gn": "group_norm+affine+gelu (gn_fused_kernel<channel,gelu,width>, one grid-synchronised pass "
+                          "at each of the four shapes)",
                     "glu_scale_residual": "glu + layer scale + residual (ew_flat_kernel<GLU_MUL_ADD>)"}
     moved = sum(sum(v) for v in moved_bytes().values())
     res = {
