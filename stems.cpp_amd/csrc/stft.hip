@@ -101,7 +101,10 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void stft_kernel(StftArgs a) {
     using C = FftCfg<M, P, N>;
     constexpr int TPJ = C::TPJ;
     constexpr int NT = JOBS * TPJ;
-    __shared__ float2 lds[JOBS * C::PADN];
+    // Slots one float2 longer than the transform's buffer, so that the same element of
+    // neighbouring slots (the lanes of one bin in the f-major stores) lies in different banks.
+    constexpr int SLOT = C::PADN + 1;
+    __shared__ float2 lds[JOBS * SLOT];
     __shared__ float2 twt[TwTable<N>::SIZE];
 
     const int lb = xcd_block();
@@ -111,7 +114,7 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void stft_kernel(StftArgs a) {
     const int j = tid % TPJ;
     const int f = lb * JOBS + slot;
     const bool active = f < a.jobs;
-    float2* buf = lds + slot * C::PADN;
+    float2* buf = lds + slot * SLOT;
 
     StagedTwiddles<N, NT> tws;
     tws.load(a.twt, tid);                              // overlaps the frame's loads
@@ -180,7 +183,7 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void stft_kernel(StftArgs a) {
         int tt = t0 + g, cc = c0;
         while (tt >= a.T) { tt -= a.T; cc++; }
         if (f0 + g < a.jobs) {
-            const float2* bs = lds + g * C::PADN;
+            const float2* bs = lds + g * SLOT;
             float2* col = a.spec + (size_t)cc * a.F * a.T + tt;
             const unsigned rs = (unsigned)a.T * KS;           // row step of one bin stride
             unsigned off = (unsigned)k0 * a.T;
@@ -208,7 +211,7 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void stft_kernel(StftArgs a) {
             const float2 w = tw_lookup<N>(twt, k);
 #pragma unroll
             for (int g = 0; g < JOBS; g++)
-                if (rows[g]) store_stream(rows[g] + k, bin(lds + g * C::PADN, k, ik, im, w, std::integral_constant<int, NT>{}));
+                if (rows[g]) store_stream(rows[g] + k, bin(lds + g * SLOT, k, ik, im, w, std::integral_constant<int, NT>{}));
         }
     }
 }
@@ -323,11 +326,12 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
     using C = FftCfg<M, P, N>;
     constexpr int TPJ = C::TPJ;
     constexpr int NT = JOBS * TPJ;
-    constexpr bool WIN_LDS = (size_t)JOBS * C::PADN * 8 + TwTable<N>::SIZE * 8 + N * 4 <= 160 * 1024;
+    constexpr int SLOT = C::PADN;                      // (a slot one float2 longer measured no faster)
+    constexpr bool WIN_LDS = (size_t)JOBS * SLOT * 8 + TwTable<N>::SIZE * 8 + N * 4 <= 160 * 1024;
     // Reciprocal window-squared envelope per position R = J mod hop where every covering
     // frame exists (R < N suffices: positions past N have no frame).
-    constexpr bool ENV_LDS = WIN_LDS && (size_t)JOBS * C::PADN * 8 + TwTable<N>::SIZE * 8 + N * 8 <= 160 * 1024;
-    __shared__ float2 lds[JOBS * C::PADN];
+    constexpr bool ENV_LDS = WIN_LDS && (size_t)JOBS * SLOT * 8 + TwTable<N>::SIZE * 8 + N * 8 <= 160 * 1024;
+    __shared__ float2 lds[JOBS * SLOT];
     __shared__ float2 twt[TwTable<N>::SIZE];
     __shared__ float wl[WIN_LDS ? N : 2];
     __shared__ float inv_env[ENV_LDS ? N : 2];
@@ -339,7 +343,7 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
     const int tid = (int)threadIdx.x;
     const int slot = tid / TPJ;
     const int j = tid % TPJ;
-    float2* buf = lds + slot * C::PADN;
+    float2* buf = lds + slot * SLOT;
     const int hop = a.hop;
 
     // The twiddle and window tables are loaded into registers here and written to LDS after the
@@ -409,9 +413,9 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
             }
             const bool live = s0 + g <= st_hi;
 #pragma unroll
-            for (int i = 0; i < P; i++) lds[g * C::PADN + k0 + i * TPJ] = live ? sv[i] : make_float2(0.f, 0.f);
+            for (int i = 0; i < P; i++) lds[g * SLOT + k0 + i * TPJ] = live ? sv[i] : make_float2(0.f, 0.f);
             if (tr < JOBS)
-                lds[tr * C::PADN + M] = (s0 + tr <= st_hi && M < a.F) ? nyq : make_float2(0.f, 0.f);
+                lds[tr * SLOT + M] = (s0 + tr <= st_hi && M < a.F) ? nyq : make_float2(0.f, 0.f);
         } else {
             // Element e = tr + i*NT: slot e / M, bin e % M.
             auto slot_of = [&](int i) {
@@ -434,9 +438,9 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
             }
 #pragma unroll
             for (int i = 0; i < P; i++)
-                lds[slot_of(i) * C::PADN + bin_of(i)] = s0 + slot_of(i) <= st_hi ? sv[i] : make_float2(0.f, 0.f);
+                lds[slot_of(i) * SLOT + bin_of(i)] = s0 + slot_of(i) <= st_hi ? sv[i] : make_float2(0.f, 0.f);
             if (tr < JOBS)
-                lds[tr * C::PADN + M] = (s0 + tr <= st_hi && M < a.F) ? nyq : make_float2(0.f, 0.f);
+                lds[tr * SLOT + M] = (s0 + tr <= st_hi && M < a.F) ? nyq : make_float2(0.f, 0.f);
         }
         __syncthreads();
         float2 v[P];
@@ -459,9 +463,9 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
             // Sample pos (0 <= pos < N) of slot g is float 2*idx(pos/2) + pos%2 of the slot,
             // i.e. pos + 2*(pos / 2P).
             unsigned pos = (unsigned)(s_first - i0 * hop);
-            const float* sl = ldsf + 2 * C::PADN * (first + i0 - s0);
+            const float* sl = ldsf + 2 * SLOT * (first + i0 - s0);
             float sum = acc[q];
-            for (int i = i0; i <= i1; i++, pos -= (unsigned)hop, sl += 2 * C::PADN)
+            for (int i = i0; i <= i1; i++, pos -= (unsigned)hop, sl += 2 * SLOT)
                 sum += sl[pos + 2 * (pos / (2 * P))];
             acc[q] = sum;
         });
