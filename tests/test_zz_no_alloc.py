@@ -32,7 +32,7 @@ def host(t):
 
 
 @pytest.mark.parametrize("calls", [
-    [((48, 1, 85995), 1, True), ((384, 1, 1344), 1, True)],            # two passes, then one (larger, then smaller)
+    [((48, 1, 85995), 1, True), ((384, 1, 1344), 1, True)],            # single pass, larger then smaller
     [((96, 1, 21499), 1, False), ((8, 1, 3000), 4, False)],
     [((1000, 1, 8192), 1000, True), ((200, 1, 4000), 50, True)],        # two passes (many groups)
 ])
