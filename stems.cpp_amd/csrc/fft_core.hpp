@@ -242,6 +242,22 @@ __device__ __forceinline__ void twiddle_powers(const float2* __restrict__ twt, i
     }
 }
 
+// Orders the LDS accesses of one wave around an exchange among its own lanes. A wave's LDS
+// instructions are performed in the order they are issued, so no wait is needed: only the
+// compiler has to be kept from moving accesses across this point.
+__device__ __forceinline__ void wave_lds_sync() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+}
+// Between two passes: the workgroup's barrier, or the wave's ordering when every transform
+// belongs to one wave (WAVE: TPJ == 64, so no lane reads another wave's data).
+template <bool WAVE>
+__device__ __forceinline__ void pass_sync() {
+    if constexpr (WAVE) wave_lds_sync();
+    else __syncthreads();
+}
+
 struct NoPost {
     __device__ __forceinline__ float2 operator()(int, float2 v) const { return v; }
 };
@@ -274,8 +290,9 @@ __device__ __forceinline__ void fft_first_pass(float2* v, float2* buf, int j, co
 
 // Remaining passes, in place in `buf`. Every thread of the workgroup must call this (it
 // contains barriers), also threads whose transform is idle. The last pass hands every output
-// element n (natural order) to sink(n, post(n, v)).
-template <int M, int P, int TN, int Ns, class Post, class Sink>
+// element n (natural order) to sink(n, post(n, v)). With WAVE (each transform is one wave's)
+// the passes are ordered per wave, and no workgroup barrier follows the last one.
+template <int M, int P, int TN, int Ns, bool WAVE = false, class Post, class Sink>
 __device__ __forceinline__ void fft_rest_passes(float2* buf, int j, const float2* __restrict__ twt,
                                                 const Post& post, const Sink& sink) {
     if constexpr (Ns < M) {
@@ -296,7 +313,7 @@ __device__ __forceinline__ void fft_rest_passes(float2* buf, int j, const float2
 #pragma unroll
             for (int r = 0; r < R; r++) v[q * R + r] = rd[r * RS];
         }
-        __syncthreads();
+        pass_sync<WAVE>();
 #pragma unroll
         for (int q = 0; q < BPT; q++) {
             const int jj = j + q * TPJ;
@@ -316,8 +333,8 @@ __device__ __forceinline__ void fft_rest_passes(float2* buf, int j, const float2
                 else wr[r * WS] = v[q * R + r];
             }
         }
-        __syncthreads();
-        fft_rest_passes<M, P, TN, Ns * R>(buf, j, twt, post, sink);
+        pass_sync<WAVE>();
+        fft_rest_passes<M, P, TN, Ns * R, WAVE>(buf, j, twt, post, sink);
     }
 }
 

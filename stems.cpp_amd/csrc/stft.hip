@@ -327,6 +327,9 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
     constexpr int TPJ = C::TPJ;
     constexpr int NT = JOBS * TPJ;
     constexpr int SLOT = C::PADN;                      // (a slot one float2 longer measured no faster)
+    // One wave per transform: between the split and the last pass every lane touches only its
+    // own wave's slot, so those passes need no workgroup barrier.
+    constexpr bool WAVE = TPJ == 64;
     constexpr bool WIN_LDS = (size_t)JOBS * SLOT * 8 + TwTable<N>::SIZE * 8 + N * 4 <= 160 * 1024;
     // Reciprocal window-squared envelope per position R = J mod hop where every covering
     // frame exists (R < N suffices: positions past N have no frame).
@@ -449,10 +452,11 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
             const int k = jr + r * TPJ;
             v[r] = inverse_split<N>(buf[k], buf[M - k], k, a.keep_nyquist, twt);
         }
-        __syncthreads();                            // staging read before the FFT overwrites it
+        pass_sync<WAVE>();                          // staging read before the FFT overwrites it
         fft_first_pass<M, P, N>(v, buf, jr, post, ToLds<P>{buf});
-        __syncthreads();
-        fft_rest_passes<M, P, N, P>(buf, jr, twt, post, ToLds<P>{buf});
+        pass_sync<WAVE>();
+        fft_rest_passes<M, P, N, P, WAVE>(buf, jr, twt, post, ToLds<P>{buf});
+        if constexpr (WAVE) __syncthreads();        // every slot written before the sums read them
         // Slot g now holds samples (2n, 2n + 1) of frame s0 + g at LDS index n, windowed: add
         // the frames of this round that cover each sample, in frame order.
         const int s_end = min(st_hi, s0 + JOBS - 1);
