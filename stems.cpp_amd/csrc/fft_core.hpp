@@ -269,6 +269,13 @@ struct ToLds {
     __device__ __forceinline__ void operator()(int n, float2 v) const { buf[n + n / P] = v; }
 };
 
+// Sink writing element n at LDS index n (unpadded): for a last pass whose consecutive lanes
+// write consecutive elements, so the reader of the result needs no padded index.
+struct ToLdsFlat {
+    float2* buf;
+    __device__ __forceinline__ void operator()(int n, float2 v) const { buf[n] = v; }
+};
+
 // LDS addressing: element i of a transform lives at idx(i) = i + i / P. For a base b and a
 // multiple s of P, idx(b + r s) = idx(b) + r (s + s / P), so every LDS access of a butterfly is
 // one base index plus a compile-time offset (an immediate of the ds instruction) instead of an

@@ -276,6 +276,15 @@ struct WindowPost {
     }
 };
 
+// The same without the norm, which the fused kernel applies with the envelope's reciprocal.
+struct WindowMul {
+    const float2* win2;
+    __device__ __forceinline__ float2 operator()(int n, float2 r) const {
+        const float2 w = win2[n];
+        return make_float2(r.x * w.x, -r.y * w.y);
+    }
+};
+
 // Two-kernel path (mixed-radix sizes), step 2: out = sum of the windowed frames over the frames covering each
 // sample, in frame order, divided by the window-squared envelope.
 __global__ __launch_bounds__(256) void istft_ola_kernel(IstftArgs a, int N) {
@@ -364,7 +373,7 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
     const int st_lo = max(0, max(0, ceildiv(J0 - N + 1, hop)) - a.frame_off);
     const int st_hi = min(a.T - 1, floordiv(J1 - 1, hop) - a.frame_off);
     const float2* sc = a.spec + (size_t)c * a.T * a.F;
-    const WindowPost post{reinterpret_cast<const float2*>(win), a.norm};
+    const WindowMul post{reinterpret_cast<const float2*>(win)};
 
     // Samples J = J0 + q*NT + tid (q < PER). With J = A*hop + R (0 <= R < hop), the frames
     // covering J are tf = A - K .. A at positions s = R + K*hop .. R, where K = K0 when
@@ -453,24 +462,22 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
             v[r] = inverse_split<N>(buf[k], buf[M - k], k, a.keep_nyquist, twt);
         }
         pass_sync<WAVE>();                          // staging read before the FFT overwrites it
-        fft_first_pass<M, P, N>(v, buf, jr, post, ToLds<P>{buf});
+        fft_first_pass<M, P, N>(v, buf, jr, post, ToLdsFlat{buf});
         pass_sync<WAVE>();
-        fft_rest_passes<M, P, N, P, WAVE>(buf, jr, twt, post, ToLds<P>{buf});
+        fft_rest_passes<M, P, N, P, WAVE>(buf, jr, twt, post, ToLdsFlat{buf});
         if constexpr (WAVE) __syncthreads();        // every slot written before the sums read them
-        // Slot g now holds samples (2n, 2n + 1) of frame s0 + g at LDS index n, windowed: add
-        // the frames of this round that cover each sample, in frame order.
+        // Slot g now holds samples (2n, 2n + 1) of frame s0 + g at LDS index n (unpadded: the
+        // last pass's lanes write consecutive n), windowed: add the frames of this round that
+        // cover each sample, in frame order.
         const int s_end = min(st_hi, s0 + JOBS - 1);
         walk(tr, [&](int q, int tf0, int s_first, int K) {
             if (q * NT + tr >= J1 - J0) return;
             const int first = tf0 - a.frame_off;              // spectrum frame of tf0
             const int i0 = max(0, s0 - first), i1 = min(K, s_end - first);
-            // Sample pos (0 <= pos < N) of slot g is float 2*idx(pos/2) + pos%2 of the slot,
-            // i.e. pos + 2*(pos / 2P).
-            unsigned pos = (unsigned)(s_first - i0 * hop);
-            const float* sl = ldsf + 2 * SLOT * (first + i0 - s0);
+            // Sample pos (0 <= pos < N) of slot g is float pos of the slot.
+            const float* sl = ldsf + 2 * SLOT * (first + i0 - s0) + (s_first - i0 * hop);
             float sum = acc[q];
-            for (int i = i0; i <= i1; i++, pos -= (unsigned)hop, sl += 2 * SLOT)
-                sum += sl[pos + 2 * (pos / (2 * P))];
+            for (int i = i0; i <= i1; i++, sl += 2 * SLOT - hop) sum += *sl;
             acc[q] = sum;
         });
         __syncthreads();
@@ -482,11 +489,12 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
     }
 
     // Envelope: win^2 summed over the envelope frames 0 <= tf < env_frames covering J, in frame
-    // order (src/stft.h:130,187); out = acc * (1 / env) where env > 1e-11, else 0 (within an ulp
-    // of the quotient). Where all K + 1 frames of J exist, env depends on R = J mod hop only: its
-    // reciprocal (0 for env <= 1e-11) comes from a table built once per workgroup when the LDS
-    // has room; elsewhere (and at the signal's ends) the same sum and reciprocal run here, so
-    // the table changes no bit.
+    // order (src/stft.h:130,187); out = acc * (norm / env) where env > 1e-11, else 0 (the sums
+    // hold frames times the window only: the transform's norm is applied here, once per
+    // sample). Where all K + 1 frames of J exist, env depends on R = J mod hop only: norm / env
+    // (0 for env <= 1e-11) comes from a table built once per workgroup when the LDS has room;
+    // elsewhere (and at the signal's ends) the same sum and quotient run here, so the table
+    // changes no bit.
     if constexpr (ENV_LDS) {
         const int nr = min(hop, N);
         for (int R = tid; R < nr; R += NT) {
@@ -496,7 +504,7 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
                 const float w = win[R + i * hop];
                 env += w * w;
             }
-            inv_env[R] = env > 1e-11f ? 1.f / env : 0.f;
+            inv_env[R] = env > 1e-11f ? a.norm / env : 0.f;
         }
         __syncthreads();
     }
@@ -516,7 +524,7 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
                 const float w = win[pos];
                 env += w * w;
             }
-            y = env > 1e-11f ? acc[q] * (1.f / env) : 0.f;   // as the table's product
+            y = env > 1e-11f ? acc[q] * (a.norm / env) : 0.f;   // as the table's product
         }
         store_stream(oc + (J - a.out_off), y);
     });
