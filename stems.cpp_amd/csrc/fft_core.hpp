@@ -148,6 +148,37 @@ template <> struct Dft<5> {
 
 constexpr int ilog2(int n) { return n <= 1 ? 0 : 1 + ilog2(n / 2); }
 
+// cos and sin of x (|x| <= pi) by their Taylor series in double, for twiddle constants computed
+// at compile time (the terms fall below 1e-17 well before the 40th).
+constexpr double cx_cos(double x) {
+    double t = 1.0, s = 0.0;
+    for (int n = 0; n < 40; n += 2) {
+        s += t;
+        t *= -x * x / ((n + 1.0) * (n + 2.0));
+    }
+    return s;
+}
+constexpr double cx_sin(double x) {
+    double t = x, s = 0.0;
+    for (int n = 1; n < 41; n += 2) {
+        s += t;
+        t *= -x * x / ((n + 1.0) * (n + 2.0));
+    }
+    return s;
+}
+constexpr double kPi = 3.14159265358979323846;
+
+// exp(-i pi r / P) for r < P, rounded to float, as compile-time constants.
+template <int P> struct HalfTurnRoots { float re[P], im[P]; };
+template <int P> constexpr HalfTurnRoots<P> half_turn_roots() {
+    HalfTurnRoots<P> t{};
+    for (int r = 0; r < P; r++) {
+        t.re[r] = (float)cx_cos(kPi * r / P);
+        t.im[r] = (float)-cx_sin(kPi * r / P);
+    }
+    return t;
+}
+
 // Two-level twiddle table for TN points: [L low entries W^m, m < L][H high entries W^(L*h)].
 template <int TN> struct TwTable {
     static constexpr int LBITS = (ilog2(TN) + 1) / 2;

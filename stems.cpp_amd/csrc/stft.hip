@@ -407,9 +407,9 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
         __builtin_assume(jr >= 0 && jr < TPJ && tr >= 0 && tr < NT);
         // Stage X[0..M] of frames s0 .. s0 + JOBS - 1 into the slots, neighbouring lanes on
         // neighbouring addresses in either layout: bins k < M are P per thread
-        // (M * JOBS = P * NT), the Nyquist bins one each for the first JOBS threads. Every
-        // load of the round is issued before the first LDS write; frames past st_hi read
-        // frame st_hi and are zeroed afterwards.
+        // (M * JOBS = P * NT), the Nyquist bins one per slot. Every load of the round is issued
+        // before the first LDS write; slots past st_hi stage frame st_hi again (finite values,
+        // transformed but never summed: the walk stops at st_hi).
         float2 sv[P];
         if (a.layout == STX_SPEC_F_MAJOR) {
             // Element e = tr + i*NT: slot e % JOBS = tr % JOBS, bin e / JOBS = tr / JOBS + i*TPJ.
@@ -423,43 +423,37 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
                 if constexpr (WIN_LDS) wins.store(wl, tid);
                 staged = true;
             }
-            const bool live = s0 + g <= st_hi;
 #pragma unroll
-            for (int i = 0; i < P; i++) lds[g * SLOT + k0 + i * TPJ] = live ? sv[i] : make_float2(0.f, 0.f);
-            if (tr < JOBS)
-                lds[tr * SLOT + M] = (s0 + tr <= st_hi && M < a.F) ? nyq : make_float2(0.f, 0.f);
+            for (int i = 0; i < P; i++) lds[g * SLOT + k0 + i * TPJ] = sv[i];
+            if (tr < JOBS) lds[tr * SLOT + M] = M < a.F ? nyq : make_float2(0.f, 0.f);
         } else {
-            // Element e = tr + i*NT: slot e / M, bin e % M.
-            auto slot_of = [&](int i) {
-                if constexpr (NT % M == 0) return tr / M + i * (NT / M);
-                else if constexpr (M % NT == 0) return i / (M / NT);
-                else return (tr + i * NT) / M;
-            };
-            auto bin_of = [&](int i) {
-                if constexpr (NT % M == 0) return tr % M;
-                else if constexpr (M % NT == 0) return tr + (i % (M / NT)) * NT;
-                else return (tr + i * NT) % M;
-            };
+            // Thread jr of a slot: bins jr + i*TPJ of the slot's frame, the FFT's own element
+            // order (one row address, then constant offsets), and the Nyquist bin for jr == 0.
+            const float2* row = sc + (size_t)min(s0 + tr / TPJ, st_hi) * a.F;
 #pragma unroll
-            for (int i = 0; i < P; i++) sv[i] = sc[(size_t)min(s0 + slot_of(i), st_hi) * a.F + bin_of(i)];
-            const float2 nyq = sc[(size_t)min(s0 + min(tr, JOBS - 1), st_hi) * a.F + min(M, a.F - 1)];
+            for (int i = 0; i < P; i++) sv[i] = row[jr + i * TPJ];
+            const float2 nyq = row[min(M, a.F - 1)];
             if (!staged) {
                 tws.store(twt, tid);
                 if constexpr (WIN_LDS) wins.store(wl, tid);
                 staged = true;
             }
+            float2* bs = lds + (tr / TPJ) * SLOT;
 #pragma unroll
-            for (int i = 0; i < P; i++)
-                lds[slot_of(i) * SLOT + bin_of(i)] = s0 + slot_of(i) <= st_hi ? sv[i] : make_float2(0.f, 0.f);
-            if (tr < JOBS)
-                lds[tr * SLOT + M] = (s0 + tr <= st_hi && M < a.F) ? nyq : make_float2(0.f, 0.f);
+            for (int i = 0; i < P; i++) bs[jr + i * TPJ] = sv[i];
+            if (jr == 0) bs[M] = M < a.F ? nyq : make_float2(0.f, 0.f);
         }
         __syncthreads();
+        // Split twiddles W_N^k for k = jr + r*TPJ: W_N^jr from the table times the constant
+        // W_N^(r*TPJ) = exp(-i pi r / P).
+        constexpr HalfTurnRoots<P> rot = half_turn_roots<P>();
+        const float2 w0 = tw_lookup<N>(twt, jr);
         float2 v[P];
 #pragma unroll
         for (int r = 0; r < P; r++) {
             const int k = jr + r * TPJ;
-            v[r] = inverse_split<N>(buf[k], buf[M - k], k, a.keep_nyquist, twt);
+            const float2 wr = r == 0 ? w0 : cmul(w0, make_float2(rot.re[r], rot.im[r]));
+            v[r] = inverse_split_w(buf[k], buf[M - k], k, a.keep_nyquist, wr);
         }
         pass_sync<WAVE>();                          // staging read before the FFT overwrites it
         fft_first_pass<M, P, N>(v, buf, jr, post, ToLdsFlat{buf});
