@@ -168,13 +168,13 @@ constexpr double cx_sin(double x) {
 }
 constexpr double kPi = 3.14159265358979323846;
 
-// exp(-i pi r / P) for r < P, rounded to float, as compile-time constants.
-template <int P> struct HalfTurnRoots { float re[P], im[P]; };
+// exp(-i pi r / P) for r <= P, rounded to float, as compile-time constants.
+template <int P> struct HalfTurnRoots { float re[P + 1], im[P + 1]; };
 template <int P> constexpr HalfTurnRoots<P> half_turn_roots() {
     HalfTurnRoots<P> t{};
-    for (int r = 0; r < P; r++) {
-        t.re[r] = (float)cx_cos(kPi * r / P);
-        t.im[r] = (float)-cx_sin(kPi * r / P);
+    for (int r = 0; r <= P; r++) {
+        t.re[r] = 2 * r == P ? 0.f : (float)cx_cos(kPi * r / P);     // exact 0 and -1 at pi/2 and pi
+        t.im[r] = r == P ? 0.f : (float)-cx_sin(kPi * r / P);
     }
     return t;
 }

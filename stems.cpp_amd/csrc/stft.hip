@@ -35,6 +35,7 @@ struct stx_fft {
     int device = 0;
     float2* twt = nullptr;   // device: two-level twiddle table for n points (fft_core.hpp)
     float* win = nullptr;    // device [n]: periodic Hann
+    float* win_hs = nullptr; // device [2][n]: the Hann window times 1/2 and times 1/(2 sqrt n) (power-of-two STFT)
     int mixed = 0;           // n = 2^a 3^b 5^c, not a power of two: the mixed-radix kernels
     float2* twn = nullptr;   // mixed: device [n], W_n^m
     float2* twm = nullptr;   // mixed: device [kMixedTwMax], the passes' two-level table (fft_core.hpp)
@@ -62,6 +63,7 @@ struct StftArgs {
     const float* x;          // [C][len]
     float2* spec;            // [C][F][T] or [C][T][F]
     const float* win;        // [N]
+    const float* win_hs;     // [N]: win * scale / 2 (power-of-two kernel: the split's 1/2 and the norm)
     const float2* twt;       // twiddle table for N
     int len;                 // samples per channel
     int len1;                // length of the pre-padded signal (len when there is no pre-pad)
@@ -124,7 +126,7 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void stft_kernel(StftArgs a) {
     const int m0 = a.frame0 + t * a.hop;               // padded index of the first sample
     const int base = m0 - N / 2 - a.pre_left;          // its signal index when nothing reflects
     const bool interior = base >= 0 && base + N <= a.len;
-    const float2* win2 = reinterpret_cast<const float2*>(a.win);
+    const float2* win2 = reinterpret_cast<const float2*>(a.win_hs);   // times scale / 2
 
     // Every load issued before the first wait (an inactive job reads frame 0 of channel 0,
     // always in range; its slot is transformed but never written). `interior` is uniform over
@@ -157,10 +159,11 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void stft_kernel(StftArgs a) {
     __syncthreads();
     fft_rest_passes<M, P, N, P>(buf, j, twt, NoPost{}, ToLds<P>{buf});
 
-    // X[k] = E[k] + W_N^k O[k] for frame g of the block, k <= N/2. Bins k = k0 + i*KS (KS a
-    // multiple of P) are read at idx(k) = idx(k0) + i*(KS + KS/P), their mirrors M - k at
-    // idx(M - k0) - i*(KS + KS/P); k = 0 and k = M pair with element 0 (k & (M - 1)).
-    const float hs = 0.5f * a.scale;
+    // X[k] = E[k] + W_N^k O[k] for frame g of the block, k <= N/2 (the frame was windowed with
+    // win * scale / 2, which folds the split's 1/2 and the norm in). Bins k = k0 + i*KS are read
+    // at idx(k) = idx(k0) + i*(KS + KS/P), their mirrors M - k at idx(M - k0) - i*(KS + KS/P);
+    // k = 0 and k = M pair with element 0 (k & (M - 1)). KS = TPJ in both layouts, so
+    // W_N^k = W_N^k0 * exp(-i pi i / P): one table lookup per thread, then compile-time roots.
     const int f0 = lb * JOBS;
     const int c0 = f0 / a.T, t0 = f0 - c0 * a.T;
     constexpr int MP = M + M / P;
@@ -172,13 +175,16 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void stft_kernel(StftArgs a) {
         const float2 zm = bs[(k & (M - 1)) == 0 ? 0 : inc ? im : C::idx(M - k)];
         const float er = zk.x + zm.x, ei = zk.y - zm.y;       // 2E
         const float orr = zk.y + zm.y, oi = zm.x - zk.x;      // 2O
-        return make_float2((er + w.x * orr - w.y * oi) * hs, (ei + w.x * oi + w.y * orr) * hs);
+        return make_float2(er + w.x * orr - w.y * oi, ei + w.x * oi + w.y * orr);
     };
+    constexpr HalfTurnRoots<P> rot = half_turn_roots<P>();
+    auto rotate = [&](float2 w0, int i) { return i == 0 ? w0 : cmul(w0, make_float2(rot.re[i], rot.im[i])); };
     if (a.layout == STX_SPEC_F_MAJOR) {
         // Element e = k*JOBS + g: with NT a multiple of JOBS every thread keeps one frame
         // g = tid % JOBS and takes bins tid / JOBS + i * NT / JOBS, so that the JOBS lanes of a
         // bin write consecutive frames of its row.
         constexpr int KS = NT / JOBS, KSP = KS + KS / P;
+        static_assert(KS == TPJ, "bin stride");
         const int g = tid % JOBS, k0 = tid / JOBS;
         int tt = t0 + g, cc = c0;
         while (tt >= a.T) { tt -= a.T; cc++; }
@@ -188,12 +194,15 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void stft_kernel(StftArgs a) {
             const unsigned rs = (unsigned)a.T * KS;           // row step of one bin stride
             unsigned off = (unsigned)k0 * a.T;
             int ik = C::idx(k0), im = C::idx(M - k0);
-#pragma unroll 4
-            for (int k = k0; k < a.F; k += KS, off += rs, ik += KSP, im -= KSP)
+            const float2 w0 = tw_lookup<N>(twt, k0);
+#pragma unroll
+            for (int i = 0; i <= P; i++, off += rs, ik += KSP, im -= KSP) {   // k0 + P*KS > M
+                const int k = k0 + i * KS;
                 // A plain store: the rows' short runs from neighbouring workgroups meet in the
                 // XCD's L2 and leave as whole lines (with the non-temporal bit, c1 13.2 -> 18.2 us
                 // and c3 13.2 -> 31.1 us).
-                col[off] = bin(bs, k, ik, im, tw_lookup<N>(twt, k), std::integral_constant<int, KS>{});
+                if (k < a.F) col[off] = bin(bs, k, ik, im, rotate(w0, i), std::integral_constant<int, KS>{});
+            }
         }
     } else {
         // Row of frame g, then each bin's twiddle once for all JOBS frames.
@@ -205,10 +214,15 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void stft_kernel(StftArgs a) {
             while (tt >= a.T) { tt -= a.T; cc++; }
             rows[g] = f0 + g < a.jobs ? a.spec + ((size_t)cc * a.T + tt) * a.F : nullptr;
         }
+        // Bin stride NT = JOBS * TPJ: W_N^(i*NT) = exp(-i pi i JOBS / P).
+        static_assert(P % JOBS == 0, "t-major bin stride");
         int ik = C::idx(tid), im = C::idx(M - tid);
-#pragma unroll 4
-        for (int k = tid; k < a.F; k += NT, ik += KSP, im -= KSP) {
-            const float2 w = tw_lookup<N>(twt, k);
+        const float2 w0 = tw_lookup<N>(twt, tid);
+#pragma unroll
+        for (int i = 0; i <= P / JOBS; i++, ik += KSP, im -= KSP) {   // tid + (P / JOBS) * NT >= M
+            const int k = tid + i * NT;
+            if (k >= a.F) continue;
+            const float2 w = rotate(w0, i * JOBS);
 #pragma unroll
             for (int g = 0; g < JOBS; g++)
                 if (rows[g]) store_stream(rows[g] + k, bin(lds + g * SLOT, k, ik, im, w, std::integral_constant<int, NT>{}));
@@ -1122,15 +1136,22 @@ STX_API stx_status stx_fft_create(int n, stx_fft** out) {
         };
         for (int m = 0; m < L; m++) twt[m] = w_n(m);
         for (int h = 0; h < H; h++) twt[L + h] = w_n((long long)h * L);
-        std::vector<float> win(n);
-        for (int m = 0; m < n; m++) win[m] = (float)(0.5 - 0.5 * std::cos(2.0 * M_PI * m / n));   // hann_periodic (src/stft.h:70-74)
+        std::vector<float> win(n), win_hs(2 * (size_t)n);
+        for (int m = 0; m < n; m++) {
+            const double w = 0.5 - 0.5 * std::cos(2.0 * M_PI * m / n);   // hann_periodic (src/stft.h:70-74)
+            win[m] = (float)w;
+            win_hs[m] = (float)(0.5 * w);                                  // STFT scale 1
+            win_hs[n + m] = (float)(0.5 * w / std::sqrt((double)n));       // STFT scale 1 / sqrt(n)
+        }
         stx_fft* f = new stx_fft;
         f->n = n;
         hipError_t e = hipGetDevice(&f->device);
         if (e == hipSuccess) e = hipMalloc(&f->twt, sizeof(float2) * twt.size());
         if (e == hipSuccess) e = hipMalloc(&f->win, sizeof(float) * n);
+        if (e == hipSuccess) e = hipMalloc(&f->win_hs, sizeof(float) * win_hs.size());
         if (e == hipSuccess) e = hipMemcpy(f->twt, twt.data(), sizeof(float2) * twt.size(), hipMemcpyHostToDevice);
         if (e == hipSuccess) e = hipMemcpy(f->win, win.data(), sizeof(float) * n, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(f->win_hs, win_hs.data(), sizeof(float) * win_hs.size(), hipMemcpyHostToDevice);
         if (e != hipSuccess) {
             stx_fft_destroy(f);
             hip_check(e, "stx_fft_create");
@@ -1186,6 +1207,7 @@ STX_API void stx_fft_destroy(stx_fft* f) {
     if (f->scratch) (void)hipFree(f->scratch);
     if (f->twt) (void)hipFree(f->twt);
     if (f->win) (void)hipFree(f->win);
+    if (f->win_hs) (void)hipFree(f->win_hs);
     if (f->twn) (void)hipFree(f->twn);
     if (f->twm) (void)hipFree(f->twm);
     delete f;
@@ -1287,6 +1309,7 @@ STX_API stx_status stx_torch_stft(const stx_fft* f, const float* x, int channels
         a.jobs = channels * a.T;
         a.layout = layout;
         a.scale = normalized ? (float)(1.0 / std::sqrt((double)n)) : 1.0f;
+        a.win_hs = f->win_hs ? f->win_hs + (normalized ? n : 0) : nullptr;
         check_extent((long long)channels * a.T * a.F, "spectrum");
         check_extent((long long)channels * len + n, "signal");
         if (f->mixed) {
@@ -1354,6 +1377,7 @@ STX_API stx_status stx_htdemucs_spec(const stx_fft* f, const float* x, int chann
         a.jobs = channels * a.T;
         a.layout = layout;
         a.scale = (float)(1.0 / std::sqrt((double)n));
+        a.win_hs = f->win_hs + n;
         check_extent((long long)channels * a.T * a.F, "spectrum");
         check_extent((long long)channels * len1 + n, "signal");
         by_size<StftL>(n, a, as_stream(stream));
