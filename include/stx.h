@@ -464,7 +464,10 @@ STX_API stx_status stx_htdemucs_wave_normalize(const float* x, int64_t n, float*
  * (rounded to float), ref_mean and ref_std = max(std, 1e-8) of mono, out = (x - ref_mean) /
  * ref_std for every channel of mix [C][len]. stats gets {ref_mean, ref_std}. INVALID_ARGUMENT
  * "empty input" when len <= 0, as the reference throws. workspace: norm_workspace_size(len).
- * out may be mix (in place); any other overlap is INVALID_ARGUMENT. */
+ * out may be mix (in place); any other overlap is INVALID_ARGUMENT. With 1 or 2 channels and
+ * out not overlapping mix, a mix whose 8192-sample chunks the device holds at once (1,024
+ * chunks of two channels on MI355X, 3.2 minutes at 44.1 kHz) is normalised by one
+ * grid-synchronised kernel with the same bits as the two kernels that every other call takes. */
 STX_API stx_status stx_htdemucs_mix_normalize(const float* mix, int channels, int64_t len, float* out, double* stats,
                                               void* workspace, size_t workspace_bytes, stx_stream stream);
 

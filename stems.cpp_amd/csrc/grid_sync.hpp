@@ -253,9 +253,9 @@ inline bool grid_sync_enabled(hipStream_t stream) {
     return set >= device_cus();
 }
 
-// Blocks of `kernel` (kGridThreads threads, no dynamic LDS) that the current device holds at
+// Blocks of `kernel` (`threads` threads, no dynamic LDS) that the current device holds at
 // once (occupancy times CUs, cached per kernel and device).
-inline int device_blocks(const void* kernel) {
+inline int device_blocks(const void* kernel, int threads = kGridThreads) {
     struct Entry {
         const void* k;
         int dev, blocks;
@@ -269,7 +269,7 @@ inline int device_blocks(const void* kernel) {
         if (e.k == kernel && e.dev == dev) return e.blocks;
     int cus = 0, per_cu = 0;
     hip_check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
-    hip_check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kGridThreads, 0),
+    hip_check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0),
               "hipOccupancyMaxActiveBlocksPerMultiprocessor");
     cache.push_back({kernel, dev, cus * per_cu});
     return cus * per_cu;
@@ -277,9 +277,9 @@ inline int device_blocks(const void* kernel) {
 
 // device_blocks for the single-pass kernels; 0 when grid_sync_enabled() is false, so that
 // callers take their multi-kernel path.
-inline int resident_blocks(const void* kernel, hipStream_t stream) {
+inline int resident_blocks(const void* kernel, hipStream_t stream, int threads = kGridThreads) {
     if (!grid_sync_enabled(stream)) return 0;
-    return device_blocks(kernel);
+    return device_blocks(kernel, threads);
 }
 
 // Whether [a, a + an) and [b, b + bn) (bytes) overlap.

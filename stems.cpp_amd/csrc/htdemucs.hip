@@ -14,9 +14,12 @@
 // the input fits in the registers of blocks that are all resident at once (one segment's
 // spectrum or waveform) and the output does not overlap the input: each block loads its chunk
 // once, the blocks exchange their partial sums (grid_sync.hpp) and normalise from registers.
-// Otherwise (the whole mix of separate()) two kernels: pass 1 writes one (sum d, sum d^2) pair
-// in double per 8192 floats, and every block of pass 2 adds them in one fixed order into
-// {mean, sd} (the same bits in every block) and normalises its 8192 values. The split's
+// Otherwise two kernels: pass 1 writes one (sum d, sum d^2) pair in double per 8192 floats, and
+// every block of pass 2 adds them in one fixed order into {mean, sd} (the same bits in every
+// block) and normalises its 8192 values. The mono mix of separate() (1 or 2 channels, as many
+// 8192-sample chunks as the device holds at once: 1,024 of two channels on MI355X, 3.2 minutes
+// at 44.1 kHz) has a single-pass kernel of its own that keeps pass 1's chunks, arithmetic and
+// order, so it gives the two kernels' bits. The split's
 // overlap-add is in gather form: each output sample sums, in chunk order and in float like the
 // reference's `out += weight * seg_out`, the <= ceil(seg / stride) chunks covering it, and
 // divides by the summed weights, so it is bit-exact.
@@ -81,6 +84,23 @@ __device__ __forceinline__ double block_sum(double v, double* red) {
     return red[0] + red[1] + red[2] + red[3];    // 256 threads: 4 waves, summed in one order
 }
 
+// This thread's sums of d = v - shift over its values of the pass-1 chunk at lo (value j at
+// lo + threadIdx.x + 256 j), in j order; moments_kernel and mix_fused_kernel share it, so their
+// chunk sums are the same bits.
+__device__ __forceinline__ void moment_add(double d, double& s, double& q) {
+    s += d;
+    q += d * d;
+}
+template <int J>
+__device__ __forceinline__ void chunk_moments(const float (&v)[J], long long lo, long long n, float shift, double& s,
+                                              double& q) {
+    s = 0.0;
+    q = 0.0;
+#pragma unroll
+    for (int j = 0; j < J; j++)
+        if (lo + threadIdx.x + 256LL * j < n) moment_add((double)v[j] - shift, s, q);
+}
+
 // KIND: MOM_FLAT or MOM_MONO; NC: channels of the mono mix (compile time; 0 = run time).
 template <int KIND, int NC>
 __global__ __launch_bounds__(256) void moments_kernel(MomArgs a) {
@@ -98,15 +118,8 @@ __global__ __launch_bounds__(256) void moments_kernel(MomArgs a) {
 #pragma unroll
         for (int j = 0; j < J; j++) v[j] = a.x[idx[j]];
     }
-    double s = 0.0, q = 0.0;
-#pragma unroll
-    for (int j = 0; j < kMomChunk / 256; j++) {
-        if (lo + threadIdx.x + 256LL * j < a.n) {
-            const double d = (double)v[j] - shift;
-            s += d;
-            q += d * d;
-        }
-    }
+    double s, q;
+    chunk_moments(v, lo, a.n, shift, s, q);
     s = block_sum(s, red);
     q = block_sum(q, red);
     if (threadIdx.x == 0) {
@@ -328,6 +341,132 @@ __global__ __launch_bounds__(kGridThreads) void norm_fused_kernel(const float* x
         norm_fused_body<KIND, VEC, true>(x, y, n, ft, cdiv, vec, stats, f, red, tot);
     else
         norm_fused_body<KIND, VEC, false>(x, y, n, ft, cdiv, vec, stats, f, red, tot);
+}
+
+// One launch of the mix's moments + normalise (NORM_MIX over the mono mix of NC = 1 or 2
+// channels of n samples), bit-identical to moments_kernel<MOM_MONO, NC> + normalize_kernel<NORM_MIX>:
+// block b holds pass 1's chunk b (kMomChunk samples, 256 threads, every channel's values in
+// registers), forms the same mono values and chunk sums (chunk_moments, block_sum), and the
+// blocks' totals are folded in fold_stats' order (thread t adds chunks t, t + 256, ..., then the
+// block sum) by the grid barrier; then every block normalises its values of every channel with
+// the same quotient. Block 0 writes {mean, sd} to stats.
+// Values j < MixKeep<NC>::regs of each channel stay in registers across the barrier, the rest in
+// the block's LDS (one slot per thread and value): the 32 or 64 values per thread, with what
+// the barrier needs, would not fit in the 128 registers that four blocks per CU allow, and the
+// LDS kept stays within a quarter of the CU's 160 KB.
+template <int NC> struct MixKeep {
+    static constexpr int regs = NC == 1 ? 16 : 13;
+    static constexpr int lds = kMomChunk / 256 - regs;
+};
+
+template <int NC, bool FULL>
+__device__ __forceinline__ void mix_fused_body(const float* x, float* y, long long n, double* stats, const GridSync& f,
+                                               double* red, double* tot, float* keep) {
+    constexpr int NT = 256;
+    constexpr int J = kMomChunk / NT;
+    constexpr int JR = MixKeep<NC>::regs;
+    const int nblk = (int)gridDim.x;
+    const long long lo = (long long)blockIdx.x * kMomChunk;
+    const float shift = mono_at(x, n, NC, 0);
+    // Loads and stores at a uniform base (this chunk of channel c) plus a 32-bit byte offset,
+    // which the compiler issues as base-register + offset-register forms instead of one 64-bit
+    // address per value.
+    auto at = [](auto* base, unsigned bytes) {
+        using T = std::remove_pointer_t<decltype(base)>;
+        return reinterpret_cast<T*>(reinterpret_cast<std::conditional_t<std::is_const_v<T>, const char*, char*>>(base) + bytes);
+    };
+    const unsigned tb = 4u * threadIdx.x, lastb = 4u * (unsigned)(n - 1 - lo);   // lastb: tail chunk only
+    float raw[J][NC];
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        const float* xc = x + c * n + lo;
+#pragma unroll
+        for (int j = 0; j < J; j++) raw[j][c] = *at(xc, FULL ? tb + 1024u * j : min(tb + 1024u * j, lastb));
+    }
+    __builtin_amdgcn_sched_barrier(0);          // every load issued before the sums start
+    // mono_batch's value and chunk_moments' sums, one value at a time (the same operations in
+    // the same order, so the same bits as pass 1, without a second array of J values).
+    double s = 0.0, q = 0.0;
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        double m = 0.0;
+#pragma unroll
+        for (int c = 0; c < NC; c++) m += raw[j][c];
+        const float v = (float)(m / NC);
+        if (FULL || lo + threadIdx.x + 256LL * j < n) moment_add((double)v - shift, s, q);
+    }
+#pragma unroll
+    for (int j = JR; j < J; j++)
+#pragma unroll
+        for (int c = 0; c < NC; c++) keep[((j - JR) * NC + c) * NT + threadIdx.x] = raw[j][c];
+    // Opaque from here: the compiler would otherwise keep the sums' double conversions of the
+    // values alive across the barrier for the quotients below (twice the registers).
+#pragma unroll
+    for (int j = 0; j < JR; j++)
+#pragma unroll
+        for (int c = 0; c < NC; c++) asm volatile("" : "+v"(raw[j][c]));
+    s = block_sum(s, red);
+    q = block_sum(q, red);
+    // A block whose wait gave up forms every chunk's sums itself, in the same order (one value
+    // at a time: its registers hold this block's values meanwhile).
+    grid_totals<NT>(f, 0, nblk, s, q, red, tot, [&](double* t) {
+        double p1 = 0.0, p2 = 0.0;
+        for (int b = 0; b < nblk; b++) {
+            const long long l = (long long)b * kMomChunk;
+            double q1 = 0.0, q2 = 0.0;
+#pragma unroll 1
+            for (int jj = 0; jj < J; jj++) {
+                const long long i = min(l + threadIdx.x + 256LL * jj, n - 1);
+                double m = 0.0;
+#pragma unroll
+                for (int c = 0; c < NC; c++) m += x[c * n + i];
+                if (l + threadIdx.x + 256LL * jj < n) moment_add((double)(float)(m / NC) - shift, q1, q2);
+            }
+            q1 = block_sum(q1, red);
+            q2 = block_sum(q2, red);
+            if ((int)threadIdx.x == b % NT) {
+                p1 += q1;
+                p2 += q2;
+            }
+        }
+        block_sum2_n<NT>(p1, p2, red);
+        if (threadIdx.x == 0) {
+            t[0] = p1;
+            t[1] = p2;
+        }
+        __syncthreads();
+    });
+    // fold_stats<NORM_MIX> from the totals.
+    const double nn = (double)n, ts = tot[0], tq = tot[1];
+    double sd = sqrt(fmax(tq - ts * (ts / nn), 0.0) / (nn - 1.0));
+    sd = sd < 1e-8 ? 1e-8 : sd;
+    const double mean = (double)shift + ts / nn, den = sd, rden = 1.0 / den;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        stats[0] = mean;
+        stats[1] = sd;
+    }
+#pragma unroll
+    for (int j = JR; j < J; j++)
+#pragma unroll
+        for (int c = 0; c < NC; c++) raw[j][c] = keep[((j - JR) * NC + c) * NT + threadIdx.x];
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        float* yc = y + c * n + lo;
+#pragma unroll
+        for (int j = 0; j < J; j++)
+            if (FULL || tb + 1024u * j <= lastb)
+                store_stream(at(yc, tb + 1024u * j), (float)div_rn((double)raw[j][c] - mean, den, rden));
+    }
+}
+
+template <int NC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void mix_fused_kernel(
+    const float* x, float* y, long long n, double* stats, GridSync f) {
+    __shared__ double red[2 * 256 / 64];
+    __shared__ double tot[2];
+    __shared__ float keep[MixKeep<NC>::lds > 0 ? MixKeep<NC>::lds * NC * 256 : 1];
+    if ((long long)(blockIdx.x + 1) * kMomChunk <= n) mix_fused_body<NC, true>(x, y, n, stats, f, red, tot, keep);
+    else mix_fused_body<NC, false>(x, y, n, stats, f, red, tot, keep);
 }
 
 // Spectral branch denormalise: ox [S][2C][FT] -> complex64 spec [S][C][FT]; blockIdx.y = s * C + c.
@@ -600,6 +739,19 @@ bool try_norm_fused(const float* x, float* y, long long n, long long ft, double*
     return true;
 }
 
+// mix_fused_kernel when y does not overlap x, C is 1 or 2 and all its blocks are resident at
+// once (at most kGridMaxGroups * kGridMaxBlocks: the sync area's records); false otherwise.
+template <int NC>
+bool try_mix_fused(const float* x, float* y, long long n, double* stats, void* ws, hipStream_t s) {
+    const long long nb = mom_blocks(n);
+    if (nb > (long long)kGridMaxGroups * kGridMaxBlocks) return false;
+    if (overlaps(x, sizeof(float) * (size_t)(NC * n), y, sizeof(float) * (size_t)(NC * n))) return false;
+    if (nb > resident_blocks(reinterpret_cast<const void*>(&mix_fused_kernel<NC>), s, 256)) return false;
+    hipLaunchKernelGGL((mix_fused_kernel<NC>), dim3((unsigned)nb), dim3(256), 0, s, x, y, n, stats, grid_sync_at(ws));
+    launch_check("mix_fused_kernel");
+    return true;
+}
+
 template <int MK, int NK>
 void normalize(const float* x, long long n_mom, long long count, int C, float* y, double* stats, void* ws,
                hipStream_t s) {
@@ -612,6 +764,9 @@ void normalize(const float* x, long long n_mom, long long count, int C, float* y
     if constexpr (NK != NORM_MIX) {
         if (try_norm_fused<NK, 1>(x, y, n_mom, count, stats, ws, s) || try_norm_fused<NK, 2>(x, y, n_mom, count, stats, ws, s) ||
             try_norm_fused<NK, 4>(x, y, n_mom, count, stats, ws, s))
+            return;
+    } else {
+        if ((C == 1 && try_mix_fused<1>(x, y, n_mom, stats, ws, s)) || (C == 2 && try_mix_fused<2>(x, y, n_mom, stats, ws, s)))
             return;
     }
     double* partial = reinterpret_cast<double*>(static_cast<char*>(ws) + kGridSyncBytes);

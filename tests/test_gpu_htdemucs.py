@@ -180,6 +180,31 @@ def test_mix_normalize_song(device, htd):
     assert rel_err(host(out), want) <= 1e-6
 
 
+@pytest.mark.parametrize("C", [1, 2])
+def test_mix_normalize_single_pass_same_bits(device, htd, C, monkeypatch):
+    """The single-pass mix normalise (one and two channels, a tail chunk of 1,000,003 % 8,192
+    samples) gives the two-kernel path's bits, and so does its fallback when every wait gives
+    up at the first look (STX_GRID_SYNC_SPIN_LIMIT=0: each block then forms all chunk sums
+    itself, in the same order); the workspace counts the fallbacks."""
+    n = 1_000_003
+    mix = synth.sines_plus_pink(20 + C, C, n)
+    m = dev(mix, device)
+    o1, s1 = stx.htdemucs_mix_normalize(m)
+    monkeypatch.setenv("STX_NO_GRID_SYNC", "1")
+    o2, s2 = stx.htdemucs_mix_normalize(m)
+    monkeypatch.delenv("STX_NO_GRID_SYNC")
+    ws = stx.workspace(stx.lib().stx_htdemucs_norm_workspace_size(n), device)
+    monkeypatch.setenv("STX_GRID_SYNC_SPIN_LIMIT", "0")
+    o3, s3 = stx.htdemucs_mix_normalize(m, workspace=ws)
+    monkeypatch.delenv("STX_GRID_SYNC_SPIN_LIMIT")
+    assert stx.grid_sync_fallbacks(ws) > 0
+    for o, s in ((o2, s2), (o3, s3)):
+        assert np.array_equal(host(o), host(o1)) and np.array_equal(host(s), host(s1))
+    want, wstats = htd.mix_normalize(mix)
+    assert close_stats(host(s1), wstats)
+    assert rel_err(host(o1), want) <= 1e-6
+
+
 def test_mix_normalize_silence_and_errors(device):
     import torch
     out, stats = stx.htdemucs_mix_normalize(torch.zeros((2, 1000), device=device))
