@@ -349,7 +349,12 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
     using C = FftCfg<M, P, N>;
     constexpr int TPJ = C::TPJ;
     constexpr int NT = JOBS * TPJ;
-    constexpr int SLOT = C::PADN;                      // (a slot one float2 longer measured no faster)
+    // Slots KPW float2 apart modulo 32 (256 bytes of banks): the f-major staging's lanes write
+    // bin tr / JOBS of slot tr % JOBS, KPW = ceil(64 / JOBS) bins per wave, so the JOBS slots'
+    // runs fall on different banks (with slots a multiple of 32 float2 apart they shared them:
+    // 5x the LDS bank-conflict cycles of the t-major staging at c1).
+    constexpr int KPW = (64 + JOBS - 1) / JOBS;                  // a wave is 64 lanes
+    constexpr int SLOT = C::PADN < 512 ? C::PADN : C::PADN + ((KPW - C::PADN % 32) % 32 + 32) % 32;  // short slots: as is
     // One wave per transform: between the split and the last pass every lane touches only its
     // own wave's slot, so those passes need no workgroup barrier.
     constexpr bool WAVE = TPJ == 64;
