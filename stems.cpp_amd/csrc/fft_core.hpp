@@ -146,6 +146,28 @@ template <> struct Dft<5> {
     }
 };
 
+// Dft<15>: the prime-factor algorithm (3 and 5 coprime, so no twiddles between them): input
+// x[(5 n1 + 3 n2) mod 15] at a[n1][n2], 5-point DFTs along n2, 3-point DFTs along n1, output
+// X[(10 k1 + 6 k2) mod 15] from b[k1][k2] (W15^(nk) = W3^(n1 k1) W5^(n2 k2) for these maps).
+template <> struct Dft<15> {
+    static STX_HD void run(float2* v) {
+        float2 a[3][5];
+#pragma unroll
+        for (int n1 = 0; n1 < 3; n1++)
+#pragma unroll
+            for (int n2 = 0; n2 < 5; n2++) a[n1][n2] = v[(5 * n1 + 3 * n2) % 15];
+#pragma unroll
+        for (int n1 = 0; n1 < 3; n1++) Dft<5>::run(a[n1]);
+#pragma unroll
+        for (int k2 = 0; k2 < 5; k2++) {
+            float2 t[3] = {a[0][k2], a[1][k2], a[2][k2]};
+            Dft<3>::run(t);
+#pragma unroll
+            for (int k1 = 0; k1 < 3; k1++) v[(10 * k1 + 6 * k2) % 15] = t[k1];
+        }
+    }
+};
+
 constexpr int ilog2(int n) { return n <= 1 ? 0 : 1 + ilog2(n / 2); }
 
 // cos and sin of x (|x| <= pi) by their Taylor series in double, for twiddle constants computed
@@ -381,7 +403,8 @@ __device__ __forceinline__ void fft_rest_passes(float2* buf, int j, const float2
 namespace stx {
 
 // Mixed-radix plan of an M-point complex transform, M = 2^a 3^b 5^c: radix 16 passes while 16
-// divides what is left, then one of 8, 4 or 2, then 3s and 5s.
+// divides what is left, then one of 8, 4 or 2, then 15s (a 3 and a 5 in one pass), then the
+// remaining 3s and 5s.
 struct MixedRadix {
     int count = 0;
     int r[24] = {};
@@ -394,6 +417,7 @@ inline bool mixed_plan(int m, MixedRadix& p) {
     while (left % 16 == 0) { p.r[p.count++] = 16; left /= 16; }
     for (int q : {8, 4, 2})
         if (left % q == 0) { p.r[p.count++] = q; left /= q; }
+    while (left % 15 == 0) { p.r[p.count++] = 15; left /= 15; }
     while (left % 3 == 0) { p.r[p.count++] = 3; left /= 3; }
     while (left % 5 == 0) { p.r[p.count++] = 5; left /= 5; }
     return left == 1 && p.count <= 24;
@@ -482,6 +506,7 @@ __device__ __forceinline__ float2* mixed_fft(float2* buf0, float2* buf1, int M, 
             case 8: mixed_pass<8, mixed_batch<8, MAXM, NT>(), NT>(src, dst, M, Ns, scale, twl, tid); break;
             case 4: mixed_pass<4, mixed_batch<4, MAXM, NT>(), NT>(src, dst, M, Ns, scale, twl, tid); break;
             case 2: mixed_pass<2, mixed_batch<2, MAXM, NT>(), NT>(src, dst, M, Ns, scale, twl, tid); break;
+            case 15: mixed_pass<15, mixed_batch<15, MAXM, NT>(), NT>(src, dst, M, Ns, scale, twl, tid); break;
             case 3: mixed_pass<3, mixed_batch<3, MAXM, NT>(), NT>(src, dst, M, Ns, scale, twl, tid); break;
             default: mixed_pass<5, mixed_batch<5, MAXM, NT>(), NT>(src, dst, M, Ns, scale, twl, tid); break;
         }
@@ -566,7 +591,7 @@ struct MixedCt {
     }
 };
 // Kim_Vocal_2's n_fft 7680: the real transform's 3840-point half.
-using MixedCt3840 = MixedCt<3840, 16, 16, 3, 5>;
+using MixedCt3840 = MixedCt<3840, 16, 16, 15>;
 
 inline bool mixed_plan_is(const MixedRadix& p, const int* radix, int count) {
     if (p.count != count) return false;
