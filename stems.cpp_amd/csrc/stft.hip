@@ -547,7 +547,7 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
 // n = 2^a 3^b 5^c that is not a power of two (VRFFT's sizes: Kim_Vocal_2's 7680, VR's 320, 640,
 // 960; src/vr_dsp.h:11-37, src/tfc_tdf.cpp:85-86,551-552). The reference reaches these sizes with
 // Bluestein (three power-of-two transforms of at least 2n - 1 points); here one workgroup runs
-// the n/2-point transform of a real frame directly, radix 16 / 8 / 4 / 2 / 3 / 5 Stockham passes
+// the n/2-point transform of a real frame directly, radix 16 / 8 / 4 / 2 / 15 / 3 / 5 Stockham passes
 // ping-ponging between two LDS buffers with twiddles W_n^m from a table computed in double.
 // Frames are packed and split as in the power-of-two kernels; the iSTFT always takes the
 // two-kernel path (frames to the workspace, then istft_ola_kernel). One frame per workgroup,
