@@ -4,7 +4,8 @@ and q0 itself when q0 is not finite. Restated here with exact fused multiply-add
 arithmetic, one rounding to double) and checked against IEEE division (Python's float /) on
 random doubles over many binades and on the denominators the kernels divide by: band counts
 per bin (1, 2), UVR window sums (sums of np.hanning values), HTDemucs 1e-5 + sd, and the
-resampler's half-widths; plus infinite and NaN numerators (ADVICE: fma(-inf, h, inf) is NaN).
+resampler's half-widths; plus infinite and NaN numerators (fma(-inf, h, inf) is NaN, so a
+non-finite q0 must be returned as it is).
 This pins Markstein's argument; the GPU parity tests pin the kernels themselves."""
 import math
 import random
