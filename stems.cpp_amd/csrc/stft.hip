@@ -1382,7 +1382,7 @@ STX_API stx_status stx_htdemucs_spec(const stx_fft* f, const float* x, int chann
         a.jobs = channels * a.T;
         a.layout = layout;
         a.scale = (float)(1.0 / std::sqrt((double)n));
-        a.win_hs = f->win_hs + n;
+        a.win_hs = f->win_hs ? f->win_hs + n : nullptr;   // power-of-two plans only
         check_extent((long long)channels * a.T * a.F, "spectrum");
         check_extent((long long)channels * len1 + n, "signal");
         by_size<StftL>(n, a, as_stream(stream));
