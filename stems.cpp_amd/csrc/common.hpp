@@ -8,9 +8,11 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 #include "stx.h"
 
@@ -239,6 +241,28 @@ inline int device_cus() {
         cache[dev].store(n, std::memory_order_relaxed);
     }
     return n;
+}
+
+// Blocks of `kernel` (`threads` threads, no dynamic LDS) that the current device holds at
+// once (occupancy times CUs, cached per kernel and device).
+inline int device_blocks(const void* kernel, int threads) {
+    struct Entry {
+        const void* k;
+        int dev, blocks;
+    };
+    static std::mutex mu;
+    static std::vector<Entry> cache;
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    std::lock_guard<std::mutex> lock(mu);
+    for (const Entry& e : cache)
+        if (e.k == kernel && e.dev == dev) return e.blocks;
+    int cus = 0, per_cu = 0;
+    hip_check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
+    hip_check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0),
+              "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+    cache.push_back({kernel, dev, cus * per_cu});
+    return cus * per_cu;
 }
 
 }  // namespace stx

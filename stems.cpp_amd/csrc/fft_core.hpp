@@ -303,12 +303,22 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_wave_barrier();
     asm volatile("" ::: "memory");
 }
-// Between two passes: the workgroup's barrier, or the wave's ordering when every transform
+// The workgroup's barrier for data exchanged through LDS only: waits for this wave's LDS
+// accesses (lgkmcnt 0; vmcnt and expcnt left at their maxima) and meets the other waves, but
+// does not wait for global loads in flight, as __syncthreads' workgroup fence does. Global
+// memory written before it is not made visible to the other waves.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+// Between two passes: the workgroup's LDS barrier, or the wave's ordering when every transform
 // belongs to one wave (WAVE: TPJ == 64, so no lane reads another wave's data).
 template <bool WAVE>
 __device__ __forceinline__ void pass_sync() {
     if constexpr (WAVE) wave_lds_sync();
-    else __syncthreads();
+    else lds_barrier();
 }
 
 struct NoPost {

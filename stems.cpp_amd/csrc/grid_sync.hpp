@@ -253,28 +253,6 @@ inline bool grid_sync_enabled(hipStream_t stream) {
     return set >= device_cus();
 }
 
-// Blocks of `kernel` (`threads` threads, no dynamic LDS) that the current device holds at
-// once (occupancy times CUs, cached per kernel and device).
-inline int device_blocks(const void* kernel, int threads = kGridThreads) {
-    struct Entry {
-        const void* k;
-        int dev, blocks;
-    };
-    static std::mutex mu;
-    static std::vector<Entry> cache;
-    int dev = 0;
-    hip_check(hipGetDevice(&dev), "hipGetDevice");
-    std::lock_guard<std::mutex> lock(mu);
-    for (const Entry& e : cache)
-        if (e.k == kernel && e.dev == dev) return e.blocks;
-    int cus = 0, per_cu = 0;
-    hip_check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
-    hip_check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0),
-              "hipOccupancyMaxActiveBlocksPerMultiprocessor");
-    cache.push_back({kernel, dev, cus * per_cu});
-    return cus * per_cu;
-}
-
 // device_blocks for the single-pass kernels; 0 when grid_sync_enabled() is false, so that
 // callers take their multi-kernel path.
 inline int resident_blocks(const void* kernel, hipStream_t stream, int threads = kGridThreads) {

@@ -251,7 +251,8 @@ struct IstftArgs {
     int tile_len;            // fused: full-signal samples per tile
     int tiles;               // fused: tiles per channel
     int jobs;                // two-kernel: channels * T
-    int nblocks;
+    int nblocks;             // fused: tiles over all channels
+    int grid;                // fused: workgroups launched (a multiple of the XCD count)
     float norm;
 };
 
@@ -342,8 +343,9 @@ __global__ __launch_bounds__(256) void istft_ola_kernel(IstftArgs a, int N) {
 // Fused path: one workgroup owns a tile of output samples and inverse-transforms, JOBS frames
 // at a time (normally all at once), every frame that overlaps it; the last FFT pass applies
 // window * norm; each thread sums its samples over the overlapping frames in frame order and
-// divides by the window-squared envelope.
-template <int N, int P, int JOBS, int PER>
+// divides by the window-squared envelope. PERSIST: fewer workgroups than tiles, each taking
+// several (launches whose tiles outnumber the workgroups the device holds at once).
+template <int N, int P, int JOBS, int PER, bool PERSIST>
 __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) {
     constexpr int M = N / 2;
     using C = FftCfg<M, P, N>;
@@ -367,10 +369,11 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
     __shared__ float wl[WIN_LDS ? N : 2];
     __shared__ float inv_env[ENV_LDS ? N : 2];
 
+    // Workgroup lb takes tile lb of the a.nblocks tiles over all channels, and with PERSIST also
+    // tiles lb + G, lb + 2G, ... (G = a.grid, the workgroups launched); at every step each XCD
+    // holds a contiguous run of tiles.
     const int lb = xcd_block();
     if (lb >= a.nblocks) return;
-    const int c = lb / a.tiles;
-    const int tile = lb % a.tiles;
     const int tid = (int)threadIdx.x;
     const int slot = tid / TPJ;
     const int j = tid % TPJ;
@@ -378,21 +381,76 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
     const int hop = a.hop;
 
     // The twiddle and window tables are loaded into registers here and written to LDS after the
-    // first round's spectrum loads are issued, so that their round trips overlap.
+    // first tile's spectrum loads are issued, so that their round trips overlap.
     StagedTwiddles<N, NT> tws;
     Staged<WIN_LDS ? N : 1, NT, float> wins;
     tws.load(a.twt, tid);
     if constexpr (WIN_LDS) wins.load(a.win, tid);
-    bool staged = false;
     const float* win = WIN_LDS ? wl : a.win;
-
-    const int J0 = max(a.out_off, a.tile_origin + tile * a.tile_len);
-    const int J1 = min(a.out_off + a.out_len, a.tile_origin + (tile + 1) * a.tile_len);
-    // Spectrum frames overlapping [J0, J1): envelope frame tf covers [tf*hop, tf*hop + N).
-    const int st_lo = max(0, max(0, ceildiv(J0 - N + 1, hop)) - a.frame_off);
-    const int st_hi = min(a.T - 1, floordiv(J1 - 1, hop) - a.frame_off);
-    const float2* sc = a.spec + (size_t)c * a.T * a.F;
     const WindowMul post{reinterpret_cast<const float2*>(win)};
+
+    struct Tile {
+        int c, J0, J1, st_lo, st_hi;
+        const float2* sc;
+    };
+    auto tile_at = [&](int ti) {
+        Tile t;
+        t.c = ti / a.tiles;
+        const int tile = ti - t.c * a.tiles;
+        t.J0 = max(a.out_off, a.tile_origin + tile * a.tile_len);
+        t.J1 = min(a.out_off + a.out_len, a.tile_origin + (tile + 1) * a.tile_len);
+        // Spectrum frames overlapping [J0, J1): envelope frame tf covers [tf*hop, tf*hop + N).
+        t.st_lo = max(0, max(0, ceildiv(t.J0 - N + 1, hop)) - a.frame_off);
+        t.st_hi = min(a.T - 1, floordiv(t.J1 - 1, hop) - a.frame_off);
+        t.sc = a.spec + (size_t)t.c * a.T * a.F;
+        return t;
+    };
+    // X[0..M] of frames s0 .. s0 + JOBS - 1 into registers, neighbouring lanes on neighbouring
+    // addresses in either layout: bins k < M are P per thread (M * JOBS = P * NT), the Nyquist
+    // bins one per slot; frames past st_hi read frame st_hi again (finite values, transformed
+    // but never summed: the walk stops at st_hi). F-major: element e = tr + i*NT is slot
+    // e % JOBS = tr % JOBS, bin tr / JOBS + i*TPJ. T-major: thread jr of a slot takes bins
+    // jr + i*TPJ of the slot's frame, the FFT's own element order (one row address, then
+    // constant offsets), and the Nyquist bin.
+    auto load_frames = [&](const Tile& t, int s0, int tr, int jr, float2 (&sv)[P], float2& nyq) {
+        if (a.layout == STX_SPEC_F_MAJOR) {
+            const float2* col = t.sc + min(s0 + tr % JOBS, t.st_hi);
+#pragma unroll
+            for (int i = 0; i < P; i++) sv[i] = col[(size_t)(tr / JOBS + i * TPJ) * a.T];
+            nyq = t.sc[(size_t)min(M, a.F - 1) * a.T + min(s0 + min(tr, JOBS - 1), t.st_hi)];
+        } else {
+            const float2* row = t.sc + (size_t)min(s0 + tr / TPJ, t.st_hi) * a.F;
+#pragma unroll
+            for (int i = 0; i < P; i++) sv[i] = row[jr + i * TPJ];
+            nyq = row[min(M, a.F - 1)];
+        }
+    };
+    auto stage_frames = [&](int tr, int jr, const float2 (&sv)[P], float2 nyq) {
+        if (a.layout == STX_SPEC_F_MAJOR) {
+            const int g = tr % JOBS, k0 = tr / JOBS;
+#pragma unroll
+            for (int i = 0; i < P; i++) lds[g * SLOT + k0 + i * TPJ] = sv[i];
+            if (tr < JOBS) lds[tr * SLOT + M] = M < a.F ? nyq : make_float2(0.f, 0.f);
+        } else {
+            float2* bs = lds + (tr / TPJ) * SLOT;
+#pragma unroll
+            for (int i = 0; i < P; i++) bs[jr + i * TPJ] = sv[i];
+            if (jr == 0) bs[M] = M < a.F ? nyq : make_float2(0.f, 0.f);
+        }
+    };
+
+    bool staged = false;
+    auto stage_tables = [&]() {
+        tws.store(twt, tid);
+        if constexpr (WIN_LDS) wins.store(wl, tid);
+        staged = true;
+    };
+    Tile t = tile_at(lb);
+    float2 sv[P], nyq = make_float2(0.f, 0.f);
+    if constexpr (PERSIST) {
+        if (t.st_lo <= t.st_hi) load_frames(t, t.st_lo, tid, j, sv, nyq);
+        stage_tables();
+    }
 
     // Samples J = J0 + q*NT + tid (q < PER). With J = A*hop + R (0 <= R < hop), the frames
     // covering J are tf = A - K .. A at positions s = R + K*hop .. R, where K = K0 when
@@ -401,7 +459,7 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
     // round's transform rather than held in registers across it.
     const int K0 = (N - 1) / hop, rK = N - 1 - K0 * hop;
     const int dA = NT / hop, dR = NT - dA * hop;
-    auto walk = [&](int lane, auto&& body) {
+    auto walk = [&](int J0, int lane, auto&& body) {
         int A = (J0 + lane) / hop, R = J0 + lane - A * hop;
 #pragma unroll
         for (int q = 0; q < PER; q++) {
@@ -412,94 +470,6 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
             if (R >= hop) { R -= hop; A++; }
         }
     };
-    float acc[PER];
-#pragma unroll
-    for (int q = 0; q < PER; q++) acc[q] = 0.f;
-    const float* ldsf = reinterpret_cast<const float*>(lds);
-
-    for (int s0 = st_lo; s0 <= st_hi; s0 += JOBS) {
-        // An opaque copy of the lane index: keeps the compiler from hoisting the (round
-        // invariant) twiddle reads, staging addresses and sample walk out of this loop, which
-        // would hold them in registers across the transform.
-        int jr = j, tr = tid;
-        asm volatile("" : "+v"(jr), "+v"(tr));
-        __builtin_assume(jr >= 0 && jr < TPJ && tr >= 0 && tr < NT);
-        // Stage X[0..M] of frames s0 .. s0 + JOBS - 1 into the slots, neighbouring lanes on
-        // neighbouring addresses in either layout: bins k < M are P per thread
-        // (M * JOBS = P * NT), the Nyquist bins one per slot. Every load of the round is issued
-        // before the first LDS write; slots past st_hi stage frame st_hi again (finite values,
-        // transformed but never summed: the walk stops at st_hi).
-        float2 sv[P];
-        if (a.layout == STX_SPEC_F_MAJOR) {
-            // Element e = tr + i*NT: slot e % JOBS = tr % JOBS, bin e / JOBS = tr / JOBS + i*TPJ.
-            const int g = tr % JOBS, k0 = tr / JOBS;
-            const float2* col = sc + min(s0 + g, st_hi);
-#pragma unroll
-            for (int i = 0; i < P; i++) sv[i] = col[(size_t)(k0 + i * TPJ) * a.T];
-            const float2 nyq = sc[(size_t)min(M, a.F - 1) * a.T + min(s0 + min(tr, JOBS - 1), st_hi)];
-            if (!staged) {
-                tws.store(twt, tid);
-                if constexpr (WIN_LDS) wins.store(wl, tid);
-                staged = true;
-            }
-#pragma unroll
-            for (int i = 0; i < P; i++) lds[g * SLOT + k0 + i * TPJ] = sv[i];
-            if (tr < JOBS) lds[tr * SLOT + M] = M < a.F ? nyq : make_float2(0.f, 0.f);
-        } else {
-            // Thread jr of a slot: bins jr + i*TPJ of the slot's frame, the FFT's own element
-            // order (one row address, then constant offsets), and the Nyquist bin for jr == 0.
-            const float2* row = sc + (size_t)min(s0 + tr / TPJ, st_hi) * a.F;
-#pragma unroll
-            for (int i = 0; i < P; i++) sv[i] = row[jr + i * TPJ];
-            const float2 nyq = row[min(M, a.F - 1)];
-            if (!staged) {
-                tws.store(twt, tid);
-                if constexpr (WIN_LDS) wins.store(wl, tid);
-                staged = true;
-            }
-            float2* bs = lds + (tr / TPJ) * SLOT;
-#pragma unroll
-            for (int i = 0; i < P; i++) bs[jr + i * TPJ] = sv[i];
-            if (jr == 0) bs[M] = M < a.F ? nyq : make_float2(0.f, 0.f);
-        }
-        __syncthreads();
-        // Split twiddles W_N^k for k = jr + r*TPJ: W_N^jr from the table times the constant
-        // W_N^(r*TPJ) = exp(-i pi r / P).
-        constexpr HalfTurnRoots<P> rot = half_turn_roots<P>();
-        const float2 w0 = tw_lookup<N>(twt, jr);
-        float2 v[P];
-#pragma unroll
-        for (int r = 0; r < P; r++) {
-            const int k = jr + r * TPJ;
-            const float2 wr = r == 0 ? w0 : cmul(w0, make_float2(rot.re[r], rot.im[r]));
-            v[r] = inverse_split_w(buf[k], buf[M - k], k, a.keep_nyquist, wr);
-        }
-        pass_sync<WAVE>();                          // staging read before the FFT overwrites it
-        fft_first_pass<M, P, N>(v, buf, jr, post, ToLdsFlat{buf});
-        pass_sync<WAVE>();
-        fft_rest_passes<M, P, N, P, WAVE>(buf, jr, twt, post, ToLdsFlat{buf});
-        if constexpr (WAVE) __syncthreads();        // every slot written before the sums read them
-        // Slot g now holds samples (2n, 2n + 1) of frame s0 + g at LDS index n (unpadded: the
-        // last pass's lanes write consecutive n), windowed: add the frames of this round that
-        // cover each sample, in frame order.
-        const int s_end = min(st_hi, s0 + JOBS - 1);
-        walk(tr, [&](int q, int tf0, int s_first, int K) {
-            if (q * NT + tr >= J1 - J0) return;
-            const int first = tf0 - a.frame_off;              // spectrum frame of tf0
-            const int i0 = max(0, s0 - first), i1 = min(K, s_end - first);
-            // Sample pos (0 <= pos < N) of slot g is float pos of the slot.
-            const float* sl = ldsf + 2 * SLOT * (first + i0 - s0) + (s_first - i0 * hop);
-            float sum = acc[q];
-            for (int i = i0; i <= i1; i++, sl += 2 * SLOT - hop) sum += *sl;
-            acc[q] = sum;
-        });
-        __syncthreads();
-    }
-    if (!staged) {                                  // no frame overlaps the tile (uniform)
-        tws.store(twt, tid);
-        if constexpr (WIN_LDS) wins.store(wl, tid);
-        __syncthreads();
-    }
 
     // Envelope: win^2 summed over the envelope frames 0 <= tf < env_frames covering J, in frame
     // order (src/stft.h:130,187); out = acc * (norm / env) where env > 1e-11, else 0 (the sums
@@ -507,8 +477,9 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
     // sample). Where all K + 1 frames of J exist, env depends on R = J mod hop only: norm / env
     // (0 for env <= 1e-11) comes from a table built once per workgroup when the LDS has room;
     // elsewhere (and at the signal's ends) the same sum and quotient run here, so the table
-    // changes no bit.
-    if constexpr (ENV_LDS) {
+    // changes no bit. Barriers here and below wait for LDS traffic only (lds_barrier), so the
+    // spectrum loads issued before them stay in flight.
+    auto build_env = [&]() {
         const int nr = min(hop, N);
         for (int R = tid; R < nr; R += NT) {
             const int K = R <= rK ? K0 : K0 - 1;
@@ -519,28 +490,110 @@ __global__ __launch_bounds__(JOBS * (N / 2 / P)) void istft_kernel(IstftArgs a) 
             }
             inv_env[R] = env > 1e-11f ? a.norm / env : 0.f;
         }
-        __syncthreads();
+    };
+    if constexpr (ENV_LDS && PERSIST) {
+        lds_barrier();                                // the window table written
+        build_env();                                  // read after the first tile's rounds
     }
-    float* oc = a.out + (size_t)c * a.out_len;
-    walk(tid, [&](int q, int tf0, int s_first, int K) {
-        const int J = J0 + q * NT + tid;
-        if (J >= J1) return;
-        float y = 0.f;
-        if (ENV_LDS && J < a.valid_end && tf0 >= 0 && tf0 + K < a.env_frames) {
-            const float r = inv_env[s_first - K * hop];
-            y = r > 0.f ? acc[q] * r : 0.f;
-        } else if (J < a.valid_end) {
-            const int i0 = max(0, -tf0), i1 = min(K, a.env_frames - 1 - tf0);
-            unsigned pos = (unsigned)(s_first - i0 * hop);
-            float env = 0.f;
-            for (int i = i0; i <= i1; i++, pos -= (unsigned)hop) {
-                const float w = win[pos];
-                env += w * w;
+    const float* ldsf = reinterpret_cast<const float*>(lds);
+
+    for (int ti = lb;; ti += a.grid) {
+        const int tn = ti + a.grid;                     // this workgroup's next tile
+        float acc[PER];
+#pragma unroll
+        for (int q = 0; q < PER; q++) acc[q] = 0.f;
+        for (int s0 = t.st_lo; s0 <= t.st_hi; s0 += JOBS) {
+            // An opaque copy of the lane index: keeps the compiler from hoisting the (round
+            // invariant) twiddle reads, staging addresses and sample walk out of this loop,
+            // which would hold them in registers across the transform.
+            int jr = j, tr = tid;
+            asm volatile("" : "+v"(jr), "+v"(tr));
+            __builtin_assume(jr >= 0 && jr < TPJ && tr >= 0 && tr < NT);
+            if constexpr (PERSIST) {
+                stage_frames(tr, jr, sv, nyq);
+                // The next round's loads (or the next tile's first), in flight through this round.
+                if (s0 + JOBS <= t.st_hi) {
+                    load_frames(t, s0 + JOBS, tr, jr, sv, nyq);
+                } else if (tn < a.nblocks) {
+                    const Tile u = tile_at(tn);
+                    if (u.st_lo <= u.st_hi) load_frames(u, u.st_lo, tr, jr, sv, nyq);
+                }
+            } else {
+                // One tile: each round's frames are loaded at its start, so that no registers are
+                // held across the transform; the tables go to LDS while the first round's loads
+                // are in flight.
+                load_frames(t, s0, tr, jr, sv, nyq);
+                if (!staged) stage_tables();
+                stage_frames(tr, jr, sv, nyq);
             }
-            y = env > 1e-11f ? acc[q] * (a.norm / env) : 0.f;   // as the table's product
+            lds_barrier();
+            // Split twiddles W_N^k for k = jr + r*TPJ: W_N^jr from the table times the
+            // constant W_N^(r*TPJ) = exp(-i pi r / P).
+            constexpr HalfTurnRoots<P> rot = half_turn_roots<P>();
+            const float2 w0 = tw_lookup<N>(twt, jr);
+            float2 v[P];
+#pragma unroll
+            for (int r = 0; r < P; r++) {
+                const int k = jr + r * TPJ;
+                const float2 wr = r == 0 ? w0 : cmul(w0, make_float2(rot.re[r], rot.im[r]));
+                v[r] = inverse_split_w(buf[k], buf[M - k], k, a.keep_nyquist, wr);
+            }
+            pass_sync<WAVE>();                          // staging read before the FFT overwrites it
+            fft_first_pass<M, P, N>(v, buf, jr, post, ToLdsFlat{buf});
+            pass_sync<WAVE>();
+            fft_rest_passes<M, P, N, P, WAVE>(buf, jr, twt, post, ToLdsFlat{buf});
+            if constexpr (WAVE) lds_barrier();          // every slot written before the sums read them
+            // Slot g now holds samples (2n, 2n + 1) of frame s0 + g at LDS index n (unpadded:
+            // the last pass's lanes write consecutive n), windowed: add the frames of this
+            // round that cover each sample, in frame order.
+            const int s_end = min(t.st_hi, s0 + JOBS - 1);
+            walk(t.J0, tr, [&](int q, int tf0, int s_first, int K) {
+                if (q * NT + tr >= t.J1 - t.J0) return;
+                const int first = tf0 - a.frame_off;              // spectrum frame of tf0
+                const int i0 = max(0, s0 - first), i1 = min(K, s_end - first);
+                // Sample pos (0 <= pos < N) of slot g is float pos of the slot.
+                const float* sl = ldsf + 2 * SLOT * (first + i0 - s0) + (s_first - i0 * hop);
+                float sum = acc[q];
+                for (int i = i0; i <= i1; i++, sl += 2 * SLOT - hop) sum += *sl;
+                acc[q] = sum;
+            });
+            lds_barrier();
         }
-        store_stream(oc + (J - a.out_off), y);
-    });
+        if constexpr (PERSIST) {
+            if (t.st_lo > t.st_hi) lds_barrier();      // no frame overlaps the tile (uniform): tables
+        } else {
+            if (!staged) {                             // no frame overlaps the tile (uniform)
+                stage_tables();
+                lds_barrier();
+            }
+            if constexpr (ENV_LDS) {
+                build_env();
+                lds_barrier();
+            }
+        }
+        float* oc = a.out + (size_t)t.c * a.out_len;
+        walk(t.J0, tid, [&](int q, int tf0, int s_first, int K) {
+            const int J = t.J0 + q * NT + tid;
+            if (J >= t.J1) return;
+            float y = 0.f;
+            if (ENV_LDS && J < a.valid_end && tf0 >= 0 && tf0 + K < a.env_frames) {
+                const float r = inv_env[s_first - K * hop];
+                y = r > 0.f ? acc[q] * r : 0.f;
+            } else if (J < a.valid_end) {
+                const int i0 = max(0, -tf0), i1 = min(K, a.env_frames - 1 - tf0);
+                unsigned pos = (unsigned)(s_first - i0 * hop);
+                float env = 0.f;
+                for (int i = i0; i <= i1; i++, pos -= (unsigned)hop) {
+                    const float w = win[pos];
+                    env += w * w;
+                }
+                y = env > 1e-11f ? acc[q] * (a.norm / env) : 0.f;   // as the table's product
+            }
+            store_stream(oc + (J - a.out_off), y);
+        });
+        if (!PERSIST || tn >= a.nblocks) break;
+        t = tile_at(tn);
+    }
 }
 
 // ------------------------------------------------------------------ mixed-radix sizes
@@ -873,12 +926,25 @@ long long plan_istft_tiles(IstftArgs& a, int channels) {
     return (long long)a.tiles * channels;
 }
 
-template <int N, int JOBS>
+// One workgroup per tile while the device holds them all at once; past that (MAY_PERSIST), as
+// many workgroups as it holds, each taking every grid-th tile.
+template <int N, int JOBS, bool MAY_PERSIST>
 void launch_istft_fused_jobs(IstftArgs a, int channels, hipStream_t s) {
     constexpr int P = fused_p(N);
+    constexpr int NT = JOBS * (N / 2 / P);
     a.nblocks = (int)plan_istft_tiles<N, JOBS>(a, channels);
-    hipLaunchKernelGGL((istft_kernel<N, P, JOBS, kIstftPer>), dim3(xcd_grid(a.nblocks)), dim3(JOBS * (N / 2 / P)),
-                       0, s, a);
+    if constexpr (MAY_PERSIST) {
+        const void* k = reinterpret_cast<const void*>(istft_kernel<N, P, JOBS, kIstftPer, true>);
+        const int resident = device_blocks(k, NT);
+        if (resident > 0 && a.nblocks > resident) {
+            a.grid = (int)xcd_grid(resident);
+            hipLaunchKernelGGL((istft_kernel<N, P, JOBS, kIstftPer, true>), dim3(a.grid), dim3(NT), 0, s, a);
+            launch_check("istft_kernel");
+            return;
+        }
+    }
+    a.grid = (int)xcd_grid(a.nblocks);
+    hipLaunchKernelGGL((istft_kernel<N, P, JOBS, kIstftPer, false>), dim3(a.grid), dim3(NT), 0, s, a);
     launch_check("istft_kernel");
 }
 
@@ -895,11 +961,11 @@ void launch_istft_fused(IstftArgs a, int channels, hipStream_t s) {
         const long long cus = device_cus();
         if (ALT - span >= 1 && plan_istft_tiles<N, JOBS>(t, channels) < cus &&
             plan_istft_tiles<N, ALT>(t, channels) <= cus) {
-            launch_istft_fused_jobs<N, ALT>(a, channels, s);
+            launch_istft_fused_jobs<N, ALT, false>(a, channels, s);
             return;
         }
     }
-    launch_istft_fused_jobs<N, JOBS>(a, channels, s);
+    launch_istft_fused_jobs<N, JOBS, true>(a, channels, s);
 }
 
 template <int N>

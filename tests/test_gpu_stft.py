@@ -218,9 +218,9 @@ def test_stft_errors(device):
 
 
 def test_small_hop_needs_several_rounds(device, orc):
-    # hop n/32 makes every output tile overlap more frames than one workgroup transforms at
-    # once, so the fused path loops over rounds.
-    n, hop, length = 1024, 32, 4000
+    # hop n/64 makes every output tile overlap 64 frames, twice the 32 one workgroup transforms
+    # at once at n_fft 1024, so the fused path loops over rounds.
+    n, hop, length = 1024, 16, 4000
     x = _stereo(55, length, 0.3)
     f = plan(n)
     spec = stx.torch_stft(f, to_dev(x, device), hop)
@@ -229,6 +229,30 @@ def test_small_hop_needs_several_rounds(device, orc):
     for c in range(2):
         ref = orc.torch_stft(x[c], n, hop)
         assert snr_db(spec_h[c], ref) >= SNR_DB
+        assert snr_db(y[c], orc.torch_istft(ref, n, hop)) >= SNR_DB
+
+
+@pytest.mark.parametrize("layout", [stx.F_MAJOR, stx.T_MAJOR])
+@pytest.mark.parametrize("n,hop,length,channels,sub", [
+    (2048, 441, 352800, 48, 3),     # 48 RoFormer chunks: 3,216 tiles; 3 chunks: 201 tiles
+    (1024, 8, 2000, 8, 1),          # 4 rounds of 32 frames per tile: 2,000 tiles; 1 channel: 250
+])
+def test_istft_more_tiles_than_resident_workgroups(device, orc, layout, n, hop, length, channels, sub):
+    # A batch whose tiles outnumber the workgroups the GPU holds at once: each workgroup takes
+    # several tiles (and prefetches the next tile's frames). Every channel must equal, bit for
+    # bit, the same channels inverted in a call small enough to give each tile its own workgroup.
+    x = synth.normal(4100 + n, (channels, length), 0.2)
+    f = plan(n)
+    spec = stx.torch_stft(f, to_dev(x, device), hop, layout=layout)
+    y = host(stx.torch_istft(f, spec, hop, layout=layout))
+    for i in range(0, channels, sub):
+        part = host(stx.torch_istft(f, spec[i:i + sub].contiguous(), hop, layout=layout))
+        assert np.array_equal(part, y[i:i + sub]), f"channels {i}..{i + sub - 1}"
+    spec_h = host(spec)
+    for c in (0, channels - 1):
+        s = spec_h[c] if layout == stx.F_MAJOR else spec_h[c].T
+        ref = orc.torch_stft(x[c], n, hop)
+        assert snr_db(s, ref) >= SNR_DB
         assert snr_db(y[c], orc.torch_istft(ref, n, hop)) >= SNR_DB
 
 
