@@ -13,10 +13,11 @@
 //   * the inverse transform is the forward one on conjugated data (ifft(X) = conj fft conj X),
 //     after the inverse split Z' = (X[k] + conj X[N/2-k]) + i W_N^-k (X[k] - conj X[N/2-k]);
 //   * the iSTFT overlap-add is in gather form, without atomics, in one of two ways:
-//       - fused (no workspace): each workgroup owns a tile of output samples, inverse-
-//         transforms every frame that overlaps it (frames shared by two tiles are transformed
-//         by both), sums the windowed frames in frame order in registers and divides by the
-//         window-squared envelope, evaluated in closed form per sample;
+//       - fused (no workspace): one workgroup owns a tile of output samples (several tiles in
+//         turn when they outnumber the workgroups the device holds), inverse-transforms every
+//         frame that overlaps it (frames shared by two tiles are transformed by both), sums the
+//         windowed frames in frame order in registers and divides by the window-squared
+//         envelope, evaluated in closed form per sample;
 //       - two kernels (the mixed-radix sizes, with a workspace of C*T*N floats): one
 //         inverse-transforms each frame once and writes it windowed to the workspace, the
 //         next sums and divides. Power-of-two sizes run the fused kernel with or without a
