@@ -256,6 +256,28 @@ def test_istft_more_tiles_than_resident_workgroups(device, orc, layout, n, hop, 
         assert snr_db(y[c], orc.torch_istft(ref, n, hop)) >= SNR_DB
 
 
+@pytest.mark.parametrize("layout", [stx.F_MAJOR, stx.T_MAJOR])
+def test_htdemucs_ispec_many_segments_same_bits_as_pairs(device, orc, layout):
+    # 16 HTDemucs segments (n_fft 4096) in one call: 8-frame tiles of 5 hops, 1,088 of them,
+    # several per workgroup; a call of two segments takes 6-frame tiles of 3 hops, one per
+    # workgroup. Each sample adds the same frames in the same order either way, so every
+    # channel must come out bit for bit the same.
+    length, channels = 343980, 16
+    x = synth.normal(4242, (channels, length), 0.1)
+    f = plan(4096)
+    spec = stx.htdemucs_spec(f, to_dev(x, device), layout=layout)
+    y = host(stx.htdemucs_ispec(f, spec, length, layout=layout))
+    for i in range(0, channels, 2):
+        part = host(stx.htdemucs_ispec(f, spec[i:i + 2].contiguous(), length, layout=layout))
+        assert np.array_equal(part, y[i:i + 2]), f"channels {i}, {i + 1}"
+    spec_h = host(spec)
+    for c in (0, channels - 1):
+        s = spec_h[c] if layout == stx.F_MAJOR else spec_h[c].T
+        ref = orc.htdemucs_spec(x[c], 4096)
+        assert snr_db(s, ref) >= SNR_DB
+        assert snr_db(y[c], orc.htdemucs_ispec(ref, 4096, length)) >= SNR_DB
+
+
 def test_workspace_too_small(device):
     f = plan(2048)
     x = to_dev(_stereo(56, 20000), device)
