@@ -278,6 +278,47 @@ def test_htdemucs_ispec_many_segments_same_bits_as_pairs(device, orc, layout):
         assert snr_db(y[c], orc.htdemucs_ispec(ref, 4096, length)) >= SNR_DB
 
 
+def test_istft_many_tiles_graph_replays(device):
+    """A captured torch_istft call whose tiles outnumber the resident workgroups, replayed on new
+    spectra with eager work between the replays: every replay equals the eager call's bits."""
+    import torch
+    n, hop, length, channels = 2048, 441, 352800, 24
+    f = plan(n)
+    x = to_dev(synth.normal(4300, (channels, length), 0.2), device)
+    spec = stx.torch_stft(f, x, hop)
+    y = torch.empty((channels, length), device=device)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        stx.torch_istft(f, spec, hop, out=y, stream=s)
+        s.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            stx.torch_istft(f, spec, hop, out=y, stream=s)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        xn = to_dev(synth.normal(4310 + rep, (channels, length), 0.1 + 0.2 * rep), device)
+        spec.copy_(stx.torch_stft(f, xn, hop))
+        want = host(stx.torch_istft(f, spec, hop))
+        g.replay()
+        assert np.array_equal(host(y), want), f"replay {rep}"
+
+
+@pytest.mark.parametrize("trim", [0, 4999])
+def test_htdemucs_ispec_many_segments_trimmed(device, orc, trim):
+    # The batched call with an output shorter than the segment (the tiles' last one cut short)
+    # against one segment at a time.
+    length, channels = 343980, 12
+    x = synth.normal(4400 + trim, (channels, length), 0.1)
+    f = plan(4096)
+    spec = stx.htdemucs_spec(f, to_dev(x, device))
+    y = host(stx.htdemucs_ispec(f, spec, length - trim))
+    for i in range(channels):
+        one = host(stx.htdemucs_ispec(f, spec[i:i + 1].contiguous(), length - trim))
+        assert np.array_equal(one, y[i:i + 1]), f"channel {i}"
+    ref = orc.htdemucs_spec(x[channels - 1], 4096)
+    assert snr_db(y[channels - 1], orc.htdemucs_ispec(ref, 4096, length - trim)) >= SNR_DB
+
+
 def test_workspace_too_small(device):
     f = plan(2048)
     x = to_dev(_stereo(56, 20000), device)
