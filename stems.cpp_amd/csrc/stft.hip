@@ -762,13 +762,23 @@ __global__ __launch_bounds__(kMixedThreads * FPB) void istft_frames_mixed_kernel
     float2 wv[RL];
 #pragma unroll
     for (int q = 0; q < RL; q++) wv[q] = win2[min(tid + q * NT, M - 1)];
+    // Windowed as WindowPost, streamed out: the overlap-add kernel reads these frames across
+    // XCDs, so they come back from memory whatever the store; with the non-temporal bit they
+    // leave during the kernel instead of as dirty L2 lines at its end (Kim 7680 iSTFT
+    // 25.3 -> 24.2 us). 8-byte stores where the workspace allows them (n is even).
+    const bool pairs = (reinterpret_cast<uintptr_t>(a.frames) & 7) == 0;
 #pragma unroll
-    for (int q = 0; q < RL; q++) {                     // windowed as WindowPost
+    for (int q = 0; q < RL; q++) {
         const int i = tid + q * NT;
         if (i >= M) break;
         const float2 ri = r[mixed_pad(i)];
-        dst[2 * i] = ri.x * wv[q].x * a.norm;
-        dst[2 * i + 1] = -ri.y * wv[q].y * a.norm;
+        const float2 o = make_float2(ri.x * wv[q].x * a.norm, -ri.y * wv[q].y * a.norm);
+        if (pairs) {
+            store_stream(reinterpret_cast<float2*>(dst + 2 * i), o);
+        } else {
+            store_stream(dst + 2 * i, o.x);
+            store_stream(dst + 2 * i + 1, o.y);
+        }
     }
 }
 
